@@ -1,0 +1,952 @@
+// C ABI of the MI355X decode path: context, weights, device-resident model,
+// KV cache, captured decode step, and kernel-level entry points.
+#include "../../include/qora_hip.h"
+#include "launch.hpp"
+
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <vector>
+
+using namespace qora;
+
+namespace {
+
+struct DevWeight {
+    int fmt = 0;            // FMT_Q4 / FMT_F16
+    uint64_t k = 0, n = 0;
+    void* w = nullptr;      // packed bytes or f16 words
+    void* scales = nullptr; // Q4 only
+    bool alive = false;
+};
+
+struct ModelState {
+    bool ready = false;
+    uint32_t L = 0, vocab = 0, hidden = 0, inter = 0, H = 0, KVH = 0, hd = 0, groups = 0, half = 0, fmt = 0;
+    uint32_t cap = 0;
+    int kv_f16 = 0;
+    uint64_t rope_positions = 0;
+    bool any_rope = false;
+    std::vector<uint32_t> wids;
+    uint32_t embed_wid = 0;
+    std::vector<void*> allocs;           // every device allocation of the model
+    uint16_t* d_norms = nullptr;         // [L][2][hidden]
+    uint16_t* d_final = nullptr;
+    float* d_cos = nullptr;
+    float* d_sin = nullptr;
+    void* d_k = nullptr;                 // [L][cap][kvd]
+    void* d_v = nullptr;
+    float* d_x = nullptr;
+    float* d_q = nullptr;
+    float* d_attn = nullptr;
+    float* d_h = nullptr;
+    float* d_logits = nullptr;
+    int32_t* d_token = nullptr;
+    int32_t* d_pos = nullptr;
+    int32_t* d_gen = nullptr;
+    int32_t* d_prompt = nullptr;
+    float* d_partials = nullptr;
+    uint32_t* d_counters = nullptr;
+    float* d_attn_part = nullptr;
+    uint32_t* d_attn_cnt = nullptr;
+    float* d_argv = nullptr;
+    uint32_t* d_argi = nullptr;
+    uint32_t* d_argc = nullptr;
+    GemvPlan pl_qkv, pl_o, pl_gu, pl_down;
+    uint32_t lm_blocks = 0;
+    std::vector<GemvParams> p_qkv, p_o, p_gu, p_down;
+    std::vector<AttnParams> p_attn;
+    RowdotParams p_lm{};
+    EmbedParams p_emb_tok{}, p_emb_prompt{};
+    hipGraphExec_t g_step = nullptr;
+    hipGraphExec_t g_prefill = nullptr;
+    uint64_t host_pos = 0;
+};
+
+}  // namespace
+
+struct qora_hip_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    int cus = 0;
+    std::string err;
+    std::vector<DevWeight> weights;
+    float* ws_part = nullptr;
+    uint64_t ws_part_n = 0;
+    uint32_t* ws_cnt = nullptr;
+    uint64_t ws_cnt_n = 0;
+    float* ws_attn_part = nullptr;
+    uint64_t ws_attn_part_n = 0;
+    uint32_t* ws_attn_cnt = nullptr;
+    uint64_t ws_attn_cnt_n = 0;
+    int32_t* h_pin = nullptr;            // pinned staging: [0] token in, [1] token out, [2] pos
+    bool capturing = false;
+    ModelState m;
+};
+
+namespace {
+
+int fail(qora_hip_ctx* c, int code, const std::string& msg) {
+    if (c) c->err = msg;
+    return code;
+}
+
+bool force_fail(const char* what) {
+    const char* v = std::getenv("QORA_HIP_FORCE_FAIL");
+    return v && std::strcmp(v, what) == 0;
+}
+
+#define HIP_TRY(ctx, expr)                                                                      \
+    do {                                                                                        \
+        hipError_t e_ = (expr);                                                                 \
+        if (e_ != hipSuccess)                                                                   \
+            return fail((ctx), QORA_HIP_E_DEVICE, std::string(#expr) + ": " + hipGetErrorString(e_)); \
+    } while (0)
+
+int dalloc(qora_hip_ctx* c, size_t bytes, void** p) {
+    *p = nullptr;
+    if (force_fail("alloc")) return fail(c, QORA_HIP_E_NOMEM, "forced allocation failure (QORA_HIP_FORCE_FAIL=alloc)");
+    if (bytes == 0) bytes = 16;
+    const hipError_t e = hipMalloc(p, bytes);
+    if (e != hipSuccess) {
+        *p = nullptr;
+        (void)hipGetLastError();
+        return fail(c, QORA_HIP_E_NOMEM, "hipMalloc(" + std::to_string(bytes) + "): " + hipGetErrorString(e));
+    }
+    return QORA_HIP_OK;
+}
+
+hipStream_t pick_stream(qora_hip_ctx* c, void* s) { return s ? reinterpret_cast<hipStream_t>(s) : c->stream; }
+
+// Grow the kernel-level scratch (split-K partials and tile counters).
+int ensure_ws(qora_hip_ctx* c, uint64_t part_floats, uint64_t counters) {
+    if (part_floats <= c->ws_part_n && counters <= c->ws_cnt_n) return QORA_HIP_OK;
+    if (c->capturing) return fail(c, QORA_HIP_E_STATE, "scratch must be sized by an eager call before capture");
+    HIP_TRY(c, hipStreamSynchronize(c->stream));
+    if (part_floats > c->ws_part_n) {
+        if (c->ws_part) (void)hipFree(c->ws_part);
+        c->ws_part = nullptr;
+        c->ws_part_n = 0;
+        void* p;
+        const uint64_t nn = part_floats + part_floats / 4;
+        if (int rc = dalloc(c, nn * sizeof(float), &p)) return rc;
+        c->ws_part = (float*)p;
+        c->ws_part_n = nn;
+    }
+    if (counters > c->ws_cnt_n) {
+        if (c->ws_cnt) (void)hipFree(c->ws_cnt);
+        c->ws_cnt = nullptr;
+        c->ws_cnt_n = 0;
+        void* p;
+        const uint64_t nn = counters < 4096 ? 4096 : counters;
+        if (int rc = dalloc(c, nn * sizeof(uint32_t), &p)) return rc;
+        HIP_TRY(c, hipMemset(p, 0, nn * sizeof(uint32_t)));
+        c->ws_cnt = (uint32_t*)p;
+        c->ws_cnt_n = nn;
+    }
+    return QORA_HIP_OK;
+}
+
+int ensure_attn_ws(qora_hip_ctx* c, uint64_t part_floats, uint64_t counters) {
+    if (part_floats <= c->ws_attn_part_n && counters <= c->ws_attn_cnt_n) return QORA_HIP_OK;
+    if (c->capturing) return fail(c, QORA_HIP_E_STATE, "scratch must be sized by an eager call before capture");
+    HIP_TRY(c, hipStreamSynchronize(c->stream));
+    if (part_floats > c->ws_attn_part_n) {
+        if (c->ws_attn_part) (void)hipFree(c->ws_attn_part);
+        c->ws_attn_part = nullptr;
+        c->ws_attn_part_n = 0;
+        void* p;
+        if (int rc = dalloc(c, part_floats * sizeof(float), &p)) return rc;
+        c->ws_attn_part = (float*)p;
+        c->ws_attn_part_n = part_floats;
+    }
+    if (counters > c->ws_attn_cnt_n) {
+        if (c->ws_attn_cnt) (void)hipFree(c->ws_attn_cnt);
+        c->ws_attn_cnt = nullptr;
+        c->ws_attn_cnt_n = 0;
+        void* p;
+        const uint64_t nn = counters < 64 ? 64 : counters;
+        if (int rc = dalloc(c, nn * sizeof(uint32_t), &p)) return rc;
+        HIP_TRY(c, hipMemset(p, 0, nn * sizeof(uint32_t)));
+        c->ws_attn_cnt = (uint32_t*)p;
+        c->ws_attn_cnt_n = nn;
+    }
+    return QORA_HIP_OK;
+}
+
+void free_model(qora_hip_ctx* c) {
+    ModelState& m = c->m;
+    if (m.g_step) (void)hipGraphExecDestroy(m.g_step);
+    if (m.g_prefill) (void)hipGraphExecDestroy(m.g_prefill);
+    for (void* p : m.allocs) (void)hipFree(p);
+    m = ModelState();
+}
+
+int model_alloc(qora_hip_ctx* c, size_t bytes, void** p) {
+    if (int rc = dalloc(c, bytes, p)) return rc;
+    c->m.allocs.push_back(*p);
+    return QORA_HIP_OK;
+}
+
+const DevWeight* get_weight(qora_hip_ctx* c, uint32_t wid) {
+    if (wid >= c->weights.size() || !c->weights[wid].alive) return nullptr;
+    return &c->weights[wid];
+}
+
+int record_step(qora_hip_ctx* c, bool with_lm_head) {
+    ModelState& m = c->m;
+    const hipStream_t s = c->stream;
+    HIP_TRY(c, launch_embed(with_lm_head ? m.p_emb_tok : m.p_emb_prompt, s));
+    for (uint32_t l = 0; l < m.L; ++l) {
+        HIP_TRY(c, launch_gemv(m.fmt, m.pl_qkv, m.p_qkv[l], s));
+        HIP_TRY(c, launch_attn(m.p_attn[l], s));
+        HIP_TRY(c, launch_gemv(m.fmt, m.pl_o, m.p_o[l], s));
+        HIP_TRY(c, launch_gemv(m.fmt, m.pl_gu, m.p_gu[l], s));
+        HIP_TRY(c, launch_gemv(m.fmt, m.pl_down, m.p_down[l], s));
+    }
+    if (with_lm_head) HIP_TRY(c, launch_rowdot(m.fmt, m.lm_blocks, m.p_lm, s));
+    else HIP_TRY(c, launch_advance_pos(m.d_pos, s));
+    return QORA_HIP_OK;
+}
+
+int capture_step(qora_hip_ctx* c, bool with_lm_head, hipGraphExec_t* out) {
+    HIP_TRY(c, hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
+    const int rc = record_step(c, with_lm_head);
+    hipGraph_t g = nullptr;
+    const hipError_t e = hipStreamEndCapture(c->stream, &g);
+    if (rc) {
+        if (g) (void)hipGraphDestroy(g);
+        return rc;
+    }
+    if (e != hipSuccess) return fail(c, QORA_HIP_E_DEVICE, std::string("hipStreamEndCapture: ") + hipGetErrorString(e));
+    const hipError_t e2 = hipGraphInstantiate(out, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e2 != hipSuccess) return fail(c, QORA_HIP_E_DEVICE, std::string("hipGraphInstantiate: ") + hipGetErrorString(e2));
+    return QORA_HIP_OK;
+}
+
+float h2f_host(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    const uint32_t exp = (h >> 10) & 0x1Fu;
+    uint32_t mant = h & 0x3FFu;
+    uint32_t bits;
+    if (exp == 0) {
+        if (mant == 0) {
+            bits = sign;
+        } else {
+            int e = -1;
+            do { mant <<= 1; ++e; } while ((mant & 0x400u) == 0);
+            mant &= 0x3FFu;
+            bits = sign | ((uint32_t)(127 - 15 - e) << 23) | (mant << 13);
+        }
+    } else if (exp == 0x1F) {
+        bits = sign | 0x7F800000u | (mant << 13);
+    } else {
+        bits = sign | ((exp + 127 - 15) << 23) | (mant << 13);
+    }
+    float f;
+    std::memcpy(&f, &bits, 4);
+    return f;
+}
+
+}  // namespace
+
+// ===========================================================================
+// context
+// ===========================================================================
+
+extern "C" int qora_hip_create(int device, qora_hip_ctx** out) {
+    if (!out) return QORA_HIP_E_INVALID;
+    *out = nullptr;
+    if (force_fail("init")) return QORA_HIP_E_DEVICE;
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count <= 0) {
+        (void)hipGetLastError();
+        return QORA_HIP_E_DEVICE;
+    }
+    if (device < 0 || device >= count) return QORA_HIP_E_INVALID;
+    qora_hip_ctx* c = new qora_hip_ctx();
+    c->device = device;
+    if (hipSetDevice(device) != hipSuccess || hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
+        delete c;
+        return QORA_HIP_E_DEVICE;
+    }
+    int cus = 0;
+    (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device);
+    c->cus = cus > 0 ? cus : 256;
+    if (hipHostMalloc((void**)&c->h_pin, 64, hipHostMallocDefault) != hipSuccess) {
+        (void)hipStreamDestroy(c->stream);
+        delete c;
+        return QORA_HIP_E_DEVICE;
+    }
+    *out = c;
+    return QORA_HIP_OK;
+}
+
+extern "C" int qora_hip_destroy(qora_hip_ctx* c) {
+    if (!c) return QORA_HIP_E_INVALID;
+    (void)hipSetDevice(c->device);
+    (void)hipStreamSynchronize(c->stream);
+    free_model(c);
+    for (DevWeight& w : c->weights) {
+        if (w.w) (void)hipFree(w.w);
+        if (w.scales) (void)hipFree(w.scales);
+    }
+    for (void* p : {(void*)c->ws_part, (void*)c->ws_cnt, (void*)c->ws_attn_part, (void*)c->ws_attn_cnt})
+        if (p) (void)hipFree(p);
+    if (c->h_pin) (void)hipHostFree(c->h_pin);
+    (void)hipStreamDestroy(c->stream);
+    delete c;
+    return QORA_HIP_OK;
+}
+
+extern "C" const char* qora_hip_last_error(const qora_hip_ctx* c) {
+    return c ? c->err.c_str() : "null context";
+}
+
+extern "C" int qora_hip_device_cus(const qora_hip_ctx* c) { return c ? c->cus : 0; }
+
+// ===========================================================================
+// weights
+// ===========================================================================
+
+extern "C" int qora_hip_upload_q4(qora_hip_ctx* c, const uint8_t* packed, size_t packed_len,
+                                  const uint16_t* scales, size_t n_scales, uint64_t k, uint64_t n, uint32_t* wid) {
+    if (!c || !packed || !scales || !wid) return fail(c, QORA_HIP_E_INVALID, "null argument");
+    if (k == 0 || n == 0 || n % 32 != 0) return fail(c, QORA_HIP_E_INVALID, "Q4 weight needs k > 0 and n % 32 == 0");
+    if (packed_len != k * n / 2 || n_scales != k * n / 32)
+        return fail(c, QORA_HIP_E_INVALID, "Q4 buffer lengths do not match k*n/2 and k*n/32");
+    DevWeight w;
+    w.fmt = FMT_Q4;
+    w.k = k;
+    w.n = n;
+    if (int rc = dalloc(c, packed_len, &w.w)) return rc;
+    if (int rc = dalloc(c, n_scales * 2, &w.scales)) { (void)hipFree(w.w); return rc; }
+    HIP_TRY(c, hipMemcpy(w.w, packed, packed_len, hipMemcpyHostToDevice));
+    HIP_TRY(c, hipMemcpy(w.scales, scales, n_scales * 2, hipMemcpyHostToDevice));
+    w.alive = true;
+    *wid = (uint32_t)c->weights.size();
+    c->weights.push_back(w);
+    return QORA_HIP_OK;
+}
+
+extern "C" int qora_hip_upload_f16(qora_hip_ctx* c, const uint16_t* data, size_t len, uint64_t k, uint64_t n,
+                                   uint32_t* wid) {
+    if (!c || !data || !wid) return fail(c, QORA_HIP_E_INVALID, "null argument");
+    if (k == 0 || n == 0 || n % 32 != 0) return fail(c, QORA_HIP_E_INVALID, "F16 weight needs k > 0 and n % 32 == 0");
+    if (len != k * n) return fail(c, QORA_HIP_E_INVALID, "F16 buffer length does not match k*n");
+    DevWeight w;
+    w.fmt = FMT_F16;
+    w.k = k;
+    w.n = n;
+    if (int rc = dalloc(c, len * 2, &w.w)) return rc;
+    HIP_TRY(c, hipMemcpy(w.w, data, len * 2, hipMemcpyHostToDevice));
+    w.alive = true;
+    *wid = (uint32_t)c->weights.size();
+    c->weights.push_back(w);
+    return QORA_HIP_OK;
+}
+
+extern "C" int qora_hip_weight_ptrs(qora_hip_ctx* c, uint32_t wid, void** data, void** scales) {
+    if (!c) return QORA_HIP_E_INVALID;
+    const DevWeight* w = get_weight(c, wid);
+    if (!w) return fail(c, QORA_HIP_E_INVALID, "unknown weight id");
+    if (data) *data = w->w;
+    if (scales) *scales = w->scales;
+    return QORA_HIP_OK;
+}
+
+// ===========================================================================
+// model
+// ===========================================================================
+
+extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
+    if (!c || !d) return fail(c, QORA_HIP_E_INVALID, "null argument");
+    HIP_TRY(c, hipSetDevice(c->device));
+    free_model(c);
+    if (d->num_layers == 0 || d->vocab == 0 || d->hidden == 0 || d->intermediate == 0 || d->num_heads == 0 ||
+        d->num_kv_heads == 0 || d->head_dim == 0 || d->kv_capacity == 0)
+        return fail(c, QORA_HIP_E_INVALID, "zero-sized model dimension");
+    if (d->format > 1) return fail(c, QORA_HIP_E_INVALID, "format must be 0 (F16) or 1 (Q4)");
+    if (d->num_heads % d->num_kv_heads != 0 || d->num_kv_groups != d->num_heads / d->num_kv_heads)
+        return fail(c, QORA_HIP_E_INVALID, "num_kv_groups must equal num_heads / num_kv_heads");
+    if (d->num_kv_groups > (uint32_t)kAttnMaxGroups || d->head_dim > (uint32_t)kAttnMaxHd)
+        return fail(c, QORA_HIP_E_INVALID, "attention kernel supports head_dim <= 128 and <= 4 query heads per KV head");
+    if (256 % d->head_dim != 0) return fail(c, QORA_HIP_E_INVALID, "head_dim must divide 256");
+    if (2 * d->rope_half_dim > d->head_dim) return fail(c, QORA_HIP_E_INVALID, "rope_half_dim exceeds head_dim / 2");
+    if (d->hidden % 32 != 0 || 64 % (d->hidden / 32) != 0 || d->intermediate % 32 != 0)
+        return fail(c, QORA_HIP_E_INVALID, "hidden/32 must divide 64 and intermediate must be a multiple of 32");
+    if (!d->layer_wids || !d->input_norm || !d->post_attn_norm || !d->final_norm || !d->use_rope)
+        return fail(c, QORA_HIP_E_INVALID, "null model pointer");
+    bool any_rope = false;
+    for (uint32_t l = 0; l < d->num_layers; ++l) any_rope |= d->use_rope[l] != 0;
+    if (any_rope && (!d->rope_cos || !d->rope_sin || d->rope_half_dim == 0 || d->rope_positions < d->kv_capacity))
+        return fail(c, QORA_HIP_E_INVALID, "RoPE tables must cover kv_capacity positions");
+
+    ModelState& m = c->m;
+    m.L = d->num_layers;
+    m.vocab = d->vocab;
+    m.hidden = d->hidden;
+    m.inter = d->intermediate;
+    m.H = d->num_heads;
+    m.KVH = d->num_kv_heads;
+    m.hd = d->head_dim;
+    m.groups = d->num_kv_groups;
+    m.half = d->rope_half_dim;
+    m.fmt = d->format;
+    m.cap = d->kv_capacity;
+    m.kv_f16 = d->kv_dtype == 1;
+    m.rope_positions = d->rope_positions;
+    m.any_rope = any_rope;
+    const uint32_t qd = m.H * m.hd, kvd = m.KVH * m.hd;
+
+    // shape and format checks of every weight (LayerWeights, gemv.rs:177-191)
+    const uint64_t shapes[7][2] = {{m.hidden, qd}, {m.hidden, kvd}, {m.hidden, kvd}, {qd, m.hidden},
+                                   {m.hidden, m.inter}, {m.hidden, m.inter}, {m.inter, m.hidden}};
+    m.wids.assign(d->layer_wids, d->layer_wids + (size_t)m.L * 7);
+    for (uint32_t l = 0; l < m.L; ++l)
+        for (int j = 0; j < 7; ++j) {
+            const DevWeight* w = get_weight(c, m.wids[l * 7 + j]);
+            if (!w) { free_model(c); return fail(c, QORA_HIP_E_INVALID, "unknown weight id in layer_wids"); }
+            if (w->fmt != (int)d->format || w->k != shapes[j][0] || w->n != shapes[j][1]) {
+                free_model(c);
+                return fail(c, QORA_HIP_E_INVALID, "layer " + std::to_string(l) + " weight " + std::to_string(j) +
+                                                       " has the wrong format or shape");
+            }
+        }
+    const DevWeight* emb = get_weight(c, d->embed_wid);
+    if (!emb || emb->fmt != (int)d->format || emb->k != m.vocab || emb->n != m.hidden) {
+        free_model(c);
+        return fail(c, QORA_HIP_E_INVALID, "embedding weight has the wrong format or shape");
+    }
+    m.embed_wid = d->embed_wid;
+
+    // launch plans
+    const uint32_t gq = qd / 32, gkv = kvd / 32, gh = m.hidden / 32, gi = m.inter / 32;
+    const uint32_t qkv_groups[3] = {gq, gkv, gkv};
+    const uint32_t gu_groups[2] = {gi, gi};
+    if (!plan_gemv(m.fmt, m.hidden, qkv_groups, 3, false, c->cus, &m.pl_qkv) ||
+        !plan_gemv(m.fmt, qd, &gh, 1, false, c->cus, &m.pl_o) ||
+        !plan_gemv(m.fmt, m.hidden, gu_groups, 2, true, c->cus, &m.pl_gu) ||
+        !plan_gemv(m.fmt, m.inter, &gh, 1, false, c->cus, &m.pl_down)) {
+        free_model(c);
+        return fail(c, QORA_HIP_E_INVALID, "unsupported GEMV shape");
+    }
+    // Each of q, k, v starts on its own column tile and head_dim divides the
+    // tile width, so the RoPE partner of a column is always in its tile.
+    m.lm_blocks = rowdot_blocks(m.vocab, m.hidden, c->cus);
+    const uint32_t s_max = attn_splits(m.cap);
+    uint64_t part_floats = 0, tiles_max = 0;
+    for (const GemvPlan* pl : {&m.pl_qkv, &m.pl_o, &m.pl_gu, &m.pl_down}) {
+        part_floats = std::max<uint64_t>(part_floats, pl->partial_floats());
+        tiles_max = std::max<uint64_t>(tiles_max, pl->tiles);
+    }
+
+    // device buffers
+    void* p = nullptr;
+    const size_t kvb = m.kv_f16 ? 2 : 4;
+#define MALLOC(field, bytes)                                   \
+    do {                                                       \
+        if (int rc_ = model_alloc(c, (bytes), &p)) { free_model(c); return rc_; } \
+        m.field = (decltype(m.field))p;                        \
+    } while (0)
+    MALLOC(d_norms, (size_t)m.L * 2 * m.hidden * 2);
+    MALLOC(d_final, (size_t)m.hidden * 2);
+    if (any_rope) {
+        MALLOC(d_cos, (size_t)m.rope_positions * m.half * 4);
+        MALLOC(d_sin, (size_t)m.rope_positions * m.half * 4);
+    }
+    MALLOC(d_k, (size_t)m.L * m.cap * kvd * kvb);
+    MALLOC(d_v, (size_t)m.L * m.cap * kvd * kvb);
+    MALLOC(d_x, (size_t)m.hidden * 4);
+    MALLOC(d_q, (size_t)qd * 4);
+    MALLOC(d_attn, (size_t)qd * 4);
+    MALLOC(d_h, (size_t)m.inter * 4);
+    MALLOC(d_logits, (size_t)m.vocab * 4);
+    MALLOC(d_token, 64);
+    MALLOC(d_pos, 64);
+    MALLOC(d_gen, (size_t)m.cap * 4 + 64);
+    MALLOC(d_prompt, (size_t)m.cap * 4 + 64);
+    MALLOC(d_partials, (size_t)std::max<uint64_t>(part_floats, 1) * 4);
+    MALLOC(d_counters, (size_t)std::max<uint64_t>(tiles_max, 1) * 4);
+    MALLOC(d_attn_part, (size_t)m.KVH * s_max * m.groups * (m.hd + 2) * 4);
+    MALLOC(d_attn_cnt, (size_t)m.KVH * 4);
+    MALLOC(d_argv, (size_t)m.lm_blocks * 4);
+    MALLOC(d_argi, (size_t)m.lm_blocks * 4);
+    MALLOC(d_argc, 64);
+#undef MALLOC
+    HIP_TRY(c, hipMemset(m.d_counters, 0, (size_t)std::max<uint64_t>(tiles_max, 1) * 4));
+    HIP_TRY(c, hipMemset(m.d_attn_cnt, 0, (size_t)m.KVH * 4));
+    HIP_TRY(c, hipMemset(m.d_argc, 0, 64));
+    HIP_TRY(c, hipMemset(m.d_pos, 0, 64));
+    HIP_TRY(c, hipMemset(m.d_token, 0, 64));
+    HIP_TRY(c, hipMemset(m.d_gen, 0, (size_t)m.cap * 4 + 64));
+    HIP_TRY(c, hipMemset(m.d_prompt, 0, (size_t)m.cap * 4 + 64));
+    for (uint32_t l = 0; l < m.L; ++l) {
+        HIP_TRY(c, hipMemcpy(m.d_norms + ((size_t)l * 2 + 0) * m.hidden, d->input_norm[l], (size_t)m.hidden * 2,
+                             hipMemcpyHostToDevice));
+        HIP_TRY(c, hipMemcpy(m.d_norms + ((size_t)l * 2 + 1) * m.hidden, d->post_attn_norm[l], (size_t)m.hidden * 2,
+                             hipMemcpyHostToDevice));
+    }
+    HIP_TRY(c, hipMemcpy(m.d_final, d->final_norm, (size_t)m.hidden * 2, hipMemcpyHostToDevice));
+    if (any_rope) {
+        HIP_TRY(c, hipMemcpy(m.d_cos, d->rope_cos, (size_t)m.rope_positions * m.half * 4, hipMemcpyHostToDevice));
+        HIP_TRY(c, hipMemcpy(m.d_sin, d->rope_sin, (size_t)m.rope_positions * m.half * 4, hipMemcpyHostToDevice));
+    }
+
+    // per-layer launch parameters
+    m.p_qkv.resize(m.L);
+    m.p_o.resize(m.L);
+    m.p_gu.resize(m.L);
+    m.p_down.resize(m.L);
+    m.p_attn.resize(m.L);
+    for (uint32_t l = 0; l < m.L; ++l) {
+        const DevWeight* W[7];
+        for (int j = 0; j < 7; ++j) W[j] = get_weight(c, m.wids[l * 7 + j]);
+        uint8_t* kl = (uint8_t*)m.d_k + (size_t)l * m.cap * kvd * kvb;
+        uint8_t* vl = (uint8_t*)m.d_v + (size_t)l * m.cap * kvd * kvb;
+
+        GemvParams& q = m.p_qkv[l];
+        q = GemvParams{};
+        for (int j = 0; j < 3; ++j) q.seg[j] = GemvSeg{(const uint8_t*)W[j]->w, (const uint16_t*)W[j]->scales,
+                                                       (uint32_t)(W[j]->n / 32), 0, 0};
+        q.nseg = 3;
+        q.x = m.d_x;
+        q.gamma = m.d_norms + ((size_t)l * 2 + 0) * m.hidden;
+        q.k = m.hidden;
+        q.partials = m.d_partials;
+        q.counters = m.d_counters;
+        q.epi = EPI_QKV;
+        q.q_out = m.d_q;
+        q.kcache = kl;
+        q.vcache = vl;
+        q.kv_f16 = m.kv_f16;
+        q.head_dim = m.hd;
+        q.half_dim = m.half;
+        q.kv_stride = kvd;
+        q.rope_cos = m.d_cos;
+        q.rope_sin = m.d_sin;
+        q.pos = m.d_pos;
+        q.use_rope = d->use_rope[l] ? 1 : 0;
+        apply_plan(m.pl_qkv, &q);
+
+        AttnParams& a = m.p_attn[l];
+        a = AttnParams{};
+        a.q = m.d_q;
+        a.kc = kl;
+        a.vc = vl;
+        a.kv_f16 = m.kv_f16;
+        a.pos = m.d_pos;
+        a.H = m.H;
+        a.KVH = m.KVH;
+        a.hd = m.hd;
+        a.groups = m.groups;
+        a.scale = 1.0f / sqrtf((float)m.hd);
+        a.part = m.d_attn_part;
+        a.counters = m.d_attn_cnt;
+        a.s_max = s_max;
+        a.out = m.d_attn;
+
+        GemvParams& o = m.p_o[l];
+        o = GemvParams{};
+        o.seg[0] = GemvSeg{(const uint8_t*)W[3]->w, (const uint16_t*)W[3]->scales, gh, 0, 0};
+        o.nseg = 1;
+        o.x = m.d_attn;
+        o.k = qd;
+        o.partials = m.d_partials;
+        o.counters = m.d_counters;
+        o.epi = EPI_RESID;
+        o.y = m.d_x;
+        apply_plan(m.pl_o, &o);
+
+        GemvParams& g = m.p_gu[l];
+        g = GemvParams{};
+        g.seg[0] = GemvSeg{(const uint8_t*)W[4]->w, (const uint16_t*)W[4]->scales, gi, 0, 0};
+        g.seg[1] = GemvSeg{(const uint8_t*)W[5]->w, (const uint16_t*)W[5]->scales, gi, 0, 0};
+        g.nseg = 2;
+        g.paired = 1;
+        g.x = m.d_x;
+        g.gamma = m.d_norms + ((size_t)l * 2 + 1) * m.hidden;
+        g.k = m.hidden;
+        g.partials = m.d_partials;
+        g.counters = m.d_counters;
+        g.epi = EPI_SILU;
+        g.y = m.d_h;
+        apply_plan(m.pl_gu, &g);
+
+        GemvParams& dn = m.p_down[l];
+        dn = GemvParams{};
+        dn.seg[0] = GemvSeg{(const uint8_t*)W[6]->w, (const uint16_t*)W[6]->scales, gh, 0, 0};
+        dn.nseg = 1;
+        dn.x = m.d_h;
+        dn.k = m.inter;
+        dn.partials = m.d_partials;
+        dn.counters = m.d_counters;
+        dn.epi = EPI_RESID;
+        dn.y = m.d_x;
+        apply_plan(m.pl_down, &dn);
+    }
+    m.p_lm = RowdotParams{};
+    m.p_lm.w = (const uint8_t*)emb->w;
+    m.p_lm.scales = (const uint16_t*)emb->scales;
+    m.p_lm.rows = m.vocab;
+    m.p_lm.cols = m.hidden;
+    m.p_lm.x = m.d_x;
+    m.p_lm.gamma = m.d_final;
+    m.p_lm.y = m.d_logits;
+    m.p_lm.do_argmax = 1;
+    m.p_lm.part_val = m.d_argv;
+    m.p_lm.part_idx = m.d_argi;
+    m.p_lm.counter = m.d_argc;
+    m.p_lm.token_out = m.d_token;
+    m.p_lm.pos = m.d_pos;
+    m.p_lm.gen = m.d_gen;
+    m.p_emb_tok = EmbedParams{(const uint8_t*)emb->w, (const uint16_t*)emb->scales, (int)m.fmt, m.hidden,
+                              m.vocab, m.d_token, nullptr, m.d_x};
+    m.p_emb_prompt = EmbedParams{(const uint8_t*)emb->w, (const uint16_t*)emb->scales, (int)m.fmt, m.hidden,
+                                 m.vocab, m.d_prompt, m.d_pos, m.d_x};
+
+    HIP_TRY(c, hipDeviceSynchronize());
+    if (int rc = capture_step(c, true, &m.g_step)) { free_model(c); return rc; }
+    if (int rc = capture_step(c, false, &m.g_prefill)) { free_model(c); return rc; }
+    m.host_pos = 0;
+    m.ready = true;
+    return QORA_HIP_OK;
+}
+
+namespace {
+
+int set_device_pos(qora_hip_ctx* c, uint64_t pos) {
+    c->h_pin[2] = (int32_t)pos;
+    HIP_TRY(c, hipMemcpyAsync(c->m.d_pos, &c->h_pin[2], 4, hipMemcpyHostToDevice, c->stream));
+    HIP_TRY(c, hipStreamSynchronize(c->stream));
+    return QORA_HIP_OK;
+}
+
+int check_step_room(qora_hip_ctx* c, uint64_t steps) {
+    ModelState& m = c->m;
+    if (!m.ready) return fail(c, QORA_HIP_E_STATE, "model not initialised");
+    if (m.host_pos + steps > m.cap)
+        return fail(c, QORA_HIP_E_STATE, "KV cache full (capacity " + std::to_string(m.cap) + ")");
+    if (m.any_rope && m.host_pos + steps > m.rope_positions)
+        return fail(c, QORA_HIP_E_STATE, "position beyond the RoPE tables");
+    return QORA_HIP_OK;
+}
+
+int finish_step(qora_hip_ctx* c, float* logits, uint32_t* argmax) {
+    ModelState& m = c->m;
+    HIP_TRY(c, hipMemcpyAsync(&c->h_pin[1], m.d_token, 4, hipMemcpyDeviceToHost, c->stream));
+    if (logits) HIP_TRY(c, hipMemcpyAsync(logits, m.d_logits, (size_t)m.vocab * 4, hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(c, hipStreamSynchronize(c->stream));
+    if (argmax) *argmax = (uint32_t)c->h_pin[1];
+    return QORA_HIP_OK;
+}
+
+}  // namespace
+
+extern "C" int qora_hip_decode(qora_hip_ctx* c, uint32_t token, float* logits, uint32_t* argmax) {
+    if (!c) return QORA_HIP_E_INVALID;
+    if (int rc = check_step_room(c, 1)) return rc;
+    ModelState& m = c->m;
+    if (token >= m.vocab) return fail(c, QORA_HIP_E_INVALID, "token id out of range");
+    if (force_fail("launch")) return fail(c, QORA_HIP_E_DEVICE, "forced launch failure (QORA_HIP_FORCE_FAIL=launch)");
+    c->h_pin[0] = (int32_t)token;
+    HIP_TRY(c, hipMemcpyAsync(m.d_token, &c->h_pin[0], 4, hipMemcpyHostToDevice, c->stream));
+    HIP_TRY(c, hipGraphLaunch(m.g_step, c->stream));
+    if (int rc = finish_step(c, logits, argmax)) return rc;
+    m.host_pos += 1;
+    return QORA_HIP_OK;
+}
+
+extern "C" int qora_hip_generate_greedy(qora_hip_ctx* c, uint32_t token, uint32_t steps, uint32_t* out) {
+    if (!c || (!out && steps)) return fail(c, QORA_HIP_E_INVALID, "null argument");
+    if (int rc = check_step_room(c, steps)) return rc;
+    ModelState& m = c->m;
+    if (token >= m.vocab) return fail(c, QORA_HIP_E_INVALID, "token id out of range");
+    if (steps == 0) return QORA_HIP_OK;
+    if (force_fail("launch")) return fail(c, QORA_HIP_E_DEVICE, "forced launch failure (QORA_HIP_FORCE_FAIL=launch)");
+    c->h_pin[0] = (int32_t)token;
+    HIP_TRY(c, hipMemcpyAsync(m.d_token, &c->h_pin[0], 4, hipMemcpyHostToDevice, c->stream));
+    for (uint32_t i = 0; i < steps; ++i) HIP_TRY(c, hipGraphLaunch(m.g_step, c->stream));
+    HIP_TRY(c, hipMemcpyAsync(out, m.d_gen + m.host_pos, (size_t)steps * 4, hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(c, hipStreamSynchronize(c->stream));
+    m.host_pos += steps;
+    return QORA_HIP_OK;
+}
+
+extern "C" int qora_hip_prefill(qora_hip_ctx* c, const uint32_t* ids, size_t n, float* logits, uint32_t* argmax) {
+    if (!c || !ids) return fail(c, QORA_HIP_E_INVALID, "null argument");
+    ModelState& m = c->m;
+    if (!m.ready) return fail(c, QORA_HIP_E_STATE, "model not initialised");
+    if (n == 0) return fail(c, QORA_HIP_E_INVALID, "empty prompt");
+    for (size_t i = 0; i < n; ++i)
+        if (ids[i] >= m.vocab) return fail(c, QORA_HIP_E_INVALID, "token id out of range");
+    m.host_pos = 0;
+    if (int rc = set_device_pos(c, 0)) return rc;
+    if (int rc = check_step_room(c, n)) return rc;
+    if (force_fail("launch")) return fail(c, QORA_HIP_E_DEVICE, "forced launch failure (QORA_HIP_FORCE_FAIL=launch)");
+    HIP_TRY(c, hipMemcpy(m.d_prompt, ids, n * 4, hipMemcpyHostToDevice));
+    for (size_t i = 0; i + 1 < n; ++i) HIP_TRY(c, hipGraphLaunch(m.g_prefill, c->stream));
+    c->h_pin[0] = (int32_t)ids[n - 1];
+    HIP_TRY(c, hipMemcpyAsync(m.d_token, &c->h_pin[0], 4, hipMemcpyHostToDevice, c->stream));
+    HIP_TRY(c, hipGraphLaunch(m.g_step, c->stream));
+    if (int rc = finish_step(c, logits, argmax)) return rc;
+    m.host_pos = n;
+    return QORA_HIP_OK;
+}
+
+extern "C" int qora_hip_kv_len(qora_hip_ctx* c, uint64_t* len) {
+    if (!c || !len) return QORA_HIP_E_INVALID;
+    if (!c->m.ready) return fail(c, QORA_HIP_E_STATE, "model not initialised");
+    *len = c->m.host_pos;
+    return QORA_HIP_OK;
+}
+
+extern "C" int qora_hip_kv_reset(qora_hip_ctx* c) {
+    if (!c) return QORA_HIP_E_INVALID;
+    if (!c->m.ready) return fail(c, QORA_HIP_E_STATE, "model not initialised");
+    c->m.host_pos = 0;
+    return set_device_pos(c, 0);
+}
+
+extern "C" int qora_hip_kv_download(qora_hip_ctx* c, uint32_t layer, float* k, float* v) {
+    if (!c || !k || !v) return fail(c, QORA_HIP_E_INVALID, "null argument");
+    ModelState& m = c->m;
+    if (!m.ready) return fail(c, QORA_HIP_E_STATE, "model not initialised");
+    if (layer >= m.L) return fail(c, QORA_HIP_E_INVALID, "layer out of range");
+    const size_t kvd = (size_t)m.KVH * m.hd;
+    const size_t count = (size_t)m.host_pos * kvd;
+    HIP_TRY(c, hipStreamSynchronize(c->stream));
+    if (count == 0) return QORA_HIP_OK;
+    if (!m.kv_f16) {
+        HIP_TRY(c, hipMemcpy(k, (float*)m.d_k + (size_t)layer * m.cap * kvd, count * 4, hipMemcpyDeviceToHost));
+        HIP_TRY(c, hipMemcpy(v, (float*)m.d_v + (size_t)layer * m.cap * kvd, count * 4, hipMemcpyDeviceToHost));
+    } else {
+        std::vector<uint16_t> tmp(count);
+        HIP_TRY(c, hipMemcpy(tmp.data(), (uint16_t*)m.d_k + (size_t)layer * m.cap * kvd, count * 2, hipMemcpyDeviceToHost));
+        for (size_t i = 0; i < count; ++i) k[i] = h2f_host(tmp[i]);
+        HIP_TRY(c, hipMemcpy(tmp.data(), (uint16_t*)m.d_v + (size_t)layer * m.cap * kvd, count * 2, hipMemcpyDeviceToHost));
+        for (size_t i = 0; i < count; ++i) v[i] = h2f_host(tmp[i]);
+    }
+    return QORA_HIP_OK;
+}
+
+// ===========================================================================
+// memory / graph plumbing
+// ===========================================================================
+
+extern "C" int qora_hip_malloc(qora_hip_ctx* c, size_t bytes, void** dptr) {
+    if (!c || !dptr) return QORA_HIP_E_INVALID;
+    return dalloc(c, bytes, dptr);
+}
+
+extern "C" int qora_hip_free(qora_hip_ctx* c, void* dptr) {
+    if (!c) return QORA_HIP_E_INVALID;
+    if (dptr) HIP_TRY(c, hipFree(dptr));
+    return QORA_HIP_OK;
+}
+
+extern "C" int qora_hip_memcpy_h2d(qora_hip_ctx* c, void* dst, const void* src, size_t bytes) {
+    if (!c || (!dst && bytes) || (!src && bytes)) return QORA_HIP_E_INVALID;
+    HIP_TRY(c, hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, c->stream));
+    HIP_TRY(c, hipStreamSynchronize(c->stream));
+    return QORA_HIP_OK;
+}
+
+extern "C" int qora_hip_memcpy_d2h(qora_hip_ctx* c, void* dst, const void* src, size_t bytes) {
+    if (!c || (!dst && bytes) || (!src && bytes)) return QORA_HIP_E_INVALID;
+    HIP_TRY(c, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(c, hipStreamSynchronize(c->stream));
+    return QORA_HIP_OK;
+}
+
+extern "C" int qora_hip_synchronize(qora_hip_ctx* c) {
+    if (!c) return QORA_HIP_E_INVALID;
+    HIP_TRY(c, hipStreamSynchronize(c->stream));
+    return QORA_HIP_OK;
+}
+
+extern "C" void* qora_hip_stream(qora_hip_ctx* c) { return c ? (void*)c->stream : nullptr; }
+
+extern "C" int qora_hip_capture_begin(qora_hip_ctx* c) {
+    if (!c || c->capturing) return QORA_HIP_E_STATE;
+    HIP_TRY(c, hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
+    c->capturing = true;
+    return QORA_HIP_OK;
+}
+
+extern "C" int qora_hip_capture_end(qora_hip_ctx* c, void** graph_exec) {
+    if (!c || !c->capturing || !graph_exec) return QORA_HIP_E_STATE;
+    c->capturing = false;
+    hipGraph_t g = nullptr;
+    HIP_TRY(c, hipStreamEndCapture(c->stream, &g));
+    hipGraphExec_t ge = nullptr;
+    const hipError_t e = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) return fail(c, QORA_HIP_E_DEVICE, std::string("hipGraphInstantiate: ") + hipGetErrorString(e));
+    *graph_exec = (void*)ge;
+    return QORA_HIP_OK;
+}
+
+extern "C" int qora_hip_graph_launch(qora_hip_ctx* c, void* graph_exec, uint32_t count) {
+    if (!c || !graph_exec) return QORA_HIP_E_INVALID;
+    for (uint32_t i = 0; i < count; ++i) HIP_TRY(c, hipGraphLaunch((hipGraphExec_t)graph_exec, c->stream));
+    return QORA_HIP_OK;
+}
+
+extern "C" int qora_hip_graph_destroy(qora_hip_ctx* c, void* graph_exec) {
+    if (!c || !graph_exec) return QORA_HIP_E_INVALID;
+    HIP_TRY(c, hipGraphExecDestroy((hipGraphExec_t)graph_exec));
+    return QORA_HIP_OK;
+}
+
+// ===========================================================================
+// kernel-level entry points
+// ===========================================================================
+
+namespace {
+
+int gemv_entry(qora_hip_ctx* c, int fmt, const void* w0, const void* s0, const void* w1, const void* s1,
+               const float* x, float* y, uint64_t k, uint64_t n, bool paired, void* stream) {
+    if (!c) return QORA_HIP_E_INVALID;
+    if (!w0 || !x || !y || (fmt == FMT_Q4 && !s0) || (paired && (!w1 || (fmt == FMT_Q4 && !s1))))
+        return fail(c, QORA_HIP_E_INVALID, "null argument");
+    if (k == 0 || n == 0 || n % 32 != 0 || k > 0xFFFFFFFFull || n / 32 > 0xFFFFFFFFull)
+        return fail(c, QORA_HIP_E_INVALID, "GEMV needs k > 0 and n % 32 == 0");
+    const uint32_t G = (uint32_t)(n / 32);
+    const uint32_t groups[2] = {G, G};
+    GemvPlan pl;
+    if (!plan_gemv(fmt, (uint32_t)k, groups, paired ? 2 : 1, paired, c->cus, &pl))
+        return fail(c, QORA_HIP_E_INVALID, "unsupported GEMV shape");
+    if (int rc = ensure_ws(c, pl.partial_floats(), pl.tiles)) return rc;
+    GemvParams p{};
+    p.seg[0] = GemvSeg{(const uint8_t*)w0, (const uint16_t*)s0, G, 0, 0};
+    p.nseg = 1;
+    if (paired) {
+        p.seg[1] = GemvSeg{(const uint8_t*)w1, (const uint16_t*)s1, G, 0, 0};
+        p.nseg = 2;
+        p.paired = 1;
+    }
+    p.x = x;
+    p.k = (uint32_t)k;
+    p.partials = c->ws_part;
+    p.counters = c->ws_cnt;
+    p.epi = paired ? EPI_SILU : EPI_STORE;
+    p.y = y;
+    apply_plan(pl, &p);
+    HIP_TRY(c, launch_gemv(fmt, pl, p, pick_stream(c, stream)));
+    return QORA_HIP_OK;
+}
+
+int rowdot_entry(qora_hip_ctx* c, int fmt, const void* w, const void* s, const float* x, float* y, uint64_t rows,
+                 uint64_t cols, void* stream) {
+    if (!c) return QORA_HIP_E_INVALID;
+    if (!w || !x || !y || (fmt == FMT_Q4 && !s)) return fail(c, QORA_HIP_E_INVALID, "null argument");
+    if (rows == 0 || rows > 0xFFFFFFFFull || cols == 0 || cols % 32 != 0 || cols / 32 > 64 || 64 % (cols / 32) != 0)
+        return fail(c, QORA_HIP_E_INVALID, "row-dot GEMV needs cols % 32 == 0 and cols/32 dividing 64");
+    RowdotParams p{};
+    p.w = (const uint8_t*)w;
+    p.scales = (const uint16_t*)s;
+    p.rows = (uint32_t)rows;
+    p.cols = (uint32_t)cols;
+    p.x = x;
+    p.y = y;
+    HIP_TRY(c, launch_rowdot(fmt, rowdot_blocks(p.rows, p.cols, c->cus), p, pick_stream(c, stream)));
+    return QORA_HIP_OK;
+}
+
+}  // namespace
+
+extern "C" int qora_hip_gemv_q4(qora_hip_ctx* c, const void* packed, const void* scales, const float* x, float* y,
+                                uint64_t k, uint64_t n, void* stream) {
+    return gemv_entry(c, FMT_Q4, packed, scales, nullptr, nullptr, x, y, k, n, false, stream);
+}
+
+extern "C" int qora_hip_gemv_f16(qora_hip_ctx* c, const void* w, const float* x, float* y, uint64_t k, uint64_t n,
+                                 void* stream) {
+    return gemv_entry(c, FMT_F16, w, nullptr, nullptr, nullptr, x, y, k, n, false, stream);
+}
+
+extern "C" int qora_hip_gate_up_q4(qora_hip_ctx* c, const void* gp, const void* gs, const void* up, const void* us,
+                                   const float* x, float* out, uint64_t k, uint64_t n, void* stream) {
+    return gemv_entry(c, FMT_Q4, gp, gs, up, us, x, out, k, n, true, stream);
+}
+
+extern "C" int qora_hip_gate_up_f16(qora_hip_ctx* c, const void* gw, const void* uw, const float* x, float* out,
+                                    uint64_t k, uint64_t n, void* stream) {
+    return gemv_entry(c, FMT_F16, gw, nullptr, uw, nullptr, x, out, k, n, true, stream);
+}
+
+extern "C" int qora_hip_gemv_q4_rowdot(qora_hip_ctx* c, const void* packed, const void* scales, const float* x,
+                                       float* y, uint64_t rows, uint64_t cols, void* stream) {
+    return rowdot_entry(c, FMT_Q4, packed, scales, x, y, rows, cols, stream);
+}
+
+extern "C" int qora_hip_gemv_f16_rowdot(qora_hip_ctx* c, const void* w, const float* x, float* y, uint64_t rows,
+                                        uint64_t cols, void* stream) {
+    return rowdot_entry(c, FMT_F16, w, nullptr, x, y, rows, cols, stream);
+}
+
+extern "C" int qora_hip_dequant_q4(qora_hip_ctx* c, const void* packed, const void* scales, uint64_t k, uint64_t n,
+                                   float* out, void* stream) {
+    if (!c) return QORA_HIP_E_INVALID;
+    if (!packed || !scales || !out) return fail(c, QORA_HIP_E_INVALID, "null argument");
+    if (k == 0 || n == 0 || n % 32 != 0) return fail(c, QORA_HIP_E_INVALID, "dequant needs n % 32 == 0");
+    HIP_TRY(c, launch_dequant_q4((const uint8_t*)packed, (const uint16_t*)scales, k, n, out, pick_stream(c, stream)));
+    return QORA_HIP_OK;
+}
+
+extern "C" int qora_hip_rmsnorm(qora_hip_ctx* c, const float* x, const void* gamma, uint64_t n, float* out,
+                                void* stream) {
+    if (!c) return QORA_HIP_E_INVALID;
+    if (!x || !gamma || !out) return fail(c, QORA_HIP_E_INVALID, "null argument");
+    if (n == 0 || n > 0xFFFFFFFFull) return fail(c, QORA_HIP_E_INVALID, "bad length");
+    HIP_TRY(c, launch_rmsnorm(x, (const uint16_t*)gamma, (uint32_t)n, out, pick_stream(c, stream)));
+    return QORA_HIP_OK;
+}
+
+extern "C" int qora_hip_rope(qora_hip_ctx* c, float* data, uint32_t num_heads, uint32_t head_dim, const float* cos_t,
+                             const float* sin_t, uint32_t half_dim, uint32_t position, void* stream) {
+    if (!c) return QORA_HIP_E_INVALID;
+    if (!data || !cos_t || !sin_t) return fail(c, QORA_HIP_E_INVALID, "null argument");
+    if (num_heads == 0 || half_dim == 0 || 2 * half_dim > head_dim)
+        return fail(c, QORA_HIP_E_INVALID, "need 0 < 2*half_dim <= head_dim");
+    HIP_TRY(c, launch_rope(data, num_heads, head_dim, cos_t, sin_t, half_dim, position, pick_stream(c, stream)));
+    return QORA_HIP_OK;
+}
+
+extern "C" int qora_hip_attn_decode(qora_hip_ctx* c, const float* q, const void* kc, const void* vc, int kv_f16,
+                                    uint32_t L, uint32_t H, uint32_t KVH, uint32_t hd, float* out, void* stream) {
+    if (!c) return QORA_HIP_E_INVALID;
+    if (!q || !kc || !vc || !out) return fail(c, QORA_HIP_E_INVALID, "null argument");
+    if (L == 0 || H == 0 || KVH == 0 || H % KVH != 0 || H / KVH > (uint32_t)kAttnMaxGroups || hd == 0 ||
+        hd > (uint32_t)kAttnMaxHd)
+        return fail(c, QORA_HIP_E_INVALID, "attention needs L > 0, H % KVH == 0, H/KVH <= 4, head_dim <= 128");
+    AttnParams a{};
+    a.q = q;
+    a.kc = kc;
+    a.vc = vc;
+    a.kv_f16 = kv_f16 ? 1 : 0;
+    a.pos = nullptr;
+    a.L = L;
+    a.H = H;
+    a.KVH = KVH;
+    a.hd = hd;
+    a.groups = H / KVH;
+    a.scale = 1.0f / sqrtf((float)hd);
+    a.s_max = attn_splits(L);
+    if (int rc = ensure_attn_ws(c, (uint64_t)KVH * a.s_max * a.groups * (hd + 2), KVH)) return rc;
+    a.part = c->ws_attn_part;
+    a.counters = c->ws_attn_cnt;
+    a.out = out;
+    HIP_TRY(c, launch_attn(a, pick_stream(c, stream)));
+    return QORA_HIP_OK;
+}
+
+extern "C" int qora_hip_argmax(qora_hip_ctx* c, const float* logits, uint64_t n, int32_t* out, void* stream) {
+    if (!c) return QORA_HIP_E_INVALID;
+    if (!logits || !out) return fail(c, QORA_HIP_E_INVALID, "null argument");
+    if (n == 0 || n > 0x7FFFFFFFull) return fail(c, QORA_HIP_E_INVALID, "bad length");
+    HIP_TRY(c, launch_argmax(logits, (uint32_t)n, out, pick_stream(c, stream)));
+    return QORA_HIP_OK;
+}

@@ -1,0 +1,152 @@
+// Kernel instantiations and launch helpers (gfx950).
+#include "launch.hpp"
+#include "gemv.hpp"
+#include "attn.hpp"
+
+#include <algorithm>
+#include <cstdlib>
+
+namespace qora {
+
+static int env_int(const char* name, int dflt) {
+    const char* v = std::getenv(name);
+    return (v && *v) ? std::atoi(v) : dflt;
+}
+
+bool plan_gemv(int fmt, uint32_t k, const uint32_t* seg_groups, int nseg, bool paired, int cus,
+               GemvPlan* plan) {
+    if (k == 0 || nseg < 1 || nseg > 3) return false;
+    if (paired && (nseg != 2 || seg_groups[0] != seg_groups[1])) return false;
+    GemvPlan pl;
+    pl.gt = paired ? 16 : 8;
+    const int forced_gt = env_int("QORA_GEMV_GT", 0);
+    if (forced_gt == 8 || forced_gt == 16) pl.gt = paired ? 16 : forced_gt;
+    if (paired) {
+        pl.tiles = (seg_groups[0] + pl.gt / 2 - 1) / (pl.gt / 2);
+    } else {
+        pl.tiles = 0;
+        for (int i = 0; i < nseg; ++i) pl.tiles += (seg_groups[i] + pl.gt - 1) / pl.gt;
+    }
+    const uint32_t rl = 256 / pl.gt;
+    const int max_rpl = 16;
+    const uint32_t target = (uint32_t)std::max(1, cus) * 5 / 2;   // ~2.5 workgroups per CU
+    uint32_t s_des = std::max(1u, (target + pl.tiles / 2) / pl.tiles);
+    const uint32_t kr_des = (k + s_des - 1) / s_des;
+    const uint32_t rpl_des = std::max(1u, (kr_des + rl - 1) / rl);
+    int rpl = 1;
+    while (rpl < max_rpl && (uint32_t)rpl * 3 / 2 < rpl_des) rpl *= 2;   // nearest power of two
+    const int forced_rpl = env_int("QORA_GEMV_RPL", 0);
+    if (forced_rpl == 1 || forced_rpl == 2 || forced_rpl == 4 || forced_rpl == 8 || forced_rpl == 16)
+        rpl = forced_rpl;
+    // keep the number of partials each tile must add bounded
+    while (rpl < max_rpl && (k + rl * rpl - 1) / (rl * rpl) > 64) rpl *= 2;
+    pl.rpl = rpl;
+    pl.kr = rl * (uint32_t)rpl;
+    pl.splits = (k + pl.kr - 1) / pl.kr;
+    (void)fmt;
+    *plan = pl;
+    return true;
+}
+
+void apply_plan(const GemvPlan& plan, GemvParams* p) {
+    uint32_t t0 = 0;
+    for (int i = 0; i < p->nseg; ++i) {
+        p->seg[i].tile0 = p->paired ? 0 : t0;
+        p->seg[i].tiles = p->paired ? plan.tiles : (p->seg[i].groups + plan.gt - 1) / plan.gt;
+        t0 += p->seg[i].tiles;
+    }
+    p->tiles = plan.tiles;
+    p->splits = plan.splits;
+    p->rows_per_split = plan.kr;
+}
+
+template <int FMT, int GT>
+static hipError_t launch_gemv_gt(const GemvPlan& plan, const GemvParams& p, hipStream_t stream) {
+    const dim3 grid(plan.blocks()), block(256);
+    switch (plan.rpl) {
+    case 1: hipLaunchKernelGGL((gemv_splitk_kernel<FMT, GT, 1>), grid, block, 0, stream, p); break;
+    case 2: hipLaunchKernelGGL((gemv_splitk_kernel<FMT, GT, 2>), grid, block, 0, stream, p); break;
+    case 4: hipLaunchKernelGGL((gemv_splitk_kernel<FMT, GT, 4>), grid, block, 0, stream, p); break;
+    case 8: hipLaunchKernelGGL((gemv_splitk_kernel<FMT, GT, 8>), grid, block, 0, stream, p); break;
+    case 16: hipLaunchKernelGGL((gemv_splitk_kernel<FMT, GT, 16>), grid, block, 0, stream, p); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_gemv(int fmt, const GemvPlan& plan, const GemvParams& p, hipStream_t stream) {
+    if (plan.blocks() == 0) return hipErrorInvalidValue;
+    if (fmt == FMT_Q4) {
+        if (plan.gt == 8) return launch_gemv_gt<FMT_Q4, 8>(plan, p, stream);
+        if (plan.gt == 16) return launch_gemv_gt<FMT_Q4, 16>(plan, p, stream);
+    } else {
+        if (plan.gt == 8) return launch_gemv_gt<FMT_F16, 8>(plan, p, stream);
+        if (plan.gt == 16) return launch_gemv_gt<FMT_F16, 16>(plan, p, stream);
+    }
+    return hipErrorInvalidValue;
+}
+
+static constexpr int kRowdotU = 8;
+
+uint32_t rowdot_blocks(uint32_t rows, uint32_t cols, int cus) {
+    const uint32_t G = cols / 32;
+    const uint32_t rpw = G >= 64 ? 1 : 64 / G;
+    const uint64_t waves_needed = ((uint64_t)rows + (uint64_t)rpw * kRowdotU - 1) / ((uint64_t)rpw * kRowdotU);
+    const uint64_t blocks_needed = (waves_needed + 3) / 4;
+    const uint32_t cap = (uint32_t)std::max(1, cus) * 4;
+    return (uint32_t)std::max<uint64_t>(1, std::min<uint64_t>(blocks_needed, cap));
+}
+
+hipError_t launch_rowdot(int fmt, uint32_t blocks, const RowdotParams& p, hipStream_t stream) {
+    const dim3 grid(blocks), block(256);
+    if (fmt == FMT_Q4) hipLaunchKernelGGL((rowdot_kernel<FMT_Q4, kRowdotU>), grid, block, 0, stream, p);
+    else hipLaunchKernelGGL((rowdot_kernel<FMT_F16, 4>), grid, block, 0, stream, p);
+    return hipGetLastError();
+}
+
+uint32_t attn_splits(uint32_t capacity) { return (capacity + kAttnChunk - 1) / kAttnChunk; }
+
+hipError_t launch_attn(const AttnParams& p, hipStream_t stream) {
+    hipLaunchKernelGGL(attn_decode_kernel, dim3(p.s_max, p.KVH), dim3(256), 0, stream, p);
+    return hipGetLastError();
+}
+
+hipError_t launch_embed(const EmbedParams& p, hipStream_t stream) {
+    const uint32_t blocks = std::max(1u, std::min(64u, (p.hidden + 255) / 256));
+    hipLaunchKernelGGL(embed_kernel, dim3(blocks), dim3(256), 0, stream, p);
+    return hipGetLastError();
+}
+
+hipError_t launch_dequant_q4(const uint8_t* packed, const uint16_t* scales, uint64_t k, uint64_t n, float* out,
+                             hipStream_t stream) {
+    const uint64_t bytes = k * n / 2;
+    const uint32_t blocks = (uint32_t)std::max<uint64_t>(1, std::min<uint64_t>(4096, (bytes + 255) / 256));
+    hipLaunchKernelGGL(dequant_q4_kernel, dim3(blocks), dim3(256), 0, stream, packed, scales, k, n, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_rmsnorm(const float* x, const uint16_t* gamma, uint32_t n, float* out, hipStream_t stream) {
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(1), dim3(256), 0, stream, x, gamma, n, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_rope(float* data, uint32_t heads, uint32_t head_dim, const float* cos_t, const float* sin_t,
+                       uint32_t half, uint32_t position, hipStream_t stream) {
+    const uint32_t total = heads * half;
+    const uint32_t blocks = std::max(1u, std::min(256u, (total + 255) / 256));
+    hipLaunchKernelGGL(rope_kernel, dim3(blocks), dim3(256), 0, stream, data, heads, head_dim, cos_t, sin_t, half,
+                       position);
+    return hipGetLastError();
+}
+
+hipError_t launch_argmax(const float* logits, uint32_t n, int32_t* out, hipStream_t stream) {
+    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(256), 0, stream, logits, n, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_advance_pos(int32_t* pos, hipStream_t stream) {
+    hipLaunchKernelGGL(advance_pos_kernel, dim3(1), dim3(64), 0, stream, pos);
+    return hipGetLastError();
+}
+
+}  // namespace qora

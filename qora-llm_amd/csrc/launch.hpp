@@ -1,0 +1,49 @@
+// Host-side launch helpers for the decode kernels (internal to the library).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "params.hpp"
+
+namespace qora {
+
+// Launch shape of one split-K GEMV call site.
+struct GemvPlan {
+    int gt = 8;           // groups per column tile
+    int rpl = 4;          // rows per lane
+    uint32_t tiles = 0;   // column tiles
+    uint32_t splits = 0;  // K slices
+    uint32_t kr = 0;      // rows per K slice
+    uint32_t blocks() const { return tiles * splits; }
+    uint64_t partial_floats() const { return splits > 1 ? (uint64_t)splits * tiles * gt * 32 : 0; }
+};
+
+// Chooses GT / RPL / S for k input rows. seg_groups: groups (n/32) of each
+// segment; paired: gate/up lane pairing (two segments of equal groups).
+// cus: compute units on the device. Returns false if the shape is unsupported.
+bool plan_gemv(int fmt, uint32_t k, const uint32_t* seg_groups, int nseg, bool paired, int cus,
+               GemvPlan* plan);
+
+// Fills seg[].tile0/tiles, p.tiles/splits/rows_per_split from the plan.
+void apply_plan(const GemvPlan& plan, GemvParams* p);
+
+hipError_t launch_gemv(int fmt, const GemvPlan& plan, const GemvParams& p, hipStream_t stream);
+
+// Row-dot GEMV (lm_head). blocks: grid size (also the argmax partial count).
+uint32_t rowdot_blocks(uint32_t rows, uint32_t cols, int cus);
+hipError_t launch_rowdot(int fmt, uint32_t blocks, const RowdotParams& p, hipStream_t stream);
+
+uint32_t attn_splits(uint32_t capacity);
+hipError_t launch_attn(const AttnParams& p, hipStream_t stream);
+
+hipError_t launch_embed(const EmbedParams& p, hipStream_t stream);
+hipError_t launch_dequant_q4(const uint8_t* packed, const uint16_t* scales, uint64_t k, uint64_t n,
+                             float* out, hipStream_t stream);
+hipError_t launch_rmsnorm(const float* x, const uint16_t* gamma, uint32_t n, float* out, hipStream_t stream);
+hipError_t launch_rope(float* data, uint32_t heads, uint32_t head_dim, const float* cos_t, const float* sin_t,
+                       uint32_t half, uint32_t position, hipStream_t stream);
+hipError_t launch_argmax(const float* logits, uint32_t n, int32_t* out, hipStream_t stream);
+hipError_t launch_advance_pos(int32_t* pos, hipStream_t stream);
+
+}  // namespace qora

@@ -1,0 +1,104 @@
+"""Model-level parity on the GPU: raw_prefill / forward_decode_raw / greedy
+decode through the C ABI against the oracle on the same seeded weights."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import __graft_entry__ as entry
+from helpers import REL_TOL, rel_err
+
+pytestmark = pytest.mark.gpu
+
+
+def small_model(pkg, fmt, layers=4, seed=0):
+    cfg = entry.smoke_config(pkg)
+    cfg.num_layers = layers
+    return pkg.synthetic_model(cfg, seed=seed, fmt=fmt, rope_positions=128)
+
+
+@pytest.mark.parametrize("fmt", [1, 0])
+def test_prefill_decode_logits_and_kv_match_oracle(ctx, pkg, orc, fmt):
+    w = small_model(pkg, fmt)
+    prompt = pkg.synth_tokens(0, 2000, 13, w.config.vocab)
+    be = pkg.HipBackend(ctx, w, kv_capacity=128)
+    om = orc.OracleModel(w, kv_capacity=128, T=4)
+    logits, tok = be.raw_prefill(prompt)
+    ref = om.prefill(prompt)
+    assert rel_err(logits, ref) <= REL_TOL
+    assert tok == orc.argmax(ref)
+    assert be.kv_len() == len(prompt)
+    for layer in (0, 3):
+        k, v = be.kv_layer(layer)
+        kr, vr = om.kv_layer(layer)
+        assert k.shape == kr.shape
+        assert rel_err(k, kr) <= REL_TOL and rel_err(v, vr) <= REL_TOL
+    # teacher-forced decode: feed fixed tokens, compare every step
+    feed = pkg.synth_tokens(0, 2001, 20, w.config.vocab)
+    for t in feed:
+        logits, tok = be.forward_decode_raw(int(t))
+        ref = om.forward_decode(int(t))
+        assert rel_err(logits, ref) <= REL_TOL
+        gap = orc.top2_gap(ref)
+        if gap > 1e-4 * float(np.max(np.abs(ref))):
+            assert tok == orc.argmax(ref)
+    assert be.kv_len() == len(prompt) + len(feed)
+
+
+def test_greedy_tokens_match_oracle_small(ctx, pkg, orc):
+    w = small_model(pkg, 1, layers=8, seed=3)
+    prompt = pkg.synth_tokens(3, 2000, 16, w.config.vocab)
+    be = pkg.HipBackend(ctx, w, kv_capacity=128)
+    om = orc.OracleModel(w, kv_capacity=128, T=4)
+    ref, gaps = om.greedy(prompt, 64)
+    got = pkg.generate_greedy_host(be, prompt, 64)
+    assert got == ref
+    # the device-chained loop produces the same sequence
+    _, first = be.raw_prefill(prompt, want_logits=False)
+    chained = be.generate_greedy(first, 63)
+    assert [first] + chained.tolist() == ref
+
+
+def test_f16_kv_cache_close_to_f32(ctx, pkg, orc):
+    w = small_model(pkg, 1)
+    prompt = pkg.synth_tokens(0, 2000, 30, w.config.vocab)
+    be = pkg.HipBackend(ctx, w, kv_capacity=128, kv_dtype=pkg.KV_F16)
+    om = orc.OracleModel(w, kv_capacity=128, T=4)
+    logits, _ = be.raw_prefill(prompt)
+    ref = om.prefill(prompt)
+    # f16 K/V rounding (2^-11 relative) is the only difference from the f32 path
+    assert rel_err(logits, ref) <= 5e-3
+
+
+def test_state_errors(ctx, pkg):
+    w = small_model(pkg, 1, layers=4)
+    be = pkg.HipBackend(ctx, w, kv_capacity=8)
+    with pytest.raises(pkg.QoraHipError) as e:
+        be.forward_decode_raw(w.config.vocab)   # token out of range
+    assert e.value.code == pkg.QORA_HIP_E_INVALID
+    be.raw_prefill([1, 2, 3, 4, 5, 6, 7, 8])
+    with pytest.raises(pkg.QoraHipError) as e:
+        be.forward_decode_raw(1)               # cache full
+    assert e.value.code == pkg.QORA_HIP_E_STATE
+    be.kv_reset()
+    assert be.kv_len() == 0
+    be.forward_decode_raw(1)
+    assert be.kv_len() == 1
+    with pytest.raises(pkg.QoraHipError):
+        be.raw_prefill([])
+
+
+def test_qora_file_roundtrip_loads_same_model(ctx, pkg, tmp_path):
+    w = small_model(pkg, 1)
+    path = str(tmp_path / "m.qora")
+    pkg.save_model(w, path)
+    prompt = pkg.synth_tokens(0, 2000, 9, w.config.vocab)
+    be = pkg.HipBackend(ctx, w, kv_capacity=64)
+    ref, _ = be.raw_prefill(prompt)
+    ctx.check(ctx.lib.qora_hip_load_model(ctx.h, path.encode(), 64, 0), "load_model")
+    logits = np.empty(w.config.vocab, dtype=np.float32)
+    tok = ctypes.c_uint32()
+    ids = np.asarray(prompt, dtype=np.uint32)
+    ctx.check(ctx.lib.qora_hip_prefill(ctx.h, ids.ctypes.data, ids.size, logits.ctypes.data, ctypes.byref(tok)),
+              "prefill")
+    assert np.array_equal(logits, ref)
