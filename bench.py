@@ -1,0 +1,334 @@
+"""Decode benchmark: SmolLM3-3B architecture, random-init Q4 weights, batch 1.
+
+Workload: a 64-token random-ID prompt (seed 0) is prefilled, then greedy
+decode runs token by token through the C ABI (qora_hip_decode: one captured
+HIP graph per token, argmax read back to the host each step). W untimed
+warmup tokens, then exactly K timed tokens. `value` is decode tokens/s with
+the weights resident in HBM.
+
+Also reported on the same JSON line:
+  roofline     - the dominant kernel (fused gate/up Q4 GEMV, 2048 -> 2x11008)
+                 timed with HIP events on the stream it is launched on, over
+                 a graph of launches that rotate through >= 768 MB of distinct
+                 weight copies (so the 256 MB Infinity Cache cannot serve
+                 them); achieved = algorithmic bytes / average launch time.
+  cpu_baseline - the reference CPU algorithm (the C oracle: AVX-512 LUT
+                 GEMV, k-split into T partials) timed on this host's cores on
+                 a bounded sample of the same workload.
+  gemv_gbps    - every per-layer GEMV shape and the tied lm_head, same method.
+  tok_s_ctx2048 - decode rate with the KV cache at ~2048 positions.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+import __graft_entry__ as entry  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+PUBLISHED_GPU_TOK_S = 4.1   # reference README.md:43,157 (GTX 1660 SUPER, Vulkan)
+
+
+class Hip:
+    """The few HIP runtime calls the harness needs (events, D2D copies)."""
+
+    def __init__(self):
+        self.h = ctypes.CDLL("libamdhip64.so")
+        self.h.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        self.h.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        self.h.hipEventSynchronize.argtypes = [ctypes.c_void_p]
+        self.h.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+        self.h.hipEventDestroy.argtypes = [ctypes.c_void_p]
+        self.h.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+
+    def event(self):
+        e = ctypes.c_void_p()
+        assert self.h.hipEventCreate(ctypes.byref(e)) == 0
+        return e.value
+
+    def record(self, e, stream):
+        assert self.h.hipEventRecord(e, stream) == 0
+
+    def elapsed_ms(self, a, b):
+        assert self.h.hipEventSynchronize(b) == 0
+        ms = ctypes.c_float()
+        assert self.h.hipEventElapsedTime(ctypes.byref(ms), a, b) == 0
+        return ms.value
+
+    def d2d(self, dst, src, n):
+        assert self.h.hipMemcpy(dst, src, n, 3) == 0
+
+
+def q4_bytes(k, n):
+    """Algorithmic bytes of one Q4 GEMV: nibbles + f16 scales + f32 x + f32 y."""
+    return k * n // 2 + k * n // 16 + 4 * k + 4 * n
+
+
+EAGER = False   # --eager: no HIP graphs (rocprofv3 does not follow graph launches)
+
+
+def time_graph(ctx, hip, launch_fns, reps=3):
+    """Capture one launch per entry of launch_fns into a graph, replay it
+    `reps` times between HIP events on the context stream; return average
+    milliseconds per launch. With --eager the launches are issued directly."""
+    for f in launch_fns[:2]:
+        f()          # eager calls size the scratch before capture
+    ctx.synchronize()
+    if EAGER:
+        a, b = hip.event(), hip.event()
+        hip.record(a, ctx.stream)
+        for _ in range(reps):
+            for f in launch_fns:
+                f()
+        hip.record(b, ctx.stream)
+        return hip.elapsed_ms(a, b) / (reps * len(launch_fns))
+    ctx.capture_begin()
+    for f in launch_fns:
+        f()
+    g = ctx.capture_end()
+    try:
+        ctx.graph_launch(g, 1)
+        ctx.synchronize()
+        a, b = hip.event(), hip.event()
+        hip.record(a, ctx.stream)
+        ctx.graph_launch(g, reps)
+        hip.record(b, ctx.stream)
+        ms = hip.elapsed_ms(a, b)
+    finally:
+        ctx.graph_destroy(g)
+    return ms / (reps * len(launch_fns))
+
+
+class Pool:
+    """Rotating device copies of one weight so the working set exceeds MALL."""
+
+    def __init__(self, ctx, hip, srcs, min_bytes=768 << 20):
+        # srcs: list of (ptr, nbytes) parts of one weight
+        self.ctx = ctx
+        total = sum(nb for _, nb in srcs)
+        self.copies = max(4, math.ceil(min_bytes / total))
+        self.parts = []
+        for ptr, nb in srcs:
+            base = ctx.malloc(nb * self.copies)
+            for c in range(self.copies):
+                hip.d2d(base + c * nb, ptr, nb)
+            self.parts.append((base, nb))
+
+    def ptrs(self, c):
+        return [base + c * nb for base, nb in self.parts]
+
+    def free(self):
+        for base, _ in self.parts:
+            self.ctx.free(base)
+
+
+def gemv_roofline(ctx, hip, be, pkg):
+    """Per-shape GB/s of the Q4 GEMV kernel on the model's own weights: each
+    launch is one qora_hip_*_accumulate call (the decode step's kernel)."""
+    c = be.config
+    lib, h = ctx.lib, ctx.h
+    x = ctx.malloc(4 * c.intermediate)
+    acc = ctx.malloc(8 * 2 * c.intermediate)
+    ctx.h2d(x, pkg.synth_f32(0, 77, c.intermediate))
+    results = {}
+    shapes = c.weight_shapes()
+    for j, label in ((0, "q/o 2048x2048"), (1, "k/v 2048x512"), (6, "down 11008x2048")):
+        k, n = shapes[j]
+        wp, sp = ctx.weight_ptrs(int(be.wids[0, j]))
+        pool = Pool(ctx, hip, [(wp, k * n // 2), (sp, k * n // 16)])
+        fns = [(lambda p=pool.ptrs(i): ctx.check(lib.qora_hip_gemv_q4_accumulate(h, p[0], p[1], x, acc, k, n, None)))
+               for i in range(pool.copies)]
+        ms = time_graph(ctx, hip, fns)
+        pool.free()
+        results[label] = {"us": ms * 1e3, "gbps": q4_bytes(k, n) / (ms * 1e-3) / 1e9}
+    # fused gate+up (the dominant kernel)
+    k, n = shapes[4]
+    gw, gs = ctx.weight_ptrs(int(be.wids[0, 4]))
+    uw, us = ctx.weight_ptrs(int(be.wids[0, 5]))
+    pool = Pool(ctx, hip, [(gw, k * n // 2), (gs, k * n // 16), (uw, k * n // 2), (us, k * n // 16)])
+    fns = [(lambda p=pool.ptrs(i): ctx.check(
+        lib.qora_hip_gate_up_q4_accumulate(h, p[0], p[1], p[2], p[3], x, acc, k, n, None)))
+        for i in range(pool.copies)]
+    ms = time_graph(ctx, hip, fns)
+    pool.free()
+    gu_bytes = 2 * (k * n // 2 + k * n // 16) + 4 * k + 4 * n
+    results["gate+up 2048x(2x11008)"] = {"us": ms * 1e3, "gbps": gu_bytes / (ms * 1e-3) / 1e9, "bytes": gu_bytes}
+    # tied lm_head, row-dot
+    ew, es = ctx.weight_ptrs(be.embed_wid)
+    V, Hd = c.vocab, c.hidden
+    pool = Pool(ctx, hip, [(ew, V * Hd // 2), (es, V * Hd // 16)])
+    lm = ctx.malloc(4 * V)
+    fns = [(lambda p=pool.ptrs(i): ctx.check(lib.qora_hip_gemv_q4_rowdot(h, p[0], p[1], x, lm, V, Hd, None)))
+           for i in range(pool.copies)]
+    ms = time_graph(ctx, hip, fns)
+    pool.free()
+    ctx.free(lm)
+    results["lm_head 128256x2048"] = {"us": ms * 1e3, "gbps": q4_bytes(V, Hd) / (ms * 1e-3) / 1e9}
+    ctx.free(x)
+    ctx.free(acc)
+    return results
+
+
+def cpu_baseline(pkg, orc, w, prompt, seconds=15.0, threads=16):
+    """Reference CPU algorithm (oracle) on this host: prefill 8 prompt tokens,
+    then decode tokens until `seconds` of decode time have passed."""
+    threads = max(1, min(threads, os.cpu_count() or 1))
+    orc.set_threads(threads)
+    om = orc.OracleModel(w, kv_capacity=256, T=threads)
+    logits = om.prefill(prompt[:8])
+    tok = orc.argmax(logits)
+    n = 0
+    t0 = time.perf_counter()
+    while True:
+        logits = om.forward_decode(tok)
+        tok = orc.argmax(logits)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or n >= 200:
+            break
+    return {"value": n / el, "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"C restatement of the reference CPU path (AVX-512 LUT GEMV, k-split T={threads}); "
+                      f"8-token prefill then {n} greedy decode tokens of the same model, {el:.1f} s"}
+
+
+def read_traffic(path):
+    """HBM bytes per launch of the dominant kernel from a committed rocprofv3
+    --pmc summary (line 'traffic_bytes_per_launch: N'), else None."""
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.strip().startswith("traffic_bytes_per_launch:"):
+                    return float(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=128)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-gemv", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--eager", action="store_true",
+                    help="launch every kernel directly instead of replaying HIP graphs (for rocprofv3)")
+    args = ap.parse_args()
+    if args.eager:
+        global EAGER
+        EAGER = True
+        os.environ["QORA_HIP_EAGER"] = "1"
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; multi-GPU scaling is not part of it",
+                          "n_gpus": args.gpus}))
+        sys.exit(2)
+    prompt_len, cap = 64, 2048
+    if prompt_len + args.warmup + args.steps > cap:
+        sys.exit("warmup + steps exceed the 2048-position KV cache")
+
+    pkg = entry.load_package()
+    cfg = pkg.SMOLLM3_3B
+    t0 = time.perf_counter()
+    w = pkg.synthetic_model(cfg, seed=0, rope_positions=cap)
+    prompt = pkg.synth_tokens(0, 2000, prompt_len, cfg.vocab)
+    print(f"# synthetic model ready in {time.perf_counter() - t0:.1f}s", file=sys.stderr, flush=True)
+    hip = Hip()
+    ctx = pkg.HipContext(0)
+    be = pkg.HipBackend(ctx, w, kv_capacity=cap, kv_dtype=pkg.KV_F32)
+    print(f"# model on device ({ctx.cus} CUs)", file=sys.stderr, flush=True)
+
+    _, tok = be.raw_prefill(prompt, want_logits=False)
+    for _ in range(args.warmup):
+        _, tok = be.forward_decode_raw(tok, want_logits=False)
+    ctx.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        _, tok = be.forward_decode_raw(tok, want_logits=False)
+    ctx.synchronize()
+    dt = time.perf_counter() - t0
+    tok_s = args.steps / dt
+    print(f"# decode {tok_s:.1f} tok/s ({dt / args.steps * 1e3:.3f} ms/token)", file=sys.stderr, flush=True)
+
+    # device-chained greedy loop (no host round trip per token)
+    be.kv_reset()
+    _, tok = be.raw_prefill(prompt, want_logits=False)
+    ctx.synchronize()
+    t0 = time.perf_counter()
+    be.generate_greedy(tok, args.steps)
+    chained = args.steps / (time.perf_counter() - t0)
+
+    # decode at ~2048 context: prefill 1920 positions, then time 120 tokens
+    long_prompt = pkg.synth_tokens(0, 2002, cap - 128, cfg.vocab)
+    _, tok = be.raw_prefill(long_prompt, want_logits=False)
+    ctx.synchronize()
+    n_long = 120
+    t0 = time.perf_counter()
+    for _ in range(n_long):
+        _, tok = be.forward_decode_raw(tok, want_logits=False)
+    ctx.synchronize()
+    tok_s_2048 = n_long / (time.perf_counter() - t0)
+    print(f"# decode at ctx ~2048: {tok_s_2048:.1f} tok/s", file=sys.stderr, flush=True)
+
+    gemv = {} if args.no_gemv else gemv_roofline(ctx, hip, be, pkg)
+    for kname, v in gemv.items():
+        print(f"# {kname}: {v['us']:.2f} us, {v['gbps']:.0f} GB/s", file=sys.stderr, flush=True)
+
+    roofline = None
+    if gemv:
+        gu = gemv["gate+up 2048x(2x11008)"]
+        roofline = {"bound": "hbm", "achieved": round(gu["gbps"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(gu["gbps"] / HBM_PEAK_GBS, 4),
+                    "traffic": read_traffic(os.path.join(ROOT, "profiles", "gate_up_q4_2048x11008_pmc.md")),
+                    "kernel": "gemv_kernel<Q4,GT=16> paired gate|up (qora_hip_gate_up_q4_accumulate)",
+                    "algorithmic_bytes_per_launch": gu["bytes"], "avg_launch_us": round(gu["us"], 3)}
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        orc = entry.load_oracle()
+        cpu = cpu_baseline(pkg, orc, w, prompt, seconds=args.cpu_seconds)
+        print(f"# cpu baseline {cpu['value']:.2f} tok/s on {cpu['cores']} threads", file=sys.stderr, flush=True)
+
+    weight_bytes = w.weight_bytes_per_token()
+    out = {
+        "metric": "decode tok/s (SmolLM3-3B Q4, bs=1) + Q4 GEMV HBM GB/s vs ~8 TB/s peak",
+        "value": round(tok_s, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dt / args.steps * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": round(tok_s / PUBLISHED_GPU_TOK_S, 1),
+        "dtype": "f32",
+        "data": "synthetic (seeded random-init weights and token ids)",
+        "config": {"workload": "SmolLM3-3B architecture (36 layers, hidden 2048, 16q/4kv heads, hd 128, "
+                               "inter 11008, vocab 128256 tied), Q4 g32 weights, 64-token prompt then greedy "
+                               "decode, f32 KV cache of 2048 positions, host-driven one token per call",
+                   "prompt_tokens": prompt_len, "kv_capacity": cap, "kv_dtype": "f32", "batch": 1, "seed": 0},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "weight_roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / weight_bytes, 1),
+        "frac_of_weight_roofline": round(tok_s * weight_bytes / (HBM_PEAK_GBS * 1e9), 4),
+        "tok_s_device_chained": round(chained, 2),
+        "tok_s_ctx2048": round(tok_s_2048, 2),
+        "gemv_gbps": {k2: round(v["gbps"], 1) for k2, v in gemv.items()},
+        "vs_baseline_ref": "reference GPU decode ~4.1 tok/s (README.md:43,157, GTX 1660 SUPER)",
+    }
+    ctx.close()
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -140,6 +140,17 @@ int qora_hip_gemv_q4(qora_hip_ctx* ctx, const void* packed, const void* scales, 
 /* gemv_f16 (gemv.rs:534-567; simd.rs:151-176). */
 int qora_hip_gemv_f16(qora_hip_ctx* ctx, const void* w, const float* x, float* y, uint64_t k, uint64_t n,
                       void* stream);
+/* Single-launch forms of the two GEMVs above, used inside the decode step:
+ * acc[j] += (x . W)[j] as fixed point (int64, value = acc / 2^36), so the
+ * split-K partial sums land in any order with identical results. gate_up
+ * accumulates gate into acc[0:n] and up into acc[n:2n]. acc_to_f32 converts
+ * (paired: y = silu(acc[0:n]) * acc[n:2n], the epilogue of gemv.rs:494-500). */
+int qora_hip_gemv_q4_accumulate(qora_hip_ctx* ctx, const void* packed, const void* scales, const float* x,
+                                long long* acc, uint64_t k, uint64_t n, void* stream);
+int qora_hip_gate_up_q4_accumulate(qora_hip_ctx* ctx, const void* gate_packed, const void* gate_scales,
+                                   const void* up_packed, const void* up_scales, const float* x, long long* acc,
+                                   uint64_t k, uint64_t n, void* stream);
+int qora_hip_acc_to_f32(qora_hip_ctx* ctx, const long long* acc, uint64_t n, int paired, float* y, void* stream);
 /* lm_head_parallel_q4 / _f16 (gemv.rs:797-864): y[r] = sum_c x[c] W[r][c]
  * over a [rows][cols] matrix (the tied embedding); cols/32 must divide 64. */
 int qora_hip_gemv_q4_rowdot(qora_hip_ctx* ctx, const void* packed, const void* scales, const float* x,

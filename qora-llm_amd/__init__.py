@@ -94,6 +94,9 @@ SIGNATURES = {
     "qora_hip_graph_destroy": (_I, [_P, _P]),
     "qora_hip_gemv_q4": (_I, [_P, _P, _P, _P, _P, _U64, _U64, _P]),
     "qora_hip_gemv_f16": (_I, [_P, _P, _P, _P, _U64, _U64, _P]),
+    "qora_hip_gemv_q4_accumulate": (_I, [_P, _P, _P, _P, _P, _U64, _U64, _P]),
+    "qora_hip_gate_up_q4_accumulate": (_I, [_P, _P, _P, _P, _P, _P, _P, _U64, _U64, _P]),
+    "qora_hip_acc_to_f32": (_I, [_P, _P, _U64, _I, _P, _P]),
     "qora_hip_gemv_q4_rowdot": (_I, [_P, _P, _P, _P, _P, _U64, _U64, _P]),
     "qora_hip_gemv_f16_rowdot": (_I, [_P, _P, _P, _P, _U64, _U64, _P]),
     "qora_hip_gate_up_q4": (_I, [_P, _P, _P, _P, _P, _P, _P, _U64, _U64, _P]),

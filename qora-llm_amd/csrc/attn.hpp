@@ -12,27 +12,61 @@ namespace qora {
 // GQA decode attention (gemv.rs:914-989 + softmax_raw gemv.rs:782-793).
 // Head h reads KV head h / groups. The KV cache is token-major
 // [capacity][kv_heads][head_dim] (RawKvCache, gemv.rs:154-156), f32 or f16.
-// Split-K over positions ("flash decoding"): block (s, kvh) takes CHUNK
-// positions, stages K and V in LDS, computes the scores of all `groups`
-// query heads of that KV head, and writes an unnormalised partial
-// (max, sum of exp, sum of exp*V). The last block of a KV head merges the
-// partials of the active splits in split order (deterministic).
-// The length L = *pos + 1 is read on the device, so the launch shape is
-// fixed for a given capacity and the step can be replayed from a graph.
-// Limits (checked on the host): head_dim <= 128, groups <= 4, CHUNK = 32.
+// Split over positions ("flash decoding"): block (s, kvh) takes `chunk`
+// positions in sub-chunks of 32 staged in LDS, runs an online softmax for
+// the `groups` query heads of that KV head and writes an unnormalised
+// partial (running max m, sum of exp l, sum of exp*V). The partials are
+// merged by the consumer (the o-projection prologue, or
+// attn_combine_kernel for the kernel-level entry point), in split order.
+// Model mode (qkv_acc set): q, k, v are read from the fixed-point q|k|v
+// accumulator of the QKV GEMV; q and k are rotated (apply_rope_raw at the
+// position being appended, gemv.rs:903-906) and the block that owns the new
+// position writes its K and V rows into the cache (gemv.rs:909-911).
+// L = *pos + 1 is read on the device, so the launch shape is fixed for a
+// given capacity and the step can be replayed from a graph.
+// Limits (checked on the host): head_dim <= 128, groups <= 4.
 // ---------------------------------------------------------------------------
 
+// Rotated value of dim d of a head whose un-rotated values are v[0..hd).
+__device__ __forceinline__ float rope_at(const float* v, uint32_t d, uint32_t half, const float* ct,
+                                         const float* st) {
+    if (d < half) return v[d] * ct[d] - v[d + half] * st[d];
+    if (d < 2 * half) return v[d] * ct[d - half] + v[d - half] * st[d - half];
+    return v[d];
+}
+
+template <int DPL>
+__device__ __forceinline__ void load_v_row(const AttnParams& p, uint64_t idx, float* v) {
+    if (p.kv_f16) {
+        const uint16_t* src = reinterpret_cast<const uint16_t*>(p.vc) + idx;
+#pragma unroll
+        for (int i = 0; i < DPL; ++i) v[i] = h2f(src[i]);
+    } else {
+        const float* src = reinterpret_cast<const float*>(p.vc) + idx;
+        if constexpr (DPL == 2) {
+            const float2 f = *reinterpret_cast<const float2*>(src);
+            v[0] = f.x;
+            v[1] = f.y;
+        } else {
+            v[0] = src[0];
+        }
+    }
+}
+
+// One wave per query head; lanes (half, r) = (lane / 32, lane % 32) own
+// position c0 + r and half of the head dims for q.k, then lanes own DPL
+// dims each for p.V. K and V are read straight from the cache (all loads of
+// a 32-position pass are issued before the math). No block-wide barrier
+// inside the position loop: each wave runs its own online softmax.
+template <int DPL>
 __global__ __launch_bounds__(256) void attn_decode_kernel(AttnParams p) {
     constexpr int NT = 256;
-    constexpr int C = kAttnChunk;
-    constexpr int KS = kAttnMaxHd + 1;   // padded LDS row
-    __shared__ float ks[C * KS];
-    __shared__ float vs[C * kAttnMaxHd];
+    constexpr int SUB = kAttnSub;                    // positions per pass (32)
     __shared__ float qs[kAttnMaxGroups * kAttnMaxHd];
-    __shared__ float sc[kAttnMaxGroups * C];
-    __shared__ float smax[kAttnMaxGroups];
-    __shared__ float ssum[kAttnMaxGroups];
-    __shared__ int s_last;
+    __shared__ float raw[(kAttnMaxGroups + 2) * kAttnMaxHd];
+    __shared__ float knew[kAttnMaxHd];
+    __shared__ float vnew[kAttnMaxHd];
+    __shared__ float es[kAttnMaxGroups * SUB];
 
     const int t = threadIdx.x;
     const int lane = t & (kWave - 1);
@@ -40,99 +74,193 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnParams p) {
     const uint32_t split = blockIdx.x;
     const uint32_t kvh = blockIdx.y;
     const uint32_t L = p.pos ? (uint32_t)(*p.pos) + 1u : p.L;
-    const uint32_t s_act = (L + C - 1) / C;
-    if (split >= s_act) return;
+    const uint32_t p0 = split * p.chunk;
+    if (p0 >= L) return;
+    const uint32_t p1 = min(L, p0 + p.chunk);
     const uint32_t hd = p.hd, G = p.groups;
-    const uint32_t p0 = split * C;
-    const uint32_t cn = min((uint32_t)C, L - p0);
     const uint64_t kv_stride = (uint64_t)p.KVH * hd;
+    const uint32_t cur = L - 1;                        // position appended this step
+    const bool model = p.qkv_acc != nullptr;
+    const bool has_new = model && cur >= p0 && cur < p1;
 
-    // stage K, V rows [p0, p0+cn) of this KV head and the group's q heads
-    for (uint32_t i = t; i < (uint32_t)C * hd; i += NT) {
-        const uint32_t r = i / hd, d = i % hd;
-        float kv = 0.f, vv = 0.f;
-        if (r < cn) {
-            const uint64_t idx = (uint64_t)(p0 + r) * kv_stride + (uint64_t)kvh * hd + d;
-            if (p.kv_f16) {
-                kv = h2f(reinterpret_cast<const uint16_t*>(p.kc)[idx]);
-                vv = h2f(reinterpret_cast<const uint16_t*>(p.vc)[idx]);
+    // ---- q of the group's heads (and the new k, v) ----
+    if (model) {
+        const uint32_t qd = p.H * hd;
+        for (uint32_t i = t; i < G * hd; i += NT) raw[i] = from_fixed(p.qkv_acc[(uint64_t)kvh * G * hd + i]);
+        if (has_new)
+            for (uint32_t d = t; d < hd; d += NT) {
+                raw[G * hd + d] = from_fixed(p.qkv_acc[qd + (uint64_t)kvh * hd + d]);
+                raw[(G + 1) * hd + d] = from_fixed(p.qkv_acc[qd + kv_stride + (uint64_t)kvh * hd + d]);
+            }
+        __syncthreads();
+        const float* ct = p.rope_cos + (uint64_t)cur * p.half;
+        const float* st = p.rope_sin + (uint64_t)cur * p.half;
+        for (uint32_t i = t; i < G * hd; i += NT)
+            qs[i] = p.use_rope ? rope_at(raw + (i / hd) * hd, i % hd, p.half, ct, st) : raw[i];
+        if (has_new)
+            for (uint32_t d = t; d < hd; d += NT) {
+                float kv = p.use_rope ? rope_at(raw + G * hd, d, p.half, ct, st) : raw[G * hd + d];
+                float vv = raw[(G + 1) * hd + d];
+                const uint64_t idx = (uint64_t)cur * kv_stride + (uint64_t)kvh * hd + d;
+                if (p.kv_f16) {
+                    const uint16_t kh = f2h(kv), vh = f2h(vv);
+                    reinterpret_cast<uint16_t*>(p.kc)[idx] = kh;
+                    reinterpret_cast<uint16_t*>(p.vc)[idx] = vh;
+                    kv = h2f(kh);   // use the stored value, as later steps will
+                    vv = h2f(vh);
+                } else {
+                    reinterpret_cast<float*>(p.kc)[idx] = kv;
+                    reinterpret_cast<float*>(p.vc)[idx] = vv;
+                }
+                knew[d] = kv;
+                vnew[d] = vv;
+            }
+    } else {
+        for (uint32_t i = t; i < G * hd; i += NT) qs[i] = p.q[(uint64_t)kvh * G * hd + i];
+    }
+    __syncthreads();
+
+    const uint32_t g = (uint32_t)wave;
+    if (g >= G) return;
+    const float* qg = qs + g * hd;
+    const uint32_t hh = hd / 2;                      // dims per half for q.k
+    const uint32_t half_id = (uint32_t)lane / 32, r_lane = (uint32_t)lane % 32;
+    const uint32_t dq0 = half_id * hh;
+    const uint32_t dv0 = (uint32_t)lane * DPL;       // dims of this lane for p.V
+    const bool vlane = dv0 < hd;
+    float m = -INFINITY, l = 0.f;
+    float acc[DPL];
+#pragma unroll
+    for (int i = 0; i < DPL; ++i) acc[i] = 0.f;
+
+    for (uint32_t c0 = p0; c0 < p1; c0 += SUB) {
+        const uint32_t cn = min((uint32_t)SUB, p1 - c0);
+        // V rows of this pass (independent of the scores: issue first)
+        float vr[SUB][DPL];
+#pragma unroll
+        for (int r = 0; r < SUB; ++r) {
+            const uint32_t ps = c0 + (uint32_t)r;
+            if ((uint32_t)r < cn && vlane) {
+                if (has_new && ps == cur) {
+#pragma unroll
+                    for (int i = 0; i < DPL; ++i) vr[r][i] = vnew[dv0 + i];
+                } else {
+                    load_v_row<DPL>(p, (uint64_t)ps * kv_stride + (uint64_t)kvh * hd + dv0, vr[r]);
+                }
             } else {
-                kv = reinterpret_cast<const float*>(p.kc)[idx];
-                vv = reinterpret_cast<const float*>(p.vc)[idx];
+#pragma unroll
+                for (int i = 0; i < DPL; ++i) vr[r][i] = 0.f;
             }
         }
-        ks[r * KS + d] = kv;
-        vs[r * kAttnMaxHd + d] = vv;
+        // q.k for position c0 + r_lane over dims [dq0, dq0 + hh)
+        float s = 0.f;
+        const uint32_t ps = c0 + r_lane;
+        if (r_lane < cn) {
+            float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+            if (has_new && ps == cur) {
+                for (uint32_t d = 0; d < hh; d += 4) {
+                    a0 = fmaf(qg[dq0 + d], knew[dq0 + d], a0);
+                    a1 = fmaf(qg[dq0 + d + 1], knew[dq0 + d + 1], a1);
+                    a2 = fmaf(qg[dq0 + d + 2], knew[dq0 + d + 2], a2);
+                    a3 = fmaf(qg[dq0 + d + 3], knew[dq0 + d + 3], a3);
+                }
+            } else {
+                const uint64_t base = (uint64_t)ps * kv_stride + (uint64_t)kvh * hd + dq0;
+                if (p.kv_f16) {
+                    const uint16_t* kr = reinterpret_cast<const uint16_t*>(p.kc) + base;
+                    for (uint32_t d = 0; d < hh; d += 4) {
+                        const uint2 w = *reinterpret_cast<const uint2*>(kr + d);
+                        a0 = fmaf(qg[dq0 + d], h2f((uint16_t)(w.x & 0xFFFFu)), a0);
+                        a1 = fmaf(qg[dq0 + d + 1], h2f((uint16_t)(w.x >> 16)), a1);
+                        a2 = fmaf(qg[dq0 + d + 2], h2f((uint16_t)(w.y & 0xFFFFu)), a2);
+                        a3 = fmaf(qg[dq0 + d + 3], h2f((uint16_t)(w.y >> 16)), a3);
+                    }
+                } else {
+                    const float* kr = reinterpret_cast<const float*>(p.kc) + base;
+                    for (uint32_t d = 0; d < hh; d += 4) {
+                        const float4 w = *reinterpret_cast<const float4*>(kr + d);
+                        a0 = fmaf(qg[dq0 + d], w.x, a0);
+                        a1 = fmaf(qg[dq0 + d + 1], w.y, a1);
+                        a2 = fmaf(qg[dq0 + d + 2], w.z, a2);
+                        a3 = fmaf(qg[dq0 + d + 3], w.w, a3);
+                    }
+                }
+            }
+            s = (a0 + a1) + (a2 + a3);
+        }
+        s += __shfl_xor(s, 32, kWave);
+        s = (r_lane < cn) ? s * p.scale : -INFINITY;
+        // online softmax over the pass (lanes r and r + 32 hold the same score)
+        const float m_new = fmaxf(m, wave_max(s));
+        const float f = expf(m - m_new);          // 0 on the first pass
+        const float e = (r_lane < cn) ? expf(s - m_new) : 0.f;
+        l = l * f + wave_sum(half_id == 0 ? e : 0.f);
+        m = m_new;
+        if (half_id == 0) es[g * SUB + r_lane] = e;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (int i = 0; i < DPL; ++i) acc[i] *= f;
+#pragma unroll
+        for (int r = 0; r < SUB; ++r) {
+            const float er = es[g * SUB + r];     // zero beyond cn
+#pragma unroll
+            for (int i = 0; i < DPL; ++i) acc[i] = fmaf(er, vr[r][i], acc[i]);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
-    for (uint32_t i = t; i < G * hd; i += NT) qs[i] = p.q[(uint64_t)(kvh * G) * hd + i];
-    __syncthreads();
+    float* part = p.part + (((uint64_t)kvh * p.s_max + split) * G + g) * (hd + 2);
+    if (vlane) {
+#pragma unroll
+        for (int i = 0; i < DPL; ++i)
+            if (dv0 + i < hd) part[dv0 + i] = acc[i];
+    }
+    if (lane == 0) {
+        part[hd] = m;
+        part[hd + 1] = l;
+    }
+}
 
-    // scores[g][r] = (q_g . k_r) * scale
-    for (uint32_t i = t; i < G * C; i += NT) {
-        const uint32_t g = i / C, r = i % C;
-        float dot = 0.f;
-        if (r < cn) {
-            const float* kr = ks + r * KS;
-            const float* qg = qs + g * hd;
-            for (uint32_t d = 0; d < hd; ++d) dot = fmaf(qg[d], kr[d], dot);
-            dot *= p.scale;
-        }
-        sc[g * C + r] = dot;
-    }
-    __syncthreads();
-    // per head: max and sum of exp over the chunk (one wave per head)
-    for (uint32_t g = wave; g < G; g += NT / kWave) {
-        const float v = (lane < (int)cn) ? sc[g * C + lane] : -INFINITY;
-        const float m = wave_max(v);
-        const float e = (lane < (int)cn) ? expf(v - m) : 0.f;
-        const float s = wave_sum(e);
-        if (lane < C) sc[g * C + lane] = e;
-        if (lane == 0) { smax[g] = m; ssum[g] = s; }
-    }
-    __syncthreads();
-    // unnormalised output: sum_r e[g][r] * V[r][d]
-    float* part = p.part + (((uint64_t)kvh * p.s_max + split) * G) * (hd + 2);
-    for (uint32_t i = t; i < G * hd; i += NT) {
-        const uint32_t g = i / hd, d = i % hd;
-        float acc = 0.f;
-        for (uint32_t r = 0; r < cn; ++r) acc = fmaf(sc[g * C + r], vs[r * kAttnMaxHd + d], acc);
-        part[g * (hd + 2) + d] = acc;
-    }
-    if (t < (int)G) {
-        part[t * (hd + 2) + hd] = smax[t];
-        part[t * (hd + 2) + hd + 1] = ssum[t];
-    }
-    __threadfence();
-    __syncthreads();
-    if (t == 0) {
-        const uint32_t prev = __hip_atomic_fetch_add(&p.counters[kvh], 1u, __ATOMIC_ACQ_REL,
-                                                     __HIP_MEMORY_SCOPE_AGENT);
-        s_last = (prev == s_act - 1) ? 1 : 0;
-    }
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-    // merge the s_act partials of every head of this KV head
-    const float* base = p.part + ((uint64_t)kvh * p.s_max * G) * (hd + 2);
-    for (uint32_t i = t; i < G * hd; i += NT) {
-        const uint32_t g = i / hd, d = i % hd;
+// Merge of the split partials into the attention output, one block per
+// query head: out = sum_s acc_s e^(m_s - m) / sum_s l_s e^(m_s - m).
+__global__ __launch_bounds__(256) void attn_combine_kernel(AttnCombineParams p) {
+    __shared__ float w[kAttnMaxSplits];
+    __shared__ float s_inv;
+    const uint32_t h = blockIdx.x;
+    const uint32_t hd = p.hd, G = p.groups, kvh = h / G, g = h % G;
+    const uint32_t L = p.pos ? (uint32_t)(*p.pos) + 1u : p.L;
+    const uint32_t s_act = min(p.s_max, (L + p.chunk - 1) / p.chunk);
+    const float* base = p.part + ((uint64_t)kvh * p.s_max * G + g) * (hd + 2);
+    if (threadIdx.x < kWave) {
+        const int lane = threadIdx.x;
         float m = -INFINITY;
-        for (uint32_t s = 0; s < s_act; ++s) m = fmaxf(m, base[(s * G + g) * (hd + 2) + hd]);
-        float num = 0.f, den = 0.f;
-        for (uint32_t s = 0; s < s_act; ++s) {
-            const float* ps = base + (s * G + g) * (hd + 2);
-            const float w = expf(ps[hd] - m);
-            num = fmaf(ps[d], w, num);
-            den = fmaf(ps[hd + 1], w, den);
+        for (uint32_t s = lane; s < s_act; s += kWave) m = fmaxf(m, base[(uint64_t)s * G * (hd + 2) + hd]);
+        m = wave_max(m);
+        float den = 0.f;
+        for (uint32_t s = lane; s < s_act; s += kWave) {
+            const float* ps = base + (uint64_t)s * G * (hd + 2);
+            const float e = expf(ps[hd] - m);
+            w[s] = e;
+            den += ps[hd + 1] * e;
         }
-        p.out[(uint64_t)(kvh * G + g) * hd + d] = num / den;
+        den = wave_sum(den);
+        if (lane == 0) s_inv = 1.0f / den;
     }
-    if (t == 0) store_u32_release(&p.counters[kvh], 0u);
+    __syncthreads();
+    for (uint32_t d = threadIdx.x; d < hd; d += blockDim.x) {
+        float v = 0.f;
+        for (uint32_t s = 0; s < s_act; ++s) v = fmaf(base[(uint64_t)s * G * (hd + 2) + d], w[s] * s_inv, v);
+        p.out[(uint64_t)h * hd + d] = v;
+    }
 }
 
 // ---------------------------------------------------------------------------
-// Embedding row (embed_lookup, gemv.rs:515-526, 710-736): x = dequant(E[tok]).
-// The token is read on the device: tok = src[idx ? *idx : 0].
+// Embedding row (embed_lookup, gemv.rs:515-526, 710-736): the fixed-point
+// residual stream is set to dequant(E[tok]). The token is read on the
+// device: tok = src[idx ? *idx : 0].
 // ---------------------------------------------------------------------------
 
 __global__ __launch_bounds__(256) void embed_kernel(EmbedParams p) {
@@ -148,7 +276,7 @@ __global__ __launch_bounds__(256) void embed_kernel(EmbedParams p) {
         } else {
             v = h2f(reinterpret_cast<const uint16_t*>(p.w)[(uint64_t)tok * p.hidden + j]);
         }
-        p.x[j] = v;
+        p.xacc[j] = to_fixed(v);
     }
 }
 

@@ -5,6 +5,8 @@
 #include <hip/hip_fp16.h>
 #include <stdint.h>
 
+#include "params.hpp"
+
 namespace qora {
 
 constexpr int kWave = 64;
@@ -24,6 +26,15 @@ __device__ __forceinline__ uint16_t f2h(float f) {
 template <int B>
 __device__ __forceinline__ float ubyte_f(uint32_t w) {
     return (float)((w >> (8 * B)) & 0xFFu);
+}
+
+// Fixed-point accumulator values (params.hpp): int64 / 2^36.
+__device__ __forceinline__ long long to_fixed(float v) {
+    return __double2ll_rn((double)v * kFixScale);
+}
+
+__device__ __forceinline__ float from_fixed(long long a) {
+    return (float)((double)a * (1.0 / kFixScale));
 }
 
 // Sum over the 64 lanes of a wave; every lane receives the total.

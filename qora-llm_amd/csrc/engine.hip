@@ -36,27 +36,24 @@ struct ModelState {
     float* d_sin = nullptr;
     void* d_k = nullptr;                 // [L][cap][kvd]
     void* d_v = nullptr;
-    float* d_x = nullptr;
-    float* d_q = nullptr;
-    float* d_attn = nullptr;
-    float* d_h = nullptr;
+    long long* d_xacc = nullptr;         // residual stream, fixed point [hidden]
+    long long* d_qkv_acc = nullptr;      // q|k|v sums [qd + 2 kvd]
+    long long* d_gu_acc = nullptr;       // gate|up sums [2 inter]
+    float* d_attn_part = nullptr;        // attention split partials
     float* d_logits = nullptr;
     int32_t* d_token = nullptr;
     int32_t* d_pos = nullptr;
     int32_t* d_gen = nullptr;
     int32_t* d_prompt = nullptr;
-    float* d_partials = nullptr;
-    uint32_t* d_counters = nullptr;
-    float* d_attn_part = nullptr;
-    uint32_t* d_attn_cnt = nullptr;
     float* d_argv = nullptr;
     uint32_t* d_argi = nullptr;
-    uint32_t* d_argc = nullptr;
     GemvPlan pl_qkv, pl_o, pl_gu, pl_down;
     uint32_t lm_blocks = 0;
+    uint32_t attn_chunk = 0, attn_s_max = 0;
     std::vector<GemvParams> p_qkv, p_o, p_gu, p_down;
     std::vector<AttnParams> p_attn;
     RowdotParams p_lm{};
+    ArgmaxFinishParams p_fin{};
     EmbedParams p_emb_tok{}, p_emb_prompt{};
     hipGraphExec_t g_step = nullptr;
     hipGraphExec_t g_prefill = nullptr;
@@ -71,14 +68,10 @@ struct qora_hip_ctx {
     int cus = 0;
     std::string err;
     std::vector<DevWeight> weights;
-    float* ws_part = nullptr;
-    uint64_t ws_part_n = 0;
-    uint32_t* ws_cnt = nullptr;
-    uint64_t ws_cnt_n = 0;
+    long long* ws_acc = nullptr;         // kernel-level fixed-point accumulator
+    uint64_t ws_acc_n = 0;
     float* ws_attn_part = nullptr;
     uint64_t ws_attn_part_n = 0;
-    uint32_t* ws_attn_cnt = nullptr;
-    uint64_t ws_attn_cnt_n = 0;
     int32_t* h_pin = nullptr;            // pinned staging: [0] token in, [1] token out, [2] pos
     bool capturing = false;
     ModelState m;
@@ -118,59 +111,33 @@ int dalloc(qora_hip_ctx* c, size_t bytes, void** p) {
 
 hipStream_t pick_stream(qora_hip_ctx* c, void* s) { return s ? reinterpret_cast<hipStream_t>(s) : c->stream; }
 
-// Grow the kernel-level scratch (split-K partials and tile counters).
-int ensure_ws(qora_hip_ctx* c, uint64_t part_floats, uint64_t counters) {
-    if (part_floats <= c->ws_part_n && counters <= c->ws_cnt_n) return QORA_HIP_OK;
+// Grow the kernel-level scratch (fixed-point accumulator, attention partials).
+int ensure_acc_ws(qora_hip_ctx* c, uint64_t n) {
+    if (n <= c->ws_acc_n) return QORA_HIP_OK;
     if (c->capturing) return fail(c, QORA_HIP_E_STATE, "scratch must be sized by an eager call before capture");
     HIP_TRY(c, hipStreamSynchronize(c->stream));
-    if (part_floats > c->ws_part_n) {
-        if (c->ws_part) (void)hipFree(c->ws_part);
-        c->ws_part = nullptr;
-        c->ws_part_n = 0;
-        void* p;
-        const uint64_t nn = part_floats + part_floats / 4;
-        if (int rc = dalloc(c, nn * sizeof(float), &p)) return rc;
-        c->ws_part = (float*)p;
-        c->ws_part_n = nn;
-    }
-    if (counters > c->ws_cnt_n) {
-        if (c->ws_cnt) (void)hipFree(c->ws_cnt);
-        c->ws_cnt = nullptr;
-        c->ws_cnt_n = 0;
-        void* p;
-        const uint64_t nn = counters < 4096 ? 4096 : counters;
-        if (int rc = dalloc(c, nn * sizeof(uint32_t), &p)) return rc;
-        HIP_TRY(c, hipMemset(p, 0, nn * sizeof(uint32_t)));
-        c->ws_cnt = (uint32_t*)p;
-        c->ws_cnt_n = nn;
-    }
+    if (c->ws_acc) (void)hipFree(c->ws_acc);
+    c->ws_acc = nullptr;
+    c->ws_acc_n = 0;
+    void* p;
+    const uint64_t nn = n < 65536 ? 65536 : n;
+    if (int rc = dalloc(c, nn * sizeof(long long), &p)) return rc;
+    c->ws_acc = (long long*)p;
+    c->ws_acc_n = nn;
     return QORA_HIP_OK;
 }
 
-int ensure_attn_ws(qora_hip_ctx* c, uint64_t part_floats, uint64_t counters) {
-    if (part_floats <= c->ws_attn_part_n && counters <= c->ws_attn_cnt_n) return QORA_HIP_OK;
+int ensure_attn_ws(qora_hip_ctx* c, uint64_t part_floats) {
+    if (part_floats <= c->ws_attn_part_n) return QORA_HIP_OK;
     if (c->capturing) return fail(c, QORA_HIP_E_STATE, "scratch must be sized by an eager call before capture");
     HIP_TRY(c, hipStreamSynchronize(c->stream));
-    if (part_floats > c->ws_attn_part_n) {
-        if (c->ws_attn_part) (void)hipFree(c->ws_attn_part);
-        c->ws_attn_part = nullptr;
-        c->ws_attn_part_n = 0;
-        void* p;
-        if (int rc = dalloc(c, part_floats * sizeof(float), &p)) return rc;
-        c->ws_attn_part = (float*)p;
-        c->ws_attn_part_n = part_floats;
-    }
-    if (counters > c->ws_attn_cnt_n) {
-        if (c->ws_attn_cnt) (void)hipFree(c->ws_attn_cnt);
-        c->ws_attn_cnt = nullptr;
-        c->ws_attn_cnt_n = 0;
-        void* p;
-        const uint64_t nn = counters < 64 ? 64 : counters;
-        if (int rc = dalloc(c, nn * sizeof(uint32_t), &p)) return rc;
-        HIP_TRY(c, hipMemset(p, 0, nn * sizeof(uint32_t)));
-        c->ws_attn_cnt = (uint32_t*)p;
-        c->ws_attn_cnt_n = nn;
-    }
+    if (c->ws_attn_part) (void)hipFree(c->ws_attn_part);
+    c->ws_attn_part = nullptr;
+    c->ws_attn_part_n = 0;
+    void* p;
+    if (int rc = dalloc(c, part_floats * sizeof(float), &p)) return rc;
+    c->ws_attn_part = (float*)p;
+    c->ws_attn_part_n = part_floats;
     return QORA_HIP_OK;
 }
 
@@ -204,8 +171,25 @@ int record_step(qora_hip_ctx* c, bool with_lm_head) {
         HIP_TRY(c, launch_gemv(m.fmt, m.pl_gu, m.p_gu[l], s));
         HIP_TRY(c, launch_gemv(m.fmt, m.pl_down, m.p_down[l], s));
     }
-    if (with_lm_head) HIP_TRY(c, launch_rowdot(m.fmt, m.lm_blocks, m.p_lm, s));
-    else HIP_TRY(c, launch_advance_pos(m.d_pos, s));
+    if (with_lm_head) {
+        HIP_TRY(c, launch_rowdot(m.fmt, m.lm_blocks, m.p_lm, s));
+        HIP_TRY(c, launch_argmax_finish(m.p_fin, s));
+    } else {
+        HIP_TRY(c, launch_advance_pos(m.d_pos, s));
+    }
+    return QORA_HIP_OK;
+}
+
+// QORA_HIP_EAGER=1 launches the decode step kernel by kernel instead of
+// replaying the captured graph (for profilers that do not follow graphs).
+bool eager_mode() {
+    const char* v = std::getenv("QORA_HIP_EAGER");
+    return v && *v && *v != '0';
+}
+
+int launch_step(qora_hip_ctx* c, bool with_lm_head) {
+    if (eager_mode()) return record_step(c, with_lm_head);
+    HIP_TRY(c, hipGraphLaunch(with_lm_head ? c->m.g_step : c->m.g_prefill, c->stream));
     return QORA_HIP_OK;
 }
 
@@ -292,7 +276,7 @@ extern "C" int qora_hip_destroy(qora_hip_ctx* c) {
         if (w.w) (void)hipFree(w.w);
         if (w.scales) (void)hipFree(w.scales);
     }
-    for (void* p : {(void*)c->ws_part, (void*)c->ws_cnt, (void*)c->ws_attn_part, (void*)c->ws_attn_cnt})
+    for (void* p : {(void*)c->ws_acc, (void*)c->ws_attn_part})
         if (p) (void)hipFree(p);
     if (c->h_pin) (void)hipHostFree(c->h_pin);
     (void)hipStreamDestroy(c->stream);
@@ -372,7 +356,8 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
         return fail(c, QORA_HIP_E_INVALID, "num_kv_groups must equal num_heads / num_kv_heads");
     if (d->num_kv_groups > (uint32_t)kAttnMaxGroups || d->head_dim > (uint32_t)kAttnMaxHd)
         return fail(c, QORA_HIP_E_INVALID, "attention kernel supports head_dim <= 128 and <= 4 query heads per KV head");
-    if (256 % d->head_dim != 0) return fail(c, QORA_HIP_E_INVALID, "head_dim must divide 256");
+    if (d->head_dim < 32 || d->head_dim % 8 != 0)
+        return fail(c, QORA_HIP_E_INVALID, "head_dim must be a multiple of 8 and at least 32");
     if (2 * d->rope_half_dim > d->head_dim) return fail(c, QORA_HIP_E_INVALID, "rope_half_dim exceeds head_dim / 2");
     if (d->hidden % 32 != 0 || 64 % (d->hidden / 32) != 0 || d->intermediate % 32 != 0)
         return fail(c, QORA_HIP_E_INVALID, "hidden/32 must divide 64 and intermediate must be a multiple of 32");
@@ -426,25 +411,19 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
     const uint32_t qkv_groups[3] = {gq, gkv, gkv};
     const uint32_t gu_groups[2] = {gi, gi};
     if (!plan_gemv(m.fmt, m.hidden, qkv_groups, 3, false, c->cus, &m.pl_qkv) ||
-        !plan_gemv(m.fmt, qd, &gh, 1, false, c->cus, &m.pl_o) ||
+        !plan_gemv(m.fmt, qd, &gh, 1, false, c->cus, &m.pl_o, m.hd) ||
         !plan_gemv(m.fmt, m.hidden, gu_groups, 2, true, c->cus, &m.pl_gu) ||
         !plan_gemv(m.fmt, m.inter, &gh, 1, false, c->cus, &m.pl_down)) {
         free_model(c);
         return fail(c, QORA_HIP_E_INVALID, "unsupported GEMV shape");
     }
-    // Each of q, k, v starts on its own column tile and head_dim divides the
-    // tile width, so the RoPE partner of a column is always in its tile.
     m.lm_blocks = rowdot_blocks(m.vocab, m.hidden, c->cus);
-    const uint32_t s_max = attn_splits(m.cap);
-    uint64_t part_floats = 0, tiles_max = 0;
-    for (const GemvPlan* pl : {&m.pl_qkv, &m.pl_o, &m.pl_gu, &m.pl_down}) {
-        part_floats = std::max<uint64_t>(part_floats, pl->partial_floats());
-        tiles_max = std::max<uint64_t>(tiles_max, pl->tiles);
-    }
+    attn_geometry(m.cap, &m.attn_chunk, &m.attn_s_max);
 
     // device buffers
     void* p = nullptr;
     const size_t kvb = m.kv_f16 ? 2 : 4;
+    const size_t qkv_n = (size_t)qd + 2 * kvd;
 #define MALLOC(field, bytes)                                   \
     do {                                                       \
         if (int rc_ = model_alloc(c, (bytes), &p)) { free_model(c); return rc_; } \
@@ -458,26 +437,21 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
     }
     MALLOC(d_k, (size_t)m.L * m.cap * kvd * kvb);
     MALLOC(d_v, (size_t)m.L * m.cap * kvd * kvb);
-    MALLOC(d_x, (size_t)m.hidden * 4);
-    MALLOC(d_q, (size_t)qd * 4);
-    MALLOC(d_attn, (size_t)qd * 4);
-    MALLOC(d_h, (size_t)m.inter * 4);
+    MALLOC(d_xacc, (size_t)m.hidden * 8);
+    MALLOC(d_qkv_acc, qkv_n * 8);
+    MALLOC(d_gu_acc, (size_t)2 * m.inter * 8);
+    MALLOC(d_attn_part, (size_t)m.KVH * m.attn_s_max * m.groups * (m.hd + 2) * 4);
     MALLOC(d_logits, (size_t)m.vocab * 4);
     MALLOC(d_token, 64);
     MALLOC(d_pos, 64);
     MALLOC(d_gen, (size_t)m.cap * 4 + 64);
     MALLOC(d_prompt, (size_t)m.cap * 4 + 64);
-    MALLOC(d_partials, (size_t)std::max<uint64_t>(part_floats, 1) * 4);
-    MALLOC(d_counters, (size_t)std::max<uint64_t>(tiles_max, 1) * 4);
-    MALLOC(d_attn_part, (size_t)m.KVH * s_max * m.groups * (m.hd + 2) * 4);
-    MALLOC(d_attn_cnt, (size_t)m.KVH * 4);
     MALLOC(d_argv, (size_t)m.lm_blocks * 4);
     MALLOC(d_argi, (size_t)m.lm_blocks * 4);
-    MALLOC(d_argc, 64);
 #undef MALLOC
-    HIP_TRY(c, hipMemset(m.d_counters, 0, (size_t)std::max<uint64_t>(tiles_max, 1) * 4));
-    HIP_TRY(c, hipMemset(m.d_attn_cnt, 0, (size_t)m.KVH * 4));
-    HIP_TRY(c, hipMemset(m.d_argc, 0, 64));
+    HIP_TRY(c, hipMemset(m.d_xacc, 0, (size_t)m.hidden * 8));
+    HIP_TRY(c, hipMemset(m.d_qkv_acc, 0, qkv_n * 8));
+    HIP_TRY(c, hipMemset(m.d_gu_acc, 0, (size_t)2 * m.inter * 8));
     HIP_TRY(c, hipMemset(m.d_pos, 0, 64));
     HIP_TRY(c, hipMemset(m.d_token, 0, 64));
     HIP_TRY(c, hipMemset(m.d_gen, 0, (size_t)m.cap * 4 + 64));
@@ -494,7 +468,13 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
         HIP_TRY(c, hipMemcpy(m.d_sin, d->rope_sin, (size_t)m.rope_positions * m.half * 4, hipMemcpyHostToDevice));
     }
 
-    // per-layer launch parameters
+    // Per-layer launch parameters. Data flow of one layer (each arrow is a
+    // kernel boundary; accumulators are fixed point, see params.hpp):
+    //   xacc --RMSNorm+q|k|v GEMV--> qkv_acc --attention(RoPE, K/V append)-->
+    //   partials --merge+o GEMV--> xacc (+=) --RMSNorm+gate|up GEMV--> gu_acc
+    //   --silu*up+down GEMV--> xacc (+=)
+    // qkv_acc is cleared by the o kernel and gu_acc by the next q|k|v kernel,
+    // each after its last reader has finished.
     m.p_qkv.resize(m.L);
     m.p_o.resize(m.L);
     m.p_gu.resize(m.L);
@@ -508,31 +488,25 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
 
         GemvParams& q = m.p_qkv[l];
         q = GemvParams{};
-        for (int j = 0; j < 3; ++j) q.seg[j] = GemvSeg{(const uint8_t*)W[j]->w, (const uint16_t*)W[j]->scales,
-                                                       (uint32_t)(W[j]->n / 32), 0, 0};
+        for (int j = 0; j < 3; ++j)
+            q.seg[j] = GemvSeg{(const uint8_t*)W[j]->w, (const uint16_t*)W[j]->scales, (uint32_t)(W[j]->n / 32), 0, 0, 0};
         q.nseg = 3;
-        q.x = m.d_x;
-        q.gamma = m.d_norms + ((size_t)l * 2 + 0) * m.hidden;
         q.k = m.hidden;
-        q.partials = m.d_partials;
-        q.counters = m.d_counters;
-        q.epi = EPI_QKV;
-        q.q_out = m.d_q;
-        q.kcache = kl;
-        q.vcache = vl;
-        q.kv_f16 = m.kv_f16;
-        q.head_dim = m.hd;
-        q.half_dim = m.half;
-        q.kv_stride = kvd;
-        q.rope_cos = m.d_cos;
-        q.rope_sin = m.d_sin;
-        q.pos = m.d_pos;
-        q.use_rope = d->use_rope[l] ? 1 : 0;
+        q.pro = PRO_NORM_FIXED;
+        q.xacc = m.d_xacc;
+        q.gamma = m.d_norms + ((size_t)l * 2 + 0) * m.hidden;
+        q.acc = m.d_qkv_acc;
+        q.zero_ptr = m.d_gu_acc;
+        q.zero_n = 2 * m.inter;
         apply_plan(m.pl_qkv, &q);
 
         AttnParams& a = m.p_attn[l];
         a = AttnParams{};
-        a.q = m.d_q;
+        a.qkv_acc = m.d_qkv_acc;
+        a.rope_cos = m.d_cos;
+        a.rope_sin = m.d_sin;
+        a.use_rope = d->use_rope[l] ? 1 : 0;
+        a.half = m.half;
         a.kc = kl;
         a.vc = vl;
         a.kv_f16 = m.kv_f16;
@@ -542,48 +516,48 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
         a.hd = m.hd;
         a.groups = m.groups;
         a.scale = 1.0f / sqrtf((float)m.hd);
+        a.chunk = m.attn_chunk;
         a.part = m.d_attn_part;
-        a.counters = m.d_attn_cnt;
-        a.s_max = s_max;
-        a.out = m.d_attn;
+        a.s_max = m.attn_s_max;
 
         GemvParams& o = m.p_o[l];
         o = GemvParams{};
-        o.seg[0] = GemvSeg{(const uint8_t*)W[3]->w, (const uint16_t*)W[3]->scales, gh, 0, 0};
+        o.seg[0] = GemvSeg{(const uint8_t*)W[3]->w, (const uint16_t*)W[3]->scales, gh, 0, 0, 0};
         o.nseg = 1;
-        o.x = m.d_attn;
         o.k = qd;
-        o.partials = m.d_partials;
-        o.counters = m.d_counters;
-        o.epi = EPI_RESID;
-        o.y = m.d_x;
+        o.pro = PRO_ATTN;
+        o.attn_part = m.d_attn_part;
+        o.attn_s_max = m.attn_s_max;
+        o.attn_chunk = m.attn_chunk;
+        o.head_dim = m.hd;
+        o.groups = m.groups;
+        o.pos = m.d_pos;
+        o.acc = m.d_xacc;
+        o.zero_ptr = m.d_qkv_acc;
+        o.zero_n = (uint32_t)qkv_n;
         apply_plan(m.pl_o, &o);
 
         GemvParams& g = m.p_gu[l];
         g = GemvParams{};
-        g.seg[0] = GemvSeg{(const uint8_t*)W[4]->w, (const uint16_t*)W[4]->scales, gi, 0, 0};
-        g.seg[1] = GemvSeg{(const uint8_t*)W[5]->w, (const uint16_t*)W[5]->scales, gi, 0, 0};
+        g.seg[0] = GemvSeg{(const uint8_t*)W[4]->w, (const uint16_t*)W[4]->scales, gi, 0, 0, 0};
+        g.seg[1] = GemvSeg{(const uint8_t*)W[5]->w, (const uint16_t*)W[5]->scales, gi, 0, 0, 0};
         g.nseg = 2;
         g.paired = 1;
-        g.x = m.d_x;
-        g.gamma = m.d_norms + ((size_t)l * 2 + 1) * m.hidden;
         g.k = m.hidden;
-        g.partials = m.d_partials;
-        g.counters = m.d_counters;
-        g.epi = EPI_SILU;
-        g.y = m.d_h;
+        g.pro = PRO_NORM_FIXED;
+        g.xacc = m.d_xacc;
+        g.gamma = m.d_norms + ((size_t)l * 2 + 1) * m.hidden;
+        g.acc = m.d_gu_acc;
         apply_plan(m.pl_gu, &g);
 
         GemvParams& dn = m.p_down[l];
         dn = GemvParams{};
-        dn.seg[0] = GemvSeg{(const uint8_t*)W[6]->w, (const uint16_t*)W[6]->scales, gh, 0, 0};
+        dn.seg[0] = GemvSeg{(const uint8_t*)W[6]->w, (const uint16_t*)W[6]->scales, gh, 0, 0, 0};
         dn.nseg = 1;
-        dn.x = m.d_h;
         dn.k = m.inter;
-        dn.partials = m.d_partials;
-        dn.counters = m.d_counters;
-        dn.epi = EPI_RESID;
-        dn.y = m.d_x;
+        dn.pro = PRO_SILU_FIXED;
+        dn.xacc = m.d_gu_acc;
+        dn.acc = m.d_xacc;
         apply_plan(m.pl_down, &dn);
     }
     m.p_lm = RowdotParams{};
@@ -591,20 +565,17 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
     m.p_lm.scales = (const uint16_t*)emb->scales;
     m.p_lm.rows = m.vocab;
     m.p_lm.cols = m.hidden;
-    m.p_lm.x = m.d_x;
+    m.p_lm.xacc = m.d_xacc;
     m.p_lm.gamma = m.d_final;
     m.p_lm.y = m.d_logits;
     m.p_lm.do_argmax = 1;
     m.p_lm.part_val = m.d_argv;
     m.p_lm.part_idx = m.d_argi;
-    m.p_lm.counter = m.d_argc;
-    m.p_lm.token_out = m.d_token;
-    m.p_lm.pos = m.d_pos;
-    m.p_lm.gen = m.d_gen;
+    m.p_fin = ArgmaxFinishParams{m.d_argv, m.d_argi, m.lm_blocks, m.d_token, m.d_pos, m.d_gen};
     m.p_emb_tok = EmbedParams{(const uint8_t*)emb->w, (const uint16_t*)emb->scales, (int)m.fmt, m.hidden,
-                              m.vocab, m.d_token, nullptr, m.d_x};
+                              m.vocab, m.d_token, nullptr, m.d_xacc};
     m.p_emb_prompt = EmbedParams{(const uint8_t*)emb->w, (const uint16_t*)emb->scales, (int)m.fmt, m.hidden,
-                                 m.vocab, m.d_prompt, m.d_pos, m.d_x};
+                                 m.vocab, m.d_prompt, m.d_pos, m.d_xacc};
 
     HIP_TRY(c, hipDeviceSynchronize());
     if (int rc = capture_step(c, true, &m.g_step)) { free_model(c); return rc; }
@@ -652,7 +623,7 @@ extern "C" int qora_hip_decode(qora_hip_ctx* c, uint32_t token, float* logits, u
     if (force_fail("launch")) return fail(c, QORA_HIP_E_DEVICE, "forced launch failure (QORA_HIP_FORCE_FAIL=launch)");
     c->h_pin[0] = (int32_t)token;
     HIP_TRY(c, hipMemcpyAsync(m.d_token, &c->h_pin[0], 4, hipMemcpyHostToDevice, c->stream));
-    HIP_TRY(c, hipGraphLaunch(m.g_step, c->stream));
+    if (int rc = launch_step(c, true)) return rc;
     if (int rc = finish_step(c, logits, argmax)) return rc;
     m.host_pos += 1;
     return QORA_HIP_OK;
@@ -667,7 +638,8 @@ extern "C" int qora_hip_generate_greedy(qora_hip_ctx* c, uint32_t token, uint32_
     if (force_fail("launch")) return fail(c, QORA_HIP_E_DEVICE, "forced launch failure (QORA_HIP_FORCE_FAIL=launch)");
     c->h_pin[0] = (int32_t)token;
     HIP_TRY(c, hipMemcpyAsync(m.d_token, &c->h_pin[0], 4, hipMemcpyHostToDevice, c->stream));
-    for (uint32_t i = 0; i < steps; ++i) HIP_TRY(c, hipGraphLaunch(m.g_step, c->stream));
+    for (uint32_t i = 0; i < steps; ++i)
+        if (int rc = launch_step(c, true)) return rc;
     HIP_TRY(c, hipMemcpyAsync(out, m.d_gen + m.host_pos, (size_t)steps * 4, hipMemcpyDeviceToHost, c->stream));
     HIP_TRY(c, hipStreamSynchronize(c->stream));
     m.host_pos += steps;
@@ -686,10 +658,11 @@ extern "C" int qora_hip_prefill(qora_hip_ctx* c, const uint32_t* ids, size_t n, 
     if (int rc = check_step_room(c, n)) return rc;
     if (force_fail("launch")) return fail(c, QORA_HIP_E_DEVICE, "forced launch failure (QORA_HIP_FORCE_FAIL=launch)");
     HIP_TRY(c, hipMemcpy(m.d_prompt, ids, n * 4, hipMemcpyHostToDevice));
-    for (size_t i = 0; i + 1 < n; ++i) HIP_TRY(c, hipGraphLaunch(m.g_prefill, c->stream));
+    for (size_t i = 0; i + 1 < n; ++i)
+        if (int rc = launch_step(c, false)) return rc;
     c->h_pin[0] = (int32_t)ids[n - 1];
     HIP_TRY(c, hipMemcpyAsync(m.d_token, &c->h_pin[0], 4, hipMemcpyHostToDevice, c->stream));
-    HIP_TRY(c, hipGraphLaunch(m.g_step, c->stream));
+    if (int rc = launch_step(c, true)) return rc;
     if (int rc = finish_step(c, logits, argmax)) return rc;
     m.host_pos = n;
     return QORA_HIP_OK;
@@ -806,10 +779,12 @@ extern "C" int qora_hip_graph_destroy(qora_hip_ctx* c, void* graph_exec) {
 
 namespace {
 
-int gemv_entry(qora_hip_ctx* c, int fmt, const void* w0, const void* s0, const void* w1, const void* s1,
-               const float* x, float* y, uint64_t k, uint64_t n, bool paired, void* stream) {
+// acc[0:n] (+ acc[n:2n] when paired) += W x, one launch of the model's GEMV
+// kernel with the plain-vector prologue.
+int gemv_acc_entry(qora_hip_ctx* c, int fmt, const void* w0, const void* s0, const void* w1, const void* s1,
+                   const float* x, long long* acc, uint64_t k, uint64_t n, bool paired, void* stream) {
     if (!c) return QORA_HIP_E_INVALID;
-    if (!w0 || !x || !y || (fmt == FMT_Q4 && !s0) || (paired && (!w1 || (fmt == FMT_Q4 && !s1))))
+    if (!w0 || !x || !acc || (fmt == FMT_Q4 && !s0) || (paired && (!w1 || (fmt == FMT_Q4 && !s1))))
         return fail(c, QORA_HIP_E_INVALID, "null argument");
     if (k == 0 || n == 0 || n % 32 != 0 || k > 0xFFFFFFFFull || n / 32 > 0xFFFFFFFFull)
         return fail(c, QORA_HIP_E_INVALID, "GEMV needs k > 0 and n % 32 == 0");
@@ -818,23 +793,36 @@ int gemv_entry(qora_hip_ctx* c, int fmt, const void* w0, const void* s0, const v
     GemvPlan pl;
     if (!plan_gemv(fmt, (uint32_t)k, groups, paired ? 2 : 1, paired, c->cus, &pl))
         return fail(c, QORA_HIP_E_INVALID, "unsupported GEMV shape");
-    if (int rc = ensure_ws(c, pl.partial_floats(), pl.tiles)) return rc;
     GemvParams p{};
-    p.seg[0] = GemvSeg{(const uint8_t*)w0, (const uint16_t*)s0, G, 0, 0};
+    p.seg[0] = GemvSeg{(const uint8_t*)w0, (const uint16_t*)s0, G, 0, 0, 0};
     p.nseg = 1;
     if (paired) {
-        p.seg[1] = GemvSeg{(const uint8_t*)w1, (const uint16_t*)s1, G, 0, 0};
+        p.seg[1] = GemvSeg{(const uint8_t*)w1, (const uint16_t*)s1, G, 0, 0, 0};
         p.nseg = 2;
         p.paired = 1;
     }
-    p.x = x;
     p.k = (uint32_t)k;
-    p.partials = c->ws_part;
-    p.counters = c->ws_cnt;
-    p.epi = paired ? EPI_SILU : EPI_STORE;
-    p.y = y;
+    p.pro = PRO_PLAIN;
+    p.x = x;
+    p.acc = acc;
     apply_plan(pl, &p);
     HIP_TRY(c, launch_gemv(fmt, pl, p, pick_stream(c, stream)));
+    return QORA_HIP_OK;
+}
+
+// y = W x (paired: y = silu(Wg x) * (Wu x)) through the context accumulator:
+// clear, accumulate, convert.
+int gemv_entry(qora_hip_ctx* c, int fmt, const void* w0, const void* s0, const void* w1, const void* s1,
+               const float* x, float* y, uint64_t k, uint64_t n, bool paired, void* stream) {
+    if (!c) return QORA_HIP_E_INVALID;
+    if (!y) return fail(c, QORA_HIP_E_INVALID, "null argument");
+    if (n == 0 || n > 0x7FFFFFFFull) return fail(c, QORA_HIP_E_INVALID, "GEMV needs 0 < n < 2^31");
+    const uint64_t accn = paired ? 2 * n : n;
+    if (int rc = ensure_acc_ws(c, accn)) return rc;
+    const hipStream_t s = pick_stream(c, stream);
+    HIP_TRY(c, launch_fill_zero(c->ws_acc, accn, s));
+    if (int rc = gemv_acc_entry(c, fmt, w0, s0, w1, s1, x, c->ws_acc, k, n, paired, stream)) return rc;
+    HIP_TRY(c, launch_acc_to_f32(c->ws_acc, (uint32_t)n, paired ? 1 : 0, y, s));
     return QORA_HIP_OK;
 }
 
@@ -875,6 +863,26 @@ extern "C" int qora_hip_gate_up_q4(qora_hip_ctx* c, const void* gp, const void* 
 extern "C" int qora_hip_gate_up_f16(qora_hip_ctx* c, const void* gw, const void* uw, const float* x, float* out,
                                     uint64_t k, uint64_t n, void* stream) {
     return gemv_entry(c, FMT_F16, gw, nullptr, uw, nullptr, x, out, k, n, true, stream);
+}
+
+extern "C" int qora_hip_gemv_q4_accumulate(qora_hip_ctx* c, const void* packed, const void* scales,
+                                           const float* x, long long* acc, uint64_t k, uint64_t n, void* stream) {
+    return gemv_acc_entry(c, FMT_Q4, packed, scales, nullptr, nullptr, x, acc, k, n, false, stream);
+}
+
+extern "C" int qora_hip_gate_up_q4_accumulate(qora_hip_ctx* c, const void* gp, const void* gs, const void* up,
+                                              const void* us, const float* x, long long* acc, uint64_t k,
+                                              uint64_t n, void* stream) {
+    return gemv_acc_entry(c, FMT_Q4, gp, gs, up, us, x, acc, k, n, true, stream);
+}
+
+extern "C" int qora_hip_acc_to_f32(qora_hip_ctx* c, const long long* acc, uint64_t n, int paired, float* y,
+                                   void* stream) {
+    if (!c) return QORA_HIP_E_INVALID;
+    if (!acc || !y) return fail(c, QORA_HIP_E_INVALID, "null argument");
+    if (n == 0 || n > 0x7FFFFFFFull) return fail(c, QORA_HIP_E_INVALID, "bad length");
+    HIP_TRY(c, launch_acc_to_f32(acc, (uint32_t)n, paired ? 1 : 0, y, pick_stream(c, stream)));
+    return QORA_HIP_OK;
 }
 
 extern "C" int qora_hip_gemv_q4_rowdot(qora_hip_ctx* c, const void* packed, const void* scales, const float* x,
@@ -920,26 +928,27 @@ extern "C" int qora_hip_attn_decode(qora_hip_ctx* c, const float* q, const void*
     if (!c) return QORA_HIP_E_INVALID;
     if (!q || !kc || !vc || !out) return fail(c, QORA_HIP_E_INVALID, "null argument");
     if (L == 0 || H == 0 || KVH == 0 || H % KVH != 0 || H / KVH > (uint32_t)kAttnMaxGroups || hd == 0 ||
-        hd > (uint32_t)kAttnMaxHd)
-        return fail(c, QORA_HIP_E_INVALID, "attention needs L > 0, H % KVH == 0, H/KVH <= 4, head_dim <= 128");
+        hd > (uint32_t)kAttnMaxHd || hd % 8 != 0)
+        return fail(c, QORA_HIP_E_INVALID,
+                    "attention needs L > 0, H % KVH == 0, H/KVH <= 4, head_dim <= 128 and a multiple of 8");
     AttnParams a{};
     a.q = q;
-    a.kc = kc;
-    a.vc = vc;
+    a.kc = const_cast<void*>(kc);
+    a.vc = const_cast<void*>(vc);
     a.kv_f16 = kv_f16 ? 1 : 0;
-    a.pos = nullptr;
     a.L = L;
     a.H = H;
     a.KVH = KVH;
     a.hd = hd;
     a.groups = H / KVH;
     a.scale = 1.0f / sqrtf((float)hd);
-    a.s_max = attn_splits(L);
-    if (int rc = ensure_attn_ws(c, (uint64_t)KVH * a.s_max * a.groups * (hd + 2), KVH)) return rc;
+    attn_geometry(L, &a.chunk, &a.s_max);
+    if (int rc = ensure_attn_ws(c, (uint64_t)KVH * a.s_max * a.groups * (hd + 2))) return rc;
     a.part = c->ws_attn_part;
-    a.counters = c->ws_attn_cnt;
-    a.out = out;
-    HIP_TRY(c, launch_attn(a, pick_stream(c, stream)));
+    const hipStream_t s = pick_stream(c, stream);
+    HIP_TRY(c, launch_attn(a, s));
+    AttnCombineParams cp{a.part, nullptr, L, H, KVH, hd, a.groups, a.chunk, a.s_max, out};
+    HIP_TRY(c, launch_attn_combine(cp, s));
     return QORA_HIP_OK;
 }
 

@@ -4,25 +4,28 @@
 //   Q4 : packed[k][n/2] bytes, low nibble = even column, q in [0,15],
 //        value = (q - 8) * scale; scales[k][n/32] binary16.
 //   F16: data[k][n] binary16.
-// y[j] = sum_i x[i] * W[i][j]  (outer-product form of gemv_q4, gemv.rs:596-675).
+// acc[j] += sum_i x[i] * W[i][j]  (the outer-product gemv_q4, gemv.rs:596-675).
 //
-// Work decomposition (split-K, no atomics on the result):
+// Work decomposition (split-K, no cross-workgroup synchronisation):
 //   * A "group" is 32 output columns of one input row: 16 bytes of nibbles
 //     plus one scale (Q4), or 64 bytes (F16). Each lane owns one group and
 //     accumulates its 32 columns in registers over RPL rows, so one 128-bit
-//     load feeds 32 multiply-adds.
+//     load feeds 32 multiply-adds, and all RPL loads are in flight at once.
 //   * A workgroup (256 lanes) covers a column tile of GT groups and a slice of
 //     KR = (256/GT)*RPL input rows. Lanes t = rl*GT + gi: the GT lanes of a
-//     row read GT*16 contiguous bytes, so every wave instruction reads 64/GT
-//     full row segments (128 B or 256 B each).
-//   * Lanes sharing a group are summed through LDS; the workgroup writes one
-//     partial per column. The last workgroup to finish a column tile (device
-//     scope counter) adds the S partials in split order, which makes the
-//     result independent of scheduling, and runs the epilogue.
+//     row read GT*16 contiguous bytes (128 B or 256 B row segments).
+//   * The row lanes of a group are summed through LDS; each column's sum is
+//     then added to a fixed-point int64 accumulator with one fire-and-forget
+//     64-bit atomic. Integer addition is exact, so the result does not
+//     depend on the order the K slices land in (deterministic), and no
+//     fence or counter is needed: the kernel boundary publishes the sums.
+//   * The prologue builds the K slice of the input in LDS: plain x, RMSNorm
+//     of the fixed-point residual, silu(gate)*up of the fixed-point gate/up
+//     sums, or the merge of split attention partials. Consumers therefore
+//     finish the previous phase's reduction on the fly.
 // Segments: up to three weight matrices are addressed as one virtual matrix
 // (q|k|v concatenated by column tiles), or two matrices are paired lane by
-// lane (gate|up) so the SiLU*up epilogue finds both halves in one workgroup.
-// The weights are read in the reference layout; nothing is repacked.
+// lane (gate|up). The weights are read in the reference layout.
 #pragma once
 
 #include "common.hpp"
@@ -30,27 +33,42 @@
 
 namespace qora {
 
-
-
+__device__ __forceinline__ void fixed_add(long long* p, float v) {
+    atomicAdd(reinterpret_cast<unsigned long long*>(p), (unsigned long long)to_fixed(v));
+}
 
 __device__ __forceinline__ float silu_mul(float g, float u) {
     const float silu_g = g / (1.0f + expf(-g));
     return silu_g * u;
 }
 
+// RMSNorm statistic of a fixed-point vector: 1 / sqrt(mean(x^2) + 1e-6)
+// (rms_norm_f16, gemv.rs:744-753).
+template <int NT>
+__device__ __forceinline__ float inv_rms_fixed(const long long* xacc, uint32_t n, float* wred) {
+    float ss = 0.f;
+    for (uint32_t i = threadIdx.x; i < n; i += NT) {
+        const float v = from_fixed(xacc[i]);
+        ss += v * v;
+    }
+    ss = block_sum<NT>(ss, wred);
+    return 1.0f / sqrtf(ss / (float)n + 1e-6f);
+}
+
 template <int FMT, int GT, int RPL>
-__global__ __launch_bounds__(256) void gemv_splitk_kernel(GemvParams p) {
+__global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
     constexpr int NT = 256;
     constexpr int RL = NT / GT;          // row lanes
     constexpr int COLS = GT * 32;        // columns per tile
     constexpr int KR = RL * RPL;         // rows per workgroup
     constexpr int RED_STRIDE = 33;       // padded group stride in LDS
     constexpr int CPT = COLS / NT;       // columns per thread in the reduction
+    constexpr int MAXH = KR / 32 + 1;    // heads a K slice can touch (head_dim >= 32)
 
     __shared__ float xs[KR];
     __shared__ float red[NT * RED_STRIDE];
     __shared__ float wred[NT / kWave];
-    __shared__ int s_last;
+    __shared__ float aw[kAttnMaxSplits * MAXH];
 
     const int t = threadIdx.x;
     const int gi = t % GT;
@@ -60,25 +78,10 @@ __global__ __launch_bounds__(256) void gemv_splitk_kernel(GemvParams p) {
     const uint32_t k0 = split * p.rows_per_split;
     const uint32_t k1 = min(p.k, k0 + p.rows_per_split);
 
-    // ---- prologue: stage x[k0, k1) (optionally RMS-normalised) in LDS ----
-    float inv_rms = 1.0f;
-    if (p.gamma) {
-        float ss = 0.f;
-        for (uint32_t i = t; i < p.k; i += NT) { const float v = p.x[i]; ss += v * v; }
-        ss = block_sum<NT>(ss, wred);
-        inv_rms = 1.0f / sqrtf(ss / (float)p.k + 1e-6f);
-    }
-    for (int i = t; i < KR; i += NT) {
-        const uint32_t r = k0 + i;
-        float v = 0.f;
-        if (r < k1) {
-            v = p.x[r];
-            if (p.gamma) v = v * inv_rms * h2f(p.gamma[r]);
-        }
-        xs[i] = v;
-    }
+    if (p.zero_ptr)
+        for (uint32_t i = blockIdx.x * NT + t; i < p.zero_n; i += gridDim.x * NT) p.zero_ptr[i] = 0;
 
-    // ---- which segment / group this lane reads ----
+    // ---- which segment / group this lane reads (issue the loads first) ----
     int sidx;
     uint32_t grp;
     if (p.paired) {
@@ -93,33 +96,93 @@ __global__ __launch_bounds__(256) void gemv_splitk_kernel(GemvParams p) {
     const GemvSeg sg = p.seg[sidx];
     const bool active = grp < sg.groups;
 
-    __syncthreads();
-
     float acc[32];
 #pragma unroll
     for (int c = 0; c < 32; ++c) acc[c] = 0.f;
 
+    uint4 wq[FMT == FMT_Q4 ? RPL : 1];
+    uint16_t sq[FMT == FMT_Q4 ? RPL : 1];
     if constexpr (FMT == FMT_Q4) {
         const uint64_t row_bytes = (uint64_t)sg.groups * 16u;
-        uint4 wv[RPL];
-        uint16_t sv[RPL];
 #pragma unroll
         for (int j = 0; j < RPL; ++j) {
             const uint32_t r = k0 + rl + j * RL;
             if (active && r < k1) {
-                wv[j] = *reinterpret_cast<const uint4*>(sg.w + r * row_bytes + (uint64_t)grp * 16u);
-                sv[j] = sg.scales[(uint64_t)r * sg.groups + grp];
+                wq[j] = *reinterpret_cast<const uint4*>(sg.w + r * row_bytes + (uint64_t)grp * 16u);
+                sq[j] = sg.scales[(uint64_t)r * sg.groups + grp];
             } else {
-                wv[j] = make_uint4(0, 0, 0, 0);
-                sv[j] = 0;
+                wq[j] = make_uint4(0, 0, 0, 0);
+                sq[j] = 0;
             }
         }
+    }
+
+    // ---- prologue: the K slice of the input vector, in LDS ----
+    if (p.pro == PRO_PLAIN) {
+        for (int i = t; i < KR; i += NT) {
+            const uint32_t r = k0 + i;
+            xs[i] = r < k1 ? p.x[r] : 0.f;
+        }
+    } else if (p.pro == PRO_NORM_FIXED) {
+        const float inv = inv_rms_fixed<NT>(p.xacc, p.k, wred);
+        for (int i = t; i < KR; i += NT) {
+            const uint32_t r = k0 + i;
+            xs[i] = r < k1 ? from_fixed(p.xacc[r]) * inv * h2f(p.gamma[r]) : 0.f;
+        }
+    } else if (p.pro == PRO_SILU_FIXED) {
+        for (int i = t; i < KR; i += NT) {
+            const uint32_t r = k0 + i;
+            xs[i] = r < k1 ? silu_mul(from_fixed(p.xacc[r]), from_fixed(p.xacc[p.k + r])) : 0.f;
+        }
+    } else {
+        // PRO_ATTN: rows [k0, k1) are dims of heads k0/hd .. (k1-1)/hd of the
+        // attention output; merge their split partials (online-softmax merge:
+        // out = sum_s acc_s e^(m_s - m) / sum_s l_s e^(m_s - m)).
+        const uint32_t hd = p.head_dim, G = p.groups;
+        const uint32_t L = (uint32_t)(*p.pos) + 1u;
+        const uint32_t s_act = min(p.attn_s_max, (L + p.attn_chunk - 1) / p.attn_chunk);
+        const uint32_t h0 = k0 / hd;
+        const uint32_t nh = (k1 - 1) / hd - h0 + 1;
+        const int wave = t / kWave, lane = t & (kWave - 1);
+        for (uint32_t hh = wave; hh < nh; hh += NT / kWave) {
+            const uint32_t h = h0 + hh, kvh = h / G, g = h % G;
+            const float* base = p.attn_part + ((uint64_t)kvh * p.attn_s_max * G + g) * (hd + 2);
+            float m = -INFINITY;
+            for (uint32_t s = lane; s < s_act; s += kWave) m = fmaxf(m, base[(uint64_t)s * G * (hd + 2) + hd]);
+            m = wave_max(m);
+            float den = 0.f;
+            for (uint32_t s = lane; s < s_act; s += kWave) {
+                const float* ps = base + (uint64_t)s * G * (hd + 2);
+                const float w = expf(ps[hd] - m);
+                aw[hh * kAttnMaxSplits + s] = w;
+                den += ps[hd + 1] * w;
+            }
+            den = wave_sum(den);
+            const float inv = 1.0f / den;
+            for (uint32_t s = lane; s < s_act; s += kWave) aw[hh * kAttnMaxSplits + s] *= inv;
+        }
+        __syncthreads();
+        for (int i = t; i < KR; i += NT) {
+            const uint32_t r = k0 + i;
+            float v = 0.f;
+            if (r < k1) {
+                const uint32_t h = r / hd, d = r % hd, hh = h - h0;
+                const float* base = p.attn_part + ((uint64_t)(h / G) * p.attn_s_max * G + (h % G)) * (hd + 2) + d;
+                for (uint32_t s = 0; s < s_act; ++s)
+                    v = fmaf(base[(uint64_t)s * G * (hd + 2)], aw[hh * kAttnMaxSplits + s], v);
+            }
+            xs[i] = v;
+        }
+    }
+    __syncthreads();
+
+    if constexpr (FMT == FMT_Q4) {
         float corr = 0.f;
 #pragma unroll
         for (int j = 0; j < RPL; ++j) {
-            const float sx = h2f(sv[j]) * xs[rl + j * RL];
+            const float sx = h2f(sq[j]) * xs[rl + j * RL];
             corr += sx;
-            const uint32_t w4[4] = {wv[j].x, wv[j].y, wv[j].z, wv[j].w};
+            const uint32_t w4[4] = {wq[j].x, wq[j].y, wq[j].z, wq[j].w};
 #pragma unroll
             for (int d = 0; d < 4; ++d) {
                 const uint32_t lo = w4[d] & 0x0F0F0F0Fu;
@@ -178,7 +241,6 @@ __global__ __launch_bounds__(256) void gemv_splitk_kernel(GemvParams p) {
         for (int c = 0; c < 32; ++c) dst[c] = acc[c];
     }
     __syncthreads();
-    float colv[CPT];
 #pragma unroll
     for (int cc = 0; cc < CPT; ++cc) {
         const int col = t + cc * NT;
@@ -186,95 +248,29 @@ __global__ __launch_bounds__(256) void gemv_splitk_kernel(GemvParams p) {
         float s = 0.f;
 #pragma unroll 8
         for (int r = 0; r < RL; ++r) s += red[(r * GT + g) * RED_STRIDE + c];
-        colv[cc] = s;
+        // tile column -> (segment, local column) -> accumulator slot
+        uint32_t local;
+        int os;
+        if (p.paired) {
+            os = g < GT / 2 ? 0 : 1;
+            local = tile * (COLS / 2) + (uint32_t)(col - os * (COLS / 2));
+        } else {
+            os = sidx;
+            local = (tile - p.seg[os].tile0) * COLS + (uint32_t)col;
+        }
+        if (local < p.seg[os].groups * 32u) fixed_add(p.acc + p.seg[os].col0 + local, s);
     }
+}
 
-    if (p.splits > 1) {
-        float* dst = p.partials + ((uint64_t)split * p.tiles + tile) * COLS;
-#pragma unroll
-        for (int cc = 0; cc < CPT; ++cc) dst[t + cc * NT] = colv[cc];
-        __threadfence();
-        __syncthreads();
-        if (t == 0) {
-            const uint32_t prev = __hip_atomic_fetch_add(&p.counters[tile], 1u, __ATOMIC_ACQ_REL,
-                                                         __HIP_MEMORY_SCOPE_AGENT);
-            s_last = (prev == p.splits - 1) ? 1 : 0;
-        }
-        __syncthreads();
-        if (!s_last) return;
-        __threadfence();
-#pragma unroll
-        for (int cc = 0; cc < CPT; ++cc) {
-            const int col = t + cc * NT;
-            float s = 0.f;
-            for (uint32_t q = 0; q < p.splits; ++q)
-                s += p.partials[((uint64_t)q * p.tiles + tile) * COLS + col];
-            colv[cc] = s;
-        }
-        if (t == 0) store_u32_release(&p.counters[tile], 0u);
-    }
+// acc (fixed point) -> y (fp32); paired: y[j] = silu(acc[j]) * acc[n + j].
+__global__ __launch_bounds__(256) void acc_to_f32_kernel(const long long* acc, uint32_t n, int paired, float* y) {
+    for (uint32_t j = blockIdx.x * blockDim.x + threadIdx.x; j < n; j += gridDim.x * blockDim.x)
+        y[j] = paired ? silu_mul(from_fixed(acc[j]), from_fixed(acc[n + j])) : from_fixed(acc[j]);
+}
 
-    // ---- epilogue on the final column sums ----
-    if (p.epi == EPI_STORE || p.epi == EPI_RESID) {
-        // single segment, plain layout
-#pragma unroll
-        for (int cc = 0; cc < CPT; ++cc) {
-            const uint32_t col = tile * COLS + t + cc * NT;
-            if (col < p.seg[0].groups * 32u) {
-                if (p.epi == EPI_STORE) p.y[col] = colv[cc];
-                else p.y[col] += colv[cc];
-            }
-        }
-        return;
-    }
-    __syncthreads();  // red[] reused as the staging buffer below
-    float* sums = red;
-#pragma unroll
-    for (int cc = 0; cc < CPT; ++cc) sums[t + cc * NT] = colv[cc];
-    __syncthreads();
-    if (p.epi == EPI_SILU) {
-        constexpr int HALF = COLS / 2;
-        const uint32_t n = p.seg[0].groups * 32u;
-        for (int c = t; c < HALF; c += NT) {
-            const uint32_t j = tile * HALF + c;
-            if (j < n) p.y[j] = silu_mul(sums[c], sums[c + HALF]);
-        }
-        return;
-    }
-    // EPI_QKV: segment 0 -> q, 1 -> K cache row, 2 -> V cache row.
-    {
-        const int s = (p.nseg > 2 && tile >= p.seg[2].tile0) ? 2 : ((tile >= p.seg[1].tile0) ? 1 : 0);
-        const uint32_t seg_cols = p.seg[s].groups * 32u;
-        const uint32_t base = (tile - p.seg[s].tile0) * COLS;
-        const int32_t pos = *p.pos;
-        const uint32_t hd = p.head_dim, half = p.half_dim;
-        for (int c = t; c < COLS; c += NT) {
-            const uint32_t lc = base + c;
-            if (lc >= seg_cols) continue;
-            float v = sums[c];
-            if (s < 2 && p.use_rope) {
-                // apply_rope_raw (gemv.rs:757-778): pairs (i, i+half) in each head
-                const uint32_t d = lc % hd;
-                const float* ct = p.rope_cos + (uint64_t)pos * half;
-                const float* st = p.rope_sin + (uint64_t)pos * half;
-                if (d < half) {
-                    const float x1 = v, x2 = sums[c + half];
-                    v = x1 * ct[d] - x2 * st[d];
-                } else if (d < 2 * half) {
-                    const float x1 = sums[c - half], x2 = v;
-                    v = x2 * ct[d - half] + x1 * st[d - half];
-                }
-            }
-            if (s == 0) {
-                p.q_out[lc] = v;
-            } else {
-                void* cache = (s == 1) ? p.kcache : p.vcache;
-                const uint64_t idx = (uint64_t)pos * p.kv_stride + lc;
-                if (p.kv_f16) reinterpret_cast<uint16_t*>(cache)[idx] = f2h(v);
-                else reinterpret_cast<float*>(cache)[idx] = v;
-            }
-        }
-    }
+__global__ __launch_bounds__(256) void fill_zero_kernel(long long* p, uint64_t n) {
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x)
+        p[i] = 0;
 }
 
 // ---------------------------------------------------------------------------
@@ -282,9 +278,9 @@ __global__ __launch_bounds__(256) void gemv_splitk_kernel(GemvParams p) {
 // lm_head_parallel_q4 / _f16, gemv.rs:805-864): y[r] = sum_c x[c] * W[r][c].
 // Lanes own one 32-column group; G = cols/32 lanes cooperate on a row
 // (64/G rows per wave instruction when G < 64). x stays in registers.
-// Optional fused final RMSNorm prologue and greedy argmax epilogue.
+// Optional fused final RMSNorm prologue and per-workgroup greedy argmax
+// (the last step, over the workgroup bests, is argmax_finish_kernel).
 // ---------------------------------------------------------------------------
-
 
 template <int FMT, int U>
 __global__ __launch_bounds__(256) void rowdot_kernel(RowdotParams p) {
@@ -292,7 +288,6 @@ __global__ __launch_bounds__(256) void rowdot_kernel(RowdotParams p) {
     __shared__ float wred[NT / kWave];
     __shared__ float s_val[NT / kWave];
     __shared__ uint32_t s_idx[NT / kWave];
-    __shared__ int s_last;
 
     const int t = threadIdx.x;
     const int lane = t & (kWave - 1);
@@ -304,17 +299,21 @@ __global__ __launch_bounds__(256) void rowdot_kernel(RowdotParams p) {
 
     float inv_rms = 1.0f;
     if (p.gamma) {
-        float ss = 0.f;
-        for (uint32_t i = t; i < p.cols; i += NT) { const float v = p.x[i]; ss += v * v; }
-        ss = block_sum<NT>(ss, wred);
-        inv_rms = 1.0f / sqrtf(ss / (float)p.cols + 1e-6f);
+        if (p.xacc) {
+            inv_rms = inv_rms_fixed<NT>(p.xacc, p.cols, wred);
+        } else {
+            float ss = 0.f;
+            for (uint32_t i = t; i < p.cols; i += NT) { const float v = p.x[i]; ss += v * v; }
+            ss = block_sum<NT>(ss, wred);
+            inv_rms = 1.0f / sqrtf(ss / (float)p.cols + 1e-6f);
+        }
     }
     float xr[32];
     float xsum = 0.f;
 #pragma unroll
     for (int c = 0; c < 32; ++c) {
         const uint32_t i = g * 32 + c;
-        float v = p.x[i];
+        float v = p.xacc ? from_fixed(p.xacc[i]) : p.x[i];
         if (p.gamma) v = v * inv_rms * h2f(p.gamma[i]);
         xr[c] = v;
         xsum += v;
@@ -404,7 +403,6 @@ __global__ __launch_bounds__(256) void rowdot_kernel(RowdotParams p) {
     }
 
     if (!p.do_argmax) return;
-    // wave argmax
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) {
         const float ov = __shfl_xor(best_v, off, kWave);
@@ -420,43 +418,42 @@ __global__ __launch_bounds__(256) void rowdot_kernel(RowdotParams p) {
             if (argmax_better(s_val[w], s_idx[w], bv, bi)) { bv = s_val[w]; bi = s_idx[w]; }
         p.part_val[blockIdx.x] = bv;
         p.part_idx[blockIdx.x] = bi;
-        __threadfence();
-        const uint32_t prev = __hip_atomic_fetch_add(p.counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-        s_last = (prev == gridDim.x - 1) ? 1 : 0;
     }
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-    best_v = -INFINITY;
-    best_i = 0xFFFFFFFFu;
-    for (uint32_t b = t; b < gridDim.x; b += NT) {
+}
+
+// Greedy token from the per-workgroup bests (generate.rs:346-352): one block.
+__global__ __launch_bounds__(256) void argmax_finish_kernel(ArgmaxFinishParams p) {
+    __shared__ float s_val[4];
+    __shared__ uint32_t s_idx[4];
+    float bv = -INFINITY;
+    uint32_t bi = 0xFFFFFFFFu;
+    for (uint32_t b = threadIdx.x; b < p.parts; b += 256) {
         const float v = p.part_val[b];
         const uint32_t i = p.part_idx[b];
-        if (argmax_better(v, i, best_v, best_i)) { best_v = v; best_i = i; }
+        if (argmax_better(v, i, bv, bi)) { bv = v; bi = i; }
     }
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) {
-        const float ov = __shfl_xor(best_v, off, kWave);
-        const uint32_t oi = __shfl_xor(best_i, off, kWave);
-        if (argmax_better(ov, oi, best_v, best_i)) { best_v = ov; best_i = oi; }
+        const float ov = __shfl_xor(bv, off, kWave);
+        const uint32_t oi = __shfl_xor(bi, off, kWave);
+        if (argmax_better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
     }
+    const int lane = threadIdx.x & 63, wave = threadIdx.x / 64;
+    if (lane == 0) { s_val[wave] = bv; s_idx[wave] = bi; }
     __syncthreads();
-    if (lane == 0) { s_val[wave] = best_v; s_idx[wave] = best_i; }
-    __syncthreads();
-    if (t == 0) {
-        float bv = s_val[0];
-        uint32_t bi = s_idx[0];
-        for (int w = 1; w < NT / kWave; ++w)
-            if (argmax_better(s_val[w], s_idx[w], bv, bi)) { bv = s_val[w]; bi = s_idx[w]; }
+    if (threadIdx.x == 0) {
+        float v0 = s_val[0];
+        uint32_t i0 = s_idx[0];
+        for (int w = 1; w < 4; ++w)
+            if (argmax_better(s_val[w], s_idx[w], v0, i0)) { v0 = s_val[w]; i0 = s_idx[w]; }
         // no candidate above -inf: the sampler returns index 0
-        const int32_t tok = (bi == 0xFFFFFFFFu) ? 0 : (int32_t)bi;
+        const int32_t tok = (i0 == 0xFFFFFFFFu) ? 0 : (int32_t)i0;
         *p.token_out = tok;
         if (p.pos) {
             const int32_t ps = *p.pos;
             p.gen[ps] = tok;
             *p.pos = ps + 1;
         }
-        store_u32_release(p.counter, 0u);
     }
 }
 

@@ -14,13 +14,13 @@ static int env_int(const char* name, int dflt) {
 }
 
 bool plan_gemv(int fmt, uint32_t k, const uint32_t* seg_groups, int nseg, bool paired, int cus,
-               GemvPlan* plan) {
-    if (k == 0 || nseg < 1 || nseg > 3) return false;
+               GemvPlan* plan, uint32_t row_align) {
+    if (k == 0 || nseg < 1 || nseg > 3 || row_align == 0) return false;
     if (paired && (nseg != 2 || seg_groups[0] != seg_groups[1])) return false;
     GemvPlan pl;
     pl.gt = paired ? 16 : 8;
     const int forced_gt = env_int("QORA_GEMV_GT", 0);
-    if (forced_gt == 8 || forced_gt == 16) pl.gt = paired ? 16 : forced_gt;
+    if (!paired && (forced_gt == 8 || forced_gt == 16)) pl.gt = forced_gt;
     if (paired) {
         pl.tiles = (seg_groups[0] + pl.gt / 2 - 1) / (pl.gt / 2);
     } else {
@@ -28,32 +28,34 @@ bool plan_gemv(int fmt, uint32_t k, const uint32_t* seg_groups, int nseg, bool p
         for (int i = 0; i < nseg; ++i) pl.tiles += (seg_groups[i] + pl.gt - 1) / pl.gt;
     }
     const uint32_t rl = 256 / pl.gt;
-    const int max_rpl = 16;
-    const uint32_t target = (uint32_t)std::max(1, cus) * 5 / 2;   // ~2.5 workgroups per CU
-    uint32_t s_des = std::max(1u, (target + pl.tiles / 2) / pl.tiles);
+    const int max_rpl = (fmt == FMT_Q4) ? 16 : 8;
+    const uint32_t target = (uint32_t)std::max(1, cus) * 2;   // ~2 workgroups per CU
+    const uint32_t s_des = std::max(1u, (target + pl.tiles / 2) / pl.tiles);
     const uint32_t kr_des = (k + s_des - 1) / s_des;
     const uint32_t rpl_des = std::max(1u, (kr_des + rl - 1) / rl);
     int rpl = 1;
     while (rpl < max_rpl && (uint32_t)rpl * 3 / 2 < rpl_des) rpl *= 2;   // nearest power of two
     const int forced_rpl = env_int("QORA_GEMV_RPL", 0);
-    if (forced_rpl == 1 || forced_rpl == 2 || forced_rpl == 4 || forced_rpl == 8 || forced_rpl == 16)
+    if ((forced_rpl == 1 || forced_rpl == 2 || forced_rpl == 4 || forced_rpl == 8 || forced_rpl == 16) &&
+        forced_rpl <= max_rpl)
         rpl = forced_rpl;
-    // keep the number of partials each tile must add bounded
-    while (rpl < max_rpl && (k + rl * rpl - 1) / (rl * rpl) > 64) rpl *= 2;
+    while (rpl < max_rpl && ((rl * (uint32_t)rpl) % row_align) != 0) rpl *= 2;
+    if ((rl * (uint32_t)rpl) % row_align != 0) return false;
     pl.rpl = rpl;
     pl.kr = rl * (uint32_t)rpl;
     pl.splits = (k + pl.kr - 1) / pl.kr;
-    (void)fmt;
     *plan = pl;
     return true;
 }
 
 void apply_plan(const GemvPlan& plan, GemvParams* p) {
-    uint32_t t0 = 0;
+    uint32_t t0 = 0, c0 = 0;
     for (int i = 0; i < p->nseg; ++i) {
         p->seg[i].tile0 = p->paired ? 0 : t0;
         p->seg[i].tiles = p->paired ? plan.tiles : (p->seg[i].groups + plan.gt - 1) / plan.gt;
+        p->seg[i].col0 = c0;
         t0 += p->seg[i].tiles;
+        c0 += p->seg[i].groups * 32u;
     }
     p->tiles = plan.tiles;
     p->splits = plan.splits;
@@ -64,11 +66,11 @@ template <int FMT, int GT>
 static hipError_t launch_gemv_gt(const GemvPlan& plan, const GemvParams& p, hipStream_t stream) {
     const dim3 grid(plan.blocks()), block(256);
     switch (plan.rpl) {
-    case 1: hipLaunchKernelGGL((gemv_splitk_kernel<FMT, GT, 1>), grid, block, 0, stream, p); break;
-    case 2: hipLaunchKernelGGL((gemv_splitk_kernel<FMT, GT, 2>), grid, block, 0, stream, p); break;
-    case 4: hipLaunchKernelGGL((gemv_splitk_kernel<FMT, GT, 4>), grid, block, 0, stream, p); break;
-    case 8: hipLaunchKernelGGL((gemv_splitk_kernel<FMT, GT, 8>), grid, block, 0, stream, p); break;
-    case 16: hipLaunchKernelGGL((gemv_splitk_kernel<FMT, GT, 16>), grid, block, 0, stream, p); break;
+    case 1: hipLaunchKernelGGL((gemv_kernel<FMT, GT, 1>), grid, block, 0, stream, p); break;
+    case 2: hipLaunchKernelGGL((gemv_kernel<FMT, GT, 2>), grid, block, 0, stream, p); break;
+    case 4: hipLaunchKernelGGL((gemv_kernel<FMT, GT, 4>), grid, block, 0, stream, p); break;
+    case 8: hipLaunchKernelGGL((gemv_kernel<FMT, GT, 8>), grid, block, 0, stream, p); break;
+    case 16: hipLaunchKernelGGL((gemv_kernel<FMT, GT, 16>), grid, block, 0, stream, p); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -84,6 +86,18 @@ hipError_t launch_gemv(int fmt, const GemvPlan& plan, const GemvParams& p, hipSt
         if (plan.gt == 16) return launch_gemv_gt<FMT_F16, 16>(plan, p, stream);
     }
     return hipErrorInvalidValue;
+}
+
+hipError_t launch_fill_zero(long long* p, uint64_t n, hipStream_t stream) {
+    const uint32_t blocks = (uint32_t)std::max<uint64_t>(1, std::min<uint64_t>(1024, (n + 255) / 256));
+    hipLaunchKernelGGL(fill_zero_kernel, dim3(blocks), dim3(256), 0, stream, p, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_acc_to_f32(const long long* acc, uint32_t n, int paired, float* y, hipStream_t stream) {
+    const uint32_t blocks = std::max(1u, std::min(1024u, (n + 255) / 256));
+    hipLaunchKernelGGL(acc_to_f32_kernel, dim3(blocks), dim3(256), 0, stream, acc, n, paired, y);
+    return hipGetLastError();
 }
 
 static constexpr int kRowdotU = 8;
@@ -104,10 +118,26 @@ hipError_t launch_rowdot(int fmt, uint32_t blocks, const RowdotParams& p, hipStr
     return hipGetLastError();
 }
 
-uint32_t attn_splits(uint32_t capacity) { return (capacity + kAttnChunk - 1) / kAttnChunk; }
+hipError_t launch_argmax_finish(const ArgmaxFinishParams& p, hipStream_t stream) {
+    hipLaunchKernelGGL(argmax_finish_kernel, dim3(1), dim3(256), 0, stream, p);
+    return hipGetLastError();
+}
+
+void attn_geometry(uint32_t positions, uint32_t* chunk, uint32_t* s_max) {
+    uint32_t c = (positions + kAttnMaxSplits - 1) / kAttnMaxSplits;
+    c = std::max<uint32_t>(kAttnSub, (c + kAttnSub - 1) / kAttnSub * kAttnSub);
+    *chunk = c;
+    *s_max = std::max<uint32_t>(1, (positions + c - 1) / c);
+}
 
 hipError_t launch_attn(const AttnParams& p, hipStream_t stream) {
-    hipLaunchKernelGGL(attn_decode_kernel, dim3(p.s_max, p.KVH), dim3(256), 0, stream, p);
+    if (p.hd <= 64) hipLaunchKernelGGL((attn_decode_kernel<1>), dim3(p.s_max, p.KVH), dim3(256), 0, stream, p);
+    else hipLaunchKernelGGL((attn_decode_kernel<2>), dim3(p.s_max, p.KVH), dim3(256), 0, stream, p);
+    return hipGetLastError();
+}
+
+hipError_t launch_attn_combine(const AttnCombineParams& p, hipStream_t stream) {
+    hipLaunchKernelGGL(attn_combine_kernel, dim3(p.H), dim3(128), 0, stream, p);
     return hipGetLastError();
 }
 

@@ -16,26 +16,35 @@ struct GemvPlan {
     uint32_t splits = 0;  // K slices
     uint32_t kr = 0;      // rows per K slice
     uint32_t blocks() const { return tiles * splits; }
-    uint64_t partial_floats() const { return splits > 1 ? (uint64_t)splits * tiles * gt * 32 : 0; }
 };
 
 // Chooses GT / RPL / S for k input rows. seg_groups: groups (n/32) of each
 // segment; paired: gate/up lane pairing (two segments of equal groups).
 // cus: compute units on the device. Returns false if the shape is unsupported.
-bool plan_gemv(int fmt, uint32_t k, const uint32_t* seg_groups, int nseg, bool paired, int cus,
-               GemvPlan* plan);
+// row_align (optional): K slices must start on multiples of it (head_dim
+// for the attention-merge prologue).
+bool plan_gemv(int fmt, uint32_t k, const uint32_t* seg_groups, int nseg, bool paired, int cus, GemvPlan* plan,
+               uint32_t row_align = 1);
 
-// Fills seg[].tile0/tiles, p.tiles/splits/rows_per_split from the plan.
+// Fills seg[].tile0/tiles/col0 and p.tiles/splits/rows_per_split from the plan.
+// Concatenated segments land one after the other in the accumulator; paired
+// segments at 0 (gate) and n (up).
 void apply_plan(const GemvPlan& plan, GemvParams* p);
 
 hipError_t launch_gemv(int fmt, const GemvPlan& plan, const GemvParams& p, hipStream_t stream);
+hipError_t launch_fill_zero(long long* p, uint64_t n, hipStream_t stream);
+hipError_t launch_acc_to_f32(const long long* acc, uint32_t n, int paired, float* y, hipStream_t stream);
 
 // Row-dot GEMV (lm_head). blocks: grid size (also the argmax partial count).
 uint32_t rowdot_blocks(uint32_t rows, uint32_t cols, int cus);
 hipError_t launch_rowdot(int fmt, uint32_t blocks, const RowdotParams& p, hipStream_t stream);
+hipError_t launch_argmax_finish(const ArgmaxFinishParams& p, hipStream_t stream);
 
-uint32_t attn_splits(uint32_t capacity);
+// Attention split geometry for up to `positions` positions: chunk is a
+// multiple of kAttnSub and s_max = ceil(positions / chunk) <= kAttnMaxSplits.
+void attn_geometry(uint32_t positions, uint32_t* chunk, uint32_t* s_max);
 hipError_t launch_attn(const AttnParams& p, hipStream_t stream);
+hipError_t launch_attn_combine(const AttnCombineParams& p, hipStream_t stream);
 
 hipError_t launch_embed(const EmbedParams& p, hipStream_t stream);
 hipError_t launch_dequant_q4(const uint8_t* packed, const uint16_t* scales, uint64_t k, uint64_t n,

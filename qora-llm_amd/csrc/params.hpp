@@ -6,75 +6,101 @@
 namespace qora {
 
 enum WFmt : int { FMT_F16 = 0, FMT_Q4 = 1 };
-enum Epi : int { EPI_STORE = 0, EPI_RESID = 1, EPI_SILU = 2, EPI_QKV = 3 };
+
+// Where a GEMV workgroup gets the input rows of its K slice.
+enum Pro : int {
+    PRO_PLAIN = 0,       // fp32 vector x[k]
+    PRO_NORM_FIXED = 1,  // RMSNorm(x) with x the fixed-point residual xacc[k] (norm over all k)
+    PRO_SILU_FIXED = 2,  // silu(g) * u with g = acc[0:k], u = acc[k:2k] (fixed point)
+    PRO_ATTN = 3,        // merge of the split-K attention partials of the heads in the slice
+};
+
+// Fixed-point accumulators: value = int64 / 2^36. Integer adds are exact and
+// associative, so the split-K sums are identical whatever order the
+// workgroups finish in. Range |v| < 1.3e8, resolution 1.5e-11.
+constexpr double kFixScale = 68719476736.0;   // 2^36
 
 struct GemvSeg {
-    const uint8_t* w;         // Q4 packed bytes or F16 words (as bytes)
+    const uint8_t* w;         // Q4 packed bytes or F16 words (as bytes), reference layout
     const uint16_t* scales;   // Q4 only
     uint32_t groups;          // n / 32
     uint32_t tile0;           // first column tile (concatenated mode)
     uint32_t tiles;           // column tiles of this segment
+    uint32_t col0;            // output offset of this segment in the accumulator
 };
 
 struct GemvParams {
     GemvSeg seg[3];
     int nseg;
     int paired;               // 1: seg0 = gate, seg1 = up, lanes split in halves
-    const float* x;           // input vector [k]
-    const uint16_t* gamma;    // optional RMSNorm gamma [k] (prologue)
     uint32_t k;
     uint32_t tiles;           // total column tiles
     uint32_t splits;          // S
     uint32_t rows_per_split;  // KR
-    float* partials;          // [S][tiles][GT*32]
-    uint32_t* counters;       // [tiles], zero between launches
-    int epi;
-    float* y;                 // STORE / RESID / SILU destination
-    // QKV epilogue
-    float* q_out;
-    void* kcache;
-    void* vcache;
-    int kv_f16;
-    uint32_t head_dim, half_dim, kv_stride;
-    const float* rope_cos;
-    const float* rope_sin;
+    int pro;
+    const float* x;           // PRO_PLAIN
+    const long long* xacc;    // PRO_NORM_FIXED / PRO_SILU_FIXED input accumulator
+    const uint16_t* gamma;    // PRO_NORM_FIXED
+    // PRO_ATTN: attention partials [KVH][s_max][groups][head_dim + 2]
+    const float* attn_part;
+    uint32_t attn_s_max, attn_chunk, head_dim, groups;
     const int32_t* pos;
-    int use_rope;
+    long long* acc;           // output: fixed-point accumulator (+= W x)
+    long long* zero_ptr;      // optional int64 buffer cleared by this launch
+    uint32_t zero_n;
 };
 
 struct RowdotParams {
     const uint8_t* w;
     const uint16_t* scales;
     uint32_t rows, cols;       // cols = hidden, multiple of 32, cols/32 divides 64
-    const float* x;
+    const float* x;            // fp32 input, or
+    const long long* xacc;     // fixed-point residual (used when non-null)
     const uint16_t* gamma;     // optional RMSNorm prologue
     float* y;                  // [rows]
     int do_argmax;
-    float* part_val;           // [gridDim.x]
+    float* part_val;           // [gridDim.x] per-workgroup best logit
     uint32_t* part_idx;
-    uint32_t* counter;         // zero between launches
-    int32_t* token_out;        // argmax result
-    int32_t* pos;              // if non-null: gen[pos] = argmax, pos += 1
+};
+
+struct ArgmaxFinishParams {
+    const float* part_val;
+    const uint32_t* part_idx;
+    uint32_t parts;
+    int32_t* token_out;
+    int32_t* pos;              // if non-null: gen[pos] = token, pos += 1
     int32_t* gen;
 };
 
-constexpr int kAttnChunk = 32;
+constexpr int kAttnSub = 32;         // positions staged in LDS at a time
 constexpr int kAttnMaxHd = 128;
 constexpr int kAttnMaxGroups = 4;
+constexpr int kAttnMaxSplits = 64;
 
 struct AttnParams {
-    const float* q;          // [H * hd]
-    const void* kc;
-    const void* vc;
+    const float* q;            // kernel-level: q [H*hd] fp32, already rotated
+    const long long* qkv_acc;  // model: fixed-point q|k|v; RoPE + cache append here
+    const float* rope_cos;
+    const float* rope_sin;
+    int use_rope;
+    uint32_t half;
+    void* kc;                  // [capacity][KVH][hd]
+    void* vc;
     int kv_f16;
-    const int32_t* pos;      // L = *pos + 1 when non-null
-    uint32_t L;              // used when pos is null
+    const int32_t* pos;        // L = *pos + 1 when non-null
+    uint32_t L;
     uint32_t H, KVH, hd, groups;
-    float scale;             // 1 / sqrt(hd)
-    float* part;             // [KVH][s_max][groups][hd + 2]
-    uint32_t* counters;      // [KVH], zero between launches
+    float scale;               // 1 / sqrt(hd)
+    uint32_t chunk;            // positions per split (multiple of kAttnSub)
+    float* part;               // [KVH][s_max][groups][hd + 2]
     uint32_t s_max;
-    float* out;              // [H * hd]
+};
+
+struct AttnCombineParams {
+    const float* part;
+    const int32_t* pos;
+    uint32_t L, H, KVH, hd, groups, chunk, s_max;
+    float* out;                // [H * hd]
 };
 
 struct EmbedParams {
@@ -85,7 +111,7 @@ struct EmbedParams {
     uint32_t vocab;          // token ids are clamped to [0, vocab)
     const int32_t* tok_src;
     const int32_t* tok_idx;  // optional index into tok_src (prefill: position)
-    float* x;
+    long long* xacc;         // fixed-point residual stream, set (not added)
 };
 
 }  // namespace qora
