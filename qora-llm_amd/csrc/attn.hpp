@@ -85,12 +85,15 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnParams p) {
 
     // ---- q of the group's heads (and the new k, v) ----
     if (model) {
+        // the q|k|v GEMV ran on x * gamma; its RMSNorm factor is applied here
+        const float inv = rms_inv_from_parts(p.ss_in, p.ss_n, p.norm_n);
         const uint32_t qd = p.H * hd;
-        for (uint32_t i = t; i < G * hd; i += NT) raw[i] = from_fixed(p.qkv_acc[(uint64_t)kvh * G * hd + i]);
+        for (uint32_t i = t; i < G * hd; i += NT)
+            raw[i] = inv * from_fixed(p.qkv_acc[(uint64_t)kvh * G * hd + i]);
         if (has_new)
             for (uint32_t d = t; d < hd; d += NT) {
-                raw[G * hd + d] = from_fixed(p.qkv_acc[qd + (uint64_t)kvh * hd + d]);
-                raw[(G + 1) * hd + d] = from_fixed(p.qkv_acc[qd + kv_stride + (uint64_t)kvh * hd + d]);
+                raw[G * hd + d] = inv * from_fixed(p.qkv_acc[qd + (uint64_t)kvh * hd + d]);
+                raw[(G + 1) * hd + d] = inv * from_fixed(p.qkv_acc[qd + kv_stride + (uint64_t)kvh * hd + d]);
             }
         __syncthreads();
         const float* ct = p.rope_cos + (uint64_t)cur * p.half;

@@ -50,6 +50,15 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
+// RMSNorm factor 1 / sqrt(sum(x^2) / n + 1e-6) (rms_norm_f16, gemv.rs:744-753)
+// from `parts` partial sums of squares (lane i loads partial i; parts <= 64).
+__device__ __forceinline__ float rms_inv_from_parts(const float* ss, uint32_t parts, uint32_t n) {
+    const uint32_t lane = threadIdx.x & (kWave - 1);
+    const float v = lane < parts ? ss[lane] : 0.f;
+    const float total = wave_sum(v);
+    return 1.0f / sqrtf(total / (float)n + 1e-6f);
+}
+
 // Block-wide sum for blockDim.x == NT (multiple of 64). `red` must hold
 // NT/64 floats of shared memory. Every thread receives the total.
 template <int NT>

@@ -40,6 +40,7 @@ struct ModelState {
     long long* d_qkv_acc = nullptr;      // q|k|v sums [qd + 2 kvd]
     long long* d_gu_acc = nullptr;       // gate|up sums [2 inter]
     float* d_attn_part = nullptr;        // attention split partials
+    float* d_ss = nullptr;               // [L][2][64] sums of squares per K slice (RMSNorm)
     float* d_logits = nullptr;
     int32_t* d_token = nullptr;
     int32_t* d_pos = nullptr;
@@ -417,6 +418,10 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
         free_model(c);
         return fail(c, QORA_HIP_E_INVALID, "unsupported GEMV shape");
     }
+    if (m.pl_qkv.splits > (uint32_t)kAttnMaxSplits || m.pl_gu.splits > (uint32_t)kAttnMaxSplits) {
+        free_model(c);
+        return fail(c, QORA_HIP_E_INVALID, "RMSNorm input split into more than 64 K slices");
+    }
     m.lm_blocks = rowdot_blocks(m.vocab, m.hidden, c->cus);
     attn_geometry(m.cap, &m.attn_chunk, &m.attn_s_max);
 
@@ -441,6 +446,7 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
     MALLOC(d_qkv_acc, qkv_n * 8);
     MALLOC(d_gu_acc, (size_t)2 * m.inter * 8);
     MALLOC(d_attn_part, (size_t)m.KVH * m.attn_s_max * m.groups * (m.hd + 2) * 4);
+    MALLOC(d_ss, (size_t)m.L * 2 * kAttnMaxSplits * 4);
     MALLOC(d_logits, (size_t)m.vocab * 4);
     MALLOC(d_token, 64);
     MALLOC(d_pos, 64);
@@ -492,9 +498,10 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
             q.seg[j] = GemvSeg{(const uint8_t*)W[j]->w, (const uint16_t*)W[j]->scales, (uint32_t)(W[j]->n / 32), 0, 0, 0};
         q.nseg = 3;
         q.k = m.hidden;
-        q.pro = PRO_NORM_FIXED;
+        q.pro = PRO_GAMMA_FIXED;
         q.xacc = m.d_xacc;
         q.gamma = m.d_norms + ((size_t)l * 2 + 0) * m.hidden;
+        q.ss_out = m.d_ss + ((size_t)l * 2 + 0) * kAttnMaxSplits;
         q.acc = m.d_qkv_acc;
         q.zero_ptr = m.d_gu_acc;
         q.zero_n = 2 * m.inter;
@@ -503,6 +510,9 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
         AttnParams& a = m.p_attn[l];
         a = AttnParams{};
         a.qkv_acc = m.d_qkv_acc;
+        a.ss_in = m.d_ss + ((size_t)l * 2 + 0) * kAttnMaxSplits;
+        a.ss_n = m.pl_qkv.splits;
+        a.norm_n = m.hidden;
         a.rope_cos = m.d_cos;
         a.rope_sin = m.d_sin;
         a.use_rope = d->use_rope[l] ? 1 : 0;
@@ -544,9 +554,10 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
         g.nseg = 2;
         g.paired = 1;
         g.k = m.hidden;
-        g.pro = PRO_NORM_FIXED;
+        g.pro = PRO_GAMMA_FIXED;
         g.xacc = m.d_xacc;
         g.gamma = m.d_norms + ((size_t)l * 2 + 1) * m.hidden;
+        g.ss_out = m.d_ss + ((size_t)l * 2 + 1) * kAttnMaxSplits;
         g.acc = m.d_gu_acc;
         apply_plan(m.pl_gu, &g);
 
@@ -557,6 +568,9 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
         dn.k = m.inter;
         dn.pro = PRO_SILU_FIXED;
         dn.xacc = m.d_gu_acc;
+        dn.ss_in = m.d_ss + ((size_t)l * 2 + 1) * kAttnMaxSplits;
+        dn.ss_n = m.pl_gu.splits;
+        dn.norm_n = m.hidden;
         dn.acc = m.d_xacc;
         apply_plan(m.pl_down, &dn);
     }

@@ -47,15 +47,22 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
 template <int NT>
 __device__ __forceinline__ float inv_rms_fixed(const long long* xacc, uint32_t n, float* wred) {
     float ss = 0.f;
-    for (uint32_t i = threadIdx.x; i < n; i += NT) {
-        const float v = from_fixed(xacc[i]);
-        ss += v * v;
+    const uint32_t last = n - 1u;
+    for (uint32_t i0 = threadIdx.x; i0 < n; i0 += 4 * NT) {
+        long long v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[u] = xacc[min(i0 + u * NT, last)];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const float f = from_fixed(v[u]);
+            ss += (i0 + u * NT < n) ? f * f : 0.f;
+        }
     }
     ss = block_sum<NT>(ss, wred);
     return 1.0f / sqrtf(ss / (float)n + 1e-6f);
 }
 
-template <int FMT, int GT, int RPL>
+template <int FMT, int GT, int RPL, int PRO>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
     constexpr int NT = 256;
     constexpr int RL = NT / GT;          // row lanes
@@ -64,11 +71,12 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
     constexpr int RED_STRIDE = 33;       // padded group stride in LDS
     constexpr int CPT = COLS / NT;       // columns per thread in the reduction
     constexpr int MAXH = KR / 32 + 1;    // heads a K slice can touch (head_dim >= 32)
+    constexpr bool kStage = PRO == PRO_ATTN;   // only the attention merge stages x in LDS
 
-    __shared__ float xs[KR];
+    __shared__ float xs[kStage ? KR : 1];
     __shared__ float red[NT * RED_STRIDE];
     __shared__ float wred[NT / kWave];
-    __shared__ float aw[kAttnMaxSplits * MAXH];
+    __shared__ float aw[kStage ? kAttnMaxSplits * MAXH : 1];
 
     const int t = threadIdx.x;
     const int gi = t % GT;
@@ -77,11 +85,12 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
     const uint32_t split = blockIdx.x / p.tiles;
     const uint32_t k0 = split * p.rows_per_split;
     const uint32_t k1 = min(p.k, k0 + p.rows_per_split);
+    const uint32_t klast = p.k - 1u;
 
     if (p.zero_ptr)
         for (uint32_t i = blockIdx.x * NT + t; i < p.zero_n; i += gridDim.x * NT) p.zero_ptr[i] = 0;
 
-    // ---- which segment / group this lane reads (issue the loads first) ----
+    // ---- which segment / group this lane reads ----
     int sidx;
     uint32_t grp;
     if (p.paired) {
@@ -91,53 +100,84 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
         sidx = 0;
         if (p.nseg > 1 && tile >= p.seg[1].tile0) sidx = 1;
         if (p.nseg > 2 && tile >= p.seg[2].tile0) sidx = 2;
-        grp = (tile - p.seg[sidx].tile0) * GT + gi;
+        const uint32_t t0 = sidx == 0 ? p.seg[0].tile0 : (sidx == 1 ? p.seg[1].tile0 : p.seg[2].tile0);
+        grp = (tile - t0) * GT + gi;
     }
-    const GemvSeg sg = p.seg[sidx];
-    const bool active = grp < sg.groups;
+    // Per-field selects over the kernarg values (a per-lane index into
+    // p.seg would fetch the struct with a vector load before any weight load).
+    GemvSeg sg;
+    sg.w = sidx == 0 ? p.seg[0].w : (sidx == 1 ? p.seg[1].w : p.seg[2].w);
+    sg.scales = sidx == 0 ? p.seg[0].scales : (sidx == 1 ? p.seg[1].scales : p.seg[2].scales);
+    sg.groups = sidx == 0 ? p.seg[0].groups : (sidx == 1 ? p.seg[1].groups : p.seg[2].groups);
+    sg.tile0 = sidx == 0 ? p.seg[0].tile0 : (sidx == 1 ? p.seg[1].tile0 : p.seg[2].tile0);
+    sg.col0 = sidx == 0 ? p.seg[0].col0 : (sidx == 1 ? p.seg[1].col0 : p.seg[2].col0);
+    // Every load is unconditional, so all of a lane's loads are in flight
+    // together and the math on row j starts when row j arrives: rows past
+    // the slice read a valid row and get a zero input; lanes past the
+    // segment read group 0 and their columns are never written.
+    const uint32_t grp_c = grp < sg.groups ? grp : 0u;
 
+    // ---- 1. input values of this lane's rows (direct loads, no LDS) ----
+    float xv[RPL];
+    long long xa[PRO == PRO_PLAIN || PRO == PRO_ATTN ? 1 : RPL];
+    long long ua[PRO == PRO_SILU_FIXED ? RPL : 1];
+    uint32_t gm[PRO == PRO_GAMMA_FIXED ? RPL : 1];
+#pragma unroll
+    for (int j = 0; j < RPL; ++j) {
+        const uint32_t rc = min(k0 + rl + j * RL, klast);
+        if constexpr (PRO == PRO_PLAIN) xv[j] = p.x[rc];
+        if constexpr (PRO == PRO_GAMMA_FIXED) {
+            xa[j] = p.xacc[rc];
+            gm[j] = p.gamma[rc];
+        }
+        if constexpr (PRO == PRO_SILU_FIXED) {
+            xa[j] = p.xacc[rc];
+            ua[j] = p.xacc[p.k + rc];
+        }
+    }
+    float ss_part = 0.f;
+    if constexpr (PRO == PRO_SILU_FIXED) ss_part = p.ss_in[min((uint32_t)(t & (kWave - 1)), p.ss_n - 1u)];
+
+    // ---- 2. weight loads ----
     float acc[32];
 #pragma unroll
     for (int c = 0; c < 32; ++c) acc[c] = 0.f;
-
     uint4 wq[FMT == FMT_Q4 ? RPL : 1];
-    uint16_t sq[FMT == FMT_Q4 ? RPL : 1];
+    uint32_t sq[FMT == FMT_Q4 ? RPL : 1];
     if constexpr (FMT == FMT_Q4) {
         const uint64_t row_bytes = (uint64_t)sg.groups * 16u;
 #pragma unroll
         for (int j = 0; j < RPL; ++j) {
-            const uint32_t r = k0 + rl + j * RL;
-            if (active && r < k1) {
-                wq[j] = *reinterpret_cast<const uint4*>(sg.w + r * row_bytes + (uint64_t)grp * 16u);
-                sq[j] = sg.scales[(uint64_t)r * sg.groups + grp];
-            } else {
-                wq[j] = make_uint4(0, 0, 0, 0);
-                sq[j] = 0;
-            }
+            const uint32_t r = min(k0 + rl + j * RL, klast);
+            wq[j] = *reinterpret_cast<const uint4*>(sg.w + r * row_bytes + (uint64_t)grp_c * 16u);
+            sq[j] = sg.scales[(uint64_t)r * sg.groups + grp_c];
         }
     }
 
-    // ---- prologue: the K slice of the input vector, in LDS ----
-    if (p.pro == PRO_PLAIN) {
-        for (int i = t; i < KR; i += NT) {
-            const uint32_t r = k0 + i;
-            xs[i] = r < k1 ? p.x[r] : 0.f;
+    // ---- 3. the input values ----
+    float ssq = 0.f;   // PRO_GAMMA_FIXED: sum of x^2 over this lane's rows
+    if constexpr (PRO == PRO_GAMMA_FIXED) {
+#pragma unroll
+        for (int j = 0; j < RPL; ++j) {
+            const bool ok = k0 + rl + j * RL < k1;
+            const float xf = ok ? from_fixed(xa[j]) : 0.f;
+            ssq += xf * xf;
+            xv[j] = xf * h2f((uint16_t)gm[j]);
         }
-    } else if (p.pro == PRO_NORM_FIXED) {
-        const float inv = inv_rms_fixed<NT>(p.xacc, p.k, wred);
-        for (int i = t; i < KR; i += NT) {
-            const uint32_t r = k0 + i;
-            xs[i] = r < k1 ? from_fixed(p.xacc[r]) * inv * h2f(p.gamma[r]) : 0.f;
+    } else if constexpr (PRO == PRO_SILU_FIXED) {
+        const float inv = 1.0f / sqrtf(wave_sum(t % kWave < (int)p.ss_n ? ss_part : 0.f) / (float)p.norm_n + 1e-6f);
+#pragma unroll
+        for (int j = 0; j < RPL; ++j) {
+            const bool ok = k0 + rl + j * RL < k1;
+            xv[j] = ok ? silu_mul(inv * from_fixed(xa[j]), inv * from_fixed(ua[j])) : 0.f;
         }
-    } else if (p.pro == PRO_SILU_FIXED) {
-        for (int i = t; i < KR; i += NT) {
-            const uint32_t r = k0 + i;
-            xs[i] = r < k1 ? silu_mul(from_fixed(p.xacc[r]), from_fixed(p.xacc[p.k + r])) : 0.f;
-        }
+    } else if constexpr (PRO == PRO_PLAIN) {
+#pragma unroll
+        for (int j = 0; j < RPL; ++j) xv[j] = (k0 + rl + j * RL < k1) ? xv[j] : 0.f;
     } else {
         // PRO_ATTN: rows [k0, k1) are dims of heads k0/hd .. (k1-1)/hd of the
         // attention output; merge their split partials (online-softmax merge:
-        // out = sum_s acc_s e^(m_s - m) / sum_s l_s e^(m_s - m)).
+        // out = sum_s acc_s e^(m_s - m) / sum_s l_s e^(m_s - m)), staged in LDS.
         const uint32_t hd = p.head_dim, G = p.groups;
         const uint32_t L = (uint32_t)(*p.pos) + 1u;
         const uint32_t s_act = min(p.attn_s_max, (L + p.attn_chunk - 1) / p.attn_chunk);
@@ -173,14 +213,16 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
             }
             xs[i] = v;
         }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < RPL; ++j) xv[j] = xs[rl + j * RL];
     }
-    __syncthreads();
 
     if constexpr (FMT == FMT_Q4) {
         float corr = 0.f;
 #pragma unroll
         for (int j = 0; j < RPL; ++j) {
-            const float sx = h2f(sq[j]) * xs[rl + j * RL];
+            const float sx = h2f((uint16_t)sq[j]) * xv[j];
             corr += sx;
             const uint32_t w4[4] = {wq[j].x, wq[j].y, wq[j].z, wq[j].w};
 #pragma unroll
@@ -208,19 +250,14 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
             uint4 wv[B][4];
 #pragma unroll
             for (int j = 0; j < B; ++j) {
-                const uint32_t r = k0 + rl + (j0 + j) * RL;
-                if (active && r < k1) {
-                    const uint4* src = reinterpret_cast<const uint4*>(sg.w + r * row_bytes + (uint64_t)grp * 64u);
+                const uint32_t r = min(k0 + rl + (j0 + j) * RL, klast);
+                const uint4* src = reinterpret_cast<const uint4*>(sg.w + r * row_bytes + (uint64_t)grp_c * 64u);
 #pragma unroll
-                    for (int v = 0; v < 4; ++v) wv[j][v] = src[v];
-                } else {
-#pragma unroll
-                    for (int v = 0; v < 4; ++v) wv[j][v] = make_uint4(0, 0, 0, 0);
-                }
+                for (int v = 0; v < 4; ++v) wv[j][v] = src[v];
             }
 #pragma unroll
             for (int j = 0; j < B; ++j) {
-                const float xr = xs[rl + (j0 + j) * RL];
+                const float xr = xv[j0 + j];
 #pragma unroll
                 for (int v = 0; v < 4; ++v) {
                     const uint32_t w4[4] = {wv[j][v].x, wv[j][v].y, wv[j][v].z, wv[j][v].w};
@@ -234,6 +271,12 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
         }
     }
 
+    // sum of x^2 of the K slice (each row once: the gi == 0 lanes of tile 0)
+    if constexpr (PRO == PRO_GAMMA_FIXED) {
+        const float ws = wave_sum((gi == 0) ? ssq : 0.f);
+        if ((t & (kWave - 1)) == 0) wred[t / kWave] = ws;
+    }
+
     // ---- reduce the RL row lanes of each group through LDS ----
     {
         float* dst = red + (rl * GT + gi) * RED_STRIDE;
@@ -241,6 +284,14 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
         for (int c = 0; c < 32; ++c) dst[c] = acc[c];
     }
     __syncthreads();
+    if constexpr (PRO == PRO_GAMMA_FIXED) {
+        if (t == 0 && tile == 0) {
+            float ws = 0.f;
+#pragma unroll
+            for (int w = 0; w < NT / kWave; ++w) ws += wred[w];
+            p.ss_out[split] = ws;
+        }
+    }
 #pragma unroll
     for (int cc = 0; cc < CPT; ++cc) {
         const int col = t + cc * NT;
@@ -249,16 +300,18 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
 #pragma unroll 8
         for (int r = 0; r < RL; ++r) s += red[(r * GT + g) * RED_STRIDE + c];
         // tile column -> (segment, local column) -> accumulator slot
-        uint32_t local;
-        int os;
+        uint32_t local, lim, col0;
         if (p.paired) {
-            os = g < GT / 2 ? 0 : 1;
-            local = tile * (COLS / 2) + (uint32_t)(col - os * (COLS / 2));
+            const bool up = g >= GT / 2;
+            local = tile * (COLS / 2) + (uint32_t)(col - (up ? COLS / 2 : 0));
+            lim = (up ? p.seg[1].groups : p.seg[0].groups) * 32u;
+            col0 = up ? p.seg[1].col0 : p.seg[0].col0;
         } else {
-            os = sidx;
-            local = (tile - p.seg[os].tile0) * COLS + (uint32_t)col;
+            local = (tile - sg.tile0) * COLS + (uint32_t)col;
+            lim = sg.groups * 32u;
+            col0 = sg.col0;
         }
-        if (local < p.seg[os].groups * 32u) fixed_add(p.acc + p.seg[os].col0 + local, s);
+        if (local < lim) fixed_add(p.acc + col0 + local, s);
     }
 }
 
@@ -309,15 +362,41 @@ __global__ __launch_bounds__(256) void rowdot_kernel(RowdotParams p) {
         }
     }
     float xr[32];
+    if (p.xacc) {
+        const longlong2* src = reinterpret_cast<const longlong2*>(p.xacc + g * 32);
+#pragma unroll
+        for (int c = 0; c < 16; ++c) {
+            const longlong2 v = src[c];
+            xr[2 * c] = from_fixed(v.x);
+            xr[2 * c + 1] = from_fixed(v.y);
+        }
+    } else {
+        const float4* src = reinterpret_cast<const float4*>(p.x + g * 32);
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            const float4 v = src[c];
+            xr[4 * c] = v.x;
+            xr[4 * c + 1] = v.y;
+            xr[4 * c + 2] = v.z;
+            xr[4 * c + 3] = v.w;
+        }
+    }
+    if (p.gamma) {
+        const uint4* gsrc = reinterpret_cast<const uint4*>(p.gamma + g * 32);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const uint4 gv = gsrc[c];
+            const uint32_t w4[4] = {gv.x, gv.y, gv.z, gv.w};
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+                xr[c * 8 + 2 * d] = xr[c * 8 + 2 * d] * inv_rms * h2f((uint16_t)(w4[d] & 0xFFFFu));
+                xr[c * 8 + 2 * d + 1] = xr[c * 8 + 2 * d + 1] * inv_rms * h2f((uint16_t)(w4[d] >> 16));
+            }
+        }
+    }
     float xsum = 0.f;
 #pragma unroll
-    for (int c = 0; c < 32; ++c) {
-        const uint32_t i = g * 32 + c;
-        float v = p.xacc ? from_fixed(p.xacc[i]) : p.x[i];
-        if (p.gamma) v = v * inv_rms * h2f(p.gamma[i]);
-        xr[c] = v;
-        xsum += v;
-    }
+    for (int c = 0; c < 32; ++c) xsum += xr[c];
 
     float best_v = -INFINITY;
     uint32_t best_i = 0xFFFFFFFFu;
@@ -328,17 +407,12 @@ __global__ __launch_bounds__(256) void rowdot_kernel(RowdotParams p) {
         float dots[U];
         if constexpr (FMT == FMT_Q4) {
             uint4 wv[U];
-            uint16_t sv[U];
+            uint32_t sv[U];
 #pragma unroll
             for (int u = 0; u < U; ++u) {
-                const uint32_t r = rb + u * row_step + ro;
-                if (r < p.rows) {
-                    wv[u] = *reinterpret_cast<const uint4*>(p.w + ((uint64_t)r * G + g) * 16u);
-                    sv[u] = p.scales[(uint64_t)r * G + g];
-                } else {
-                    wv[u] = make_uint4(0, 0, 0, 0);
-                    sv[u] = 0;
-                }
+                const uint32_t r = min(rb + u * row_step + ro, p.rows - 1u);
+                wv[u] = *reinterpret_cast<const uint4*>(p.w + ((uint64_t)r * G + g) * 16u);
+                sv[u] = p.scales[(uint64_t)r * G + g];
             }
 #pragma unroll
             for (int u = 0; u < U; ++u) {
@@ -364,15 +438,10 @@ __global__ __launch_bounds__(256) void rowdot_kernel(RowdotParams p) {
             uint4 wv[U][4];
 #pragma unroll
             for (int u = 0; u < U; ++u) {
-                const uint32_t r = rb + u * row_step + ro;
-                if (r < p.rows) {
-                    const uint4* src = reinterpret_cast<const uint4*>(p.w + ((uint64_t)r * G + g) * 64u);
+                const uint32_t r = min(rb + u * row_step + ro, p.rows - 1u);
+                const uint4* src = reinterpret_cast<const uint4*>(p.w + ((uint64_t)r * G + g) * 64u);
 #pragma unroll
-                    for (int v = 0; v < 4; ++v) wv[u][v] = src[v];
-                } else {
-#pragma unroll
-                    for (int v = 0; v < 4; ++v) wv[u][v] = make_uint4(0, 0, 0, 0);
-                }
+                for (int v = 0; v < 4; ++v) wv[u][v] = src[v];
             }
 #pragma unroll
             for (int u = 0; u < U; ++u) {

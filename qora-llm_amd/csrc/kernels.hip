@@ -62,18 +62,34 @@ void apply_plan(const GemvPlan& plan, GemvParams* p) {
     p->rows_per_split = plan.kr;
 }
 
-template <int FMT, int GT>
-static hipError_t launch_gemv_gt(const GemvPlan& plan, const GemvParams& p, hipStream_t stream) {
+template <int FMT, int GT, int PRO>
+static hipError_t launch_gemv_pro(const GemvPlan& plan, const GemvParams& p, hipStream_t stream) {
     const dim3 grid(plan.blocks()), block(256);
     switch (plan.rpl) {
-    case 1: hipLaunchKernelGGL((gemv_kernel<FMT, GT, 1>), grid, block, 0, stream, p); break;
-    case 2: hipLaunchKernelGGL((gemv_kernel<FMT, GT, 2>), grid, block, 0, stream, p); break;
-    case 4: hipLaunchKernelGGL((gemv_kernel<FMT, GT, 4>), grid, block, 0, stream, p); break;
-    case 8: hipLaunchKernelGGL((gemv_kernel<FMT, GT, 8>), grid, block, 0, stream, p); break;
-    case 16: hipLaunchKernelGGL((gemv_kernel<FMT, GT, 16>), grid, block, 0, stream, p); break;
+    case 1: hipLaunchKernelGGL((gemv_kernel<FMT, GT, 1, PRO>), grid, block, 0, stream, p); break;
+    case 2: hipLaunchKernelGGL((gemv_kernel<FMT, GT, 2, PRO>), grid, block, 0, stream, p); break;
+    case 4: hipLaunchKernelGGL((gemv_kernel<FMT, GT, 4, PRO>), grid, block, 0, stream, p); break;
+    case 8: hipLaunchKernelGGL((gemv_kernel<FMT, GT, 8, PRO>), grid, block, 0, stream, p); break;
+    case 16:
+        if constexpr (FMT == FMT_Q4) {
+            hipLaunchKernelGGL((gemv_kernel<FMT, GT, 16, PRO>), grid, block, 0, stream, p);
+            break;
+        }
+        return hipErrorInvalidValue;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
+}
+
+template <int FMT, int GT>
+static hipError_t launch_gemv_gt(const GemvPlan& plan, const GemvParams& p, hipStream_t stream) {
+    switch (p.pro) {
+    case PRO_PLAIN: return launch_gemv_pro<FMT, GT, PRO_PLAIN>(plan, p, stream);
+    case PRO_GAMMA_FIXED: return launch_gemv_pro<FMT, GT, PRO_GAMMA_FIXED>(plan, p, stream);
+    case PRO_SILU_FIXED: return launch_gemv_pro<FMT, GT, PRO_SILU_FIXED>(plan, p, stream);
+    case PRO_ATTN: return launch_gemv_pro<FMT, GT, PRO_ATTN>(plan, p, stream);
+    default: return hipErrorInvalidValue;
+    }
 }
 
 hipError_t launch_gemv(int fmt, const GemvPlan& plan, const GemvParams& p, hipStream_t stream) {

@@ -9,10 +9,14 @@ enum WFmt : int { FMT_F16 = 0, FMT_Q4 = 1 };
 
 // Where a GEMV workgroup gets the input rows of its K slice.
 enum Pro : int {
-    PRO_PLAIN = 0,       // fp32 vector x[k]
-    PRO_NORM_FIXED = 1,  // RMSNorm(x) with x the fixed-point residual xacc[k] (norm over all k)
-    PRO_SILU_FIXED = 2,  // silu(g) * u with g = acc[0:k], u = acc[k:2k] (fixed point)
-    PRO_ATTN = 3,        // merge of the split-K attention partials of the heads in the slice
+    PRO_PLAIN = 0,        // fp32 vector x[k]
+    PRO_GAMMA_FIXED = 1,  // x * gamma, x = the fixed-point residual xacc[k]. The RMSNorm
+                          // factor is a scalar, so it is applied by the consumer of the
+                          // output; workgroups of column tile 0 write sum(x^2) of their
+                          // K slice to ss_out[split] for it.
+    PRO_SILU_FIXED = 2,   // silu(inv * g) * (inv * u), g = xacc[0:k], u = xacc[k:2k], with
+                          // inv = RMSNorm factor from the ss_in partials
+    PRO_ATTN = 3,         // merge of the split attention partials of the heads in the slice
 };
 
 // Fixed-point accumulators: value = int64 / 2^36. Integer adds are exact and
@@ -39,8 +43,12 @@ struct GemvParams {
     uint32_t rows_per_split;  // KR
     int pro;
     const float* x;           // PRO_PLAIN
-    const long long* xacc;    // PRO_NORM_FIXED / PRO_SILU_FIXED input accumulator
-    const uint16_t* gamma;    // PRO_NORM_FIXED
+    const long long* xacc;    // PRO_GAMMA_FIXED / PRO_SILU_FIXED input accumulator
+    const uint16_t* gamma;    // PRO_GAMMA_FIXED
+    float* ss_out;            // PRO_GAMMA_FIXED: sum of squares per K slice [splits]
+    const float* ss_in;       // PRO_SILU_FIXED: partial sums of squares of the norm input
+    uint32_t ss_n;            // number of ss_in partials (<= 64)
+    uint32_t norm_n;          // length of the normalised vector
     // PRO_ATTN: attention partials [KVH][s_max][groups][head_dim + 2]
     const float* attn_part;
     uint32_t attn_s_max, attn_chunk, head_dim, groups;
@@ -80,6 +88,9 @@ constexpr int kAttnMaxSplits = 64;
 struct AttnParams {
     const float* q;            // kernel-level: q [H*hd] fp32, already rotated
     const long long* qkv_acc;  // model: fixed-point q|k|v; RoPE + cache append here
+    const float* ss_in;        // model: partial sums of squares of the q|k|v GEMV input
+    uint32_t ss_n;             // (the RMSNorm factor is applied to q, k, v here)
+    uint32_t norm_n;
     const float* rope_cos;
     const float* rope_sin;
     int use_rope;
