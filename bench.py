@@ -132,9 +132,23 @@ class Pool:
             self.ctx.free(base)
 
 
+def prepared_time(ctx, hip, wid, wid_up, paired, nbytes, x, acc):
+    """Average ms per launch of the decode step's GEMV kernel (tile layout,
+    qora_hip_gemv_run) over >= 768 MB of distinct packed copies."""
+    copies = max(4, math.ceil((768 << 20) / nbytes))
+    gids = [ctx.gemv_prepare(wid, wid_up, paired) for _ in range(copies)]
+    try:
+        fns = [(lambda g=g: ctx.check(ctx.lib.qora_hip_gemv_run(ctx.h, g, x, acc, None), "gemv_run")) for g in gids]
+        return time_graph(ctx, hip, fns)
+    finally:
+        for g in gids:
+            ctx.gemv_release(g)
+
+
 def gemv_roofline(ctx, hip, be, pkg):
-    """Per-shape GB/s of the Q4 GEMV kernel on the model's own weights: each
-    launch is one qora_hip_*_accumulate call (the decode step's kernel)."""
+    """Per-shape GB/s of the decode step's Q4 GEMV kernel on the model's own
+    weights (tile layout, qora_hip_gemv_prepare / qora_hip_gemv_run), and of
+    the tied lm_head row-dot kernel."""
     c = be.config
     lib, h = ctx.lib, ctx.h
     x = ctx.malloc(4 * c.intermediate)
@@ -144,24 +158,13 @@ def gemv_roofline(ctx, hip, be, pkg):
     shapes = c.weight_shapes()
     for j, label in ((0, "q/o 2048x2048"), (1, "k/v 2048x512"), (6, "down 11008x2048")):
         k, n = shapes[j]
-        wp, sp = ctx.weight_ptrs(int(be.wids[0, j]))
-        pool = Pool(ctx, hip, [(wp, k * n // 2), (sp, k * n // 16)])
-        fns = [(lambda p=pool.ptrs(i): ctx.check(lib.qora_hip_gemv_q4_accumulate(h, p[0], p[1], x, acc, k, n, None)))
-               for i in range(pool.copies)]
-        ms = time_graph(ctx, hip, fns)
-        pool.free()
+        ms = prepared_time(ctx, hip, int(be.wids[0, j]), 0, False, k * n // 2 + k * n // 16, x, acc)
         results[label] = {"us": ms * 1e3, "gbps": q4_bytes(k, n) / (ms * 1e-3) / 1e9}
     # fused gate+up (the dominant kernel)
     k, n = shapes[4]
-    gw, gs = ctx.weight_ptrs(int(be.wids[0, 4]))
-    uw, us = ctx.weight_ptrs(int(be.wids[0, 5]))
-    pool = Pool(ctx, hip, [(gw, k * n // 2), (gs, k * n // 16), (uw, k * n // 2), (us, k * n // 16)])
-    fns = [(lambda p=pool.ptrs(i): ctx.check(
-        lib.qora_hip_gate_up_q4_accumulate(h, p[0], p[1], p[2], p[3], x, acc, k, n, None)))
-        for i in range(pool.copies)]
-    ms = time_graph(ctx, hip, fns)
-    pool.free()
-    gu_bytes = 2 * (k * n // 2 + k * n // 16) + 4 * k + 4 * n
+    gu_w = 2 * (k * n // 2 + k * n // 16)
+    ms = prepared_time(ctx, hip, int(be.wids[0, 4]), int(be.wids[0, 5]), True, gu_w, x, acc)
+    gu_bytes = gu_w + 4 * k + 8 * n
     results["gate+up 2048x(2x11008)"] = {"us": ms * 1e3, "gbps": gu_bytes / (ms * 1e-3) / 1e9, "bytes": gu_bytes}
     # tied lm_head, row-dot
     ew, es = ctx.weight_ptrs(be.embed_wid)

@@ -151,6 +151,15 @@ int qora_hip_gate_up_q4_accumulate(qora_hip_ctx* ctx, const void* gate_packed, c
                                    const void* up_packed, const void* up_scales, const float* x, long long* acc,
                                    uint64_t k, uint64_t n, void* stream);
 int qora_hip_acc_to_f32(qora_hip_ctx* ctx, const long long* acc, uint64_t n, int paired, float* y, void* stream);
+/* The decode step's GEMV on uploaded weights (same kernel, plain fp32 x):
+ * prepare packs weight `wid` (paired != 0: the gate|up pair wid, wid_up)
+ * once into the tile layout the decode step streams (each workgroup reads
+ * one contiguous block); run launches acc[j] += (x . W)[j] exactly like
+ * the *_accumulate calls above; release frees the packed copy. prepare and
+ * release allocate / free, so they are refused during capture. */
+int qora_hip_gemv_prepare(qora_hip_ctx* ctx, uint32_t wid, uint32_t wid_up, int paired, uint32_t* gemv_id);
+int qora_hip_gemv_run(qora_hip_ctx* ctx, uint32_t gemv_id, const float* x, long long* acc, void* stream);
+int qora_hip_gemv_release(qora_hip_ctx* ctx, uint32_t gemv_id);
 /* lm_head_parallel_q4 / _f16 (gemv.rs:797-864): y[r] = sum_c x[c] W[r][c]
  * over a [rows][cols] matrix (the tied embedding); cols/32 must divide 64. */
 int qora_hip_gemv_q4_rowdot(qora_hip_ctx* ctx, const void* packed, const void* scales, const float* x,

@@ -97,6 +97,9 @@ SIGNATURES = {
     "qora_hip_gemv_q4_accumulate": (_I, [_P, _P, _P, _P, _P, _U64, _U64, _P]),
     "qora_hip_gate_up_q4_accumulate": (_I, [_P, _P, _P, _P, _P, _P, _P, _U64, _U64, _P]),
     "qora_hip_acc_to_f32": (_I, [_P, _P, _U64, _I, _P, _P]),
+    "qora_hip_gemv_prepare": (_I, [_P, _U32, _U32, _I, _P]),
+    "qora_hip_gemv_run": (_I, [_P, _U32, _P, _P, _P]),
+    "qora_hip_gemv_release": (_I, [_P, _U32]),
     "qora_hip_gemv_q4_rowdot": (_I, [_P, _P, _P, _P, _P, _U64, _U64, _P]),
     "qora_hip_gemv_f16_rowdot": (_I, [_P, _P, _P, _P, _U64, _U64, _P]),
     "qora_hip_gate_up_q4": (_I, [_P, _P, _P, _P, _P, _P, _P, _U64, _U64, _P]),
@@ -413,6 +416,20 @@ class HipContext:
             rc = self.lib.qora_hip_upload_f16(self.h, _ptr(w.data), w.data.size, w.k, w.n, ctypes.byref(wid))
         self.check(rc, "upload")
         return wid.value
+
+    def gemv_prepare(self, wid: int, wid_up: int = 0, paired: bool = False) -> int:
+        """Packs uploaded weights into the decode step's GEMV tile layout."""
+        gid = ctypes.c_uint32()
+        self.check(self.lib.qora_hip_gemv_prepare(self.h, wid, wid_up, int(paired), ctypes.byref(gid)),
+                   "gemv_prepare")
+        return gid.value
+
+    def gemv_run(self, gemv_id: int, x_dev: int, acc_dev: int, stream: int = 0) -> None:
+        """acc += x . W (fixed point) with the decode step's GEMV kernel."""
+        self.check(self.lib.qora_hip_gemv_run(self.h, gemv_id, x_dev, acc_dev, stream or None), "gemv_run")
+
+    def gemv_release(self, gemv_id: int) -> None:
+        self.check(self.lib.qora_hip_gemv_release(self.h, gemv_id), "gemv_release")
 
     def weight_ptrs(self, wid: int):
         a, b = ctypes.c_void_p(), ctypes.c_void_p()

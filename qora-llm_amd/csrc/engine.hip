@@ -63,6 +63,18 @@ struct ModelState {
 
 }  // namespace
 
+// A kernel-level GEMV bound to uploaded weights in tile layout.
+struct PreparedGemv {
+    bool alive = false;
+    int fmt = 0;
+    bool paired = false;
+    uint64_t k = 0, n = 0;
+    GemvPlan plan;
+    GemvParams p{};
+    void* tw = nullptr;
+    void* ts = nullptr;
+};
+
 struct qora_hip_ctx {
     int device = 0;
     hipStream_t stream = nullptr;
@@ -75,6 +87,7 @@ struct qora_hip_ctx {
     uint64_t ws_attn_part_n = 0;
     int32_t* h_pin = nullptr;            // pinned staging: [0] token in, [1] token out, [2] pos
     bool capturing = false;
+    std::vector<PreparedGemv> gemvs;
     ModelState m;
 };
 
@@ -159,6 +172,22 @@ int model_alloc(qora_hip_ctx* c, size_t bytes, void** p) {
 const DevWeight* get_weight(qora_hip_ctx* c, uint32_t wid) {
     if (wid >= c->weights.size() || !c->weights[wid].alive) return nullptr;
     return &c->weights[wid];
+}
+
+// Allocates the tile layout of a planned GEMV (model-owned) and packs the
+// reference-layout segments of *p into it.
+int pack_model_gemv(qora_hip_ctx* c, int fmt, const GemvPlan& pl, GemvParams* p) {
+    uint64_t wb = 0, sb = 0;
+    gemv_tile_bytes(fmt, pl, &wb, &sb);
+    void* tw = nullptr;
+    void* ts = nullptr;
+    if (int rc = model_alloc(c, wb, &tw)) return rc;
+    if (sb)
+        if (int rc = model_alloc(c, sb, &ts)) return rc;
+    HIP_TRY(c, launch_gemv_tile(fmt, pl, *p, (uint8_t*)tw, (uint16_t*)ts, c->stream));
+    p->tw = (const uint8_t*)tw;
+    p->ts = (const uint16_t*)ts;
+    return QORA_HIP_OK;
 }
 
 int record_step(qora_hip_ctx* c, bool with_lm_head) {
@@ -273,6 +302,10 @@ extern "C" int qora_hip_destroy(qora_hip_ctx* c) {
     (void)hipSetDevice(c->device);
     (void)hipStreamSynchronize(c->stream);
     free_model(c);
+    for (PreparedGemv& g : c->gemvs) {
+        if (g.tw) (void)hipFree(g.tw);
+        if (g.ts) (void)hipFree(g.ts);
+    }
     for (DevWeight& w : c->weights) {
         if (w.w) (void)hipFree(w.w);
         if (w.scales) (void)hipFree(w.scales);
@@ -506,6 +539,7 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
         q.zero_ptr = m.d_gu_acc;
         q.zero_n = 2 * m.inter;
         apply_plan(m.pl_qkv, &q);
+        if (int rc = pack_model_gemv(c, (int)m.fmt, m.pl_qkv, &q)) { free_model(c); return rc; }
 
         AttnParams& a = m.p_attn[l];
         a = AttnParams{};
@@ -546,6 +580,7 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
         o.zero_ptr = m.d_qkv_acc;
         o.zero_n = (uint32_t)qkv_n;
         apply_plan(m.pl_o, &o);
+        if (int rc = pack_model_gemv(c, (int)m.fmt, m.pl_o, &o)) { free_model(c); return rc; }
 
         GemvParams& g = m.p_gu[l];
         g = GemvParams{};
@@ -560,6 +595,7 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
         g.ss_out = m.d_ss + ((size_t)l * 2 + 1) * kAttnMaxSplits;
         g.acc = m.d_gu_acc;
         apply_plan(m.pl_gu, &g);
+        if (int rc = pack_model_gemv(c, (int)m.fmt, m.pl_gu, &g)) { free_model(c); return rc; }
 
         GemvParams& dn = m.p_down[l];
         dn = GemvParams{};
@@ -573,6 +609,7 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
         dn.norm_n = m.hidden;
         dn.acc = m.d_xacc;
         apply_plan(m.pl_down, &dn);
+        if (int rc = pack_model_gemv(c, (int)m.fmt, m.pl_down, &dn)) { free_model(c); return rc; }
     }
     m.p_lm = RowdotParams{};
     m.p_lm.w = (const uint8_t*)emb->w;
@@ -888,6 +925,80 @@ extern "C" int qora_hip_gate_up_q4_accumulate(qora_hip_ctx* c, const void* gp, c
                                               const void* us, const float* x, long long* acc, uint64_t k,
                                               uint64_t n, void* stream) {
     return gemv_acc_entry(c, FMT_Q4, gp, gs, up, us, x, acc, k, n, true, stream);
+}
+
+extern "C" int qora_hip_gemv_prepare(qora_hip_ctx* c, uint32_t wid, uint32_t wid_up, int paired, uint32_t* gemv_id) {
+    if (!c) return QORA_HIP_E_INVALID;
+    if (!gemv_id) return fail(c, QORA_HIP_E_INVALID, "null argument");
+    if (c->capturing) return fail(c, QORA_HIP_E_STATE, "gemv_prepare allocates: not allowed during capture");
+    const DevWeight* w0 = get_weight(c, wid);
+    const DevWeight* w1 = paired ? get_weight(c, wid_up) : nullptr;
+    if (!w0 || (paired && !w1)) return fail(c, QORA_HIP_E_INVALID, "unknown weight id");
+    if (paired && (w1->fmt != w0->fmt || w1->k != w0->k || w1->n != w0->n))
+        return fail(c, QORA_HIP_E_INVALID, "gate and up weights differ in format or shape");
+    if (w0->k > 0xFFFFFFFFull || w0->n / 32 > 0xFFFFFFFFull)
+        return fail(c, QORA_HIP_E_INVALID, "GEMV shape too large");
+    PreparedGemv g;
+    g.fmt = w0->fmt;
+    g.paired = paired != 0;
+    g.k = w0->k;
+    g.n = w0->n;
+    const uint32_t G = (uint32_t)(w0->n / 32);
+    const uint32_t groups[2] = {G, G};
+    if (!plan_gemv(g.fmt, (uint32_t)g.k, groups, g.paired ? 2 : 1, g.paired, c->cus, &g.plan))
+        return fail(c, QORA_HIP_E_INVALID, "unsupported GEMV shape");
+    g.p.seg[0] = GemvSeg{(const uint8_t*)w0->w, (const uint16_t*)w0->scales, G, 0, 0, 0};
+    g.p.nseg = 1;
+    if (g.paired) {
+        g.p.seg[1] = GemvSeg{(const uint8_t*)w1->w, (const uint16_t*)w1->scales, G, 0, 0, 0};
+        g.p.nseg = 2;
+        g.p.paired = 1;
+    }
+    g.p.k = (uint32_t)g.k;
+    g.p.pro = PRO_PLAIN;
+    apply_plan(g.plan, &g.p);
+    uint64_t wb = 0, sb = 0;
+    gemv_tile_bytes(g.fmt, g.plan, &wb, &sb);
+    if (int rc = dalloc(c, wb, &g.tw)) return rc;
+    if (sb)
+        if (int rc = dalloc(c, sb, &g.ts)) { (void)hipFree(g.tw); return rc; }
+    const hipError_t e = launch_gemv_tile(g.fmt, g.plan, g.p, (uint8_t*)g.tw, (uint16_t*)g.ts, c->stream);
+    const hipError_t e2 = e == hipSuccess ? hipStreamSynchronize(c->stream) : e;
+    if (e2 != hipSuccess) {
+        (void)hipFree(g.tw);
+        if (g.ts) (void)hipFree(g.ts);
+        return fail(c, QORA_HIP_E_DEVICE, std::string("gemv tile packing: ") + hipGetErrorString(e2));
+    }
+    g.p.tw = (const uint8_t*)g.tw;
+    g.p.ts = (const uint16_t*)g.ts;
+    g.alive = true;
+    *gemv_id = (uint32_t)c->gemvs.size();
+    c->gemvs.push_back(g);
+    return QORA_HIP_OK;
+}
+
+extern "C" int qora_hip_gemv_run(qora_hip_ctx* c, uint32_t gemv_id, const float* x, long long* acc, void* stream) {
+    if (!c) return QORA_HIP_E_INVALID;
+    if (gemv_id >= c->gemvs.size() || !c->gemvs[gemv_id].alive) return fail(c, QORA_HIP_E_INVALID, "unknown GEMV id");
+    if (!x || !acc) return fail(c, QORA_HIP_E_INVALID, "null argument");
+    const PreparedGemv& g = c->gemvs[gemv_id];
+    GemvParams p = g.p;
+    p.x = x;
+    p.acc = acc;
+    HIP_TRY(c, launch_gemv(g.fmt, g.plan, p, pick_stream(c, stream)));
+    return QORA_HIP_OK;
+}
+
+extern "C" int qora_hip_gemv_release(qora_hip_ctx* c, uint32_t gemv_id) {
+    if (!c) return QORA_HIP_E_INVALID;
+    if (gemv_id >= c->gemvs.size() || !c->gemvs[gemv_id].alive) return fail(c, QORA_HIP_E_INVALID, "unknown GEMV id");
+    if (c->capturing) return fail(c, QORA_HIP_E_STATE, "gemv_release frees: not allowed during capture");
+    HIP_TRY(c, hipStreamSynchronize(c->stream));
+    PreparedGemv& g = c->gemvs[gemv_id];
+    (void)hipFree(g.tw);
+    if (g.ts) (void)hipFree(g.ts);
+    g = PreparedGemv();
+    return QORA_HIP_OK;
 }
 
 extern "C" int qora_hip_acc_to_f32(qora_hip_ctx* c, const long long* acc, uint64_t n, int paired, float* y,

@@ -25,7 +25,13 @@
 //     finish the previous phase's reduction on the fly.
 // Segments: up to three weight matrices are addressed as one virtual matrix
 // (q|k|v concatenated by column tiles), or two matrices are paired lane by
-// lane (gate|up). The weights are read in the reference layout.
+// lane (gate|up).
+// Layouts: read in the reference layout, the GT*16-byte row segments of a
+// workgroup lie a full row apart (5.5 KB for 11008 columns), which the DRAM
+// serves at a fraction of its streaming rate. The decode step therefore
+// reads a copy in tile layout (gemv_tile_kernel): the bytes of each
+// workgroup in the order its lanes load them, one contiguous block per
+// workgroup and 4 KB per load step.
 #pragma once
 
 #include "common.hpp"
@@ -62,7 +68,67 @@ __device__ __forceinline__ float inv_rms_fixed(const long long* xacc, uint32_t n
     return 1.0f / sqrtf(ss / (float)n + 1e-6f);
 }
 
-template <int FMT, int GT, int RPL, int PRO>
+// Which matrix and which 32-column group lane gi of column tile `tile` reads
+// (shared by the GEMV kernel and the tile-layout packer, so both agree).
+// Lanes past the segment get group 0 (grp_c): their columns are never written.
+struct LaneSrc {
+    GemvSeg sg;
+    uint32_t grp;     // group within the segment (may be past the end)
+    uint32_t grp_c;   // grp clamped into the segment
+};
+
+__device__ __forceinline__ LaneSrc lane_source(const GemvParams& p, uint32_t tile, int gi, int gt) {
+    int sidx;
+    uint32_t grp;
+    if (p.paired) {
+        sidx = gi < gt / 2 ? 0 : 1;
+        grp = tile * (uint32_t)(gt / 2) + (uint32_t)(gi % (gt / 2));
+    } else {
+        sidx = 0;
+        if (p.nseg > 1 && tile >= p.seg[1].tile0) sidx = 1;
+        if (p.nseg > 2 && tile >= p.seg[2].tile0) sidx = 2;
+        const uint32_t t0 = sidx == 0 ? p.seg[0].tile0 : (sidx == 1 ? p.seg[1].tile0 : p.seg[2].tile0);
+        grp = (tile - t0) * (uint32_t)gt + (uint32_t)gi;
+    }
+    // Per-field selects over the kernarg values (a per-lane index into
+    // p.seg would fetch the struct with a vector load before any weight load).
+    LaneSrc s;
+    s.sg.w = sidx == 0 ? p.seg[0].w : (sidx == 1 ? p.seg[1].w : p.seg[2].w);
+    s.sg.scales = sidx == 0 ? p.seg[0].scales : (sidx == 1 ? p.seg[1].scales : p.seg[2].scales);
+    s.sg.groups = sidx == 0 ? p.seg[0].groups : (sidx == 1 ? p.seg[1].groups : p.seg[2].groups);
+    s.sg.tile0 = sidx == 0 ? p.seg[0].tile0 : (sidx == 1 ? p.seg[1].tile0 : p.seg[2].tile0);
+    s.sg.col0 = sidx == 0 ? p.seg[0].col0 : (sidx == 1 ? p.seg[1].col0 : p.seg[2].col0);
+    s.sg.tiles = 0;
+    s.grp = grp;
+    s.grp_c = grp < s.sg.groups ? grp : 0u;
+    return s;
+}
+
+// Tile-layout packer: one workgroup per (GEMV workgroup b, row step j)
+// copies what lane t of GEMV workgroup b loads at step j (16 B of Q4 or 64 B
+// of F16, and the Q4 scale) into load order. grid = blocks * rpl, 256 lanes.
+template <int FMT>
+__global__ __launch_bounds__(256) void gemv_tile_kernel(GemvParams p, int gt, int rpl, uint8_t* tw, uint16_t* ts) {
+    const int t = threadIdx.x;
+    const uint32_t b = blockIdx.x / (uint32_t)rpl;
+    const uint32_t j = blockIdx.x % (uint32_t)rpl;
+    const uint32_t tile = b % p.tiles, split = b / p.tiles;
+    const uint32_t RL = 256u / (uint32_t)gt;
+    const LaneSrc src = lane_source(p, tile, t % gt, gt);
+    const uint32_t r = min(split * p.rows_per_split + (uint32_t)(t / gt) + j * RL, p.k - 1u);
+    if constexpr (FMT == FMT_Q4) {
+        const uint4 v = *reinterpret_cast<const uint4*>(src.sg.w + ((uint64_t)r * src.sg.groups + src.grp_c) * 16u);
+        *reinterpret_cast<uint4*>(tw + (((uint64_t)b * rpl + j) * 256u + t) * 16u) = v;
+        ts[((uint64_t)b * 256u + t) * rpl + j] = src.sg.scales[(uint64_t)r * src.sg.groups + src.grp_c];
+    } else {
+        const uint4* s = reinterpret_cast<const uint4*>(src.sg.w + ((uint64_t)r * src.sg.groups + src.grp_c) * 64u);
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+            *reinterpret_cast<uint4*>(tw + ((((uint64_t)b * rpl + j) * 4u + v) * 256u + t) * 16u) = s[v];
+    }
+}
+
+template <int FMT, int GT, int RPL, int PRO, bool TILED>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
     constexpr int NT = 256;
     constexpr int RL = NT / GT;          // row lanes
@@ -91,31 +157,13 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
         for (uint32_t i = blockIdx.x * NT + t; i < p.zero_n; i += gridDim.x * NT) p.zero_ptr[i] = 0;
 
     // ---- which segment / group this lane reads ----
-    int sidx;
-    uint32_t grp;
-    if (p.paired) {
-        sidx = gi < GT / 2 ? 0 : 1;
-        grp = tile * (GT / 2) + (gi % (GT / 2));
-    } else {
-        sidx = 0;
-        if (p.nseg > 1 && tile >= p.seg[1].tile0) sidx = 1;
-        if (p.nseg > 2 && tile >= p.seg[2].tile0) sidx = 2;
-        const uint32_t t0 = sidx == 0 ? p.seg[0].tile0 : (sidx == 1 ? p.seg[1].tile0 : p.seg[2].tile0);
-        grp = (tile - t0) * GT + gi;
-    }
-    // Per-field selects over the kernarg values (a per-lane index into
-    // p.seg would fetch the struct with a vector load before any weight load).
-    GemvSeg sg;
-    sg.w = sidx == 0 ? p.seg[0].w : (sidx == 1 ? p.seg[1].w : p.seg[2].w);
-    sg.scales = sidx == 0 ? p.seg[0].scales : (sidx == 1 ? p.seg[1].scales : p.seg[2].scales);
-    sg.groups = sidx == 0 ? p.seg[0].groups : (sidx == 1 ? p.seg[1].groups : p.seg[2].groups);
-    sg.tile0 = sidx == 0 ? p.seg[0].tile0 : (sidx == 1 ? p.seg[1].tile0 : p.seg[2].tile0);
-    sg.col0 = sidx == 0 ? p.seg[0].col0 : (sidx == 1 ? p.seg[1].col0 : p.seg[2].col0);
+    const LaneSrc src = lane_source(p, tile, gi, GT);
+    const GemvSeg& sg = src.sg;
     // Every load is unconditional, so all of a lane's loads are in flight
     // together and the math on row j starts when row j arrives: rows past
     // the slice read a valid row and get a zero input; lanes past the
     // segment read group 0 and their columns are never written.
-    const uint32_t grp_c = grp < sg.groups ? grp : 0u;
+    const uint32_t grp_c = src.grp_c;
 
     // ---- 1. input values of this lane's rows (direct loads, no LDS) ----
     float xv[RPL];
@@ -144,7 +192,34 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
     for (int c = 0; c < 32; ++c) acc[c] = 0.f;
     uint4 wq[FMT == FMT_Q4 ? RPL : 1];
     uint32_t sq[FMT == FMT_Q4 ? RPL : 1];
-    if constexpr (FMT == FMT_Q4) {
+    if constexpr (FMT == FMT_Q4 && TILED) {
+        // one contiguous block per workgroup: step j reads 4 KB, lane t 16 B
+        const uint8_t* bw = p.tw + (uint64_t)blockIdx.x * (RPL * 4096u) + (uint32_t)t * 16u;
+#pragma unroll
+        for (int j = 0; j < RPL; ++j) wq[j] = *reinterpret_cast<const uint4*>(bw + j * 4096u);
+        // the lane's RPL scales are adjacent
+        const uint16_t* bs = p.ts + ((uint64_t)blockIdx.x * 256u + (uint32_t)t) * RPL;
+        if constexpr (RPL >= 8) {
+#pragma unroll
+            for (int h = 0; h < RPL / 8; ++h) {
+                const uint4 v = reinterpret_cast<const uint4*>(bs)[h];
+                const uint32_t v4[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    sq[8 * h + 2 * e] = v4[e] & 0xFFFFu;
+                    sq[8 * h + 2 * e + 1] = v4[e] >> 16;
+                }
+            }
+        } else if constexpr (RPL == 4) {
+            const uint2 v = *reinterpret_cast<const uint2*>(bs);
+            sq[0] = v.x & 0xFFFFu; sq[1] = v.x >> 16; sq[2] = v.y & 0xFFFFu; sq[3] = v.y >> 16;
+        } else if constexpr (RPL == 2) {
+            const uint32_t v = *reinterpret_cast<const uint32_t*>(bs);
+            sq[0] = v & 0xFFFFu; sq[1] = v >> 16;
+        } else {
+            sq[0] = bs[0];
+        }
+    } else if constexpr (FMT == FMT_Q4) {
         const uint64_t row_bytes = (uint64_t)sg.groups * 16u;
 #pragma unroll
         for (int j = 0; j < RPL; ++j) {
@@ -219,29 +294,24 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
     }
 
     if constexpr (FMT == FMT_Q4) {
-        float corr = 0.f;
+        const NibbleConsts nk = nibble_consts();
 #pragma unroll
         for (int j = 0; j < RPL; ++j) {
             const float sx = h2f((uint16_t)sq[j]) * xv[j];
-            corr += sx;
             const uint32_t w4[4] = {wq[j].x, wq[j].y, wq[j].z, wq[j].w};
 #pragma unroll
             for (int d = 0; d < 4; ++d) {
-                const uint32_t lo = w4[d] & 0x0F0F0F0Fu;
-                const uint32_t hi = (w4[d] >> 4) & 0x0F0F0F0Fu;
-                acc[d * 8 + 0] = fmaf(sx, ubyte_f<0>(lo), acc[d * 8 + 0]);
-                acc[d * 8 + 1] = fmaf(sx, ubyte_f<0>(hi), acc[d * 8 + 1]);
-                acc[d * 8 + 2] = fmaf(sx, ubyte_f<1>(lo), acc[d * 8 + 2]);
-                acc[d * 8 + 3] = fmaf(sx, ubyte_f<1>(hi), acc[d * 8 + 3]);
-                acc[d * 8 + 4] = fmaf(sx, ubyte_f<2>(lo), acc[d * 8 + 4]);
-                acc[d * 8 + 5] = fmaf(sx, ubyte_f<2>(hi), acc[d * 8 + 5]);
-                acc[d * 8 + 6] = fmaf(sx, ubyte_f<3>(lo), acc[d * 8 + 6]);
-                acc[d * 8 + 7] = fmaf(sx, ubyte_f<3>(hi), acc[d * 8 + 7]);
+                const Nib8 nb = unpack_nibbles(w4[d], nk);
+                acc[d * 8 + 0] = fmaf(f16lo(nb.c04), sx, acc[d * 8 + 0]);
+                acc[d * 8 + 4] = fmaf(f16hi(nb.c04), sx, acc[d * 8 + 4]);
+                acc[d * 8 + 1] = fmaf(f16lo(nb.c15), sx, acc[d * 8 + 1]);
+                acc[d * 8 + 5] = fmaf(f16hi(nb.c15), sx, acc[d * 8 + 5]);
+                acc[d * 8 + 2] = fmaf(f16lo(nb.c26), sx, acc[d * 8 + 2]);
+                acc[d * 8 + 6] = fmaf(f16hi(nb.c26), sx, acc[d * 8 + 6]);
+                acc[d * 8 + 3] = fmaf(f16lo(nb.c37), sx, acc[d * 8 + 3]);
+                acc[d * 8 + 7] = fmaf(f16hi(nb.c37), sx, acc[d * 8 + 7]);
             }
         }
-        // sum_r sx_r*(q-8) = sum_r sx_r*q - 8*sum_r sx_r
-#pragma unroll
-        for (int c = 0; c < 32; ++c) acc[c] = fmaf(-8.0f, corr, acc[c]);
     } else {
         const uint64_t row_bytes = (uint64_t)sg.groups * 64u;
         constexpr int B = RPL < 4 ? RPL : 4;   // rows of 64 B in flight per batch
@@ -250,10 +320,17 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
             uint4 wv[B][4];
 #pragma unroll
             for (int j = 0; j < B; ++j) {
-                const uint32_t r = min(k0 + rl + (j0 + j) * RL, klast);
-                const uint4* src = reinterpret_cast<const uint4*>(sg.w + r * row_bytes + (uint64_t)grp_c * 64u);
+                if constexpr (TILED) {
+                    const uint8_t* bw = p.tw + ((uint64_t)blockIdx.x * RPL + (uint32_t)(j0 + j)) * 16384u +
+                                        (uint32_t)t * 16u;
 #pragma unroll
-                for (int v = 0; v < 4; ++v) wv[j][v] = src[v];
+                    for (int v = 0; v < 4; ++v) wv[j][v] = *reinterpret_cast<const uint4*>(bw + v * 4096u);
+                } else {
+                    const uint32_t r = min(k0 + rl + (j0 + j) * RL, klast);
+                    const uint4* wsrc = reinterpret_cast<const uint4*>(sg.w + r * row_bytes + (uint64_t)grp_c * 64u);
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) wv[j][v] = wsrc[v];
+                }
             }
 #pragma unroll
             for (int j = 0; j < B; ++j) {
@@ -394,9 +471,7 @@ __global__ __launch_bounds__(256) void rowdot_kernel(RowdotParams p) {
             }
         }
     }
-    float xsum = 0.f;
-#pragma unroll
-    for (int c = 0; c < 32; ++c) xsum += xr[c];
+    const NibbleConsts nk = nibble_consts();
 
     float best_v = -INFINITY;
     uint32_t best_i = 0xFFFFFFFFu;
@@ -420,19 +495,18 @@ __global__ __launch_bounds__(256) void rowdot_kernel(RowdotParams p) {
                 float d0 = 0.f, d1 = 0.f;
 #pragma unroll
                 for (int d = 0; d < 4; ++d) {
-                    const uint32_t lo = w4[d] & 0x0F0F0F0Fu;
-                    const uint32_t hi = (w4[d] >> 4) & 0x0F0F0F0Fu;
-                    d0 = fmaf(xr[d * 8 + 0], ubyte_f<0>(lo), d0);
-                    d1 = fmaf(xr[d * 8 + 1], ubyte_f<0>(hi), d1);
-                    d0 = fmaf(xr[d * 8 + 2], ubyte_f<1>(lo), d0);
-                    d1 = fmaf(xr[d * 8 + 3], ubyte_f<1>(hi), d1);
-                    d0 = fmaf(xr[d * 8 + 4], ubyte_f<2>(lo), d0);
-                    d1 = fmaf(xr[d * 8 + 5], ubyte_f<2>(hi), d1);
-                    d0 = fmaf(xr[d * 8 + 6], ubyte_f<3>(lo), d0);
-                    d1 = fmaf(xr[d * 8 + 7], ubyte_f<3>(hi), d1);
+                    const Nib8 nb = unpack_nibbles(w4[d], nk);
+                    d0 = fmaf(f16lo(nb.c04), xr[d * 8 + 0], d0);
+                    d1 = fmaf(f16hi(nb.c04), xr[d * 8 + 4], d1);
+                    d0 = fmaf(f16lo(nb.c15), xr[d * 8 + 1], d0);
+                    d1 = fmaf(f16hi(nb.c15), xr[d * 8 + 5], d1);
+                    d0 = fmaf(f16lo(nb.c26), xr[d * 8 + 2], d0);
+                    d1 = fmaf(f16hi(nb.c26), xr[d * 8 + 6], d1);
+                    d0 = fmaf(f16lo(nb.c37), xr[d * 8 + 3], d0);
+                    d1 = fmaf(f16hi(nb.c37), xr[d * 8 + 7], d1);
                 }
-                // sum_c x_c * s * (q_c - 8) = s * (sum_c x_c q_c - 8 sum_c x_c)
-                dots[u] = h2f(sv[u]) * fmaf(-8.0f, xsum, d0 + d1);
+                // sum_c x_c * s * (q_c - 8) = s * sum_c x_c * (q_c - 8)
+                dots[u] = h2f(sv[u]) * (d0 + d1);
             }
         } else {
             uint4 wv[U][4];

@@ -62,17 +62,17 @@ void apply_plan(const GemvPlan& plan, GemvParams* p) {
     p->rows_per_split = plan.kr;
 }
 
-template <int FMT, int GT, int PRO>
+template <int FMT, int GT, int PRO, bool TILED>
 static hipError_t launch_gemv_pro(const GemvPlan& plan, const GemvParams& p, hipStream_t stream) {
     const dim3 grid(plan.blocks()), block(256);
     switch (plan.rpl) {
-    case 1: hipLaunchKernelGGL((gemv_kernel<FMT, GT, 1, PRO>), grid, block, 0, stream, p); break;
-    case 2: hipLaunchKernelGGL((gemv_kernel<FMT, GT, 2, PRO>), grid, block, 0, stream, p); break;
-    case 4: hipLaunchKernelGGL((gemv_kernel<FMT, GT, 4, PRO>), grid, block, 0, stream, p); break;
-    case 8: hipLaunchKernelGGL((gemv_kernel<FMT, GT, 8, PRO>), grid, block, 0, stream, p); break;
+    case 1: hipLaunchKernelGGL((gemv_kernel<FMT, GT, 1, PRO, TILED>), grid, block, 0, stream, p); break;
+    case 2: hipLaunchKernelGGL((gemv_kernel<FMT, GT, 2, PRO, TILED>), grid, block, 0, stream, p); break;
+    case 4: hipLaunchKernelGGL((gemv_kernel<FMT, GT, 4, PRO, TILED>), grid, block, 0, stream, p); break;
+    case 8: hipLaunchKernelGGL((gemv_kernel<FMT, GT, 8, PRO, TILED>), grid, block, 0, stream, p); break;
     case 16:
         if constexpr (FMT == FMT_Q4) {
-            hipLaunchKernelGGL((gemv_kernel<FMT, GT, 16, PRO>), grid, block, 0, stream, p);
+            hipLaunchKernelGGL((gemv_kernel<FMT, GT, 16, PRO, TILED>), grid, block, 0, stream, p);
             break;
         }
         return hipErrorInvalidValue;
@@ -83,11 +83,17 @@ static hipError_t launch_gemv_pro(const GemvPlan& plan, const GemvParams& p, hip
 
 template <int FMT, int GT>
 static hipError_t launch_gemv_gt(const GemvPlan& plan, const GemvParams& p, hipStream_t stream) {
+    if (!p.tw) {
+        // reference layout: the kernel-level plain GEMV entry points only
+        if (p.pro != PRO_PLAIN) return hipErrorInvalidValue;
+        return launch_gemv_pro<FMT, GT, PRO_PLAIN, false>(plan, p, stream);
+    }
+    if (FMT == FMT_Q4 && !p.ts) return hipErrorInvalidValue;
     switch (p.pro) {
-    case PRO_PLAIN: return launch_gemv_pro<FMT, GT, PRO_PLAIN>(plan, p, stream);
-    case PRO_GAMMA_FIXED: return launch_gemv_pro<FMT, GT, PRO_GAMMA_FIXED>(plan, p, stream);
-    case PRO_SILU_FIXED: return launch_gemv_pro<FMT, GT, PRO_SILU_FIXED>(plan, p, stream);
-    case PRO_ATTN: return launch_gemv_pro<FMT, GT, PRO_ATTN>(plan, p, stream);
+    case PRO_PLAIN: return launch_gemv_pro<FMT, GT, PRO_PLAIN, true>(plan, p, stream);
+    case PRO_GAMMA_FIXED: return launch_gemv_pro<FMT, GT, PRO_GAMMA_FIXED, true>(plan, p, stream);
+    case PRO_SILU_FIXED: return launch_gemv_pro<FMT, GT, PRO_SILU_FIXED, true>(plan, p, stream);
+    case PRO_ATTN: return launch_gemv_pro<FMT, GT, PRO_ATTN, true>(plan, p, stream);
     default: return hipErrorInvalidValue;
     }
 }
@@ -102,6 +108,27 @@ hipError_t launch_gemv(int fmt, const GemvPlan& plan, const GemvParams& p, hipSt
         if (plan.gt == 16) return launch_gemv_gt<FMT_F16, 16>(plan, p, stream);
     }
     return hipErrorInvalidValue;
+}
+
+void gemv_tile_bytes(int fmt, const GemvPlan& plan, uint64_t* w_bytes, uint64_t* s_bytes) {
+    const uint64_t steps = (uint64_t)plan.blocks() * (uint64_t)plan.rpl;
+    *w_bytes = steps * 256u * (fmt == FMT_Q4 ? 16u : 64u);
+    *s_bytes = fmt == FMT_Q4 ? steps * 256u * 2u : 0u;
+}
+
+hipError_t launch_gemv_tile(int fmt, const GemvPlan& plan, const GemvParams& p, uint8_t* tw, uint16_t* ts,
+                            hipStream_t stream) {
+    const uint64_t grid = (uint64_t)plan.blocks() * (uint64_t)plan.rpl;
+    if (grid == 0 || grid > 0x7FFFFFFFull || p.k == 0) return hipErrorInvalidValue;
+    if (fmt == FMT_Q4) {
+        if (!ts) return hipErrorInvalidValue;
+        hipLaunchKernelGGL(gemv_tile_kernel<FMT_Q4>, dim3((uint32_t)grid), dim3(256), 0, stream, p, plan.gt, plan.rpl,
+                           tw, ts);
+    } else {
+        hipLaunchKernelGGL(gemv_tile_kernel<FMT_F16>, dim3((uint32_t)grid), dim3(256), 0, stream, p, plan.gt,
+                           plan.rpl, tw, ts);
+    }
+    return hipGetLastError();
 }
 
 hipError_t launch_fill_zero(long long* p, uint64_t n, hipStream_t stream) {

@@ -31,7 +31,15 @@ bool plan_gemv(int fmt, uint32_t k, const uint32_t* seg_groups, int nseg, bool p
 // segments at 0 (gate) and n (up).
 void apply_plan(const GemvPlan& plan, GemvParams* p);
 
+// p.tw == nullptr: reference layout, plain prologue only (kernel-level
+// entry points). Otherwise the tile layout written by launch_gemv_tile.
 hipError_t launch_gemv(int fmt, const GemvPlan& plan, const GemvParams& p, hipStream_t stream);
+// Size of the tile layout of a planned GEMV (scales: Q4 only).
+void gemv_tile_bytes(int fmt, const GemvPlan& plan, uint64_t* w_bytes, uint64_t* s_bytes);
+// Writes the tile layout of the reference-layout segments of p (after
+// apply_plan) into tw / ts, sized by gemv_tile_bytes.
+hipError_t launch_gemv_tile(int fmt, const GemvPlan& plan, const GemvParams& p, uint8_t* tw, uint16_t* ts,
+                            hipStream_t stream);
 hipError_t launch_fill_zero(long long* p, uint64_t n, hipStream_t stream);
 hipError_t launch_acc_to_f32(const long long* acc, uint32_t n, int paired, float* y, hipStream_t stream);
 

@@ -56,6 +56,13 @@ struct GemvParams {
     long long* acc;           // output: fixed-point accumulator (+= W x)
     long long* zero_ptr;      // optional int64 buffer cleared by this launch
     uint32_t zero_n;
+    // Tile layout (set by gemv_tile_kernel): the bytes every workgroup loads,
+    // stored in load order so each workgroup streams one contiguous block.
+    //   Q4 : tw[block][j < RPL][lane < 256] x 16 B, ts[block][lane][j] scales
+    //   F16: tw[block][j][v < 4][lane] x 16 B
+    // The segment pointers then only describe the shape.
+    const uint8_t* tw;
+    const uint16_t* ts;
 };
 
 struct RowdotParams {

@@ -1,0 +1,168 @@
+"""The decode step's GEMV on the tile layout, through qora_hip_gemv_prepare/run.
+
+The tile layout only reorders bytes (each workgroup's loads in load order),
+so with the same launch plan the prepared GEMV does the same per-lane
+arithmetic as the reference-layout *_accumulate entry points: the fixed-point
+sums are compared bit-exactly against them, and the outputs against the
+oracle at REL_TOL (max error over max |reference|, fp32 accumulation)."""
+import numpy as np
+import pytest
+
+from helpers import REL_TOL, device, dequant_np, exact_q4, rel_err
+
+pytestmark = pytest.mark.gpu
+
+FIX = 2.0 ** 36
+SHAPES = [(2048, 11008), (11008, 2048), (2048, 2048), (2048, 512), (1, 32), (3, 96), (37, 224), (300, 352),
+          (513, 64), (4097, 1056)]
+PAIRED = [(2048, 11008), (2048, 1024), (37, 224), (513, 96), (1, 32)]
+
+
+def _upload_q4(ctx, pkg, packed, scales, k, n):
+    return ctx.upload(pkg.Weight(k=k, n=n, packed=packed, scales=scales))
+
+
+def _run_prepared(ctx, d, gid, x, nacc):
+    xd = d.put(x.astype(np.float32))
+    acc = d.put(np.zeros(nacc, np.int64))
+    ctx.gemv_run(gid, xd, acc)
+    return d.get(acc, nacc, np.int64)
+
+
+@pytest.mark.parametrize("k,n", SHAPES)
+def test_prepared_q4_equals_reference_layout(ctx, orc, pkg, k, n):
+    print(f"case prepared q4 k={k} n={n}", flush=True)
+    packed, scales = pkg.synth_q4(11, 5, k, n)
+    x = pkg.synth_f32(11, 6, k)
+    wid = _upload_q4(ctx, pkg, packed, scales, k, n)
+    gid = ctx.gemv_prepare(wid)
+    try:
+        with device(ctx) as d:
+            tiled = _run_prepared(ctx, d, gid, x, n)
+            w, s = ctx.weight_ptrs(wid)
+            xd = d.put(x)
+            acc = d.put(np.zeros(n, np.int64))
+            ctx.check(ctx.lib.qora_hip_gemv_q4_accumulate(ctx.h, w, s, xd, acc, k, n, None), "accumulate")
+            ref_layout = d.get(acc, n, np.int64)
+    finally:
+        ctx.gemv_release(gid)
+    assert np.array_equal(tiled, ref_layout)
+    ref = orc.gemv_q4(x, packed, scales, k, n, T=1)
+    assert rel_err(tiled / FIX, ref) <= REL_TOL
+
+
+@pytest.mark.parametrize("k,n", [(2048, 2048), (37, 224), (4097, 1056)])
+def test_prepared_q4_exact_regime(ctx, pkg, k, n):
+    r = np.random.default_rng(k + n)
+    packed, scales = exact_q4(r, k, n)
+    x = r.integers(-4, 5, size=k).astype(np.float32)
+    truth = dequant_np(packed, scales, k, n).T @ x.astype(np.float64)
+    gid = ctx.gemv_prepare(_upload_q4(ctx, pkg, packed, scales, k, n))
+    try:
+        with device(ctx) as d:
+            acc = _run_prepared(ctx, d, gid, x, n)
+    finally:
+        ctx.gemv_release(gid)
+    assert np.array_equal(acc / FIX, truth)
+
+
+def test_prepared_q4_zero_cases(ctx, pkg):
+    k, n = 256, 512
+    packed, scales = pkg.synth_q4(3, 1, k, n)
+    gid = ctx.gemv_prepare(_upload_q4(ctx, pkg, packed, scales, k, n))
+    gid8 = ctx.gemv_prepare(_upload_q4(ctx, pkg, np.full_like(packed, 0x88), scales, k, n))
+    try:
+        with device(ctx) as d:
+            assert not np.any(_run_prepared(ctx, d, gid, np.zeros(k, np.float32), n))
+            assert not np.any(_run_prepared(ctx, d, gid8, pkg.synth_f32(3, 2, k) * 100, n))
+    finally:
+        ctx.gemv_release(gid)
+        ctx.gemv_release(gid8)
+
+
+@pytest.mark.parametrize("k,n", PAIRED)
+def test_prepared_gate_up_equals_reference_layout(ctx, orc, pkg, k, n):
+    print(f"case prepared gate_up k={k} n={n}", flush=True)
+    gp, gs = pkg.synth_q4(12, 1, k, n)
+    up, us = pkg.synth_q4(12, 2, k, n)
+    x = pkg.synth_f32(12, 3, k)
+    wg = _upload_q4(ctx, pkg, gp, gs, k, n)
+    wu = _upload_q4(ctx, pkg, up, us, k, n)
+    gid = ctx.gemv_prepare(wg, wu, paired=True)
+    try:
+        with device(ctx) as d:
+            tiled = _run_prepared(ctx, d, gid, x, 2 * n)
+            a, b = ctx.weight_ptrs(wg)
+            c, e = ctx.weight_ptrs(wu)
+            xd = d.put(x)
+            acc = d.put(np.zeros(2 * n, np.int64))
+            ctx.check(ctx.lib.qora_hip_gate_up_q4_accumulate(ctx.h, a, b, c, e, xd, acc, k, n, None), "accumulate")
+            ref_layout = d.get(acc, 2 * n, np.int64)
+    finally:
+        ctx.gemv_release(gid)
+    assert np.array_equal(tiled, ref_layout)
+    assert rel_err(tiled[:n] / FIX, orc.gemv_q4(x, gp, gs, k, n, T=1)) <= REL_TOL
+    assert rel_err(tiled[n:] / FIX, orc.gemv_q4(x, up, us, k, n, T=1)) <= REL_TOL
+
+
+@pytest.mark.parametrize("k,n", [(2048, 2048), (300, 352), (2048, 512)])
+def test_prepared_f16_vs_oracle(ctx, orc, pkg, k, n):
+    w = pkg.synth_f16(13, 1, k * n, 0.02)
+    x = pkg.synth_f32(13, 2, k)
+    wid = ctx.upload(pkg.Weight(k=k, n=n, data=w))
+    gid = ctx.gemv_prepare(wid)
+    try:
+        with device(ctx) as d:
+            acc = _run_prepared(ctx, d, gid, x, n)
+            # the reference-layout entry (clear, accumulate, convert) must agree exactly
+            y = d.empty(n * 4)
+            wp, _ = ctx.weight_ptrs(wid)
+            ctx.check(ctx.lib.qora_hip_gemv_f16(ctx.h, wp, d.put(x), y, k, n, None), "gemv_f16")
+            y_ref_layout = d.get(y, n, np.float32)
+    finally:
+        ctx.gemv_release(gid)
+    assert np.array_equal((acc / FIX).astype(np.float32), y_ref_layout)
+    for avx in (False, True):
+        assert rel_err(acc / FIX, orc.gemv_f16(x, w, k, n, avx512=avx)) <= REL_TOL
+
+
+def test_prepared_graph_replay(ctx, pkg):
+    k, n = 2048, 2048
+    packed, scales = pkg.synth_q4(14, 1, k, n)
+    x = pkg.synth_f32(14, 2, k)
+    gid = ctx.gemv_prepare(_upload_q4(ctx, pkg, packed, scales, k, n))
+    try:
+        with device(ctx) as d:
+            once = _run_prepared(ctx, d, gid, x, n)
+            xd = d.put(x)
+            acc = d.put(np.zeros(n, np.int64))
+            ctx.capture_begin()
+            ctx.gemv_run(gid, xd, acc, ctx.stream)
+            g = ctx.capture_end()
+            try:
+                for rep in range(1, 4):
+                    ctx.graph_launch(g)
+                    ctx.synchronize()
+                    assert np.array_equal(d.get(acc, n, np.int64), once * rep)
+            finally:
+                ctx.graph_destroy(g)
+    finally:
+        ctx.gemv_release(gid)
+
+
+def test_prepared_errors(ctx, pkg):
+    packed, scales = pkg.synth_q4(15, 1, 64, 64)
+    a = _upload_q4(ctx, pkg, packed, scales, 64, 64)
+    packed2, scales2 = pkg.synth_q4(15, 2, 64, 96)
+    b = _upload_q4(ctx, pkg, packed2, scales2, 64, 96)
+    with pytest.raises(pkg.QoraHipError):
+        ctx.gemv_prepare(a, b, paired=True)          # gate/up shapes differ
+    with pytest.raises(pkg.QoraHipError):
+        ctx.gemv_prepare(10 ** 6)                    # unknown weight
+    gid = ctx.gemv_prepare(a)
+    ctx.gemv_release(gid)
+    with pytest.raises(pkg.QoraHipError):
+        ctx.gemv_release(gid)                        # released twice
+    with device(ctx) as d:
+        with pytest.raises(pkg.QoraHipError):
+            ctx.gemv_run(gid, d.put(np.zeros(64, np.float32)), d.put(np.zeros(64, np.int64)))
