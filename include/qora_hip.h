@@ -85,6 +85,9 @@ typedef struct {
     uint32_t kv_dtype;                      /* 0 = f32 (reference RawKvCache), 1 = f16 */
 } qora_model_desc;
 
+/* The KV cache starts zero-filled; QORA_HIP_KV_FILL=nan fills it with NaN
+ * bit patterns instead (a test that slots past the current length never
+ * reach the attention output). */
 int qora_hip_model_init(qora_hip_ctx* ctx, const qora_model_desc* desc);
 
 /* save::load_model (save.rs:154-210): read a .qora v1 file, upload it and

@@ -27,45 +27,96 @@ namespace qora {
 // Limits (checked on the host): head_dim <= 128, groups <= 4.
 // ---------------------------------------------------------------------------
 
-// Rotated value of dim d of a head whose un-rotated values are v[0..hd).
-__device__ __forceinline__ float rope_at(const float* v, uint32_t d, uint32_t half, const float* ct,
-                                         const float* st) {
-    if (d < half) return v[d] * ct[d] - v[d + half] * st[d];
-    if (d < 2 * half) return v[d] * ct[d - half] + v[d - half] * st[d - half];
-    return v[d];
+// RoPE partner of dim d (rotate_half over the first 2*half dims,
+// apply_rope_raw gemv.rs:869-887): rotated = v[d] * c + sgn * v[partner] * s,
+// with c, s the table entries of dim d mod half. Dims past 2*half pass
+// through (partner = d, s = 0).
+__device__ __forceinline__ uint32_t rope_partner(uint32_t d, uint32_t half) {
+    return d < half ? d + half : (d < 2 * half ? d - half : d);
 }
 
-template <int DPL>
-__device__ __forceinline__ void load_v_row(const AttnParams& p, uint64_t idx, float* v) {
-    if (p.kv_f16) {
-        const uint16_t* src = reinterpret_cast<const uint16_t*>(p.vc) + idx;
+// K and V float4s of one 32-position tile held by one thread (thread t takes
+// float4 e = t + 256*j of the [32][head_dim/4] tile).
+template <int TL>
+struct KvTileRegs {
+    float4 k[TL], v[TL];
+};
+
+template <int TL, bool F16KV>
+__device__ __forceinline__ KvTileRegs<TL> attn_load_tile(const AttnParams& p, uint32_t c0, uint32_t L,
+                                                          uint64_t kv_stride, uint64_t head_off, uint32_t q4_row,
+                                                          uint32_t tile_n) {
+    KvTileRegs<TL> r;
 #pragma unroll
-        for (int i = 0; i < DPL; ++i) v[i] = h2f(src[i]);
-    } else {
-        const float* src = reinterpret_cast<const float*>(p.vc) + idx;
-        if constexpr (DPL == 2) {
-            const float2 f = *reinterpret_cast<const float2*>(src);
-            v[0] = f.x;
-            v[1] = f.y;
+    for (int j = 0; j < TL; ++j) {
+        const uint32_t e = min(threadIdx.x + (uint32_t)(256 * j), tile_n - 1u);
+        const uint32_t row = e / q4_row, c4 = e % q4_row;
+        const uint32_t pos = min(c0 + row, L - 1u);
+        const uint64_t idx = (uint64_t)pos * kv_stride + head_off + 4u * c4;
+        if constexpr (F16KV) {
+            const uint2 a = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(p.kc) + idx);
+            const uint2 b = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(p.vc) + idx);
+            r.k[j] = make_float4(h2f((uint16_t)(a.x & 0xFFFFu)), h2f((uint16_t)(a.x >> 16)),
+                                 h2f((uint16_t)(a.y & 0xFFFFu)), h2f((uint16_t)(a.y >> 16)));
+            r.v[j] = make_float4(h2f((uint16_t)(b.x & 0xFFFFu)), h2f((uint16_t)(b.x >> 16)),
+                                 h2f((uint16_t)(b.y & 0xFFFFu)), h2f((uint16_t)(b.y >> 16)));
         } else {
-            v[0] = src[0];
+            r.k[j] = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(p.kc) + idx);
+            r.v[j] = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(p.vc) + idx);
+        }
+    }
+    return r;
+}
+
+// Rows at or past cn become zeros (a bit mask, not a select: exact zeros
+// whatever stale bits the unwritten slots hold); row `skip` (the appended
+// position, or >= 32 for none) is left to its writer.
+template <int TL, int KSTR, int VSTR>
+__device__ __forceinline__ void attn_store_tile(const KvTileRegs<TL>& r, float* ktile, float* vtile, uint32_t cn,
+                                                uint32_t skip, uint32_t q4_row, uint32_t tile_n) {
+#pragma unroll
+    for (int j = 0; j < TL; ++j) {
+        const uint32_t e = threadIdx.x + (uint32_t)(256 * j);
+        const uint32_t row = e / q4_row, c4 = e % q4_row;
+        if (e < tile_n && row != skip) {
+            const uint32_t msk = row < cn ? 0xFFFFFFFFu : 0u;
+            const uint4 kb = make_uint4(__float_as_uint(r.k[j].x) & msk, __float_as_uint(r.k[j].y) & msk,
+                                        __float_as_uint(r.k[j].z) & msk, __float_as_uint(r.k[j].w) & msk);
+            const uint4 vb = make_uint4(__float_as_uint(r.v[j].x) & msk, __float_as_uint(r.v[j].y) & msk,
+                                        __float_as_uint(r.v[j].z) & msk, __float_as_uint(r.v[j].w) & msk);
+            *reinterpret_cast<uint4*>(ktile + row * KSTR + 4 * c4) = kb;
+            *reinterpret_cast<uint4*>(vtile + row * VSTR + 4 * c4) = vb;
         }
     }
 }
 
-// One wave per query head; lanes (half, r) = (lane / 32, lane % 32) own
-// position c0 + r and half of the head dims for q.k, then lanes own DPL
-// dims each for p.V. K and V are read straight from the cache (all loads of
-// a 32-position pass are issued before the math). No block-wide barrier
-// inside the position loop: each wave runs its own online softmax.
-template <int DPL>
+// Block (split, kvh) walks its positions in passes of 32. Each pass's K and
+// V rows are loaded once per block with coalesced 16-byte loads (256 lanes,
+// 4 KB per instruction) and staged in LDS as fp32; rows past the pass are
+// stored as zeros. The next pass is prefetched into registers while the
+// current one is computed. One wave per query head then takes its scores
+// from the K tile (lanes (half, r) = (lane / 32, lane % 32): position r,
+// half of the dims), runs the online softmax and accumulates p.V from the V
+// tile (DPL dims per lane). In model mode the appended position's K/V row
+// is computed here (RMSNorm factor, RoPE), written to the cache and put
+// into the tile directly.
+// Latency: the loads that do not depend on the position (q|k|v sums,
+// RMSNorm partials) are issued together with the position load; the cache
+// tile and RoPE tables follow as soon as the position arrives. q and the K
+// rows are zero-padded to HDM dims in LDS so the dot products run without
+// predicates. DPL = 2 covers head_dim <= 128, DPL = 1 head_dim <= 64.
+template <int DPL, bool F16KV>
 __global__ __launch_bounds__(256) void attn_decode_kernel(AttnParams p) {
     constexpr int NT = 256;
     constexpr int SUB = kAttnSub;                    // positions per pass (32)
-    __shared__ float qs[kAttnMaxGroups * kAttnMaxHd];
-    __shared__ float raw[(kAttnMaxGroups + 2) * kAttnMaxHd];
-    __shared__ float knew[kAttnMaxHd];
-    __shared__ float vnew[kAttnMaxHd];
+    constexpr int HDM = 64 * DPL;                    // head_dim bound of this instance
+    constexpr int KQ = HDM / 8;                      // float4 chunks per lane for q.k (half of HDM)
+    constexpr int KSTR = HDM + 4;                    // padded K row stride (floats): no bank conflicts
+    constexpr int VSTR = HDM;
+    constexpr int TL = SUB * HDM / 4 / NT;           // float4 per thread per tile
+    __shared__ __align__(16) float ktile[SUB * KSTR];
+    __shared__ __align__(16) float vtile[SUB * VSTR];
+    __shared__ __align__(16) float qs[kAttnMaxGroups * HDM];
     __shared__ float es[kAttnMaxGroups * SUB];
 
     const int t = threadIdx.x;
@@ -73,64 +124,117 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnParams p) {
     const int wave = t / kWave;
     const uint32_t split = blockIdx.x;
     const uint32_t kvh = blockIdx.y;
-    const uint32_t L = p.pos ? (uint32_t)(*p.pos) + 1u : p.L;
+    const uint32_t hd = p.hd, G = p.groups;
+    const bool model = p.qkv_acc != nullptr;
+    const uint64_t kv_stride = (uint64_t)p.KVH * hd;
+    const uint64_t head_off = (uint64_t)kvh * hd;
+    const uint32_t nq = G * hd;
+
+    // ---- position-independent loads, in flight with the position ----
+    const int32_t pos_raw = p.pos ? *p.pos : (int32_t)p.L - 1;
+    long long qa[2] = {0, 0}, qb[2] = {0, 0};
+    long long ka = 0, kb = 0, va = 0;
+    float ssp = 0.f;
+    const uint32_t dn = min((uint32_t)t, hd - 1u);
+    if (model) {
+        const uint32_t qd = p.H * hd;
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const uint32_t i = min((uint32_t)t + (uint32_t)u * NT, nq - 1u);
+            const uint32_t d = i % hd;
+            qa[u] = p.qkv_acc[(uint64_t)kvh * G * hd + i];
+            qb[u] = p.qkv_acc[(uint64_t)kvh * G * hd + (i - d) + rope_partner(d, p.half)];
+        }
+        ka = p.qkv_acc[qd + head_off + dn];
+        kb = p.qkv_acc[qd + head_off + rope_partner(dn, p.half)];
+        va = p.qkv_acc[qd + kv_stride + head_off + dn];
+        ssp = p.ss_in[min((uint32_t)lane, p.ss_n - 1u)];
+    }
+
+    const uint32_t L = (uint32_t)pos_raw + 1u;
     const uint32_t p0 = split * p.chunk;
     if (p0 >= L) return;
     const uint32_t p1 = min(L, p0 + p.chunk);
-    const uint32_t hd = p.hd, G = p.groups;
-    const uint64_t kv_stride = (uint64_t)p.KVH * hd;
     const uint32_t cur = L - 1;                        // position appended this step
-    const bool model = p.qkv_acc != nullptr;
     const bool has_new = model && cur >= p0 && cur < p1;
+    const uint32_t q4_row = hd / 4;                    // float4 per row
+    const uint32_t tile_n = SUB * q4_row;              // float4 per tile
 
-    // ---- q of the group's heads (and the new k, v) ----
-    if (model) {
-        // the q|k|v GEMV ran on x * gamma; its RMSNorm factor is applied here
-        const float inv = rms_inv_from_parts(p.ss_in, p.ss_n, p.norm_n);
-        const uint32_t qd = p.H * hd;
-        for (uint32_t i = t; i < G * hd; i += NT)
-            raw[i] = inv * from_fixed(p.qkv_acc[(uint64_t)kvh * G * hd + i]);
-        if (has_new)
-            for (uint32_t d = t; d < hd; d += NT) {
-                raw[G * hd + d] = inv * from_fixed(p.qkv_acc[qd + (uint64_t)kvh * hd + d]);
-                raw[(G + 1) * hd + d] = inv * from_fixed(p.qkv_acc[qd + kv_stride + (uint64_t)kvh * hd + d]);
-            }
-        __syncthreads();
+    // ---- position-dependent loads: RoPE entries of `cur`, first cache tile ----
+    float qc[2] = {1.f, 1.f}, qsn[2] = {0.f, 0.f}, kc_ = 1.f, ks_ = 0.f;
+    if (model && p.use_rope) {
         const float* ct = p.rope_cos + (uint64_t)cur * p.half;
         const float* st = p.rope_sin + (uint64_t)cur * p.half;
-        for (uint32_t i = t; i < G * hd; i += NT)
-            qs[i] = p.use_rope ? rope_at(raw + (i / hd) * hd, i % hd, p.half, ct, st) : raw[i];
-        if (has_new)
-            for (uint32_t d = t; d < hd; d += NT) {
-                float kv = p.use_rope ? rope_at(raw + G * hd, d, p.half, ct, st) : raw[G * hd + d];
-                float vv = raw[(G + 1) * hd + d];
-                const uint64_t idx = (uint64_t)cur * kv_stride + (uint64_t)kvh * hd + d;
-                if (p.kv_f16) {
-                    const uint16_t kh = f2h(kv), vh = f2h(vv);
-                    reinterpret_cast<uint16_t*>(p.kc)[idx] = kh;
-                    reinterpret_cast<uint16_t*>(p.vc)[idx] = vh;
-                    kv = h2f(kh);   // use the stored value, as later steps will
-                    vv = h2f(vh);
-                } else {
-                    reinterpret_cast<float*>(p.kc)[idx] = kv;
-                    reinterpret_cast<float*>(p.vc)[idx] = vv;
-                }
-                knew[d] = kv;
-                vnew[d] = vv;
-            }
-    } else {
-        for (uint32_t i = t; i < G * hd; i += NT) qs[i] = p.q[(uint64_t)kvh * G * hd + i];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const uint32_t d = min((uint32_t)t + (uint32_t)u * NT, nq - 1u) % hd;
+            const uint32_t td = d < p.half ? d : (d < 2 * p.half ? d - p.half : 0u);
+            qc[u] = ct[td];
+            qsn[u] = st[td];
+        }
+        const uint32_t td = dn < p.half ? dn : (dn < 2 * p.half ? dn - p.half : 0u);
+        kc_ = ct[td];
+        ks_ = st[td];
     }
-    __syncthreads();
+    KvTileRegs<TL> tr = attn_load_tile<TL, F16KV>(p, p0, L, kv_stride, head_off, q4_row, tile_n);
+
+    // K padding columns [hd, HDM) stay zero for the whole kernel
+    if (hd < (uint32_t)HDM)
+        for (uint32_t e = t; e < SUB * ((uint32_t)HDM - hd); e += NT)
+            ktile[(e / ((uint32_t)HDM - hd)) * KSTR + hd + e % ((uint32_t)HDM - hd)] = 0.f;
+
+    // ---- q of the group's heads (and the appended k, v) ----
+    float k_app = 0.f, v_app = 0.f;                   // thread t < hd: dim t of the appended row
+    if (model) {
+        // the q|k|v GEMV ran on x * gamma; its RMSNorm factor is applied here
+        const float inv = 1.0f / sqrtf(wave_sum(lane < (int)p.ss_n ? ssp : 0.f) / (float)p.norm_n + 1e-6f);
+        const bool rot = p.use_rope != 0;
+        // padding dims [hd, HDM) of each q row are zero
+        for (uint32_t i = t; i < G * HDM; i += NT)
+            if (i % HDM >= hd) qs[i] = 0.f;
+        // q values: thread t owns flat index i = t + 256u of [G][hd]
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const uint32_t i = (uint32_t)t + (uint32_t)u * NT;
+            if (i < nq) {
+                const uint32_t d = i % hd;
+                const float a = inv * from_fixed(qa[u]), b = inv * from_fixed(qb[u]);
+                // rotate_half: the first half takes -partner * sin, the second +partner * sin
+                qs[(i / hd) * HDM + d] = (rot && d < 2 * p.half) ? (d < p.half ? a * qc[u] - b * qsn[u]
+                                                                                 : a * qc[u] + b * qsn[u])
+                                                                  : a;
+            }
+        }
+        if (has_new && (uint32_t)t < hd) {
+            const float a = inv * from_fixed(ka), b = inv * from_fixed(kb);
+            float kv = (rot && dn < 2 * p.half) ? (dn < p.half ? a * kc_ - b * ks_ : a * kc_ + b * ks_) : a;
+            float vv = inv * from_fixed(va);
+            const uint64_t idx = (uint64_t)cur * kv_stride + head_off + dn;
+            if constexpr (F16KV) {
+                const uint16_t kh = f2h(kv), vh = f2h(vv);
+                reinterpret_cast<uint16_t*>(p.kc)[idx] = kh;
+                reinterpret_cast<uint16_t*>(p.vc)[idx] = vh;
+                kv = h2f(kh);   // use the stored value, as later steps will
+                vv = h2f(vh);
+            } else {
+                reinterpret_cast<float*>(p.kc)[idx] = kv;
+                reinterpret_cast<float*>(p.vc)[idx] = vv;
+            }
+            k_app = kv;
+            v_app = vv;
+        }
+    } else {
+        for (uint32_t i = t; i < G * HDM; i += NT) {
+            const uint32_t g = i / HDM, d = i % HDM;
+            qs[i] = d < hd ? p.q[(uint64_t)(kvh * G + g) * hd + d] : 0.f;
+        }
+    }
 
     const uint32_t g = (uint32_t)wave;
-    if (g >= G) return;
-    const float* qg = qs + g * hd;
-    const uint32_t hh = hd / 2;                      // dims per half for q.k
     const uint32_t half_id = (uint32_t)lane / 32, r_lane = (uint32_t)lane % 32;
-    const uint32_t dq0 = half_id * hh;
-    const uint32_t dv0 = (uint32_t)lane * DPL;       // dims of this lane for p.V
-    const bool vlane = dv0 < hd;
+    const uint32_t dq0 = half_id * (HDM / 2);
+    const uint32_t dv0c = min((uint32_t)lane * DPL, hd - DPL);   // clamped V dims of this lane
+    const bool vlane = (uint32_t)lane * DPL < hd;
     float m = -INFINITY, l = 0.f;
     float acc[DPL];
 #pragma unroll
@@ -138,88 +242,69 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnParams p) {
 
     for (uint32_t c0 = p0; c0 < p1; c0 += SUB) {
         const uint32_t cn = min((uint32_t)SUB, p1 - c0);
-        // V rows of this pass (independent of the scores: issue first)
-        float vr[SUB][DPL];
-#pragma unroll
-        for (int r = 0; r < SUB; ++r) {
-            const uint32_t ps = c0 + (uint32_t)r;
-            if ((uint32_t)r < cn && vlane) {
-                if (has_new && ps == cur) {
-#pragma unroll
-                    for (int i = 0; i < DPL; ++i) vr[r][i] = vnew[dv0 + i];
-                } else {
-                    load_v_row<DPL>(p, (uint64_t)ps * kv_stride + (uint64_t)kvh * hd + dv0, vr[r]);
-                }
-            } else {
-#pragma unroll
-                for (int i = 0; i < DPL; ++i) vr[r][i] = 0.f;
-            }
+        const bool new_here = has_new && cur >= c0 && cur < c0 + cn;
+        attn_store_tile<TL, KSTR, VSTR>(tr, ktile, vtile, cn, new_here ? cur - c0 : 0xFFFFFFFFu, q4_row, tile_n);
+        if (new_here && (uint32_t)t < hd) {
+            ktile[(cur - c0) * KSTR + t] = k_app;
+            vtile[(cur - c0) * VSTR + t] = v_app;
         }
-        // q.k for position c0 + r_lane over dims [dq0, dq0 + hh)
-        float s = 0.f;
-        const uint32_t ps = c0 + r_lane;
-        if (r_lane < cn) {
+        __syncthreads();
+        if (c0 + SUB < p1)                            // next pass, in flight during this one
+            tr = attn_load_tile<TL, F16KV>(p, c0 + SUB, L, kv_stride, head_off, q4_row, tile_n);
+        if (g < G) {
+            // q.k for position c0 + r_lane over padded dims [dq0, dq0 + HDM/2)
+            const float* qg = qs + g * HDM + dq0;
+            const float* krow = ktile + r_lane * KSTR + dq0;
+            float4 q4[KQ], k4[KQ];
+#pragma unroll
+            for (int i = 0; i < KQ; ++i) {
+                q4[i] = *reinterpret_cast<const float4*>(qg + 4 * i);
+                k4[i] = *reinterpret_cast<const float4*>(krow + 4 * i);
+            }
             float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
-            if (has_new && ps == cur) {
-                for (uint32_t d = 0; d < hh; d += 4) {
-                    a0 = fmaf(qg[dq0 + d], knew[dq0 + d], a0);
-                    a1 = fmaf(qg[dq0 + d + 1], knew[dq0 + d + 1], a1);
-                    a2 = fmaf(qg[dq0 + d + 2], knew[dq0 + d + 2], a2);
-                    a3 = fmaf(qg[dq0 + d + 3], knew[dq0 + d + 3], a3);
-                }
-            } else {
-                const uint64_t base = (uint64_t)ps * kv_stride + (uint64_t)kvh * hd + dq0;
-                if (p.kv_f16) {
-                    const uint16_t* kr = reinterpret_cast<const uint16_t*>(p.kc) + base;
-                    for (uint32_t d = 0; d < hh; d += 4) {
-                        const uint2 w = *reinterpret_cast<const uint2*>(kr + d);
-                        a0 = fmaf(qg[dq0 + d], h2f((uint16_t)(w.x & 0xFFFFu)), a0);
-                        a1 = fmaf(qg[dq0 + d + 1], h2f((uint16_t)(w.x >> 16)), a1);
-                        a2 = fmaf(qg[dq0 + d + 2], h2f((uint16_t)(w.y & 0xFFFFu)), a2);
-                        a3 = fmaf(qg[dq0 + d + 3], h2f((uint16_t)(w.y >> 16)), a3);
-                    }
+#pragma unroll
+            for (int i = 0; i < KQ; ++i) {
+                a0 = fmaf(q4[i].x, k4[i].x, a0);
+                a1 = fmaf(q4[i].y, k4[i].y, a1);
+                a2 = fmaf(q4[i].z, k4[i].z, a2);
+                a3 = fmaf(q4[i].w, k4[i].w, a3);
+            }
+            float s = (a0 + a1) + (a2 + a3);
+            s += __shfl_xor(s, 32, kWave);
+            s = (r_lane < cn) ? s * p.scale : -INFINITY;
+            // online softmax over the pass (lanes r and r + 32 hold the same score)
+            const float m_new = fmaxf(m, wave_max(s));
+            const float f = expf(m - m_new);          // 0 on the first pass
+            const float e = (r_lane < cn) ? expf(s - m_new) : 0.f;
+            l = l * f + wave_sum(half_id == 0 ? e : 0.f);
+            m = m_new;
+            if (half_id == 0) es[g * SUB + r_lane] = e;
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+            for (int i = 0; i < DPL; ++i) acc[i] *= f;
+            // rows past the pass are zeros in the tile and have zero weight
+#pragma unroll
+            for (int r = 0; r < SUB; ++r) {
+                const float er = es[g * SUB + r];
+                const float* vrow = vtile + r * VSTR + dv0c;
+                if constexpr (DPL == 2) {
+                    const float2 v2 = *reinterpret_cast<const float2*>(vrow);
+                    acc[0] = fmaf(er, v2.x, acc[0]);
+                    acc[1] = fmaf(er, v2.y, acc[1]);
                 } else {
-                    const float* kr = reinterpret_cast<const float*>(p.kc) + base;
-                    for (uint32_t d = 0; d < hh; d += 4) {
-                        const float4 w = *reinterpret_cast<const float4*>(kr + d);
-                        a0 = fmaf(qg[dq0 + d], w.x, a0);
-                        a1 = fmaf(qg[dq0 + d + 1], w.y, a1);
-                        a2 = fmaf(qg[dq0 + d + 2], w.z, a2);
-                        a3 = fmaf(qg[dq0 + d + 3], w.w, a3);
-                    }
+                    acc[0] = fmaf(er, vrow[0], acc[0]);
                 }
             }
-            s = (a0 + a1) + (a2 + a3);
         }
-        s += __shfl_xor(s, 32, kWave);
-        s = (r_lane < cn) ? s * p.scale : -INFINITY;
-        // online softmax over the pass (lanes r and r + 32 hold the same score)
-        const float m_new = fmaxf(m, wave_max(s));
-        const float f = expf(m - m_new);          // 0 on the first pass
-        const float e = (r_lane < cn) ? expf(s - m_new) : 0.f;
-        l = l * f + wave_sum(half_id == 0 ? e : 0.f);
-        m = m_new;
-        if (half_id == 0) es[g * SUB + r_lane] = e;
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
-        for (int i = 0; i < DPL; ++i) acc[i] *= f;
-#pragma unroll
-        for (int r = 0; r < SUB; ++r) {
-            const float er = es[g * SUB + r];     // zero beyond cn
-#pragma unroll
-            for (int i = 0; i < DPL; ++i) acc[i] = fmaf(er, vr[r][i], acc[i]);
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        __syncthreads();                              // the tile is rewritten next pass
     }
+    if (g >= G) return;
     float* part = p.part + (((uint64_t)kvh * p.s_max + split) * G + g) * (hd + 2);
     if (vlane) {
 #pragma unroll
-        for (int i = 0; i < DPL; ++i)
-            if (dv0 + i < hd) part[dv0 + i] = acc[i];
+        for (int i = 0; i < DPL; ++i) part[dv0c + i] = acc[i];
     }
     if (lane == 0) {
         part[hd] = m;

@@ -88,17 +88,34 @@ __device__ __forceinline__ float from_fixed(long long a) {
     return (float)((double)a * (1.0 / kFixScale));
 }
 
-// Sum over the 64 lanes of a wave; every lane receives the total.
+// Cross-lane reductions over a wave64 with DPP (no LDS round trips): two
+// quad permutes and two row rotates give every lane the total of its
+// 16-lane row, then the four row totals are read with v_readlane and
+// combined in a fixed order, so every lane receives the same value. Must be
+// called with all 64 lanes active (wave-uniform control flow).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+__device__ __forceinline__ float lane_f32(float v, int lane) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
-    return v;
+    v += dpp_f32<0xB1>(v);    // quad_perm [1,0,3,2]
+    v += dpp_f32<0x4E>(v);    // quad_perm [2,3,0,1]
+    v += dpp_f32<0x124>(v);   // row_ror:4
+    v += dpp_f32<0x128>(v);   // row_ror:8
+    return (lane_f32(v, 0) + lane_f32(v, 16)) + (lane_f32(v, 32) + lane_f32(v, 48));
 }
 
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
-    return v;
+    v = fmaxf(v, dpp_f32<0xB1>(v));
+    v = fmaxf(v, dpp_f32<0x4E>(v));
+    v = fmaxf(v, dpp_f32<0x124>(v));
+    v = fmaxf(v, dpp_f32<0x128>(v));
+    return fmaxf(fmaxf(lane_f32(v, 0), lane_f32(v, 16)), fmaxf(lane_f32(v, 32), lane_f32(v, 48)));
 }
 
 // RMSNorm factor 1 / sqrt(sum(x^2) / n + 1e-6) (rms_norm_f16, gemv.rs:744-753)

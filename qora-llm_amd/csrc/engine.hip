@@ -488,6 +488,15 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
     MALLOC(d_argv, (size_t)m.lm_blocks * 4);
     MALLOC(d_argi, (size_t)m.lm_blocks * 4);
 #undef MALLOC
+    {
+        // Cache slots past the current length are read (and skipped) by the
+        // attention kernel; they start as zeros, or as NaN bit patterns with
+        // QORA_HIP_KV_FILL=nan (a test of that skipping).
+        const char* fill = std::getenv("QORA_HIP_KV_FILL");
+        const int byte = (fill && std::strcmp(fill, "nan") == 0) ? 0xFF : 0;
+        HIP_TRY(c, hipMemset(m.d_k, byte, (size_t)m.L * m.cap * kvd * kvb));
+        HIP_TRY(c, hipMemset(m.d_v, byte, (size_t)m.L * m.cap * kvd * kvb));
+    }
     HIP_TRY(c, hipMemset(m.d_xacc, 0, (size_t)m.hidden * 8));
     HIP_TRY(c, hipMemset(m.d_qkv_acc, 0, qkv_n * 8));
     HIP_TRY(c, hipMemset(m.d_gu_acc, 0, (size_t)2 * m.inter * 8));

@@ -174,8 +174,14 @@ void attn_geometry(uint32_t positions, uint32_t* chunk, uint32_t* s_max) {
 }
 
 hipError_t launch_attn(const AttnParams& p, hipStream_t stream) {
-    if (p.hd <= 64) hipLaunchKernelGGL((attn_decode_kernel<1>), dim3(p.s_max, p.KVH), dim3(256), 0, stream, p);
-    else hipLaunchKernelGGL((attn_decode_kernel<2>), dim3(p.s_max, p.KVH), dim3(256), 0, stream, p);
+    const dim3 grid(p.s_max, p.KVH), block(256);
+    if (p.hd <= 64) {
+        if (p.kv_f16) hipLaunchKernelGGL((attn_decode_kernel<1, true>), grid, block, 0, stream, p);
+        else hipLaunchKernelGGL((attn_decode_kernel<1, false>), grid, block, 0, stream, p);
+    } else {
+        if (p.kv_f16) hipLaunchKernelGGL((attn_decode_kernel<2, true>), grid, block, 0, stream, p);
+        else hipLaunchKernelGGL((attn_decode_kernel<2, false>), grid, block, 0, stream, p);
+    }
     return hipGetLastError();
 }
 

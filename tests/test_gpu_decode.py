@@ -45,6 +45,28 @@ def test_prefill_decode_logits_and_kv_match_oracle(ctx, pkg, orc, fmt):
     assert be.kv_len() == len(prompt) + len(feed)
 
 
+@pytest.mark.parametrize("kv_dtype", [0, 1])
+def test_stale_nan_cache_slots_never_reach_the_output(ctx, pkg, orc, monkeypatch, kv_dtype):
+    """The attention kernel reads cache slots at and past the appended
+    position before they are written; they must be skipped, not multiplied
+    by a zero weight (0 * NaN = NaN). The cache starts as NaN bit patterns."""
+    monkeypatch.setenv("QORA_HIP_KV_FILL", "nan")
+    w = small_model(pkg, 1)
+    prompt = pkg.synth_tokens(0, 2000, 13, w.config.vocab)
+    be = pkg.HipBackend(ctx, w, kv_capacity=128, kv_dtype=kv_dtype)
+    om = orc.OracleModel(w, kv_capacity=128, T=4)
+    logits, _ = be.raw_prefill(prompt)
+    ref = om.prefill(prompt)
+    tol = REL_TOL if kv_dtype == 0 else 5e-3
+    assert np.isfinite(logits).all()
+    assert rel_err(logits, ref) <= tol
+    for t in pkg.synth_tokens(0, 2001, 6, w.config.vocab):
+        logits, _ = be.forward_decode_raw(int(t))
+        ref = om.forward_decode(int(t))
+        assert np.isfinite(logits).all()
+        assert rel_err(logits, ref) <= tol
+
+
 def test_greedy_tokens_match_oracle_small(ctx, pkg, orc):
     w = small_model(pkg, 1, layers=8, seed=3)
     prompt = pkg.synth_tokens(3, 2000, 16, w.config.vocab)
