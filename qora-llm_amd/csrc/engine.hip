@@ -73,6 +73,7 @@ struct PreparedGemv {
     GemvParams p{};
     void* tw = nullptr;
     void* ts = nullptr;
+    void* te = nullptr;
 };
 
 struct qora_hip_ctx {
@@ -174,19 +175,31 @@ const DevWeight* get_weight(qora_hip_ctx* c, uint32_t wid) {
     return &c->weights[wid];
 }
 
+// Launch plan of a decode-step GEMV: Q4 runs on the matrix cores
+// (gemv_q4m_kernel), F16 on the VALU kernel.
+bool plan_model_gemv(int fmt, uint32_t k, const uint32_t* seg_groups, int nseg, bool paired, int cus, GemvPlan* pl,
+                     uint32_t row_align = 1) {
+    return fmt == FMT_Q4 ? plan_gemv_q4m(k, seg_groups, nseg, paired, cus, pl, row_align)
+                         : plan_gemv(fmt, k, seg_groups, nseg, paired, cus, pl, row_align);
+}
+
 // Allocates the tile layout of a planned GEMV (model-owned) and packs the
 // reference-layout segments of *p into it.
 int pack_model_gemv(qora_hip_ctx* c, int fmt, const GemvPlan& pl, GemvParams* p) {
-    uint64_t wb = 0, sb = 0;
-    gemv_tile_bytes(fmt, pl, &wb, &sb);
+    uint64_t wb = 0, sb = 0, eb = 0;
+    gemv_tile_bytes(fmt, pl, &wb, &sb, &eb);
     void* tw = nullptr;
     void* ts = nullptr;
+    void* te = nullptr;
     if (int rc = model_alloc(c, wb, &tw)) return rc;
     if (sb)
         if (int rc = model_alloc(c, sb, &ts)) return rc;
-    HIP_TRY(c, launch_gemv_tile(fmt, pl, *p, (uint8_t*)tw, (uint16_t*)ts, c->stream));
+    if (eb)
+        if (int rc = model_alloc(c, eb, &te)) return rc;
+    HIP_TRY(c, launch_gemv_tile(fmt, pl, *p, (uint8_t*)tw, (uint16_t*)ts, (int8_t*)te, c->stream));
     p->tw = (const uint8_t*)tw;
     p->ts = (const uint16_t*)ts;
+    p->tes = (const int8_t*)te;
     return QORA_HIP_OK;
 }
 
@@ -302,10 +315,9 @@ extern "C" int qora_hip_destroy(qora_hip_ctx* c) {
     (void)hipSetDevice(c->device);
     (void)hipStreamSynchronize(c->stream);
     free_model(c);
-    for (PreparedGemv& g : c->gemvs) {
-        if (g.tw) (void)hipFree(g.tw);
-        if (g.ts) (void)hipFree(g.ts);
-    }
+    for (PreparedGemv& g : c->gemvs)
+        for (void* q : {g.tw, g.ts, g.te})
+            if (q) (void)hipFree(q);
     for (DevWeight& w : c->weights) {
         if (w.w) (void)hipFree(w.w);
         if (w.scales) (void)hipFree(w.scales);
@@ -444,10 +456,10 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
     const uint32_t gq = qd / 32, gkv = kvd / 32, gh = m.hidden / 32, gi = m.inter / 32;
     const uint32_t qkv_groups[3] = {gq, gkv, gkv};
     const uint32_t gu_groups[2] = {gi, gi};
-    if (!plan_gemv(m.fmt, m.hidden, qkv_groups, 3, false, c->cus, &m.pl_qkv) ||
-        !plan_gemv(m.fmt, qd, &gh, 1, false, c->cus, &m.pl_o, m.hd) ||
-        !plan_gemv(m.fmt, m.hidden, gu_groups, 2, true, c->cus, &m.pl_gu) ||
-        !plan_gemv(m.fmt, m.inter, &gh, 1, false, c->cus, &m.pl_down)) {
+    if (!plan_model_gemv(m.fmt, m.hidden, qkv_groups, 3, false, c->cus, &m.pl_qkv) ||
+        !plan_model_gemv(m.fmt, qd, &gh, 1, false, c->cus, &m.pl_o, m.hd) ||
+        !plan_model_gemv(m.fmt, m.hidden, gu_groups, 2, true, c->cus, &m.pl_gu) ||
+        !plan_model_gemv(m.fmt, m.inter, &gh, 1, false, c->cus, &m.pl_down)) {
         free_model(c);
         return fail(c, QORA_HIP_E_INVALID, "unsupported GEMV shape");
     }
@@ -954,7 +966,7 @@ extern "C" int qora_hip_gemv_prepare(qora_hip_ctx* c, uint32_t wid, uint32_t wid
     g.n = w0->n;
     const uint32_t G = (uint32_t)(w0->n / 32);
     const uint32_t groups[2] = {G, G};
-    if (!plan_gemv(g.fmt, (uint32_t)g.k, groups, g.paired ? 2 : 1, g.paired, c->cus, &g.plan))
+    if (!plan_model_gemv(g.fmt, (uint32_t)g.k, groups, g.paired ? 2 : 1, g.paired, c->cus, &g.plan))
         return fail(c, QORA_HIP_E_INVALID, "unsupported GEMV shape");
     g.p.seg[0] = GemvSeg{(const uint8_t*)w0->w, (const uint16_t*)w0->scales, G, 0, 0, 0};
     g.p.nseg = 1;
@@ -966,20 +978,27 @@ extern "C" int qora_hip_gemv_prepare(qora_hip_ctx* c, uint32_t wid, uint32_t wid
     g.p.k = (uint32_t)g.k;
     g.p.pro = PRO_PLAIN;
     apply_plan(g.plan, &g.p);
-    uint64_t wb = 0, sb = 0;
-    gemv_tile_bytes(g.fmt, g.plan, &wb, &sb);
+    uint64_t wb = 0, sb = 0, eb = 0;
+    gemv_tile_bytes(g.fmt, g.plan, &wb, &sb, &eb);
+    auto release = [&]() {
+        for (void* q : {g.tw, g.ts, g.te})
+            if (q) (void)hipFree(q);
+    };
     if (int rc = dalloc(c, wb, &g.tw)) return rc;
     if (sb)
-        if (int rc = dalloc(c, sb, &g.ts)) { (void)hipFree(g.tw); return rc; }
-    const hipError_t e = launch_gemv_tile(g.fmt, g.plan, g.p, (uint8_t*)g.tw, (uint16_t*)g.ts, c->stream);
+        if (int rc = dalloc(c, sb, &g.ts)) { release(); return rc; }
+    if (eb)
+        if (int rc = dalloc(c, eb, &g.te)) { release(); return rc; }
+    const hipError_t e =
+        launch_gemv_tile(g.fmt, g.plan, g.p, (uint8_t*)g.tw, (uint16_t*)g.ts, (int8_t*)g.te, c->stream);
     const hipError_t e2 = e == hipSuccess ? hipStreamSynchronize(c->stream) : e;
     if (e2 != hipSuccess) {
-        (void)hipFree(g.tw);
-        if (g.ts) (void)hipFree(g.ts);
+        release();
         return fail(c, QORA_HIP_E_DEVICE, std::string("gemv tile packing: ") + hipGetErrorString(e2));
     }
     g.p.tw = (const uint8_t*)g.tw;
     g.p.ts = (const uint16_t*)g.ts;
+    g.p.tes = (const int8_t*)g.te;
     g.alive = true;
     *gemv_id = (uint32_t)c->gemvs.size();
     c->gemvs.push_back(g);
@@ -1004,8 +1023,8 @@ extern "C" int qora_hip_gemv_release(qora_hip_ctx* c, uint32_t gemv_id) {
     if (c->capturing) return fail(c, QORA_HIP_E_STATE, "gemv_release frees: not allowed during capture");
     HIP_TRY(c, hipStreamSynchronize(c->stream));
     PreparedGemv& g = c->gemvs[gemv_id];
-    (void)hipFree(g.tw);
-    if (g.ts) (void)hipFree(g.ts);
+    for (void* q : {g.tw, g.ts, g.te})
+        if (q) (void)hipFree(q);
     g = PreparedGemv();
     return QORA_HIP_OK;
 }

@@ -68,6 +68,53 @@ __device__ __forceinline__ float inv_rms_fixed(const long long* xacc, uint32_t n
     return 1.0f / sqrtf(ss / (float)n + 1e-6f);
 }
 
+// Attention-merge prologue (PRO_ATTN): rows [k0, k1) are dims of heads
+// k0/hd .. (k1-1)/hd of the attention output; their split partials are
+// merged (online-softmax merge: out = sum_s acc_s e^(m_s - m) /
+// sum_s l_s e^(m_s - m), in split order) into xs[0, nrows) (zeros past k1).
+// aw: LDS of kAttnMaxSplits floats per head the slice touches. Contains
+// block barriers: every thread of the block calls it.
+template <int NT>
+__device__ __forceinline__ void attn_merge_rows(const GemvParams& p, uint32_t k0, uint32_t k1, uint32_t nrows,
+                                                float* xs, float* aw) {
+    const int t = threadIdx.x;
+    const uint32_t hd = p.head_dim, G = p.groups;
+    const uint32_t L = (uint32_t)(*p.pos) + 1u;
+    const uint32_t s_act = min(p.attn_s_max, (L + p.attn_chunk - 1) / p.attn_chunk);
+    const uint32_t h0 = k0 / hd;
+    const uint32_t nh = (k1 - 1) / hd - h0 + 1;
+    const int wave = t / kWave, lane = t & (kWave - 1);
+    for (uint32_t hh = wave; hh < nh; hh += NT / kWave) {
+        const uint32_t h = h0 + hh, kvh = h / G, g = h % G;
+        const float* base = p.attn_part + ((uint64_t)kvh * p.attn_s_max * G + g) * (hd + 2);
+        float m = -INFINITY;
+        for (uint32_t s = lane; s < s_act; s += kWave) m = fmaxf(m, base[(uint64_t)s * G * (hd + 2) + hd]);
+        m = wave_max(m);
+        float den = 0.f;
+        for (uint32_t s = lane; s < s_act; s += kWave) {
+            const float* ps = base + (uint64_t)s * G * (hd + 2);
+            const float w = expf(ps[hd] - m);
+            aw[hh * kAttnMaxSplits + s] = w;
+            den += ps[hd + 1] * w;
+        }
+        den = wave_sum(den);
+        const float inv = 1.0f / den;
+        for (uint32_t s = lane; s < s_act; s += kWave) aw[hh * kAttnMaxSplits + s] *= inv;
+    }
+    __syncthreads();
+    for (uint32_t i = t; i < nrows; i += NT) {
+        const uint32_t r = k0 + i;
+        float v = 0.f;
+        if (r < k1) {
+            const uint32_t h = r / hd, d = r % hd, hh = h - h0;
+            const float* base = p.attn_part + ((uint64_t)(h / G) * p.attn_s_max * G + (h % G)) * (hd + 2) + d;
+            for (uint32_t s = 0; s < s_act; ++s) v = fmaf(base[(uint64_t)s * G * (hd + 2)], aw[hh * kAttnMaxSplits + s], v);
+        }
+        xs[i] = v;
+    }
+    __syncthreads();
+}
+
 // Which matrix and which 32-column group lane gi of column tile `tile` reads
 // (shared by the GEMV kernel and the tile-layout packer, so both agree).
 // Lanes past the segment get group 0 (grp_c): their columns are never written.
@@ -250,45 +297,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
 #pragma unroll
         for (int j = 0; j < RPL; ++j) xv[j] = (k0 + rl + j * RL < k1) ? xv[j] : 0.f;
     } else {
-        // PRO_ATTN: rows [k0, k1) are dims of heads k0/hd .. (k1-1)/hd of the
-        // attention output; merge their split partials (online-softmax merge:
-        // out = sum_s acc_s e^(m_s - m) / sum_s l_s e^(m_s - m)), staged in LDS.
-        const uint32_t hd = p.head_dim, G = p.groups;
-        const uint32_t L = (uint32_t)(*p.pos) + 1u;
-        const uint32_t s_act = min(p.attn_s_max, (L + p.attn_chunk - 1) / p.attn_chunk);
-        const uint32_t h0 = k0 / hd;
-        const uint32_t nh = (k1 - 1) / hd - h0 + 1;
-        const int wave = t / kWave, lane = t & (kWave - 1);
-        for (uint32_t hh = wave; hh < nh; hh += NT / kWave) {
-            const uint32_t h = h0 + hh, kvh = h / G, g = h % G;
-            const float* base = p.attn_part + ((uint64_t)kvh * p.attn_s_max * G + g) * (hd + 2);
-            float m = -INFINITY;
-            for (uint32_t s = lane; s < s_act; s += kWave) m = fmaxf(m, base[(uint64_t)s * G * (hd + 2) + hd]);
-            m = wave_max(m);
-            float den = 0.f;
-            for (uint32_t s = lane; s < s_act; s += kWave) {
-                const float* ps = base + (uint64_t)s * G * (hd + 2);
-                const float w = expf(ps[hd] - m);
-                aw[hh * kAttnMaxSplits + s] = w;
-                den += ps[hd + 1] * w;
-            }
-            den = wave_sum(den);
-            const float inv = 1.0f / den;
-            for (uint32_t s = lane; s < s_act; s += kWave) aw[hh * kAttnMaxSplits + s] *= inv;
-        }
-        __syncthreads();
-        for (int i = t; i < KR; i += NT) {
-            const uint32_t r = k0 + i;
-            float v = 0.f;
-            if (r < k1) {
-                const uint32_t h = r / hd, d = r % hd, hh = h - h0;
-                const float* base = p.attn_part + ((uint64_t)(h / G) * p.attn_s_max * G + (h % G)) * (hd + 2) + d;
-                for (uint32_t s = 0; s < s_act; ++s)
-                    v = fmaf(base[(uint64_t)s * G * (hd + 2)], aw[hh * kAttnMaxSplits + s], v);
-            }
-            xs[i] = v;
-        }
-        __syncthreads();
+        attn_merge_rows<NT>(p, k0, k1, KR, xs, aw);
 #pragma unroll
         for (int j = 0; j < RPL; ++j) xv[j] = xs[rl + j * RL];
     }

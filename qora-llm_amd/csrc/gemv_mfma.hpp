@@ -1,0 +1,397 @@
+// Q4 GEMV on the gfx950 integer matrix cores (v_mfma_i32_16x16x64_i8).
+//
+// y[j] = sum_k x[k] * s[k][g(j)] * (q[k][j] - 8)   (gemv_q4, gemv.rs:596-675)
+//
+// At batch 1 a VALU GEMV spends ~2 instructions per nibble (unpack, convert,
+// multiply-add) and is bound by issue, not by HBM. Here the multiply-add
+// runs on the matrix cores in exact integer arithmetic:
+//   * weights: the int8 B operand is 16 * (q - 8), made from packed nibbles
+//     by one bit operation per 4 nibbles: (w & 0xF0F0F0F0) ^ 0x80808080 maps
+//     a high nibble q to the byte 16q - 128 = 16 (q - 8) (two's complement),
+//     and the low nibbles take the same after a 4-bit shift;
+//   * inputs: z[k][g] = x[k] * s[k][g] (fp32) is quantised against a block
+//     exponent E (2^E bounds |z| over the K slice of the group) to the
+//     integer M = round(z * 2^(30-E)), |M| <= 2^30, split into four signed
+//     base-256 digits ("limbs", each in [-128, 127]: M + 0x808080 with the
+//     low three bytes re-centred by ^ 0x80), which form rows 0..3 of the A
+//     operand (rows 4..15 are zero);
+//   * the MFMA sums limb * 16 (q - 8) over 64 rows in int32 (|C| < 2^22 per
+//     slice), and C0 + 2^8 C1 + 2^16 C2 + 2^24 C3 = sum_k M_k * 16 (q_k - 8)
+//     exactly; times 2^(E-34) it is the slice's contribution, which lands in
+//     the fixed-point accumulator (value * 2^36) as one int64 atomic.
+// Every step after the fp32 product x*s is exact, so the result is
+// deterministic, and the only rounding (|M| quantised to 2^-30 of the
+// block bound) is ~2^-27 of the largest term, below fp32 accumulation error.
+//
+// Operand layouts of v_mfma_i32_16x16x64_i8 (lane l, byte b = 0..15):
+//   A[i = l % 16][k = 16 (l / 16) + b], B[k = 16 (l / 16) + b][j = l % 16],
+//   C[i = 4 (l / 16) + r][j = l % 16] in result register r.
+// So lanes 0..15 end with the four limb sums of column j = l.
+//
+// Work decomposition: a workgroup is 4 waves x GW groups (32 columns each)
+// over a K slice of KW rows (a multiple of 64); all 4 waves share the slice.
+// Column tiles map to (segment, group) through lane_source with
+// gt = 4 * GW, so q|k|v concatenation and gate|up pairing work as in the
+// VALU kernel. Tile layout (gemv_q4m_pack_kernel), per (workgroup, wave):
+//   tw: [group g < GW][K block kb < KW/64][lane < 64] x 16 B: lane l's B
+//       fragments of column blocks 2g (bytes 0-7) and 2g+1 (bytes 8-15) for
+//       column 16 * blk + l % 16 and rows 64 kb + 16 (l / 16) + b; in each
+//       8-byte fragment, byte m of word w holds row 8w + m in its high
+//       nibble and row 8w + 4 + m in its low nibble;
+//   ts: [lane][u < NZ] scales of the lane's z values (e = lane * NZ + u:
+//       row e % KW, group e / KW);
+//   tes: [group] exponent bound of the slice's scales (max |s| <= 2^tes).
+#pragma once
+
+#include "common.hpp"
+#include "gemv.hpp"
+#include "params.hpp"
+
+namespace qora {
+
+typedef int v4i32 __attribute__((ext_vector_type(4)));
+
+// exponent bound of a binary16 magnitude: |s| <= 2^e
+__device__ __forceinline__ int f16_exp_bound(uint16_t h) {
+    const int e = (h >> 10) & 0x1F;
+    return e == 0 ? -14 : e - 14;
+}
+
+// One workgroup per (GEMV workgroup b, wave w), 64 lanes: lane l writes its
+// 16-byte fragment pair for every (group, K block), its NZ scales, and lanes
+// 0..gw-1 the exponent bound of their group.
+__global__ __launch_bounds__(64) void gemv_q4m_pack_kernel(GemvParams p, int gw, int kw, uint8_t* tw, uint16_t* ts,
+                                                           int8_t* te) {
+    const uint32_t l = threadIdx.x;
+    const uint32_t b = blockIdx.x / 4, w = blockIdx.x % 4;
+    const uint32_t tile = b % p.tiles, split = b / p.tiles;
+    const uint32_t k0 = split * (uint32_t)kw;
+    const uint32_t k1 = min(p.k, k0 + (uint32_t)kw);
+    const uint32_t nkb = (uint32_t)kw / 64, nz = (uint32_t)(gw * kw) / 64;
+    const uint64_t bw = (uint64_t)b * 4 + w;
+    for (int g = 0; g < gw; ++g) {
+        const LaneSrc src = lane_source(p, tile, (int)w * gw + g, 4 * gw);
+        const uint64_t row_bytes = (uint64_t)src.sg.groups * 16u;
+        for (uint32_t kb = 0; kb < nkb; ++kb) {
+            uint32_t word[4];
+            for (int half = 0; half < 2; ++half) {
+                const uint32_t c = src.grp_c * 32u + (uint32_t)half * 16u + (l % 16);   // column in the segment
+                const uint32_t rbase = k0 + kb * 64u + 16u * (l / 16);
+                for (int wi = 0; wi < 2; ++wi) {
+                    uint32_t v = 0;
+                    for (int m = 0; m < 4; ++m) {
+                        const uint32_t rh = min(rbase + 8u * wi + m, p.k - 1u);
+                        const uint32_t rl = min(rbase + 8u * wi + 4u + m, p.k - 1u);
+                        const uint8_t bh = src.sg.w[rh * row_bytes + c / 2];
+                        const uint8_t bl = src.sg.w[rl * row_bytes + c / 2];
+                        const uint32_t qh = (c & 1) ? (bh >> 4) : (bh & 0xF);
+                        const uint32_t ql = (c & 1) ? (bl >> 4) : (bl & 0xF);
+                        v |= ((qh << 4) | ql) << (8 * m);
+                    }
+                    word[half * 2 + wi] = v;
+                }
+            }
+            *reinterpret_cast<uint4*>(tw + ((bw * gw + g) * nkb + kb) * 1024u + l * 16u) =
+                make_uint4(word[0], word[1], word[2], word[3]);
+        }
+    }
+    for (uint32_t u = 0; u < nz; ++u) {
+        const uint32_t e = l * nz + u;
+        const LaneSrc src = lane_source(p, tile, (int)(w * gw + e / (uint32_t)kw), 4 * gw);
+        const uint32_t r = min(k0 + e % (uint32_t)kw, p.k - 1u);
+        ts[(bw * 64u + l) * nz + u] = src.sg.scales[(uint64_t)r * src.sg.groups + src.grp_c];
+    }
+    if (l < (uint32_t)gw) {
+        const LaneSrc src = lane_source(p, tile, (int)(w * gw + l), 4 * gw);
+        int eb = -14;
+        for (uint32_t r = k0; r < k1; ++r)
+            eb = max(eb, f16_exp_bound(src.sg.scales[(uint64_t)r * src.sg.groups + src.grp_c] & 0x7FFFu));
+        te[bw * gw + l] = (int8_t)eb;
+    }
+}
+
+// 16 nibbles (8 bytes) -> B fragment of 16 int8 values 16 * (q - 8)
+__device__ __forceinline__ v4i32 q4_bfrag(uint32_t w0, uint32_t w1) {
+    v4i32 r;
+    r[0] = (int)((w0 & 0xF0F0F0F0u) ^ 0x80808080u);
+    r[1] = (int)(((w0 << 4) & 0xF0F0F0F0u) ^ 0x80808080u);
+    r[2] = (int)((w1 & 0xF0F0F0F0u) ^ 0x80808080u);
+    r[3] = (int)(((w1 << 4) & 0xF0F0F0F0u) ^ 0x80808080u);
+    return r;
+}
+
+// Weight fragments of one wave: [group][K block] x 16 B per lane.
+template <int GW, int NKB>
+__device__ __forceinline__ void gemv_q4m_load_weights(const GemvParams& p, uint64_t bw, int lane, uint4 (&wq)[GW][NKB]) {
+    const uint8_t* src = p.tw + bw * (uint64_t)(GW * NKB * 1024) + (uint32_t)lane * 16u;
+#pragma unroll
+    for (int g = 0; g < GW; ++g)
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb) wq[g][kb] = *reinterpret_cast<const uint4*>(src + (g * NKB + kb) * 1024);
+}
+
+// The lane's NZ scales (adjacent binary16) and the wave's exponent bounds.
+template <int GW, int NZ>
+__device__ __forceinline__ void gemv_q4m_load_scales(const GemvParams& p, uint64_t bw, int lane,
+                                                     uint32_t (&sw)[(NZ + 1) / 2], int (&esg)[GW]) {
+    const uint16_t* src = p.ts + (bw * 64u + (uint32_t)lane) * NZ;
+    if constexpr (NZ >= 8) {
+#pragma unroll
+        for (int h = 0; h < NZ / 8; ++h) {
+            const uint4 v = reinterpret_cast<const uint4*>(src)[h];
+            sw[4 * h] = v.x;
+            sw[4 * h + 1] = v.y;
+            sw[4 * h + 2] = v.z;
+            sw[4 * h + 3] = v.w;
+        }
+    } else if constexpr (NZ == 4) {
+        const uint2 v = *reinterpret_cast<const uint2*>(src);
+        sw[0] = v.x;
+        sw[1] = v.y;
+    } else if constexpr (NZ == 2) {
+        sw[0] = *reinterpret_cast<const uint32_t*>(src);
+    } else {
+        sw[0] = src[0];
+    }
+#pragma unroll
+    for (int g = 0; g < GW; ++g) esg[g] = __builtin_amdgcn_readfirstlane((int)p.tes[bw * GW + g]);
+}
+
+// Attention-merge prologue run by one wave (see attn_merge_rows) for rows
+// [r0, r1) of the slice that starts at k0 (r1 - r0 <= 32): the per-split
+// weights of each head the rows touch, then each row's merge, with lane l
+// taking row r0 + l % 32 and the splits of parity l / 32 (all of its loads
+// issued together; slots past the active splits are skipped by selection,
+// so stale bits never reach the sum). aw: LDS of kAttnMaxSplits floats per
+// head, private to the calling wave.
+__device__ __forceinline__ void attn_merge_rows_wave(const GemvParams& p, uint32_t k0, uint32_t r0, uint32_t r1,
+                                                     uint32_t k1, float* xs, float* aw) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const uint32_t hd = p.head_dim, G = p.groups;
+    const uint32_t L = (uint32_t)(*p.pos) + 1u;
+    const uint32_t s_act = min(p.attn_s_max, (L + p.attn_chunk - 1) / p.attn_chunk);
+    const uint64_t sstride = (uint64_t)G * (hd + 2);
+    const uint32_t a0 = k0 + r0, a1 = min(k0 + r1, k1);      // absolute rows
+    if (a0 >= a1) {
+        for (uint32_t i = r0 + (uint32_t)lane; i < r1; i += kWave) xs[i] = 0.f;
+        return;
+    }
+    const uint32_t h0 = a0 / hd;
+    const uint32_t nh = (a1 - 1) / hd - h0 + 1;
+    for (uint32_t hh = 0; hh < nh; ++hh) {
+        const uint32_t h = h0 + hh, kvh = h / G, g = h % G;
+        const float* base = p.attn_part + ((uint64_t)kvh * p.attn_s_max * G + g) * (hd + 2);
+        const uint32_t sc = min((uint32_t)lane, s_act - 1u);     // s_act <= 64 = lanes
+        const float ms = base[(uint64_t)sc * sstride + hd];
+        const float ls = base[(uint64_t)sc * sstride + hd + 1];
+        const bool ok = (uint32_t)lane < s_act;
+        const float m = wave_max(ok ? ms : -INFINITY);
+        const float w = ok ? expf(ms - m) : 0.f;
+        const float den = wave_sum(ok ? ls * w : 0.f);
+        aw[hh * kAttnMaxSplits + lane] = w / den;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const uint32_t i = r0 + (uint32_t)(lane % 32);
+    const uint32_t par = (uint32_t)lane / 32;
+    const uint32_t r = min(k0 + i, a1 - 1u);
+    const uint32_t h = r / hd, d = r % hd, hh = h - h0;
+    const float* base = p.attn_part + ((uint64_t)(h / G) * p.attn_s_max * G + (h % G)) * (hd + 2) + d;
+    const float* wrow = aw + hh * kAttnMaxSplits;
+    float pv[kAttnMaxSplits / 2];
+#pragma unroll
+    for (int j = 0; j < kAttnMaxSplits / 2; ++j)
+        pv[j] = base[(uint64_t)min(par + 2u * j, s_act - 1u) * sstride];
+    float v = 0.f;
+#pragma unroll
+    for (int j = 0; j < kAttnMaxSplits / 2; ++j) {
+        const uint32_t sj = par + 2u * j;
+        v = sj < s_act ? fmaf(pv[j], wrow[sj], v) : v;
+    }
+    v += __shfl_xor(v, 32, kWave);
+    if (lane < 32 && i < r1) xs[i] = k0 + i < k1 ? v : 0.f;
+}
+
+// Four matrix-core waves plus one prologue wave. A wave waits on its loads
+// in issue order, so the roles are split by wave: the prologue wave loads
+// the slice's inputs and builds x (xs in LDS) while the matrix-core waves
+// stream their scales and weights from the first cycle; the one block
+// barrier hands x over without waiting for the weight loads.
+template <int GW, int KW, int PRO>
+__global__ __launch_bounds__(PRO == PRO_ATTN ? 512 : 320) void gemv_q4m_kernel(GemvParams p) {
+    constexpr int NW = 4;                    // matrix-core waves
+    constexpr int NPW = PRO == PRO_ATTN ? 4 : 1;   // prologue waves (the attention merge gets four)
+    constexpr int NT = (NW + NPW) * kWave;
+    constexpr int NKB = KW / 64;            // K blocks (one MFMA each) per slice
+    constexpr int NZ = GW * KW / 64;        // z values per lane
+    constexpr int RPW = KW / 64;            // prologue rows per lane
+    constexpr int MAXH = KW / 32 + 1;       // heads a slice can touch (head_dim >= 32)
+    constexpr bool kAttn = PRO == PRO_ATTN;
+    static_assert(KW % 64 == 0 && KW <= 256, "slice of 64..256 rows");
+    __shared__ __align__(16) float xs[KW];
+    __shared__ float wred[2][NPW];
+    __shared__ __align__(16) uint8_t zl[NW][GW][4][KW];   // limb bytes: [wave][group][limb][row]
+    __shared__ __align__(16) uint8_t zero16[16];          // A rows 4..15
+    __shared__ float aw[kAttn ? NPW * kAttnMaxSplits * MAXH : 1];
+
+    const int t = threadIdx.x;
+    const int lane = t & (kWave - 1);
+    // wave-uniform (scalar) so segment lookups and addresses stay on the SALU
+    const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
+    const uint32_t tile = blockIdx.x % p.tiles;
+    const uint32_t split = blockIdx.x / p.tiles;
+    const uint32_t k0 = split * (uint32_t)KW;
+    const uint32_t k1 = min(p.k, k0 + (uint32_t)KW);
+    const uint64_t bw = (uint64_t)blockIdx.x * NW + wave;
+
+    if (p.zero_ptr)
+        for (uint32_t i = blockIdx.x * NT + t; i < p.zero_n; i += gridDim.x * NT) p.zero_ptr[i] = 0;
+
+    uint4 wq[GW][NKB];
+    uint32_t sw[(NZ + 1) / 2];
+    int esg[GW];
+    if (wave >= NW) {
+        // ---- prologue wave(s): rows [k0, k1) of the input into xs, max |x|, sum x^2 ----
+        // Raised issue priority: their few input loads enter the CU's memory
+        // queue ahead of the weight streams of the other waves on the CU.
+        __builtin_amdgcn_s_setprio(3);
+        float mx = 0.f, ss = 0.f;
+        if constexpr (kAttn) {
+            const uint32_t pw = (uint32_t)(wave - NW);
+            constexpr uint32_t RW = KW / NPW;   // rows per prologue wave (<= 64)
+#pragma unroll
+            for (uint32_t c = 0; c < RW; c += 32)
+                attn_merge_rows_wave(p, k0, pw * RW + c, pw * RW + min(c + 32, RW), k1, xs,
+                                     aw + pw * kAttnMaxSplits * MAXH);
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            for (uint32_t j = (uint32_t)lane; j < RW; j += kWave) mx = fmaxf(mx, fabsf(xs[pw * RW + j]));
+        } else {
+            float xp[RPW], ssp = 0.f;
+            long long xa[RPW], xb[RPW];
+            uint16_t gm[RPW];
+#pragma unroll
+            for (int j = 0; j < RPW; ++j) {
+                const uint32_t rc = min(k0 + (uint32_t)(lane + 64 * j), p.k - 1u);
+                if constexpr (PRO == PRO_PLAIN) xp[j] = p.x[rc];
+                if constexpr (PRO == PRO_GAMMA_FIXED) {
+                    xa[j] = p.xacc[rc];
+                    gm[j] = p.gamma[rc];
+                }
+                if constexpr (PRO == PRO_SILU_FIXED) {
+                    xa[j] = p.xacc[rc];
+                    xb[j] = p.xacc[p.k + rc];
+                }
+            }
+            if constexpr (PRO == PRO_SILU_FIXED) ssp = p.ss_in[min((uint32_t)lane, p.ss_n - 1u)];
+            float inv = 1.f;
+            if constexpr (PRO == PRO_SILU_FIXED)
+                inv = 1.0f / sqrtf(wave_sum(lane < (int)p.ss_n ? ssp : 0.f) / (float)p.norm_n + 1e-6f);
+#pragma unroll
+            for (int j = 0; j < RPW; ++j) {
+                const bool ok = k0 + (uint32_t)(lane + 64 * j) < k1;
+                float x;
+                if constexpr (PRO == PRO_PLAIN) {
+                    x = ok ? xp[j] : 0.f;
+                } else if constexpr (PRO == PRO_GAMMA_FIXED) {
+                    const float xf = ok ? from_fixed(xa[j]) : 0.f;
+                    ss += xf * xf;
+                    x = xf * h2f(gm[j]);
+                } else {
+                    x = ok ? silu_mul(inv * from_fixed(xa[j]), inv * from_fixed(xb[j])) : 0.f;
+                }
+                xs[lane + 64 * j] = x;
+                mx = fmaxf(mx, fabsf(x));
+            }
+        }
+        mx = wave_max(mx);
+        if constexpr (PRO == PRO_GAMMA_FIXED) ss = wave_sum(ss);
+        if (lane == 0) {
+            wred[0][wave - NW] = mx;
+            wred[1][wave - NW] = ss;
+        }
+        if (wave == NW && lane < 4) reinterpret_cast<uint32_t*>(zero16)[lane] = 0u;
+    } else {
+        // ---- matrix-core waves: scales first (the quantisation needs them), then weights ----
+        gemv_q4m_load_scales<GW, NZ>(p, bw, lane, sw, esg);
+        gemv_q4m_load_weights<GW, NKB>(p, bw, lane, wq);
+    }
+    __syncthreads();
+    if (wave >= NW) return;
+    float xm = wred[0][0];
+#pragma unroll
+    for (int w = 1; w < NPW; ++w) xm = fmaxf(xm, wred[0][w]);
+    if constexpr (PRO == PRO_GAMMA_FIXED) {
+        if (t == 0 && tile == 0) p.ss_out[split] = wred[1][0];
+    }
+    // 2^ex bounds max |x| (0 for an all-zero slice)
+    const int ex = __builtin_amdgcn_readfirstlane(xm > 0.f ? (int)((__float_as_uint(xm) >> 23) & 0xFFu) - 126 : 0);
+
+    // ---- z = x * s quantised to 30-bit integers, stored as limb bytes ----
+#pragma unroll
+    for (int u = 0; u < NZ; ++u) {
+        const uint32_t e = (uint32_t)lane * NZ + u;
+        const uint32_t rz = e % KW, gz = e / KW;
+        int es = esg[0];
+#pragma unroll
+        for (int g = 1; g < GW; ++g) es = gz == (uint32_t)g ? esg[g] : es;
+        const uint16_t sbits = (uint16_t)((u & 1) ? (sw[u / 2] >> 16) : (sw[u / 2] & 0xFFFFu));
+        const float z = xs[rz] * h2f(sbits);
+        const int M = (int)rintf(ldexpf(z, 30 - (ex + es)));
+        const uint32_t limbs = (uint32_t)(M + 0x808080) ^ 0x808080u;
+        uint8_t* zp = &zl[wave][gz][0][rz];
+        zp[0] = (uint8_t)(limbs & 0xFFu);
+        zp[KW] = (uint8_t)((limbs >> 8) & 0xFFu);
+        zp[2 * KW] = (uint8_t)((limbs >> 16) & 0xFFu);
+        zp[3 * KW] = (uint8_t)(limbs >> 24);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    // ---- matrix cores: C[limb][column] += A[limb][k] * B[k][column] ----
+    v4i32 acc[2 * GW];
+#pragma unroll
+    for (int c = 0; c < 2 * GW; ++c) acc[c] = (v4i32){0, 0, 0, 0};
+    const uint32_t li = (uint32_t)lane % 16, lk = (uint32_t)lane / 16;
+#pragma unroll
+    for (int g = 0; g < GW; ++g) {
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb) {
+            const uint8_t* ap = li < 4 ? &zl[wave][g][li][kb * 64 + 16 * lk] : zero16;
+            const v4i32 a = *reinterpret_cast<const v4i32*>(ap);
+            const uint4 w = wq[g][kb];
+            acc[2 * g] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, q4_bfrag(w.x, w.y), acc[2 * g], 0, 0, 0);
+            acc[2 * g + 1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, q4_bfrag(w.z, w.w), acc[2 * g + 1], 0, 0, 0);
+        }
+    }
+
+    // ---- epilogue: lanes 0..15 hold limbs 0..3 of column l of each block ----
+    // Y = C0 + 2^8 C1 + 2^16 C2 + 2^24 C3 as (C0 + 2^8 C1) + 2^16 (C2 + 2^8 C3):
+    // each half fits int32 (|C| < 2^22). value = Y * 2^(E - 34), so the
+    // fixed-point amount (2^36 units) is Y << (E + 2), rounded when E + 2 < 0.
+    if (lane < 16) {
+#pragma unroll
+        for (int g = 0; g < GW; ++g) {
+            const LaneSrc src = lane_source(p, tile, wave * GW + g, 4 * GW);
+            if (src.grp >= src.sg.groups) continue;
+            const int sh = max(min(ex + esg[g] + 2, 62), -62);
+            const int rsh = sh < 0 ? -sh : 0, lsh = sh > 0 ? sh : 0;
+            const long long rnd = rsh > 0 ? (1LL << (rsh - 1)) : 0;
+            long long* dst = p.acc + src.sg.col0 + src.grp * 32u + (uint32_t)lane;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const v4i32 c = acc[2 * g + h];
+                const int lo = c[0] + (c[1] << 8);
+                const int hi = c[2] + (c[3] << 8);
+                const long long Y = (long long)lo + ((long long)hi << 16);
+                const long long f = ((Y + rnd) >> rsh) << lsh;
+                atomicAdd(reinterpret_cast<unsigned long long*>(dst + h * 16), (unsigned long long)f);
+            }
+        }
+    }
+}
+
+}  // namespace qora

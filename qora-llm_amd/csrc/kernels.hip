@@ -1,6 +1,7 @@
 // Kernel instantiations and launch helpers (gfx950).
 #include "launch.hpp"
 #include "gemv.hpp"
+#include "gemv_mfma.hpp"
 #include "attn.hpp"
 
 #include <algorithm>
@@ -48,6 +49,47 @@ bool plan_gemv(int fmt, uint32_t k, const uint32_t* seg_groups, int nseg, bool p
     return true;
 }
 
+bool plan_gemv_q4m(uint32_t k, const uint32_t* seg_groups, int nseg, bool paired, int cus, GemvPlan* plan,
+                   uint32_t row_align) {
+    if (k == 0 || nseg < 1 || nseg > 3 || row_align == 0) return false;
+    if (paired && (nseg != 2 || seg_groups[0] != seg_groups[1])) return false;
+    // One group (32 columns) per wave and the deepest K slice that still
+    // gives every CU a workgroup: measured on the decode shapes, deeper
+    // slices beat wider tiles (fewer workgroups pay the input latency and
+    // the atomics, and each streams a longer contiguous block).
+    static const uint32_t kws[3] = {256, 128, 64};
+    const uint32_t want = (uint32_t)std::max(1, cus);
+    const int forced_gw = env_int("QORA_GEMV_GW", 0), forced_kw = env_int("QORA_GEMV_KW", 0);
+    const int gw = (forced_gw == 1 || forced_gw == 2 || forced_gw == 4) ? forced_gw : 1;
+    GemvPlan best;
+    bool have = false;
+    for (uint32_t kw : kws) {
+        if (forced_kw && kw != (uint32_t)forced_kw) continue;
+        if (!(kw % row_align == 0 || row_align % kw == 0)) continue;
+        GemvPlan pl;
+        pl.mfma = 1;
+        pl.gw = gw;
+        pl.gt = 4 * gw;
+        pl.rpl = 0;
+        if (paired) {
+            pl.tiles = (seg_groups[0] + 2 * gw - 1) / (2 * gw);
+        } else {
+            pl.tiles = 0;
+            for (int i = 0; i < nseg; ++i) pl.tiles += (seg_groups[i] + pl.gt - 1) / pl.gt;
+        }
+        pl.kr = kw;
+        pl.splits = (k + pl.kr - 1) / pl.kr;
+        if (!have || (best.blocks() < want && pl.blocks() > best.blocks())) {
+            best = pl;
+            have = true;
+        }
+        if (best.blocks() >= want) break;
+    }
+    if (!have) return false;
+    *plan = best;
+    return true;
+}
+
 void apply_plan(const GemvPlan& plan, GemvParams* p) {
     uint32_t t0 = 0, c0 = 0;
     for (int i = 0; i < p->nseg; ++i) {
@@ -88,18 +130,54 @@ static hipError_t launch_gemv_gt(const GemvPlan& plan, const GemvParams& p, hipS
         if (p.pro != PRO_PLAIN) return hipErrorInvalidValue;
         return launch_gemv_pro<FMT, GT, PRO_PLAIN, false>(plan, p, stream);
     }
-    if (FMT == FMT_Q4 && !p.ts) return hipErrorInvalidValue;
+    if constexpr (FMT == FMT_Q4) {
+        return hipErrorInvalidValue;   // the Q4 tile layout runs on the matrix cores (launch_q4m_*)
+    } else {
+        switch (p.pro) {
+        case PRO_PLAIN: return launch_gemv_pro<FMT, GT, PRO_PLAIN, true>(plan, p, stream);
+        case PRO_GAMMA_FIXED: return launch_gemv_pro<FMT, GT, PRO_GAMMA_FIXED, true>(plan, p, stream);
+        case PRO_SILU_FIXED: return launch_gemv_pro<FMT, GT, PRO_SILU_FIXED, true>(plan, p, stream);
+        case PRO_ATTN: return launch_gemv_pro<FMT, GT, PRO_ATTN, true>(plan, p, stream);
+        default: return hipErrorInvalidValue;
+        }
+    }
+}
+
+template <int GW, int KW>
+static hipError_t launch_q4m_kw(const GemvPlan& plan, const GemvParams& p, hipStream_t stream) {
+    // 4 matrix-core waves + the prologue wave (four for the attention merge)
+    const dim3 grid(plan.blocks()), block(320), block_attn(512);
     switch (p.pro) {
-    case PRO_PLAIN: return launch_gemv_pro<FMT, GT, PRO_PLAIN, true>(plan, p, stream);
-    case PRO_GAMMA_FIXED: return launch_gemv_pro<FMT, GT, PRO_GAMMA_FIXED, true>(plan, p, stream);
-    case PRO_SILU_FIXED: return launch_gemv_pro<FMT, GT, PRO_SILU_FIXED, true>(plan, p, stream);
-    case PRO_ATTN: return launch_gemv_pro<FMT, GT, PRO_ATTN, true>(plan, p, stream);
+    case PRO_PLAIN: hipLaunchKernelGGL((gemv_q4m_kernel<GW, KW, PRO_PLAIN>), grid, block, 0, stream, p); break;
+    case PRO_GAMMA_FIXED: hipLaunchKernelGGL((gemv_q4m_kernel<GW, KW, PRO_GAMMA_FIXED>), grid, block, 0, stream, p); break;
+    case PRO_SILU_FIXED: hipLaunchKernelGGL((gemv_q4m_kernel<GW, KW, PRO_SILU_FIXED>), grid, block, 0, stream, p); break;
+    case PRO_ATTN: hipLaunchKernelGGL((gemv_q4m_kernel<GW, KW, PRO_ATTN>), grid, block_attn, 0, stream, p); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+template <int GW>
+static hipError_t launch_q4m_gw(const GemvPlan& plan, const GemvParams& p, hipStream_t stream) {
+    switch (plan.kr) {
+    case 64: return launch_q4m_kw<GW, 64>(plan, p, stream);
+    case 128: return launch_q4m_kw<GW, 128>(plan, p, stream);
+    case 256: return launch_q4m_kw<GW, 256>(plan, p, stream);
     default: return hipErrorInvalidValue;
     }
 }
 
 hipError_t launch_gemv(int fmt, const GemvPlan& plan, const GemvParams& p, hipStream_t stream) {
     if (plan.blocks() == 0) return hipErrorInvalidValue;
+    if (plan.mfma) {
+        if (fmt != FMT_Q4 || !p.tw || !p.ts || !p.tes) return hipErrorInvalidValue;
+        switch (plan.gw) {
+        case 1: return launch_q4m_gw<1>(plan, p, stream);
+        case 2: return launch_q4m_gw<2>(plan, p, stream);
+        case 4: return launch_q4m_gw<4>(plan, p, stream);
+        default: return hipErrorInvalidValue;
+        }
+    }
     if (fmt == FMT_Q4) {
         if (plan.gt == 8) return launch_gemv_gt<FMT_Q4, 8>(plan, p, stream);
         if (plan.gt == 16) return launch_gemv_gt<FMT_Q4, 16>(plan, p, stream);
@@ -110,16 +188,33 @@ hipError_t launch_gemv(int fmt, const GemvPlan& plan, const GemvParams& p, hipSt
     return hipErrorInvalidValue;
 }
 
-void gemv_tile_bytes(int fmt, const GemvPlan& plan, uint64_t* w_bytes, uint64_t* s_bytes) {
+void gemv_tile_bytes(int fmt, const GemvPlan& plan, uint64_t* w_bytes, uint64_t* s_bytes, uint64_t* e_bytes) {
+    if (plan.mfma) {
+        const uint64_t waves = (uint64_t)plan.blocks() * 4u;
+        const uint64_t nkb = plan.kr / 64u, nz = (uint64_t)plan.gw * plan.kr / 64u;
+        *w_bytes = waves * (uint64_t)plan.gw * nkb * 1024u;
+        *s_bytes = waves * 64u * nz * 2u;
+        *e_bytes = waves * (uint64_t)plan.gw;
+        return;
+    }
     const uint64_t steps = (uint64_t)plan.blocks() * (uint64_t)plan.rpl;
     *w_bytes = steps * 256u * (fmt == FMT_Q4 ? 16u : 64u);
     *s_bytes = fmt == FMT_Q4 ? steps * 256u * 2u : 0u;
+    *e_bytes = 0;
 }
 
 hipError_t launch_gemv_tile(int fmt, const GemvPlan& plan, const GemvParams& p, uint8_t* tw, uint16_t* ts,
-                            hipStream_t stream) {
+                            int8_t* te, hipStream_t stream) {
+    if (p.k == 0) return hipErrorInvalidValue;
+    if (plan.mfma) {
+        const uint64_t grid = (uint64_t)plan.blocks() * 4u;
+        if (fmt != FMT_Q4 || !ts || !te || grid == 0 || grid > 0x7FFFFFFFull) return hipErrorInvalidValue;
+        hipLaunchKernelGGL(gemv_q4m_pack_kernel, dim3((uint32_t)grid), dim3(64), 0, stream, p, plan.gw, (int)plan.kr,
+                           tw, ts, te);
+        return hipGetLastError();
+    }
     const uint64_t grid = (uint64_t)plan.blocks() * (uint64_t)plan.rpl;
-    if (grid == 0 || grid > 0x7FFFFFFFull || p.k == 0) return hipErrorInvalidValue;
+    if (grid == 0 || grid > 0x7FFFFFFFull) return hipErrorInvalidValue;
     if (fmt == FMT_Q4) {
         if (!ts) return hipErrorInvalidValue;
         hipLaunchKernelGGL(gemv_tile_kernel<FMT_Q4>, dim3((uint32_t)grid), dim3(256), 0, stream, p, plan.gt, plan.rpl,

@@ -11,10 +11,12 @@ namespace qora {
 // Launch shape of one split-K GEMV call site.
 struct GemvPlan {
     int gt = 8;           // groups per column tile
-    int rpl = 4;          // rows per lane
+    int rpl = 4;          // rows per lane (VALU kernel)
     uint32_t tiles = 0;   // column tiles
     uint32_t splits = 0;  // K slices
     uint32_t kr = 0;      // rows per K slice
+    int mfma = 0;         // 1: Q4 on the matrix cores (gemv_q4m_kernel): gt = 4*gw, kr = kw
+    int gw = 0;           // groups per wave (MFMA kernel)
     uint32_t blocks() const { return tiles * splits; }
 };
 
@@ -26,6 +28,12 @@ struct GemvPlan {
 bool plan_gemv(int fmt, uint32_t k, const uint32_t* seg_groups, int nseg, bool paired, int cus, GemvPlan* plan,
                uint32_t row_align = 1);
 
+// Q4 GEMV on the matrix cores: one group per wave (QORA_GEMV_GW may force 2
+// or 4) and the deepest K slice of 256, 128 or 64 rows (QORA_GEMV_KW may
+// force one) that gives every CU a workgroup.
+bool plan_gemv_q4m(uint32_t k, const uint32_t* seg_groups, int nseg, bool paired, int cus, GemvPlan* plan,
+                   uint32_t row_align = 1);
+
 // Fills seg[].tile0/tiles/col0 and p.tiles/splits/rows_per_split from the plan.
 // Concatenated segments land one after the other in the accumulator; paired
 // segments at 0 (gate) and n (up).
@@ -34,12 +42,12 @@ void apply_plan(const GemvPlan& plan, GemvParams* p);
 // p.tw == nullptr: reference layout, plain prologue only (kernel-level
 // entry points). Otherwise the tile layout written by launch_gemv_tile.
 hipError_t launch_gemv(int fmt, const GemvPlan& plan, const GemvParams& p, hipStream_t stream);
-// Size of the tile layout of a planned GEMV (scales: Q4 only).
-void gemv_tile_bytes(int fmt, const GemvPlan& plan, uint64_t* w_bytes, uint64_t* s_bytes);
+// Size of the tile layout of a planned GEMV (scales, exponent bounds: Q4 only).
+void gemv_tile_bytes(int fmt, const GemvPlan& plan, uint64_t* w_bytes, uint64_t* s_bytes, uint64_t* e_bytes);
 // Writes the tile layout of the reference-layout segments of p (after
-// apply_plan) into tw / ts, sized by gemv_tile_bytes.
+// apply_plan) into tw / ts / te, sized by gemv_tile_bytes.
 hipError_t launch_gemv_tile(int fmt, const GemvPlan& plan, const GemvParams& p, uint8_t* tw, uint16_t* ts,
-                            hipStream_t stream);
+                            int8_t* te, hipStream_t stream);
 hipError_t launch_fill_zero(long long* p, uint64_t n, hipStream_t stream);
 hipError_t launch_acc_to_f32(const long long* acc, uint32_t n, int paired, float* y, hipStream_t stream);
 

@@ -63,6 +63,9 @@ struct GemvParams {
     // The segment pointers then only describe the shape.
     const uint8_t* tw;
     const uint16_t* ts;
+    // Q4 on the matrix cores (gemv_q4m_kernel): per (workgroup, wave, group)
+    // exponent bound of the K slice's scales, max |s| <= 2^tes.
+    const int8_t* tes;
 };
 
 struct RowdotParams {
