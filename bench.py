@@ -217,6 +217,65 @@ def read_traffic(path):
     return None
 
 
+def extra_decode_rates(be, ctx, pkg, cfg, prompt, cap, steps):
+    """Device-chained greedy loop (no host round trip per token), and the
+    host-driven decode rate with the KV cache at ~2048 positions."""
+    be.kv_reset()
+    _, tok = be.raw_prefill(prompt, want_logits=False)
+    ctx.synchronize()
+    t0 = time.perf_counter()
+    be.generate_greedy(tok, steps)
+    chained = steps / (time.perf_counter() - t0)
+    # prefill 1920 positions, then time 120 tokens
+    long_prompt = pkg.synth_tokens(0, 2002, cap - 128, cfg.vocab)
+    _, tok = be.raw_prefill(long_prompt, want_logits=False)
+    ctx.synchronize()
+    n_long = 120
+    t0 = time.perf_counter()
+    for _ in range(n_long):
+        _, tok = be.forward_decode_raw(tok, want_logits=False)
+    ctx.synchronize()
+    tok_s_2048 = n_long / (time.perf_counter() - t0)
+    print(f"# decode at ctx ~2048: {tok_s_2048:.1f} tok/s", file=sys.stderr, flush=True)
+    return chained, tok_s_2048
+
+
+COPY_BYTES = 64 << 20
+
+
+def profile_kernel(launches=8):
+    """The dominant kernel alone, for rocprofv3 --pmc runs: three device
+    copies of COPY_BYTES (hipMemcpy's blit kernel: reads and writes
+    COPY_BYTES each, the counter calibration), then `launches` launches of
+    the gate|up GEMV (2048 -> 2 x 11008, SmolLM3-3B layer 0 weights) on
+    distinct packed copies, so each launch reads its weights from HBM."""
+    pkg = entry.load_package()
+    cfg = pkg.SMOLLM3_3B
+    hip = Hip()
+    ctx = pkg.HipContext(0)
+    k, n = cfg.hidden, cfg.intermediate
+    gp, gs = pkg.synth_q4(0, 4, k, n)
+    up, us = pkg.synth_q4(0, 5, k, n)
+    wg = ctx.upload(pkg.Weight(k=k, n=n, packed=gp, scales=gs))
+    wu = ctx.upload(pkg.Weight(k=k, n=n, packed=up, scales=us))
+    x = ctx.malloc(4 * k)
+    acc = ctx.malloc(8 * 2 * n)
+    ctx.h2d(x, pkg.synth_f32(0, 77, k))
+    src, dst = ctx.malloc(COPY_BYTES), ctx.malloc(COPY_BYTES)
+    for _ in range(3):
+        hip.d2d(dst, src, COPY_BYTES)
+    gids = [ctx.gemv_prepare(wg, wu, True) for _ in range(launches)]
+    ctx.synchronize()
+    for g in gids:
+        ctx.check(ctx.lib.qora_hip_gemv_run(ctx.h, g, x, acc, None), "gemv_run")
+    ctx.synchronize()
+    gu_bytes = 2 * (k * n // 2 + k * n // 16) + 4 * k + 8 * n
+    print(json.dumps({"profile_kernel": "gemv_q4m_kernel gate|up 2048x(2x11008)", "launches": launches,
+                      "algorithmic_bytes_per_launch": gu_bytes, "copy_bytes": COPY_BYTES}), flush=True)
+    for g in gids:
+        ctx.gemv_release(g)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -225,8 +284,13 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-gemv", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--decode-only", action="store_true",
+                    help="time only the host-driven decode (skips the chained loop and the ~2048-context run)")
     ap.add_argument("--eager", action="store_true",
                     help="launch every kernel directly instead of replaying HIP graphs (for rocprofv3)")
+    ap.add_argument("--profile-kernel", action="store_true",
+                    help="only launch the dominant kernel (gate|up GEMV) eagerly, after a device copy of "
+                         "known size, for hardware-counter runs")
     args = ap.parse_args()
     if args.eager:
         global EAGER
@@ -236,6 +300,9 @@ def main():
         print(json.dumps({"error": "this build runs on one GPU only; multi-GPU scaling is not part of it",
                           "n_gpus": args.gpus}))
         sys.exit(2)
+    if args.profile_kernel:
+        profile_kernel()
+        return
     prompt_len, cap = 64, 2048
     if prompt_len + args.warmup + args.steps > cap:
         sys.exit("warmup + steps exceed the 2048-position KV cache")
@@ -263,25 +330,9 @@ def main():
     tok_s = args.steps / dt
     print(f"# decode {tok_s:.1f} tok/s ({dt / args.steps * 1e3:.3f} ms/token)", file=sys.stderr, flush=True)
 
-    # device-chained greedy loop (no host round trip per token)
-    be.kv_reset()
-    _, tok = be.raw_prefill(prompt, want_logits=False)
-    ctx.synchronize()
-    t0 = time.perf_counter()
-    be.generate_greedy(tok, args.steps)
-    chained = args.steps / (time.perf_counter() - t0)
-
-    # decode at ~2048 context: prefill 1920 positions, then time 120 tokens
-    long_prompt = pkg.synth_tokens(0, 2002, cap - 128, cfg.vocab)
-    _, tok = be.raw_prefill(long_prompt, want_logits=False)
-    ctx.synchronize()
-    n_long = 120
-    t0 = time.perf_counter()
-    for _ in range(n_long):
-        _, tok = be.forward_decode_raw(tok, want_logits=False)
-    ctx.synchronize()
-    tok_s_2048 = n_long / (time.perf_counter() - t0)
-    print(f"# decode at ctx ~2048: {tok_s_2048:.1f} tok/s", file=sys.stderr, flush=True)
+    chained = tok_s_2048 = None
+    if not args.decode_only:
+        chained, tok_s_2048 = extra_decode_rates(be, ctx, pkg, cfg, prompt, cap, args.steps)
 
     gemv = {} if args.no_gemv else gemv_roofline(ctx, hip, be, pkg)
     for kname, v in gemv.items():
@@ -293,7 +344,7 @@ def main():
         roofline = {"bound": "hbm", "achieved": round(gu["gbps"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                     "frac": round(gu["gbps"] / HBM_PEAK_GBS, 4),
                     "traffic": read_traffic(os.path.join(ROOT, "profiles", "gate_up_q4_2048x11008_pmc.md")),
-                    "kernel": "gemv_kernel<Q4,GT=16> paired gate|up (qora_hip_gate_up_q4_accumulate)",
+                    "kernel": "gemv_q4m_kernel<GW=1,KW=256,PRO_PLAIN> paired gate|up 2048->2x11008 (qora_hip_gemv_run)",
                     "algorithmic_bytes_per_launch": gu["bytes"], "avg_launch_us": round(gu["us"], 3)}
 
     cpu = None
@@ -314,7 +365,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": round(tok_s / PUBLISHED_GPU_TOK_S, 1),
-        "dtype": "f32",
+        "dtype": "int8 MFMA + f32",
         "data": "synthetic (seeded random-init weights and token ids)",
         "config": {"workload": "SmolLM3-3B architecture (36 layers, hidden 2048, 16q/4kv heads, hd 128, "
                                "inter 11008, vocab 128256 tied), Q4 g32 weights, 64-token prompt then greedy "
@@ -324,8 +375,8 @@ def main():
         "cpu_baseline": cpu,
         "weight_roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / weight_bytes, 1),
         "frac_of_weight_roofline": round(tok_s * weight_bytes / (HBM_PEAK_GBS * 1e9), 4),
-        "tok_s_device_chained": round(chained, 2),
-        "tok_s_ctx2048": round(tok_s_2048, 2),
+        "tok_s_device_chained": round(chained, 2) if chained else None,
+        "tok_s_ctx2048": round(tok_s_2048, 2) if tok_s_2048 else None,
         "gemv_gbps": {k2: round(v["gbps"], 1) for k2, v in gemv.items()},
         "vs_baseline_ref": "reference GPU decode ~4.1 tok/s (README.md:43,157, GTX 1660 SUPER)",
     }

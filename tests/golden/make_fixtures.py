@@ -1,0 +1,97 @@
+"""Writes the golden fixtures under tests/golden/ (run on the CPU; the
+oracle is the checker, see oracle/oracle.c):
+
+  smollm3_q4_seed0_greedy64.json - the SmolLM3-3B architecture with the
+      seeded synthetic Q4 weights (seed 0): SHA-256 of every generated
+      weight byte (in model order), the 64-token prompt, and the oracle's
+      64 greedy tokens with the top-2 logit gap of each step;
+  smoke_q4_seed3_greedy64.json - the same for the 8-layer test model.
+Each step also records the top logit, so a consumer can tell a near-tie
+(gap < 1e-4 * |top logit|) from a real disagreement.
+
+Usage: python tests/golden/make_fixtures.py [--threads N]"""
+import argparse
+import hashlib
+import json
+import os
+import sys
+import time
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(os.path.dirname(HERE))
+sys.path.insert(0, ROOT)
+
+import __graft_entry__ as entry  # noqa: E402
+
+
+def weights_sha256(w):
+    h = hashlib.sha256()
+    for ws in w.layers:
+        for wt in ws:
+            h.update(wt.packed.tobytes())
+            h.update(wt.scales.tobytes())
+    h.update(w.embed.packed.tobytes())
+    h.update(w.embed.scales.tobytes())
+    for g in list(w.input_norm) + list(w.post_attn_norm) + [w.final_norm]:
+        h.update(g.tobytes())
+    h.update(w.rope_cos.tobytes())
+    h.update(w.rope_sin.tobytes())
+    return h.hexdigest()
+
+
+def fixture(pkg, orc, cfg, seed, prompt_tid, prompt_len, steps, threads, rope_positions, note):
+    t0 = time.time()
+    w = pkg.synthetic_model(cfg, seed=seed, rope_positions=rope_positions)
+    prompt = pkg.synth_tokens(seed, prompt_tid, prompt_len, cfg.vocab).tolist()
+    orc.set_threads(threads)
+    om = orc.OracleModel(w, kv_capacity=prompt_len + steps + 8, T=threads)
+    # the greedy loop of generate_raw (generate.rs:308-322) at temperature 0
+    tokens, gaps, tops = [], [], []
+    logits = om.prefill(prompt)
+    for i in range(steps):
+        t = orc.argmax(logits)
+        tokens.append(t)
+        gaps.append(orc.top2_gap(logits))
+        tops.append(float(logits[t]))
+        if i + 1 < steps:
+            logits = om.forward_decode(t)
+    return {
+        "description": note,
+        "config": {k: getattr(cfg, k) for k in ("num_layers", "vocab", "hidden", "intermediate", "num_heads",
+                                                "num_kv_heads", "head_dim", "rope_half_dim", "rope_theta")},
+        "rope_positions": rope_positions,
+        "seed": seed,
+        "weights_sha256": weights_sha256(w),
+        "prompt": prompt,
+        "oracle_threads": threads,
+        "greedy_tokens": [int(t) for t in tokens],
+        "top2_gap": [float(g) for g in gaps],
+        "top_logit": tops,
+        "seconds": round(time.time() - t0, 1),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--threads", type=int, default=min(16, os.cpu_count() or 1))
+    args = ap.parse_args()
+    pkg, orc = entry.load_package(), entry.load_oracle()
+    small = entry.smoke_config(pkg)
+    small.num_layers = 8
+    out = {
+        "smoke_q4_seed3_greedy64.json": fixture(
+            pkg, orc, small, 3, 2000, 16, 64, args.threads, 128,
+            "8-layer smoke model (vocab 1000, hidden 256), seed 3, 16-token prompt (synth_tokens tid 2000)"),
+        "smollm3_q4_seed0_greedy64.json": fixture(
+            pkg, orc, pkg.SMOLLM3_3B, 0, 2000, 64, 64, args.threads, 2048,
+            "SmolLM3-3B architecture, synthetic Q4 weights seed 0, 64-token prompt (synth_tokens tid 2000), "
+            "the bench's decode workload"),
+    }
+    for name, data in out.items():
+        with open(os.path.join(HERE, name), "w") as f:
+            json.dump(data, f, indent=1)
+        print(f"{name}: {data['seconds']} s, min gap {min(data['top2_gap']):.3g}", flush=True)
+
+
+if __name__ == "__main__":
+    main()
