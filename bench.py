@@ -109,29 +109,6 @@ def time_graph(ctx, hip, launch_fns, reps=3):
     return ms / (reps * len(launch_fns))
 
 
-class Pool:
-    """Rotating device copies of one weight so the working set exceeds MALL."""
-
-    def __init__(self, ctx, hip, srcs, min_bytes=768 << 20):
-        # srcs: list of (ptr, nbytes) parts of one weight
-        self.ctx = ctx
-        total = sum(nb for _, nb in srcs)
-        self.copies = max(4, math.ceil(min_bytes / total))
-        self.parts = []
-        for ptr, nb in srcs:
-            base = ctx.malloc(nb * self.copies)
-            for c in range(self.copies):
-                hip.d2d(base + c * nb, ptr, nb)
-            self.parts.append((base, nb))
-
-    def ptrs(self, c):
-        return [base + c * nb for base, nb in self.parts]
-
-    def free(self):
-        for base, _ in self.parts:
-            self.ctx.free(base)
-
-
 def prepared_time(ctx, hip, wid, wid_up, paired, nbytes, x, acc):
     """Average ms per launch of the decode step's GEMV kernel (tile layout,
     qora_hip_gemv_run) over >= 768 MB of distinct packed copies."""
@@ -166,16 +143,19 @@ def gemv_roofline(ctx, hip, be, pkg):
     ms = prepared_time(ctx, hip, int(be.wids[0, 4]), int(be.wids[0, 5]), True, gu_w, x, acc)
     gu_bytes = gu_w + 4 * k + 8 * n
     results["gate+up 2048x(2x11008)"] = {"us": ms * 1e3, "gbps": gu_bytes / (ms * 1e-3) / 1e9, "bytes": gu_bytes}
-    # tied lm_head, row-dot
-    ew, es = ctx.weight_ptrs(be.embed_wid)
+    # tied lm_head: the decode step's matrix-core kernel (qora_hip_lm_head_run,
+    # logits only) on distinct packed copies of the embedding
     V, Hd = c.vocab, c.hidden
-    pool = Pool(ctx, hip, [(ew, V * Hd // 2), (es, V * Hd // 16)])
+    copies = max(4, math.ceil((768 << 20) / (V * Hd // 2 + V * Hd // 16)))
+    lids = [ctx.lm_head_prepare(be.embed_wid) for _ in range(copies)]
     lm = ctx.malloc(4 * V)
-    fns = [(lambda p=pool.ptrs(i): ctx.check(lib.qora_hip_gemv_q4_rowdot(h, p[0], p[1], x, lm, V, Hd, None)))
-           for i in range(pool.copies)]
-    ms = time_graph(ctx, hip, fns)
-    pool.free()
-    ctx.free(lm)
+    try:
+        fns = [(lambda i=i: ctx.check(lib.qora_hip_lm_head_run(h, i, x, lm, None, None), "lm_head_run")) for i in lids]
+        ms = time_graph(ctx, hip, fns)
+    finally:
+        for i in lids:
+            ctx.gemv_release(i)
+        ctx.free(lm)
     results["lm_head 128256x2048"] = {"us": ms * 1e3, "gbps": q4_bytes(V, Hd) / (ms * 1e-3) / 1e9}
     ctx.free(x)
     ctx.free(acc)

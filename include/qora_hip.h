@@ -163,6 +163,16 @@ int qora_hip_acc_to_f32(qora_hip_ctx* ctx, const long long* acc, uint64_t n, int
 int qora_hip_gemv_prepare(qora_hip_ctx* ctx, uint32_t wid, uint32_t wid_up, int paired, uint32_t* gemv_id);
 int qora_hip_gemv_run(qora_hip_ctx* ctx, uint32_t gemv_id, const float* x, long long* acc, void* stream);
 int qora_hip_gemv_release(qora_hip_ctx* ctx, uint32_t gemv_id);
+/* The decode step's lm_head on an uploaded Q4 weight [rows][cols] (the tied
+ * embedding; lm_head_parallel_q4, gemv.rs:825-864, with the greedy branch
+ * of sample_token_top_k, generate.rs:346-352): prepare packs it once into
+ * the matrix-core tile layout (cols must be 128, 256, 512, 1024 or 2048);
+ * run writes logits[r] = sum_c x[c] W[r][c] and, if argmax_device is not
+ * NULL, the first-max index as a device int32. Release the id with
+ * qora_hip_gemv_release. */
+int qora_hip_lm_head_prepare(qora_hip_ctx* ctx, uint32_t wid, uint32_t* lm_id);
+int qora_hip_lm_head_run(qora_hip_ctx* ctx, uint32_t lm_id, const float* x, float* logits, int32_t* argmax_device,
+                         void* stream);
 /* lm_head_parallel_q4 / _f16 (gemv.rs:797-864): y[r] = sum_c x[c] W[r][c]
  * over a [rows][cols] matrix (the tied embedding); cols/32 must divide 64. */
 int qora_hip_gemv_q4_rowdot(qora_hip_ctx* ctx, const void* packed, const void* scales, const float* x,

@@ -100,6 +100,8 @@ SIGNATURES = {
     "qora_hip_gemv_prepare": (_I, [_P, _U32, _U32, _I, _P]),
     "qora_hip_gemv_run": (_I, [_P, _U32, _P, _P, _P]),
     "qora_hip_gemv_release": (_I, [_P, _U32]),
+    "qora_hip_lm_head_prepare": (_I, [_P, _U32, _P]),
+    "qora_hip_lm_head_run": (_I, [_P, _U32, _P, _P, _P, _P]),
     "qora_hip_gemv_q4_rowdot": (_I, [_P, _P, _P, _P, _P, _U64, _U64, _P]),
     "qora_hip_gemv_f16_rowdot": (_I, [_P, _P, _P, _P, _U64, _U64, _P]),
     "qora_hip_gate_up_q4": (_I, [_P, _P, _P, _P, _P, _P, _P, _U64, _U64, _P]),
@@ -430,6 +432,18 @@ class HipContext:
 
     def gemv_release(self, gemv_id: int) -> None:
         self.check(self.lib.qora_hip_gemv_release(self.h, gemv_id), "gemv_release")
+
+    def lm_head_prepare(self, wid: int) -> int:
+        """Packs an uploaded Q4 [rows][cols] weight into the lm_head tile layout."""
+        lid = ctypes.c_uint32()
+        self.check(self.lib.qora_hip_lm_head_prepare(self.h, wid, ctypes.byref(lid)), "lm_head_prepare")
+        return lid.value
+
+    def lm_head_run(self, lm_id: int, x_dev: int, logits_dev: int, argmax_dev: int = 0, stream: int = 0) -> None:
+        """logits = W . x with the decode step's lm_head kernel; argmax_dev (device
+        int32) receives the greedy token when given."""
+        self.check(self.lib.qora_hip_lm_head_run(self.h, lm_id, x_dev, logits_dev, argmax_dev or None,
+                                                 stream or None), "lm_head_run")
 
     def weight_ptrs(self, wid: int):
         a, b = ctypes.c_void_p(), ctypes.c_void_p()

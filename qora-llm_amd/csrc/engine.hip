@@ -49,11 +49,13 @@ struct ModelState {
     float* d_argv = nullptr;
     uint32_t* d_argi = nullptr;
     GemvPlan pl_qkv, pl_o, pl_gu, pl_down;
-    uint32_t lm_blocks = 0;
+    uint32_t lm_blocks = 0;              // argmax partials of the lm_head launch
+    bool lm_mfma = false;                // Q4 lm_head on the matrix cores (else the VALU row-dot)
     uint32_t attn_chunk = 0, attn_s_max = 0;
     std::vector<GemvParams> p_qkv, p_o, p_gu, p_down;
     std::vector<AttnParams> p_attn;
     RowdotParams p_lm{};
+    LmHeadParams p_lmq{};
     ArgmaxFinishParams p_fin{};
     EmbedParams p_emb_tok{}, p_emb_prompt{};
     hipGraphExec_t g_step = nullptr;
@@ -74,6 +76,12 @@ struct PreparedGemv {
     void* tw = nullptr;
     void* ts = nullptr;
     void* te = nullptr;
+    // lm_head (qora_hip_lm_head_prepare): k = rows, n = cols
+    bool lm_head = false;
+    LmHeadParams lp{};
+    uint32_t lm_blocks = 0;
+    void* part_val = nullptr;
+    void* part_idx = nullptr;
 };
 
 struct qora_hip_ctx {
@@ -215,7 +223,8 @@ int record_step(qora_hip_ctx* c, bool with_lm_head) {
         HIP_TRY(c, launch_gemv(m.fmt, m.pl_down, m.p_down[l], s));
     }
     if (with_lm_head) {
-        HIP_TRY(c, launch_rowdot(m.fmt, m.lm_blocks, m.p_lm, s));
+        if (m.lm_mfma) HIP_TRY(c, launch_lmhead(m.lm_blocks, m.p_lmq, s));
+        else HIP_TRY(c, launch_rowdot(m.fmt, m.lm_blocks, m.p_lm, s));
         HIP_TRY(c, launch_argmax_finish(m.p_fin, s));
     } else {
         HIP_TRY(c, launch_advance_pos(m.d_pos, s));
@@ -467,7 +476,8 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
         free_model(c);
         return fail(c, QORA_HIP_E_INVALID, "RMSNorm input split into more than 64 K slices");
     }
-    m.lm_blocks = rowdot_blocks(m.vocab, m.hidden, c->cus);
+    m.lm_mfma = m.fmt == FMT_Q4 && lmhead_supported(m.hidden) && !std::getenv("QORA_HIP_LM_ROWDOT");
+    m.lm_blocks = m.lm_mfma ? lmhead_blocks(m.vocab, c->cus) : rowdot_blocks(m.vocab, m.hidden, c->cus);
     attn_geometry(m.cap, &m.attn_chunk, &m.attn_s_max);
 
     // device buffers
@@ -643,6 +653,28 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
     m.p_lm.do_argmax = 1;
     m.p_lm.part_val = m.d_argv;
     m.p_lm.part_idx = m.d_argi;
+    if (m.lm_mfma) {
+        uint64_t wb = 0, sb = 0;
+        lmhead_tile_bytes(m.vocab, m.hidden, &wb, &sb);
+        void* tw = nullptr;
+        void* ts = nullptr;
+        if (int rc = model_alloc(c, wb, &tw)) { free_model(c); return rc; }
+        if (int rc = model_alloc(c, sb, &ts)) { free_model(c); return rc; }
+        HIP_TRY(c, launch_lmhead_pack((const uint8_t*)emb->w, (const uint16_t*)emb->scales, m.vocab, m.hidden,
+                                      (uint8_t*)tw, (uint32_t*)ts, c->stream));
+        m.p_lmq = LmHeadParams{};
+        m.p_lmq.tw = (const uint8_t*)tw;
+        m.p_lmq.ts = (const uint32_t*)ts;
+        m.p_lmq.rows = m.vocab;
+        m.p_lmq.cols = m.hidden;
+        m.p_lmq.tiles = lmhead_tiles(m.vocab);
+        m.p_lmq.xacc = m.d_xacc;
+        m.p_lmq.gamma = m.d_final;
+        m.p_lmq.y = m.d_logits;
+        m.p_lmq.do_argmax = 1;
+        m.p_lmq.part_val = m.d_argv;
+        m.p_lmq.part_idx = m.d_argi;
+    }
     m.p_fin = ArgmaxFinishParams{m.d_argv, m.d_argi, m.lm_blocks, m.d_token, m.d_pos, m.d_gen};
     m.p_emb_tok = EmbedParams{(const uint8_t*)emb->w, (const uint16_t*)emb->scales, (int)m.fmt, m.hidden,
                               m.vocab, m.d_token, nullptr, m.d_xacc};
@@ -1010,6 +1042,7 @@ extern "C" int qora_hip_gemv_run(qora_hip_ctx* c, uint32_t gemv_id, const float*
     if (gemv_id >= c->gemvs.size() || !c->gemvs[gemv_id].alive) return fail(c, QORA_HIP_E_INVALID, "unknown GEMV id");
     if (!x || !acc) return fail(c, QORA_HIP_E_INVALID, "null argument");
     const PreparedGemv& g = c->gemvs[gemv_id];
+    if (g.lm_head) return fail(c, QORA_HIP_E_INVALID, "id was prepared by lm_head_prepare: use lm_head_run");
     GemvParams p = g.p;
     p.x = x;
     p.acc = acc;
@@ -1023,9 +1056,75 @@ extern "C" int qora_hip_gemv_release(qora_hip_ctx* c, uint32_t gemv_id) {
     if (c->capturing) return fail(c, QORA_HIP_E_STATE, "gemv_release frees: not allowed during capture");
     HIP_TRY(c, hipStreamSynchronize(c->stream));
     PreparedGemv& g = c->gemvs[gemv_id];
-    for (void* q : {g.tw, g.ts, g.te})
+    for (void* q : {g.tw, g.ts, g.te, g.part_val, g.part_idx})
         if (q) (void)hipFree(q);
     g = PreparedGemv();
+    return QORA_HIP_OK;
+}
+
+extern "C" int qora_hip_lm_head_prepare(qora_hip_ctx* c, uint32_t wid, uint32_t* lm_id) {
+    if (!c) return QORA_HIP_E_INVALID;
+    if (!lm_id) return fail(c, QORA_HIP_E_INVALID, "null argument");
+    if (c->capturing) return fail(c, QORA_HIP_E_STATE, "lm_head_prepare allocates: not allowed during capture");
+    const DevWeight* w = get_weight(c, wid);
+    if (!w) return fail(c, QORA_HIP_E_INVALID, "unknown weight id");
+    if (w->fmt != FMT_Q4) return fail(c, QORA_HIP_E_INVALID, "lm_head_prepare takes a Q4 weight");
+    if (w->k == 0 || w->k > 0x7FFFFFF0ull || w->n > 0xFFFFFFFFull || !lmhead_supported((uint32_t)w->n))
+        return fail(c, QORA_HIP_E_INVALID, "lm_head shape: cols must be 128, 256, 512, 1024 or 2048");
+    PreparedGemv g;
+    g.fmt = FMT_Q4;
+    g.lm_head = true;
+    g.k = w->k;
+    g.n = w->n;
+    const uint32_t rows = (uint32_t)w->k, cols = (uint32_t)w->n;
+    g.lm_blocks = lmhead_blocks(rows, c->cus);
+    uint64_t wb = 0, sb = 0;
+    lmhead_tile_bytes(rows, cols, &wb, &sb);
+    auto release = [&]() {
+        for (void* q : {g.tw, g.ts, g.part_val, g.part_idx})
+            if (q) (void)hipFree(q);
+    };
+    if (int rc = dalloc(c, wb, &g.tw)) return rc;
+    if (int rc = dalloc(c, sb, &g.ts)) { release(); return rc; }
+    if (int rc = dalloc(c, (size_t)g.lm_blocks * 4, &g.part_val)) { release(); return rc; }
+    if (int rc = dalloc(c, (size_t)g.lm_blocks * 4, &g.part_idx)) { release(); return rc; }
+    const hipError_t e = launch_lmhead_pack((const uint8_t*)w->w, (const uint16_t*)w->scales, rows, cols,
+                                            (uint8_t*)g.tw, (uint32_t*)g.ts, c->stream);
+    const hipError_t e2 = e == hipSuccess ? hipStreamSynchronize(c->stream) : e;
+    if (e2 != hipSuccess) {
+        release();
+        return fail(c, QORA_HIP_E_DEVICE, std::string("lm_head tile packing: ") + hipGetErrorString(e2));
+    }
+    g.lp.tw = (const uint8_t*)g.tw;
+    g.lp.ts = (const uint32_t*)g.ts;
+    g.lp.rows = rows;
+    g.lp.cols = cols;
+    g.lp.tiles = lmhead_tiles(rows);
+    g.lp.part_val = (float*)g.part_val;
+    g.lp.part_idx = (uint32_t*)g.part_idx;
+    g.alive = true;
+    *lm_id = (uint32_t)c->gemvs.size();
+    c->gemvs.push_back(g);
+    return QORA_HIP_OK;
+}
+
+extern "C" int qora_hip_lm_head_run(qora_hip_ctx* c, uint32_t lm_id, const float* x, float* logits,
+                                    int32_t* argmax_device, void* stream) {
+    if (!c) return QORA_HIP_E_INVALID;
+    if (lm_id >= c->gemvs.size() || !c->gemvs[lm_id].alive) return fail(c, QORA_HIP_E_INVALID, "unknown lm_head id");
+    if (!x || !logits) return fail(c, QORA_HIP_E_INVALID, "null argument");
+    const PreparedGemv& g = c->gemvs[lm_id];
+    if (!g.lm_head) return fail(c, QORA_HIP_E_INVALID, "id was prepared by gemv_prepare: use gemv_run");
+    LmHeadParams p = g.lp;
+    p.x = x;
+    p.y = logits;
+    p.do_argmax = argmax_device != nullptr;
+    const hipStream_t s = pick_stream(c, stream);
+    HIP_TRY(c, launch_lmhead(g.lm_blocks, p, s));
+    if (argmax_device) {
+        const ArgmaxFinishParams f{p.part_val, p.part_idx, g.lm_blocks, argmax_device, nullptr, nullptr};
+        HIP_TRY(c, launch_argmax_finish(f, s));
+    }
     return QORA_HIP_OK;
 }
 

@@ -2,6 +2,7 @@
 #include "launch.hpp"
 #include "gemv.hpp"
 #include "gemv_mfma.hpp"
+#include "lmhead_mfma.hpp"
 #include "attn.hpp"
 
 #include <algorithm>
@@ -253,6 +254,59 @@ hipError_t launch_rowdot(int fmt, uint32_t blocks, const RowdotParams& p, hipStr
     const dim3 grid(blocks), block(256);
     if (fmt == FMT_Q4) hipLaunchKernelGGL((rowdot_kernel<FMT_Q4, kRowdotU>), grid, block, 0, stream, p);
     else hipLaunchKernelGGL((rowdot_kernel<FMT_F16, 4>), grid, block, 0, stream, p);
+    return hipGetLastError();
+}
+
+bool lmhead_supported(uint32_t cols) {
+    return cols == 128 || cols == 256 || cols == 512 || cols == 1024 || cols == 2048;
+}
+
+uint32_t lmhead_tiles(uint32_t rows) {
+    return (rows + 15u) / 16u;
+}
+
+uint32_t lmhead_blocks(uint32_t rows, int cus) {
+    const uint32_t tiles = lmhead_tiles(rows);
+    const int bpc = std::max(1, std::min(8, env_int("QORA_LM_BPC", 2)));   // workgroups per CU
+    const uint64_t cap = (uint64_t)std::max(1, cus) * (uint64_t)bpc;
+    return (uint32_t)std::max<uint64_t>(1, std::min<uint64_t>((tiles + 3u) / 4u, cap));
+}
+
+void lmhead_tile_bytes(uint32_t rows, uint32_t cols, uint64_t* w_bytes, uint64_t* s_bytes) {
+    const uint64_t units = (uint64_t)lmhead_tiles(rows) * (cols / 128u);
+    *w_bytes = units * 1024u;
+    *s_bytes = units * 128u;
+}
+
+hipError_t launch_lmhead_pack(const uint8_t* w, const uint16_t* scales, uint32_t rows, uint32_t cols, uint8_t* tw,
+                              uint32_t* ts, hipStream_t stream) {
+    if (rows == 0 || !lmhead_supported(cols)) return hipErrorInvalidValue;
+    const uint32_t tiles = lmhead_tiles(rows);
+    const uint64_t threads = (uint64_t)tiles * (cols / 128u) * 64u;
+    hipLaunchKernelGGL(lmhead_q4m_pack_kernel, dim3((uint32_t)((threads + 255) / 256)), dim3(256), 0, stream, w,
+                       scales, rows, cols, tiles, tw, ts);
+    return hipGetLastError();
+}
+
+hipError_t launch_lmhead(uint32_t blocks, const LmHeadParams& p, hipStream_t stream) {
+    if (p.rows == 0 || p.tiles != lmhead_tiles(p.rows) || blocks == 0) return hipErrorInvalidValue;
+    const bool fixed = p.xacc != nullptr;
+    if (fixed ? !p.gamma : !p.x) return hipErrorInvalidValue;
+    const dim3 grid(blocks), block(256);
+#define QORA_LM_CASE(COLS_, NP_)                                                                           \
+    case COLS_:                                                                                            \
+        if (fixed) hipLaunchKernelGGL((lmhead_q4m_kernel<NP_, true>), grid, block, 0, stream, p);          \
+        else hipLaunchKernelGGL((lmhead_q4m_kernel<NP_, false>), grid, block, 0, stream, p);               \
+        break;
+    switch (p.cols) {
+        QORA_LM_CASE(128, 2)
+        QORA_LM_CASE(256, 4)
+        QORA_LM_CASE(512, 8)
+        QORA_LM_CASE(1024, 16)
+        QORA_LM_CASE(2048, 32)
+        default: return hipErrorInvalidValue;
+    }
+#undef QORA_LM_CASE
     return hipGetLastError();
 }
 

@@ -56,6 +56,16 @@ uint32_t rowdot_blocks(uint32_t rows, uint32_t cols, int cus);
 hipError_t launch_rowdot(int fmt, uint32_t blocks, const RowdotParams& p, hipStream_t stream);
 hipError_t launch_argmax_finish(const ArgmaxFinishParams& p, hipStream_t stream);
 
+// Tied lm_head on the matrix cores (Q4, cols in {128, 256, 512, 1024, 2048}).
+// blocks: grid size (also the argmax partial count).
+bool lmhead_supported(uint32_t cols);
+uint32_t lmhead_tiles(uint32_t rows);
+uint32_t lmhead_blocks(uint32_t rows, int cus);
+void lmhead_tile_bytes(uint32_t rows, uint32_t cols, uint64_t* w_bytes, uint64_t* s_bytes);
+hipError_t launch_lmhead_pack(const uint8_t* w, const uint16_t* scales, uint32_t rows, uint32_t cols, uint8_t* tw,
+                              uint32_t* ts, hipStream_t stream);
+hipError_t launch_lmhead(uint32_t blocks, const LmHeadParams& p, hipStream_t stream);
+
 // Attention split geometry for up to `positions` positions: chunk is a
 // multiple of kAttnSub and s_max = ceil(positions / chunk) <= kAttnMaxSplits.
 void attn_geometry(uint32_t positions, uint32_t* chunk, uint32_t* s_max);

@@ -81,6 +81,26 @@ struct RowdotParams {
     uint32_t* part_idx;
 };
 
+// Row-dot Q4 GEMV on the matrix cores (lmhead_q4m_kernel): the tied lm_head,
+// y[r] = sum_c x[c] * W[r][c] over W [rows][cols], groups of 32 along cols.
+// Tile layout (lmhead_q4m_pack_kernel): 16 rows per tile, cols / 128
+// 16-byte units per lane:
+//   tw: [tile][unit][lane < 64] x 16 B   B fragments of column pairs 2u, 2u+1
+//   ts: [tile][unit][lane < 32] x 4 B    two f16 scales of the lane's groups
+struct LmHeadParams {
+    const uint8_t* tw;
+    const uint32_t* ts;
+    uint32_t rows, cols;       // cols = 64 * NP
+    uint32_t tiles;            // ceil(rows / 16)
+    const float* x;            // fp32 input (used as is), or
+    const long long* xacc;     // fixed-point residual with the RMSNorm prologue (when non-null)
+    const uint16_t* gamma;     // RMSNorm gamma, required with xacc
+    float* y;                  // [rows]
+    int do_argmax;
+    float* part_val;           // [gridDim.x] per-workgroup best logit
+    uint32_t* part_idx;
+};
+
 struct ArgmaxFinishParams {
     const float* part_val;
     const uint32_t* part_idx;
