@@ -111,6 +111,12 @@ int qora_hip_decode(qora_hip_ctx* ctx, uint32_t token, float* logits_or_null, ui
  * argmax of step i. */
 int qora_hip_generate_greedy(qora_hip_ctx* ctx, uint32_t token, uint32_t steps, uint32_t* tokens_out);
 
+/* How decode steps run on this context (no counterpart in the reference):
+ * 0 = no model, 1 = one captured graph of kernels per step (the default),
+ * 2 = one persistent launch per step (opt-in, QORA_HIP_DECODE=mk at
+ * model_init; Q4 weights). */
+int qora_hip_decode_mode(const qora_hip_ctx* ctx);
+
 /* RawKvCache access (gemv.rs:154-166): current length, reset to empty, and a
  * copy of one layer's [len][kv_heads][head_dim] K and V as f32. */
 int qora_hip_kv_len(qora_hip_ctx* ctx, uint64_t* len);

@@ -3,6 +3,7 @@
 #include "gemv.hpp"
 #include "gemv_mfma.hpp"
 #include "lmhead_mfma.hpp"
+#include "decode_mk.hpp"
 #include "attn.hpp"
 
 #include <algorithm>
@@ -51,7 +52,7 @@ bool plan_gemv(int fmt, uint32_t k, const uint32_t* seg_groups, int nseg, bool p
 }
 
 bool plan_gemv_q4m(uint32_t k, const uint32_t* seg_groups, int nseg, bool paired, int cus, GemvPlan* plan,
-                   uint32_t row_align) {
+                   uint32_t row_align, uint32_t force_kw) {
     if (k == 0 || nseg < 1 || nseg > 3 || row_align == 0) return false;
     if (paired && (nseg != 2 || seg_groups[0] != seg_groups[1])) return false;
     // One group (32 columns) per wave and the deepest K slice that still
@@ -60,7 +61,8 @@ bool plan_gemv_q4m(uint32_t k, const uint32_t* seg_groups, int nseg, bool paired
     // the atomics, and each streams a longer contiguous block).
     static const uint32_t kws[3] = {256, 128, 64};
     const uint32_t want = (uint32_t)std::max(1, cus);
-    const int forced_gw = env_int("QORA_GEMV_GW", 0), forced_kw = env_int("QORA_GEMV_KW", 0);
+    const int forced_gw = force_kw ? 1 : env_int("QORA_GEMV_GW", 0);
+    const int forced_kw = force_kw ? (int)force_kw : env_int("QORA_GEMV_KW", 0);
     const int gw = (forced_gw == 1 || forced_gw == 2 || forced_gw == 4) ? forced_gw : 1;
     GemvPlan best;
     bool have = false;
@@ -308,6 +310,37 @@ hipError_t launch_lmhead(uint32_t blocks, const LmHeadParams& p, hipStream_t str
     }
 #undef QORA_LM_CASE
     return hipGetLastError();
+}
+
+// Instances of the persistent decode step: (hidden, head_dim) of SmolLM3-3B
+// (2048, 128) and of the small test models (256, 64), f32 or f16 KV cache.
+static const void* decode_mk_fn(uint32_t hidden, uint32_t hd, int kv_f16) {
+    if (hidden == 2048 && hd == 128)
+        return kv_f16 ? (const void*)decode_mk_kernel<32, 2, true> : (const void*)decode_mk_kernel<32, 2, false>;
+    if (hidden == 256 && hd == 64)
+        return kv_f16 ? (const void*)decode_mk_kernel<4, 1, true> : (const void*)decode_mk_kernel<4, 1, false>;
+    return nullptr;
+}
+
+bool decode_mk_supported(uint32_t hidden, uint32_t hd) {
+    return decode_mk_fn(hidden, hd, 0) != nullptr;
+}
+
+int decode_mk_blocks_per_cu(uint32_t hidden, uint32_t hd, int kv_f16) {
+    const void* fn = decode_mk_fn(hidden, hd, kv_f16);
+    int occ = 0;
+    if (!fn || hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, kMkNT, 0) != hipSuccess) return 0;
+    return occ;
+}
+
+hipError_t launch_decode_mk(const MkParams& host, const MkParams* dev, uint32_t blocks, hipStream_t stream) {
+    const void* fn = decode_mk_fn(host.hidden, host.hd, host.kv_f16);
+    if (!fn || !dev || blocks == 0) return hipErrorInvalidValue;
+    const MkParams* arg = dev;
+    void* args[] = {&arg};
+    if (env_int("QORA_HIP_MK_COOP", 1))
+        return hipLaunchCooperativeKernel(fn, dim3(blocks), dim3(kMkNT), args, 0, stream);
+    return hipLaunchKernel(fn, dim3(blocks), dim3(kMkNT), args, 0, stream);
 }
 
 hipError_t launch_argmax_finish(const ArgmaxFinishParams& p, hipStream_t stream) {

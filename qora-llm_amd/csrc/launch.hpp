@@ -31,8 +31,10 @@ bool plan_gemv(int fmt, uint32_t k, const uint32_t* seg_groups, int nseg, bool p
 // Q4 GEMV on the matrix cores: one group per wave (QORA_GEMV_GW may force 2
 // or 4) and the deepest K slice of 256, 128 or 64 rows (QORA_GEMV_KW may
 // force one) that gives every CU a workgroup.
+// force_kw (256, 128 or 64): that K slice and one group per wave, whatever the
+// environment says (the persistent decode step needs kMkKW).
 bool plan_gemv_q4m(uint32_t k, const uint32_t* seg_groups, int nseg, bool paired, int cus, GemvPlan* plan,
-                   uint32_t row_align = 1);
+                   uint32_t row_align = 1, uint32_t force_kw = 0);
 
 // Fills seg[].tile0/tiles/col0 and p.tiles/splits/rows_per_split from the plan.
 // Concatenated segments land one after the other in the accumulator; paired
@@ -65,6 +67,12 @@ void lmhead_tile_bytes(uint32_t rows, uint32_t cols, uint64_t* w_bytes, uint64_t
 hipError_t launch_lmhead_pack(const uint8_t* w, const uint16_t* scales, uint32_t rows, uint32_t cols, uint8_t* tw,
                               uint32_t* ts, hipStream_t stream);
 hipError_t launch_lmhead(uint32_t blocks, const LmHeadParams& p, hipStream_t stream);
+
+// Persistent decode step (one cooperative launch per token).
+bool decode_mk_supported(uint32_t hidden, uint32_t hd);
+int decode_mk_blocks_per_cu(uint32_t hidden, uint32_t hd, int kv_f16);
+// host: the parameters (for dispatch); dev: the same struct in device memory.
+hipError_t launch_decode_mk(const MkParams& host, const MkParams* dev, uint32_t blocks, hipStream_t stream);
 
 // Attention split geometry for up to `positions` positions: chunk is a
 // multiple of kAttnSub and s_max = ceil(positions / chunk) <= kAttnMaxSplits.

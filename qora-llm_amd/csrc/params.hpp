@@ -101,6 +101,59 @@ struct LmHeadParams {
     uint32_t* part_idx;
 };
 
+// Persistent decode step (decode_mk_kernel, opt-in): every GEMV uses K slices of
+// kMkKW rows and one 32-column group per wave; a workgroup takes at most
+// kMkSlots items of a GEMV (a contiguous range of the split-major item order).
+constexpr int kMkKW = 256;
+constexpr int kMkSlots = 6;
+
+enum MkGemv : int { MK_QKV = 0, MK_O = 1, MK_GU = 2, MK_DOWN = 3 };
+
+struct MkLayer {
+    const uint8_t* tw[4];
+    const uint16_t* ts[4];
+    const int8_t* te[4];
+    const uint16_t* gamma[2];   // input norm, post-attention norm
+    uint8_t* kc;                // this layer's K cache [cap][KVH][hd]
+    uint8_t* vc;
+    int use_rope;
+    int pad_;
+};
+
+struct MkBufs {
+    long long* R;    // [nl + 1][hidden] residual entering layer l (R[nl]: final)
+    long long* Q;    // [nl][qkv_n]
+    long long* RP;   // [nl][hidden] residual after attention
+    long long* U;    // [nl][2 inter]
+    long long* SS;   // [nl][2] sums of squares of R[l] and RP[l]
+    uint32_t* A;     // [nl][KVH] attention items done
+};
+
+struct MkParams {
+    GemvParams g[4];           // shapes of the four GEMVs (K slice kMkKW, one group per wave)
+    const MkLayer* layers;
+    uint32_t nl, hidden, inter, H, KVH, hd, G, half, vocab;
+    uint32_t chunk, s_max;     // attention split geometry
+    int kv_f16;
+    const float* rope_cos;
+    const float* rope_sin;
+    float* part;               // attention partials [KVH][s_max][G][hd + 2]
+    MkBufs buf[2];
+    void* clear_base[2];       // each parity's buffers, one region (16-byte aligned)
+    uint64_t clear_n;          // 16-byte words per region
+    const int32_t* pos;
+    const int32_t* token;      // decode: the token of this step
+    const int32_t* prompt;     // prefill: prompt[pos]
+    const uint8_t* emb_w;      // reference-layout embedding (row lookup)
+    const uint16_t* emb_s;
+    int with_lm;
+    int residency_test;        // set-up check: count resident workgroups and exit
+    unsigned long long* trace; // optional: [workgroup][phase][3] clock stamps (enter, inputs ready, done)
+    LmHeadParams lm;           // tw, ts, rows, cols, tiles, gamma, y, part_val, part_idx
+    uint32_t* err;
+};
+
+
 struct ArgmaxFinishParams {
     const float* part_val;
     const uint32_t* part_idx;
