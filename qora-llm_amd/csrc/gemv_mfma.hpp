@@ -158,18 +158,23 @@ __device__ __forceinline__ void gemv_q4m_load_scales(const GemvParams& p, uint64
 }
 
 // Attention-merge prologue run by one wave (see attn_merge_rows) for rows
-// [r0, r1) of the slice that starts at k0 (r1 - r0 <= 32): the per-split
-// weights of each head the rows touch, then each row's merge, with lane l
-// taking row r0 + l % 32 and the splits of parity l / 32 (all of its loads
-// issued together; slots past the active splits are skipped by selection,
-// so stale bits never reach the sum). aw: LDS of kAttnMaxSplits floats per
-// head, private to the calling wave.
+// [r0, r1) of the slice that starts at k0 (r1 - r0 <= 32, so at most two
+// heads): the per-split weights of each head the rows touch, then each row's
+// merge, with lane l taking row r0 + l % 32 and the splits of parity l / 32.
+// Slots past the active splits are skipped by selection, so stale bits never
+// reach the sum. aw: LDS of kAttnMaxSplits floats per head, private to the
+// calling wave.
+// Latency: the number of active splits depends on the position, so the
+// loads that do not are issued with the position load: the running max and
+// sum of every split (lane s: split s) and the rows of the first
+// kMergeSpec splits, which cover every split of a short context; longer
+// contexts fetch the remaining rows after the position arrives.
+constexpr uint32_t kMergeSpec = 4;
+
 __device__ __forceinline__ void attn_merge_rows_wave(const GemvParams& p, uint32_t k0, uint32_t r0, uint32_t r1,
                                                      uint32_t k1, float* xs, float* aw) {
     const int lane = threadIdx.x & (kWave - 1);
     const uint32_t hd = p.head_dim, G = p.groups;
-    const uint32_t L = (uint32_t)(*p.pos) + 1u;
-    const uint32_t s_act = min(p.attn_s_max, (L + p.attn_chunk - 1) / p.attn_chunk);
     const uint64_t sstride = (uint64_t)G * (hd + 2);
     const uint32_t a0 = k0 + r0, a1 = min(k0 + r1, k1);      // absolute rows
     if (a0 >= a1) {
@@ -177,37 +182,54 @@ __device__ __forceinline__ void attn_merge_rows_wave(const GemvParams& p, uint32
         return;
     }
     const uint32_t h0 = a0 / hd;
-    const uint32_t nh = (a1 - 1) / hd - h0 + 1;
-    for (uint32_t hh = 0; hh < nh; ++hh) {
-        const uint32_t h = h0 + hh, kvh = h / G, g = h % G;
-        const float* base = p.attn_part + ((uint64_t)kvh * p.attn_s_max * G + g) * (hd + 2);
-        const uint32_t sc = min((uint32_t)lane, s_act - 1u);     // s_act <= 64 = lanes
-        const float ms = base[(uint64_t)sc * sstride + hd];
-        const float ls = base[(uint64_t)sc * sstride + hd + 1];
-        const bool ok = (uint32_t)lane < s_act;
-        const float m = wave_max(ok ? ms : -INFINITY);
-        const float w = ok ? expf(ms - m) : 0.f;
-        const float den = wave_sum(ok ? ls * w : 0.f);
-        aw[hh * kAttnMaxSplits + lane] = w / den;
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const uint32_t nh = (a1 - 1) / hd - h0 + 1;                // 1 or 2
     const uint32_t i = r0 + (uint32_t)(lane % 32);
     const uint32_t par = (uint32_t)lane / 32;
     const uint32_t r = min(k0 + i, a1 - 1u);
     const uint32_t h = r / hd, d = r % hd, hh = h - h0;
-    const float* base = p.attn_part + ((uint64_t)(h / G) * p.attn_s_max * G + (h % G)) * (hd + 2) + d;
-    const float* wrow = aw + hh * kAttnMaxSplits;
+    const float* rbase = p.attn_part + ((uint64_t)(h / G) * p.attn_s_max * G + (h % G)) * (hd + 2) + d;
+    // ---- issued together: position, every split's (m, l), the first rows ----
+    const int32_t pos_raw = *p.pos;
+    const uint32_t sl = min((uint32_t)lane, p.attn_s_max - 1u);
+    float ms[2], ls[2];
+#pragma unroll
+    for (uint32_t q = 0; q < 2; ++q) {
+        const uint32_t hq = h0 + min(q, nh - 1u);
+        const float* base = p.attn_part + ((uint64_t)(hq / G) * p.attn_s_max * G + hq % G) * (hd + 2);
+        ms[q] = base[(uint64_t)sl * sstride + hd];
+        ls[q] = base[(uint64_t)sl * sstride + hd + 1];
+    }
     float pv[kAttnMaxSplits / 2];
 #pragma unroll
-    for (int j = 0; j < kAttnMaxSplits / 2; ++j)
-        pv[j] = base[(uint64_t)min(par + 2u * j, s_act - 1u) * sstride];
+    for (uint32_t j = 0; j < kMergeSpec / 2; ++j)
+        pv[j] = rbase[(uint64_t)min(par + 2u * j, p.attn_s_max - 1u) * sstride];
+    const uint32_t L = (uint32_t)pos_raw + 1u;
+    const uint32_t s_act = min(p.attn_s_max, (L + p.attn_chunk - 1) / p.attn_chunk);
+    // ---- the remaining rows of a longer context ----
+    if (s_act > kMergeSpec) {
+#pragma unroll
+        for (uint32_t j = kMergeSpec / 2; j < kAttnMaxSplits / 2; ++j)
+            pv[j] = rbase[(uint64_t)min(par + 2u * j, s_act - 1u) * sstride];
+    }
+    const bool ok = (uint32_t)lane < s_act;
+#pragma unroll
+    for (uint32_t q = 0; q < 2; ++q) {
+        if (q < nh) {
+            const float m = wave_max(ok ? ms[q] : -INFINITY);
+            const float w = ok ? expf(ms[q] - m) : 0.f;
+            const float den = wave_sum(ok ? ls[q] * w : 0.f);
+            aw[q * kAttnMaxSplits + lane] = w / den;
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const float* wrow = aw + hh * kAttnMaxSplits;
     float v = 0.f;
 #pragma unroll
-    for (int j = 0; j < kAttnMaxSplits / 2; ++j) {
+    for (uint32_t j = 0; j < kAttnMaxSplits / 2; ++j) {
         const uint32_t sj = par + 2u * j;
-        v = sj < s_act ? fmaf(pv[j], wrow[sj], v) : v;
+        if (j < kMergeSpec / 2 || s_act > kMergeSpec) v = sj < s_act ? fmaf(pv[j], wrow[sj], v) : v;
     }
     v += __shfl_xor(v, 32, kWave);
     if (lane < 32 && i < r1) xs[i] = k0 + i < k1 ? v : 0.f;
