@@ -122,6 +122,12 @@ int qora_hip_decode_mode(const qora_hip_ctx* ctx);
 int qora_hip_kv_len(qora_hip_ctx* ctx, uint64_t* len);
 int qora_hip_kv_reset(qora_hip_ctx* ctx);
 int qora_hip_kv_download(qora_hip_ctx* ctx, uint32_t layer, float* k, float* v);
+/* The reverse of kv_download (a caller-built RawKvCache, gemv.rs:154-166):
+ * rows [0, len) of one layer's K and V from f32 [len][kv_heads][head_dim]
+ * (rounded to binary16 for an f16 cache), and the cache length set to len,
+ * so the next decode step appends at position len. Upload every layer with
+ * the same len. len <= kv_capacity (and the RoPE table length). */
+int qora_hip_kv_upload(qora_hip_ctx* ctx, uint32_t layer, const float* k, const float* v, uint64_t len);
 
 /* ---- device memory and graphs (harness plumbing) ------------------------ */
 int qora_hip_malloc(qora_hip_ctx* ctx, size_t bytes, void** dptr);

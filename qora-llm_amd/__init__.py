@@ -82,6 +82,7 @@ SIGNATURES = {
     "qora_hip_kv_len": (_I, [_P, ctypes.POINTER(_U64)]),
     "qora_hip_kv_reset": (_I, [_P]),
     "qora_hip_kv_download": (_I, [_P, _U32, _P, _P]),
+    "qora_hip_kv_upload": (_I, [_P, _U32, _P, _P, _U64]),
     "qora_hip_malloc": (_I, [_P, _SZ, ctypes.POINTER(_P)]),
     "qora_hip_free": (_I, [_P, _P]),
     "qora_hip_memcpy_h2d": (_I, [_P, _P, _P, _SZ]),
@@ -538,6 +539,16 @@ class HipBackend:
         v = np.empty((max(n, 1), kvd), dtype=np.float32)
         self.ctx.check(self.ctx.lib.qora_hip_kv_download(self.ctx.h, layer, _ptr(k), _ptr(v)), "kv_download")
         return k[:n], v[:n]
+
+    def kv_upload(self, layer: int, k: np.ndarray, v: np.ndarray) -> None:
+        """Sets one layer's cache rows [0, len) from f32 [len][kv_heads*head_dim]
+        and the cache length to len."""
+        k = np.ascontiguousarray(k, dtype=np.float32)
+        v = np.ascontiguousarray(v, dtype=np.float32)
+        if k.shape != v.shape or k.ndim != 2:
+            raise ValueError("k and v must be [len][kv_heads*head_dim]")
+        self.ctx.check(self.ctx.lib.qora_hip_kv_upload(self.ctx.h, layer, _ptr(k), _ptr(v), k.shape[0]),
+                       "kv_upload")
 
 
 def generate_greedy_host(backend: HipBackend, prompt: Sequence[int], steps: int) -> List[int]:

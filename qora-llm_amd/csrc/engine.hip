@@ -1094,6 +1094,41 @@ extern "C" int qora_hip_kv_reset(qora_hip_ctx* c) {
     return set_device_pos(c, 0);
 }
 
+extern "C" int qora_hip_kv_upload(qora_hip_ctx* c, uint32_t layer, const float* k, const float* v, uint64_t len) {
+    if (!c) return QORA_HIP_E_INVALID;
+    ModelState& m = c->m;
+    if (!m.ready) return fail(c, QORA_HIP_E_STATE, "model not initialised");
+    if (layer >= m.L) return fail(c, QORA_HIP_E_INVALID, "layer out of range");
+    if (len > m.cap) return fail(c, QORA_HIP_E_INVALID, "len beyond the KV capacity");
+    if (m.any_rope && len > m.rope_positions) return fail(c, QORA_HIP_E_INVALID, "len beyond the RoPE tables");
+    if (len && (!k || !v)) return fail(c, QORA_HIP_E_INVALID, "null argument");
+    if (c->capturing) return fail(c, QORA_HIP_E_STATE, "kv_upload is not allowed during capture");
+    const size_t kvd = (size_t)m.KVH * m.hd;
+    const size_t count = (size_t)len * kvd;
+    if (count) {
+        if (!m.kv_f16) {
+            HIP_TRY(c, hipMemcpy((float*)m.d_k + (size_t)layer * m.cap * kvd, k, count * 4, hipMemcpyHostToDevice));
+            HIP_TRY(c, hipMemcpy((float*)m.d_v + (size_t)layer * m.cap * kvd, v, count * 4, hipMemcpyHostToDevice));
+        } else {
+            void* tmp = nullptr;
+            if (int rc = dalloc(c, count * 4, &tmp)) return rc;
+            const float* src[2] = {k, v};
+            uint16_t* dst[2] = {(uint16_t*)m.d_k + (size_t)layer * m.cap * kvd,
+                                (uint16_t*)m.d_v + (size_t)layer * m.cap * kvd};
+            hipError_t e = hipSuccess;
+            for (int i = 0; i < 2 && e == hipSuccess; ++i) {
+                e = hipMemcpy(tmp, src[i], count * 4, hipMemcpyHostToDevice);
+                if (e == hipSuccess) e = launch_f32_to_f16((const float*)tmp, dst[i], count, c->stream);
+                if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+            }
+            (void)hipFree(tmp);
+            if (e != hipSuccess) return fail(c, QORA_HIP_E_DEVICE, std::string("kv_upload: ") + hipGetErrorString(e));
+        }
+    }
+    m.host_pos = len;
+    return set_device_pos(c, len);
+}
+
 extern "C" int qora_hip_kv_download(qora_hip_ctx* c, uint32_t layer, float* k, float* v) {
     if (!c || !k || !v) return fail(c, QORA_HIP_E_INVALID, "null argument");
     ModelState& m = c->m;

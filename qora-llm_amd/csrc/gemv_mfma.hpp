@@ -250,7 +250,7 @@ __global__ __launch_bounds__(PRO == PRO_ATTN ? 512 : 320) void gemv_q4m_kernel(G
     constexpr int RPW = KW / 64;            // prologue rows per lane
     constexpr int MAXH = KW / 32 + 1;       // heads a slice can touch (head_dim >= 32)
     constexpr bool kAttn = PRO == PRO_ATTN;
-    static_assert(KW % 64 == 0 && KW <= 256, "slice of 64..256 rows");
+    static_assert(KW % 64 == 0 && KW <= 512, "slice of 64..512 rows");
     __shared__ __align__(16) float xs[KW];
     __shared__ float wred[2][NPW];
     __shared__ __align__(16) uint8_t zl[NW][GW][4][KW];   // limb bytes: [wave][group][limb][row]
@@ -406,9 +406,16 @@ __global__ __launch_bounds__(PRO == PRO_ATTN ? 512 : 320) void gemv_q4m_kernel(G
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
                 const v4i32 c = acc[2 * g + h];
-                const int lo = c[0] + (c[1] << 8);
-                const int hi = c[2] + (c[3] << 8);
-                const long long Y = (long long)lo + ((long long)hi << 16);
+                // |C| < 2^22 for 256 rows: each half fits int32; 512 rows need 64 bits
+                long long lo, hi;
+                if constexpr (KW <= 256) {
+                    lo = c[0] + (c[1] << 8);
+                    hi = c[2] + (c[3] << 8);
+                } else {
+                    lo = (long long)c[0] + ((long long)c[1] << 8);
+                    hi = (long long)c[2] + ((long long)c[3] << 8);
+                }
+                const long long Y = lo + (hi << 16);
                 const long long f = ((Y + rnd) >> rsh) << lsh;
                 atomicAdd(reinterpret_cast<unsigned long long*>(dst + h * 16), (unsigned long long)f);
             }

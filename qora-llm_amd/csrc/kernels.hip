@@ -64,6 +64,25 @@ bool plan_gemv_q4m(uint32_t k, const uint32_t* seg_groups, int nseg, bool paired
     const int forced_gw = force_kw ? 1 : env_int("QORA_GEMV_GW", 0);
     const int forced_kw = force_kw ? (int)force_kw : env_int("QORA_GEMV_KW", 0);
     const int gw = (forced_gw == 1 || forced_gw == 2 || forced_gw == 4) ? forced_gw : 1;
+    if (forced_kw == 512) {
+        // 512-row slices (one group per wave), only when asked for
+        if (gw != 1 || row_align > 512 || 512 % row_align != 0) return false;
+        GemvPlan pl;
+        pl.mfma = 1;
+        pl.gw = 1;
+        pl.gt = 4;
+        pl.rpl = 0;
+        if (paired) {
+            pl.tiles = (seg_groups[0] + 1) / 2;
+        } else {
+            pl.tiles = 0;
+            for (int i = 0; i < nseg; ++i) pl.tiles += (seg_groups[i] + 3) / 4;
+        }
+        pl.kr = 512;
+        pl.splits = (k + 511) / 512;
+        *plan = pl;
+        return true;
+    }
     GemvPlan best;
     bool have = false;
     for (uint32_t kw : kws) {
@@ -166,6 +185,9 @@ static hipError_t launch_q4m_gw(const GemvPlan& plan, const GemvParams& p, hipSt
     case 64: return launch_q4m_kw<GW, 64>(plan, p, stream);
     case 128: return launch_q4m_kw<GW, 128>(plan, p, stream);
     case 256: return launch_q4m_kw<GW, 256>(plan, p, stream);
+    case 512:
+        if constexpr (GW == 1) return launch_q4m_kw<1, 512>(plan, p, stream);
+        else return hipErrorInvalidValue;
     default: return hipErrorInvalidValue;
     }
 }
@@ -226,6 +248,18 @@ hipError_t launch_gemv_tile(int fmt, const GemvPlan& plan, const GemvParams& p, 
         hipLaunchKernelGGL(gemv_tile_kernel<FMT_F16>, dim3((uint32_t)grid), dim3(256), 0, stream, p, plan.gt,
                            plan.rpl, tw, ts);
     }
+    return hipGetLastError();
+}
+
+__global__ __launch_bounds__(256) void f32_to_f16_kernel(const float* src, uint16_t* dst, uint64_t n) {
+    for (uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x; i < n; i += (uint64_t)gridDim.x * 256u)
+        dst[i] = f2h(src[i]);
+}
+
+hipError_t launch_f32_to_f16(const float* src, uint16_t* dst, uint64_t n, hipStream_t stream) {
+    if (n == 0) return hipSuccess;
+    const uint32_t blocks = (uint32_t)std::min<uint64_t>(4096, (n + 255) / 256);
+    hipLaunchKernelGGL(f32_to_f16_kernel, dim3(blocks), dim3(256), 0, stream, src, dst, n);
     return hipGetLastError();
 }
 

@@ -51,6 +51,8 @@ void gemv_tile_bytes(int fmt, const GemvPlan& plan, uint64_t* w_bytes, uint64_t*
 hipError_t launch_gemv_tile(int fmt, const GemvPlan& plan, const GemvParams& p, uint8_t* tw, uint16_t* ts,
                             int8_t* te, hipStream_t stream);
 hipError_t launch_fill_zero(long long* p, uint64_t n, hipStream_t stream);
+// dst[i] = binary16(src[i]), round to nearest even
+hipError_t launch_f32_to_f16(const float* src, uint16_t* dst, uint64_t n, hipStream_t stream);
 hipError_t launch_acc_to_f32(const long long* acc, uint32_t n, int paired, float* y, hipStream_t stream);
 
 // Row-dot GEMV (lm_head). blocks: grid size (also the argmax partial count).

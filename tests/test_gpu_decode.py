@@ -124,3 +124,57 @@ def test_qora_file_roundtrip_loads_same_model(ctx, pkg, tmp_path):
     ctx.check(ctx.lib.qora_hip_prefill(ctx.h, ids.ctypes.data, ids.size, logits.ctypes.data, ctypes.byref(tok)),
               "prefill")
     assert np.array_equal(logits, ref)
+
+
+@pytest.mark.parametrize("kv_dtype", [0, 1])
+def test_kv_upload_round_trip_is_bit_exact(ctx, pkg, kv_dtype):
+    """kv_download -> kv_reset -> kv_upload restores the cache exactly: the next
+    decode step gives the same logits, bit for bit, as without the round trip."""
+    w = small_model(pkg, 1)
+    L = w.config.num_layers
+    prompt = pkg.synth_tokens(0, 2000, 21, w.config.vocab)
+    be = pkg.HipBackend(ctx, w, kv_capacity=128, kv_dtype=kv_dtype)
+    be.raw_prefill(prompt, want_logits=False)
+    saved = [be.kv_layer(l) for l in range(L)]
+    want, wtok = be.forward_decode_raw(77)
+    be.kv_reset()
+    for l, (k, v) in enumerate(saved):
+        be.kv_upload(l, k, v)
+    assert be.kv_len() == len(prompt)
+    got, gtok = be.forward_decode_raw(77)
+    assert np.array_equal(got, want) and gtok == wtok
+    assert be.kv_len() == len(prompt) + 1
+
+
+def test_kv_upload_rounds_to_f16_nearest_even(ctx, pkg):
+    w = small_model(pkg, 1)
+    kvd = w.config.num_kv_heads * w.config.head_dim
+    be = pkg.HipBackend(ctx, w, kv_capacity=64, kv_dtype=pkg.KV_F16)
+    r = np.random.default_rng(5)
+    k = (r.standard_normal((40, kvd)) * np.exp2(r.integers(-20, 17, (40, kvd)))).astype(np.float32)
+    k[0, :4] = [65519.0, 65520.0, -1e9, 2.0 ** -25]    # largest finite, overflow, underflow to zero
+    v = r.standard_normal((40, kvd)).astype(np.float32)
+    be.kv_upload(2, k, v)
+    gk, gv = be.kv_layer(2)
+    with np.errstate(over="ignore"):
+        assert np.array_equal(gk, k.astype(np.float16).astype(np.float32))
+    assert np.array_equal(gv, v.astype(np.float16).astype(np.float32))
+    be.kv_upload(2, k[:0], v[:0])
+    assert be.kv_len() == 0
+
+
+def test_kv_upload_errors(ctx, pkg):
+    w = small_model(pkg, 1)
+    kvd = w.config.num_kv_heads * w.config.head_dim
+    be = pkg.HipBackend(ctx, w, kv_capacity=16)
+    z = np.zeros((17, kvd), np.float32)
+    with pytest.raises(pkg.QoraHipError):
+        be.kv_upload(0, z, z)                       # beyond the capacity
+    with pytest.raises(pkg.QoraHipError):
+        be.kv_upload(w.config.num_layers, z[:4], z[:4])
+    with pytest.raises(pkg.QoraHipError):
+        ctx.check(ctx.lib.qora_hip_kv_upload(ctx.h, 0, None, None, 3), "kv_upload")
+    be.kv_upload(0, z[:16], z[:16])
+    with pytest.raises(pkg.QoraHipError) as e:
+        be.forward_decode_raw(1)                    # cache full
+    assert e.value.code == pkg.QORA_HIP_E_STATE
