@@ -542,6 +542,16 @@ uint64_t oq_kv_len(const oq_kv* kv, uint32_t layer) { return kv->len[layer]; }
 const float* oq_kv_k(const oq_kv* kv, uint32_t layer) { return kv->k[layer]; }
 const float* oq_kv_v(const oq_kv* kv, uint32_t layer) { return kv->v[layer]; }
 
+/* A caller-built RawKvCache entry (gemv.rs:154-166): rows [0, len) of one
+ * layer, token-major [len][kv_stride]. */
+int oq_kv_set(oq_kv* kv, uint32_t layer, const float* k, const float* v, uint64_t len) {
+    if (layer >= kv->num_layers || len > kv->capacity) return -1;
+    memcpy(kv->k[layer], k, len * kv->kv_stride * sizeof(float));
+    memcpy(kv->v[layer], v, len * kv->kv_stride * sizeof(float));
+    kv->len[layer] = len;
+    return 0;
+}
+
 enum { W_Q = 0, W_K, W_V, W_O, W_GATE, W_UP, W_DOWN };
 
 typedef struct { uint64_t k, n; } shape_t;

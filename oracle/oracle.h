@@ -126,6 +126,7 @@ void oq_kv_free(oq_kv* kv);
 uint64_t oq_kv_len(const oq_kv* kv, uint32_t layer);
 const float* oq_kv_k(const oq_kv* kv, uint32_t layer);
 const float* oq_kv_v(const oq_kv* kv, uint32_t layer);
+int oq_kv_set(oq_kv* kv, uint32_t layer, const float* k, const float* v, uint64_t len);
 
 /* forward_decode_raw (gemv.rs:872-1019). T = rayon thread count. Returns 0
  * on success, -1 if the cache is full. logits: [vocab]. */

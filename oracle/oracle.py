@@ -55,6 +55,7 @@ _SIGS = {
     "oq_kv_len": (_U64, [_P, _U32]),
     "oq_kv_k": (_P, [_P, _U32]),
     "oq_kv_v": (_P, [_P, _U32]),
+    "oq_kv_set": (_I, [_P, _U32, _P, _P, _U64]),
     "oq_forward_decode": (_I, [ctypes.POINTER(OqModelDesc), _P, _U32, _I, _I, _P]),
     "oq_prefill": (_I, [ctypes.POINTER(OqModelDesc), _P, _P, _U64, _I, _P]),
     "oq_set_threads": (None, [_I]),
@@ -258,6 +259,13 @@ class OracleModel:
         k = np.ctypeslib.as_array((ctypes.c_float * (n * kvd)).from_address(kp)).reshape(n, kvd).copy()
         v = np.ctypeslib.as_array((ctypes.c_float * (n * kvd)).from_address(vp)).reshape(n, kvd).copy()
         return k, v
+
+    def kv_set(self, layer, k, v):
+        """Sets one layer's cache rows [0, len) from f32 [len][kv_heads*head_dim]."""
+        k = np.ascontiguousarray(k, dtype=np.float32)
+        v = np.ascontiguousarray(v, dtype=np.float32)
+        if lib().oq_kv_set(self.kv, layer, _p(k), _p(v), k.shape[0]) != 0:
+            raise RuntimeError("oracle kv_set: bad layer or beyond the capacity")
 
     def greedy(self, prompt, steps):
         """Prefill then `steps` greedy tokens (generate_raw with temperature 0)."""

@@ -3,6 +3,8 @@
 // argmax used by the kernel-level entry points.
 #pragma once
 
+#include <type_traits>
+
 #include "common.hpp"
 #include "params.hpp"
 
@@ -35,21 +37,21 @@ __device__ __forceinline__ uint32_t rope_partner(uint32_t d, uint32_t half) {
     return d < half ? d + half : (d < 2 * half ? d - half : d);
 }
 
-// K and V float4s of one 32-position tile held by one thread (thread t takes
-// float4 e = t + 256*j of the [32][head_dim/4] tile).
+// K and V float4s of one 32-position tile held by one thread (thread t of the
+// 256-thread subgroup takes float4 e = t + 256*j of the [32][head_dim/4] tile).
 template <int TL>
 struct KvTileRegs {
     float4 k[TL], v[TL];
 };
 
 template <int TL, bool F16KV>
-__device__ __forceinline__ KvTileRegs<TL> attn_load_tile(const AttnParams& p, uint32_t c0, uint32_t L,
+__device__ __forceinline__ KvTileRegs<TL> attn_load_tile(const AttnParams& p, uint32_t t, uint32_t c0, uint32_t L,
                                                           uint64_t kv_stride, uint64_t head_off, uint32_t q4_row,
                                                           uint32_t tile_n) {
     KvTileRegs<TL> r;
 #pragma unroll
     for (int j = 0; j < TL; ++j) {
-        const uint32_t e = min(threadIdx.x + (uint32_t)(256 * j), tile_n - 1u);
+        const uint32_t e = min(t + (uint32_t)(256 * j), tile_n - 1u);
         const uint32_t row = e / q4_row, c4 = e % q4_row;
         const uint32_t pos = min(c0 + row, L - 1u);
         const uint64_t idx = (uint64_t)pos * kv_stride + head_off + 4u * c4;
@@ -72,11 +74,11 @@ __device__ __forceinline__ KvTileRegs<TL> attn_load_tile(const AttnParams& p, ui
 // whatever stale bits the unwritten slots hold); row `skip` (the appended
 // position, or >= 32 for none) is left to its writer.
 template <int TL, int KSTR, int VSTR>
-__device__ __forceinline__ void attn_store_tile(const KvTileRegs<TL>& r, float* ktile, float* vtile, uint32_t cn,
-                                                uint32_t skip, uint32_t q4_row, uint32_t tile_n) {
+__device__ __forceinline__ void attn_store_tile(const KvTileRegs<TL>& r, uint32_t t, float* ktile, float* vtile,
+                                                uint32_t cn, uint32_t skip, uint32_t q4_row, uint32_t tile_n) {
 #pragma unroll
     for (int j = 0; j < TL; ++j) {
-        const uint32_t e = threadIdx.x + (uint32_t)(256 * j);
+        const uint32_t e = t + (uint32_t)(256 * j);
         const uint32_t row = e / q4_row, c4 = e % q4_row;
         if (e < tile_n && row != skip) {
             const uint32_t msk = row < cn ? 0xFFFFFFFFu : 0u;
@@ -105,6 +107,9 @@ __device__ __forceinline__ void attn_store_tile(const KvTileRegs<TL>& r, float* 
 // tile and RoPE tables follow as soon as the position arrives. q and the K
 // rows are zero-padded to HDM dims in LDS so the dot products run without
 // predicates. DPL = 2 covers head_dim <= 128, DPL = 1 head_dim <= 64.
+// chunk = p.chunk, or attn_chunk_for(L) when 0 (the split count then stays
+// within kAttnMaxSplits at every context length). Contexts whose splits hold
+// many passes take attn_decode_long_kernel instead.
 template <int DPL, bool F16KV>
 __global__ __launch_bounds__(256) void attn_decode_kernel(AttnParams p) {
     constexpr int NT = 256;
@@ -152,9 +157,10 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnParams p) {
     }
 
     const uint32_t L = (uint32_t)pos_raw + 1u;
-    const uint32_t p0 = split * p.chunk;
+    const uint32_t chunk = p.chunk ? p.chunk : attn_chunk_for(L);
+    const uint32_t p0 = split * chunk;
     if (p0 >= L) return;
-    const uint32_t p1 = min(L, p0 + p.chunk);
+    const uint32_t p1 = min(L, p0 + chunk);
     const uint32_t cur = L - 1;                        // position appended this step
     const bool has_new = model && cur >= p0 && cur < p1;
     const uint32_t q4_row = hd / 4;                    // float4 per row
@@ -176,7 +182,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnParams p) {
         kc_ = ct[td];
         ks_ = st[td];
     }
-    KvTileRegs<TL> tr = attn_load_tile<TL, F16KV>(p, p0, L, kv_stride, head_off, q4_row, tile_n);
+    KvTileRegs<TL> tr = attn_load_tile<TL, F16KV>(p, threadIdx.x, p0, L, kv_stride, head_off, q4_row, tile_n);
 
     // K padding columns [hd, HDM) stay zero for the whole kernel
     if (hd < (uint32_t)HDM)
@@ -243,14 +249,14 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnParams p) {
     for (uint32_t c0 = p0; c0 < p1; c0 += SUB) {
         const uint32_t cn = min((uint32_t)SUB, p1 - c0);
         const bool new_here = has_new && cur >= c0 && cur < c0 + cn;
-        attn_store_tile<TL, KSTR, VSTR>(tr, ktile, vtile, cn, new_here ? cur - c0 : 0xFFFFFFFFu, q4_row, tile_n);
+        attn_store_tile<TL, KSTR, VSTR>(tr, threadIdx.x, ktile, vtile, cn, new_here ? cur - c0 : 0xFFFFFFFFu, q4_row, tile_n);
         if (new_here && (uint32_t)t < hd) {
             ktile[(cur - c0) * KSTR + t] = k_app;
             vtile[(cur - c0) * VSTR + t] = v_app;
         }
         __syncthreads();
         if (c0 + SUB < p1)                            // next pass, in flight during this one
-            tr = attn_load_tile<TL, F16KV>(p, c0 + SUB, L, kv_stride, head_off, q4_row, tile_n);
+            tr = attn_load_tile<TL, F16KV>(p, threadIdx.x, c0 + SUB, L, kv_stride, head_off, q4_row, tile_n);
         if (g < G) {
             // q.k for position c0 + r_lane over padded dims [dq0, dq0 + HDM/2)
             const float* qg = qs + g * HDM + dq0;
@@ -312,6 +318,358 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnParams p) {
     }
 }
 
+// Raw cache words of one 32-position tile as loaded (binary16 quads or fp32
+// float4s), converted to fp32 only when stored to LDS: an f16 tile then costs
+// 16 VGPRs instead of 32, so two tiles can be in flight per subgroup.
+template <int TL, bool F16KV>
+struct KvRaw {
+    using W = typename std::conditional<F16KV, uint2, float4>::type;
+    W k[TL], v[TL];
+};
+
+template <int TL, bool F16KV>
+__device__ __forceinline__ void attn_load_raw(KvRaw<TL, F16KV>& r, const AttnParams& p, uint32_t t, uint32_t c0,
+                                              uint32_t L, uint64_t kv_stride, uint64_t head_off, uint32_t q4_row,
+                                              uint32_t tile_n) {
+    using W = typename KvRaw<TL, F16KV>::W;
+    constexpr uint32_t wb = F16KV ? 2u : 4u;   // bytes per element
+#pragma unroll
+    for (int j = 0; j < TL; ++j) {
+        const uint32_t e = min(t + (uint32_t)(256 * j), tile_n - 1u);
+        const uint32_t row = e / q4_row, c4 = e % q4_row;
+        const uint32_t pos = min(c0 + row, L - 1u);
+        const uint64_t off = ((uint64_t)pos * kv_stride + head_off + 4u * c4) * wb;
+        r.k[j] = *reinterpret_cast<const W*>(reinterpret_cast<const uint8_t*>(p.kc) + off);
+        r.v[j] = *reinterpret_cast<const W*>(reinterpret_cast<const uint8_t*>(p.vc) + off);
+    }
+}
+
+__device__ __forceinline__ float4 kv_words_f32(uint2 a) {
+    return make_float4(h2f((uint16_t)(a.x & 0xFFFFu)), h2f((uint16_t)(a.x >> 16)), h2f((uint16_t)(a.y & 0xFFFFu)),
+                       h2f((uint16_t)(a.y >> 16)));
+}
+__device__ __forceinline__ float4 kv_words_f32(float4 a) { return a; }
+
+// As attn_store_tile, from raw words.
+template <int TL, bool F16KV, int KSTR, int VSTR>
+__device__ __forceinline__ void attn_store_raw(const KvRaw<TL, F16KV>& r, uint32_t t, float* ktile, float* vtile,
+                                               uint32_t cn, uint32_t skip, uint32_t q4_row, uint32_t tile_n) {
+#pragma unroll
+    for (int j = 0; j < TL; ++j) {
+        const uint32_t e = t + (uint32_t)(256 * j);
+        const uint32_t row = e / q4_row, c4 = e % q4_row;
+        if (e < tile_n && row != skip) {
+            const uint32_t msk = row < cn ? 0xFFFFFFFFu : 0u;
+            const float4 kf = kv_words_f32(r.k[j]), vf = kv_words_f32(r.v[j]);
+            const uint4 kb = make_uint4(__float_as_uint(kf.x) & msk, __float_as_uint(kf.y) & msk,
+                                        __float_as_uint(kf.z) & msk, __float_as_uint(kf.w) & msk);
+            const uint4 vb = make_uint4(__float_as_uint(vf.x) & msk, __float_as_uint(vf.y) & msk,
+                                        __float_as_uint(vf.z) & msk, __float_as_uint(vf.w) & msk);
+            *reinterpret_cast<uint4*>(ktile + row * KSTR + 4 * c4) = kb;
+            *reinterpret_cast<uint4*>(vtile + row * VSTR + 4 * c4) = vb;
+        }
+    }
+}
+
+// Long contexts: the same computation with each block's passes split among
+// NSG = 4 subgroups of 256 threads (subgroup sg takes passes sg, sg + NSG, ...).
+// Each pass's K and V rows are loaded once with coalesced 16-byte loads
+// (256 lanes, 4 KB per instruction) and staged in the subgroup's LDS tiles as
+// fp32; rows past the pass are stored as zeros. The subgroup's next pass is
+// prefetched into registers (raw cache words) while the current one is
+// computed, so 4 tiles per block are in flight: a split of a long context
+// holds many passes, and one tile in flight per block leaves HBM idle. One wave per
+// query head then takes its scores from the K tile (lanes (half, r) =
+// (lane / 32, lane % 32): position r, half of the dims), runs the online
+// softmax and accumulates p.V from the V tile (DPL dims per lane). The
+// subgroups' (max, sum, p.V) states are merged in LDS, in subgroup order.
+// In model mode the appended position's K/V row is computed here (RMSNorm
+// factor, RoPE), written to the cache and put into the tile directly.
+// Latency: the loads that do not depend on the position (q|k|v sums,
+// RMSNorm partials) are issued together with the position load; the cache
+// tile and RoPE tables follow as soon as the position arrives. q and the K
+// rows are zero-padded to HDM dims in LDS so the dot products run without
+// predicates. DPL = 2 covers head_dim <= 128, DPL = 1 head_dim <= 64.
+// chunk = p.chunk, or attn_chunk_for(L) when 0 (the split count then stays
+// within kAttnMaxSplits at every context length).
+constexpr int kAttnLongNsg = 4;
+
+template <int DPL, bool F16KV>
+__global__ __launch_bounds__(256 * kAttnLongNsg) void attn_decode_long_kernel(AttnParams p) {
+    constexpr int NSG = kAttnLongNsg;
+    constexpr int NT = 256;                          // threads per subgroup
+    constexpr int SUB = kAttnSub;                    // positions per pass (32)
+    constexpr int HDM = 64 * DPL;                    // head_dim bound of this instance
+    constexpr int KQ = HDM / 8;                      // float4 chunks per lane for q.k (half of HDM)
+    constexpr int KSTR = HDM + 4;                    // padded K row stride (floats): no bank conflicts
+    constexpr int VSTR = HDM;
+    constexpr int TL = SUB * HDM / 4 / NT;           // float4 per thread per tile
+    constexpr int QC = 4;
+    static_assert(NSG * SUB * KSTR >= NSG * kAttnMaxGroups * HDM, "merge scratch must fit in the K tiles");
+    __shared__ __align__(16) float ktile[NSG][SUB * KSTR];
+    __shared__ __align__(16) float vtile[NSG][SUB * VSTR];
+    __shared__ __align__(16) float qs[kAttnMaxGroups * HDM];
+    __shared__ float es[NSG][kAttnMaxGroups * SUB];
+    __shared__ float knew[HDM], vnew[HDM];
+    __shared__ float red_m[NSG][kAttnMaxGroups], red_l[NSG][kAttnMaxGroups];
+
+    const int t = (int)(threadIdx.x % NT);           // thread within the subgroup
+    // wave-uniform (a scalar register), so the pass bookkeeping stays scalar
+    const int sg = __builtin_amdgcn_readfirstlane(threadIdx.x / NT);
+    const int lane = t & (kWave - 1);
+    const int wave = t / kWave;
+    const uint32_t split = blockIdx.x;
+    const uint32_t kvh = blockIdx.y;
+    const uint32_t hd = p.hd, G = p.groups;
+    const bool model = p.qkv_acc != nullptr;
+    const bool lead = sg == 0;                       // subgroup 0 sets up q and the appended row
+    const uint64_t kv_stride = (uint64_t)p.KVH * hd;
+    const uint64_t head_off = (uint64_t)kvh * hd;
+    const uint32_t nq = G * hd;
+
+    // ---- position-independent loads, in flight with the position ----
+    const int32_t pos_raw = p.pos ? *p.pos : (int32_t)p.L - 1;
+    long long qa[2] = {0, 0}, qb[2] = {0, 0};
+    long long ka = 0, kb = 0, va = 0;
+    float ssp = 0.f;
+    const uint32_t dn = min((uint32_t)t, hd - 1u);
+    if (model && lead) {
+        const uint32_t qd = p.H * hd;
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const uint32_t i = min((uint32_t)t + (uint32_t)u * NT, nq - 1u);
+            const uint32_t d = i % hd;
+            qa[u] = p.qkv_acc[(uint64_t)kvh * G * hd + i];
+            qb[u] = p.qkv_acc[(uint64_t)kvh * G * hd + (i - d) + rope_partner(d, p.half)];
+        }
+        ka = p.qkv_acc[qd + head_off + dn];
+        kb = p.qkv_acc[qd + head_off + rope_partner(dn, p.half)];
+        va = p.qkv_acc[qd + kv_stride + head_off + dn];
+        ssp = p.ss_in[min((uint32_t)lane, p.ss_n - 1u)];
+    }
+
+    const uint32_t L = (uint32_t)pos_raw + 1u;
+    const uint32_t chunk = p.chunk ? p.chunk : attn_chunk_for(L);
+    const uint32_t p0 = split * chunk;
+    if (p0 >= L) return;                               // whole block: no barrier reached yet
+    const uint32_t p1 = min(L, p0 + chunk);
+    const uint32_t cur = L - 1;                        // position appended this step
+    const bool has_new = model && cur >= p0 && cur < p1;
+    const uint32_t q4_row = hd / 4;                    // float4 per row
+    const uint32_t tile_n = SUB * q4_row;              // float4 per tile
+    const uint32_t npass = (p1 - p0 + SUB - 1) / SUB;
+    const uint32_t iters = (npass + NSG - 1) / NSG;
+
+    // ---- position-dependent loads: RoPE entries of `cur`, first cache tile ----
+    float qc[2] = {1.f, 1.f}, qsn[2] = {0.f, 0.f}, kc_ = 1.f, ks_ = 0.f;
+    if (model && lead && p.use_rope) {
+        const float* ct = p.rope_cos + (uint64_t)cur * p.half;
+        const float* st = p.rope_sin + (uint64_t)cur * p.half;
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const uint32_t d = min((uint32_t)t + (uint32_t)u * NT, nq - 1u) % hd;
+            const uint32_t td = d < p.half ? d : (d < 2 * p.half ? d - p.half : 0u);
+            qc[u] = ct[td];
+            qsn[u] = st[td];
+        }
+        const uint32_t td = dn < p.half ? dn : (dn < 2 * p.half ? dn - p.half : 0u);
+        kc_ = ct[td];
+        ks_ = st[td];
+    }
+    // passes in flight per subgroup; 2 (an f16 tile is 16 VGPRs raw) measured
+    // no faster at 32768 positions: the LDS traffic of the q.k and p.V loops,
+    // not HBM latency, is then what bounds the kernel
+    constexpr int DEPTH = 1;
+    KvRaw<TL, F16KV> tr[DEPTH];
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d)
+        if ((uint32_t)sg + (uint32_t)(d * NSG) < npass)
+            attn_load_raw<TL, F16KV>(tr[d], p, t, p0 + ((uint32_t)sg + (uint32_t)(d * NSG)) * SUB, L, kv_stride,
+                                     head_off, q4_row, tile_n);
+
+    // K padding columns [hd, HDM) stay zero for the whole kernel
+    if (hd < (uint32_t)HDM)
+        for (uint32_t e = t; e < SUB * ((uint32_t)HDM - hd); e += NT)
+            ktile[sg][(e / ((uint32_t)HDM - hd)) * KSTR + hd + e % ((uint32_t)HDM - hd)] = 0.f;
+
+    // ---- q of the group's heads (and the appended k, v) ----
+    if (model && lead) {
+        // the q|k|v GEMV ran on x * gamma; its RMSNorm factor is applied here
+        const float inv = 1.0f / sqrtf(wave_sum(lane < (int)p.ss_n ? ssp : 0.f) / (float)p.norm_n + 1e-6f);
+        const bool rot = p.use_rope != 0;
+        // padding dims [hd, HDM) of each q row are zero
+        for (uint32_t i = t; i < G * HDM; i += NT)
+            if (i % HDM >= hd) qs[i] = 0.f;
+        // q values: thread t owns flat index i = t + 256u of [G][hd]
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const uint32_t i = (uint32_t)t + (uint32_t)u * NT;
+            if (i < nq) {
+                const uint32_t d = i % hd;
+                const float a = inv * from_fixed(qa[u]), b = inv * from_fixed(qb[u]);
+                // rotate_half: the first half takes -partner * sin, the second +partner * sin
+                qs[(i / hd) * HDM + d] = (rot && d < 2 * p.half) ? (d < p.half ? a * qc[u] - b * qsn[u]
+                                                                                 : a * qc[u] + b * qsn[u])
+                                                                  : a;
+            }
+        }
+        if (has_new && (uint32_t)t < hd) {
+            const float a = inv * from_fixed(ka), b = inv * from_fixed(kb);
+            float kv = (rot && dn < 2 * p.half) ? (dn < p.half ? a * kc_ - b * ks_ : a * kc_ + b * ks_) : a;
+            float vv = inv * from_fixed(va);
+            const uint64_t idx = (uint64_t)cur * kv_stride + head_off + dn;
+            if constexpr (F16KV) {
+                const uint16_t kh = f2h(kv), vh = f2h(vv);
+                reinterpret_cast<uint16_t*>(p.kc)[idx] = kh;
+                reinterpret_cast<uint16_t*>(p.vc)[idx] = vh;
+                kv = h2f(kh);   // use the stored value, as later steps will
+                vv = h2f(vh);
+            } else {
+                reinterpret_cast<float*>(p.kc)[idx] = kv;
+                reinterpret_cast<float*>(p.vc)[idx] = vv;
+            }
+            knew[t] = kv;
+            vnew[t] = vv;
+        }
+    } else if (lead) {
+        for (uint32_t i = t; i < G * HDM; i += NT) {
+            const uint32_t g = i / HDM, d = i % HDM;
+            qs[i] = d < hd ? p.q[(uint64_t)(kvh * G + g) * hd + d] : 0.f;
+        }
+    }
+    __syncthreads();                                 // qs, knew, vnew
+
+    const uint32_t g = (uint32_t)wave;
+    const uint32_t half_id = (uint32_t)lane / 32, r_lane = (uint32_t)lane % 32;
+    const uint32_t dq0 = half_id * (HDM / 2);
+    const uint32_t dv0c = min((uint32_t)lane * DPL, hd - DPL);   // clamped V dims of this lane
+    const bool vlane = (uint32_t)lane * DPL < hd;
+    float* kt = ktile[sg];
+    float* vt = vtile[sg];
+    float* et = es[sg];
+    float m = -INFINITY, l = 0.f;
+    float acc[DPL];
+#pragma unroll
+    for (int i = 0; i < DPL; ++i) acc[i] = 0.f;
+
+    // one pass of this subgroup, from the raw tile `rt` (refilled with the pass
+    // DEPTH rounds ahead once its words are in LDS)
+    auto pass = [&](KvRaw<TL, F16KV>& rt, uint32_t it) {
+        const uint32_t pi = it * NSG + (uint32_t)sg;   // this subgroup's pass
+        const bool active = pi < npass;
+        const uint32_t c0 = p0 + pi * SUB;
+        const uint32_t cn = active ? min((uint32_t)SUB, p1 - c0) : 0u;
+        if (active) {
+            const bool new_here = has_new && cur >= c0 && cur < c0 + cn;
+            attn_store_raw<TL, F16KV, KSTR, VSTR>(rt, t, kt, vt, cn, new_here ? cur - c0 : 0xFFFFFFFFu, q4_row, tile_n);
+            if (new_here && (uint32_t)t < hd) {
+                kt[(cur - c0) * KSTR + t] = knew[t];
+                vt[(cur - c0) * VSTR + t] = vnew[t];
+            }
+        }
+        __syncthreads();
+        if (pi + DEPTH * NSG < npass)                  // in flight during the next DEPTH passes
+            attn_load_raw<TL, F16KV>(rt, p, t, c0 + DEPTH * NSG * SUB, L, kv_stride, head_off, q4_row, tile_n);
+        if (active && g < G) {
+            // q.k for position c0 + r_lane over padded dims [dq0, dq0 + HDM/2)
+            const float* qg = qs + g * HDM + dq0;
+            const float* krow = kt + r_lane * KSTR + dq0;
+            float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+            // QC float4 pairs at a time: the whole row in registers (128 VGPRs)
+            // would not fit the 128-VGPR budget of a 1024-thread block
+#pragma unroll
+            for (int i0 = 0; i0 < KQ; i0 += QC) {
+                float4 q4[QC], k4[QC];
+#pragma unroll
+                for (int i = 0; i < QC; ++i) {
+                    q4[i] = *reinterpret_cast<const float4*>(qg + 4 * (i0 + i));
+                    k4[i] = *reinterpret_cast<const float4*>(krow + 4 * (i0 + i));
+                }
+#pragma unroll
+                for (int i = 0; i < QC; ++i) {
+                    a0 = fmaf(q4[i].x, k4[i].x, a0);
+                    a1 = fmaf(q4[i].y, k4[i].y, a1);
+                    a2 = fmaf(q4[i].z, k4[i].z, a2);
+                    a3 = fmaf(q4[i].w, k4[i].w, a3);
+                }
+            }
+            float s = (a0 + a1) + (a2 + a3);
+            s += __shfl_xor(s, 32, kWave);
+            s = (r_lane < cn) ? s * p.scale : -INFINITY;
+            // online softmax over the pass (lanes r and r + 32 hold the same score)
+            const float m_new = fmaxf(m, wave_max(s));
+            const float f = expf(m - m_new);          // 0 on the first pass
+            const float e = (r_lane < cn) ? expf(s - m_new) : 0.f;
+            l = l * f + wave_sum(half_id == 0 ? e : 0.f);
+            m = m_new;
+            if (half_id == 0) et[g * SUB + r_lane] = e;
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+            for (int i = 0; i < DPL; ++i) acc[i] *= f;
+            // rows past the pass are zeros in the tile and have zero weight
+#pragma unroll
+            for (int r = 0; r < SUB; ++r) {
+                const float er = et[g * SUB + r];
+                const float* vrow = vt + r * VSTR + dv0c;
+                if constexpr (DPL == 2) {
+                    const float2 v2 = *reinterpret_cast<const float2*>(vrow);
+                    acc[0] = fmaf(er, v2.x, acc[0]);
+                    acc[1] = fmaf(er, v2.y, acc[1]);
+                } else {
+                    acc[0] = fmaf(er, vrow[0], acc[0]);
+                }
+            }
+        }
+        __syncthreads();                              // the tile is rewritten next pass
+    };
+    for (uint32_t it = 0; it < iters; it += DEPTH) {
+        pass(tr[0], it);
+        if (DEPTH == 2 && it + 1 < iters) pass(tr[DEPTH - 1], it + 1);
+    }
+    {
+        // merge the subgroups' states (the K tiles are free after the last barrier)
+        float* racc = &ktile[0][0];                    // [NSG][G][HDM]
+        if (g < G) {
+            if (vlane) {
+#pragma unroll
+                for (int i = 0; i < DPL; ++i) racc[((uint32_t)sg * G + g) * HDM + dv0c + i] = acc[i];
+            }
+            if (lane == 0) {
+                red_m[sg][g] = m;
+                red_l[sg][g] = l;
+            }
+        }
+        __syncthreads();
+        if (sg != 0 || g >= G) return;
+        float mx = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < NSG; ++j) mx = fmaxf(mx, red_m[j][g]);
+        l = 0.f;
+#pragma unroll
+        for (int i = 0; i < DPL; ++i) acc[i] = 0.f;
+#pragma unroll
+        for (int j = 0; j < NSG; ++j) {
+            const float w = expf(red_m[j][g] - mx);     // 0 for a subgroup without passes
+            l = fmaf(red_l[j][g], w, l);
+#pragma unroll
+            for (int i = 0; i < DPL; ++i) acc[i] = fmaf(racc[((uint32_t)j * G + g) * HDM + dv0c + i], w, acc[i]);
+        }
+        m = mx;
+    }
+    if (g >= G) return;
+    float* part = p.part + (((uint64_t)kvh * p.s_max + split) * G + g) * (hd + 2);
+    if (vlane) {
+#pragma unroll
+        for (int i = 0; i < DPL; ++i) part[dv0c + i] = acc[i];
+    }
+    if (lane == 0) {
+        part[hd] = m;
+        part[hd + 1] = l;
+    }
+}
+
 // Merge of the split partials into the attention output, one block per
 // query head: out = sum_s acc_s e^(m_s - m) / sum_s l_s e^(m_s - m).
 __global__ __launch_bounds__(256) void attn_combine_kernel(AttnCombineParams p) {
@@ -320,7 +678,8 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnCombineParams p) 
     const uint32_t h = blockIdx.x;
     const uint32_t hd = p.hd, G = p.groups, kvh = h / G, g = h % G;
     const uint32_t L = p.pos ? (uint32_t)(*p.pos) + 1u : p.L;
-    const uint32_t s_act = min(p.s_max, (L + p.chunk - 1) / p.chunk);
+    const uint32_t chunk = p.chunk ? p.chunk : attn_chunk_for(L);
+    const uint32_t s_act = min(p.s_max, (L + chunk - 1) / chunk);
     const float* base = p.part + ((uint64_t)kvh * p.s_max * G + g) * (hd + 2);
     if (threadIdx.x < kWave) {
         const int lane = threadIdx.x;

@@ -102,6 +102,13 @@ __device__ __forceinline__ float lane_f32(float v, int lane) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
 }
 
+// Positions per attention split at context length L: the smallest multiple of
+// kAttnSub that keeps the number of splits within kAttnMaxSplits.
+__host__ __device__ __forceinline__ uint32_t attn_chunk_for(uint32_t L) {
+    const uint32_t c = (L + kAttnMaxSplits - 1) / kAttnMaxSplits;
+    return c <= (uint32_t)kAttnSub ? (uint32_t)kAttnSub : (c + kAttnSub - 1) / kAttnSub * kAttnSub;
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
     v += dpp_f32<0xB1>(v);    // quad_perm [1,0,3,2]
     v += dpp_f32<0x4E>(v);    // quad_perm [2,3,0,1]

@@ -503,7 +503,7 @@ __device__ __forceinline__ bool mk_attn_phase(const MkParams& p, const MkLayer& 
     ap.hd = hd;
     // waves 0..3: the first cache tile (independent of this step's q, k, v)
     KvTileRegs<TL> tr;
-    if (t < NTT) tr = attn_load_tile<TL, F16KV>(ap, p0, L, kv_stride, head_off, q4_row, tile_n);
+    if (t < NTT) tr = attn_load_tile<TL, F16KV>(ap, threadIdx.x, p0, L, kv_stride, head_off, q4_row, tile_n);
     const long long* Qb = bf.Q + (uint64_t)l * (qd + 2 * kv_stride);
     if (wave == kMkNW) {
         // control wave: q of the group's heads and the appended k, v, normalised and rotated
@@ -617,7 +617,7 @@ __device__ __forceinline__ bool mk_attn_phase(const MkParams& p, const MkLayer& 
         const bool new_here = has_new && cur >= c0 && cur < c0 + cn;
         if (t < NTT) {
             // attn_store_tile indexes by threadIdx.x < 256
-            attn_store_tile<TL, KSTR, VSTR>(tr, sm.ktile, sm.vtile, cn, new_here ? cur - c0 : 0xFFFFFFFFu, q4_row,
+            attn_store_tile<TL, KSTR, VSTR>(tr, threadIdx.x, sm.ktile, sm.vtile, cn, new_here ? cur - c0 : 0xFFFFFFFFu, q4_row,
                                             tile_n);
             if (new_here && (uint32_t)t < hd) {
                 sm.ktile[(cur - c0) * KSTR + t] = sm.kapp[t];
@@ -626,7 +626,7 @@ __device__ __forceinline__ bool mk_attn_phase(const MkParams& p, const MkLayer& 
         }
         __syncthreads();
         if (c0 + SUB < p1 && t < NTT)
-            tr = attn_load_tile<TL, F16KV>(ap, c0 + SUB, L, kv_stride, head_off, q4_row, tile_n);
+            tr = attn_load_tile<TL, F16KV>(ap, threadIdx.x, c0 + SUB, L, kv_stride, head_off, q4_row, tile_n);
         if (g < G) {
             const float* qg = sm.qs + g * HDM + dq0;
             const float* krow = sm.ktile + r_lane * KSTR + dq0;

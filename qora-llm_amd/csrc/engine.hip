@@ -246,6 +246,14 @@ int record_step(qora_hip_ctx* c, bool with_lm_head) {
 
 // QORA_HIP_EAGER=1 launches the decode step kernel by kernel instead of
 // replaying the captured graph (for profilers that do not follow graphs).
+// Attention subgroups per block (1 or 4): by default 4 when a split can hold
+// more than one 32-position pass; QORA_HIP_ATTN_NSG overrides.
+uint32_t attn_nsg(uint32_t max_chunk) {
+    const char* v = std::getenv("QORA_HIP_ATTN_NSG");
+    if (v && *v) return std::atoi(v) > 1 ? 4u : 1u;
+    return max_chunk > (uint32_t)kAttnSub ? 4u : 1u;
+}
+
 bool eager_mode() {
     const char* v = std::getenv("QORA_HIP_EAGER");
     return v && *v && *v != '0';
@@ -804,9 +812,10 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
         a.hd = m.hd;
         a.groups = m.groups;
         a.scale = 1.0f / sqrtf((float)m.hd);
-        a.chunk = m.attn_chunk;
+        a.chunk = 0;                       // split length follows the live context length
         a.part = m.d_attn_part;
         a.s_max = m.attn_s_max;
+        a.nsg = attn_nsg(m.attn_chunk);
 
         GemvParams& o = m.p_o[l];
         o = GemvParams{};
@@ -816,7 +825,7 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
         o.pro = PRO_ATTN;
         o.attn_part = m.d_attn_part;
         o.attn_s_max = m.attn_s_max;
-        o.attn_chunk = m.attn_chunk;
+        o.attn_chunk = 0;
         o.head_dim = m.hd;
         o.groups = m.groups;
         o.pos = m.d_pos;
@@ -1538,6 +1547,7 @@ extern "C" int qora_hip_attn_decode(qora_hip_ctx* c, const float* q, const void*
     a.groups = H / KVH;
     a.scale = 1.0f / sqrtf((float)hd);
     attn_geometry(L, &a.chunk, &a.s_max);
+    a.nsg = attn_nsg(a.chunk);
     if (int rc = ensure_attn_ws(c, (uint64_t)KVH * a.s_max * a.groups * (hd + 2))) return rc;
     a.part = c->ws_attn_part;
     const hipStream_t s = pick_stream(c, stream);

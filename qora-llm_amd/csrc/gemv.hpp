@@ -80,7 +80,8 @@ __device__ __forceinline__ void attn_merge_rows(const GemvParams& p, uint32_t k0
     const int t = threadIdx.x;
     const uint32_t hd = p.head_dim, G = p.groups;
     const uint32_t L = (uint32_t)(*p.pos) + 1u;
-    const uint32_t s_act = min(p.attn_s_max, (L + p.attn_chunk - 1) / p.attn_chunk);
+    const uint32_t chunk = p.attn_chunk ? p.attn_chunk : attn_chunk_for(L);
+    const uint32_t s_act = min(p.attn_s_max, (L + chunk - 1) / chunk);
     const uint32_t h0 = k0 / hd;
     const uint32_t nh = (k1 - 1) / hd - h0 + 1;
     const int wave = t / kWave, lane = t & (kWave - 1);

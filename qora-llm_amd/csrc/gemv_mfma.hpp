@@ -204,7 +204,8 @@ __device__ __forceinline__ void attn_merge_rows_wave(const GemvParams& p, uint32
     for (uint32_t j = 0; j < kMergeSpec / 2; ++j)
         pv[j] = rbase[(uint64_t)min(par + 2u * j, p.attn_s_max - 1u) * sstride];
     const uint32_t L = (uint32_t)pos_raw + 1u;
-    const uint32_t s_act = min(p.attn_s_max, (L + p.attn_chunk - 1) / p.attn_chunk);
+    const uint32_t chunk = p.attn_chunk ? p.attn_chunk : attn_chunk_for(L);
+    const uint32_t s_act = min(p.attn_s_max, (L + chunk - 1) / chunk);
     // ---- the remaining rows of a longer context ----
     if (s_act > kMergeSpec) {
 #pragma unroll

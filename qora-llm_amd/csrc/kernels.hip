@@ -390,14 +390,19 @@ void attn_geometry(uint32_t positions, uint32_t* chunk, uint32_t* s_max) {
 }
 
 hipError_t launch_attn(const AttnParams& p, hipStream_t stream) {
-    const dim3 grid(p.s_max, p.KVH), block(256);
-    if (p.hd <= 64) {
-        if (p.kv_f16) hipLaunchKernelGGL((attn_decode_kernel<1, true>), grid, block, 0, stream, p);
-        else hipLaunchKernelGGL((attn_decode_kernel<1, false>), grid, block, 0, stream, p);
-    } else {
-        if (p.kv_f16) hipLaunchKernelGGL((attn_decode_kernel<2, true>), grid, block, 0, stream, p);
-        else hipLaunchKernelGGL((attn_decode_kernel<2, false>), grid, block, 0, stream, p);
-    }
+    const dim3 grid(p.s_max, p.KVH);
+    const bool lng = p.nsg > 1;
+    const dim3 block(lng ? 256 * kAttnLongNsg : 256);
+#define QORA_ATTN(DPL)                                                                                   \
+    do {                                                                                                \
+        if (lng && p.kv_f16) hipLaunchKernelGGL((attn_decode_long_kernel<DPL, true>), grid, block, 0, stream, p); \
+        else if (lng) hipLaunchKernelGGL((attn_decode_long_kernel<DPL, false>), grid, block, 0, stream, p); \
+        else if (p.kv_f16) hipLaunchKernelGGL((attn_decode_kernel<DPL, true>), grid, block, 0, stream, p); \
+        else hipLaunchKernelGGL((attn_decode_kernel<DPL, false>), grid, block, 0, stream, p);          \
+    } while (0)
+    if (p.hd <= 64) QORA_ATTN(1);
+    else QORA_ATTN(2);
+#undef QORA_ATTN
     return hipGetLastError();
 }
 

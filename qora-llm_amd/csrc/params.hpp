@@ -51,7 +51,7 @@ struct GemvParams {
     uint32_t norm_n;          // length of the normalised vector
     // PRO_ATTN: attention partials [KVH][s_max][groups][head_dim + 2]
     const float* attn_part;
-    uint32_t attn_s_max, attn_chunk, head_dim, groups;
+    uint32_t attn_s_max, attn_chunk, head_dim, groups;   // attn_chunk 0: attn_chunk_for(L)
     const int32_t* pos;
     long long* acc;           // output: fixed-point accumulator (+= W x)
     long long* zero_ptr;      // optional int64 buffer cleared by this launch
@@ -185,9 +185,10 @@ struct AttnParams {
     uint32_t L;
     uint32_t H, KVH, hd, groups;
     float scale;               // 1 / sqrt(hd)
-    uint32_t chunk;            // positions per split (multiple of kAttnSub)
+    uint32_t chunk;            // positions per split (multiple of kAttnSub); 0: attn_chunk_for(L)
     float* part;               // [KVH][s_max][groups][hd + 2]
     uint32_t s_max;
+    uint32_t nsg;              // 1: attn_decode_kernel; > 1: attn_decode_long_kernel (4 passes in flight per split)
 };
 
 struct AttnCombineParams {

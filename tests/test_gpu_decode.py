@@ -178,3 +178,33 @@ def test_kv_upload_errors(ctx, pkg):
     with pytest.raises(pkg.QoraHipError) as e:
         be.forward_decode_raw(1)                    # cache full
     assert e.value.code == pkg.QORA_HIP_E_STATE
+
+
+@pytest.mark.parametrize("kv_dtype,hd", [(0, 128), (1, 128), (1, 64)])
+def test_long_context_decode_matches_oracle(ctx, pkg, orc, kv_dtype, hd):
+    """Decode over a cache of ~6000 uploaded positions (capacity 8192): the
+    split length follows the context (96 positions per split here) and each
+    attention block runs four subgroups; the appended row lands in a pass
+    owned by a later subgroup."""
+    heads, kvh = (16, 4) if hd == 128 else (4, 2)
+    cap, n = 8192, 6001
+    cfg = pkg.ModelConfig(num_layers=4, vocab=1000, hidden=256, intermediate=704, num_heads=heads,
+                          num_kv_heads=kvh, head_dim=hd, rope_half_dim=hd // 2, rope_theta=5e6, rope_positions=cap)
+    w = pkg.synthetic_model(cfg, seed=4, rope_positions=cap)
+    be = pkg.HipBackend(ctx, w, kv_capacity=cap, kv_dtype=kv_dtype)
+    om = orc.OracleModel(w, kv_capacity=cap, T=4)
+    r = np.random.default_rng(11)
+    for layer in range(cfg.num_layers):
+        k = r.standard_normal((n, kvh * hd), dtype=np.float32)
+        v = r.standard_normal((n, kvh * hd), dtype=np.float32)
+        if kv_dtype:
+            k, v = k.astype(np.float16).astype(np.float32), v.astype(np.float16).astype(np.float32)
+        be.kv_upload(layer, k, v)
+        om.kv_set(layer, k, v)
+    tol = REL_TOL if kv_dtype == 0 else 5e-3
+    for t in pkg.synth_tokens(4, 2001, 4, cfg.vocab):
+        print(f"case long-context decode kv_dtype={kv_dtype} hd={hd} pos={be.kv_len()}", flush=True)
+        logits, _ = be.forward_decode_raw(int(t))
+        ref = om.forward_decode(int(t))
+        assert rel_err(logits, ref) <= tol
+    assert be.kv_len() == n + 4

@@ -250,7 +250,7 @@ def test_rope_vs_oracle(ctx, orc, pkg, pos):
         assert np.array_equal(got, data)
 
 
-@pytest.mark.parametrize("L", [1, 2, 31, 32, 33, 100, 2048])
+@pytest.mark.parametrize("L", [1, 2, 31, 32, 33, 100, 2048, 2049, 5000, 32768])
 @pytest.mark.parametrize("kv_f16", [0, 1])
 def test_attention_vs_oracle(ctx, orc, pkg, L, kv_f16):
     H, KVH, hd = 16, 4, 128
