@@ -220,6 +220,27 @@ def extra_decode_rates(be, ctx, pkg, cfg, prompt, cap, steps):
     return chained, tok_s_2048
 
 
+def prefill_rate(be, ctx, pkg, cfg, n=512, reps=3):
+    """Batched prefill of n seeded random token ids (seed 1): ms per prompt,
+    tokens/s, and the projection GEMMs' useful rate (2 * weights * n flops,
+    lm_head and attention excluded) in TFLOP/s."""
+    ids = pkg.synth_tokens(1, 2500, n, cfg.vocab)
+    be.kv_reset()
+    be.raw_prefill(ids, want_logits=False)
+    ctx.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        be.kv_reset()
+        be.raw_prefill(ids, want_logits=False)
+    ctx.synchronize()
+    dt = (time.perf_counter() - t0) / reps
+    params = sum(k * n_ for (k, n_) in cfg.weight_shapes()) * cfg.num_layers
+    tflops = 2.0 * params * n / dt / 1e12
+    print(f"# prefill {n} tokens: {dt * 1e3:.2f} ms ({n / dt:.0f} tok/s, projections {tflops:.1f} TFLOP/s)",
+          file=sys.stderr, flush=True)
+    return {"tokens": n, "ms": round(dt * 1e3, 3), "tok_s": round(n / dt, 1), "gemm_tflops": round(tflops, 2)}
+
+
 def long_context_rate(ctx, pkg, w, n_ctx=32768, n_tok=64):
     """Host-driven decode with an f16 KV cache holding ~n_ctx positions: every
     layer's cache is filled with seeded random K/V through qora_hip_kv_upload
@@ -345,6 +366,8 @@ def main():
     if not args.decode_only:
         chained, tok_s_2048 = extra_decode_rates(be, ctx, pkg, cfg, prompt, cap, args.steps)
 
+    prefill = None if args.decode_only else prefill_rate(be, ctx, pkg, cfg)
+
     gemv = {} if args.no_gemv else gemv_roofline(ctx, hip, be, pkg)
     for kname, v in gemv.items():
         print(f"# {kname}: {v['us']:.2f} us, {v['gbps']:.0f} GB/s", file=sys.stderr, flush=True)
@@ -393,6 +416,7 @@ def main():
         "tok_s_device_chained": round(chained, 2) if chained else None,
         "tok_s_ctx2048": round(tok_s_2048, 2) if tok_s_2048 else None,
         "tok_s_ctx32768_f16kv": round(long_rate, 2) if long_rate else None,
+        "prefill_512": prefill,
         "frac_of_roofline_ctx32768": (round(long_rate * long_bytes / (HBM_PEAK_GBS * 1e9), 4)
                                       if long_rate else None),
         "gemv_gbps": {k2: round(v["gbps"], 1) for k2, v in gemv.items()},

@@ -211,6 +211,18 @@ int qora_hip_rope(qora_hip_ctx* ctx, float* data, uint32_t num_heads, uint32_t h
 int qora_hip_attn_decode(qora_hip_ctx* ctx, const float* q, const void* kc, const void* vc, int kv_f16,
                          uint32_t L, uint32_t num_heads, uint32_t num_kv_heads, uint32_t head_dim, float* out,
                          void* stream);
+/* gemm -> gemm_q4 / gemm_f16 (gemv.rs:505-511, 569-588, 677-706), the
+ * prefill projection: y [T][n] = x [T][k] . W for uploaded weight `wid`
+ * (k a multiple of 32), on the matrix cores with both operands split into two
+ * binary16 parts (the batched-prefill GEMM). Scratch comes from the context. */
+int qora_hip_gemm(qora_hip_ctx* ctx, uint32_t wid, const float* x, float* y, uint64_t T, void* stream);
+/* Causal attention of raw_prefill (gemv.rs:1088-1130) for T query rows at
+ * positions pos0 .. pos0 + T - 1: q [T][H*hd] (already rotated), caches
+ * token-major [pos0 + T][KVH][hd] (f32, or f16 when kv_f16), out [T][H*hd];
+ * row t attends to cache rows 0 .. pos0 + t. */
+int qora_hip_attn_prefill(qora_hip_ctx* ctx, const float* q, const void* kc, const void* vc, int kv_f16,
+                          uint32_t pos0, uint32_t T, uint32_t num_heads, uint32_t num_kv_heads, uint32_t head_dim,
+                          float* out, void* stream);
 /* Greedy branch of sample_token_top_k (generate.rs:346-352); the token is
  * written to a device int32. */
 int qora_hip_argmax(qora_hip_ctx* ctx, const float* logits, uint64_t n, int32_t* out_device, void* stream);

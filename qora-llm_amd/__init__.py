@@ -112,6 +112,8 @@ SIGNATURES = {
     "qora_hip_rmsnorm": (_I, [_P, _P, _P, _U64, _P, _P]),
     "qora_hip_rope": (_I, [_P, _P, _U32, _U32, _P, _P, _U32, _U32, _P]),
     "qora_hip_attn_decode": (_I, [_P, _P, _P, _P, _I, _U32, _U32, _U32, _U32, _P, _P]),
+    "qora_hip_gemm": (_I, [_P, _U32, _P, _P, _U64, _P]),
+    "qora_hip_attn_prefill": (_I, [_P, _P, _P, _P, _I, _U32, _U32, _U32, _U32, _U32, _P, _P]),
     "qora_hip_argmax": (_I, [_P, _P, _U64, _P, _P]),
     "qora_synth_q4": (None, [_U64, _U64, _U64, _U64, _P, _P]),
     "qora_synth_f16": (None, [_U64, _U64, _U64, _F, _P]),

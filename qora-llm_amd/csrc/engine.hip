@@ -73,6 +73,23 @@ struct ModelState {
     hipGraphExec_t g_step = nullptr;
     hipGraphExec_t g_prefill = nullptr;
     uint64_t host_pos = 0;
+    // batched prefill (prefill.hpp), set up on first use
+    bool pf_ready = false;
+    uint32_t pf_tc = 0;                  // tokens per chunk
+    float* d_pf_x = nullptr;             // residual rows [tc][hidden]
+    float* d_pf_qkv = nullptr;           // q|k|v rows [tc][qd + 2 kvd]
+    float* d_pf_q = nullptr;             // rotated q [tc][qd]
+    float* d_pf_ao = nullptr;            // attention output [tc][qd]
+    float* d_pf_gu = nullptr;            // gate|up rows [tc][2 inter]
+    float* d_pf_xn = nullptr;            // final-normed last row [hidden]
+    uint16_t* d_pf_xh = nullptr;         // split GEMM operand [tc][max k]
+    uint16_t* d_pf_xl = nullptr;
+    int32_t* d_pf_xe = nullptr;          // [tc]
+    uint32_t* d_pf_ids = nullptr;        // [cap]
+    std::vector<int8_t*> pf_wf;          // [L][7] Q4 group exponents
+    LmHeadParams p_lmq_pf{};
+    RowdotParams p_lm_pf{};
+    ArgmaxFinishParams p_fin_pf{};
 };
 
 }  // namespace
@@ -104,6 +121,8 @@ struct qora_hip_ctx {
     std::vector<DevWeight> weights;
     long long* ws_acc = nullptr;         // kernel-level fixed-point accumulator
     uint64_t ws_acc_n = 0;
+    void* ws_pf = nullptr;               // kernel-level GEMM: split operand and group exponents
+    uint64_t ws_pf_bytes = 0;
     float* ws_attn_part = nullptr;
     uint64_t ws_attn_part_n = 0;
     int32_t* h_pin = nullptr;            // pinned staging: [0] token in, [1] token out, [2] pos
@@ -173,6 +192,20 @@ int ensure_attn_ws(qora_hip_ctx* c, uint64_t part_floats) {
     if (int rc = dalloc(c, part_floats * sizeof(float), &p)) return rc;
     c->ws_attn_part = (float*)p;
     c->ws_attn_part_n = part_floats;
+    return QORA_HIP_OK;
+}
+
+int ensure_pf_ws(qora_hip_ctx* c, uint64_t bytes) {
+    if (bytes <= c->ws_pf_bytes) return QORA_HIP_OK;
+    if (c->capturing) return fail(c, QORA_HIP_E_STATE, "scratch must be sized by an eager call before capture");
+    HIP_TRY(c, hipStreamSynchronize(c->stream));
+    if (c->ws_pf) (void)hipFree(c->ws_pf);
+    c->ws_pf = nullptr;
+    c->ws_pf_bytes = 0;
+    void* p;
+    if (int rc = dalloc(c, bytes, &p)) return rc;
+    c->ws_pf = p;
+    c->ws_pf_bytes = bytes;
     return QORA_HIP_OK;
 }
 
@@ -352,13 +385,13 @@ extern "C" int qora_hip_destroy(qora_hip_ctx* c) {
     (void)hipStreamSynchronize(c->stream);
     free_model(c);
     for (PreparedGemv& g : c->gemvs)
-        for (void* q : {g.tw, g.ts, g.te})
+        for (void* q : {g.tw, g.ts, g.te, g.part_val, g.part_idx})
             if (q) (void)hipFree(q);
     for (DevWeight& w : c->weights) {
         if (w.w) (void)hipFree(w.w);
         if (w.scales) (void)hipFree(w.scales);
     }
-    for (void* p : {(void*)c->ws_acc, (void*)c->ws_attn_part})
+    for (void* p : {(void*)c->ws_acc, (void*)c->ws_attn_part, c->ws_pf})
         if (p) (void)hipFree(p);
     if (c->h_pin) (void)hipHostFree(c->h_pin);
     (void)hipStreamDestroy(c->stream);
@@ -1062,6 +1095,178 @@ extern "C" int qora_hip_generate_greedy(qora_hip_ctx* c, uint32_t token, uint32_
     return QORA_HIP_OK;
 }
 
+namespace {
+
+// Batched prefill unless QORA_HIP_PREFILL=seq (one decode step per prompt
+// position) or a contraction length is not a multiple of 32.
+bool pf_batched(const ModelState& m) {
+    const char* v = std::getenv("QORA_HIP_PREFILL");
+    if (v && std::strcmp(v, "seq") == 0) return false;
+    return pf_gemm_supported(m.hidden, 2) && pf_gemm_supported(m.H * m.hd, 2) && pf_gemm_supported(m.inter, 2);
+}
+
+int pf_setup(qora_hip_ctx* c) {
+    ModelState& m = c->m;
+    if (m.pf_ready) return QORA_HIP_OK;
+    if (c->capturing) return fail(c, QORA_HIP_E_STATE, "prefill set-up allocates: not allowed during capture");
+    const uint32_t qd = m.H * m.hd, kvd = m.KVH * m.hd;
+    const uint32_t tc = std::min<uint32_t>(512, m.cap);
+    const uint32_t kmax = std::max(std::max(m.hidden, qd), m.inter);
+    void* ptr = nullptr;
+#define PF_ALLOC(field, bytes)                                                     \
+    do {                                                                           \
+        if (int rc_ = model_alloc(c, (bytes), &ptr)) return rc_;                   \
+        m.field = reinterpret_cast<decltype(m.field)>(ptr);                        \
+    } while (0)
+    PF_ALLOC(d_pf_x, (size_t)tc * m.hidden * 4);
+    PF_ALLOC(d_pf_qkv, (size_t)tc * (qd + 2 * kvd) * 4);
+    PF_ALLOC(d_pf_q, (size_t)tc * qd * 4);
+    PF_ALLOC(d_pf_ao, (size_t)tc * qd * 4);
+    PF_ALLOC(d_pf_gu, (size_t)tc * 2 * m.inter * 4);
+    PF_ALLOC(d_pf_xn, (size_t)m.hidden * 4);
+    PF_ALLOC(d_pf_xh, (size_t)tc * kmax * 2);
+    PF_ALLOC(d_pf_xl, (size_t)tc * kmax * 2);
+    PF_ALLOC(d_pf_xe, (size_t)tc * 4);
+    PF_ALLOC(d_pf_ids, (size_t)m.cap * 4);
+#undef PF_ALLOC
+    m.pf_wf.assign((size_t)m.L * 7, nullptr);
+    if (m.fmt == FMT_Q4) {
+        for (uint32_t l = 0; l < m.L; ++l)
+            for (int j = 0; j < 7; ++j) {
+                const DevWeight* w = get_weight(c, m.wids[(size_t)l * 7 + j]);
+                if (!w) return fail(c, QORA_HIP_E_STATE, "model weight released");
+                const uint32_t groups = (uint32_t)(w->n / 32);
+                if (int rc = model_alloc(c, groups, &ptr)) return rc;
+                m.pf_wf[(size_t)l * 7 + j] = (int8_t*)ptr;
+                HIP_TRY(c, launch_pf_weight_exp((const uint16_t*)w->scales, (uint32_t)w->k, groups, (int8_t*)ptr,
+                                                c->stream));
+            }
+    }
+    // the lm_head of the last prompt row reads the final-normed fp32 row
+    m.p_lmq_pf = m.p_lmq;
+    m.p_lmq_pf.x = m.d_pf_xn;
+    m.p_lmq_pf.xacc = nullptr;
+    m.p_lmq_pf.gamma = nullptr;
+    m.p_lm_pf = m.p_lm;
+    m.p_lm_pf.x = m.d_pf_xn;
+    m.p_lm_pf.xacc = nullptr;
+    m.p_lm_pf.gamma = nullptr;
+    m.p_fin_pf = ArgmaxFinishParams{m.d_argv, m.d_argi, m.lm_blocks, m.d_token, nullptr, nullptr};
+    m.pf_tc = tc;
+    m.pf_ready = true;
+    return QORA_HIP_OK;
+}
+
+int pf_gemm(qora_hip_ctx* c, uint32_t l, int j, uint32_t T, float* y, uint32_t ldy, bool accumulate) {
+    ModelState& m = c->m;
+    const DevWeight* w = get_weight(c, m.wids[(size_t)l * 7 + j]);
+    if (!w) return fail(c, QORA_HIP_E_STATE, "model weight released");
+    PrefillGemmParams g{};
+    g.xh = m.d_pf_xh;
+    g.xl = m.d_pf_xl;
+    g.xe = m.d_pf_xe;
+    g.T = T;
+    g.k = (uint32_t)w->k;
+    g.n = (uint32_t)w->n;
+    g.w = (const uint8_t*)w->w;
+    g.scales = (const uint16_t*)w->scales;
+    g.wf = m.pf_wf[(size_t)l * 7 + j];
+    g.y = y;
+    g.ldy = ldy;
+    g.accumulate = accumulate ? 1 : 0;
+    HIP_TRY(c, launch_pf_gemm(w->fmt, g, c->cus, c->stream));
+    return QORA_HIP_OK;
+}
+
+// raw_prefill (gemv.rs:1027-1190) over the prompt in chunks of pf_tc tokens:
+// every layer runs on the whole chunk (GEMMs on the matrix cores, causal
+// attention over the cache rows written so far), then the last row's final
+// norm and lm_head give the logits and the greedy token.
+int prefill_batched(qora_hip_ctx* c, size_t n, float* logits, uint32_t* argmax) {
+    ModelState& m = c->m;
+    if (int rc = pf_setup(c)) return rc;
+    const hipStream_t s = c->stream;
+    const uint32_t qd = m.H * m.hd, kvd = m.KVH * m.hd, qkvn = qd + 2 * kvd;
+    const size_t kvb = m.kv_f16 ? 2 : 4;
+    const DevWeight* emb = get_weight(c, m.embed_wid);
+    if (!emb) return fail(c, QORA_HIP_E_STATE, "embedding weight released");
+    uint32_t T = 0;
+    for (size_t c0 = 0; c0 < n; c0 += m.pf_tc) {
+        T = (uint32_t)std::min<size_t>(m.pf_tc, n - c0);
+        PrefillRowParams r{};
+        r.ids = m.d_pf_ids + c0;
+        r.vocab = m.vocab;
+        r.fmt = (int)m.fmt;
+        r.emb_w = (const uint8_t*)emb->w;
+        r.emb_s = (const uint16_t*)emb->scales;
+        r.x = m.d_pf_x;
+        r.n = m.hidden;
+        HIP_TRY(c, launch_pf_rows(PF_ROW_EMBED, r, T, s));
+        for (uint32_t l = 0; l < m.L; ++l) {
+            PrefillRowParams nr{};
+            nr.x = m.d_pf_x;
+            nr.n = m.hidden;
+            nr.gamma = m.d_norms + ((size_t)l * 2 + 0) * m.hidden;
+            nr.xh = m.d_pf_xh;
+            nr.xl = m.d_pf_xl;
+            nr.xe = m.d_pf_xe;
+            HIP_TRY(c, launch_pf_rows(PF_ROW_RMSNORM, nr, T, s));
+            if (int rc = pf_gemm(c, l, 0, T, m.d_pf_qkv, qkvn, false)) return rc;
+            if (int rc = pf_gemm(c, l, 1, T, m.d_pf_qkv + qd, qkvn, false)) return rc;
+            if (int rc = pf_gemm(c, l, 2, T, m.d_pf_qkv + qd + kvd, qkvn, false)) return rc;
+            PrefillAttnParams a{};
+            a.qkv = m.d_pf_qkv;
+            a.q = m.d_pf_q;
+            a.kc = (uint8_t*)m.d_k + (size_t)l * m.cap * kvd * kvb;
+            a.vc = (uint8_t*)m.d_v + (size_t)l * m.cap * kvd * kvb;
+            a.kv_f16 = m.kv_f16;
+            a.rope_cos = m.d_cos;
+            a.rope_sin = m.d_sin;
+            a.use_rope = m.p_attn[l].use_rope;
+            a.half = m.half;
+            a.pos0 = (uint32_t)c0;
+            a.T = T;
+            a.H = m.H;
+            a.KVH = m.KVH;
+            a.hd = m.hd;
+            a.scale = 1.0f / sqrtf((float)m.hd);
+            a.out = m.d_pf_ao;
+            HIP_TRY(c, launch_pf_rope_cache(a, s));
+            HIP_TRY(c, launch_pf_attn(a, s));
+            PrefillRowParams sr{};
+            sr.x = m.d_pf_ao;
+            sr.n = qd;
+            sr.xh = m.d_pf_xh;
+            sr.xl = m.d_pf_xl;
+            sr.xe = m.d_pf_xe;
+            HIP_TRY(c, launch_pf_rows(PF_ROW_SPLIT, sr, T, s));
+            if (int rc = pf_gemm(c, l, 3, T, m.d_pf_x, m.hidden, true)) return rc;
+            nr.gamma = m.d_norms + ((size_t)l * 2 + 1) * m.hidden;
+            HIP_TRY(c, launch_pf_rows(PF_ROW_RMSNORM, nr, T, s));
+            if (int rc = pf_gemm(c, l, 4, T, m.d_pf_gu, 2 * m.inter, false)) return rc;
+            if (int rc = pf_gemm(c, l, 5, T, m.d_pf_gu + m.inter, 2 * m.inter, false)) return rc;
+            PrefillRowParams gr{};
+            gr.x = m.d_pf_gu;
+            gr.u = m.d_pf_gu + m.inter;
+            gr.ld = 2 * m.inter;
+            gr.n = m.inter;
+            gr.xh = m.d_pf_xh;
+            gr.xl = m.d_pf_xl;
+            gr.xe = m.d_pf_xe;
+            HIP_TRY(c, launch_pf_rows(PF_ROW_SILU, gr, T, s));
+            if (int rc = pf_gemm(c, l, 6, T, m.d_pf_x, m.hidden, true)) return rc;
+        }
+    }
+    HIP_TRY(c, launch_rmsnorm(m.d_pf_x + (size_t)(T - 1) * m.hidden, m.d_final, m.hidden, m.d_pf_xn, s));
+    if (m.lm_mfma) HIP_TRY(c, launch_lmhead(m.lm_blocks, m.p_lmq_pf, s));
+    else HIP_TRY(c, launch_rowdot(m.fmt, m.lm_blocks, m.p_lm_pf, s));
+    HIP_TRY(c, launch_argmax_finish(m.p_fin_pf, s));
+    if (int rc = set_device_pos(c, n)) return rc;
+    return finish_step(c, logits, argmax);
+}
+
+}  // namespace
+
 extern "C" int qora_hip_prefill(qora_hip_ctx* c, const uint32_t* ids, size_t n, float* logits, uint32_t* argmax) {
     if (!c || !ids) return fail(c, QORA_HIP_E_INVALID, "null argument");
     ModelState& m = c->m;
@@ -1073,6 +1278,13 @@ extern "C" int qora_hip_prefill(qora_hip_ctx* c, const uint32_t* ids, size_t n, 
     if (int rc = set_device_pos(c, 0)) return rc;
     if (int rc = check_step_room(c, n)) return rc;
     if (force_fail("launch")) return fail(c, QORA_HIP_E_DEVICE, "forced launch failure (QORA_HIP_FORCE_FAIL=launch)");
+    if (pf_batched(m) && n > 1) {
+        if (int rc = pf_setup(c)) return rc;
+        HIP_TRY(c, hipMemcpy(m.d_pf_ids, ids, n * 4, hipMemcpyHostToDevice));
+        if (int rc = prefill_batched(c, n, logits, argmax)) return rc;
+        m.host_pos = n;
+        return QORA_HIP_OK;
+    }
     HIP_TRY(c, hipMemcpy(m.d_prompt, ids, n * 4, hipMemcpyHostToDevice));
     for (size_t i = 0; i + 1 < n; ++i)
         if (int rc = launch_step(c, false)) return rc;
@@ -1554,6 +1766,68 @@ extern "C" int qora_hip_attn_decode(qora_hip_ctx* c, const float* q, const void*
     HIP_TRY(c, launch_attn(a, s));
     AttnCombineParams cp{a.part, nullptr, L, H, KVH, hd, a.groups, a.chunk, a.s_max, out};
     HIP_TRY(c, launch_attn_combine(cp, s));
+    return QORA_HIP_OK;
+}
+
+extern "C" int qora_hip_gemm(qora_hip_ctx* c, uint32_t wid, const float* x, float* y, uint64_t T, void* stream) {
+    if (!c) return QORA_HIP_E_INVALID;
+    if (!x || !y) return fail(c, QORA_HIP_E_INVALID, "null argument");
+    const DevWeight* w = get_weight(c, wid);
+    if (!w) return fail(c, QORA_HIP_E_INVALID, "unknown weight id");
+    if (T == 0 || T > 0x7FFFFFFFull) return fail(c, QORA_HIP_E_INVALID, "bad row count");
+    if (!pf_gemm_supported((uint32_t)w->k, (uint32_t)w->n)) return fail(c, QORA_HIP_E_INVALID, "k must be a multiple of 32");
+    // scratch: xh, xl [T][k] binary16, xe [T], wf [n/32] (each 256-byte aligned)
+    auto al = [](uint64_t b) { return (b + 255) & ~uint64_t(255); };
+    const uint64_t bx = al(T * w->k * 2), be = al(T * 4), bf = al(w->n / 32 + 1);
+    if (int rc = ensure_pf_ws(c, 2 * bx + be + bf)) return rc;
+    uint8_t* base = (uint8_t*)c->ws_pf;
+    const hipStream_t s = pick_stream(c, stream);
+    PrefillRowParams r{};
+    r.x = const_cast<float*>(x);
+    r.n = (uint32_t)w->k;
+    r.xh = (uint16_t*)base;
+    r.xl = (uint16_t*)(base + bx);
+    r.xe = (int32_t*)(base + 2 * bx);
+    HIP_TRY(c, launch_pf_rows(PF_ROW_SPLIT, r, (uint32_t)T, s));
+    PrefillGemmParams g{};
+    g.xh = r.xh;
+    g.xl = r.xl;
+    g.xe = r.xe;
+    g.T = (uint32_t)T;
+    g.k = (uint32_t)w->k;
+    g.n = (uint32_t)w->n;
+    g.w = (const uint8_t*)w->w;
+    g.scales = (const uint16_t*)w->scales;
+    if (w->fmt == FMT_Q4) {
+        g.wf = (const int8_t*)(base + 2 * bx + be);
+        HIP_TRY(c, launch_pf_weight_exp(g.scales, g.k, g.n / 32, const_cast<int8_t*>(g.wf), s));
+    }
+    g.y = y;
+    g.ldy = g.n;
+    HIP_TRY(c, launch_pf_gemm(w->fmt, g, c->cus, s));
+    return QORA_HIP_OK;
+}
+
+extern "C" int qora_hip_attn_prefill(qora_hip_ctx* c, const float* q, const void* kc, const void* vc, int kv_f16,
+                                     uint32_t pos0, uint32_t T, uint32_t H, uint32_t KVH, uint32_t hd, float* out,
+                                     void* stream) {
+    if (!c) return QORA_HIP_E_INVALID;
+    if (!q || !kc || !vc || !out) return fail(c, QORA_HIP_E_INVALID, "null argument");
+    if (T == 0 || H == 0 || KVH == 0 || H % KVH != 0 || hd == 0 || hd > (uint32_t)kAttnMaxHd || hd % 8 != 0)
+        return fail(c, QORA_HIP_E_INVALID, "attention needs T > 0, H % KVH == 0, head_dim <= 128 and a multiple of 8");
+    PrefillAttnParams a{};
+    a.q = const_cast<float*>(q);
+    a.kc = const_cast<void*>(kc);
+    a.vc = const_cast<void*>(vc);
+    a.kv_f16 = kv_f16 ? 1 : 0;
+    a.pos0 = pos0;
+    a.T = T;
+    a.H = H;
+    a.KVH = KVH;
+    a.hd = hd;
+    a.scale = 1.0f / sqrtf((float)hd);
+    a.out = out;
+    HIP_TRY(c, launch_pf_attn(a, pick_stream(c, stream)));
     return QORA_HIP_OK;
 }
 

@@ -5,6 +5,7 @@
 #include "lmhead_mfma.hpp"
 #include "decode_mk.hpp"
 #include "attn.hpp"
+#include "prefill.hpp"
 
 #include <algorithm>
 #include <cstdlib>
@@ -446,6 +447,60 @@ hipError_t launch_argmax(const float* logits, uint32_t n, int32_t* out, hipStrea
 
 hipError_t launch_advance_pos(int32_t* pos, hipStream_t stream) {
     hipLaunchKernelGGL(advance_pos_kernel, dim3(1), dim3(64), 0, stream, pos);
+    return hipGetLastError();
+}
+
+// ---- batched prefill ----
+
+hipError_t launch_pf_rows(int kind, const PrefillRowParams& p, uint32_t T, hipStream_t stream) {
+    if (T == 0) return hipSuccess;
+    switch (kind) {
+    case PF_ROW_EMBED: hipLaunchKernelGGL(pf_embed_kernel, dim3(T), dim3(256), 0, stream, p); break;
+    case PF_ROW_RMSNORM: hipLaunchKernelGGL(pf_rmsnorm_split_kernel, dim3(T), dim3(256), 0, stream, p); break;
+    case PF_ROW_SPLIT: hipLaunchKernelGGL(pf_split_kernel, dim3(T), dim3(256), 0, stream, p); break;
+    case PF_ROW_SILU: hipLaunchKernelGGL(pf_silu_split_kernel, dim3(T), dim3(256), 0, stream, p); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_pf_weight_exp(const uint16_t* scales, uint32_t k, uint32_t groups, int8_t* wf, hipStream_t stream) {
+    hipLaunchKernelGGL(pf_weight_exp_kernel, dim3((groups + 255) / 256), dim3(256), 0, stream, scales, k, groups, wf);
+    return hipGetLastError();
+}
+
+bool pf_gemm_supported(uint32_t k, uint32_t n) { return k > 0 && k % 32 == 0 && n >= 2 && n % 2 == 0; }
+
+hipError_t launch_pf_gemm(int fmt, const PrefillGemmParams& p, int cus, hipStream_t stream) {
+    if (!pf_gemm_supported(p.k, p.n) || p.T == 0) return hipErrorInvalidValue;
+    const uint32_t mt = (p.T + 63) / 64;
+    // 128-column tiles when they still give every CU a block, else 64
+    const bool wide = p.n % 128 == 0 && (uint64_t)(p.n / 128) * mt >= (uint64_t)cus;
+    const uint32_t nt = wide ? 128 : 64;
+    const dim3 grid((p.n + nt - 1) / nt, mt);
+    if (fmt == FMT_Q4) {
+        if (wide) hipLaunchKernelGGL((pf_gemm_kernel<128, true>), grid, dim3(256), 0, stream, p);
+        else hipLaunchKernelGGL((pf_gemm_kernel<64, true>), grid, dim3(256), 0, stream, p);
+    } else {
+        if (wide) hipLaunchKernelGGL((pf_gemm_kernel<128, false>), grid, dim3(256), 0, stream, p);
+        else hipLaunchKernelGGL((pf_gemm_kernel<64, false>), grid, dim3(256), 0, stream, p);
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_pf_rope_cache(const PrefillAttnParams& p, hipStream_t stream) {
+    if (p.T == 0) return hipSuccess;
+    if (p.kv_f16) hipLaunchKernelGGL((pf_rope_cache_kernel<true>), dim3(p.T), dim3(256), 0, stream, p);
+    else hipLaunchKernelGGL((pf_rope_cache_kernel<false>), dim3(p.T), dim3(256), 0, stream, p);
+    return hipGetLastError();
+}
+
+hipError_t launch_pf_attn(const PrefillAttnParams& p, hipStream_t stream) {
+    if (p.T == 0) return hipSuccess;
+    if (p.hd > (uint32_t)kAttnMaxHd || p.hd % 8 != 0 || p.H % p.KVH != 0) return hipErrorInvalidValue;
+    const dim3 grid((p.T + 31) / 32, p.H);
+    if (p.kv_f16) hipLaunchKernelGGL((pf_attn_kernel<true>), grid, dim3(256), 0, stream, p);
+    else hipLaunchKernelGGL((pf_attn_kernel<false>), grid, dim3(256), 0, stream, p);
     return hipGetLastError();
 }
 

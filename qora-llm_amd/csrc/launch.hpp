@@ -91,4 +91,13 @@ hipError_t launch_rope(float* data, uint32_t heads, uint32_t head_dim, const flo
 hipError_t launch_argmax(const float* logits, uint32_t n, int32_t* out, hipStream_t stream);
 hipError_t launch_advance_pos(int32_t* pos, hipStream_t stream);
 
+// batched prefill (prefill.hpp)
+enum PfRow : int { PF_ROW_EMBED = 0, PF_ROW_RMSNORM = 1, PF_ROW_SPLIT = 2, PF_ROW_SILU = 3 };
+hipError_t launch_pf_rows(int kind, const PrefillRowParams& p, uint32_t T, hipStream_t stream);
+hipError_t launch_pf_weight_exp(const uint16_t* scales, uint32_t k, uint32_t groups, int8_t* wf, hipStream_t stream);
+bool pf_gemm_supported(uint32_t k, uint32_t n);
+hipError_t launch_pf_gemm(int fmt, const PrefillGemmParams& p, int cus, hipStream_t stream);
+hipError_t launch_pf_rope_cache(const PrefillAttnParams& p, hipStream_t stream);
+hipError_t launch_pf_attn(const PrefillAttnParams& p, hipStream_t stream);
+
 }  // namespace qora

@@ -154,6 +154,54 @@ struct MkParams {
 };
 
 
+// Batched prefill (prefill.hpp). Split GEMM operands: xh, xl binary16 words
+// [T][k] and xe[T] exponents (x = (xh + xl) * 2^xe).
+struct PrefillRowParams {
+    const uint32_t* ids;       // pf_embed_kernel: token ids [T]
+    uint32_t vocab;
+    int fmt;
+    const uint8_t* emb_w;
+    const uint16_t* emb_s;
+    float* x;                  // fp32 rows [T][ld] (embedding output, norm input, gate rows)
+    const float* u;            // pf_silu_split_kernel: up rows [T][ld]
+    uint32_t ld;               // row stride of x / u (pf_silu_split_kernel)
+    uint32_t n;                // row length
+    const uint16_t* gamma;     // pf_rmsnorm_split_kernel
+    uint16_t* xh;
+    uint16_t* xl;
+    int32_t* xe;
+};
+
+struct PrefillGemmParams {
+    const uint16_t* xh;
+    const uint16_t* xl;
+    const int32_t* xe;
+    uint32_t T, k, n;
+    const uint8_t* w;          // reference layout: Q4 packed [k][n/2] or f16 [k][n]
+    const uint16_t* scales;    // Q4 [k][n/32]
+    const int8_t* wf;          // Q4 per-group exponents [n/32]
+    float* y;                  // [T][ldy]
+    uint32_t ldy;
+    int accumulate;            // 1: y += result (residual add)
+};
+
+struct PrefillAttnParams {
+    const float* qkv;          // GEMM output rows [T][qd + 2 kvd]
+    float* q;                  // rotated q [T][qd]
+    void* kc;                  // this layer's cache [cap][kvd]
+    void* vc;
+    int kv_f16;
+    const float* rope_cos;
+    const float* rope_sin;
+    int use_rope;
+    uint32_t half;
+    uint32_t pos0;             // absolute position of the chunk's first token
+    uint32_t T;                // tokens in the chunk
+    uint32_t H, KVH, hd;
+    float scale;
+    float* out;                // attention output [T][qd]
+};
+
 struct ArgmaxFinishParams {
     const float* part_val;
     const uint32_t* part_idx;
