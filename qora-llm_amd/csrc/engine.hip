@@ -86,6 +86,7 @@ struct ModelState {
     uint16_t* d_pf_xl = nullptr;
     int32_t* d_pf_xe = nullptr;          // [tc]
     uint32_t* d_pf_ids = nullptr;        // [cap]
+    float* d_pf_part = nullptr;          // split-K partials of the GEMMs
     std::vector<int8_t*> pf_wf;          // [L][7] Q4 group exponents
     LmHeadParams p_lmq_pf{};
     RowdotParams p_lm_pf{};
@@ -1128,9 +1129,32 @@ int pf_setup(qora_hip_ctx* c) {
     PF_ALLOC(d_pf_xl, (size_t)tc * kmax * 2);
     PF_ALLOC(d_pf_xe, (size_t)tc * 4);
     PF_ALLOC(d_pf_ids, (size_t)m.cap * 4);
+    {
+        // the largest split-K partial set over every chunk length (the 7 shapes
+        // repeat in every layer)
+        uint64_t pb = 4;
+        for (int j = 0; j < 7; ++j) {
+            const DevWeight* w = get_weight(c, m.wids[(size_t)j]);
+            if (!w) return fail(c, QORA_HIP_E_STATE, "model weight released");
+            for (uint32_t t = 1; t <= tc; ++t) {
+                const PfGemmShape sh = pf_gemm_shape(t, (uint32_t)w->k, (uint32_t)w->n, c->cus);
+                if (sh.splits > 1) pb = std::max<uint64_t>(pb, (uint64_t)sh.splits * t * w->n * 4);
+            }
+        }
+        PF_ALLOC(d_pf_part, pb);
+    }
 #undef PF_ALLOC
     m.pf_wf.assign((size_t)m.L * 7, nullptr);
     if (m.fmt == FMT_Q4) {
+        uint64_t sb = 0;
+        for (uint32_t l = 0; l < m.L; ++l)
+            for (int j = 0; j < 7; ++j) {
+                const DevWeight* w = get_weight(c, m.wids[(size_t)l * 7 + j]);
+                if (!w) return fail(c, QORA_HIP_E_STATE, "model weight released");
+                sb = std::max(sb, pf_weight_exp_scratch((uint32_t)w->k, (uint32_t)(w->n / 32)));
+            }
+        if (int rc = model_alloc(c, sb, &ptr)) return rc;
+        uint32_t* scratch = (uint32_t*)ptr;
         for (uint32_t l = 0; l < m.L; ++l)
             for (int j = 0; j < 7; ++j) {
                 const DevWeight* w = get_weight(c, m.wids[(size_t)l * 7 + j]);
@@ -1139,7 +1163,7 @@ int pf_setup(qora_hip_ctx* c) {
                 if (int rc = model_alloc(c, groups, &ptr)) return rc;
                 m.pf_wf[(size_t)l * 7 + j] = (int8_t*)ptr;
                 HIP_TRY(c, launch_pf_weight_exp((const uint16_t*)w->scales, (uint32_t)w->k, groups, (int8_t*)ptr,
-                                                c->stream));
+                                                scratch, c->stream));
             }
     }
     // the lm_head of the last prompt row reads the final-normed fp32 row
@@ -1174,7 +1198,12 @@ int pf_gemm(qora_hip_ctx* c, uint32_t l, int j, uint32_t T, float* y, uint32_t l
     g.y = y;
     g.ldy = ldy;
     g.accumulate = accumulate ? 1 : 0;
-    HIP_TRY(c, launch_pf_gemm(w->fmt, g, c->cus, c->stream));
+    const PfGemmShape sh = pf_gemm_shape(T, g.k, g.n, c->cus);
+    g.nt = sh.nt;
+    g.splits = sh.splits;
+    g.kper = sh.kper;
+    g.part = m.d_pf_part;
+    HIP_TRY(c, launch_pf_gemm(w->fmt, g, c->stream));
     return QORA_HIP_OK;
 }
 
@@ -1776,10 +1805,13 @@ extern "C" int qora_hip_gemm(qora_hip_ctx* c, uint32_t wid, const float* x, floa
     if (!w) return fail(c, QORA_HIP_E_INVALID, "unknown weight id");
     if (T == 0 || T > 0x7FFFFFFFull) return fail(c, QORA_HIP_E_INVALID, "bad row count");
     if (!pf_gemm_supported((uint32_t)w->k, (uint32_t)w->n)) return fail(c, QORA_HIP_E_INVALID, "k must be a multiple of 32");
-    // scratch: xh, xl [T][k] binary16, xe [T], wf [n/32] (each 256-byte aligned)
+    // scratch: xh, xl [T][k] binary16, xe [T], wf [n/32], exponent partials (each 256-byte aligned)
     auto al = [](uint64_t b) { return (b + 255) & ~uint64_t(255); };
     const uint64_t bx = al(T * w->k * 2), be = al(T * 4), bf = al(w->n / 32 + 1);
-    if (int rc = ensure_pf_ws(c, 2 * bx + be + bf)) return rc;
+    const uint64_t bs = al(pf_weight_exp_scratch((uint32_t)w->k, (uint32_t)(w->n / 32)));
+    const PfGemmShape sh = pf_gemm_shape((uint32_t)T, (uint32_t)w->k, (uint32_t)w->n, c->cus);
+    const uint64_t bp = sh.splits > 1 ? al((uint64_t)sh.splits * T * w->n * 4) : 0;
+    if (int rc = ensure_pf_ws(c, 2 * bx + be + bf + bs + bp)) return rc;
     uint8_t* base = (uint8_t*)c->ws_pf;
     const hipStream_t s = pick_stream(c, stream);
     PrefillRowParams r{};
@@ -1800,11 +1832,16 @@ extern "C" int qora_hip_gemm(qora_hip_ctx* c, uint32_t wid, const float* x, floa
     g.scales = (const uint16_t*)w->scales;
     if (w->fmt == FMT_Q4) {
         g.wf = (const int8_t*)(base + 2 * bx + be);
-        HIP_TRY(c, launch_pf_weight_exp(g.scales, g.k, g.n / 32, const_cast<int8_t*>(g.wf), s));
+        HIP_TRY(c, launch_pf_weight_exp(g.scales, g.k, g.n / 32, const_cast<int8_t*>(g.wf),
+                                        (uint32_t*)(base + 2 * bx + be + bf), s));
     }
     g.y = y;
     g.ldy = g.n;
-    HIP_TRY(c, launch_pf_gemm(w->fmt, g, c->cus, s));
+    g.nt = sh.nt;
+    g.splits = sh.splits;
+    g.kper = sh.kper;
+    g.part = sh.splits > 1 ? (float*)(base + 2 * bx + be + bf + bs) : nullptr;
+    HIP_TRY(c, launch_pf_gemm(w->fmt, g, s));
     return QORA_HIP_OK;
 }
 

@@ -464,26 +464,62 @@ hipError_t launch_pf_rows(int kind, const PrefillRowParams& p, uint32_t T, hipSt
     return hipGetLastError();
 }
 
-hipError_t launch_pf_weight_exp(const uint16_t* scales, uint32_t k, uint32_t groups, int8_t* wf, hipStream_t stream) {
-    hipLaunchKernelGGL(pf_weight_exp_kernel, dim3((groups + 255) / 256), dim3(256), 0, stream, scales, k, groups, wf);
+uint64_t pf_weight_exp_scratch(uint32_t k, uint32_t groups) {
+    return (uint64_t)((k + kPfExpRows - 1) / kPfExpRows) * groups * 4;
+}
+
+hipError_t launch_pf_weight_exp(const uint16_t* scales, uint32_t k, uint32_t groups, int8_t* wf, uint32_t* scratch,
+                                hipStream_t stream) {
+    const uint32_t nblk = (k + kPfExpRows - 1) / kPfExpRows;
+    hipLaunchKernelGGL(pf_weight_exp_part_kernel, dim3((groups + kWave - 1) / kWave, nblk), dim3(256), 0, stream,
+                       scales, k, groups, scratch);
+    hipLaunchKernelGGL(pf_weight_exp_kernel, dim3((groups + 255) / 256), dim3(256), 0, stream, scratch, nblk, groups,
+                       wf);
     return hipGetLastError();
 }
 
 bool pf_gemm_supported(uint32_t k, uint32_t n) { return k > 0 && k % 32 == 0 && n >= 2 && n % 2 == 0; }
 
-hipError_t launch_pf_gemm(int fmt, const PrefillGemmParams& p, int cus, hipStream_t stream) {
-    if (!pf_gemm_supported(p.k, p.n) || p.T == 0) return hipErrorInvalidValue;
-    const uint32_t mt = (p.T + 63) / 64;
-    // 128-column tiles when they still give every CU a block, else 64
-    const bool wide = p.n % 128 == 0 && (uint64_t)(p.n / 128) * mt >= (uint64_t)cus;
-    const uint32_t nt = wide ? 128 : 64;
-    const dim3 grid((p.n + nt - 1) / nt, mt);
+// Launch shape of the prefill GEMM: 128-column tiles when they still give
+// every CU a block, else 64; then split K (into runs of at least 256 rows)
+// until about four blocks per CU are in flight, since each block's K loop is
+// bound by its global-load latency.
+PfGemmShape pf_gemm_shape(uint32_t T, uint32_t k, uint32_t n, int cus) {
+    PfGemmShape sh{};
+    const uint32_t mt = (T + 63) / 64;
+    const char* ev = std::getenv("QORA_HIP_PF_NT");
+    bool wide = n % 128 == 0 && (uint64_t)(n / 128) * mt >= (uint64_t)cus;
+    if (ev && *ev) wide = std::atoi(ev) == 128 && n % 128 == 0;
+    sh.nt = wide ? 128 : 64;
+    const uint64_t blocks = (uint64_t)((n + sh.nt - 1) / sh.nt) * mt;
+    uint32_t splits = (uint32_t)std::min<uint64_t>(std::max<uint64_t>(1, (4ull * cus) / blocks), std::max(1u, k / 256));
+    const char* es = std::getenv("QORA_HIP_PF_SPLITS");
+    if (es && *es) splits = std::max(1, std::atoi(es));
+    const uint32_t steps = k / 32;
+    splits = std::min(splits, steps);
+    const uint32_t per = (steps + splits - 1) / splits;
+    sh.kper = per * 32;
+    sh.splits = (steps + per - 1) / per;
+    return sh;
+}
+
+hipError_t launch_pf_gemm(int fmt, const PrefillGemmParams& p, hipStream_t stream) {
+    if (!pf_gemm_supported(p.k, p.n) || p.T == 0 || p.splits == 0 || p.kper % 32 != 0 ||
+        (uint64_t)p.splits * p.kper < p.k || (p.splits > 1 && !p.part))
+        return hipErrorInvalidValue;
+    const uint32_t nt = (p.n % 128 == 0 && p.nt == 128) ? 128 : 64;
+    const dim3 grid((p.n + nt - 1) / nt, (p.T + 63) / 64, p.splits);
     if (fmt == FMT_Q4) {
-        if (wide) hipLaunchKernelGGL((pf_gemm_kernel<128, true>), grid, dim3(256), 0, stream, p);
+        if (nt == 128) hipLaunchKernelGGL((pf_gemm_kernel<128, true>), grid, dim3(256), 0, stream, p);
         else hipLaunchKernelGGL((pf_gemm_kernel<64, true>), grid, dim3(256), 0, stream, p);
     } else {
-        if (wide) hipLaunchKernelGGL((pf_gemm_kernel<128, false>), grid, dim3(256), 0, stream, p);
+        if (nt == 128) hipLaunchKernelGGL((pf_gemm_kernel<128, false>), grid, dim3(256), 0, stream, p);
         else hipLaunchKernelGGL((pf_gemm_kernel<64, false>), grid, dim3(256), 0, stream, p);
+    }
+    if (p.splits > 1) {
+        const uint64_t total = (uint64_t)p.T * p.n;
+        const uint32_t blocks = (uint32_t)std::min<uint64_t>(4096, (total + 255) / 256);
+        hipLaunchKernelGGL(pf_splitk_reduce_kernel, dim3(blocks), dim3(256), 0, stream, p);
     }
     return hipGetLastError();
 }
@@ -498,9 +534,23 @@ hipError_t launch_pf_rope_cache(const PrefillAttnParams& p, hipStream_t stream) 
 hipError_t launch_pf_attn(const PrefillAttnParams& p, hipStream_t stream) {
     if (p.T == 0) return hipSuccess;
     if (p.hd > (uint32_t)kAttnMaxHd || p.hd % 8 != 0 || p.H % p.KVH != 0) return hipErrorInvalidValue;
+    const uint32_t G = p.H / p.KVH;
+    if ((p.hd == 64 || p.hd == 128) && (G == 1 || G == 2 || G == 4)) {
+        const uint32_t qt = 16u * (4u / G);
+        const dim3 grid((p.T + qt - 1) / qt, p.KVH);
+#define QORA_PF_ATTN(HD)                                                                                     \
+    do {                                                                                                    \
+        if (p.kv_f16) hipLaunchKernelGGL((pf_attn_mfma_kernel<HD, true>), grid, dim3(256), 0, stream, p);   \
+        else hipLaunchKernelGGL((pf_attn_mfma_kernel<HD, false>), grid, dim3(256), 0, stream, p);           \
+    } while (0)
+        if (p.hd == 128) QORA_PF_ATTN(128);
+        else QORA_PF_ATTN(64);
+#undef QORA_PF_ATTN
+        return hipGetLastError();
+    }
     const dim3 grid((p.T + 31) / 32, p.H);
-    if (p.kv_f16) hipLaunchKernelGGL((pf_attn_kernel<true>), grid, dim3(256), 0, stream, p);
-    else hipLaunchKernelGGL((pf_attn_kernel<false>), grid, dim3(256), 0, stream, p);
+    if (p.kv_f16) hipLaunchKernelGGL((pf_attn_vec_kernel<true>), grid, dim3(256), 0, stream, p);
+    else hipLaunchKernelGGL((pf_attn_vec_kernel<false>), grid, dim3(256), 0, stream, p);
     return hipGetLastError();
 }
 

@@ -94,9 +94,17 @@ hipError_t launch_advance_pos(int32_t* pos, hipStream_t stream);
 // batched prefill (prefill.hpp)
 enum PfRow : int { PF_ROW_EMBED = 0, PF_ROW_RMSNORM = 1, PF_ROW_SPLIT = 2, PF_ROW_SILU = 3 };
 hipError_t launch_pf_rows(int kind, const PrefillRowParams& p, uint32_t T, hipStream_t stream);
-hipError_t launch_pf_weight_exp(const uint16_t* scales, uint32_t k, uint32_t groups, int8_t* wf, hipStream_t stream);
+// per-group weight exponents; scratch holds pf_weight_exp_scratch(k, groups) bytes
+uint64_t pf_weight_exp_scratch(uint32_t k, uint32_t groups);
+hipError_t launch_pf_weight_exp(const uint16_t* scales, uint32_t k, uint32_t groups, int8_t* wf, uint32_t* scratch,
+                                hipStream_t stream);
 bool pf_gemm_supported(uint32_t k, uint32_t n);
-hipError_t launch_pf_gemm(int fmt, const PrefillGemmParams& p, int cus, hipStream_t stream);
+struct PfGemmShape {
+    uint32_t nt, splits, kper;
+};
+PfGemmShape pf_gemm_shape(uint32_t T, uint32_t k, uint32_t n, int cus);
+// p.nt, p.splits, p.kper from pf_gemm_shape; p.part holds splits * T * n floats when splits > 1
+hipError_t launch_pf_gemm(int fmt, const PrefillGemmParams& p, hipStream_t stream);
 hipError_t launch_pf_rope_cache(const PrefillAttnParams& p, hipStream_t stream);
 hipError_t launch_pf_attn(const PrefillAttnParams& p, hipStream_t stream);
 

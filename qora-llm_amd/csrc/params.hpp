@@ -183,6 +183,12 @@ struct PrefillGemmParams {
     float* y;                  // [T][ldy]
     uint32_t ldy;
     int accumulate;            // 1: y += result (residual add)
+    // split K: grid.z = splits, split z takes rows [z kper, (z + 1) kper) and
+    // writes its partial to part[z][T][n]; pf_splitk_reduce_kernel sums the
+    // partials in split order into y
+    uint32_t splits, kper;
+    float* part;
+    uint32_t nt;               // column tile (64 or 128), from pf_gemm_shape
 };
 
 struct PrefillAttnParams {

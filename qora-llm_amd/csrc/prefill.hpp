@@ -144,14 +144,33 @@ __global__ __launch_bounds__(256) void pf_silu_split_kernel(PrefillRowParams p) 
 // ---------------------------------------------------------------------------
 // Per-group weight exponents f_g (Q4): |s[k][g] * (q - 8)| <= 2^(eb + 3) with
 // |s| <= 2^eb over the column group, so f_g = eb - 12 keeps |w'| <= 2^15.
-// One thread per group.
+// Two passes: blocks of 64 groups x 256 rows write the largest scale
+// magnitude bits of their rows to part[row block][group]; then one thread per
+// group reduces its row blocks.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void pf_weight_exp_kernel(const uint16_t* scales, uint32_t k, uint32_t groups,
+constexpr uint32_t kPfExpRows = 256;
+
+__global__ __launch_bounds__(256) void pf_weight_exp_part_kernel(const uint16_t* scales, uint32_t k, uint32_t groups,
+                                                                 uint32_t* part) {
+    __shared__ uint32_t red[4][kWave];
+    const uint32_t lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+    const uint32_t g = blockIdx.x * kWave + lane;
+    const uint32_t r0 = blockIdx.y * kPfExpRows, r1 = min(k, r0 + kPfExpRows);
+    uint32_t mx = 0;
+    if (g < groups)
+        for (uint32_t r = r0 + wave; r < r1; r += 4) mx = max(mx, (uint32_t)(scales[(uint64_t)r * groups + g] & 0x7FFFu));
+    red[wave][lane] = mx;
+    __syncthreads();
+    if (wave == 0 && g < groups)
+        part[(uint64_t)blockIdx.y * groups + g] = max(max(red[0][lane], red[1][lane]), max(red[2][lane], red[3][lane]));
+}
+
+__global__ __launch_bounds__(256) void pf_weight_exp_kernel(const uint32_t* part, uint32_t nblk, uint32_t groups,
                                                             int8_t* wf) {
     const uint32_t g = blockIdx.x * 256u + threadIdx.x;
     if (g >= groups) return;
     uint32_t mx = 0;
-    for (uint32_t r = 0; r < k; ++r) mx = max(mx, (uint32_t)(scales[(uint64_t)r * groups + g] & 0x7FFFu));
+    for (uint32_t b = 0; b < nblk; ++b) mx = max(mx, part[(uint64_t)b * groups + g]);
     const int e = (int)((mx >> 10) & 0x1F);
     const int eb = e == 0 ? -14 : e - 14;      // |s| <= 2^eb (infinities and NaN: e = 31)
     wf[g] = (int8_t)(eb - 12);
@@ -264,13 +283,14 @@ __global__ __launch_bounds__(256) void pf_gemm_kernel(PrefillGemmParams p) {
         for (int j = 0; j < TN; ++j) acc[i][j] = f32x4v{0.f, 0.f, 0.f, 0.f};
 
     const uint32_t li = (uint32_t)lane % 16u, kq = (uint32_t)lane / 16u;
-    const uint32_t steps = K / KC;
-    load_slice(0);
+    const uint32_t kb = blockIdx.z * p.kper;        // this split's rows [kb, kb + steps * KC)
+    const uint32_t steps = (min(K, kb + p.kper) - kb) / KC;
+    load_slice(kb);
     store_slice(0);
     __syncthreads();
     for (uint32_t s = 0; s < steps; ++s) {
         const int buf = (int)(s & 1u);
-        if (s + 1 < steps) load_slice((s + 1) * KC);
+        if (s + 1 < steps) load_slice(kb + (s + 1) * KC);
         half8v ah[2], al[2];
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
@@ -311,11 +331,28 @@ __global__ __launch_bounds__(256) void pf_gemm_kernel(PrefillGemmParams p) {
                 const uint32_t row = m0 + (uint32_t)wm * 32u + (uint32_t)i * 16u + kq * 4u + (uint32_t)r;
                 if (row >= p.T) continue;
                 const float v = ldexpf(acc[i][j][r], p.xe[row] + fg);
-                float* y = p.y + (uint64_t)row * p.ldy + c;
-                if (p.accumulate) *y += v;
-                else *y = v;
+                if (p.splits > 1) {
+                    p.part[((uint64_t)blockIdx.z * p.T + row) * N + c] = v;
+                } else {
+                    float* y = p.y + (uint64_t)row * p.ldy + c;
+                    if (p.accumulate) *y += v;
+                    else *y = v;
+                }
             }
         }
+    }
+}
+
+// Split-K partials summed in split order (deterministic), stored or added.
+__global__ __launch_bounds__(256) void pf_splitk_reduce_kernel(PrefillGemmParams p) {
+    const uint64_t total = (uint64_t)p.T * p.n;
+    for (uint64_t e = (uint64_t)blockIdx.x * 256u + threadIdx.x; e < total; e += (uint64_t)gridDim.x * 256u) {
+        float v = p.part[e];
+        for (uint32_t z = 1; z < p.splits; ++z) v += p.part[(uint64_t)z * total + e];
+        const uint64_t row = e / p.n, c = e % p.n;
+        float* y = p.y + row * p.ldy + c;
+        if (p.accumulate) *y += v;
+        else *y = v;
     }
 }
 
@@ -362,10 +399,11 @@ __global__ __launch_bounds__(256) void pf_rope_cache_kernel(PrefillAttnParams p)
 // tile, head): 32 queries x 32 keys per step from LDS, online softmax, 8
 // threads per query row (4 keys and hd/8 output dims each). The cache values
 // read back are the stored ones (binary16 for an f16 cache), as decode reads
-// them.
+// them. This VALU form covers every head shape; pf_attn_mfma_kernel below
+// takes head_dim 64 or 128 with 1, 2 or 4 query heads per KV head.
 // ---------------------------------------------------------------------------
 template <bool F16KV>
-__global__ __launch_bounds__(256) void pf_attn_kernel(PrefillAttnParams p) {
+__global__ __launch_bounds__(256) void pf_attn_vec_kernel(PrefillAttnParams p) {
     constexpr int QT = 32, KT = 32, HDM = kAttnMaxHd;
     constexpr int KSTR = HDM + 4;
     __shared__ __align__(16) float qs[QT * HDM];
@@ -464,6 +502,177 @@ __global__ __launch_bounds__(256) void pf_attn_kernel(PrefillAttnParams p) {
 #pragma unroll
     for (int i = 0; i < 16; ++i)
         if ((uint32_t)i < dpt) out[i] = o[i] * inv;
+}
+
+// ---------------------------------------------------------------------------
+// Causal prefill attention on the fp32 matrix cores (v_mfma_f32_16x16x4_f32:
+// exact products, fp32 accumulation). Block (query tile, KV head), 4 waves;
+// wave w takes query head kvh * G + w % G for 16 queries (sub-tile w / G), so
+// the G heads sharing a KV head share each K/V tile staged in LDS (64 keys
+// per step). Per wave and key tile: S = Q K^T (16 x 64, Q held in registers),
+// online softmax in registers, P through LDS into the A layout, O += P V
+// (16 x HD). The contraction index of step s in lane group g = l / 16 is
+// d = g HD/4 + s for Q K^T and key = 16 g + s for P V, so each lane reads its
+// operands as contiguous 16-byte runs.
+// Operand layouts of v_mfma_f32_16x16x4_f32 (lane l): A[i = l % 16][k = l / 16],
+// B[k = l / 16][j = l % 16], C[i = 4 (l / 16) + r][j = l % 16] in register r.
+// ---------------------------------------------------------------------------
+template <int HD, bool F16KV>
+__global__ __launch_bounds__(256) void pf_attn_mfma_kernel(PrefillAttnParams p) {
+    constexpr int KT = 64;                          // keys per step
+    constexpr int KS = HD + 4;                      // K row stride (floats)
+    constexpr int VS = HD + 1;                      // V row stride
+    constexpr int PS = KT + 4;                      // P row stride
+    constexpr int QS = HD / 4;                      // contraction steps of Q K^T
+    constexpr int OC = HD / 16;                     // 16-dim output tiles
+    __shared__ __align__(16) float ks[KT * KS];
+    __shared__ __align__(16) float vs[KT * VS];
+    __shared__ __align__(16) float ps[4][16 * PS];
+
+    const uint32_t t = threadIdx.x;
+    const uint32_t lane = t % kWave, g4 = lane / 16u, li = lane % 16u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(t / kWave);
+    const uint32_t G = p.H / p.KVH, kvh = blockIdx.y;
+    const uint32_t sub = wave / G;                  // query sub-tile of this wave
+    const uint32_t h = kvh * G + wave % G;
+    const uint32_t QT = 16u * (4u / G);             // queries per block
+    const uint32_t q0 = blockIdx.x * QT;            // chunk-relative first query of the block
+    const uint32_t qd = p.H * HD, kvd = p.KVH * HD;
+    const uint32_t nq = min(QT, p.T - q0);
+    const uint32_t last = p.pos0 + q0 + nq - 1u;    // last key any query of the block needs
+    const uint32_t wq0 = q0 + sub * 16u;            // this wave's first query
+    const bool wave_on = sub * 16u < nq;            // waves of a partial tile may hold no query
+
+    // Q fragment: lane holds q[wq0 + li][g4 * QS + s]
+    float qf[QS];
+    {
+        const uint32_t qi = min(wq0 + li, p.T - 1u);
+        const float* qrow = p.q + (uint64_t)qi * qd + (uint64_t)h * HD + g4 * QS;
+#pragma unroll
+        for (int s4 = 0; s4 < QS / 4; ++s4) {
+            const float4 v = *reinterpret_cast<const float4*>(qrow + 4 * s4);
+            qf[4 * s4] = v.x;
+            qf[4 * s4 + 1] = v.y;
+            qf[4 * s4 + 2] = v.z;
+            qf[4 * s4 + 3] = v.w;
+        }
+    }
+    float m[4], l[4];
+    f32x4v o[OC];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) { m[r] = -INFINITY; l[r] = 0.f; }
+#pragma unroll
+    for (int c = 0; c < OC; ++c) o[c] = f32x4v{0.f, 0.f, 0.f, 0.f};
+    float* pw = ps[wave];
+
+    for (uint32_t k0 = 0; k0 <= last; k0 += KT) {
+        __syncthreads();                            // the previous tiles are consumed
+        // stage K and V rows k0 .. k0 + 63 (clamped to `last`; masked below)
+        for (uint32_t e = t; e < (uint32_t)(KT * HD / 4); e += 256) {
+            const uint32_t r = e / (HD / 4), c4 = e % (HD / 4);
+            const uint64_t idx = (uint64_t)min(k0 + r, last) * kvd + (uint64_t)kvh * HD + 4u * c4;
+            float4 kv, vv;
+            if constexpr (F16KV) {
+                const uint2 a = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(p.kc) + idx);
+                const uint2 b = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(p.vc) + idx);
+                kv = make_float4(h2f((uint16_t)(a.x & 0xFFFFu)), h2f((uint16_t)(a.x >> 16)),
+                                 h2f((uint16_t)(a.y & 0xFFFFu)), h2f((uint16_t)(a.y >> 16)));
+                vv = make_float4(h2f((uint16_t)(b.x & 0xFFFFu)), h2f((uint16_t)(b.x >> 16)),
+                                 h2f((uint16_t)(b.y & 0xFFFFu)), h2f((uint16_t)(b.y >> 16)));
+            } else {
+                kv = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(p.kc) + idx);
+                vv = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(p.vc) + idx);
+            }
+            *reinterpret_cast<float4*>(&ks[r * KS + 4 * c4]) = kv;
+            float* vr = &vs[r * VS + 4 * c4];
+            vr[0] = vv.x;
+            vr[1] = vv.y;
+            vr[2] = vv.z;
+            vr[3] = vv.w;
+        }
+        __syncthreads();
+        if (!wave_on || k0 > p.pos0 + wq0 + 15u) continue;   // no key of this tile is visible to the wave
+        // ---- S = Q K^T: four 16 x 16 tiles ----
+        f32x4v sacc[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            sacc[c] = f32x4v{0.f, 0.f, 0.f, 0.f};
+            const float* krow = &ks[(16u * c + li) * KS + g4 * QS];
+#pragma unroll
+            for (int s4 = 0; s4 < QS / 4; ++s4) {
+                const float4 kb = *reinterpret_cast<const float4*>(krow + 4 * s4);
+                sacc[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(qf[4 * s4], kb.x, sacc[c], 0, 0, 0);
+                sacc[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(qf[4 * s4 + 1], kb.y, sacc[c], 0, 0, 0);
+                sacc[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(qf[4 * s4 + 2], kb.z, sacc[c], 0, 0, 0);
+                sacc[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(qf[4 * s4 + 3], kb.w, sacc[c], 0, 0, 0);
+            }
+        }
+        // ---- online softmax: lane holds rows 4 g4 + r, keys 16 c + li ----
+        float f[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t qpos = p.pos0 + wq0 + 4u * g4 + (uint32_t)r;
+            float sv[4];
+            float mx = -INFINITY;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const uint32_t kp = k0 + 16u * c + li;
+                sv[c] = kp <= qpos ? sacc[c][r] * p.scale : -INFINITY;
+                mx = fmaxf(mx, sv[c]);
+            }
+            mx = fmaxf(mx, __shfl_xor(mx, 1, kWave));
+            mx = fmaxf(mx, __shfl_xor(mx, 2, kWave));
+            mx = fmaxf(mx, __shfl_xor(mx, 4, kWave));
+            mx = fmaxf(mx, __shfl_xor(mx, 8, kWave));
+            const float m_new = fmaxf(m[r], mx);
+            const float mref = m_new == -INFINITY ? 0.f : m_new;   // a row with no visible key yet
+            f[r] = expf(m[r] - mref);
+            float sum = 0.f;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const float e = expf(sv[c] - mref);
+                pw[(4u * g4 + (uint32_t)r) * PS + 16u * c + li] = e;
+                sum += e;
+            }
+            sum += __shfl_xor(sum, 1, kWave);
+            sum += __shfl_xor(sum, 2, kWave);
+            sum += __shfl_xor(sum, 4, kWave);
+            sum += __shfl_xor(sum, 8, kWave);
+            l[r] = l[r] * f[r] + sum;
+            m[r] = m_new;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (int c = 0; c < OC; ++c)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) o[c][r] *= f[r];
+        // ---- O += P V: A = P[li][16 g4 + s], B = V[16 g4 + s][16 c + li] ----
+        const float* prow = &pw[li * PS + 16u * g4];
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4) {
+            const float4 pa = *reinterpret_cast<const float4*>(prow + 4 * s4);
+            const float pav[4] = {pa.x, pa.y, pa.z, pa.w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float* vrow = &vs[(16u * g4 + 4u * s4 + (uint32_t)j) * VS + li];
+#pragma unroll
+                for (int c = 0; c < OC; ++c)
+                    o[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(pav[j], vrow[16 * c], o[c], 0, 0, 0);
+            }
+        }
+    }
+    if (!wave_on) return;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const uint32_t qi = wq0 + 4u * g4 + (uint32_t)r;
+        if (qi >= q0 + nq) continue;
+        const float inv = 1.0f / l[r];
+        float* out = p.out + (uint64_t)qi * qd + (uint64_t)h * HD + li;
+#pragma unroll
+        for (int c = 0; c < OC; ++c) out[16 * c] = o[c][r] * inv;
+    }
 }
 
 }  // namespace qora
