@@ -320,6 +320,10 @@ def main():
                     help="time only the host-driven decode (skips the chained loop and the ~2048-context run)")
     ap.add_argument("--eager", action="store_true",
                     help="launch every kernel directly instead of replaying HIP graphs (for rocprofv3)")
+    ap.add_argument("--profile-prefill", action="store_true",
+                    help="only the 512-token batched prefill of the SmolLM3-3B model (for rocprofv3)")
+    ap.add_argument("--profile-long", action="store_true",
+                    help="only the decode at ~32768 positions with an f16 KV cache (for rocprofv3)")
     ap.add_argument("--profile-kernel", action="store_true",
                     help="only launch the dominant kernel (gate|up GEMV) eagerly, after a device copy of "
                          "known size, for hardware-counter runs")
@@ -334,6 +338,19 @@ def main():
         sys.exit(2)
     if args.profile_kernel:
         profile_kernel()
+        return
+    if args.profile_prefill or args.profile_long:
+        pkg = entry.load_package()
+        cfg = pkg.SMOLLM3_3B
+        w = pkg.synthetic_model(cfg, seed=0, rope_positions=2048)
+        ctx = pkg.HipContext(0)
+        if args.profile_prefill:
+            be = pkg.HipBackend(ctx, w, kv_capacity=2048, kv_dtype=pkg.KV_F32)
+            print(json.dumps({"profile_prefill": prefill_rate(be, ctx, pkg, cfg)}), flush=True)
+        else:
+            rate, _ = long_context_rate(ctx, pkg, w)
+            print(json.dumps({"profile_long_tok_s": round(rate, 2)}), flush=True)
+        ctx.close()
         return
     prompt_len, cap = 64, 2048
     if prompt_len + args.warmup + args.steps > cap:
