@@ -217,7 +217,19 @@ def extra_decode_rates(be, ctx, pkg, cfg, prompt, cap, steps):
     ctx.synchronize()
     tok_s_2048 = n_long / (time.perf_counter() - t0)
     print(f"# decode at ctx ~2048: {tok_s_2048:.1f} tok/s", file=sys.stderr, flush=True)
-    return chained, tok_s_2048
+    # sampled decode (main.rs defaults: T 0.7, top-p 0.95, top-k 20, penalties 1.1 / 1.5) on the device
+    be.kv_reset()
+    _, tok = be.raw_prefill(prompt, want_logits=False)
+    params = pkg.SampleParams(**pkg.DEFAULT_SAMPLING)
+    hist, st = [tok], 0x9E3779B97F4A7C15
+    ctx.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        _, tok, st = be.decode_sample(hist[-1], hist, params, st)
+        hist.append(tok)
+    sampled = steps / (time.perf_counter() - t0)
+    print(f"# sampled decode (device top-k/top-p + penalties): {sampled:.1f} tok/s", file=sys.stderr, flush=True)
+    return chained, tok_s_2048, sampled
 
 
 def prefill_rate(be, ctx, pkg, cfg, n=512, reps=3):
@@ -379,9 +391,9 @@ def main():
     tok_s = args.steps / dt
     print(f"# decode {tok_s:.1f} tok/s ({dt / args.steps * 1e3:.3f} ms/token)", file=sys.stderr, flush=True)
 
-    chained = tok_s_2048 = None
+    chained = tok_s_2048 = sampled = None
     if not args.decode_only:
-        chained, tok_s_2048 = extra_decode_rates(be, ctx, pkg, cfg, prompt, cap, args.steps)
+        chained, tok_s_2048, sampled = extra_decode_rates(be, ctx, pkg, cfg, prompt, cap, args.steps)
 
     prefill = None if args.decode_only else prefill_rate(be, ctx, pkg, cfg)
 
@@ -432,6 +444,7 @@ def main():
         "frac_of_weight_roofline": round(tok_s * weight_bytes / (HBM_PEAK_GBS * 1e9), 4),
         "tok_s_device_chained": round(chained, 2) if chained else None,
         "tok_s_ctx2048": round(tok_s_2048, 2) if tok_s_2048 else None,
+        "tok_s_sampled": round(sampled, 2) if sampled else None,
         "tok_s_ctx32768_f16kv": round(long_rate, 2) if long_rate else None,
         "prefill_512": prefill,
         "frac_of_roofline_ctx32768": (round(long_rate * long_bytes / (HBM_PEAK_GBS * 1e9), 4)

@@ -111,6 +111,32 @@ int qora_hip_decode(qora_hip_ctx* ctx, uint32_t token, float* logits_or_null, ui
  * argmax of step i. */
 int qora_hip_generate_greedy(qora_hip_ctx* ctx, uint32_t token, uint32_t steps, uint32_t* tokens_out);
 
+/* Sampling settings of generate_raw (GenerateParams, generate.rs:15-35;
+ * defaults main.rs:130-141). */
+typedef struct {
+    float temperature;          /* <= 0: greedy, the first-max rule */
+    float top_p;                /* nucleus mass, e.g. 0.95 */
+    uint32_t top_k;             /* 1 .. 64 (the reference default is 20) */
+    float repetition_penalty;   /* <= 1: off; once per occurrence in the last 64 history tokens */
+    float presence_penalty;     /* <= 0: off; once for every token present in the history */
+} qora_sample_params;
+
+/* apply_repetition_penalty, then apply_presence_penalty, then
+ * sample_token_top_k (generate.rs:64-91, 345-395) on device logits [vocab]
+ * (vocab <= 131072; the logits are not modified): history is the host array
+ * of generated tokens, rng_state the Rng (xorshift64, generate.rs:38-61)
+ * state, advanced in place by the one draw a sampled token takes. The
+ * reference seeds it from the clock; callers pass any non-zero seed. */
+int qora_hip_sample(qora_hip_ctx* ctx, const float* logits, uint64_t vocab, const uint32_t* history,
+                    uint64_t n_history, const qora_sample_params* params, uint64_t* rng_state, uint32_t* token,
+                    void* stream);
+
+/* qora_hip_decode followed by qora_hip_sample on the step's logits, which
+ * stay on the device (copied out only if logits_or_null is given). */
+int qora_hip_decode_sample(qora_hip_ctx* ctx, uint32_t token, const uint32_t* history, uint64_t n_history,
+                           const qora_sample_params* params, uint64_t* rng_state, float* logits_or_null,
+                           uint32_t* token_out);
+
 /* How decode steps run on this context (no counterpart in the reference):
  * 0 = no model, 1 = one captured graph of kernels per step (the default),
  * 2 = one persistent launch per step (opt-in, QORA_HIP_DECODE=mk at

@@ -755,3 +755,103 @@ int oq_prefill(const oq_model_desc* m, oq_kv* kv, const uint32_t* ids, uint64_t 
     free(x); free(xn); free(qa); free(attn); free(o); free(gate); free(upv);
     return 0;
 }
+
+
+/* ---- sampling (generate.rs:38-91, 345-395) ---- */
+
+/* Rng::next_f32 (generate.rs:54-60): xorshift64 (13, 7, 17), top 24 bits. */
+float oq_rng_next_f32(uint64_t* state) {
+    uint64_t x = *state;
+    x ^= x << 13;
+    x ^= x >> 7;
+    x ^= x << 17;
+    *state = x;
+    return (float)(uint32_t)(x >> 40) / 16777216.0f;
+}
+
+/* apply_repetition_penalty (generate.rs:64-78): the last min(len, 64) tokens,
+ * one penalty per occurrence. */
+void oq_repetition_penalty(float* logits, uint64_t vocab, const uint32_t* gen, uint64_t n, float penalty) {
+    if (penalty <= 1.0f) return;
+    const uint64_t window = n < 64 ? n : 64;
+    for (uint64_t i = n - window; i < n; ++i) {
+        const uint32_t idx = gen[i];
+        if (idx < vocab) {
+            if (logits[idx] > 0.0f) logits[idx] /= penalty;
+            else logits[idx] *= penalty;
+        }
+    }
+}
+
+/* apply_presence_penalty (generate.rs:80-91): once per distinct token present. */
+void oq_presence_penalty(float* logits, uint64_t vocab, const uint32_t* gen, uint64_t n, float penalty) {
+    if (penalty <= 0.0f || n == 0) return;
+    unsigned char* seen = (unsigned char*)calloc(vocab, 1);
+    for (uint64_t i = 0; i < n; ++i)
+        if (gen[i] < vocab) seen[gen[i]] = 1;
+    for (uint64_t i = 0; i < vocab; ++i)
+        if (seen[i]) logits[i] -= penalty;
+    free(seen);
+}
+
+typedef struct {
+    uint32_t id;
+    float v;
+} oq_cand;
+
+/* sort_by(b.1.partial_cmp(&a.1)) is a stable sort by value descending: equal
+ * values keep ascending index order. */
+static int oq_cand_cmp(const void* a, const void* b) {
+    const oq_cand* x = (const oq_cand*)a;
+    const oq_cand* y = (const oq_cand*)b;
+    if (x->v > y->v) return -1;
+    if (x->v < y->v) return 1;
+    return x->id < y->id ? -1 : (x->id > y->id ? 1 : 0);
+}
+
+/* sample_token_top_k (generate.rs:345-395). */
+uint32_t oq_sample_top_k(const float* logits, uint64_t vocab, float temperature, float top_p, uint64_t top_k,
+                         uint64_t* rng) {
+    if (temperature <= 0.0f) {
+        uint64_t best = 0;
+        float bv = -INFINITY;
+        for (uint64_t i = 0; i < vocab; ++i)
+            if (logits[i] > bv) { bv = logits[i]; best = i; }
+        return (uint32_t)best;
+    }
+    const float inv_temp = 1.0f / temperature;
+    float max_logit = -INFINITY;
+    for (uint64_t i = 0; i < vocab; ++i) max_logit = fmaxf(max_logit, logits[i]);
+    oq_cand* c = (oq_cand*)malloc(vocab * sizeof(oq_cand));
+    for (uint64_t i = 0; i < vocab; ++i) { c[i].id = (uint32_t)i; c[i].v = logits[i]; }
+    qsort(c, vocab, sizeof(oq_cand), oq_cand_cmp);
+    const uint64_t k = top_k > 0 ? (top_k < vocab ? top_k : vocab) : vocab;
+    float* p = (float*)malloc(k * sizeof(float));
+    float sum = 0.0f;
+    for (uint64_t i = 0; i < k; ++i) { p[i] = expf((c[i].v - max_logit) * inv_temp); sum += p[i]; }
+    uint32_t out = c[0].id;
+    if (sum > 0.0f) {
+        const float inv = 1.0f / sum;
+        for (uint64_t i = 0; i < k; ++i) p[i] *= inv;
+        float cum = 0.0f;
+        uint64_t cutoff = k;
+        for (uint64_t i = 0; i < k; ++i) {
+            cum += p[i];
+            if (cum >= top_p) { cutoff = i + 1; break; }
+        }
+        float total = 0.0f;
+        for (uint64_t i = 0; i < cutoff; ++i) total += p[i];
+        if (total > 0.0f) {
+            const float rand_val = oq_rng_next_f32(rng) * total;
+            float acc = 0.0f;
+            out = c[0].id;
+            for (uint64_t i = 0; i < cutoff; ++i) {
+                acc += p[i];
+                if (acc >= rand_val) { out = c[i].id; break; }
+            }
+        }
+    }
+    free(p);
+    free(c);
+    return out;
+}

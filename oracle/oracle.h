@@ -128,6 +128,14 @@ const float* oq_kv_k(const oq_kv* kv, uint32_t layer);
 const float* oq_kv_v(const oq_kv* kv, uint32_t layer);
 int oq_kv_set(oq_kv* kv, uint32_t layer, const float* k, const float* v, uint64_t len);
 
+/* sampling (generate.rs:38-91, 345-395) */
+float oq_rng_next_f32(uint64_t* state);
+void oq_repetition_penalty(float* logits, uint64_t vocab, const uint32_t* gen, uint64_t n, float penalty);
+void oq_presence_penalty(float* logits, uint64_t vocab, const uint32_t* gen, uint64_t n, float penalty);
+uint32_t oq_sample_top_k(const float* logits, uint64_t vocab, float temperature, float top_p, uint64_t top_k,
+                         uint64_t* rng);
+
+
 /* forward_decode_raw (gemv.rs:872-1019). T = rayon thread count. Returns 0
  * on success, -1 if the cache is full. logits: [vocab]. */
 int oq_forward_decode(const oq_model_desc* m, oq_kv* kv, uint32_t token,

@@ -56,6 +56,10 @@ _SIGS = {
     "oq_kv_k": (_P, [_P, _U32]),
     "oq_kv_v": (_P, [_P, _U32]),
     "oq_kv_set": (_I, [_P, _U32, _P, _P, _U64]),
+    "oq_rng_next_f32": (ctypes.c_float, [_P]),
+    "oq_repetition_penalty": (None, [_P, _U64, _P, _U64, ctypes.c_float]),
+    "oq_presence_penalty": (None, [_P, _U64, _P, _U64, ctypes.c_float]),
+    "oq_sample_top_k": (_U32, [_P, _U64, ctypes.c_float, ctypes.c_float, _U64, _P]),
     "oq_forward_decode": (_I, [ctypes.POINTER(OqModelDesc), _P, _U32, _I, _I, _P]),
     "oq_prefill": (_I, [ctypes.POINTER(OqModelDesc), _P, _P, _U64, _I, _P]),
     "oq_set_threads": (None, [_I]),
@@ -277,6 +281,27 @@ class OracleModel:
             toks.append(argmax(logits))
             gaps.append(top2_gap(logits))
         return toks, gaps
+
+
+def rng_next_f32(state):
+    """Rng::next_f32 (generate.rs:54-60); returns (value, new state)."""
+    st = ctypes.c_uint64(state)
+    v = lib().oq_rng_next_f32(ctypes.byref(st))
+    return v, st.value
+
+
+def sample(logits, history, temperature, top_p, top_k, repetition_penalty, presence_penalty, rng_state):
+    """apply_repetition_penalty, apply_presence_penalty, sample_token_top_k
+    (generate.rs:64-91, 345-395) on a copy; returns (token, new rng state).
+    Penalties apply only when sampling (temperature > 0), as at generate.rs:132-136."""
+    lg = np.ascontiguousarray(logits, dtype=np.float32).copy()
+    h = np.ascontiguousarray(np.asarray(history, dtype=np.uint32))
+    if temperature > 0:
+        lib().oq_repetition_penalty(_p(lg), lg.size, _p(h), h.size, repetition_penalty)
+        lib().oq_presence_penalty(_p(lg), lg.size, _p(h), h.size, presence_penalty)
+    st = ctypes.c_uint64(rng_state)
+    tok = lib().oq_sample_top_k(_p(lg), lg.size, temperature, top_p, top_k, ctypes.byref(st))
+    return int(tok), st.value
 
 
 def top2_gap(logits):

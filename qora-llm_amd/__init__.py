@@ -114,6 +114,8 @@ SIGNATURES = {
     "qora_hip_attn_decode": (_I, [_P, _P, _P, _P, _I, _U32, _U32, _U32, _U32, _P, _P]),
     "qora_hip_gemm": (_I, [_P, _U32, _P, _P, _U64, _P]),
     "qora_hip_attn_prefill": (_I, [_P, _P, _P, _P, _I, _U32, _U32, _U32, _U32, _U32, _P, _P]),
+    "qora_hip_sample": (_I, [_P, _P, _U64, _P, _U64, _P, _P, _P, _P]),
+    "qora_hip_decode_sample": (_I, [_P, _U32, _P, _U64, _P, _P, _P, _P]),
     "qora_hip_argmax": (_I, [_P, _P, _U64, _P, _P]),
     "qora_synth_q4": (None, [_U64, _U64, _U64, _U64, _P, _P]),
     "qora_synth_f16": (None, [_U64, _U64, _U64, _F, _P]),
@@ -449,6 +451,17 @@ class HipContext:
         self.check(self.lib.qora_hip_lm_head_run(self.h, lm_id, x_dev, logits_dev, argmax_dev or None,
                                                  stream or None), "lm_head_run")
 
+    def sample(self, logits_dev: int, vocab: int, history: Sequence[int], params: "SampleParams",
+               rng_state: int):
+        """Penalties and top-k/top-p sampling of device logits; returns (token, new rng state)."""
+        hist = np.ascontiguousarray(np.asarray(history, dtype=np.uint32))
+        st = ctypes.c_uint64(rng_state)
+        tok = ctypes.c_uint32()
+        self.check(self.lib.qora_hip_sample(self.h, logits_dev, vocab, _ptr(hist) if hist.size else None, hist.size,
+                                            ctypes.byref(params), ctypes.byref(st), ctypes.byref(tok), None),
+                   "sample")
+        return tok.value, st.value
+
     def weight_ptrs(self, wid: int):
         a, b = ctypes.c_void_p(), ctypes.c_void_p()
         self.check(self.lib.qora_hip_weight_ptrs(self.h, wid, ctypes.byref(a), ctypes.byref(b)), "weight_ptrs")
@@ -468,6 +481,17 @@ class HipContext:
 
     def graph_destroy(self, g: int) -> None:
         self.check(self.lib.qora_hip_graph_destroy(self.h, g), "graph_destroy")
+
+
+class SampleParams(ctypes.Structure):
+    """qora_sample_params: GenerateParams' sampling fields (generate.rs:15-35)."""
+
+    _fields_ = [("temperature", ctypes.c_float), ("top_p", ctypes.c_float), ("top_k", ctypes.c_uint32),
+                ("repetition_penalty", ctypes.c_float), ("presence_penalty", ctypes.c_float)]
+
+
+# main.rs:130-141 defaults
+DEFAULT_SAMPLING = dict(temperature=0.7, top_p=0.95, top_k=20, repetition_penalty=1.1, presence_penalty=1.5)
 
 
 class HipBackend:
@@ -541,6 +565,20 @@ class HipBackend:
         v = np.empty((max(n, 1), kvd), dtype=np.float32)
         self.ctx.check(self.ctx.lib.qora_hip_kv_download(self.ctx.h, layer, _ptr(k), _ptr(v)), "kv_download")
         return k[:n], v[:n]
+
+    def decode_sample(self, token_id: int, history: Sequence[int], params: "SampleParams", rng_state: int,
+                      want_logits: bool = False):
+        """One decode step, then the penalties and top-k/top-p sampling on the
+        device; returns (logits or None, token, new rng state)."""
+        hist = np.ascontiguousarray(np.asarray(history, dtype=np.uint32))
+        logits = np.empty(self.config.vocab, dtype=np.float32) if want_logits else None
+        st = ctypes.c_uint64(rng_state)
+        tok = ctypes.c_uint32()
+        self.ctx.check(self.ctx.lib.qora_hip_decode_sample(self.ctx.h, int(token_id), _ptr(hist) if hist.size else None,
+                                                           hist.size, ctypes.byref(params), ctypes.byref(st),
+                                                           _ptr(logits) if want_logits else None, ctypes.byref(tok)),
+                       "decode_sample")
+        return logits, tok.value, st.value
 
     def kv_upload(self, layer: int, k: np.ndarray, v: np.ndarray) -> None:
         """Sets one layer's cache rows [0, len) from f32 [len][kv_heads*head_dim]

@@ -8,6 +8,7 @@
 #include <cstring>
 #include <cstdio>
 #include <string>
+#include <unordered_map>
 #include <vector>
 
 using namespace qora;
@@ -122,6 +123,14 @@ struct qora_hip_ctx {
     std::vector<DevWeight> weights;
     long long* ws_acc = nullptr;         // kernel-level fixed-point accumulator
     uint64_t ws_acc_n = 0;
+    // on-device sampling scratch (grown to the largest vocab seen)
+    float* smp_work = nullptr;
+    unsigned long long* smp_cand = nullptr;
+    unsigned long long* smp_rng = nullptr;
+    int32_t* smp_tok = nullptr;
+    SamplePenalty* smp_pen = nullptr;
+    uint32_t smp_vocab = 0;
+    uint64_t smp_pen_n = 0;
     void* ws_pf = nullptr;               // kernel-level GEMM: split operand and group exponents
     uint64_t ws_pf_bytes = 0;
     float* ws_attn_part = nullptr;
@@ -392,7 +401,8 @@ extern "C" int qora_hip_destroy(qora_hip_ctx* c) {
         if (w.w) (void)hipFree(w.w);
         if (w.scales) (void)hipFree(w.scales);
     }
-    for (void* p : {(void*)c->ws_acc, (void*)c->ws_attn_part, c->ws_pf})
+    for (void* p : {(void*)c->ws_acc, (void*)c->ws_attn_part, c->ws_pf, (void*)c->smp_work, (void*)c->smp_cand,
+                    (void*)c->smp_rng, (void*)c->smp_tok, (void*)c->smp_pen})
         if (p) (void)hipFree(p);
     if (c->h_pin) (void)hipHostFree(c->h_pin);
     (void)hipStreamDestroy(c->stream);
@@ -1866,6 +1876,123 @@ extern "C" int qora_hip_attn_prefill(qora_hip_ctx* c, const float* q, const void
     a.out = out;
     HIP_TRY(c, launch_pf_attn(a, pick_stream(c, stream)));
     return QORA_HIP_OK;
+}
+
+namespace {
+
+// Penalty list and device scratch for one sampling call, then the kernels;
+// the token and the advanced rng state come back to the host.
+int sample_device(qora_hip_ctx* c, const float* logits, uint64_t vocab, const uint32_t* history, uint64_t n_history,
+                  const qora_sample_params* sp, uint64_t* rng_state, uint32_t* token, hipStream_t s) {
+    if (!logits || !sp || !rng_state || !token || (n_history && !history))
+        return fail(c, QORA_HIP_E_INVALID, "null argument");
+    if (vocab == 0 || vocab > 0xFFFFFFFFull || !smp_supported((uint32_t)vocab))
+        return fail(c, QORA_HIP_E_INVALID, "sampling supports vocab <= 131072");
+    if (sp->top_k == 0 || sp->top_k > 64) return fail(c, QORA_HIP_E_INVALID, "top_k must be 1 .. 64");
+    if (c->capturing) return fail(c, QORA_HIP_E_STATE, "sampling copies to the host: not allowed during capture");
+    const bool greedy = !(sp->temperature > 0.0f);
+    const bool rep = !greedy && sp->repetition_penalty > 1.0f;
+    const bool pres = !greedy && sp->presence_penalty > 0.0f;
+    // distinct history tokens with their penalties (apply_repetition_penalty walks the last 64
+    // tokens, apply_presence_penalty every token; ids >= vocab are skipped, generate.rs:68, 85)
+    std::vector<SamplePenalty> pen;
+    {
+        std::unordered_map<uint32_t, size_t> at;
+        auto entry = [&](uint32_t t) -> SamplePenalty& {
+            auto it = at.find(t);
+            if (it != at.end()) return pen[it->second];
+            at.emplace(t, pen.size());
+            pen.push_back(SamplePenalty{t, 0, 0, 0});
+            return pen.back();
+        };
+        if (rep)
+            for (uint64_t i = n_history - std::min<uint64_t>(64, n_history); i < n_history; ++i)
+                if (history[i] < vocab) entry(history[i]).rep_count += 1;
+        if (pres)
+            for (uint64_t i = 0; i < n_history; ++i)
+                if (history[i] < vocab) entry(history[i]).seen = 1;
+    }
+    const uint32_t V = (uint32_t)vocab, blocks = smp_blocks(V);
+    if (V > c->smp_vocab || !c->smp_rng) {
+        HIP_TRY(c, hipStreamSynchronize(c->stream));
+        for (void* q : {(void*)c->smp_work, (void*)c->smp_cand, (void*)c->smp_rng, (void*)c->smp_tok})
+            if (q) (void)hipFree(q);
+        c->smp_work = nullptr;
+        c->smp_cand = nullptr;
+        c->smp_rng = nullptr;
+        c->smp_tok = nullptr;
+        c->smp_vocab = 0;
+        void* q = nullptr;
+        if (int rc = dalloc(c, (size_t)V * 4, &q)) return rc;
+        c->smp_work = (float*)q;
+        if (int rc = dalloc(c, (size_t)blocks * 64 * 8, &q)) return rc;
+        c->smp_cand = (unsigned long long*)q;
+        if (int rc = dalloc(c, 256, &q)) return rc;
+        c->smp_rng = (unsigned long long*)q;
+        c->smp_tok = (int32_t*)((uint8_t*)q + 64);
+        c->smp_vocab = V;
+    }
+    if (pen.size() > c->smp_pen_n) {
+        HIP_TRY(c, hipStreamSynchronize(c->stream));
+        if (c->smp_pen) (void)hipFree(c->smp_pen);
+        c->smp_pen = nullptr;
+        c->smp_pen_n = 0;
+        void* q = nullptr;
+        const uint64_t n = std::max<uint64_t>(pen.size(), 1024);
+        if (int rc = dalloc(c, n * sizeof(SamplePenalty), &q)) return rc;
+        c->smp_pen = (SamplePenalty*)q;
+        c->smp_pen_n = n;
+    }
+    if (!pen.empty()) HIP_TRY(c, hipMemcpyAsync(c->smp_pen, pen.data(), pen.size() * sizeof(SamplePenalty),
+                                                hipMemcpyHostToDevice, s));
+    HIP_TRY(c, hipMemcpyAsync(c->smp_rng, rng_state, 8, hipMemcpyHostToDevice, s));
+    SampleParams p{};
+    p.work = c->smp_work;
+    p.vocab = V;
+    p.pen = c->smp_pen;
+    p.n_pen = (uint32_t)pen.size();
+    p.repetition = sp->repetition_penalty;
+    p.presence = sp->presence_penalty;
+    p.cand = c->smp_cand;
+    p.blocks = blocks;
+    p.temperature = sp->temperature;
+    p.top_p = sp->top_p;
+    p.top_k = sp->top_k;
+    p.rng = c->smp_rng;
+    p.token_out = c->smp_tok;
+    HIP_TRY(c, launch_sample(logits, p, s));
+    HIP_TRY(c, hipMemcpyAsync(&c->h_pin[20], c->smp_tok, 4, hipMemcpyDeviceToHost, s));
+    HIP_TRY(c, hipMemcpyAsync(&c->h_pin[22], c->smp_rng, 8, hipMemcpyDeviceToHost, s));
+    HIP_TRY(c, hipStreamSynchronize(s));
+    *token = (uint32_t)c->h_pin[20];
+    std::memcpy(rng_state, &c->h_pin[22], 8);
+    return QORA_HIP_OK;
+}
+
+}  // namespace
+
+extern "C" int qora_hip_sample(qora_hip_ctx* c, const float* logits, uint64_t vocab, const uint32_t* history,
+                               uint64_t n_history, const qora_sample_params* params, uint64_t* rng_state,
+                               uint32_t* token, void* stream) {
+    if (!c) return QORA_HIP_E_INVALID;
+    return sample_device(c, logits, vocab, history, n_history, params, rng_state, token, pick_stream(c, stream));
+}
+
+extern "C" int qora_hip_decode_sample(qora_hip_ctx* c, uint32_t token, const uint32_t* history, uint64_t n_history,
+                                      const qora_sample_params* params, uint64_t* rng_state, float* logits,
+                                      uint32_t* token_out) {
+    if (!c) return QORA_HIP_E_INVALID;
+    if (!params || !rng_state || !token_out) return fail(c, QORA_HIP_E_INVALID, "null argument");
+    if (int rc = check_step_room(c, 1)) return rc;
+    ModelState& m = c->m;
+    if (token >= m.vocab) return fail(c, QORA_HIP_E_INVALID, "token id out of range");
+    c->h_pin[0] = (int32_t)token;
+    HIP_TRY(c, hipMemcpyAsync(m.d_token, &c->h_pin[0], 4, hipMemcpyHostToDevice, c->stream));
+    if (int rc = launch_step(c, true)) return rc;
+    uint32_t greedy = 0;
+    if (int rc = finish_step(c, logits, &greedy)) return rc;
+    m.host_pos += 1;
+    return sample_device(c, m.d_logits, m.vocab, history, n_history, params, rng_state, token_out, c->stream);
 }
 
 extern "C" int qora_hip_argmax(qora_hip_ctx* c, const float* logits, uint64_t n, int32_t* out, void* stream) {

@@ -6,6 +6,7 @@
 #include "decode_mk.hpp"
 #include "attn.hpp"
 #include "prefill.hpp"
+#include "sample.hpp"
 
 #include <algorithm>
 #include <cstdlib>
@@ -551,6 +552,22 @@ hipError_t launch_pf_attn(const PrefillAttnParams& p, hipStream_t stream) {
     const dim3 grid((p.T + 31) / 32, p.H);
     if (p.kv_f16) hipLaunchKernelGGL((pf_attn_vec_kernel<true>), grid, dim3(256), 0, stream, p);
     else hipLaunchKernelGGL((pf_attn_vec_kernel<false>), grid, dim3(256), 0, stream, p);
+    return hipGetLastError();
+}
+
+// ---- on-device sampling ----
+
+uint32_t smp_blocks(uint32_t vocab) { return (vocab + kSmpBlock - 1) / kSmpBlock; }
+bool smp_supported(uint32_t vocab) { return vocab > 0 && smp_blocks(vocab) * kSmpKeep <= kSmpFinal; }
+
+hipError_t launch_sample(const float* logits, const SampleParams& p, hipStream_t stream) {
+    if (!smp_supported(p.vocab) || p.blocks != smp_blocks(p.vocab) || p.top_k == 0 || p.top_k > kSmpKeep)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(smp_copy_kernel, dim3(std::min<uint32_t>(1024, (p.vocab + 255) / 256)), dim3(256), 0, stream,
+                       logits, p.work, p.vocab);
+    if (p.n_pen) hipLaunchKernelGGL(smp_penalty_kernel, dim3((p.n_pen + 255) / 256), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL(smp_block_topk_kernel, dim3(p.blocks), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL(smp_final_kernel, dim3(1), dim3(256), 0, stream, p);
     return hipGetLastError();
 }
 

@@ -108,4 +108,9 @@ hipError_t launch_pf_gemm(int fmt, const PrefillGemmParams& p, hipStream_t strea
 hipError_t launch_pf_rope_cache(const PrefillAttnParams& p, hipStream_t stream);
 hipError_t launch_pf_attn(const PrefillAttnParams& p, hipStream_t stream);
 
+// on-device sampling (sample.hpp): vocab <= 131072, 1 <= top_k <= 64
+uint32_t smp_blocks(uint32_t vocab);
+bool smp_supported(uint32_t vocab);
+hipError_t launch_sample(const float* logits, const SampleParams& p, hipStream_t stream);
+
 }  // namespace qora

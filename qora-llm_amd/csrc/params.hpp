@@ -208,6 +208,28 @@ struct PrefillAttnParams {
     float* out;                // attention output [T][qd]
 };
 
+// On-device sampling (sample.hpp).
+struct SamplePenalty {
+    uint32_t token;
+    uint32_t rep_count;        // occurrences in the last 64 history tokens (repetition penalty)
+    uint32_t seen;             // 1: the presence penalty applies
+    uint32_t pad_;
+};
+
+struct SampleParams {
+    float* work;               // [vocab] penalised copy of the logits
+    uint32_t vocab;
+    const SamplePenalty* pen;  // distinct history tokens
+    uint32_t n_pen;
+    float repetition, presence;
+    unsigned long long* cand;  // [blocks][kSmpKeep] per-block best keys
+    uint32_t blocks;
+    float temperature, top_p;
+    uint32_t top_k;
+    unsigned long long* rng;   // xorshift64 state, updated in place
+    int32_t* token_out;
+};
+
 struct ArgmaxFinishParams {
     const float* part_val;
     const uint32_t* part_idx;

@@ -1,0 +1,148 @@
+// On-device sampling: the penalties and sample_token_top_k of generate.rs
+// (apply_repetition_penalty 64-70, apply_presence_penalty 80-91,
+// sample_token_top_k 345-395, Rng 38-61) on the step's logits, so a sampled
+// decode step returns a token instead of the 513 KB logits vector.
+//
+// 1. smp_copy_kernel + smp_penalty_kernel: a scratch copy of the logits; for
+//    each distinct history token, the repetition penalty once per occurrence in
+//    the last 64 tokens (x / p for x > 0, else x * p, in sequence) and then
+//    the presence penalty once if the token occurs anywhere.
+// 2. smp_block_topk_kernel: each block sorts 2048 (value, index) keys in LDS
+//    (bitonic) and keeps its best kSmpKeep. Keys order by value descending,
+//    then index ascending: the order of the reference's stable sort_by on
+//    partial_cmp. NaN ranks last.
+// 3. smp_final_kernel: one block sorts the blocks' candidates, keeps top_k,
+//    and one thread runs the reference's arithmetic in the reference's order
+//    (softmax over the top k against the global max, nucleus cut-off, one
+//    xorshift64 draw, linear scan). Greedy (temperature <= 0) takes the first
+//    candidate: the first-max rule.
+#pragma once
+
+#include "common.hpp"
+#include "params.hpp"
+
+namespace qora {
+
+constexpr uint32_t kSmpBlock = 2048;    // logits per block in the first pass
+constexpr uint32_t kSmpKeep = 64;       // candidates kept per block (top_k <= kSmpKeep)
+constexpr uint32_t kSmpFinal = 4096;    // candidate keys sorted by the final block
+
+// Orderable key: ascending key = value descending, then index ascending.
+__device__ __forceinline__ unsigned long long smp_key(float v, uint32_t idx) {
+    uint32_t b = __float_as_uint(v);
+    if (v != v) b = 0xFF800000u;                       // NaN ranks as -inf, after every number
+    if (v == 0.0f) b = 0u;                             // -0 == +0: the index decides, as in a stable sort
+    const uint32_t ord = (b & 0x80000000u) ? ~b : (b | 0x80000000u);   // ascending with the value
+    return ((unsigned long long)(~ord) << 32) | idx;
+}
+__device__ __forceinline__ float smp_key_value(unsigned long long k) {
+    const uint32_t ord = ~(uint32_t)(k >> 32);
+    const uint32_t b = (ord & 0x80000000u) ? (ord & 0x7FFFFFFFu) : ~ord;
+    return __uint_as_float(b);
+}
+
+// In-place ascending bitonic sort of n (power of two) keys in LDS by 256 threads.
+template <uint32_t N>
+__device__ __forceinline__ void smp_bitonic(unsigned long long* keys) {
+    for (uint32_t size = 2; size <= N; size <<= 1) {
+        for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
+            __syncthreads();
+            for (uint32_t i = threadIdx.x; i < N / 2; i += 256) {
+                const uint32_t lo = 2 * i - (i & (stride - 1));
+                const uint32_t hi = lo + stride;
+                const bool up = (lo & size) == 0;
+                const unsigned long long a = keys[lo], b = keys[hi];
+                if ((a > b) == up) {
+                    keys[lo] = b;
+                    keys[hi] = a;
+                }
+            }
+        }
+    }
+    __syncthreads();
+}
+
+__global__ __launch_bounds__(256) void smp_copy_kernel(const float* in, float* out, uint32_t n) {
+    for (uint32_t i = blockIdx.x * 256u + threadIdx.x; i < n; i += gridDim.x * 256u) out[i] = in[i];
+}
+
+__global__ __launch_bounds__(256) void smp_penalty_kernel(SampleParams p) {
+    const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+    if (i >= p.n_pen) return;
+    const SamplePenalty e = p.pen[i];
+    float x = p.work[e.token];
+    for (uint32_t r = 0; r < e.rep_count; ++r) x = x > 0.0f ? x / p.repetition : x * p.repetition;
+    if (e.seen) x -= p.presence;
+    p.work[e.token] = x;
+}
+
+__global__ __launch_bounds__(256) void smp_block_topk_kernel(SampleParams p) {
+    __shared__ unsigned long long keys[kSmpBlock];
+    const uint32_t base = blockIdx.x * kSmpBlock;
+    for (uint32_t j = threadIdx.x; j < kSmpBlock; j += 256) {
+        const uint32_t i = base + j;
+        keys[j] = i < p.vocab ? smp_key(p.work[i], i) : ~0ull;
+    }
+    smp_bitonic<kSmpBlock>(keys);
+    for (uint32_t j = threadIdx.x; j < kSmpKeep; j += 256) p.cand[blockIdx.x * kSmpKeep + j] = keys[j];
+}
+
+__global__ __launch_bounds__(256) void smp_final_kernel(SampleParams p) {
+    __shared__ unsigned long long keys[kSmpFinal];
+    const uint32_t nc = p.blocks * kSmpKeep;
+    for (uint32_t j = threadIdx.x; j < kSmpFinal; j += 256) keys[j] = j < nc ? p.cand[j] : ~0ull;
+    smp_bitonic<kSmpFinal>(keys);
+    if (threadIdx.x != 0) return;
+    const uint32_t k = min(p.top_k, min(p.vocab, kSmpKeep));
+    uint32_t token = (uint32_t)keys[0];
+    unsigned long long state = *p.rng;
+    if (p.temperature > 0.0f) {
+        // softmax over the top k (generate.rs:360-370)
+        const float inv_temp = 1.0f / p.temperature;
+        const float max_logit = smp_key_value(keys[0]);
+        float prob[kSmpKeep];
+        float sum = 0.0f;
+        for (uint32_t i = 0; i < k; ++i) {
+            prob[i] = expf((smp_key_value(keys[i]) - max_logit) * inv_temp);
+            sum += prob[i];
+        }
+        if (sum > 0.0f) {
+            const float inv = 1.0f / sum;
+            for (uint32_t i = 0; i < k; ++i) prob[i] *= inv;
+            // nucleus cut-off (generate.rs:372-380)
+            float cum = 0.0f;
+            uint32_t cutoff = k;
+            for (uint32_t i = 0; i < k; ++i) {
+                cum += prob[i];
+                if (cum >= p.top_p) {
+                    cutoff = i + 1;
+                    break;
+                }
+            }
+            float total = 0.0f;
+            for (uint32_t i = 0; i < cutoff; ++i) total += prob[i];
+            if (total > 0.0f) {
+                // one xorshift64 draw (Rng::next_f32, generate.rs:54-60) and the scan (382-393)
+                state ^= state << 13;
+                state ^= state >> 7;
+                state ^= state << 17;
+                const float rand_val = (float)(uint32_t)(state >> 40) / 16777216.0f * total;
+                float acc = 0.0f;
+                bool hit = false;
+                for (uint32_t i = 0; i < cutoff; ++i) {
+                    acc += prob[i];
+                    if (acc >= rand_val) {
+                        token = (uint32_t)keys[i];
+                        hit = true;
+                        break;
+                    }
+                }
+                if (!hit) token = (uint32_t)keys[0];
+            }
+        }
+    }
+    *p.rng = state;
+    *p.token_out = (int32_t)token;
+}
+
+}  // namespace qora

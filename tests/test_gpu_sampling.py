@@ -1,0 +1,92 @@
+"""On-device sampling (qora_hip_sample, qora_hip_decode_sample) against the
+oracle's restatement of generate.rs:38-91, 345-395 on the same logits: the
+same token and the same Rng state, draw for draw."""
+import numpy as np
+import pytest
+
+import __graft_entry__ as entry
+from helpers import device
+
+pytestmark = pytest.mark.gpu
+
+SETTINGS = [
+    dict(temperature=0.7, top_p=0.95, top_k=20, repetition_penalty=1.1, presence_penalty=1.5),   # main.rs defaults
+    dict(temperature=1.3, top_p=1.0, top_k=64, repetition_penalty=1.0, presence_penalty=0.0),
+    dict(temperature=0.35, top_p=0.5, top_k=5, repetition_penalty=1.3, presence_penalty=0.0),
+    dict(temperature=0.0, top_p=0.95, top_k=20, repetition_penalty=1.1, presence_penalty=1.5),   # greedy
+    dict(temperature=0.9, top_p=0.95, top_k=1, repetition_penalty=1.1, presence_penalty=0.5),
+]
+
+
+@pytest.mark.parametrize("vocab", [128256, 1000, 4097])
+@pytest.mark.parametrize("si", range(len(SETTINGS)))
+def test_sample_matches_oracle(ctx, pkg, orc, vocab, si):
+    sp = SETTINGS[si]
+    print(f"case sample vocab={vocab} settings={si}", flush=True)
+    r = np.random.default_rng(vocab + si)
+    params = pkg.SampleParams(**sp)
+    st_gpu = st_orc = 0x2545F4914F6CDD1D + si
+    with device(ctx) as d:
+        for trial in range(40):
+            lg = (r.standard_normal(vocab) * 2.5).astype(np.float32)
+            hist = r.integers(0, vocab, size=int(r.integers(0, 150))).tolist()
+            hist += hist[-5:] * 2                 # repeats inside the last-64 window
+            dl = d.put(lg)
+            tok, st_gpu = ctx.sample(dl, vocab, hist, params, st_gpu)
+            want, st_orc = orc.sample(lg, hist, sp["temperature"], sp["top_p"], sp["top_k"],
+                                      sp["repetition_penalty"], sp["presence_penalty"], st_orc)
+            assert tok == want, trial
+            assert st_gpu == st_orc
+
+
+def test_sample_ties_and_zero_signs(ctx, pkg, orc):
+    vocab = 3000
+    lg = np.full(vocab, -5.0, np.float32)
+    lg[[2999, 17, 2048, 700]] = 4.0                 # four-way tie for the maximum
+    lg[5] = -0.0
+    lg[6] = 0.0
+    greedy = pkg.SampleParams(temperature=0.0, top_p=0.95, top_k=20, repetition_penalty=1.1, presence_penalty=1.5)
+    top1 = pkg.SampleParams(temperature=0.8, top_p=0.95, top_k=1, repetition_penalty=1.0, presence_penalty=0.0)
+    with device(ctx) as d:
+        dl = d.put(lg)
+        assert ctx.sample(dl, vocab, [], greedy, 9)[0] == 17
+        assert ctx.sample(dl, vocab, [], top1, 9)[0] == 17
+        st = 11
+        for _ in range(30):
+            sp = dict(temperature=2.0, top_p=1.0, top_k=6, repetition_penalty=1.0, presence_penalty=0.0)
+            tok, st2 = ctx.sample(dl, vocab, [], pkg.SampleParams(**sp), st)
+            want, st3 = orc.sample(lg, [], 2.0, 1.0, 6, 1.0, 0.0, st)
+            assert tok == want and st2 == st3
+            st = st2
+
+
+def test_sample_errors(ctx, pkg):
+    with device(ctx) as d:
+        dl = d.put(np.zeros(300000, np.float32))
+        bad_k = pkg.SampleParams(temperature=0.7, top_p=0.9, top_k=0, repetition_penalty=1.0, presence_penalty=0.0)
+        ok = pkg.SampleParams(temperature=0.7, top_p=0.9, top_k=20, repetition_penalty=1.0, presence_penalty=0.0)
+        with pytest.raises(pkg.QoraHipError):
+            ctx.sample(dl, 1000, [], bad_k, 1)
+        with pytest.raises(pkg.QoraHipError):
+            ctx.sample(dl, 300000, [], ok, 1)      # beyond the supported vocabulary
+
+
+def test_decode_sample_matches_decode_plus_oracle_sampling(ctx, pkg, orc):
+    """A sampled generation on the device equals, token for token, the decode
+    step's logits sampled by the oracle with the same Rng stream."""
+    cfg = entry.smoke_config(pkg)
+    w = pkg.synthetic_model(cfg, seed=5, rope_positions=64)
+    prompt = pkg.synth_tokens(5, 2000, 9, cfg.vocab)
+    sp = dict(temperature=0.9, top_p=0.95, top_k=20, repetition_penalty=1.1, presence_penalty=1.5)
+    params = pkg.SampleParams(**sp)
+    be = pkg.HipBackend(ctx, w, kv_capacity=64)
+    _, tok = be.raw_prefill(prompt, want_logits=False)
+    hist, st, toks = [tok], 4242, []
+    for _ in range(24):
+        logits, nxt, st_new = be.decode_sample(hist[-1], hist, params, st, want_logits=True)
+        want, st_want = orc.sample(logits, hist, sp["temperature"], sp["top_p"], sp["top_k"],
+                                   sp["repetition_penalty"], sp["presence_penalty"], st)
+        assert nxt == want and st_new == st_want
+        hist.append(nxt)
+        st = st_new
+    assert be.kv_len() == len(prompt) + 24
