@@ -123,7 +123,9 @@ typedef struct {
 
 /* apply_repetition_penalty, then apply_presence_penalty, then
  * sample_token_top_k (generate.rs:64-91, 345-395) on device logits [vocab]
- * (vocab <= 131072; the logits are not modified): history is the host array
+ * (vocab <= 131072; the logits are not modified). The penalties apply only
+ * when temperature > 0, as at every call site (generate.rs:141-145, 216-235).
+ * history is the host array
  * of generated tokens, rng_state the Rng (xorshift64, generate.rs:38-61)
  * state, advanced in place by the one draw a sampled token takes. The
  * reference seeds it from the clock; callers pass any non-zero seed. */
