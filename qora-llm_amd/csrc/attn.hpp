@@ -29,6 +29,15 @@ namespace qora {
 // Limits (checked on the host): head_dim <= 128, groups <= 4.
 // ---------------------------------------------------------------------------
 
+// Cache element (pos, kvh, d) at pos * ps + kvh * hs + d: the layout the
+// caller declares (AttnParams::kv_ps / kv_hs), token-major by default.
+__device__ __forceinline__ uint64_t kv_pos_stride(const AttnParams& p) {
+    return p.kv_ps ? p.kv_ps : (uint64_t)p.KVH * p.hd;
+}
+__device__ __forceinline__ uint64_t kv_head_off(const AttnParams& p, uint32_t kvh) {
+    return (uint64_t)kvh * (p.kv_ps ? p.kv_hs : (uint64_t)p.hd);
+}
+
 // RoPE partner of dim d (rotate_half over the first 2*half dims,
 // apply_rope_raw gemv.rs:869-887): rotated = v[d] * c + sgn * v[partner] * s,
 // with c, s the table entries of dim d mod half. Dims past 2*half pass
@@ -46,7 +55,7 @@ struct KvTileRegs {
 
 template <int TL, bool F16KV>
 __device__ __forceinline__ KvTileRegs<TL> attn_load_tile(const AttnParams& p, uint32_t t, uint32_t c0, uint32_t L,
-                                                          uint64_t kv_stride, uint64_t head_off, uint32_t q4_row,
+                                                          uint64_t pos_stride, uint64_t head_base, uint32_t q4_row,
                                                           uint32_t tile_n) {
     KvTileRegs<TL> r;
 #pragma unroll
@@ -54,7 +63,7 @@ __device__ __forceinline__ KvTileRegs<TL> attn_load_tile(const AttnParams& p, ui
         const uint32_t e = min(t + (uint32_t)(256 * j), tile_n - 1u);
         const uint32_t row = e / q4_row, c4 = e % q4_row;
         const uint32_t pos = min(c0 + row, L - 1u);
-        const uint64_t idx = (uint64_t)pos * kv_stride + head_off + 4u * c4;
+        const uint64_t idx = (uint64_t)pos * pos_stride + head_base + 4u * c4;
         if constexpr (F16KV) {
             const uint2 a = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(p.kc) + idx);
             const uint2 b = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(p.vc) + idx);
@@ -131,8 +140,9 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnParams p) {
     const uint32_t kvh = blockIdx.y;
     const uint32_t hd = p.hd, G = p.groups;
     const bool model = p.qkv_acc != nullptr;
-    const uint64_t kv_stride = (uint64_t)p.KVH * hd;
+    const uint64_t kv_stride = (uint64_t)p.KVH * hd;    // q|k|v accumulator layout
     const uint64_t head_off = (uint64_t)kvh * hd;
+    const uint64_t cps = kv_pos_stride(p), coff = kv_head_off(p, kvh);   // cache layout
     const uint32_t nq = G * hd;
 
     // ---- position-independent loads, in flight with the position ----
@@ -182,7 +192,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnParams p) {
         kc_ = ct[td];
         ks_ = st[td];
     }
-    KvTileRegs<TL> tr = attn_load_tile<TL, F16KV>(p, threadIdx.x, p0, L, kv_stride, head_off, q4_row, tile_n);
+    KvTileRegs<TL> tr = attn_load_tile<TL, F16KV>(p, threadIdx.x, p0, L, cps, coff, q4_row, tile_n);
 
     // K padding columns [hd, HDM) stay zero for the whole kernel
     if (hd < (uint32_t)HDM)
@@ -215,7 +225,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnParams p) {
             const float a = inv * from_fixed(ka), b = inv * from_fixed(kb);
             float kv = (rot && dn < 2 * p.half) ? (dn < p.half ? a * kc_ - b * ks_ : a * kc_ + b * ks_) : a;
             float vv = inv * from_fixed(va);
-            const uint64_t idx = (uint64_t)cur * kv_stride + head_off + dn;
+            const uint64_t idx = (uint64_t)cur * cps + coff + dn;
             if constexpr (F16KV) {
                 const uint16_t kh = f2h(kv), vh = f2h(vv);
                 reinterpret_cast<uint16_t*>(p.kc)[idx] = kh;
@@ -256,7 +266,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnParams p) {
         }
         __syncthreads();
         if (c0 + SUB < p1)                            // next pass, in flight during this one
-            tr = attn_load_tile<TL, F16KV>(p, threadIdx.x, c0 + SUB, L, kv_stride, head_off, q4_row, tile_n);
+            tr = attn_load_tile<TL, F16KV>(p, threadIdx.x, c0 + SUB, L, cps, coff, q4_row, tile_n);
         if (g < G) {
             // q.k for position c0 + r_lane over padded dims [dq0, dq0 + HDM/2)
             const float* qg = qs + g * HDM + dq0;
@@ -329,7 +339,7 @@ struct KvRaw {
 
 template <int TL, bool F16KV>
 __device__ __forceinline__ void attn_load_raw(KvRaw<TL, F16KV>& r, const AttnParams& p, uint32_t t, uint32_t c0,
-                                              uint32_t L, uint64_t kv_stride, uint64_t head_off, uint32_t q4_row,
+                                              uint32_t L, uint64_t pos_stride, uint64_t head_base, uint32_t q4_row,
                                               uint32_t tile_n) {
     using W = typename KvRaw<TL, F16KV>::W;
     constexpr uint32_t wb = F16KV ? 2u : 4u;   // bytes per element
@@ -338,7 +348,7 @@ __device__ __forceinline__ void attn_load_raw(KvRaw<TL, F16KV>& r, const AttnPar
         const uint32_t e = min(t + (uint32_t)(256 * j), tile_n - 1u);
         const uint32_t row = e / q4_row, c4 = e % q4_row;
         const uint32_t pos = min(c0 + row, L - 1u);
-        const uint64_t off = ((uint64_t)pos * kv_stride + head_off + 4u * c4) * wb;
+        const uint64_t off = ((uint64_t)pos * pos_stride + head_base + 4u * c4) * wb;
         r.k[j] = *reinterpret_cast<const W*>(reinterpret_cast<const uint8_t*>(p.kc) + off);
         r.v[j] = *reinterpret_cast<const W*>(reinterpret_cast<const uint8_t*>(p.vc) + off);
     }
@@ -423,8 +433,9 @@ __global__ __launch_bounds__(256 * kAttnLongNsg) void attn_decode_long_kernel(At
     const uint32_t hd = p.hd, G = p.groups;
     const bool model = p.qkv_acc != nullptr;
     const bool lead = sg == 0;                       // subgroup 0 sets up q and the appended row
-    const uint64_t kv_stride = (uint64_t)p.KVH * hd;
+    const uint64_t kv_stride = (uint64_t)p.KVH * hd;    // q|k|v accumulator layout
     const uint64_t head_off = (uint64_t)kvh * hd;
+    const uint64_t cps = kv_pos_stride(p), coff = kv_head_off(p, kvh);   // cache layout
     const uint32_t nq = G * hd;
 
     // ---- position-independent loads, in flight with the position ----
@@ -484,8 +495,8 @@ __global__ __launch_bounds__(256 * kAttnLongNsg) void attn_decode_long_kernel(At
 #pragma unroll
     for (int d = 0; d < DEPTH; ++d)
         if ((uint32_t)sg + (uint32_t)(d * NSG) < npass)
-            attn_load_raw<TL, F16KV>(tr[d], p, t, p0 + ((uint32_t)sg + (uint32_t)(d * NSG)) * SUB, L, kv_stride,
-                                     head_off, q4_row, tile_n);
+            attn_load_raw<TL, F16KV>(tr[d], p, t, p0 + ((uint32_t)sg + (uint32_t)(d * NSG)) * SUB, L, cps, coff,
+                                     q4_row, tile_n);
 
     // K padding columns [hd, HDM) stay zero for the whole kernel
     if (hd < (uint32_t)HDM)
@@ -517,7 +528,7 @@ __global__ __launch_bounds__(256 * kAttnLongNsg) void attn_decode_long_kernel(At
             const float a = inv * from_fixed(ka), b = inv * from_fixed(kb);
             float kv = (rot && dn < 2 * p.half) ? (dn < p.half ? a * kc_ - b * ks_ : a * kc_ + b * ks_) : a;
             float vv = inv * from_fixed(va);
-            const uint64_t idx = (uint64_t)cur * kv_stride + head_off + dn;
+            const uint64_t idx = (uint64_t)cur * cps + coff + dn;
             if constexpr (F16KV) {
                 const uint16_t kh = f2h(kv), vh = f2h(vv);
                 reinterpret_cast<uint16_t*>(p.kc)[idx] = kh;
@@ -569,7 +580,7 @@ __global__ __launch_bounds__(256 * kAttnLongNsg) void attn_decode_long_kernel(At
         }
         __syncthreads();
         if (pi + DEPTH * NSG < npass)                  // in flight during the next DEPTH passes
-            attn_load_raw<TL, F16KV>(rt, p, t, c0 + DEPTH * NSG * SUB, L, kv_stride, head_off, q4_row, tile_n);
+            attn_load_raw<TL, F16KV>(rt, p, t, c0 + DEPTH * NSG * SUB, L, cps, coff, q4_row, tile_n);
         if (active && g < G) {
             // q.k for position c0 + r_lane over padded dims [dq0, dq0 + HDM/2)
             const float* qg = qs + g * HDM + dq0;
@@ -667,6 +678,249 @@ __global__ __launch_bounds__(256 * kAttnLongNsg) void attn_decode_long_kernel(At
     if (lane == 0) {
         part[hd] = m;
         part[hd + 1] = l;
+    }
+}
+
+// Long contexts with an f16 cache: no LDS staging of the cache. Block (KV
+// head, split) of NWV waves; wave w takes the 32-position passes w, w + NWV,
+// ... of the split. Every lane works on the same slice of the row throughout:
+// lane (c, j) = (l % 16, l / 16) holds dims [c HD/16, (c + 1) HD/16) of
+// positions 4 i + j (i < 8) of the pass, so each K and V load instruction
+// reads 4 whole rows (1 KB at HD 128) and a lane's scores are those of the
+// very positions whose V it holds: the probabilities never leave the lane.
+// Partial dot products are summed over the 16 lanes of a row (4 shuffles),
+// the online softmax runs per wave for the G query heads, and the waves'
+// (max, sum, p.V) states are merged in wave order at the end. The appended
+// row (model mode) comes from LDS, and positions at or past the split's end
+// never reach a sum (selection, not a zero weight: stale slots may hold NaN).
+template <int HD>
+__global__ __launch_bounds__(512) void attn_decode_direct_kernel(AttnParams p) {
+    constexpr int NWV = 8;                           // waves per block
+    constexpr int PP = 32;                           // positions per pass
+    constexpr int VD = HD / 16;                      // dims per lane
+    constexpr int NI = PP / 4;                       // rows per lane per pass
+    constexpr int G4 = kAttnMaxGroups;
+    typedef typename std::conditional<VD == 8, uint4, uint2>::type VW;
+    __shared__ __align__(16) float qs[G4 * HD];
+    __shared__ float knew[HD], vnew[HD];
+    __shared__ __align__(16) float red_o[NWV][G4][HD];
+    __shared__ float red_m[NWV][G4], red_l[NWV][G4];
+
+    const uint32_t t = threadIdx.x;
+    const uint32_t lane = t % kWave;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(t / kWave);
+    // grid (KVH, splits)
+    const uint32_t kvh = blockIdx.x, split = blockIdx.y;
+    const uint32_t hd = HD, G = p.groups;
+    const bool model = p.qkv_acc != nullptr;
+    const uint64_t kv_stride = (uint64_t)p.KVH * HD;    // q|k|v accumulator layout
+    const uint64_t head_off = (uint64_t)kvh * HD;
+    const uint64_t cps = kv_pos_stride(p), coff = kv_head_off(p, kvh);   // cache layout
+
+    const int32_t pos_raw = p.pos ? *p.pos : (int32_t)p.L - 1;
+    const uint32_t L = (uint32_t)pos_raw + 1u;
+    const uint32_t chunk = p.chunk ? p.chunk : attn_chunk_for(L);
+    const uint32_t p0 = split * chunk;
+    if (p0 >= L) return;                               // whole block: no barrier reached yet
+    const uint32_t p1 = min(L, p0 + chunk);
+    const uint32_t cur = L - 1;
+    const bool has_new = model && cur >= p0 && cur < p1;
+    const uint32_t npass = (p1 - p0 + PP - 1) / PP;
+
+    // ---- q of the G heads (rotated, RMSNorm factor applied) and the appended row: threads 0..255 ----
+    if (t < 256) {
+        if (model) {
+            const uint32_t qd = p.H * hd;
+            const float inv = 1.0f / sqrtf(wave_sum(lane < p.ss_n ? p.ss_in[lane] : 0.f) / (float)p.norm_n + 1e-6f);
+            const bool rot = p.use_rope != 0;
+            const float* ct = p.rope_cos + (uint64_t)cur * p.half;
+            const float* st = p.rope_sin + (uint64_t)cur * p.half;
+            auto rotated = [&](const long long* src, uint32_t d) -> float {
+                const float a = inv * from_fixed(src[d]);
+                if (!rot || d >= 2 * p.half) return a;
+                const float b = inv * from_fixed(src[rope_partner(d, p.half)]);
+                const uint32_t td = d < p.half ? d : d - p.half;
+                return d < p.half ? a * ct[td] - b * st[td] : a * ct[td] + b * st[td];
+            };
+            for (uint32_t i = t; i < G * hd; i += 256)
+                qs[(i / hd) * HD + i % hd] = rotated(p.qkv_acc + (uint64_t)kvh * G * hd + (i / hd) * hd, i % hd);
+            if (has_new && t < hd) {
+                float kv = rotated(p.qkv_acc + qd + head_off, t);
+                float vv = inv * from_fixed(p.qkv_acc[qd + kv_stride + head_off + t]);
+                const uint16_t kh = f2h(kv), vh = f2h(vv);
+                const uint64_t idx = (uint64_t)cur * cps + coff + t;
+                reinterpret_cast<uint16_t*>(p.kc)[idx] = kh;
+                reinterpret_cast<uint16_t*>(p.vc)[idx] = vh;
+                knew[t] = h2f(kh);                   // the stored values, as later steps read them
+                vnew[t] = h2f(vh);
+            }
+        } else {
+            for (uint32_t i = t; i < G * hd; i += 256)
+                qs[(i / hd) * HD + i % hd] = p.q[(uint64_t)(kvh * G + i / hd) * hd + i % hd];
+        }
+    }
+    __syncthreads();
+
+    const uint32_t vc = lane % 16, vj = lane / 16;    // dim slice, position phase
+    float qv[G4][VD];
+#pragma unroll
+    for (int g = 0; g < G4; ++g)
+#pragma unroll
+        for (int d = 0; d < VD; ++d) qv[g][d] = (uint32_t)g < G ? qs[g * HD + vc * VD + d] : 0.f;
+    float m[G4], l[G4], o[G4][VD];
+#pragma unroll
+    for (int g = 0; g < G4; ++g) {
+        m[g] = -INFINITY;
+        l[g] = 0.f;
+#pragma unroll
+        for (int d = 0; d < VD; ++d) o[g][d] = 0.f;
+    }
+    const uint16_t* kc = reinterpret_cast<const uint16_t*>(p.kc);
+    const uint16_t* vcache = reinterpret_cast<const uint16_t*>(p.vc);
+    for (uint32_t pi = wave; pi < npass; pi += NWV) {
+        const uint32_t c0 = p0 + pi * PP;
+        const uint32_t cn = min((uint32_t)PP, p1 - c0);
+        VW kr[NI], vr[NI];
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const uint64_t off = (uint64_t)min(c0 + 4u * i + vj, p1 - 1u) * cps + coff + vc * VD;
+            kr[i] = *reinterpret_cast<const VW*>(kc + off);
+            vr[i] = *reinterpret_cast<const VW*>(vcache + off);
+        }
+        // ---- scores of the lane's positions: partial dots, summed over the row's 16 lanes ----
+        float s[NI][G4];
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const uint32_t pos = c0 + 4u * i + vj;
+            float k[VD];
+            if constexpr (VD == 8) {
+                const uint32_t w4[4] = {kr[i].x, kr[i].y, kr[i].z, kr[i].w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    k[2 * e] = h2f((uint16_t)(w4[e] & 0xFFFFu));
+                    k[2 * e + 1] = h2f((uint16_t)(w4[e] >> 16));
+                }
+            } else {
+                const uint32_t w2[2] = {kr[i].x, kr[i].y};
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
+                    k[2 * e] = h2f((uint16_t)(w2[e] & 0xFFFFu));
+                    k[2 * e + 1] = h2f((uint16_t)(w2[e] >> 16));
+                }
+            }
+            if (has_new && pos == cur) {
+#pragma unroll
+                for (int d = 0; d < VD; ++d) k[d] = knew[vc * VD + d];
+            }
+#pragma unroll
+            for (int g = 0; g < G4; ++g) {
+                float a = 0.f;
+#pragma unroll
+                for (int d = 0; d < VD; ++d) a = fmaf(qv[g][d], k[d], a);
+                a += __shfl_xor(a, 1, kWave);
+                a += __shfl_xor(a, 2, kWave);
+                a += __shfl_xor(a, 4, kWave);
+                a += __shfl_xor(a, 8, kWave);
+                s[i][g] = 4u * i + vj < cn ? a * p.scale : -INFINITY;
+            }
+        }
+        // ---- online softmax per head over the pass ----
+        float f[G4];
+#pragma unroll
+        for (int g = 0; g < G4; ++g) {
+            float mx = s[0][g];
+#pragma unroll
+            for (int i = 1; i < NI; ++i) mx = fmaxf(mx, s[i][g]);
+            mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
+            mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+            const float m_new = fmaxf(m[g], mx);
+            f[g] = expf(m[g] - m_new);              // 0 on the first pass
+            float sum = 0.f;
+#pragma unroll
+            for (int i = 0; i < NI; ++i) {
+                const float e = 4u * i + vj < cn ? expf(s[i][g] - m_new) : 0.f;
+                s[i][g] = e;
+                sum += e;
+            }
+            sum += __shfl_xor(sum, 16, kWave);
+            sum += __shfl_xor(sum, 32, kWave);
+            l[g] = l[g] * f[g] + sum;
+            m[g] = m_new;
+        }
+        // ---- o[g] = o[g] f[g] + sum over the lane's positions of e V ----
+#pragma unroll
+        for (int g = 0; g < G4; ++g)
+#pragma unroll
+            for (int d = 0; d < VD; ++d) o[g][d] *= f[g];
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            if (4u * i + vj >= cn) continue;
+            float v[VD];
+            if constexpr (VD == 8) {
+                const uint32_t w4[4] = {vr[i].x, vr[i].y, vr[i].z, vr[i].w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    v[2 * e] = h2f((uint16_t)(w4[e] & 0xFFFFu));
+                    v[2 * e + 1] = h2f((uint16_t)(w4[e] >> 16));
+                }
+            } else {
+                const uint32_t w2[2] = {vr[i].x, vr[i].y};
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
+                    v[2 * e] = h2f((uint16_t)(w2[e] & 0xFFFFu));
+                    v[2 * e + 1] = h2f((uint16_t)(w2[e] >> 16));
+                }
+            }
+            if (has_new && c0 + 4u * i + vj == cur) {
+#pragma unroll
+                for (int d = 0; d < VD; ++d) v[d] = vnew[vc * VD + d];
+            }
+#pragma unroll
+            for (int g = 0; g < G4; ++g)
+#pragma unroll
+                for (int d = 0; d < VD; ++d) o[g][d] = fmaf(s[i][g], v[d], o[g][d]);
+        }
+    }
+    // ---- this wave's totals: sum the four position phases (lanes c, c + 16, c + 32, c + 48) ----
+#pragma unroll
+    for (int g = 0; g < G4; ++g)
+#pragma unroll
+        for (int d = 0; d < VD; ++d) {
+            float v = o[g][d];
+            v += __shfl_xor(v, 16, kWave);
+            v += __shfl_xor(v, 32, kWave);
+            o[g][d] = v;
+        }
+    if (vj == 0) {
+#pragma unroll
+        for (int g = 0; g < G4; ++g)
+#pragma unroll
+            for (int d = 0; d < VD; ++d) red_o[wave][g][vc * VD + d] = o[g][d];
+    }
+    if (lane == 0) {
+#pragma unroll
+        for (int g = 0; g < G4; ++g) {
+            red_m[wave][g] = m[g];
+            red_l[wave][g] = l[g];
+        }
+    }
+    __syncthreads();
+    // ---- merge the waves in order: thread (g, d) ----
+    if (t >= G * HD) return;
+    const uint32_t g = t / HD, d = t % HD;
+    float mx = -INFINITY;
+    for (int w = 0; w < NWV; ++w) mx = fmaxf(mx, red_m[w][g]);
+    float acc = 0.f, lt = 0.f;
+    for (int w = 0; w < NWV; ++w) {
+        const float wt = expf(red_m[w][g] - mx);   // 0 for a wave without passes
+        acc = fmaf(red_o[w][g][d], wt, acc);
+        lt = fmaf(red_l[w][g], wt, lt);
+    }
+    float* part = p.part + (((uint64_t)kvh * p.s_max + split) * G + g) * (hd + 2);
+    part[d] = acc;
+    if (d == 0) {
+        part[hd] = mx;
+        part[hd + 1] = lt;
     }
 }
 

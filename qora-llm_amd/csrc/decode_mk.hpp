@@ -489,8 +489,9 @@ __device__ __forceinline__ bool mk_attn_phase(const MkParams& p, const MkLayer& 
     const int wave = t / 64;
     const uint32_t kvh = item / s_act, split = item % s_act;
     const uint32_t hd = p.hd, G = p.G, nq = G * hd, qd = p.H * hd;
-    const uint64_t kv_stride = (uint64_t)p.KVH * hd;
+    const uint64_t kv_stride = (uint64_t)p.KVH * hd;    // q|k|v accumulator layout
     const uint64_t head_off = (uint64_t)kvh * hd;
+    const uint64_t cps = p.kv_ps, coff = (uint64_t)kvh * p.kv_hs;   // cache layout
     const uint32_t p0 = split * p.chunk;
     const uint32_t p1 = min(L, p0 + p.chunk);
     const uint32_t cur = L - 1;
@@ -503,7 +504,7 @@ __device__ __forceinline__ bool mk_attn_phase(const MkParams& p, const MkLayer& 
     ap.hd = hd;
     // waves 0..3: the first cache tile (independent of this step's q, k, v)
     KvTileRegs<TL> tr;
-    if (t < NTT) tr = attn_load_tile<TL, F16KV>(ap, threadIdx.x, p0, L, kv_stride, head_off, q4_row, tile_n);
+    if (t < NTT) tr = attn_load_tile<TL, F16KV>(ap, threadIdx.x, p0, L, cps, coff, q4_row, tile_n);
     const long long* Qb = bf.Q + (uint64_t)l * (qd + 2 * kv_stride);
     if (wave == kMkNW) {
         // control wave: q of the group's heads and the appended k, v, normalised and rotated
@@ -579,7 +580,7 @@ __device__ __forceinline__ bool mk_attn_phase(const MkParams& p, const MkLayer& 
             if (has_new) {
                 // the appended row goes into the cache (read by later steps)
                 for (uint32_t d = (uint32_t)lane; d < hd; d += 64) {
-                    const uint64_t idx = (uint64_t)cur * kv_stride + head_off + d;
+                    const uint64_t idx = (uint64_t)cur * cps + coff + d;
                     if constexpr (F16KV) {
                         const uint16_t kh = f2h(sm.kapp[d]), vh = f2h(sm.vapp[d]);
                         reinterpret_cast<uint16_t*>(ly.kc)[idx] = kh;
@@ -626,7 +627,7 @@ __device__ __forceinline__ bool mk_attn_phase(const MkParams& p, const MkLayer& 
         }
         __syncthreads();
         if (c0 + SUB < p1 && t < NTT)
-            tr = attn_load_tile<TL, F16KV>(ap, threadIdx.x, c0 + SUB, L, kv_stride, head_off, q4_row, tile_n);
+            tr = attn_load_tile<TL, F16KV>(ap, threadIdx.x, c0 + SUB, L, cps, coff, q4_row, tile_n);
         if (g < G) {
             const float* qg = sm.qs + g * HDM + dq0;
             const float* krow = sm.ktile + r_lane * KSTR + dq0;

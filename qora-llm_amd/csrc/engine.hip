@@ -604,6 +604,8 @@ int setup_mk(qora_hip_ctx* c, const qora_model_desc* d, const DevWeight* emb, ui
     P.vocab = m.vocab;
     P.chunk = m.attn_chunk;
     P.s_max = m.attn_s_max;
+    P.kv_ps = m.hd;                      // head-major cache: [KVH][cap][hd] per layer
+    P.kv_hs = (uint64_t)m.cap * m.hd;
     P.kv_f16 = m.kv_f16;
     P.rope_cos = m.d_cos;
     P.rope_sin = m.d_sin;
@@ -860,6 +862,8 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
         a.part = m.d_attn_part;
         a.s_max = m.attn_s_max;
         a.nsg = attn_nsg(m.attn_chunk);
+        a.kv_ps = m.hd;                  // head-major cache: [KVH][cap][hd] per layer
+        a.kv_hs = (uint64_t)m.cap * m.hd;
 
         GemvParams& o = m.p_o[l];
         o = GemvParams{};
@@ -1270,6 +1274,8 @@ int prefill_batched(qora_hip_ctx* c, size_t n, float* logits, uint32_t* argmax) 
             a.hd = m.hd;
             a.scale = 1.0f / sqrtf((float)m.hd);
             a.out = m.d_pf_ao;
+            a.kv_ps = m.hd;
+            a.kv_hs = (uint64_t)m.cap * m.hd;
             HIP_TRY(c, launch_pf_rope_cache(a, s));
             HIP_TRY(c, launch_pf_attn(a, s));
             PrefillRowParams sr{};
@@ -1366,19 +1372,29 @@ extern "C" int qora_hip_kv_upload(qora_hip_ctx* c, uint32_t layer, const float* 
     const size_t kvd = (size_t)m.KVH * m.hd;
     const size_t count = (size_t)len * kvd;
     if (count) {
+        // host: token-major [len][KVH][hd] f32; device: head-major [KVH][cap][hd]
+        const size_t row32 = (size_t)m.hd * 4;
+        const float* src[2] = {k, v};
         if (!m.kv_f16) {
-            HIP_TRY(c, hipMemcpy((float*)m.d_k + (size_t)layer * m.cap * kvd, k, count * 4, hipMemcpyHostToDevice));
-            HIP_TRY(c, hipMemcpy((float*)m.d_v + (size_t)layer * m.cap * kvd, v, count * 4, hipMemcpyHostToDevice));
+            for (int which = 0; which < 2; ++which) {
+                uint8_t* base = (uint8_t*)(which ? m.d_v : m.d_k) + (size_t)layer * m.cap * kvd * 4;
+                for (uint32_t h = 0; h < m.KVH; ++h)
+                    HIP_TRY(c, hipMemcpy2D(base + (size_t)h * m.cap * row32, row32, (const uint8_t*)src[which] + h * row32,
+                                           kvd * 4, row32, len, hipMemcpyHostToDevice));
+            }
         } else {
+            // head-major f32 staging [KVH][len][hd], then binary16 per head
             void* tmp = nullptr;
             if (int rc = dalloc(c, count * 4, &tmp)) return rc;
-            const float* src[2] = {k, v};
-            uint16_t* dst[2] = {(uint16_t*)m.d_k + (size_t)layer * m.cap * kvd,
-                                (uint16_t*)m.d_v + (size_t)layer * m.cap * kvd};
             hipError_t e = hipSuccess;
-            for (int i = 0; i < 2 && e == hipSuccess; ++i) {
-                e = hipMemcpy(tmp, src[i], count * 4, hipMemcpyHostToDevice);
-                if (e == hipSuccess) e = launch_f32_to_f16((const float*)tmp, dst[i], count, c->stream);
+            for (int which = 0; which < 2 && e == hipSuccess; ++which) {
+                uint16_t* base = (uint16_t*)(which ? m.d_v : m.d_k) + (size_t)layer * m.cap * kvd;
+                for (uint32_t h = 0; h < m.KVH && e == hipSuccess; ++h)
+                    e = hipMemcpy2D((uint8_t*)tmp + (size_t)h * len * row32, row32,
+                                    (const uint8_t*)src[which] + h * row32, kvd * 4, row32, len, hipMemcpyHostToDevice);
+                for (uint32_t h = 0; h < m.KVH && e == hipSuccess; ++h)
+                    e = launch_f32_to_f16((const float*)tmp + (size_t)h * len * m.hd, base + (size_t)h * m.cap * m.hd,
+                                          (uint64_t)len * m.hd, c->stream);
                 if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
             }
             (void)hipFree(tmp);
@@ -1395,18 +1411,24 @@ extern "C" int qora_hip_kv_download(qora_hip_ctx* c, uint32_t layer, float* k, f
     if (!m.ready) return fail(c, QORA_HIP_E_STATE, "model not initialised");
     if (layer >= m.L) return fail(c, QORA_HIP_E_INVALID, "layer out of range");
     const size_t kvd = (size_t)m.KVH * m.hd;
-    const size_t count = (size_t)m.host_pos * kvd;
+    const size_t n = (size_t)m.host_pos;
     HIP_TRY(c, hipStreamSynchronize(c->stream));
-    if (count == 0) return QORA_HIP_OK;
-    if (!m.kv_f16) {
-        HIP_TRY(c, hipMemcpy(k, (float*)m.d_k + (size_t)layer * m.cap * kvd, count * 4, hipMemcpyDeviceToHost));
-        HIP_TRY(c, hipMemcpy(v, (float*)m.d_v + (size_t)layer * m.cap * kvd, count * 4, hipMemcpyDeviceToHost));
-    } else {
-        std::vector<uint16_t> tmp(count);
-        HIP_TRY(c, hipMemcpy(tmp.data(), (uint16_t*)m.d_k + (size_t)layer * m.cap * kvd, count * 2, hipMemcpyDeviceToHost));
-        for (size_t i = 0; i < count; ++i) k[i] = h2f_host(tmp[i]);
-        HIP_TRY(c, hipMemcpy(tmp.data(), (uint16_t*)m.d_v + (size_t)layer * m.cap * kvd, count * 2, hipMemcpyDeviceToHost));
-        for (size_t i = 0; i < count; ++i) v[i] = h2f_host(tmp[i]);
+    if (n == 0) return QORA_HIP_OK;
+    // device: head-major [KVH][cap][hd]; host: the reference's token-major [len][KVH][hd]
+    const size_t eb = m.kv_f16 ? 2 : 4;
+    const size_t row = (size_t)m.hd * eb;
+    std::vector<uint8_t> tmp(m.kv_f16 ? n * kvd * 2 : 0);
+    for (int which = 0; which < 2; ++which) {
+        const uint8_t* base = (const uint8_t*)(which ? m.d_v : m.d_k) + (size_t)layer * m.cap * kvd * eb;
+        float* out = which ? v : k;
+        uint8_t* dst = m.kv_f16 ? tmp.data() : (uint8_t*)out;
+        for (uint32_t h = 0; h < m.KVH; ++h)
+            HIP_TRY(c, hipMemcpy2D(dst + h * row, kvd * eb, base + (size_t)h * m.cap * row, row, row, n,
+                                   hipMemcpyDeviceToHost));
+        if (m.kv_f16) {
+            const uint16_t* t16 = (const uint16_t*)tmp.data();
+            for (size_t i = 0; i < n * kvd; ++i) out[i] = h2f_host(t16[i]);
+        }
     }
     return QORA_HIP_OK;
 }

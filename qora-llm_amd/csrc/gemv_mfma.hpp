@@ -241,7 +241,11 @@ __device__ __forceinline__ void attn_merge_rows_wave(const GemvParams& p, uint32
 // the slice's inputs and builds x (xs in LDS) while the matrix-core waves
 // stream their scales and weights from the first cycle; the one block
 // barrier hands x over without waiting for the weight loads.
-template <int GW, int KW, int PRO>
+// IPW > 1: each workgroup takes IPW consecutive work items (column tile,
+// K slice) of the grid a one-item launch would have, with every item's
+// scales and weights requested up front: fewer, longer-lived workgroups,
+// all loads in flight from the start.
+template <int GW, int KW, int PRO, int IPW = 1>
 __global__ __launch_bounds__(PRO == PRO_ATTN ? 512 : 320) void gemv_q4m_kernel(GemvParams p) {
     constexpr int NW = 4;                    // matrix-core waves
     constexpr int NPW = PRO == PRO_ATTN ? 4 : 1;   // prologue waves (the attention merge gets four)
@@ -252,8 +256,9 @@ __global__ __launch_bounds__(PRO == PRO_ATTN ? 512 : 320) void gemv_q4m_kernel(G
     constexpr int MAXH = KW / 32 + 1;       // heads a slice can touch (head_dim >= 32)
     constexpr bool kAttn = PRO == PRO_ATTN;
     static_assert(KW % 64 == 0 && KW <= 512, "slice of 64..512 rows");
-    __shared__ __align__(16) float xs[KW];
-    __shared__ float wred[2][NPW];
+    static_assert(IPW == 1 || !kAttn, "the attention-merge prologue takes one item per workgroup");
+    __shared__ __align__(16) float xs[IPW][KW];
+    __shared__ float wred[IPW][2][NPW];
     __shared__ __align__(16) uint8_t zl[NW][GW][4][KW];   // limb bytes: [wave][group][limb][row]
     __shared__ __align__(16) uint8_t zero16[16];          // A rows 4..15
     __shared__ float aw[kAttn ? NPW * kAttnMaxSplits * MAXH : 1];
@@ -262,163 +267,185 @@ __global__ __launch_bounds__(PRO == PRO_ATTN ? 512 : 320) void gemv_q4m_kernel(G
     const int lane = t & (kWave - 1);
     // wave-uniform (scalar) so segment lookups and addresses stay on the SALU
     const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
-    const uint32_t tile = blockIdx.x % p.tiles;
-    const uint32_t split = blockIdx.x / p.tiles;
-    const uint32_t k0 = split * (uint32_t)KW;
-    const uint32_t k1 = min(p.k, k0 + (uint32_t)KW);
-    const uint64_t bw = (uint64_t)blockIdx.x * NW + wave;
+    const uint32_t items = p.tiles * p.splits;
+    const uint32_t item0 = blockIdx.x * IPW;
+    const uint32_t nit = min((uint32_t)IPW, items - item0);
 
     if (p.zero_ptr)
         for (uint32_t i = blockIdx.x * NT + t; i < p.zero_n; i += gridDim.x * NT) p.zero_ptr[i] = 0;
 
-    uint4 wq[GW][NKB];
-    uint32_t sw[(NZ + 1) / 2];
-    int esg[GW];
+    uint4 wq[IPW][GW][NKB];
+    uint32_t sw[IPW][(NZ + 1) / 2];
+    int esg[IPW][GW];
     if (wave >= NW) {
         // ---- prologue wave(s): rows [k0, k1) of the input into xs, max |x|, sum x^2 ----
         // Raised issue priority: their few input loads enter the CU's memory
         // queue ahead of the weight streams of the other waves on the CU.
         __builtin_amdgcn_s_setprio(3);
-        float mx = 0.f, ss = 0.f;
-        if constexpr (kAttn) {
-            const uint32_t pw = (uint32_t)(wave - NW);
-            constexpr uint32_t RW = KW / NPW;   // rows per prologue wave (<= 64)
 #pragma unroll
-            for (uint32_t c = 0; c < RW; c += 32)
-                attn_merge_rows_wave(p, k0, pw * RW + c, pw * RW + min(c + 32, RW), k1, xs,
-                                     aw + pw * kAttnMaxSplits * MAXH);
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            for (uint32_t j = (uint32_t)lane; j < RW; j += kWave) mx = fmaxf(mx, fabsf(xs[pw * RW + j]));
-        } else {
-            float xp[RPW], ssp = 0.f;
-            long long xa[RPW], xb[RPW];
-            uint16_t gm[RPW];
+        for (int j = 0; j < IPW; ++j) {
+            if ((uint32_t)j >= nit) break;
+            const uint32_t split = (item0 + j) / p.tiles;
+            const uint32_t k0 = split * (uint32_t)KW;
+            const uint32_t k1 = min(p.k, k0 + (uint32_t)KW);
+            float mx = 0.f, ss = 0.f;
+            if constexpr (kAttn) {
+                const uint32_t pw = (uint32_t)(wave - NW);
+                constexpr uint32_t RW = KW / NPW;   // rows per prologue wave (<= 64)
 #pragma unroll
-            for (int j = 0; j < RPW; ++j) {
-                const uint32_t rc = min(k0 + (uint32_t)(lane + 64 * j), p.k - 1u);
-                if constexpr (PRO == PRO_PLAIN) xp[j] = p.x[rc];
-                if constexpr (PRO == PRO_GAMMA_FIXED) {
-                    xa[j] = p.xacc[rc];
-                    gm[j] = p.gamma[rc];
+                for (uint32_t c = 0; c < RW; c += 32)
+                    attn_merge_rows_wave(p, k0, pw * RW + c, pw * RW + min(c + 32, RW), k1, xs[j],
+                                         aw + pw * kAttnMaxSplits * MAXH);
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                for (uint32_t i = (uint32_t)lane; i < RW; i += kWave) mx = fmaxf(mx, fabsf(xs[j][pw * RW + i]));
+            } else {
+                float xp[RPW], ssp = 0.f;
+                long long xa[RPW], xb[RPW];
+                uint16_t gm[RPW];
+#pragma unroll
+                for (int r = 0; r < RPW; ++r) {
+                    const uint32_t rc = min(k0 + (uint32_t)(lane + 64 * r), p.k - 1u);
+                    if constexpr (PRO == PRO_PLAIN) xp[r] = p.x[rc];
+                    if constexpr (PRO == PRO_GAMMA_FIXED) {
+                        xa[r] = p.xacc[rc];
+                        gm[r] = p.gamma[rc];
+                    }
+                    if constexpr (PRO == PRO_SILU_FIXED) {
+                        xa[r] = p.xacc[rc];
+                        xb[r] = p.xacc[p.k + rc];
+                    }
                 }
-                if constexpr (PRO == PRO_SILU_FIXED) {
-                    xa[j] = p.xacc[rc];
-                    xb[j] = p.xacc[p.k + rc];
+                if constexpr (PRO == PRO_SILU_FIXED) ssp = p.ss_in[min((uint32_t)lane, p.ss_n - 1u)];
+                float inv = 1.f;
+                if constexpr (PRO == PRO_SILU_FIXED)
+                    inv = 1.0f / sqrtf(wave_sum(lane < (int)p.ss_n ? ssp : 0.f) / (float)p.norm_n + 1e-6f);
+#pragma unroll
+                for (int r = 0; r < RPW; ++r) {
+                    const bool ok = k0 + (uint32_t)(lane + 64 * r) < k1;
+                    float x;
+                    if constexpr (PRO == PRO_PLAIN) {
+                        x = ok ? xp[r] : 0.f;
+                    } else if constexpr (PRO == PRO_GAMMA_FIXED) {
+                        const float xf = ok ? from_fixed(xa[r]) : 0.f;
+                        ss += xf * xf;
+                        x = xf * h2f(gm[r]);
+                    } else {
+                        x = ok ? silu_mul(inv * from_fixed(xa[r]), inv * from_fixed(xb[r])) : 0.f;
+                    }
+                    xs[j][lane + 64 * r] = x;
+                    mx = fmaxf(mx, fabsf(x));
                 }
             }
-            if constexpr (PRO == PRO_SILU_FIXED) ssp = p.ss_in[min((uint32_t)lane, p.ss_n - 1u)];
-            float inv = 1.f;
-            if constexpr (PRO == PRO_SILU_FIXED)
-                inv = 1.0f / sqrtf(wave_sum(lane < (int)p.ss_n ? ssp : 0.f) / (float)p.norm_n + 1e-6f);
-#pragma unroll
-            for (int j = 0; j < RPW; ++j) {
-                const bool ok = k0 + (uint32_t)(lane + 64 * j) < k1;
-                float x;
-                if constexpr (PRO == PRO_PLAIN) {
-                    x = ok ? xp[j] : 0.f;
-                } else if constexpr (PRO == PRO_GAMMA_FIXED) {
-                    const float xf = ok ? from_fixed(xa[j]) : 0.f;
-                    ss += xf * xf;
-                    x = xf * h2f(gm[j]);
-                } else {
-                    x = ok ? silu_mul(inv * from_fixed(xa[j]), inv * from_fixed(xb[j])) : 0.f;
-                }
-                xs[lane + 64 * j] = x;
-                mx = fmaxf(mx, fabsf(x));
+            mx = wave_max(mx);
+            if constexpr (PRO == PRO_GAMMA_FIXED) ss = wave_sum(ss);
+            if (lane == 0) {
+                wred[j][0][wave - NW] = mx;
+                wred[j][1][wave - NW] = ss;
             }
-        }
-        mx = wave_max(mx);
-        if constexpr (PRO == PRO_GAMMA_FIXED) ss = wave_sum(ss);
-        if (lane == 0) {
-            wred[0][wave - NW] = mx;
-            wred[1][wave - NW] = ss;
         }
         if (wave == NW && lane < 4) reinterpret_cast<uint32_t*>(zero16)[lane] = 0u;
     } else {
-        // ---- matrix-core waves: scales first (the quantisation needs them), then weights ----
-        gemv_q4m_load_scales<GW, NZ>(p, bw, lane, sw, esg);
-        gemv_q4m_load_weights<GW, NKB>(p, bw, lane, wq);
+        // ---- matrix-core waves: every item's scales first (the quantisation needs them), then weights ----
+#pragma unroll
+        for (int j = 0; j < IPW; ++j)
+            if ((uint32_t)j < nit) gemv_q4m_load_scales<GW, NZ>(p, (uint64_t)(item0 + j) * NW + wave, lane, sw[j], esg[j]);
+#pragma unroll
+        for (int j = 0; j < IPW; ++j)
+            if ((uint32_t)j < nit) gemv_q4m_load_weights<GW, NKB>(p, (uint64_t)(item0 + j) * NW + wave, lane, wq[j]);
     }
     __syncthreads();
     if (wave >= NW) return;
-    float xm = wred[0][0];
-#pragma unroll
-    for (int w = 1; w < NPW; ++w) xm = fmaxf(xm, wred[0][w]);
-    if constexpr (PRO == PRO_GAMMA_FIXED) {
-        if (t == 0 && tile == 0) p.ss_out[split] = wred[1][0];
-    }
-    // 2^ex bounds max |x| (0 for an all-zero slice)
-    const int ex = __builtin_amdgcn_readfirstlane(xm > 0.f ? (int)((__float_as_uint(xm) >> 23) & 0xFFu) - 126 : 0);
-
-    // ---- z = x * s quantised to 30-bit integers, stored as limb bytes ----
-#pragma unroll
-    for (int u = 0; u < NZ; ++u) {
-        const uint32_t e = (uint32_t)lane * NZ + u;
-        const uint32_t rz = e % KW, gz = e / KW;
-        int es = esg[0];
-#pragma unroll
-        for (int g = 1; g < GW; ++g) es = gz == (uint32_t)g ? esg[g] : es;
-        const uint16_t sbits = (uint16_t)((u & 1) ? (sw[u / 2] >> 16) : (sw[u / 2] & 0xFFFFu));
-        const float z = xs[rz] * h2f(sbits);
-        const int M = (int)rintf(ldexpf(z, 30 - (ex + es)));
-        const uint32_t limbs = (uint32_t)(M + 0x808080) ^ 0x808080u;
-        uint8_t* zp = &zl[wave][gz][0][rz];
-        zp[0] = (uint8_t)(limbs & 0xFFu);
-        zp[KW] = (uint8_t)((limbs >> 8) & 0xFFu);
-        zp[2 * KW] = (uint8_t)((limbs >> 16) & 0xFFu);
-        zp[3 * KW] = (uint8_t)(limbs >> 24);
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
-    // ---- matrix cores: C[limb][column] += A[limb][k] * B[k][column] ----
-    v4i32 acc[2 * GW];
-#pragma unroll
-    for (int c = 0; c < 2 * GW; ++c) acc[c] = (v4i32){0, 0, 0, 0};
     const uint32_t li = (uint32_t)lane % 16, lk = (uint32_t)lane / 16;
 #pragma unroll
-    for (int g = 0; g < GW; ++g) {
+    for (int j = 0; j < IPW; ++j) {
+        if ((uint32_t)j >= nit) break;
+        const uint32_t item = item0 + j;
+        const uint32_t tile = item % p.tiles;
+        const uint32_t split = item / p.tiles;
+        float xm = wred[j][0][0];
 #pragma unroll
-        for (int kb = 0; kb < NKB; ++kb) {
-            const uint8_t* ap = li < 4 ? &zl[wave][g][li][kb * 64 + 16 * lk] : zero16;
-            const v4i32 a = *reinterpret_cast<const v4i32*>(ap);
-            const uint4 w = wq[g][kb];
-            acc[2 * g] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, q4_bfrag(w.x, w.y), acc[2 * g], 0, 0, 0);
-            acc[2 * g + 1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, q4_bfrag(w.z, w.w), acc[2 * g + 1], 0, 0, 0);
+        for (int w = 1; w < NPW; ++w) xm = fmaxf(xm, wred[j][0][w]);
+        if constexpr (PRO == PRO_GAMMA_FIXED) {
+            if (t == 0 && tile == 0) p.ss_out[split] = wred[j][1][0];
         }
-    }
+        // 2^ex bounds max |x| (0 for an all-zero slice)
+        const int ex =
+            __builtin_amdgcn_readfirstlane(xm > 0.f ? (int)((__float_as_uint(xm) >> 23) & 0xFFu) - 126 : 0);
 
-    // ---- epilogue: lanes 0..15 hold limbs 0..3 of column l of each block ----
-    // Y = C0 + 2^8 C1 + 2^16 C2 + 2^24 C3 as (C0 + 2^8 C1) + 2^16 (C2 + 2^8 C3):
-    // each half fits int32 (|C| < 2^22). value = Y * 2^(E - 34), so the
-    // fixed-point amount (2^36 units) is Y << (E + 2), rounded when E + 2 < 0.
-    if (lane < 16) {
+        // ---- z = x * s quantised to 30-bit integers, stored as limb bytes ----
+#pragma unroll
+        for (int u = 0; u < NZ; ++u) {
+            const uint32_t e = (uint32_t)lane * NZ + u;
+            const uint32_t rz = e % KW, gz = e / KW;
+            int es = esg[j][0];
+#pragma unroll
+            for (int g = 1; g < GW; ++g) es = gz == (uint32_t)g ? esg[j][g] : es;
+            const uint16_t sbits = (uint16_t)((u & 1) ? (sw[j][u / 2] >> 16) : (sw[j][u / 2] & 0xFFFFu));
+            const float z = xs[j][rz] * h2f(sbits);
+            const int M = (int)rintf(ldexpf(z, 30 - (ex + es)));
+            const uint32_t limbs = (uint32_t)(M + 0x808080) ^ 0x808080u;
+            uint8_t* zp = &zl[wave][gz][0][rz];
+            zp[0] = (uint8_t)(limbs & 0xFFu);
+            zp[KW] = (uint8_t)((limbs >> 8) & 0xFFu);
+            zp[2 * KW] = (uint8_t)((limbs >> 16) & 0xFFu);
+            zp[3 * KW] = (uint8_t)(limbs >> 24);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+        // ---- matrix cores: C[limb][column] += A[limb][k] * B[k][column] ----
+        v4i32 acc[2 * GW];
+#pragma unroll
+        for (int c = 0; c < 2 * GW; ++c) acc[c] = (v4i32){0, 0, 0, 0};
 #pragma unroll
         for (int g = 0; g < GW; ++g) {
-            const LaneSrc src = lane_source(p, tile, wave * GW + g, 4 * GW);
-            if (src.grp >= src.sg.groups) continue;
-            const int sh = max(min(ex + esg[g] + 2, 62), -62);
-            const int rsh = sh < 0 ? -sh : 0, lsh = sh > 0 ? sh : 0;
-            const long long rnd = rsh > 0 ? (1LL << (rsh - 1)) : 0;
-            long long* dst = p.acc + src.sg.col0 + src.grp * 32u + (uint32_t)lane;
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const v4i32 c = acc[2 * g + h];
-                // |C| < 2^22 for 256 rows: each half fits int32; 512 rows need 64 bits
-                long long lo, hi;
-                if constexpr (KW <= 256) {
-                    lo = c[0] + (c[1] << 8);
-                    hi = c[2] + (c[3] << 8);
-                } else {
-                    lo = (long long)c[0] + ((long long)c[1] << 8);
-                    hi = (long long)c[2] + ((long long)c[3] << 8);
+            for (int kb = 0; kb < NKB; ++kb) {
+                const uint8_t* ap = li < 4 ? &zl[wave][g][li][kb * 64 + 16 * lk] : zero16;
+                const v4i32 a = *reinterpret_cast<const v4i32*>(ap);
+                const uint4 w = wq[j][g][kb];
+                acc[2 * g] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, q4_bfrag(w.x, w.y), acc[2 * g], 0, 0, 0);
+                acc[2 * g + 1] =
+                    __builtin_amdgcn_mfma_i32_16x16x64_i8(a, q4_bfrag(w.z, w.w), acc[2 * g + 1], 0, 0, 0);
+            }
+        }
+        // the next item rewrites zl: this item's operand reads come first
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+        // ---- epilogue: lanes 0..15 hold limbs 0..3 of column l of each block ----
+        // Y = C0 + 2^8 C1 + 2^16 C2 + 2^24 C3 as (C0 + 2^8 C1) + 2^16 (C2 + 2^8 C3):
+        // each half fits int32 (|C| < 2^22). value = Y * 2^(E - 34), so the
+        // fixed-point amount (2^36 units) is Y << (E + 2), rounded when E + 2 < 0.
+        if (lane < 16) {
+#pragma unroll
+            for (int g = 0; g < GW; ++g) {
+                const LaneSrc src = lane_source(p, tile, wave * GW + g, 4 * GW);
+                if (src.grp >= src.sg.groups) continue;
+                const int sh = max(min(ex + esg[j][g] + 2, 62), -62);
+                const int rsh = sh < 0 ? -sh : 0, lsh = sh > 0 ? sh : 0;
+                const long long rnd = rsh > 0 ? (1LL << (rsh - 1)) : 0;
+                long long* dst = p.acc + src.sg.col0 + src.grp * 32u + (uint32_t)lane;
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const v4i32 c = acc[2 * g + h];
+                    // |C| < 2^22 for 256 rows: each half fits int32; 512 rows need 64 bits
+                    long long lo, hi;
+                    if constexpr (KW <= 256) {
+                        lo = c[0] + (c[1] << 8);
+                        hi = c[2] + (c[3] << 8);
+                    } else {
+                        lo = (long long)c[0] + ((long long)c[1] << 8);
+                        hi = (long long)c[2] + ((long long)c[3] << 8);
+                    }
+                    const long long Y = lo + (hi << 16);
+                    const long long f = ((Y + rnd) >> rsh) << lsh;
+                    atomicAdd(reinterpret_cast<unsigned long long*>(dst + h * 16), (unsigned long long)f);
                 }
-                const long long Y = lo + (hi << 16);
-                const long long f = ((Y + rnd) >> rsh) << lsh;
-                atomicAdd(reinterpret_cast<unsigned long long*>(dst + h * 16), (unsigned long long)f);
             }
         }
     }

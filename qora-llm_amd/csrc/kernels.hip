@@ -110,6 +110,9 @@ bool plan_gemv_q4m(uint32_t k, const uint32_t* seg_groups, int nseg, bool paired
         if (best.blocks() >= want) break;
     }
     if (!have) return false;
+    // several work items per workgroup (QORA_GEMV_IPW = 2 or 4; K slices of 256, one group per wave)
+    const int ipw = env_int("QORA_GEMV_IPW", 1);
+    if ((ipw == 2 || ipw == 4) && best.gw == 1 && best.kr == 256 && row_align == 1) best.ipw = ipw;
     *plan = best;
     return true;
 }
@@ -167,18 +170,42 @@ static hipError_t launch_gemv_gt(const GemvPlan& plan, const GemvParams& p, hipS
     }
 }
 
-template <int GW, int KW>
-static hipError_t launch_q4m_kw(const GemvPlan& plan, const GemvParams& p, hipStream_t stream) {
+template <int GW, int KW, int IPW>
+static hipError_t launch_q4m_ipw(const GemvPlan& plan, const GemvParams& p, hipStream_t stream) {
     // 4 matrix-core waves + the prologue wave (four for the attention merge)
-    const dim3 grid(plan.blocks()), block(320), block_attn(512);
+    const dim3 grid(plan.grid()), block(320), block_attn(512);
     switch (p.pro) {
-    case PRO_PLAIN: hipLaunchKernelGGL((gemv_q4m_kernel<GW, KW, PRO_PLAIN>), grid, block, 0, stream, p); break;
-    case PRO_GAMMA_FIXED: hipLaunchKernelGGL((gemv_q4m_kernel<GW, KW, PRO_GAMMA_FIXED>), grid, block, 0, stream, p); break;
-    case PRO_SILU_FIXED: hipLaunchKernelGGL((gemv_q4m_kernel<GW, KW, PRO_SILU_FIXED>), grid, block, 0, stream, p); break;
-    case PRO_ATTN: hipLaunchKernelGGL((gemv_q4m_kernel<GW, KW, PRO_ATTN>), grid, block_attn, 0, stream, p); break;
+    case PRO_PLAIN: hipLaunchKernelGGL((gemv_q4m_kernel<GW, KW, PRO_PLAIN, IPW>), grid, block, 0, stream, p); break;
+    case PRO_GAMMA_FIXED:
+        hipLaunchKernelGGL((gemv_q4m_kernel<GW, KW, PRO_GAMMA_FIXED, IPW>), grid, block, 0, stream, p);
+        break;
+    case PRO_SILU_FIXED:
+        hipLaunchKernelGGL((gemv_q4m_kernel<GW, KW, PRO_SILU_FIXED, IPW>), grid, block, 0, stream, p);
+        break;
+    case PRO_ATTN:
+        if constexpr (IPW == 1) {
+            hipLaunchKernelGGL((gemv_q4m_kernel<GW, KW, PRO_ATTN, 1>), grid, block_attn, 0, stream, p);
+            break;
+        } else {
+            return hipErrorInvalidValue;
+        }
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
+}
+
+template <int GW, int KW>
+static hipError_t launch_q4m_kw(const GemvPlan& plan, const GemvParams& p, hipStream_t stream) {
+    if constexpr (GW == 1 && KW == 256) {
+        switch (plan.ipw) {
+        case 1: return launch_q4m_ipw<GW, KW, 1>(plan, p, stream);
+        case 2: return launch_q4m_ipw<GW, KW, 2>(plan, p, stream);
+        case 4: return launch_q4m_ipw<GW, KW, 4>(plan, p, stream);
+        default: return hipErrorInvalidValue;
+        }
+    }
+    if (plan.ipw != 1) return hipErrorInvalidValue;
+    return launch_q4m_ipw<GW, KW, 1>(plan, p, stream);
 }
 
 template <int GW>
@@ -197,6 +224,7 @@ static hipError_t launch_q4m_gw(const GemvPlan& plan, const GemvParams& p, hipSt
 hipError_t launch_gemv(int fmt, const GemvPlan& plan, const GemvParams& p, hipStream_t stream) {
     if (plan.blocks() == 0) return hipErrorInvalidValue;
     if (plan.mfma) {
+        if (plan.ipw != 1 && (p.pro == PRO_ATTN || plan.gw != 1 || plan.kr != 256)) return hipErrorInvalidValue;
         if (fmt != FMT_Q4 || !p.tw || !p.ts || !p.tes) return hipErrorInvalidValue;
         switch (plan.gw) {
         case 1: return launch_q4m_gw<1>(plan, p, stream);
@@ -394,6 +422,13 @@ void attn_geometry(uint32_t positions, uint32_t* chunk, uint32_t* s_max) {
 hipError_t launch_attn(const AttnParams& p, hipStream_t stream) {
     const dim3 grid(p.s_max, p.KVH);
     const bool lng = p.nsg > 1;
+    if (lng && p.kv_f16 && (p.hd == 128 || p.hd == 64) && p.groups <= (uint32_t)kAttnMaxGroups &&
+        !std::getenv("QORA_HIP_ATTN_STAGED")) {
+        const dim3 grid_t(p.KVH, p.s_max);
+        if (p.hd == 128) hipLaunchKernelGGL((attn_decode_direct_kernel<128>), grid_t, dim3(512), 0, stream, p);
+        else hipLaunchKernelGGL((attn_decode_direct_kernel<64>), grid_t, dim3(512), 0, stream, p);
+        return hipGetLastError();
+    }
     const dim3 block(lng ? 256 * kAttnLongNsg : 256);
 #define QORA_ATTN(DPL)                                                                                   \
     do {                                                                                                \

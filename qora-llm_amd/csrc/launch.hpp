@@ -17,7 +17,9 @@ struct GemvPlan {
     uint32_t kr = 0;      // rows per K slice
     int mfma = 0;         // 1: Q4 on the matrix cores (gemv_q4m_kernel): gt = 4*gw, kr = kw
     int gw = 0;           // groups per wave (MFMA kernel)
-    uint32_t blocks() const { return tiles * splits; }
+    int ipw = 1;          // work items (tile, K slice) per workgroup (MFMA kernel)
+    uint32_t blocks() const { return tiles * splits; }                // work items
+    uint32_t grid() const { return (blocks() + (uint32_t)ipw - 1) / (uint32_t)ipw; }
 };
 
 // Chooses GT / RPL / S for k input rows. seg_groups: groups (n/32) of each

@@ -151,6 +151,7 @@ struct MkParams {
     unsigned long long* trace; // optional: [workgroup][phase][3] clock stamps (enter, inputs ready, done)
     LmHeadParams lm;           // tw, ts, rows, cols, tiles, gamma, y, part_val, part_idx
     uint32_t* err;
+    uint64_t kv_ps, kv_hs;     // cache addressing as in AttnParams
 };
 
 
@@ -206,6 +207,7 @@ struct PrefillAttnParams {
     uint32_t H, KVH, hd;
     float scale;
     float* out;                // attention output [T][qd]
+    uint64_t kv_ps, kv_hs;     // cache addressing as in AttnParams (0: token-major)
 };
 
 // On-device sampling (sample.hpp).
@@ -265,6 +267,9 @@ struct AttnParams {
     float* part;               // [KVH][s_max][groups][hd + 2]
     uint32_t s_max;
     uint32_t nsg;              // 1: attn_decode_kernel; > 1: attn_decode_long_kernel (4 passes in flight per split)
+    // cache addressing: element (pos, kvh, d) at pos * kv_ps + kvh * kv_hs + d;
+    // kv_ps = 0: token-major [pos][KVH][hd] (kv_ps = KVH hd, kv_hs = hd)
+    uint64_t kv_ps, kv_hs;
 };
 
 struct AttnCombineParams {

@@ -379,15 +379,16 @@ __global__ __launch_bounds__(256) void pf_rope_cache_kernel(PrefillAttnParams p)
         return d < half ? v[i] * c - v[base + d + half] * s : v[i] * c + v[base + d - half] * s;
     };
     for (uint32_t i = threadIdx.x; i < qd; i += 256) p.q[(uint64_t)t * qd + i] = rotate(row, i);
-    const uint64_t crow = (uint64_t)pos * kvd;
+    const uint64_t cps = p.kv_ps ? p.kv_ps : kvd, chs = p.kv_ps ? p.kv_hs : hd;   // cache layout
     for (uint32_t i = threadIdx.x; i < kvd; i += 256) {
         const float kv = rotate(row + qd, i), vv = row[qd + kvd + i];
+        const uint64_t idx = (uint64_t)pos * cps + (uint64_t)(i / hd) * chs + i % hd;
         if constexpr (F16KV) {
-            reinterpret_cast<uint16_t*>(p.kc)[crow + i] = f2h(kv);
-            reinterpret_cast<uint16_t*>(p.vc)[crow + i] = f2h(vv);
+            reinterpret_cast<uint16_t*>(p.kc)[idx] = f2h(kv);
+            reinterpret_cast<uint16_t*>(p.vc)[idx] = f2h(vv);
         } else {
-            reinterpret_cast<float*>(p.kc)[crow + i] = kv;
-            reinterpret_cast<float*>(p.vc)[crow + i] = vv;
+            reinterpret_cast<float*>(p.kc)[idx] = kv;
+            reinterpret_cast<float*>(p.vc)[idx] = vv;
         }
     }
 }
@@ -415,6 +416,7 @@ __global__ __launch_bounds__(256) void pf_attn_vec_kernel(PrefillAttnParams p) {
     const uint32_t h = blockIdx.y;
     const uint32_t hd = p.hd, G = p.H / p.KVH, kvh = h / G;
     const uint32_t qd = p.H * hd, kvd = p.KVH * hd;
+    const uint64_t cps = p.kv_ps ? p.kv_ps : kvd, chs = p.kv_ps ? p.kv_hs : hd;   // cache layout
     const uint32_t nq = min((uint32_t)QT, p.T - qt0);
     const uint32_t qr = t / 8u, sub = t % 8u;       // query row, lane within the row's 8 threads
     const uint32_t qpos = p.pos0 + qt0 + qr;        // absolute position of this thread's query
@@ -436,7 +438,7 @@ __global__ __launch_bounds__(256) void pf_attn_vec_kernel(PrefillAttnParams p) {
         for (uint32_t e = t; e < KT * hd; e += 256) {
             const uint32_t r = e / hd, d = e % hd;
             const uint32_t kp = min(k0 + r, last);
-            const uint64_t idx = (uint64_t)kp * kvd + (uint64_t)kvh * hd + d;
+            const uint64_t idx = (uint64_t)kp * cps + (uint64_t)kvh * chs + d;
             float kv, vv;
             if constexpr (F16KV) {
                 kv = h2f(reinterpret_cast<const uint16_t*>(p.kc)[idx]);
@@ -538,6 +540,7 @@ __global__ __launch_bounds__(256) void pf_attn_mfma_kernel(PrefillAttnParams p) 
     const uint32_t QT = 16u * (4u / G);             // queries per block
     const uint32_t q0 = blockIdx.x * QT;            // chunk-relative first query of the block
     const uint32_t qd = p.H * HD, kvd = p.KVH * HD;
+    const uint64_t cps = p.kv_ps ? p.kv_ps : kvd, chs = p.kv_ps ? p.kv_hs : HD;   // cache layout
     const uint32_t nq = min(QT, p.T - q0);
     const uint32_t last = p.pos0 + q0 + nq - 1u;    // last key any query of the block needs
     const uint32_t wq0 = q0 + sub * 16u;            // this wave's first query
@@ -570,7 +573,7 @@ __global__ __launch_bounds__(256) void pf_attn_mfma_kernel(PrefillAttnParams p) 
         // stage K and V rows k0 .. k0 + 63 (clamped to `last`; masked below)
         for (uint32_t e = t; e < (uint32_t)(KT * HD / 4); e += 256) {
             const uint32_t r = e / (HD / 4), c4 = e % (HD / 4);
-            const uint64_t idx = (uint64_t)min(k0 + r, last) * kvd + (uint64_t)kvh * HD + 4u * c4;
+            const uint64_t idx = (uint64_t)min(k0 + r, last) * cps + (uint64_t)kvh * chs + 4u * c4;
             float4 kv, vv;
             if constexpr (F16KV) {
                 const uint2 a = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(p.kc) + idx);
