@@ -145,6 +145,13 @@ int qora_hip_decode_sample(qora_hip_ctx* ctx, uint32_t token, const uint32_t* hi
  * model_init; Q4 weights). */
 int qora_hip_decode_mode(const qora_hip_ctx* ctx);
 
+/* Context bound of the fused short-context step (no counterpart in the
+ * reference): graph-driven steps that append a position below it run each
+ * layer's attention inside the o-projection kernel; longer contexts take the
+ * split attention kernel. 0 = never (no model, F16 weights, a shape the fused
+ * kernel does not cover, or QORA_HIP_ATTN_O=0 at model_init). */
+uint32_t qora_hip_attn_o_limit(const qora_hip_ctx* ctx);
+
 /* RawKvCache access (gemv.rs:154-166): current length, reset to empty, and a
  * copy of one layer's [len][kv_heads][head_dim] K and V as f32. */
 int qora_hip_kv_len(qora_hip_ctx* ctx, uint64_t* len);

@@ -102,6 +102,7 @@ SIGNATURES = {
     "qora_hip_gemv_run": (_I, [_P, _U32, _P, _P, _P]),
     "qora_hip_gemv_release": (_I, [_P, _U32]),
     "qora_hip_decode_mode": (_I, [_P]),
+    "qora_hip_attn_o_limit": (_U32, [_P]),
     "qora_hip_lm_head_prepare": (_I, [_P, _U32, _P]),
     "qora_hip_lm_head_run": (_I, [_P, _U32, _P, _P, _P, _P]),
     "qora_hip_gemv_q4_rowdot": (_I, [_P, _P, _P, _P, _P, _U64, _U64, _P]),
@@ -556,6 +557,10 @@ class HipBackend:
     def decode_mode(self) -> int:
         """1: one captured graph per step, 2: one persistent launch per step."""
         return int(self.ctx.lib.qora_hip_decode_mode(self.ctx.h))
+
+    def attn_o_limit(self) -> int:
+        """Steps appending a position below this run attention inside the o GEMV."""
+        return int(self.ctx.lib.qora_hip_attn_o_limit(self.ctx.h))
 
     def kv_layer(self, layer: int):
         """(k, v) of one layer as f32 [len][kv_heads*head_dim] (RawKvCache entry)."""

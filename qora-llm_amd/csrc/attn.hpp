@@ -121,6 +121,7 @@ __device__ __forceinline__ void attn_store_tile(const KvTileRegs<TL>& r, uint32_
 // many passes take attn_decode_long_kernel instead.
 template <int DPL, bool F16KV>
 __global__ __launch_bounds__(256) void attn_decode_kernel(AttnParams p) {
+    kernarg_warm(p);
     constexpr int NT = 256;
     constexpr int SUB = kAttnSub;                    // positions per pass (32)
     constexpr int HDM = 64 * DPL;                    // head_dim bound of this instance
@@ -406,6 +407,7 @@ constexpr int kAttnLongNsg = 4;
 
 template <int DPL, bool F16KV>
 __global__ __launch_bounds__(256 * kAttnLongNsg) void attn_decode_long_kernel(AttnParams p) {
+    kernarg_warm(p);
     constexpr int NSG = kAttnLongNsg;
     constexpr int NT = 256;                          // threads per subgroup
     constexpr int SUB = kAttnSub;                    // positions per pass (32)
@@ -695,6 +697,7 @@ __global__ __launch_bounds__(256 * kAttnLongNsg) void attn_decode_long_kernel(At
 // never reach a sum (selection, not a zero weight: stale slots may hold NaN).
 template <int HD>
 __global__ __launch_bounds__(512) void attn_decode_direct_kernel(AttnParams p) {
+    kernarg_warm(p);
     constexpr int NWV = 8;                           // waves per block
     constexpr int PP = 32;                           // positions per pass
     constexpr int VD = HD / 16;                      // dims per lane
@@ -965,6 +968,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnCombineParams p) 
 // ---------------------------------------------------------------------------
 
 __global__ __launch_bounds__(256) void embed_kernel(EmbedParams p) {
+    kernarg_warm(p);
     int32_t tok = p.tok_src[p.tok_idx ? *p.tok_idx : 0];
     tok = tok < 0 ? 0 : (tok >= (int32_t)p.vocab ? (int32_t)p.vocab - 1 : tok);
     for (uint32_t j = blockIdx.x * blockDim.x + threadIdx.x; j < p.hidden; j += gridDim.x * blockDim.x) {

@@ -1,0 +1,326 @@
+// Short-context decode: GQA attention and the o projection in one kernel.
+//
+// The split attention kernel and the o GEMV each pay a launch's fixed
+// latency (wave launch, first loads, drain) of a few microseconds, far more
+// than their work at a short context. Here the o GEMV's K slice is one query
+// head h (KW = head_dim), so a workgroup needs only head h's attention output:
+// it computes it itself, from the q|k|v sums of the q|k|v GEMV and the cache,
+// and feeds it to the same matrix-core pass as gemv_q4m_kernel (same work
+// items, same packed weights). The 16 column tiles of a head repeat its
+// attention; at a short context that costs less than a launch.
+//
+// Attention (gemv.rs:914-989, softmax_raw gemv.rs:782-793) of head h over
+// KV head h / groups, positions [0, L), L = *pos + 1:
+//   * q, the appended k row and v row: RMSNorm factor of the q|k|v GEMV input
+//     applied to the fixed-point sums, q and k rotated at position L - 1
+//     (apply_rope_raw, gemv.rs:903-906); the workgroup of column tile 0 of the
+//     group's first head writes the k and v rows into the cache
+//     (gemv.rs:909-911), every workgroup uses them from LDS;
+//   * all 8 waves take positions: lane (c, j) = (lane % 16, lane / 16) of wave
+//     w holds position 32 i + 4 w + j of pass i and dims 64 u + 4 c .. + 3, so
+//     each load instruction reads four whole rows; passes are loaded in
+//     blocks of kFusedPasses (K and V together) before any arithmetic;
+//   * a row's partial dots are summed over its 16 lanes by a DPP butterfly
+//     (every lane gets the same bits); each wave keeps its own running max,
+//     sum and p.V, merged in wave order at the end.
+// The cache rows read are those below L - 1 (written by earlier steps), so
+// the row being appended is never read while it is written.
+#pragma once
+
+#include <type_traits>
+
+#include "attn.hpp"
+#include "common.hpp"
+#include "gemv_mfma.hpp"
+#include "params.hpp"
+
+namespace qora {
+
+constexpr int kFusedWaves = 8;          // waves per workgroup, all in the attention
+constexpr uint32_t kFusedPass = 32;     // positions per pass: 8 waves x 4 row slots
+constexpr int kFusedPasses = 8;         // passes loaded together (256 positions)
+
+// Sum over each 16-lane row by a butterfly: lane ^ 1, lane ^ 2, then the
+// mirrored quad and the mirrored half row. Each step adds two equal-bit
+// operands in either order, so all 16 lanes end with identical bits.
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp_f32<0xB1>(v);    // quad_perm [1,0,3,2]
+    v += dpp_f32<0x4E>(v);    // quad_perm [2,3,0,1]
+    v += dpp_f32<0x141>(v);   // row_half_mirror
+    v += dpp_f32<0x140>(v);   // row_mirror
+    return v;
+}
+
+template <bool F16KV>
+__device__ __forceinline__ float4 kv_word_f32(typename std::conditional<F16KV, uint2, float4>::type w) {
+    if constexpr (F16KV) return kv_words_f32(w);
+    else return w;
+}
+
+template <int HD, bool F16KV>
+__global__ __launch_bounds__(kFusedWaves * kWave) void gemv_q4m_attn_kernel(AttnOParams ap) {
+    constexpr int GW = 1, NW = 4;
+    constexpr int KW = HD;                  // one query head per K slice
+    constexpr int NKB = KW / 64, NZ = GW * KW / 64;
+    constexpr int NQ = HD / 64;             // dim quads per lane
+    constexpr int PB = kFusedPasses;
+    static_assert(HD == 64 || HD == 128, "head_dim 64 or 128");
+    using W = typename std::conditional<F16KV, uint2, float4>::type;
+    kernarg_warm(ap);
+    const GemvParams& p = ap.g;
+    const AttnParams& a = ap.a;
+    __shared__ __align__(16) float qs[HD];
+    __shared__ __align__(16) float kn[HD];
+    __shared__ __align__(16) float vn[HD];
+    __shared__ __align__(16) float accs[kFusedWaves][HD];
+    __shared__ float mls[kFusedWaves][2];
+    __shared__ __align__(16) uint8_t zl[NW][GW][4][KW];
+    __shared__ __align__(16) uint8_t zero16[16];
+
+    const int t = threadIdx.x;
+    const int lane = t & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
+    // Work item of this workgroup. Workgroups go to the 8 XCDs round-robin
+    // (blockIdx % 8); item = (blockIdx % 8) * (grid / 8) + blockIdx / 8 gives
+    // each XCD consecutive items, i.e. the column tiles of two query heads of
+    // one KV head at the model shape, so an XCD's L2 serves one KV head's
+    // rows to all of its workgroups.
+    const uint32_t item = gridDim.x % 8u == 0u ? (blockIdx.x % 8u) * (gridDim.x / 8u) + blockIdx.x / 8u : blockIdx.x;
+    const uint32_t tile = item % p.tiles;
+    const uint32_t h = item / p.tiles;                 // K slice = query head
+    const uint32_t kvh = h / a.groups;
+    const uint32_t qd = a.H * HD, kvd = a.KVH * HD;
+    const uint64_t cps = kv_pos_stride(a), coff = kv_head_off(a, kvh);
+
+    // ---- the position first: every cache address depends on it ----
+    int32_t pos_raw = __builtin_amdgcn_readfirstlane(*a.pos);
+    sgpr_pin(pos_raw);
+    const uint32_t L = (uint32_t)pos_raw + 1u;
+    const uint32_t cur = L - 1u;                       // position appended this step
+
+    // ---- cache rows of the first block's live passes, then the q|k|v sums
+    // and (matrix-core waves) the work item's scales and weights: loads
+    // complete in issue order, and the rows are needed first ----
+    const uint32_t c = (uint32_t)lane % 16, j = (uint32_t)lane / 16;
+    const uint32_t slot = 4u * (uint32_t)wave + j;     // position of pass i: b0 + 32 i + slot
+    const uint8_t* kcache = reinterpret_cast<const uint8_t*>(a.kc);
+    const uint8_t* vcache = reinterpret_cast<const uint8_t*>(a.vc);
+    constexpr uint32_t EB = F16KV ? 2u : 4u;
+    W kr[PB][NQ], vr[PB][NQ];
+    // passes of the block at b0 holding positions below L (wave-uniform)
+    auto live_passes = [&](uint32_t b0) { return min((uint32_t)PB, (L - b0 + kFusedPass - 1) / kFusedPass); };
+    auto load_block = [&](uint32_t b0) {
+        // rows >= cur are not read (clamped to cur - 1, discarded below); none when cur == 0
+        const uint32_t np = cur == 0 ? 0u : live_passes(b0);
+#pragma unroll
+        for (int i = 0; i < PB; ++i) {
+            if ((uint32_t)i < np) {
+                const uint32_t pos = min(b0 + kFusedPass * (uint32_t)i + slot, cur - 1u);
+#pragma unroll
+                for (int u = 0; u < NQ; ++u) {
+                    const uint64_t off = ((uint64_t)pos * cps + coff + 64u * (uint32_t)u + 4u * c) * EB;
+                    kr[i][u] = *reinterpret_cast<const W*>(kcache + off);
+                    vr[i][u] = *reinterpret_cast<const W*>(vcache + off);
+                }
+            } else {
+#pragma unroll
+                for (int u = 0; u < NQ; ++u) {
+                    kr[i][u] = W{};
+                    vr[i][u] = W{};
+                }
+            }
+        }
+    };
+    load_block(0);
+    // ---- q|k|v sums of the head (waves NW.., one dim per thread): issued
+    // after the cache rows, so their arithmetic waits for both at once ----
+    const bool qkv_wave = wave >= NW && wave < NW + HD / kWave;
+    const uint32_t d = (uint32_t)(t - NW * kWave) % HD;
+    const uint32_t pd = rope_partner(d, a.half);
+    long long qa = 0, qb = 0, ka = 0, kb = 0, va = 0;
+    float ssp = 0.f;
+    if (qkv_wave) {
+        qa = a.qkv_acc[(uint64_t)h * HD + d];
+        qb = a.qkv_acc[(uint64_t)h * HD + pd];
+        ka = a.qkv_acc[qd + (uint64_t)kvh * HD + d];
+        kb = a.qkv_acc[qd + (uint64_t)kvh * HD + pd];
+        va = a.qkv_acc[qd + kvd + (uint64_t)kvh * HD + d];
+        ssp = a.ss_in[min((uint32_t)lane, a.ss_n - 1u)];
+    }
+    float rc = 1.f, rs = 0.f;
+    if (qkv_wave && a.use_rope && d < 2 * a.half) {
+        const uint32_t td = d < a.half ? d : d - a.half;
+        rc = a.rope_cos[(uint64_t)cur * a.half + td];
+        rs = a.rope_sin[(uint64_t)cur * a.half + td];
+    }
+
+    uint4 wq[GW][NKB];
+    uint32_t sw[(NZ + 1) / 2];
+    int esg[GW];
+    if (wave < NW) {
+        gemv_q4m_load_scales<GW, NZ>(p, (uint64_t)item * NW + wave, lane, sw, esg);
+        gemv_q4m_load_weights<GW, NKB>(p, (uint64_t)item * NW + wave, lane, wq);
+    }
+
+    if (qkv_wave) {
+        // the q|k|v GEMV ran on x * gamma; its RMSNorm factor is applied here
+        const float inv = 1.0f / sqrtf(wave_sum(lane < (int)a.ss_n ? ssp : 0.f) / (float)a.norm_n + 1e-6f);
+        const bool rot = a.use_rope != 0 && d < 2 * a.half;
+        auto rotate = [&](long long x, long long y) {
+            const float u = inv * from_fixed(x), v = inv * from_fixed(y);
+            return rot ? (d < a.half ? u * rc - v * rs : u * rc + v * rs) : u;
+        };
+        qs[d] = rotate(qa, qb);
+        float kv = rotate(ka, kb);
+        float vv = inv * from_fixed(va);
+        const bool owner = tile == 0 && h % a.groups == 0;
+        const uint64_t idx = (uint64_t)cur * cps + coff + d;
+        if constexpr (F16KV) {
+            const uint16_t kh = f2h(kv), vh = f2h(vv);
+            if (owner) {
+                reinterpret_cast<uint16_t*>(a.kc)[idx] = kh;
+                reinterpret_cast<uint16_t*>(a.vc)[idx] = vh;
+            }
+            kv = h2f(kh);   // the stored values, as later steps read them
+            vv = h2f(vh);
+        } else if (owner) {
+            reinterpret_cast<float*>(a.kc)[idx] = kv;
+            reinterpret_cast<float*>(a.vc)[idx] = vv;
+        }
+        kn[d] = kv;
+        vn[d] = vv;
+    }
+    if (wave == 0 && lane < 4) reinterpret_cast<uint32_t*>(zero16)[lane] = 0u;
+    __syncthreads();
+
+    float q[NQ][4];
+#pragma unroll
+    for (int u = 0; u < NQ; ++u) {
+        const float4 v = *reinterpret_cast<const float4*>(qs + 64 * u + 4 * c);
+        q[u][0] = v.x;
+        q[u][1] = v.y;
+        q[u][2] = v.z;
+        q[u][3] = v.w;
+    }
+    const float scale2 = a.scale * 1.4426950408889634f;   // log2(e)
+    float m_w = -INFINITY, l_w = 0.f;
+    float o[NQ][4];
+#pragma unroll
+    for (int u = 0; u < NQ; ++u)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[u][e] = 0.f;
+
+    for (uint32_t b0 = 0; b0 < L; b0 += kFusedPass * PB) {
+        if (b0 > 0) load_block(b0);
+        const uint32_t np = live_passes(b0);
+        // ---- scores of the lane's positions, in log2 units (scale * log2 e):
+        // the weights 2^(s - m) equal e^(s' - m') of the natural-log scores.
+        // A pass wholly below cur reads only cached rows; the pass holding
+        // cur (and any rows past L) takes the selects ----
+        float s[PB];
+#pragma unroll
+        for (int i = 0; i < PB; ++i) {
+            s[i] = -INFINITY;
+            if ((uint32_t)i >= np) continue;
+            const uint32_t base = b0 + kFusedPass * (uint32_t)i;
+            const uint32_t pos = base + slot;
+            const bool plain = base + kFusedPass <= cur;   // wave-uniform
+            float dot = 0.f;
+#pragma unroll
+            for (int u = 0; u < NQ; ++u) {
+                float4 k = kv_word_f32<F16KV>(kr[i][u]);
+                if (!plain && pos == cur) k = *reinterpret_cast<const float4*>(kn + 64 * u + 4 * c);
+                dot = fmaf(q[u][0], k.x, dot);
+                dot = fmaf(q[u][1], k.y, dot);
+                dot = fmaf(q[u][2], k.z, dot);
+                dot = fmaf(q[u][3], k.w, dot);
+            }
+            dot = row16_sum(dot) * scale2;
+            s[i] = (plain || pos < L) ? dot : -INFINITY;
+        }
+        // ---- the wave's running softmax state and p.V ----
+        float mx = s[0];
+#pragma unroll
+        for (int i = 1; i < PB; ++i) mx = fmaxf(mx, s[i]);
+        mx = wave_max(mx);
+        if (mx == -INFINITY) continue;                 // no position of this wave in the block
+        const float m_new = fmaxf(m_w, mx);
+        const float f = exp2f(m_w - m_new);            // 0 while m_w = -inf
+        float sum = 0.f;
+#pragma unroll
+        for (int u = 0; u < NQ; ++u)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[u][e] *= f;
+#pragma unroll
+        for (int i = 0; i < PB; ++i) {
+            if ((uint32_t)i >= np) continue;
+            const uint32_t base = b0 + kFusedPass * (uint32_t)i;
+            const uint32_t pos = base + slot;
+            const bool plain = base + kFusedPass <= cur;   // wave-uniform
+            const float p_i = (plain || pos < L) ? exp2f(s[i] - m_new) : 0.f;
+            sum += p_i;
+#pragma unroll
+            for (int u = 0; u < NQ; ++u) {
+                float4 v = kv_word_f32<F16KV>(vr[i][u]);
+                if (!plain) {
+                    if (pos == cur) v = *reinterpret_cast<const float4*>(vn + 64 * u + 4 * c);
+                    if (pos >= L) v = make_float4(0.f, 0.f, 0.f, 0.f);   // select: stale bits never reach the sum
+                }
+                o[u][0] = fmaf(p_i, v.x, o[u][0]);
+                o[u][1] = fmaf(p_i, v.y, o[u][1]);
+                o[u][2] = fmaf(p_i, v.z, o[u][2]);
+                o[u][3] = fmaf(p_i, v.w, o[u][3]);
+            }
+        }
+        // each row slot counted once (its 16 lanes hold the same weights)
+        l_w = l_w * f + wave_sum(c == 0 ? sum : 0.f);
+        m_w = m_new;
+    }
+
+    // ---- merge: the wave's 4 row slots, then the 8 waves in order ----
+#pragma unroll
+    for (int u = 0; u < NQ; ++u)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            o[u][e] += __shfl_xor(o[u][e], 16, kWave);
+            o[u][e] += __shfl_xor(o[u][e], 32, kWave);
+        }
+    if (j == 0) {
+#pragma unroll
+        for (int u = 0; u < NQ; ++u)
+            *reinterpret_cast<float4*>(&accs[wave][64 * u + 4 * c]) = make_float4(o[u][0], o[u][1], o[u][2], o[u][3]);
+    }
+    if (lane == 0) {
+        mls[wave][0] = m_w;
+        mls[wave][1] = l_w;
+    }
+    __syncthreads();
+    if (wave >= NW) return;
+    // ---- each matrix-core wave merges the 8 waves' states for the rows its
+    // lanes quantise (lane l: rows l * NQ + u), in wave order ----
+    float M = mls[0][0];
+#pragma unroll
+    for (int w = 1; w < kFusedWaves; ++w) M = fmaxf(M, mls[w][0]);
+    float den = 0.f;
+    float xr[NQ];
+#pragma unroll
+    for (int u = 0; u < NQ; ++u) xr[u] = 0.f;
+#pragma unroll
+    for (int w = 0; w < kFusedWaves; ++w) {
+        const float sc = mls[w][0] == -INFINITY ? 0.f : exp2f(mls[w][0] - M);
+        den = fmaf(mls[w][1], sc, den);
+#pragma unroll
+        for (int u = 0; u < NQ; ++u) xr[u] = fmaf(accs[w][lane * NQ + u], sc, xr[u]);
+    }
+    float xm = 0.f;
+#pragma unroll
+    for (int u = 0; u < NQ; ++u) {
+        xr[u] = xr[u] / den;
+        xm = fmaxf(xm, fabsf(xr[u]));
+    }
+    xm = wave_max(xm);
+    gemv_q4m_item<GW, KW>(p, tile, wave, lane, [&xr](int u, uint32_t) { return xr[u]; }, xm, sw, esg, wq, zl[wave],
+                          zero16);
+}
+
+}  // namespace qora

@@ -84,6 +84,31 @@ __device__ __forceinline__ long long to_fixed(float v) {
     return __double2ll_rn((double)v * kFixScale);
 }
 
+// Kernel arguments are read by scalar loads that the compiler places next to
+// each field's first use, each waited for on its own: a chain of memory round
+// trips before a kernel's first large load (the argument lines do not stay
+// cached across launches). kernarg_warm(p) reads one dword of every 64-byte
+// line of the argument block in one statement, so all the line misses go out
+// together and are waited for once; later field reads hit the scalar cache.
+template <typename T>
+__device__ __forceinline__ void kernarg_warm(const T& p) {
+    static_assert(sizeof(T) % 4 == 0 && sizeof(T) <= 512, "argument block of at most 512 bytes");
+    constexpr int N = (int)(sizeof(T) / 4);
+    constexpr int I1 = 16 < N ? 16 : N - 1, I2 = 32 < N ? 32 : N - 1, I3 = 48 < N ? 48 : N - 1;
+    constexpr int I4 = 64 < N ? 64 : N - 1, I5 = 80 < N ? 80 : N - 1, I6 = 96 < N ? 96 : N - 1;
+    constexpr int I7 = 112 < N ? 112 : N - 1;
+    const uint32_t* w = reinterpret_cast<const uint32_t*>(&p);
+    asm volatile("" ::"s"(w[0]), "s"(w[I1]), "s"(w[I2]), "s"(w[I3]), "s"(w[I4]), "s"(w[I5]), "s"(w[I6]), "s"(w[I7]),
+                 "s"(w[N - 1]));
+}
+
+// Makes v a value the code below cannot re-load or move above this point:
+// its load is issued and waited for here.
+template <typename T>
+__device__ __forceinline__ void sgpr_pin(T& v) {
+    asm volatile("" : "+s"(v));
+}
+
 __device__ __forceinline__ float from_fixed(long long a) {
     return (float)((double)a * (1.0 / kFixScale));
 }

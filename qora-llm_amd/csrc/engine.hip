@@ -67,12 +67,18 @@ struct ModelState {
     uint32_t attn_chunk = 0, attn_s_max = 0;
     std::vector<GemvParams> p_qkv, p_o, p_gu, p_down;
     std::vector<AttnParams> p_attn;
+    // short contexts: attention inside the o GEMV (gemv_q4m_attn_kernel) for
+    // steps that append a position below attn_o_max
+    std::vector<AttnOParams> p_ao;
+    uint32_t attn_o_max = 0;
     RowdotParams p_lm{};
     LmHeadParams p_lmq{};
     ArgmaxFinishParams p_fin{};
     EmbedParams p_emb_tok{}, p_emb_prompt{};
     hipGraphExec_t g_step = nullptr;
     hipGraphExec_t g_prefill = nullptr;
+    hipGraphExec_t g_step_ao = nullptr;      // the same steps with the fused attention + o kernel
+    hipGraphExec_t g_prefill_ao = nullptr;
     uint64_t host_pos = 0;
     // batched prefill (prefill.hpp), set up on first use
     bool pf_ready = false;
@@ -223,6 +229,8 @@ void free_model(qora_hip_ctx* c) {
     ModelState& m = c->m;
     if (m.g_step) (void)hipGraphExecDestroy(m.g_step);
     if (m.g_prefill) (void)hipGraphExecDestroy(m.g_prefill);
+    if (m.g_step_ao) (void)hipGraphExecDestroy(m.g_step_ao);
+    if (m.g_prefill_ao) (void)hipGraphExecDestroy(m.g_prefill_ao);
     for (void* p : m.allocs) (void)hipFree(p);
     m = ModelState();
 }
@@ -266,14 +274,19 @@ int pack_model_gemv(qora_hip_ctx* c, int fmt, const GemvPlan& pl, GemvParams* p)
     return QORA_HIP_OK;
 }
 
-int record_step(qora_hip_ctx* c, bool with_lm_head) {
+// fused: attention inside the o GEMV (short contexts, see attn_o_max)
+int record_step(qora_hip_ctx* c, bool with_lm_head, bool fused) {
     ModelState& m = c->m;
     const hipStream_t s = c->stream;
     HIP_TRY(c, launch_embed(with_lm_head ? m.p_emb_tok : m.p_emb_prompt, s));
     for (uint32_t l = 0; l < m.L; ++l) {
         HIP_TRY(c, launch_gemv(m.fmt, m.pl_qkv, m.p_qkv[l], s));
-        HIP_TRY(c, launch_attn(m.p_attn[l], s));
-        HIP_TRY(c, launch_gemv(m.fmt, m.pl_o, m.p_o[l], s));
+        if (fused) {
+            HIP_TRY(c, launch_attn_o(m.pl_o, m.p_ao[l], s));
+        } else {
+            HIP_TRY(c, launch_attn(m.p_attn[l], s));
+            HIP_TRY(c, launch_gemv(m.fmt, m.pl_o, m.p_o[l], s));
+        }
         HIP_TRY(c, launch_gemv(m.fmt, m.pl_gu, m.p_gu[l], s));
         HIP_TRY(c, launch_gemv(m.fmt, m.pl_down, m.p_down[l], s));
     }
@@ -297,12 +310,26 @@ uint32_t attn_nsg(uint32_t max_chunk) {
     return max_chunk > (uint32_t)kAttnSub ? 4u : 1u;
 }
 
+// Steps that append a position below this bound run attention inside the o
+// GEMV (gemv_q4m_attn_kernel): every workgroup reads its head's whole
+// context, so the fused step pays off only while the context is short.
+// QORA_HIP_ATTN_O overrides the bound (0: never fused).
+constexpr uint32_t kAttnODefaultMax = 256;
+
+uint32_t attn_o_limit(const ModelState& m) {
+    if (m.fmt != FMT_Q4 || !attn_o_supported(m.pl_o, m.hd, m.H, m.groups)) return 0;
+    const char* v = std::getenv("QORA_HIP_ATTN_O");
+    const long n = (v && *v) ? std::atol(v) : (long)kAttnODefaultMax;
+    return n <= 0 ? 0u : (uint32_t)std::min<long>(n, (long)m.cap);
+}
+
 bool eager_mode() {
     const char* v = std::getenv("QORA_HIP_EAGER");
     return v && *v && *v != '0';
 }
 
-int launch_step(qora_hip_ctx* c, bool with_lm_head) {
+// pos: the position the step appends (its context length is pos + 1).
+int launch_step(qora_hip_ctx* c, bool with_lm_head, uint64_t pos) {
     ModelState& m = c->m;
     if (m.mk) {
         HIP_TRY(c, launch_decode_mk(m.mkp, m.d_mkp[with_lm_head ? 1 : 0], m.mk_blocks, c->stream));
@@ -310,14 +337,16 @@ int launch_step(qora_hip_ctx* c, bool with_lm_head) {
         else HIP_TRY(c, launch_advance_pos(m.d_pos, c->stream));
         return QORA_HIP_OK;
     }
-    if (eager_mode()) return record_step(c, with_lm_head);
-    HIP_TRY(c, hipGraphLaunch(with_lm_head ? c->m.g_step : c->m.g_prefill, c->stream));
+    const bool fused = pos < (uint64_t)m.attn_o_max;
+    if (eager_mode()) return record_step(c, with_lm_head, fused);
+    hipGraphExec_t g = fused ? (with_lm_head ? m.g_step_ao : m.g_prefill_ao) : (with_lm_head ? m.g_step : m.g_prefill);
+    HIP_TRY(c, hipGraphLaunch(g, c->stream));
     return QORA_HIP_OK;
 }
 
-int capture_step(qora_hip_ctx* c, bool with_lm_head, hipGraphExec_t* out) {
+int capture_step(qora_hip_ctx* c, bool with_lm_head, bool fused, hipGraphExec_t* out) {
     HIP_TRY(c, hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
-    const int rc = record_step(c, with_lm_head);
+    const int rc = record_step(c, with_lm_head, fused);
     hipGraph_t g = nullptr;
     const hipError_t e = hipStreamEndCapture(c->stream, &g);
     if (rc) {
@@ -731,8 +760,12 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
     const uint32_t gq = qd / 32, gkv = kvd / 32, gh = m.hidden / 32, gi = m.inter / 32;
     const uint32_t qkv_groups[3] = {gq, gkv, gkv};
     const uint32_t gu_groups[2] = {gi, gi};
+    // Q4 o projection: K slices of exactly one head (64 or 128 rows), the
+    // work items of the fused short-context step (gemv_q4m_attn_kernel)
+    const bool o_by_head = m.fmt == FMT_Q4 && (m.hd == 64 || m.hd == 128);
     if (!plan_model_gemv(m.fmt, m.hidden, qkv_groups, 3, false, c->cus, &m.pl_qkv) ||
-        !plan_model_gemv(m.fmt, qd, &gh, 1, false, c->cus, &m.pl_o, m.hd) ||
+        !(o_by_head ? plan_gemv_q4m(qd, &gh, 1, false, c->cus, &m.pl_o, m.hd, m.hd)
+                    : plan_model_gemv(m.fmt, qd, &gh, 1, false, c->cus, &m.pl_o, m.hd)) ||
         !plan_model_gemv(m.fmt, m.hidden, gu_groups, 2, true, c->cus, &m.pl_gu) ||
         !plan_model_gemv(m.fmt, m.inter, &gh, 1, false, c->cus, &m.pl_down)) {
         free_model(c);
@@ -810,13 +843,17 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
     //   xacc --RMSNorm+q|k|v GEMV--> qkv_acc --attention(RoPE, K/V append)-->
     //   partials --merge+o GEMV--> xacc (+=) --RMSNorm+gate|up GEMV--> gu_acc
     //   --silu*up+down GEMV--> xacc (+=)
-    // qkv_acc is cleared by the o kernel and gu_acc by the next q|k|v kernel,
-    // each after its last reader has finished.
+    // qkv_acc is cleared by the gate|up kernel and gu_acc by the next q|k|v
+    // kernel, each after its last reader has finished. Below attn_o_max
+    // positions, attention and the o GEMV run as one kernel
+    // (gemv_q4m_attn_kernel) that reads qkv_acc itself.
     m.p_qkv.resize(m.L);
     m.p_o.resize(m.L);
     m.p_gu.resize(m.L);
     m.p_down.resize(m.L);
     m.p_attn.resize(m.L);
+    m.attn_o_max = attn_o_limit(m);
+    if (m.attn_o_max) m.p_ao.resize(m.L);
     for (uint32_t l = 0; l < m.L; ++l) {
         const DevWeight* W[7];
         for (int j = 0; j < 7; ++j) W[j] = get_weight(c, m.wids[l * 7 + j]);
@@ -878,10 +915,9 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
         o.groups = m.groups;
         o.pos = m.d_pos;
         o.acc = m.d_xacc;
-        o.zero_ptr = m.d_qkv_acc;
-        o.zero_n = (uint32_t)qkv_n;
         apply_plan(m.pl_o, &o);
         if (int rc = pack_model_gemv(c, (int)m.fmt, m.pl_o, &o)) { free_model(c); return rc; }
+        if (m.attn_o_max) m.p_ao[l] = AttnOParams{o, a};
 
         GemvParams& g = m.p_gu[l];
         g = GemvParams{};
@@ -895,6 +931,8 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
         g.gamma = m.d_norms + ((size_t)l * 2 + 1) * m.hidden;
         g.ss_out = m.d_ss + ((size_t)l * 2 + 1) * kAttnMaxSplits;
         g.acc = m.d_gu_acc;
+        g.zero_ptr = m.d_qkv_acc;
+        g.zero_n = (uint32_t)qkv_n;
         apply_plan(m.pl_gu, &g);
         if (int rc = pack_model_gemv(c, (int)m.fmt, m.pl_gu, &g)) { free_model(c); return rc; }
 
@@ -954,8 +992,12 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
     if (mk_grid)
         if (int rc = setup_mk(c, d, emb, mk_grid)) { free_model(c); return rc; }
     HIP_TRY(c, hipDeviceSynchronize());
-    if (int rc = capture_step(c, true, &m.g_step)) { free_model(c); return rc; }
-    if (int rc = capture_step(c, false, &m.g_prefill)) { free_model(c); return rc; }
+    if (int rc = capture_step(c, true, false, &m.g_step)) { free_model(c); return rc; }
+    if (int rc = capture_step(c, false, false, &m.g_prefill)) { free_model(c); return rc; }
+    if (m.attn_o_max) {
+        if (int rc = capture_step(c, true, true, &m.g_step_ao)) { free_model(c); return rc; }
+        if (int rc = capture_step(c, false, true, &m.g_prefill_ao)) { free_model(c); return rc; }
+    }
     m.host_pos = 0;
     m.ready = true;
     return QORA_HIP_OK;
@@ -1085,7 +1127,7 @@ extern "C" int qora_hip_decode(qora_hip_ctx* c, uint32_t token, float* logits, u
     if (force_fail("launch")) return fail(c, QORA_HIP_E_DEVICE, "forced launch failure (QORA_HIP_FORCE_FAIL=launch)");
     c->h_pin[0] = (int32_t)token;
     HIP_TRY(c, hipMemcpyAsync(m.d_token, &c->h_pin[0], 4, hipMemcpyHostToDevice, c->stream));
-    if (int rc = launch_step(c, true)) return rc;
+    if (int rc = launch_step(c, true, m.host_pos)) return rc;
     if (int rc = finish_step(c, logits, argmax)) return rc;
     m.host_pos += 1;
     return QORA_HIP_OK;
@@ -1101,7 +1143,7 @@ extern "C" int qora_hip_generate_greedy(qora_hip_ctx* c, uint32_t token, uint32_
     c->h_pin[0] = (int32_t)token;
     HIP_TRY(c, hipMemcpyAsync(m.d_token, &c->h_pin[0], 4, hipMemcpyHostToDevice, c->stream));
     for (uint32_t i = 0; i < steps; ++i)
-        if (int rc = launch_step(c, true)) return rc;
+        if (int rc = launch_step(c, true, m.host_pos + i)) return rc;
     HIP_TRY(c, hipMemcpyAsync(out, m.d_gen + m.host_pos, (size_t)steps * 4, hipMemcpyDeviceToHost, c->stream));
     if (m.mk) HIP_TRY(c, hipMemcpyAsync(&c->h_pin[24], m.d_mk_err, 4, hipMemcpyDeviceToHost, c->stream));
     HIP_TRY(c, hipStreamSynchronize(c->stream));
@@ -1332,10 +1374,10 @@ extern "C" int qora_hip_prefill(qora_hip_ctx* c, const uint32_t* ids, size_t n, 
     }
     HIP_TRY(c, hipMemcpy(m.d_prompt, ids, n * 4, hipMemcpyHostToDevice));
     for (size_t i = 0; i + 1 < n; ++i)
-        if (int rc = launch_step(c, false)) return rc;
+        if (int rc = launch_step(c, false, i)) return rc;
     c->h_pin[0] = (int32_t)ids[n - 1];
     HIP_TRY(c, hipMemcpyAsync(m.d_token, &c->h_pin[0], 4, hipMemcpyHostToDevice, c->stream));
-    if (int rc = launch_step(c, true)) return rc;
+    if (int rc = launch_step(c, true, n - 1)) return rc;
     if (int rc = finish_step(c, logits, argmax)) return rc;
     m.host_pos = n;
     return QORA_HIP_OK;
@@ -1344,6 +1386,11 @@ extern "C" int qora_hip_prefill(qora_hip_ctx* c, const uint32_t* ids, size_t n, 
 extern "C" int qora_hip_decode_mode(const qora_hip_ctx* c) {
     if (!c || !c->m.ready) return 0;
     return c->m.mk ? 2 : 1;
+}
+
+extern "C" uint32_t qora_hip_attn_o_limit(const qora_hip_ctx* c) {
+    if (!c || !c->m.ready) return 0;
+    return c->m.attn_o_max;
 }
 
 extern "C" int qora_hip_kv_len(qora_hip_ctx* c, uint64_t* len) {
@@ -2010,7 +2057,7 @@ extern "C" int qora_hip_decode_sample(qora_hip_ctx* c, uint32_t token, const uin
     if (token >= m.vocab) return fail(c, QORA_HIP_E_INVALID, "token id out of range");
     c->h_pin[0] = (int32_t)token;
     HIP_TRY(c, hipMemcpyAsync(m.d_token, &c->h_pin[0], 4, hipMemcpyHostToDevice, c->stream));
-    if (int rc = launch_step(c, true)) return rc;
+    if (int rc = launch_step(c, true, m.host_pos)) return rc;
     uint32_t greedy = 0;
     if (int rc = finish_step(c, logits, &greedy)) return rc;
     m.host_pos += 1;

@@ -131,6 +131,9 @@ __device__ __forceinline__ void gemv_q4m_load_weights(const GemvParams& p, uint6
 }
 
 // The lane's NZ scales (adjacent binary16) and the wave's exponent bounds.
+// The bounds stay per-lane values (every lane loads the same byte) until the
+// quantisation reads them: taking them to a scalar here would wait for the
+// load before the weight loads are issued.
 template <int GW, int NZ>
 __device__ __forceinline__ void gemv_q4m_load_scales(const GemvParams& p, uint64_t bw, int lane,
                                                      uint32_t (&sw)[(NZ + 1) / 2], int (&esg)[GW]) {
@@ -154,8 +157,9 @@ __device__ __forceinline__ void gemv_q4m_load_scales(const GemvParams& p, uint64
         sw[0] = src[0];
     }
 #pragma unroll
-    for (int g = 0; g < GW; ++g) esg[g] = __builtin_amdgcn_readfirstlane((int)p.tes[bw * GW + g]);
+    for (int g = 0; g < GW; ++g) esg[g] = (int)p.tes[bw * GW + g];
 }
+
 
 // Attention-merge prologue run by one wave (see attn_merge_rows) for rows
 // [r0, r1) of the slice that starts at k0 (r1 - r0 <= 32, so at most two
@@ -236,6 +240,103 @@ __device__ __forceinline__ void attn_merge_rows_wave(const GemvParams& p, uint32
     if (lane < 32 && i < r1) xs[i] = k0 + i < k1 ? v : 0.f;
 }
 
+// One work item (column tile, K slice) of one matrix-core wave, once the
+// slice's input x is known: x * s quantised to 30-bit limbs (LDS), the
+// matrix-core pass over the wave's weight fragments, and the fixed-point
+// epilogue (one int64 atomic per column). xm = max |x| over the slice;
+// xval(u, r) returns x of slice row r, the lane's u-th z value (r = (lane *
+// NZ + u) % KW).
+template <int GW, int KW, typename XVal>
+__device__ __forceinline__ void gemv_q4m_item(const GemvParams& p, uint32_t tile, int wave, int lane, XVal xval,
+                                              float xm, const uint32_t (&sw)[(GW * KW / 64 + 1) / 2],
+                                              const int (&esv)[GW], const uint4 (&wq)[GW][KW / 64],
+                                              uint8_t (*zlw)[4][KW], const uint8_t* zero16) {
+    constexpr int NKB = KW / 64;
+    constexpr int NZ = GW * KW / 64;
+    const uint32_t li = (uint32_t)lane % 16, lk = (uint32_t)lane / 16;
+    int esg[GW];
+#pragma unroll
+    for (int g = 0; g < GW; ++g) esg[g] = __builtin_amdgcn_readfirstlane(esv[g]);
+    // 2^ex bounds max |x| (0 for an all-zero slice)
+    const int ex =
+        __builtin_amdgcn_readfirstlane(xm > 0.f ? (int)((__float_as_uint(xm) >> 23) & 0xFFu) - 126 : 0);
+
+    // ---- z = x * s quantised to 30-bit integers, stored as limb bytes ----
+#pragma unroll
+    for (int u = 0; u < NZ; ++u) {
+        const uint32_t e = (uint32_t)lane * NZ + u;
+        const uint32_t rz = e % KW, gz = e / KW;
+        int es = esg[0];
+#pragma unroll
+        for (int g = 1; g < GW; ++g) es = gz == (uint32_t)g ? esg[g] : es;
+        const uint16_t sbits = (uint16_t)((u & 1) ? (sw[u / 2] >> 16) : (sw[u / 2] & 0xFFFFu));
+        const float z = xval(u, rz) * h2f(sbits);
+        const int M = (int)rintf(ldexpf(z, 30 - (ex + es)));
+        const uint32_t limbs = (uint32_t)(M + 0x808080) ^ 0x808080u;
+        uint8_t* zp = &zlw[gz][0][rz];
+        zp[0] = (uint8_t)(limbs & 0xFFu);
+        zp[KW] = (uint8_t)((limbs >> 8) & 0xFFu);
+        zp[2 * KW] = (uint8_t)((limbs >> 16) & 0xFFu);
+        zp[3 * KW] = (uint8_t)(limbs >> 24);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    // ---- matrix cores: C[limb][column] += A[limb][k] * B[k][column] ----
+    v4i32 acc[2 * GW];
+#pragma unroll
+    for (int c = 0; c < 2 * GW; ++c) acc[c] = (v4i32){0, 0, 0, 0};
+#pragma unroll
+    for (int g = 0; g < GW; ++g) {
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb) {
+            const uint8_t* ap = li < 4 ? &zlw[g][li][kb * 64 + 16 * lk] : zero16;
+            const v4i32 a = *reinterpret_cast<const v4i32*>(ap);
+            const uint4 w = wq[g][kb];
+            acc[2 * g] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, q4_bfrag(w.x, w.y), acc[2 * g], 0, 0, 0);
+            acc[2 * g + 1] =
+                __builtin_amdgcn_mfma_i32_16x16x64_i8(a, q4_bfrag(w.z, w.w), acc[2 * g + 1], 0, 0, 0);
+        }
+    }
+    // the next item rewrites zl: this item's operand reads come first
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    // ---- epilogue: lanes 0..15 hold limbs 0..3 of column l of each block ----
+    // Y = C0 + 2^8 C1 + 2^16 C2 + 2^24 C3 as (C0 + 2^8 C1) + 2^16 (C2 + 2^8 C3):
+    // each half fits int32 (|C| < 2^22). value = Y * 2^(E - 34), so the
+    // fixed-point amount (2^36 units) is Y << (E + 2), rounded when E + 2 < 0.
+    if (lane < 16) {
+#pragma unroll
+        for (int g = 0; g < GW; ++g) {
+            const LaneSrc src = lane_source(p, tile, wave * GW + g, 4 * GW);
+            if (src.grp >= src.sg.groups) continue;
+            const int sh = max(min(ex + esg[g] + 2, 62), -62);
+            const int rsh = sh < 0 ? -sh : 0, lsh = sh > 0 ? sh : 0;
+            const long long rnd = rsh > 0 ? (1LL << (rsh - 1)) : 0;
+            long long* dst = p.acc + src.sg.col0 + src.grp * 32u + (uint32_t)lane;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const v4i32 c = acc[2 * g + h];
+                // |C| < 2^22 for 256 rows: each half fits int32; 512 rows need 64 bits
+                long long lo, hi;
+                if constexpr (KW <= 256) {
+                    lo = c[0] + (c[1] << 8);
+                    hi = c[2] + (c[3] << 8);
+                } else {
+                    lo = (long long)c[0] + ((long long)c[1] << 8);
+                    hi = (long long)c[2] + ((long long)c[3] << 8);
+                }
+                const long long Y = lo + (hi << 16);
+                const long long f = ((Y + rnd) >> rsh) << lsh;
+                atomicAdd(reinterpret_cast<unsigned long long*>(dst + h * 16), (unsigned long long)f);
+            }
+        }
+    }
+}
+
 // Four matrix-core waves plus one prologue wave. A wave waits on its loads
 // in issue order, so the roles are split by wave: the prologue wave loads
 // the slice's inputs and builds x (xs in LDS) while the matrix-core waves
@@ -247,6 +348,7 @@ __device__ __forceinline__ void attn_merge_rows_wave(const GemvParams& p, uint32
 // all loads in flight from the start.
 template <int GW, int KW, int PRO, int IPW = 1>
 __global__ __launch_bounds__(PRO == PRO_ATTN ? 512 : 320) void gemv_q4m_kernel(GemvParams p) {
+    kernarg_warm(p);
     constexpr int NW = 4;                    // matrix-core waves
     constexpr int NPW = PRO == PRO_ATTN ? 4 : 1;   // prologue waves (the attention merge gets four)
     constexpr int NT = (NW + NPW) * kWave;
@@ -357,7 +459,6 @@ __global__ __launch_bounds__(PRO == PRO_ATTN ? 512 : 320) void gemv_q4m_kernel(G
     }
     __syncthreads();
     if (wave >= NW) return;
-    const uint32_t li = (uint32_t)lane % 16, lk = (uint32_t)lane / 16;
 #pragma unroll
     for (int j = 0; j < IPW; ++j) {
         if ((uint32_t)j >= nit) break;
@@ -370,84 +471,9 @@ __global__ __launch_bounds__(PRO == PRO_ATTN ? 512 : 320) void gemv_q4m_kernel(G
         if constexpr (PRO == PRO_GAMMA_FIXED) {
             if (t == 0 && tile == 0) p.ss_out[split] = wred[j][1][0];
         }
-        // 2^ex bounds max |x| (0 for an all-zero slice)
-        const int ex =
-            __builtin_amdgcn_readfirstlane(xm > 0.f ? (int)((__float_as_uint(xm) >> 23) & 0xFFu) - 126 : 0);
-
-        // ---- z = x * s quantised to 30-bit integers, stored as limb bytes ----
-#pragma unroll
-        for (int u = 0; u < NZ; ++u) {
-            const uint32_t e = (uint32_t)lane * NZ + u;
-            const uint32_t rz = e % KW, gz = e / KW;
-            int es = esg[j][0];
-#pragma unroll
-            for (int g = 1; g < GW; ++g) es = gz == (uint32_t)g ? esg[j][g] : es;
-            const uint16_t sbits = (uint16_t)((u & 1) ? (sw[j][u / 2] >> 16) : (sw[j][u / 2] & 0xFFFFu));
-            const float z = xs[j][rz] * h2f(sbits);
-            const int M = (int)rintf(ldexpf(z, 30 - (ex + es)));
-            const uint32_t limbs = (uint32_t)(M + 0x808080) ^ 0x808080u;
-            uint8_t* zp = &zl[wave][gz][0][rz];
-            zp[0] = (uint8_t)(limbs & 0xFFu);
-            zp[KW] = (uint8_t)((limbs >> 8) & 0xFFu);
-            zp[2 * KW] = (uint8_t)((limbs >> 16) & 0xFFu);
-            zp[3 * KW] = (uint8_t)(limbs >> 24);
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
-        // ---- matrix cores: C[limb][column] += A[limb][k] * B[k][column] ----
-        v4i32 acc[2 * GW];
-#pragma unroll
-        for (int c = 0; c < 2 * GW; ++c) acc[c] = (v4i32){0, 0, 0, 0};
-#pragma unroll
-        for (int g = 0; g < GW; ++g) {
-#pragma unroll
-            for (int kb = 0; kb < NKB; ++kb) {
-                const uint8_t* ap = li < 4 ? &zl[wave][g][li][kb * 64 + 16 * lk] : zero16;
-                const v4i32 a = *reinterpret_cast<const v4i32*>(ap);
-                const uint4 w = wq[j][g][kb];
-                acc[2 * g] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, q4_bfrag(w.x, w.y), acc[2 * g], 0, 0, 0);
-                acc[2 * g + 1] =
-                    __builtin_amdgcn_mfma_i32_16x16x64_i8(a, q4_bfrag(w.z, w.w), acc[2 * g + 1], 0, 0, 0);
-            }
-        }
-        // the next item rewrites zl: this item's operand reads come first
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
-        // ---- epilogue: lanes 0..15 hold limbs 0..3 of column l of each block ----
-        // Y = C0 + 2^8 C1 + 2^16 C2 + 2^24 C3 as (C0 + 2^8 C1) + 2^16 (C2 + 2^8 C3):
-        // each half fits int32 (|C| < 2^22). value = Y * 2^(E - 34), so the
-        // fixed-point amount (2^36 units) is Y << (E + 2), rounded when E + 2 < 0.
-        if (lane < 16) {
-#pragma unroll
-            for (int g = 0; g < GW; ++g) {
-                const LaneSrc src = lane_source(p, tile, wave * GW + g, 4 * GW);
-                if (src.grp >= src.sg.groups) continue;
-                const int sh = max(min(ex + esg[j][g] + 2, 62), -62);
-                const int rsh = sh < 0 ? -sh : 0, lsh = sh > 0 ? sh : 0;
-                const long long rnd = rsh > 0 ? (1LL << (rsh - 1)) : 0;
-                long long* dst = p.acc + src.sg.col0 + src.grp * 32u + (uint32_t)lane;
-#pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    const v4i32 c = acc[2 * g + h];
-                    // |C| < 2^22 for 256 rows: each half fits int32; 512 rows need 64 bits
-                    long long lo, hi;
-                    if constexpr (KW <= 256) {
-                        lo = c[0] + (c[1] << 8);
-                        hi = c[2] + (c[3] << 8);
-                    } else {
-                        lo = (long long)c[0] + ((long long)c[1] << 8);
-                        hi = (long long)c[2] + ((long long)c[3] << 8);
-                    }
-                    const long long Y = lo + (hi << 16);
-                    const long long f = ((Y + rnd) >> rsh) << lsh;
-                    atomicAdd(reinterpret_cast<unsigned long long*>(dst + h * 16), (unsigned long long)f);
-                }
-            }
-        }
+        const float* xj = xs[j];
+        gemv_q4m_item<GW, KW>(p, tile, wave, lane, [xj](int, uint32_t r) { return xj[r]; }, xm, sw[j], esg[j], wq[j],
+                              zl[wave], zero16);
     }
 }
 

@@ -5,6 +5,7 @@
 #include "lmhead_mfma.hpp"
 #include "decode_mk.hpp"
 #include "attn.hpp"
+#include "attn_o.hpp"
 #include "prefill.hpp"
 #include "sample.hpp"
 
@@ -440,6 +441,24 @@ hipError_t launch_attn(const AttnParams& p, hipStream_t stream) {
     if (p.hd <= 64) QORA_ATTN(1);
     else QORA_ATTN(2);
 #undef QORA_ATTN
+    return hipGetLastError();
+}
+
+bool attn_o_supported(const GemvPlan& pl, uint32_t hd, uint32_t H, uint32_t groups) {
+    return pl.mfma && pl.gw == 1 && pl.ipw <= 1 && pl.kr == hd && pl.splits == H && (hd == 64 || hd == 128) &&
+           groups >= 1 && groups <= (uint32_t)kAttnMaxGroups;
+}
+
+hipError_t launch_attn_o(const GemvPlan& pl, const AttnOParams& p, hipStream_t stream) {
+    if (p.g.zero_ptr) return hipErrorInvalidValue;   // the fused kernel clears nothing
+    const dim3 grid(pl.blocks()), block(kFusedWaves * kWave);
+    if (p.a.hd == 128) {
+        if (p.a.kv_f16) hipLaunchKernelGGL((gemv_q4m_attn_kernel<128, true>), grid, block, 0, stream, p);
+        else hipLaunchKernelGGL((gemv_q4m_attn_kernel<128, false>), grid, block, 0, stream, p);
+    } else {
+        if (p.a.kv_f16) hipLaunchKernelGGL((gemv_q4m_attn_kernel<64, true>), grid, block, 0, stream, p);
+        else hipLaunchKernelGGL((gemv_q4m_attn_kernel<64, false>), grid, block, 0, stream, p);
+    }
     return hipGetLastError();
 }
 

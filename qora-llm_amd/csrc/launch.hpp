@@ -83,6 +83,11 @@ hipError_t launch_decode_mk(const MkParams& host, const MkParams* dev, uint32_t 
 void attn_geometry(uint32_t positions, uint32_t* chunk, uint32_t* s_max);
 hipError_t launch_attn(const AttnParams& p, hipStream_t stream);
 hipError_t launch_attn_combine(const AttnCombineParams& p, hipStream_t stream);
+// Short-context decode: attention of each query head in the o GEMV's
+// prologue (gemv_q4m_attn_kernel). The o plan must be an MFMA plan with one
+// group per wave and K slices of exactly one head (kr = hd, splits = H).
+bool attn_o_supported(const GemvPlan& pl, uint32_t hd, uint32_t H, uint32_t groups);
+hipError_t launch_attn_o(const GemvPlan& pl, const AttnOParams& p, hipStream_t stream);
 
 hipError_t launch_embed(const EmbedParams& p, hipStream_t stream);
 hipError_t launch_dequant_q4(const uint8_t* packed, const uint16_t* scales, uint64_t k, uint64_t n,

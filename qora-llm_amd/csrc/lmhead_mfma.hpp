@@ -106,6 +106,7 @@ __device__ __forceinline__ float block_max(float v, float* red) {
 // prologue (gamma p.gamma); otherwise the fp32 vector p.x as is.
 template <int NP, bool FIXED>
 __global__ __launch_bounds__(256) void lmhead_q4m_kernel(LmHeadParams p) {
+    kernarg_warm(p);
     constexpr int NT = 256, NW = 4;
     constexpr int UPT = NP / 2;                 // 16-byte units per lane per tile
     constexpr int COLS = 64 * NP;

@@ -272,6 +272,14 @@ struct AttnParams {
     uint64_t kv_ps, kv_hs;
 };
 
+// o projection with the attention of its query head computed in the
+// prologue (gemv_q4m_attn_kernel): the GEMV part (K slice = one head) and
+// the model-mode attention inputs (q|k|v sums, RoPE tables, cache).
+struct AttnOParams {
+    GemvParams g;
+    AttnParams a;
+};
+
 struct AttnCombineParams {
     const float* part;
     const int32_t* pos;

@@ -1,0 +1,129 @@
+"""The fused short-context decode step on the GPU: each layer's attention
+computed inside the o-projection kernel (gemv_q4m_attn_kernel) for steps that
+append a position below qora_hip_attn_o_limit, the split attention kernel
+above it. Both against the oracle (gemv.rs:914-989 inside forward_decode_raw,
+gemv.rs:872-1019), across the bound, from the first position, over several
+256-position blocks, and with f32 and f16 caches."""
+import numpy as np
+import pytest
+
+import __graft_entry__ as entry
+from helpers import REL_TOL, rel_err
+
+pytestmark = pytest.mark.gpu
+
+
+def _model(pkg, hd, layers=4, seed=0, positions=1024, fmt=1):
+    if hd == 64:
+        cfg = entry.smoke_config(pkg)
+    else:
+        cfg = pkg.ModelConfig(num_layers=layers, vocab=1000, hidden=256, intermediate=704, num_heads=16,
+                              num_kv_heads=4, head_dim=128, rope_half_dim=64, rope_theta=5e6,
+                              rope_positions=positions)
+    cfg.num_layers = layers
+    cfg.rope_positions = positions
+    return pkg.synthetic_model(cfg, seed=seed, fmt=fmt, rope_positions=positions)
+
+
+def test_limit_policy(ctx, pkg, monkeypatch):
+    w = _model(pkg, 64)
+    be = pkg.HipBackend(ctx, w, kv_capacity=512)
+    assert be.attn_o_limit() == 256                       # the default bound
+    be = pkg.HipBackend(ctx, w, kv_capacity=100)
+    assert be.attn_o_limit() == 100                       # never above the capacity
+    monkeypatch.setenv("QORA_HIP_ATTN_O", "0")
+    assert pkg.HipBackend(ctx, w, kv_capacity=128).attn_o_limit() == 0
+    monkeypatch.setenv("QORA_HIP_ATTN_O", "40")
+    assert pkg.HipBackend(ctx, _model(pkg, 128), kv_capacity=128).attn_o_limit() == 40
+    monkeypatch.delenv("QORA_HIP_ATTN_O")
+    # F16 weights run the VALU GEMVs: no fused step
+    assert pkg.HipBackend(ctx, _model(pkg, 64, fmt=0), kv_capacity=128).attn_o_limit() == 0
+
+
+@pytest.mark.parametrize("hd,kv_dtype", [(64, 0), (128, 0), (128, 1), (64, 1)])
+def test_steps_across_the_bound_match_oracle(ctx, pkg, orc, monkeypatch, hd, kv_dtype):
+    """Bound 24: a 12-token prompt, then 24 teacher-forced steps appending
+    positions 12..35 (fused up to 23, split from 24 on)."""
+    print(f"case attn_o across bound hd={hd} kv={kv_dtype}", flush=True)
+    monkeypatch.setenv("QORA_HIP_ATTN_O", "24")
+    w = _model(pkg, hd, positions=128)
+    be = pkg.HipBackend(ctx, w, kv_capacity=128, kv_dtype=kv_dtype)
+    assert be.attn_o_limit() == 24
+    om = orc.OracleModel(w, kv_capacity=128, T=4)
+    tol = REL_TOL if kv_dtype == 0 else 5e-3
+    prompt = pkg.synth_tokens(hd, 2000, 12, w.config.vocab)
+    logits, _ = be.raw_prefill(prompt)
+    assert rel_err(logits, om.prefill(prompt)) <= tol
+    for t in pkg.synth_tokens(hd, 2001, 24, w.config.vocab):
+        pos = be.kv_len()
+        logits, tok = be.forward_decode_raw(int(t))
+        ref = om.forward_decode(int(t))
+        assert rel_err(logits, ref) <= tol, pos
+        if orc.top2_gap(ref) > 1e-4 * float(np.max(np.abs(ref))):
+            assert tok == orc.argmax(ref), pos
+    for layer in (0, w.config.num_layers - 1):
+        k, v = be.kv_layer(layer)
+        kr, vr = om.kv_layer(layer)
+        assert rel_err(k, kr) <= tol and rel_err(v, vr) <= tol
+
+
+@pytest.mark.parametrize("hd", [64, 128])
+def test_fused_from_the_first_position(ctx, pkg, orc, monkeypatch, hd):
+    """Token-by-token prefill: the first step appends position 0 with no
+    cached row to read."""
+    print(f"case attn_o first position hd={hd}", flush=True)
+    monkeypatch.setenv("QORA_HIP_PREFILL", "seq")
+    w = _model(pkg, hd, positions=64)
+    be = pkg.HipBackend(ctx, w, kv_capacity=64)
+    assert be.attn_o_limit() == 64
+    om = orc.OracleModel(w, kv_capacity=64, T=4)
+    for n in (1, 5):
+        be.kv_reset()
+        prompt = pkg.synth_tokens(hd + n, 2100, n, w.config.vocab)
+        logits, _ = be.raw_prefill(prompt)
+        assert rel_err(logits, om.prefill(prompt)) <= REL_TOL, n
+    k, v = be.kv_layer(1)
+    kr, vr = om.kv_layer(1)
+    assert rel_err(k, kr) <= REL_TOL and rel_err(v, vr) <= REL_TOL
+
+
+@pytest.mark.parametrize("kv_dtype", [0, 1])
+def test_fused_over_several_blocks(ctx, pkg, orc, monkeypatch, kv_dtype):
+    """Bound raised to 640: contexts of 501..504 positions take two 256-position
+    blocks per workgroup, the appended row in the second."""
+    print(f"case attn_o blocks kv={kv_dtype}", flush=True)
+    monkeypatch.setenv("QORA_HIP_ATTN_O", "640")
+    cap, n = 640, 500
+    w = _model(pkg, 128, positions=cap, seed=5)
+    be = pkg.HipBackend(ctx, w, kv_capacity=cap, kv_dtype=kv_dtype)
+    assert be.attn_o_limit() == 640
+    om = orc.OracleModel(w, kv_capacity=cap, T=4)
+    r = np.random.default_rng(21)
+    kvd = w.config.num_kv_heads * w.config.head_dim
+    for layer in range(w.config.num_layers):
+        k = r.standard_normal((n, kvd), dtype=np.float32)
+        v = r.standard_normal((n, kvd), dtype=np.float32)
+        if kv_dtype:
+            k, v = k.astype(np.float16).astype(np.float32), v.astype(np.float16).astype(np.float32)
+        be.kv_upload(layer, k, v)
+        om.kv_set(layer, k, v)
+    tol = REL_TOL if kv_dtype == 0 else 5e-3
+    for t in pkg.synth_tokens(5, 2001, 4, w.config.vocab):
+        logits, _ = be.forward_decode_raw(int(t))
+        assert rel_err(logits, om.forward_decode(int(t))) <= tol
+    k, v = be.kv_layer(2)
+    kr, vr = om.kv_layer(2)
+    assert rel_err(k, kr) <= tol and rel_err(v, vr) <= tol
+
+
+def test_device_chained_greedy_crosses_the_bound(ctx, pkg, orc, monkeypatch):
+    """generate_greedy launches every step from the host in one call; each
+    picks its graph by the position it appends."""
+    monkeypatch.setenv("QORA_HIP_ATTN_O", "30")
+    w = _model(pkg, 128, positions=128, seed=6)
+    be = pkg.HipBackend(ctx, w, kv_capacity=128)
+    om = orc.OracleModel(w, kv_capacity=128, T=4)
+    prompt = pkg.synth_tokens(6, 2000, 10, w.config.vocab)
+    ref, _ = om.greedy(prompt, 40)
+    _, first = be.raw_prefill(prompt, want_logits=False)
+    assert [first] + be.generate_greedy(first, 39).tolist() == ref
