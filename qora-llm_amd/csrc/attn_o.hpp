@@ -109,13 +109,18 @@ __global__ __launch_bounds__(kFusedWaves * kWave) void gemv_q4m_attn_kernel(Attn
     W kr[PB][NQ], vr[PB][NQ];
     // passes of the block at b0 holding positions below L (wave-uniform)
     auto live_passes = [&](uint32_t b0) { return min((uint32_t)PB, (L - b0 + kFusedPass - 1) / kFusedPass); };
+    // Register slot i holds pass (i + rot) mod np: the workgroups of an XCD
+    // read the same rows, and staggering their order spreads the requests
+    // over the L2 channels instead of all asking for the same lines at once.
+    const uint32_t rot = blockIdx.x / 8u;
+    auto pass_base = [&](uint32_t b0, uint32_t i, uint32_t np) { return b0 + kFusedPass * ((i + rot) % np); };
     auto load_block = [&](uint32_t b0) {
         // rows >= cur are not read (clamped to cur - 1, discarded below); none when cur == 0
         const uint32_t np = cur == 0 ? 0u : live_passes(b0);
 #pragma unroll
         for (int i = 0; i < PB; ++i) {
             if ((uint32_t)i < np) {
-                const uint32_t pos = min(b0 + kFusedPass * (uint32_t)i + slot, cur - 1u);
+                const uint32_t pos = min(pass_base(b0, (uint32_t)i, np) + slot, cur - 1u);
 #pragma unroll
                 for (int u = 0; u < NQ; ++u) {
                     const uint64_t off = ((uint64_t)pos * cps + coff + 64u * (uint32_t)u + 4u * c) * EB;
@@ -222,7 +227,7 @@ __global__ __launch_bounds__(kFusedWaves * kWave) void gemv_q4m_attn_kernel(Attn
         for (int i = 0; i < PB; ++i) {
             s[i] = -INFINITY;
             if ((uint32_t)i >= np) continue;
-            const uint32_t base = b0 + kFusedPass * (uint32_t)i;
+            const uint32_t base = pass_base(b0, (uint32_t)i, np);
             const uint32_t pos = base + slot;
             const bool plain = base + kFusedPass <= cur;   // wave-uniform
             float dot = 0.f;
@@ -254,7 +259,7 @@ __global__ __launch_bounds__(kFusedWaves * kWave) void gemv_q4m_attn_kernel(Attn
 #pragma unroll
         for (int i = 0; i < PB; ++i) {
             if ((uint32_t)i >= np) continue;
-            const uint32_t base = b0 + kFusedPass * (uint32_t)i;
+            const uint32_t base = pass_base(b0, (uint32_t)i, np);
             const uint32_t pos = base + slot;
             const bool plain = base + kFusedPass <= cur;   // wave-uniform
             const float p_i = (plain || pos < L) ? exp2f(s[i] - m_new) : 0.f;
