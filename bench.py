@@ -167,7 +167,7 @@ def cpu_baseline(pkg, orc, w, prompt, seconds=15.0, threads=16):
     then decode tokens until `seconds` of decode time have passed."""
     threads = max(1, min(threads, os.cpu_count() or 1))
     orc.set_threads(threads)
-    om = orc.OracleModel(w, kv_capacity=256, T=threads)
+    om = orc.OracleModel(w, kv_capacity=1024, T=threads)
     logits = om.prefill(prompt[:8])
     tok = orc.argmax(logits)
     n = 0
@@ -177,7 +177,7 @@ def cpu_baseline(pkg, orc, w, prompt, seconds=15.0, threads=16):
         tok = orc.argmax(logits)
         n += 1
         el = time.perf_counter() - t0
-        if el >= seconds or n >= 200:
+        if el >= seconds or n >= 1000:
             break
     return {"value": n / el, "unit": "tok/s", "cores": threads, "kind": "port",
             "sample": f"C restatement of the reference CPU path (AVX-512 LUT GEMV, k-split T={threads}); "
