@@ -537,8 +537,8 @@ bool pf_gemm_supported(uint32_t k, uint32_t n) { return k > 0 && k % 32 == 0 && 
 
 // Launch shape of the prefill GEMM: 128-column tiles when they still give
 // every CU a block, else 64; then split K (into runs of at least 256 rows)
-// until about four blocks per CU are in flight, since each block's K loop is
-// bound by its global-load latency.
+// until about four blocks per CU are in flight (four fit at once), since
+// each block's K loop is bound by its global-load latency.
 PfGemmShape pf_gemm_shape(uint32_t T, uint32_t k, uint32_t n, int cus) {
     PfGemmShape sh{};
     const uint32_t mt = (T + 63) / 64;
@@ -564,13 +564,22 @@ hipError_t launch_pf_gemm(int fmt, const PrefillGemmParams& p, hipStream_t strea
         return hipErrorInvalidValue;
     const uint32_t nt = (p.n % 128 == 0 && p.nt == 128) ? 128 : 64;
     const dim3 grid((p.n + nt - 1) / nt, (p.T + 63) / 64, p.splits);
+    // QORA_HIP_PF_MODE=0 selects the double-buffered K loop (pf_gemm_kernel MODE 0)
+    const char* em = std::getenv("QORA_HIP_PF_MODE");
+    const int mode = (em && *em && std::atoi(em) == 0) ? 0 : 1;
+#define QORA_PF_GEMM(NT_, Q4_)                                                                              \
+    do {                                                                                                   \
+        if (mode == 0) hipLaunchKernelGGL((pf_gemm_kernel<NT_, Q4_, 0>), grid, dim3(256), 0, stream, p);  \
+        else hipLaunchKernelGGL((pf_gemm_kernel<NT_, Q4_, 1>), grid, dim3(256), 0, stream, p);            \
+    } while (0)
     if (fmt == FMT_Q4) {
-        if (nt == 128) hipLaunchKernelGGL((pf_gemm_kernel<128, true>), grid, dim3(256), 0, stream, p);
-        else hipLaunchKernelGGL((pf_gemm_kernel<64, true>), grid, dim3(256), 0, stream, p);
+        if (nt == 128) QORA_PF_GEMM(128, true);
+        else QORA_PF_GEMM(64, true);
     } else {
-        if (nt == 128) hipLaunchKernelGGL((pf_gemm_kernel<128, false>), grid, dim3(256), 0, stream, p);
-        else hipLaunchKernelGGL((pf_gemm_kernel<64, false>), grid, dim3(256), 0, stream, p);
+        if (nt == 128) QORA_PF_GEMM(128, false);
+        else QORA_PF_GEMM(64, false);
     }
+#undef QORA_PF_GEMM
     if (p.splits > 1) {
         const uint64_t total = (uint64_t)p.T * p.n;
         const uint32_t blocks = (uint32_t)std::min<uint64_t>(4096, (total + 255) / 256);

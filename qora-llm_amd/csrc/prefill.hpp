@@ -179,15 +179,23 @@ __global__ __launch_bounds__(256) void pf_weight_exp_kernel(const uint32_t* part
 // ---------------------------------------------------------------------------
 // The GEMM. Grid (n / NT column tiles, ceil(T / 64) token tiles).
 // ---------------------------------------------------------------------------
-template <int NT, bool Q4>
+// The K loop waits on each slice's global loads (~1 us under load) with one
+// slice in flight, so what hides that latency is other blocks on the CU.
+// MODE 1 (default): one LDS buffer, a second barrier per slice, 30 KB, four
+// blocks per CU (512 tokens: prefill 23.4 ms). MODE 0: double-buffered LDS,
+// 60 KB, two blocks per CU (26.4 ms). Two slices in flight in registers
+// (141 VGPRs, two blocks per CU) measured 26.0 ms.
+template <int NT, bool Q4, int MODE>
 __global__ __launch_bounds__(256) void pf_gemm_kernel(PrefillGemmParams p) {
     constexpr int MT = 64, KC = 32;
+    constexpr bool DB = MODE == 0;
+    constexpr int NB = DB ? 2 : 1;                   // LDS buffers
     constexpr int XS = KC + 8;                      // LDS row stride in halves (80 B: 16-B aligned, no read conflicts)
     constexpr int WN = NT / 2;                      // columns per wave
     constexpr int TN = WN / 16;                     // 16-column MFMA tiles per wave
     constexpr int RPT = NT / 16;                    // weight rows per thread per slice (8 or 4)
-    __shared__ __align__(16) _Float16 xs[2][2][MT * XS];
-    __shared__ __align__(16) _Float16 ws[2][Q4 ? 2 : 1][NT * XS];
+    __shared__ __align__(16) _Float16 xs[NB][2][MT * XS];
+    __shared__ __align__(16) _Float16 ws[NB][Q4 ? 2 : 1][NT * XS];
 
     const int t = threadIdx.x;
     const int lane = t & (kWave - 1);
@@ -210,31 +218,37 @@ __global__ __launch_bounds__(256) void pf_gemm_kernel(PrefillGemmParams p) {
     float wscale = 1.0f;                            // 2^-f_g
     if constexpr (Q4) wscale = ldexpf(1.0f, -(int)p.wf[grp]);
 
-    uint4 xh_r, xl_r;
-    uint32_t wq[RPT];                               // Q4: byte (2 columns) per row; F16: 2 halves per row
-    uint16_t sc[Q4 ? RPT : 1];
+    // one slice of operands in registers, between its loads and its LDS stores
+    struct Slice {
+        uint4 xh, xl;
+        uint32_t wq[RPT];                           // Q4: byte (2 columns) per row; F16: 2 halves per row
+        uint16_t sc[Q4 ? RPT : 1];
+    };
 
-    auto load_slice = [&](uint32_t k0) {
+    auto load_slice = [&](Slice& q, uint32_t k0) {
         if (xrow_ok) {
-            xh_r = *reinterpret_cast<const uint4*>(p.xh + xoff + k0);
-            xl_r = *reinterpret_cast<const uint4*>(p.xl + xoff + k0);
+            q.xh = *reinterpret_cast<const uint4*>(p.xh + xoff + k0);
+            q.xl = *reinterpret_cast<const uint4*>(p.xl + xoff + k0);
         } else {
-            xh_r = make_uint4(0, 0, 0, 0);
-            xl_r = make_uint4(0, 0, 0, 0);
+            q.xh = make_uint4(0, 0, 0, 0);
+            q.xl = make_uint4(0, 0, 0, 0);
         }
 #pragma unroll
         for (int r = 0; r < RPT; ++r) {
             const uint64_t row = k0 + rg * RPT + r;
             if constexpr (Q4) {
-                wq[r] = p.w[row * (N / 2) + colc / 2];
-                sc[r] = p.scales[row * groups + grp];
+                q.wq[r] = p.w[row * (N / 2) + colc / 2];
+                q.sc[r] = p.scales[row * groups + grp];
             } else {
-                wq[r] = *reinterpret_cast<const uint32_t*>(p.w + (row * N + colc) * 2);
+                q.wq[r] = *reinterpret_cast<const uint32_t*>(p.w + (row * N + colc) * 2);
             }
         }
     };
 
-    auto store_slice = [&](int buf) {
+    auto store_slice = [&](const Slice& q, int buf) {
+        const uint4 xh_r = q.xh, xl_r = q.xl;
+        const uint32_t* wq = q.wq;
+        const uint16_t* sc = q.sc;
         *reinterpret_cast<uint4*>(&xs[buf][0][xr * XS + xp * 8]) = xh_r;
         *reinterpret_cast<uint4*>(&xs[buf][1][xr * XS + xp * 8]) = xl_r;
         // two columns, RPT consecutive k each
@@ -285,12 +299,7 @@ __global__ __launch_bounds__(256) void pf_gemm_kernel(PrefillGemmParams p) {
     const uint32_t li = (uint32_t)lane % 16u, kq = (uint32_t)lane / 16u;
     const uint32_t kb = blockIdx.z * p.kper;        // this split's rows [kb, kb + steps * KC)
     const uint32_t steps = (min(K, kb + p.kper) - kb) / KC;
-    load_slice(kb);
-    store_slice(0);
-    __syncthreads();
-    for (uint32_t s = 0; s < steps; ++s) {
-        const int buf = (int)(s & 1u);
-        if (s + 1 < steps) load_slice(kb + (s + 1) * KC);
+    auto compute = [&](int buf) {
         half8v ah[2], al[2];
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
@@ -314,8 +323,28 @@ __global__ __launch_bounds__(256) void pf_gemm_kernel(PrefillGemmParams p) {
                     acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], bl, acc[i][j], 0, 0, 0);
             }
         }
-        if (s + 1 < steps) store_slice(buf ^ 1);
+    };
+
+    Slice sa;
+    load_slice(sa, kb);
+    if constexpr (MODE == 0) {
+        store_slice(sa, 0);
         __syncthreads();
+        for (uint32_t s = 0; s < steps; ++s) {
+            const int buf = (int)(s & 1u);
+            if (s + 1 < steps) load_slice(sa, kb + (s + 1) * KC);
+            compute(buf);
+            if (s + 1 < steps) store_slice(sa, buf ^ 1);
+            __syncthreads();
+        }
+    } else {
+        for (uint32_t s = 0; s < steps; ++s) {
+            if (s > 0) __syncthreads();                // every wave has read the buffer
+            store_slice(sa, 0);
+            __syncthreads();
+            if (s + 1 < steps) load_slice(sa, kb + (s + 1) * KC);
+            compute(0);
+        }
     }
 
     // epilogue: y = acc * 2^(e_t + f_g), stored or added to the residual rows

@@ -194,3 +194,18 @@ def test_batched_and_sequential_prefill_agree(ctx, pkg, orc, monkeypatch):
     assert rel_err(batched, seq) <= REL_TOL
     if orc.top2_gap(seq) > 1e-4 * float(np.max(np.abs(seq))):
         assert tb == ts
+
+
+@pytest.mark.parametrize("k,n,T", [(2048, 11008, 130), (2048, 512, 64)])
+def test_gemm_loop_modes_bit_identical(ctx, pkg, monkeypatch, k, n, T):
+    """The single-buffered K loop (default) and the double-buffered one
+    (QORA_HIP_PF_MODE=0) issue the same products in the same order."""
+    print(f"case gemm modes k={k} n={n} T={T}", flush=True)
+    packed, scales = pkg.synth_q4(34, k + n, k, n)
+    x = (rng(T + 3).standard_normal((T, k)) * 2).astype(np.float32)
+    wid = ctx.upload(pkg.Weight(k=k, n=n, packed=packed, scales=scales))
+    with device(ctx) as d:
+        y1 = _gemm(ctx, d, wid, x, T, n)
+        monkeypatch.setenv("QORA_HIP_PF_MODE", "0")
+        y0 = _gemm(ctx, d, wid, x, T, n)
+    assert np.array_equal(y0, y1)
