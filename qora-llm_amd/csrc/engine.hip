@@ -80,6 +80,9 @@ struct ModelState {
     hipGraphExec_t g_step_ao = nullptr;      // the same steps with the fused attention + o kernel
     hipGraphExec_t g_prefill_ao = nullptr;
     uint64_t host_pos = 0;
+    // token id that d_token holds once the queued work is done (-1: not known):
+    // a decode call passing that id skips the upload
+    int64_t dev_token = -1;
     // batched prefill (prefill.hpp), set up on first use
     bool pf_ready = false;
     uint32_t pf_tc = 0;                  // tokens per chunk
@@ -142,6 +145,11 @@ struct qora_hip_ctx {
     float* ws_attn_part = nullptr;
     uint64_t ws_attn_part_n = 0;
     int32_t* h_pin = nullptr;            // pinned staging: [0] token in, [1] token out, [2] pos
+    // The step's argmax, stored by argmax_finish_kernel straight into mapped,
+    // coherent pinned memory: reading it back takes the stream sync only, not
+    // a copy (null if that allocation failed: then a copy is used).
+    int32_t* h_tok = nullptr;
+    int32_t* d_h_tok = nullptr;
     bool capturing = false;
     std::vector<PreparedGemv> gemvs;
     ModelState m;
@@ -414,6 +422,11 @@ extern "C" int qora_hip_create(int device, qora_hip_ctx** out) {
         delete c;
         return QORA_HIP_E_DEVICE;
     }
+    if (hipHostMalloc((void**)&c->h_tok, 64, hipHostMallocMapped | hipHostMallocCoherent) == hipSuccess) {
+        if (hipHostGetDevicePointer((void**)&c->d_h_tok, c->h_tok, 0) != hipSuccess) c->d_h_tok = nullptr;
+    } else {
+        c->h_tok = nullptr;
+    }
     *out = c;
     return QORA_HIP_OK;
 }
@@ -434,6 +447,7 @@ extern "C" int qora_hip_destroy(qora_hip_ctx* c) {
                     (void*)c->smp_rng, (void*)c->smp_tok, (void*)c->smp_pen})
         if (p) (void)hipFree(p);
     if (c->h_pin) (void)hipHostFree(c->h_pin);
+    if (c->h_tok) (void)hipHostFree(c->h_tok);
     (void)hipStreamDestroy(c->stream);
     delete c;
     return QORA_HIP_OK;
@@ -687,7 +701,7 @@ int setup_mk(qora_hip_ctx* c, const qora_model_desc* d, const DevWeight* emb, ui
         m.d_mkp[i] = (MkParams*)dp;
     }
     m.mk_blocks = nb;
-    m.p_fin_mk = ArgmaxFinishParams{m.d_argv, m.d_argi, nb, m.d_token, m.d_pos, m.d_gen};
+    m.p_fin_mk = ArgmaxFinishParams{m.d_argv, m.d_argi, nb, m.d_token, m.d_pos, m.d_gen, c->d_h_tok};
     m.mk = true;
     return QORA_HIP_OK;
 }
@@ -983,7 +997,7 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
         m.p_lmq.part_val = m.d_argv;
         m.p_lmq.part_idx = m.d_argi;
     }
-    m.p_fin = ArgmaxFinishParams{m.d_argv, m.d_argi, m.lm_blocks, m.d_token, m.d_pos, m.d_gen};
+    m.p_fin = ArgmaxFinishParams{m.d_argv, m.d_argi, m.lm_blocks, m.d_token, m.d_pos, m.d_gen, c->d_h_tok};
     m.p_emb_tok = EmbedParams{(const uint8_t*)emb->w, (const uint16_t*)emb->scales, (int)m.fmt, m.hidden,
                               m.vocab, m.d_token, nullptr, m.d_xacc};
     m.p_emb_prompt = EmbedParams{(const uint8_t*)emb->w, (const uint16_t*)emb->scales, (int)m.fmt, m.hidden,
@@ -1107,13 +1121,29 @@ void print_mk_trace(qora_hip_ctx* c) {
 
 int finish_step(qora_hip_ctx* c, float* logits, uint32_t* argmax) {
     ModelState& m = c->m;
-    HIP_TRY(c, hipMemcpyAsync(&c->h_pin[16], m.d_token, 4, hipMemcpyDeviceToHost, c->stream));
+    const bool mapped = c->d_h_tok != nullptr;   // argmax_finish_kernel stored the token in h_tok
+    if (!mapped) HIP_TRY(c, hipMemcpyAsync(&c->h_pin[16], m.d_token, 4, hipMemcpyDeviceToHost, c->stream));
     if (m.mk) HIP_TRY(c, hipMemcpyAsync(&c->h_pin[24], m.d_mk_err, 4, hipMemcpyDeviceToHost, c->stream));
     if (logits) HIP_TRY(c, hipMemcpyAsync(logits, m.d_logits, (size_t)m.vocab * 4, hipMemcpyDeviceToHost, c->stream));
     HIP_TRY(c, hipStreamSynchronize(c->stream));
     if (int rc = check_mk_error(c)) return rc;
     print_mk_trace(c);
-    if (argmax) *argmax = (uint32_t)c->h_pin[16];
+    const int32_t tok = mapped ? *reinterpret_cast<volatile int32_t*>(c->h_tok) : c->h_pin[16];
+    m.dev_token = tok;
+    if (argmax) *argmax = (uint32_t)tok;
+    return QORA_HIP_OK;
+}
+
+// Uploads the step's input token unless d_token already holds it (the previous
+// step's argmax, the usual greedy case). The known value is dropped until the
+// new step's result has been read back.
+int put_token(qora_hip_ctx* c, uint32_t token) {
+    ModelState& m = c->m;
+    const bool known = m.dev_token == (int64_t)token;
+    m.dev_token = -1;
+    if (known) return QORA_HIP_OK;
+    c->h_pin[0] = (int32_t)token;
+    HIP_TRY(c, hipMemcpyAsync(m.d_token, &c->h_pin[0], 4, hipMemcpyHostToDevice, c->stream));
     return QORA_HIP_OK;
 }
 
@@ -1125,8 +1155,7 @@ extern "C" int qora_hip_decode(qora_hip_ctx* c, uint32_t token, float* logits, u
     ModelState& m = c->m;
     if (token >= m.vocab) return fail(c, QORA_HIP_E_INVALID, "token id out of range");
     if (force_fail("launch")) return fail(c, QORA_HIP_E_DEVICE, "forced launch failure (QORA_HIP_FORCE_FAIL=launch)");
-    c->h_pin[0] = (int32_t)token;
-    HIP_TRY(c, hipMemcpyAsync(m.d_token, &c->h_pin[0], 4, hipMemcpyHostToDevice, c->stream));
+    if (int rc = put_token(c, token)) return rc;
     if (int rc = launch_step(c, true, m.host_pos)) return rc;
     if (int rc = finish_step(c, logits, argmax)) return rc;
     m.host_pos += 1;
@@ -1140,14 +1169,14 @@ extern "C" int qora_hip_generate_greedy(qora_hip_ctx* c, uint32_t token, uint32_
     if (token >= m.vocab) return fail(c, QORA_HIP_E_INVALID, "token id out of range");
     if (steps == 0) return QORA_HIP_OK;
     if (force_fail("launch")) return fail(c, QORA_HIP_E_DEVICE, "forced launch failure (QORA_HIP_FORCE_FAIL=launch)");
-    c->h_pin[0] = (int32_t)token;
-    HIP_TRY(c, hipMemcpyAsync(m.d_token, &c->h_pin[0], 4, hipMemcpyHostToDevice, c->stream));
+    if (int rc = put_token(c, token)) return rc;
     for (uint32_t i = 0; i < steps; ++i)
         if (int rc = launch_step(c, true, m.host_pos + i)) return rc;
     HIP_TRY(c, hipMemcpyAsync(out, m.d_gen + m.host_pos, (size_t)steps * 4, hipMemcpyDeviceToHost, c->stream));
     if (m.mk) HIP_TRY(c, hipMemcpyAsync(&c->h_pin[24], m.d_mk_err, 4, hipMemcpyDeviceToHost, c->stream));
     HIP_TRY(c, hipStreamSynchronize(c->stream));
     if (int rc = check_mk_error(c)) return rc;
+    m.dev_token = out[steps - 1];   // the last step's argmax stays in d_token
     m.host_pos += steps;
     return QORA_HIP_OK;
 }
@@ -1231,7 +1260,7 @@ int pf_setup(qora_hip_ctx* c) {
     m.p_lm_pf.x = m.d_pf_xn;
     m.p_lm_pf.xacc = nullptr;
     m.p_lm_pf.gamma = nullptr;
-    m.p_fin_pf = ArgmaxFinishParams{m.d_argv, m.d_argi, m.lm_blocks, m.d_token, nullptr, nullptr};
+    m.p_fin_pf = ArgmaxFinishParams{m.d_argv, m.d_argi, m.lm_blocks, m.d_token, nullptr, nullptr, c->d_h_tok};
     m.pf_tc = tc;
     m.pf_ready = true;
     return QORA_HIP_OK;
@@ -1362,6 +1391,7 @@ extern "C" int qora_hip_prefill(qora_hip_ctx* c, const uint32_t* ids, size_t n, 
     for (size_t i = 0; i < n; ++i)
         if (ids[i] >= m.vocab) return fail(c, QORA_HIP_E_INVALID, "token id out of range");
     m.host_pos = 0;
+    m.dev_token = -1;
     if (int rc = set_device_pos(c, 0)) return rc;
     if (int rc = check_step_room(c, n)) return rc;
     if (force_fail("launch")) return fail(c, QORA_HIP_E_DEVICE, "forced launch failure (QORA_HIP_FORCE_FAIL=launch)");
@@ -1375,8 +1405,7 @@ extern "C" int qora_hip_prefill(qora_hip_ctx* c, const uint32_t* ids, size_t n, 
     HIP_TRY(c, hipMemcpy(m.d_prompt, ids, n * 4, hipMemcpyHostToDevice));
     for (size_t i = 0; i + 1 < n; ++i)
         if (int rc = launch_step(c, false, i)) return rc;
-    c->h_pin[0] = (int32_t)ids[n - 1];
-    HIP_TRY(c, hipMemcpyAsync(m.d_token, &c->h_pin[0], 4, hipMemcpyHostToDevice, c->stream));
+    if (int rc = put_token(c, ids[n - 1])) return rc;
     if (int rc = launch_step(c, true, n - 1)) return rc;
     if (int rc = finish_step(c, logits, argmax)) return rc;
     m.host_pos = n;
@@ -2055,8 +2084,7 @@ extern "C" int qora_hip_decode_sample(qora_hip_ctx* c, uint32_t token, const uin
     if (int rc = check_step_room(c, 1)) return rc;
     ModelState& m = c->m;
     if (token >= m.vocab) return fail(c, QORA_HIP_E_INVALID, "token id out of range");
-    c->h_pin[0] = (int32_t)token;
-    HIP_TRY(c, hipMemcpyAsync(m.d_token, &c->h_pin[0], 4, hipMemcpyHostToDevice, c->stream));
+    if (int rc = put_token(c, token)) return rc;
     if (int rc = launch_step(c, true, m.host_pos)) return rc;
     uint32_t greedy = 0;
     if (int rc = finish_step(c, logits, &greedy)) return rc;

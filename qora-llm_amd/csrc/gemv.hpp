@@ -602,6 +602,7 @@ __global__ __launch_bounds__(256) void argmax_finish_kernel(ArgmaxFinishParams p
         // no candidate above -inf: the sampler returns index 0
         const int32_t tok = (i0 == 0xFFFFFFFFu) ? 0 : (int32_t)i0;
         *p.token_out = tok;
+        if (p.host_token) *p.host_token = tok;
         if (p.pos) {
             const int32_t ps = *p.pos;
             p.gen[ps] = tok;

@@ -239,6 +239,7 @@ struct ArgmaxFinishParams {
     int32_t* token_out;
     int32_t* pos;              // if non-null: gen[pos] = token, pos += 1
     int32_t* gen;
+    int32_t* host_token;       // optional: the token also stored here (mapped host memory, read after a sync)
 };
 
 constexpr int kAttnSub = 32;         // positions staged in LDS at a time
