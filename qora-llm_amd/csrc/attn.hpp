@@ -730,26 +730,78 @@ __global__ __launch_bounds__(512) void attn_decode_direct_kernel(AttnParams p) {
     const bool has_new = model && cur >= p0 && cur < p1;
     const uint32_t npass = (p1 - p0 + PP - 1) / PP;
 
+    // ---- loads, in the order their data is needed: the q set-up's inputs
+    // (threads 0..255), then this wave's first pass of cache rows (they depend
+    // on the position only; the row being appended, if read here, is replaced
+    // from LDS below), then the q arithmetic waits for its own loads only ----
+    const uint32_t vc = lane % 16, vj = lane / 16;    // dim slice, position phase
+    const uint16_t* kc = reinterpret_cast<const uint16_t*>(p.kc);
+    const uint16_t* vcache = reinterpret_cast<const uint16_t*>(p.vc);
+    VW kr[NI], vr[NI];
+    auto load_rows = [&](VW (&dst)[NI], const uint16_t* src, uint32_t c0) {
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const uint64_t off = (uint64_t)min(c0 + 4u * i + vj, p1 - 1u) * cps + coff + vc * VD;
+            dst[i] = *reinterpret_cast<const VW*>(src + off);
+        }
+    };
+    constexpr uint32_t QPT = G4 * HD / 256;          // q values per set-up thread
+    const bool qset = t < 256 && model;
+    const uint32_t qd = p.H * hd;
+    const bool rot = p.use_rope != 0;
+    long long qa[QPT], qb[QPT], ka = 0, kb = 0, va = 0;
+    float qc[QPT], qsn[QPT], kc_ = 1.f, ks_ = 0.f, ssp = 0.f;
+    if (qset) {
+        ssp = p.ss_in[min((uint32_t)lane, p.ss_n - 1u)];
+        const float* ct = p.rope_cos + (uint64_t)cur * p.half;
+        const float* st = p.rope_sin + (uint64_t)cur * p.half;
+#pragma unroll
+        for (uint32_t u = 0; u < QPT; ++u) {
+            const uint32_t i = min(t + 256u * u, G * hd - 1u), d = i % hd;
+            const long long* src = p.qkv_acc + (uint64_t)kvh * G * hd + (i / hd) * hd;
+            qa[u] = src[d];
+            qb[u] = src[rope_partner(d, p.half)];
+            const uint32_t td = d < p.half ? d : (d < 2 * p.half ? d - p.half : 0u);
+            qc[u] = rot ? ct[td] : 1.f;
+            qsn[u] = rot ? st[td] : 0.f;
+        }
+        if (has_new && t < hd) {
+            ka = p.qkv_acc[qd + head_off + t];
+            kb = p.qkv_acc[qd + head_off + rope_partner(t, p.half)];
+            va = p.qkv_acc[qd + kv_stride + head_off + t];
+            const uint32_t td = t < p.half ? t : (t < 2 * p.half ? t - p.half : 0u);
+            kc_ = rot ? ct[td] : 1.f;
+            ks_ = rot ? st[td] : 0.f;
+        }
+    }
+    // The q set-up's loads stay ahead of the cache rows, so a wait for them
+    // does not also wait for the rows (loads complete in issue order). The
+    // row loads are unconditional (a pass past the split re-reads its last
+    // row; the address is clamped): loads under a branch would leave the
+    // compiler's wait counts conservative, waiting for every load in flight.
+    __builtin_amdgcn_sched_barrier(0);
+    load_rows(kr, kc, p0 + (uint32_t)wave * PP);
+    load_rows(vr, vcache, p0 + (uint32_t)wave * PP);
+    __builtin_amdgcn_sched_barrier(0);
+
     // ---- q of the G heads (rotated, RMSNorm factor applied) and the appended row: threads 0..255 ----
     if (t < 256) {
         if (model) {
-            const uint32_t qd = p.H * hd;
-            const float inv = 1.0f / sqrtf(wave_sum(lane < p.ss_n ? p.ss_in[lane] : 0.f) / (float)p.norm_n + 1e-6f);
-            const bool rot = p.use_rope != 0;
-            const float* ct = p.rope_cos + (uint64_t)cur * p.half;
-            const float* st = p.rope_sin + (uint64_t)cur * p.half;
-            auto rotated = [&](const long long* src, uint32_t d) -> float {
-                const float a = inv * from_fixed(src[d]);
+            const float inv = 1.0f / sqrtf(wave_sum(lane < p.ss_n ? ssp : 0.f) / (float)p.norm_n + 1e-6f);
+            auto rot_val = [&](long long a_, long long b_, uint32_t d, float c, float sn) -> float {
+                const float a = inv * from_fixed(a_);
                 if (!rot || d >= 2 * p.half) return a;
-                const float b = inv * from_fixed(src[rope_partner(d, p.half)]);
-                const uint32_t td = d < p.half ? d : d - p.half;
-                return d < p.half ? a * ct[td] - b * st[td] : a * ct[td] + b * st[td];
+                const float b = inv * from_fixed(b_);
+                return d < p.half ? a * c - b * sn : a * c + b * sn;
             };
-            for (uint32_t i = t; i < G * hd; i += 256)
-                qs[(i / hd) * HD + i % hd] = rotated(p.qkv_acc + (uint64_t)kvh * G * hd + (i / hd) * hd, i % hd);
+#pragma unroll
+            for (uint32_t u = 0; u < QPT; ++u) {
+                const uint32_t i = t + 256u * u;
+                if (i < G * hd) qs[(i / hd) * HD + i % hd] = rot_val(qa[u], qb[u], i % hd, qc[u], qsn[u]);
+            }
             if (has_new && t < hd) {
-                float kv = rotated(p.qkv_acc + qd + head_off, t);
-                float vv = inv * from_fixed(p.qkv_acc[qd + kv_stride + head_off + t]);
+                float kv = rot_val(ka, kb, t, kc_, ks_);
+                float vv = inv * from_fixed(va);
                 const uint16_t kh = f2h(kv), vh = f2h(vv);
                 const uint64_t idx = (uint64_t)cur * cps + coff + t;
                 reinterpret_cast<uint16_t*>(p.kc)[idx] = kh;
@@ -764,7 +816,6 @@ __global__ __launch_bounds__(512) void attn_decode_direct_kernel(AttnParams p) {
     }
     __syncthreads();
 
-    const uint32_t vc = lane % 16, vj = lane / 16;    // dim slice, position phase
     float qv[G4][VD];
 #pragma unroll
     for (int g = 0; g < G4; ++g)
@@ -778,18 +829,13 @@ __global__ __launch_bounds__(512) void attn_decode_direct_kernel(AttnParams p) {
 #pragma unroll
         for (int d = 0; d < VD; ++d) o[g][d] = 0.f;
     }
-    const uint16_t* kc = reinterpret_cast<const uint16_t*>(p.kc);
-    const uint16_t* vcache = reinterpret_cast<const uint16_t*>(p.vc);
+    // Each wave's passes: wave, wave + NWV, ... The next pass's K rows go into
+    // the K registers as soon as the scores are done, its V rows into the V
+    // registers after p.V, so one pass's loads overlap the other's arithmetic.
     for (uint32_t pi = wave; pi < npass; pi += NWV) {
         const uint32_t c0 = p0 + pi * PP;
         const uint32_t cn = min((uint32_t)PP, p1 - c0);
-        VW kr[NI], vr[NI];
-#pragma unroll
-        for (int i = 0; i < NI; ++i) {
-            const uint64_t off = (uint64_t)min(c0 + 4u * i + vj, p1 - 1u) * cps + coff + vc * VD;
-            kr[i] = *reinterpret_cast<const VW*>(kc + off);
-            vr[i] = *reinterpret_cast<const VW*>(vcache + off);
-        }
+        const uint32_t pn = pi + NWV;                  // this wave's next pass
         // ---- scores of the lane's positions: partial dots, summed over the row's 16 lanes ----
         float s[NI][G4];
 #pragma unroll
@@ -820,13 +866,11 @@ __global__ __launch_bounds__(512) void attn_decode_direct_kernel(AttnParams p) {
                 float a = 0.f;
 #pragma unroll
                 for (int d = 0; d < VD; ++d) a = fmaf(qv[g][d], k[d], a);
-                a += __shfl_xor(a, 1, kWave);
-                a += __shfl_xor(a, 2, kWave);
-                a += __shfl_xor(a, 4, kWave);
-                a += __shfl_xor(a, 8, kWave);
+                a = row16_sum(a);
                 s[i][g] = 4u * i + vj < cn ? a * p.scale : -INFINITY;
             }
         }
+        load_rows(kr, kc, p0 + pn * PP);
         // ---- online softmax per head over the pass ----
         float f[G4];
 #pragma unroll
@@ -883,6 +927,7 @@ __global__ __launch_bounds__(512) void attn_decode_direct_kernel(AttnParams p) {
 #pragma unroll
                 for (int d = 0; d < VD; ++d) o[g][d] = fmaf(s[i][g], v[d], o[g][d]);
         }
+        load_rows(vr, vcache, p0 + pn * PP);
     }
     // ---- this wave's totals: sum the four position phases (lanes c, c + 16, c + 32, c + 48) ----
 #pragma unroll

@@ -40,17 +40,6 @@ constexpr int kFusedWaves = 8;          // waves per workgroup, all in the atten
 constexpr uint32_t kFusedPass = 32;     // positions per pass: 8 waves x 4 row slots
 constexpr int kFusedPasses = 8;         // passes loaded together (256 positions)
 
-// Sum over each 16-lane row by a butterfly: lane ^ 1, lane ^ 2, then the
-// mirrored quad and the mirrored half row. Each step adds two equal-bit
-// operands in either order, so all 16 lanes end with identical bits.
-__device__ __forceinline__ float row16_sum(float v) {
-    v += dpp_f32<0xB1>(v);    // quad_perm [1,0,3,2]
-    v += dpp_f32<0x4E>(v);    // quad_perm [2,3,0,1]
-    v += dpp_f32<0x141>(v);   // row_half_mirror
-    v += dpp_f32<0x140>(v);   // row_mirror
-    return v;
-}
-
 template <bool F16KV>
 __device__ __forceinline__ float4 kv_word_f32(typename std::conditional<F16KV, uint2, float4>::type w) {
     if constexpr (F16KV) return kv_words_f32(w);

@@ -142,6 +142,17 @@ __device__ __forceinline__ float wave_sum(float v) {
     return (lane_f32(v, 0) + lane_f32(v, 16)) + (lane_f32(v, 32) + lane_f32(v, 48));
 }
 
+// Sum over each 16-lane row by a DPP butterfly (no LDS): lane ^ 1, lane ^ 2,
+// then the mirrored quad and the mirrored half row. Each step adds two
+// equal-bit operands in either order, so all 16 lanes end with identical bits.
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp_f32<0xB1>(v);    // quad_perm [1,0,3,2]
+    v += dpp_f32<0x4E>(v);    // quad_perm [2,3,0,1]
+    v += dpp_f32<0x141>(v);   // row_half_mirror
+    v += dpp_f32<0x140>(v);   // row_mirror
+    return v;
+}
+
 __device__ __forceinline__ float wave_max(float v) {
     v = fmaxf(v, dpp_f32<0xB1>(v));
     v = fmaxf(v, dpp_f32<0x4E>(v));
