@@ -10,6 +10,7 @@
 #include "sample.hpp"
 
 #include <algorithm>
+#include <cstring>
 #include <cstdlib>
 
 namespace qora {
@@ -507,8 +508,32 @@ hipError_t launch_advance_pos(int32_t* pos, hipStream_t stream) {
 
 // ---- batched prefill ----
 
+// Register-cached row producer for rows of at most 256 * EPT elements (EPT in
+// {8, 16, 48}), else false (the two- or three-pass kernels take the row).
+template <int EPT>
+static void launch_pf_rows_reg(int kind, const PrefillRowParams& p, uint32_t T, hipStream_t stream) {
+    switch (kind) {
+    case PF_ROW_RMSNORM: hipLaunchKernelGGL((pf_rmsnorm_split_reg_kernel<EPT>), dim3(T), dim3(256), 0, stream, p); break;
+    case PF_ROW_SPLIT: hipLaunchKernelGGL((pf_split_reg_kernel<EPT>), dim3(T), dim3(256), 0, stream, p); break;
+    default: hipLaunchKernelGGL((pf_silu_split_reg_kernel<EPT>), dim3(T), dim3(256), 0, stream, p); break;
+    }
+}
+
+static bool pf_rows_reg(int kind, const PrefillRowParams& p, uint32_t T, hipStream_t stream) {
+    if (kind != PF_ROW_RMSNORM && kind != PF_ROW_SPLIT && kind != PF_ROW_SILU) return false;
+    if (p.n <= 256u * 8u) launch_pf_rows_reg<8>(kind, p, T, stream);
+    else if (p.n <= 256u * 16u) launch_pf_rows_reg<16>(kind, p, T, stream);
+    else if (p.n <= 256u * 48u) launch_pf_rows_reg<48>(kind, p, T, stream);
+    else return false;
+    return true;
+}
+
 hipError_t launch_pf_rows(int kind, const PrefillRowParams& p, uint32_t T, hipStream_t stream) {
     if (T == 0) return hipSuccess;
+    // QORA_HIP_PF_ROWS=loop keeps every row on the multi-pass kernels
+    const char* er = std::getenv("QORA_HIP_PF_ROWS");
+    const bool loop = er && std::strcmp(er, "loop") == 0;
+    if (!loop && pf_rows_reg(kind, p, T, stream)) return hipGetLastError();
     switch (kind) {
     case PF_ROW_EMBED: hipLaunchKernelGGL(pf_embed_kernel, dim3(T), dim3(256), 0, stream, p); break;
     case PF_ROW_RMSNORM: hipLaunchKernelGGL(pf_rmsnorm_split_kernel, dim3(T), dim3(256), 0, stream, p); break;

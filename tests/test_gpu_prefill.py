@@ -209,3 +209,23 @@ def test_gemm_loop_modes_bit_identical(ctx, pkg, monkeypatch, k, n, T):
         monkeypatch.setenv("QORA_HIP_PF_MODE", "0")
         y0 = _gemm(ctx, d, wid, x, T, n)
     assert np.array_equal(y0, y1)
+
+
+@pytest.mark.parametrize("hidden,inter,heads", [(2048, 11008, 16), (512, 3008, 4)])
+def test_row_producers_register_and_loop_bit_identical(ctx, pkg, monkeypatch, hidden, inter, heads):
+    """The register-cached row producers (rows up to 2048, 4096 and 12288 wide)
+    and the multi-pass ones (QORA_HIP_PF_ROWS=loop) compute the same values."""
+    print(f"case row producers hidden={hidden} inter={inter}", flush=True)
+    cfg = pkg.ModelConfig(num_layers=2, vocab=1000, hidden=hidden, intermediate=inter, num_heads=heads,
+                          num_kv_heads=4, head_dim=128, rope_half_dim=64, rope_theta=5e6, rope_positions=128)
+    w = pkg.synthetic_model(cfg, seed=9, fmt=1, rope_positions=128)
+    prompt = pkg.synth_tokens(9, 2500, 70, cfg.vocab)
+    be = pkg.HipBackend(ctx, w, kv_capacity=128)
+    reg, treg = be.raw_prefill(prompt)
+    kreg, vreg = be.kv_layer(1)
+    be.kv_reset()
+    monkeypatch.setenv("QORA_HIP_PF_ROWS", "loop")
+    loop, tloop = be.raw_prefill(prompt)
+    kl, vl = be.kv_layer(1)
+    assert np.array_equal(reg, loop) and treg == tloop
+    assert np.array_equal(kreg, kl) and np.array_equal(vreg, vl)
