@@ -508,14 +508,15 @@ hipError_t launch_advance_pos(int32_t* pos, hipStream_t stream) {
 
 // ---- batched prefill ----
 
-// Register-cached row producer for rows of at most 256 * EPT elements (EPT in
-// {8, 16, 48}), else false (the two- or three-pass kernels take the row).
+// Register-cached row producers: rows of up to 4096 elements on 256 threads
+// (8 or 16 per thread), SwiGLU rows of up to 12288 on 1024 threads (12 per
+// thread); wider rows go to the two- or three-pass kernels.
 template <int EPT>
 static void launch_pf_rows_reg(int kind, const PrefillRowParams& p, uint32_t T, hipStream_t stream) {
     switch (kind) {
     case PF_ROW_RMSNORM: hipLaunchKernelGGL((pf_rmsnorm_split_reg_kernel<EPT>), dim3(T), dim3(256), 0, stream, p); break;
     case PF_ROW_SPLIT: hipLaunchKernelGGL((pf_split_reg_kernel<EPT>), dim3(T), dim3(256), 0, stream, p); break;
-    default: hipLaunchKernelGGL((pf_silu_split_reg_kernel<EPT>), dim3(T), dim3(256), 0, stream, p); break;
+    default: hipLaunchKernelGGL((pf_silu_split_reg_kernel<256, EPT>), dim3(T), dim3(256), 0, stream, p); break;
     }
 }
 
@@ -523,7 +524,8 @@ static bool pf_rows_reg(int kind, const PrefillRowParams& p, uint32_t T, hipStre
     if (kind != PF_ROW_RMSNORM && kind != PF_ROW_SPLIT && kind != PF_ROW_SILU) return false;
     if (p.n <= 256u * 8u) launch_pf_rows_reg<8>(kind, p, T, stream);
     else if (p.n <= 256u * 16u) launch_pf_rows_reg<16>(kind, p, T, stream);
-    else if (p.n <= 256u * 48u) launch_pf_rows_reg<48>(kind, p, T, stream);
+    else if (kind == PF_ROW_SILU && p.n <= 1024u * 12u)
+        hipLaunchKernelGGL((pf_silu_split_reg_kernel<1024, 12>), dim3(T), dim3(1024), 0, stream, p);
     else return false;
     return true;
 }

@@ -142,7 +142,7 @@ __global__ __launch_bounds__(256) void pf_silu_split_kernel(PrefillRowParams p) 
 }
 
 // The same three producers with the row held in registers (thread t keeps
-// elements t + 256 i, i < EPT): each element is read once instead of two or
+// elements t + NT i, i < EPT, NT = 256 unless stated): each element is read once instead of two or
 // three times, with the same arithmetic. For rows of at most 256 * EPT.
 template <int EPT>
 __global__ __launch_bounds__(256) void pf_rmsnorm_split_reg_kernel(PrefillRowParams p) {
@@ -202,9 +202,11 @@ __global__ __launch_bounds__(256) void pf_split_reg_kernel(PrefillRowParams p) {
     if (threadIdx.x == 0) p.xe[t] = e;
 }
 
-template <int EPT>
-__global__ __launch_bounds__(256) void pf_silu_split_reg_kernel(PrefillRowParams p) {
-    __shared__ float red[4];
+// NT threads per row: the row's maximum does not depend on the thread count,
+// so any NT gives the same values (1024 for 11008-wide rows: 16 waves a row).
+template <int NT, int EPT>
+__global__ __launch_bounds__(NT) void pf_silu_split_reg_kernel(PrefillRowParams p) {
+    __shared__ float red[NT / kWave];
     const uint32_t t = blockIdx.x;
     const float* g = p.x + (uint64_t)t * p.ld;
     const float* u = p.u + (uint64_t)t * p.ld;
@@ -212,7 +214,7 @@ __global__ __launch_bounds__(256) void pf_silu_split_reg_kernel(PrefillRowParams
     float amax = 0.f;
 #pragma unroll
     for (int i = 0; i < EPT; ++i) {
-        const uint32_t j = threadIdx.x + 256u * (uint32_t)i;
+        const uint32_t j = threadIdx.x + (uint32_t)NT * (uint32_t)i;
         float h = 0.f;
         if (j < p.n) {
             const float gv = g[j];
@@ -221,12 +223,12 @@ __global__ __launch_bounds__(256) void pf_silu_split_reg_kernel(PrefillRowParams
         v[i] = h;
         amax = fmaxf(amax, fabsf(h));
     }
-    const int e = pf_row_exponent(pf_block_max<256>(amax, red));
+    const int e = pf_row_exponent(pf_block_max<NT>(amax, red));
     _Float16* xh = reinterpret_cast<_Float16*>(p.xh) + (uint64_t)t * p.n;
     _Float16* xl = reinterpret_cast<_Float16*>(p.xl) + (uint64_t)t * p.n;
 #pragma unroll
     for (int i = 0; i < EPT; ++i) {
-        const uint32_t j = threadIdx.x + 256u * (uint32_t)i;
+        const uint32_t j = threadIdx.x + (uint32_t)NT * (uint32_t)i;
         if (j < p.n) pf_split(v[i], e, xh + j, xl + j);
     }
     if (threadIdx.x == 0) p.xe[t] = e;
