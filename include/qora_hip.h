@@ -145,6 +145,17 @@ int qora_hip_decode_sample(qora_hip_ctx* ctx, uint32_t token, const uint32_t* hi
  * model_init; Q4 weights). */
 int qora_hip_decode_mode(const qora_hip_ctx* ctx);
 
+/* 1 when the decode step runs the gate|up and down projections of each layer
+ * as one launch (the down workgroups wait on arrival counts of the gate|up
+ * workgroups while their weights stream in; opt-in with QORA_HIP_MLP=1 at
+ * model_init, slower than two launches on MI355X), 0 when they are two
+ * launches (the default; also F16 weights or a plan the fused kernel does not
+ * take).
+ * Either way the same accumulations (exact integer sums) give the same
+ * results. The reference's decode step runs the fused gate+up GEMV and then
+ * the down GEMV (gemv.rs:1002-1006 inside forward_decode_raw). */
+uint32_t qora_hip_mlp_fused(const qora_hip_ctx* ctx);
+
 /* Context bound of the fused short-context step (no counterpart in the
  * reference): graph-driven steps that append a position below it run each
  * layer's attention inside the o-projection kernel; longer contexts take the

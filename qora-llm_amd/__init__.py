@@ -103,6 +103,7 @@ SIGNATURES = {
     "qora_hip_gemv_release": (_I, [_P, _U32]),
     "qora_hip_decode_mode": (_I, [_P]),
     "qora_hip_attn_o_limit": (_U32, [_P]),
+    "qora_hip_mlp_fused": (_U32, [_P]),
     "qora_hip_lm_head_prepare": (_I, [_P, _U32, _P]),
     "qora_hip_lm_head_run": (_I, [_P, _U32, _P, _P, _P, _P]),
     "qora_hip_gemv_q4_rowdot": (_I, [_P, _P, _P, _P, _P, _U64, _U64, _P]),
@@ -561,6 +562,10 @@ class HipBackend:
     def attn_o_limit(self) -> int:
         """Steps appending a position below this run attention inside the o GEMV."""
         return int(self.ctx.lib.qora_hip_attn_o_limit(self.ctx.h))
+
+    def mlp_fused(self) -> bool:
+        """Whether each layer's gate|up and down projections run as one launch."""
+        return bool(self.ctx.lib.qora_hip_mlp_fused(self.ctx.h))
 
     def kv_layer(self, layer: int):
         """(k, v) of one layer as f32 [len][kv_heads*head_dim] (RawKvCache entry)."""

@@ -71,6 +71,10 @@ struct ModelState {
     // steps that append a position below attn_o_max
     std::vector<AttnOParams> p_ao;
     uint32_t attn_o_max = 0;
+    // gate|up and down in one launch (gemv_q4m_mlp_kernel); done counter in
+    // the slot after the gate|up sums, wait-failure flag in the mapped h_tok[1]
+    std::vector<GemvMlpParams> p_mlp;
+    bool mlp = false;
     RowdotParams p_lm{};
     LmHeadParams p_lmq{};
     ArgmaxFinishParams p_fin{};
@@ -295,8 +299,12 @@ int record_step(qora_hip_ctx* c, bool with_lm_head, bool fused) {
             HIP_TRY(c, launch_attn(m.p_attn[l], s));
             HIP_TRY(c, launch_gemv(m.fmt, m.pl_o, m.p_o[l], s));
         }
-        HIP_TRY(c, launch_gemv(m.fmt, m.pl_gu, m.p_gu[l], s));
-        HIP_TRY(c, launch_gemv(m.fmt, m.pl_down, m.p_down[l], s));
+        if (m.mlp) {
+            HIP_TRY(c, launch_gemv_mlp(m.pl_gu, m.pl_down, m.p_mlp[l], s));
+        } else {
+            HIP_TRY(c, launch_gemv(m.fmt, m.pl_gu, m.p_gu[l], s));
+            HIP_TRY(c, launch_gemv(m.fmt, m.pl_down, m.p_down[l], s));
+        }
     }
     if (with_lm_head) {
         if (m.lm_mfma) HIP_TRY(c, launch_lmhead(m.lm_blocks, m.p_lmq, s));
@@ -329,6 +337,20 @@ uint32_t attn_o_limit(const ModelState& m) {
     const char* v = std::getenv("QORA_HIP_ATTN_O");
     const long n = (v && *v) ? std::atol(v) : (long)kAttnODefaultMax;
     return n <= 0 ? 0u : (uint32_t)std::min<long>(n, (long)m.cap);
+}
+
+// int64 words after the gate|up sums: the fused MLP's count and its 32 group
+// counters, 128 bytes apart
+constexpr uint32_t kMlpCounterWords = 16 * 33;
+
+// The fused MLP launch, opt-in (QORA_HIP_MLP=1): it measures slower than the
+// two launches (938 against 1013 tok/s), the chain of arrival atomics and
+// polls costing more than the kernel boundary it removes. It needs the
+// mapped host word that reports a failed wait.
+bool mlp_enabled(const ModelState& m, const qora_hip_ctx* c) {
+    if (m.fmt != FMT_Q4 || !gemv_mlp_supported(m.pl_gu, m.pl_down) || !c->d_h_tok) return false;
+    const char* v = std::getenv("QORA_HIP_MLP");
+    return v && std::strcmp(v, "1") == 0;
 }
 
 bool eager_mode() {
@@ -423,6 +445,7 @@ extern "C" int qora_hip_create(int device, qora_hip_ctx** out) {
         return QORA_HIP_E_DEVICE;
     }
     if (hipHostMalloc((void**)&c->h_tok, 64, hipHostMallocMapped | hipHostMallocCoherent) == hipSuccess) {
+        std::memset(c->h_tok, 0, 64);   // [0] argmax token, [1] fused-MLP wait failure
         if (hipHostGetDevicePointer((void**)&c->d_h_tok, c->h_tok, 0) != hipSuccess) c->d_h_tok = nullptr;
     } else {
         c->h_tok = nullptr;
@@ -812,7 +835,7 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
     MALLOC(d_v, (size_t)m.L * m.cap * kvd * kvb);
     MALLOC(d_xacc, (size_t)m.hidden * 8);
     MALLOC(d_qkv_acc, qkv_n * 8);
-    MALLOC(d_gu_acc, (size_t)2 * m.inter * 8);
+    MALLOC(d_gu_acc, ((size_t)2 * m.inter + kMlpCounterWords) * 8);   // + the fused MLP's counters
     MALLOC(d_attn_part, (size_t)m.KVH * m.attn_s_max * m.groups * (m.hd + 2) * 4);
     MALLOC(d_ss, (size_t)m.L * 2 * kAttnMaxSplits * 4);
     MALLOC(d_logits, (size_t)m.vocab * 4);
@@ -835,7 +858,7 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
     }
     HIP_TRY(c, hipMemset(m.d_xacc, 0, (size_t)m.hidden * 8));
     HIP_TRY(c, hipMemset(m.d_qkv_acc, 0, qkv_n * 8));
-    HIP_TRY(c, hipMemset(m.d_gu_acc, 0, (size_t)2 * m.inter * 8));
+    HIP_TRY(c, hipMemset(m.d_gu_acc, 0, ((size_t)2 * m.inter + kMlpCounterWords) * 8));
     HIP_TRY(c, hipMemset(m.d_pos, 0, 64));
     HIP_TRY(c, hipMemset(m.d_token, 0, 64));
     HIP_TRY(c, hipMemset(m.d_gen, 0, (size_t)m.cap * 4 + 64));
@@ -868,6 +891,8 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
     m.p_attn.resize(m.L);
     m.attn_o_max = attn_o_limit(m);
     if (m.attn_o_max) m.p_ao.resize(m.L);
+    m.mlp = mlp_enabled(m, c);
+    if (m.mlp) m.p_mlp.resize(m.L);
     for (uint32_t l = 0; l < m.L; ++l) {
         const DevWeight* W[7];
         for (int j = 0; j < 7; ++j) W[j] = get_weight(c, m.wids[l * 7 + j]);
@@ -886,7 +911,7 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
         q.ss_out = m.d_ss + ((size_t)l * 2 + 0) * kAttnMaxSplits;
         q.acc = m.d_qkv_acc;
         q.zero_ptr = m.d_gu_acc;
-        q.zero_n = 2 * m.inter;
+        q.zero_n = 2 * m.inter + kMlpCounterWords;   // the gate|up sums and the fused MLP's counters
         apply_plan(m.pl_qkv, &q);
         if (int rc = pack_model_gemv(c, (int)m.fmt, m.pl_qkv, &q)) { free_model(c); return rc; }
 
@@ -963,6 +988,9 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
         dn.acc = m.d_xacc;
         apply_plan(m.pl_down, &dn);
         if (int rc = pack_model_gemv(c, (int)m.fmt, m.pl_down, &dn)) { free_model(c); return rc; }
+        if (m.mlp)
+            m.p_mlp[l] = GemvMlpParams{g, dn, m.pl_gu.grid(), reinterpret_cast<uint32_t*>(m.d_gu_acc + 2 * m.inter),
+                                       c->d_h_tok + 1};
     }
     m.p_lm = RowdotParams{};
     m.p_lm.w = (const uint8_t*)emb->w;
@@ -1046,6 +1074,11 @@ int check_step_room(qora_hip_ctx* c, uint64_t steps) {
 // into h_pin[24]); on an error the reports of the timed-out waits follow.
 int check_mk_error(qora_hip_ctx* c) {
     ModelState& m = c->m;
+    if (m.mlp && reinterpret_cast<volatile int32_t*>(c->h_tok)[1] != 0) {
+        reinterpret_cast<volatile int32_t*>(c->h_tok)[1] = 0;
+        return fail(c, QORA_HIP_E_DEVICE,
+                    "decode step: the down projection's wait for the gate|up workgroups timed out; reset the KV cache");
+    }
     if (!m.mk || c->h_pin[24] == 0) return QORA_HIP_OK;
     uint32_t e[64] = {};
     HIP_TRY(c, hipMemcpy(e, m.d_mk_err, sizeof e, hipMemcpyDeviceToHost));
@@ -1415,6 +1448,11 @@ extern "C" int qora_hip_prefill(qora_hip_ctx* c, const uint32_t* ids, size_t n, 
 extern "C" int qora_hip_decode_mode(const qora_hip_ctx* c) {
     if (!c || !c->m.ready) return 0;
     return c->m.mk ? 2 : 1;
+}
+
+extern "C" uint32_t qora_hip_mlp_fused(const qora_hip_ctx* c) {
+    if (!c || !c->m.ready) return 0;
+    return c->m.mlp ? 1u : 0u;
 }
 
 extern "C" uint32_t qora_hip_attn_o_limit(const qora_hip_ctx* c) {

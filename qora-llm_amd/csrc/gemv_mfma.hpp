@@ -346,9 +346,44 @@ __device__ __forceinline__ void gemv_q4m_item(const GemvParams& p, uint32_t tile
 // K slice) of the grid a one-item launch would have, with every item's
 // scales and weights requested up front: fewer, longer-lived workgroups,
 // all loads in flight from the start.
-template <int GW, int KW, int PRO, int IPW = 1>
-__global__ __launch_bounds__(PRO == PRO_ATTN ? 512 : 320) void gemv_q4m_kernel(GemvParams p) {
-    kernarg_warm(p);
+// LDS of one gemv_q4m workgroup.
+template <int GW, int KW, int PRO, int IPW>
+struct GemvQ4mSmem {
+    static constexpr int NPW = PRO == PRO_ATTN ? 4 : 1;
+    static constexpr int MAXH = KW / 32 + 1;
+    __align__(16) float xs[IPW][KW];
+    float wred[IPW][2][NPW];
+    __align__(16) uint8_t zl[4][GW][4][KW];   // limb bytes: [wave][group][limb][row]
+    __align__(16) uint8_t zero16[16];         // A rows 4..15
+    float aw[PRO == PRO_ATTN ? NPW * kAttnMaxSplits * MAXH : 1];
+};
+
+// Waits of a prologue wave (fused MLP step) before it reads its input rows:
+// until *ctr >= target, at most kGemvWaitSpins polls; past that it stores 1
+// to *err and goes on (the host reports the failure). The polls and the input
+// reads that follow are agent-scope atomic loads, which read past this XCD's
+// L2 without invalidating it (an acquire would invalidate the L2 on every
+// poll and stall the other XCD traffic); the producers' sums are atomics
+// and their norm sums atomic stores, all complete before the count rises.
+constexpr uint32_t kGemvWaitSpins = 1u << 20;
+
+__device__ __forceinline__ long long ld_agent(const long long* p) {
+    return __hip_atomic_load(const_cast<long long*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_agent(const float* p) {
+    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+struct GemvWait {
+    uint32_t* ctr;
+    uint32_t target;
+    int32_t* err;
+};
+
+// The body of gemv_q4m_kernel for workgroup `block` of `nblocks`.
+template <int GW, int KW, int PRO, int IPW>
+__device__ __forceinline__ void gemv_q4m_body(const GemvParams& p, uint32_t block, uint32_t nblocks,
+                                              GemvQ4mSmem<GW, KW, PRO, IPW>& sm, const GemvWait* wait) {
     constexpr int NW = 4;                    // matrix-core waves
     constexpr int NPW = PRO == PRO_ATTN ? 4 : 1;   // prologue waves (the attention merge gets four)
     constexpr int NT = (NW + NPW) * kWave;
@@ -359,28 +394,39 @@ __global__ __launch_bounds__(PRO == PRO_ATTN ? 512 : 320) void gemv_q4m_kernel(G
     constexpr bool kAttn = PRO == PRO_ATTN;
     static_assert(KW % 64 == 0 && KW <= 512, "slice of 64..512 rows");
     static_assert(IPW == 1 || !kAttn, "the attention-merge prologue takes one item per workgroup");
-    __shared__ __align__(16) float xs[IPW][KW];
-    __shared__ float wred[IPW][2][NPW];
-    __shared__ __align__(16) uint8_t zl[NW][GW][4][KW];   // limb bytes: [wave][group][limb][row]
-    __shared__ __align__(16) uint8_t zero16[16];          // A rows 4..15
-    __shared__ float aw[kAttn ? NPW * kAttnMaxSplits * MAXH : 1];
+    auto& xs = sm.xs;
+    auto& wred = sm.wred;
+    auto& zl = sm.zl;
+    auto& zero16 = sm.zero16;
+    float* aw = sm.aw;
 
     const int t = threadIdx.x;
     const int lane = t & (kWave - 1);
     // wave-uniform (scalar) so segment lookups and addresses stay on the SALU
     const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
     const uint32_t items = p.tiles * p.splits;
-    const uint32_t item0 = blockIdx.x * IPW;
+    const uint32_t item0 = block * IPW;
     const uint32_t nit = min((uint32_t)IPW, items - item0);
 
     if (p.zero_ptr)
-        for (uint32_t i = blockIdx.x * NT + t; i < p.zero_n; i += gridDim.x * NT) p.zero_ptr[i] = 0;
+        for (uint32_t i = block * NT + t; i < p.zero_n; i += nblocks * NT) p.zero_ptr[i] = 0;
 
     uint4 wq[IPW][GW][NKB];
     uint32_t sw[IPW][(NZ + 1) / 2];
     int esg[IPW][GW];
     if (wave >= NW) {
         // ---- prologue wave(s): rows [k0, k1) of the input into xs, max |x|, sum x^2 ----
+        if (wait) {
+            for (uint32_t spins = 0;; ++spins) {
+                if (__hip_atomic_load(wait->ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= wait->target) break;
+                if (spins >= kGemvWaitSpins) {
+                    if (lane == 0) *wait->err = 1;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(8);
+            }
+            asm volatile("" ::: "memory");   // the input reads stay below the wait
+        }
         // Raised issue priority: their few input loads enter the CU's memory
         // queue ahead of the weight streams of the other waves on the CU.
         __builtin_amdgcn_s_setprio(3);
@@ -415,11 +461,14 @@ __global__ __launch_bounds__(PRO == PRO_ATTN ? 512 : 320) void gemv_q4m_kernel(G
                         gm[r] = p.gamma[rc];
                     }
                     if constexpr (PRO == PRO_SILU_FIXED) {
-                        xa[r] = p.xacc[rc];
-                        xb[r] = p.xacc[p.k + rc];
+                        xa[r] = wait ? ld_agent(p.xacc + rc) : p.xacc[rc];
+                        xb[r] = wait ? ld_agent(p.xacc + p.k + rc) : p.xacc[p.k + rc];
                     }
                 }
-                if constexpr (PRO == PRO_SILU_FIXED) ssp = p.ss_in[min((uint32_t)lane, p.ss_n - 1u)];
+                if constexpr (PRO == PRO_SILU_FIXED) {
+                    const float* sp = p.ss_in + min((uint32_t)lane, p.ss_n - 1u);
+                    ssp = wait ? ld_agent(sp) : *sp;
+                }
                 float inv = 1.f;
                 if constexpr (PRO == PRO_SILU_FIXED)
                     inv = 1.0f / sqrtf(wave_sum(lane < (int)p.ss_n ? ssp : 0.f) / (float)p.norm_n + 1e-6f);
@@ -469,11 +518,63 @@ __global__ __launch_bounds__(PRO == PRO_ATTN ? 512 : 320) void gemv_q4m_kernel(G
 #pragma unroll
         for (int w = 1; w < NPW; ++w) xm = fmaxf(xm, wred[j][0][w]);
         if constexpr (PRO == PRO_GAMMA_FIXED) {
-            if (t == 0 && tile == 0) p.ss_out[split] = wred[j][1][0];
+            // an atomic store: a fused down launch reads it past this XCD's L2
+            if (t == 0 && tile == 0)
+                __hip_atomic_store(p.ss_out + split, wred[j][1][0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
         const float* xj = xs[j];
         gemv_q4m_item<GW, KW>(p, tile, wave, lane, [xj](int, uint32_t r) { return xj[r]; }, xm, sw[j], esg[j], wq[j],
                               zl[wave], zero16);
+    }
+}
+
+template <int GW, int KW, int PRO, int IPW = 1>
+__global__ __launch_bounds__(PRO == PRO_ATTN ? 512 : 320) void gemv_q4m_kernel(GemvParams p) {
+    kernarg_warm(p);
+    __shared__ GemvQ4mSmem<GW, KW, PRO, IPW> sm;
+    gemv_q4m_body<GW, KW, PRO, IPW>(p, blockIdx.x, gridDim.x, sm, nullptr);
+}
+
+// Fused MLP step: the gate|up GEMV (workgroups [0, gu_grid)) and the down GEMV
+// (the rest) in one launch. A gate|up workgroup whose accumulator atomics are
+// all acknowledged adds 1 to its group's counter (32 counters 128 bytes apart:
+// on one address ~1400 arrivals serialise, 4.7 ms a step); the last of a group
+// adds 1 to done[0]. The down workgroups' prologue waves poll done[0] (polling
+// all 32 counters costs more) before reading the gate|up sums, while their
+// matrix-core waves already stream the down weights. Opt-in: slower than the
+// two launches on MI355X (1.066 against 0.987 ms a decode step).
+// Workgroups are dispatched in index order, so every gate|up workgroup has
+// been placed on a CU before any down workgroup waits: the waits always end.
+constexpr uint32_t kMlpGroups = 32;        // arrival groups of gate|up workgroups
+constexpr uint32_t kMlpGroupStride = 32;   // words between counters (128 bytes)
+
+template <int GW, int KW>
+__global__ __launch_bounds__(320) void gemv_q4m_mlp_kernel(GemvMlpParams mp) {
+    __shared__ GemvQ4mSmem<GW, KW, PRO_GAMMA_FIXED, 1> sm;
+    static_assert(sizeof(GemvQ4mSmem<GW, KW, PRO_GAMMA_FIXED, 1>) == sizeof(GemvQ4mSmem<GW, KW, PRO_SILU_FIXED, 1>),
+                  "both bodies use the same LDS layout");
+    if (blockIdx.x < mp.gu_grid) {
+        kernarg_warm(mp.gu);
+        gemv_q4m_body<GW, KW, PRO_GAMMA_FIXED, 1>(mp.gu, blockIdx.x, mp.gu_grid, sm, nullptr);
+        if (threadIdx.x >= 4 * kWave) return;
+        // every wave's accumulator atomics (and norm-sum store) acknowledged first
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            // group counters (one 128-byte line each) spread the arrivals; the
+            // last of a group raises the count the down workgroups wait on
+            const uint32_t g = blockIdx.x % kMlpGroups;
+            const uint32_t size = mp.gu_grid / kMlpGroups + (g < mp.gu_grid % kMlpGroups ? 1u : 0u);
+            const uint32_t old =
+                __hip_atomic_fetch_add(mp.done + kMlpGroupStride * (1 + g), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (old + 1u == size) __hip_atomic_fetch_add(mp.done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    } else {
+        kernarg_warm(mp.dn);
+        const GemvWait w{mp.done, min(mp.gu_grid, kMlpGroups), mp.err};
+        gemv_q4m_body<GW, KW, PRO_SILU_FIXED, 1>(
+            mp.dn, blockIdx.x - mp.gu_grid, gridDim.x - mp.gu_grid,
+            reinterpret_cast<GemvQ4mSmem<GW, KW, PRO_SILU_FIXED, 1>&>(sm), &w);
     }
 }
 

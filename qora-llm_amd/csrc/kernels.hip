@@ -223,6 +223,19 @@ static hipError_t launch_q4m_gw(const GemvPlan& plan, const GemvParams& p, hipSt
     }
 }
 
+bool gemv_mlp_supported(const GemvPlan& gu, const GemvPlan& dn) {
+    return gu.mfma && dn.mfma && gu.gw == 1 && dn.gw == 1 && gu.ipw == 1 && dn.ipw == 1 && gu.kr == 256 &&
+           dn.kr == 256 && gu.blocks() > 0 && dn.blocks() > 0;
+}
+
+hipError_t launch_gemv_mlp(const GemvPlan& gu, const GemvPlan& dn, const GemvMlpParams& p, hipStream_t stream) {
+    if (!gemv_mlp_supported(gu, dn) || p.gu_grid != gu.grid() || !p.done || !p.err ||
+        p.gu.pro != PRO_GAMMA_FIXED || p.dn.pro != PRO_SILU_FIXED || !p.gu.tw || !p.dn.tw)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL((gemv_q4m_mlp_kernel<1, 256>), dim3(gu.grid() + dn.grid()), dim3(320), 0, stream, p);
+    return hipGetLastError();
+}
+
 hipError_t launch_gemv(int fmt, const GemvPlan& plan, const GemvParams& p, hipStream_t stream) {
     if (plan.blocks() == 0) return hipErrorInvalidValue;
     if (plan.mfma) {

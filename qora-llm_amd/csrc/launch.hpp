@@ -46,6 +46,10 @@ void apply_plan(const GemvPlan& plan, GemvParams* p);
 // p.tw == nullptr: reference layout, plain prologue only (kernel-level
 // entry points). Otherwise the tile layout written by launch_gemv_tile.
 hipError_t launch_gemv(int fmt, const GemvPlan& plan, const GemvParams& p, hipStream_t stream);
+// Fused gate|up + down launch: both plans on the matrix cores with one group
+// per wave, 256-row K slices and one item per workgroup.
+bool gemv_mlp_supported(const GemvPlan& gu, const GemvPlan& dn);
+hipError_t launch_gemv_mlp(const GemvPlan& gu, const GemvPlan& dn, const GemvMlpParams& p, hipStream_t stream);
 // Size of the tile layout of a planned GEMV (scales, exponent bounds: Q4 only).
 void gemv_tile_bytes(int fmt, const GemvPlan& plan, uint64_t* w_bytes, uint64_t* s_bytes, uint64_t* e_bytes);
 // Writes the tile layout of the reference-layout segments of p (after

@@ -273,6 +273,18 @@ struct AttnParams {
     uint64_t kv_ps, kv_hs;
 };
 
+// Fused gate|up + down launch (gemv_q4m_mlp_kernel). done[0]: the count the
+// down workgroups wait on; done[32 (1 + g)], g < 32: the group counters, 128
+// bytes apart. All zeroed before the launch (the q|k|v GEMV clears them with
+// the gate|up sums). err: set to 1 if a wait gave up.
+struct GemvMlpParams {
+    GemvParams gu;
+    GemvParams dn;
+    uint32_t gu_grid;
+    uint32_t* done;
+    int32_t* err;
+};
+
 // o projection with the attention of its query head computed in the
 // prologue (gemv_q4m_attn_kernel): the GEMV part (K slice = one head) and
 // the model-mode attention inputs (q|k|v sums, RoPE tables, cache).
