@@ -101,6 +101,7 @@ struct ModelState {
     int32_t* d_pf_xe = nullptr;          // [tc]
     uint32_t* d_pf_ids = nullptr;        // [cap]
     float* d_pf_part = nullptr;          // split-K partials of the GEMMs
+    float* d_pf_apart = nullptr;         // key-chunk partials of the prefill attention
     std::vector<int8_t*> pf_wf;          // [L][7] Q4 group exponents
     LmHeadParams p_lmq_pf{};
     RowdotParams p_lm_pf{};
@@ -1224,6 +1225,8 @@ bool pf_batched(const ModelState& m) {
     return pf_gemm_supported(m.hidden, 2) && pf_gemm_supported(m.H * m.hd, 2) && pf_gemm_supported(m.inter, 2);
 }
 
+constexpr uint32_t kPfAttnChunks = 8;   // key chunks per query block of the prefill attention
+
 int pf_setup(qora_hip_ctx* c) {
     ModelState& m = c->m;
     if (m.pf_ready) return QORA_HIP_OK;
@@ -1247,6 +1250,9 @@ int pf_setup(qora_hip_ctx* c) {
     PF_ALLOC(d_pf_xl, (size_t)tc * kmax * 2);
     PF_ALLOC(d_pf_xe, (size_t)tc * 4);
     PF_ALLOC(d_pf_ids, (size_t)m.cap * 4);
+    // attention key chunks: up to kPfAttnChunks per query block of >= 16 rows,
+    // 64 rows (4 waves x 16) of hd values plus (m, l) per block
+    PF_ALLOC(d_pf_apart, (size_t)((tc + 15) / 16) * kPfAttnChunks * m.KVH * 64 * (m.hd + 2) * 4);
     {
         // the largest split-K partial set over every chunk length (the 7 shapes
         // repeat in every layer)
@@ -1380,6 +1386,8 @@ int prefill_batched(qora_hip_ctx* c, size_t n, float* logits, uint32_t* argmax) 
             a.out = m.d_pf_ao;
             a.kv_ps = m.hd;
             a.kv_hs = (uint64_t)m.cap * m.hd;
+            a.part = m.d_pf_apart;
+            a.part_nc = kPfAttnChunks;
             HIP_TRY(c, launch_pf_rope_cache(a, s));
             HIP_TRY(c, launch_pf_attn(a, s));
             PrefillRowParams sr{};

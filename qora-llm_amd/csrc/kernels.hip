@@ -641,11 +641,34 @@ hipError_t launch_pf_attn(const PrefillAttnParams& p, hipStream_t stream) {
     const uint32_t G = p.H / p.KVH;
     if ((p.hd == 64 || p.hd == 128) && (G == 1 || G == 2 || G == 4)) {
         const uint32_t qt = 16u * (4u / G);
-        const dim3 grid((p.T + qt - 1) / qt, p.KVH);
+        // Key chunks: a query block's keys split over up to part_nc blocks
+        // (128 keys each, more when that would exceed part_nc) so that the
+        // long rows of the causal triangle do not set the kernel's length;
+        // pf_attn_merge_kernel combines the chunks. QORA_HIP_PF_ATTN_CH sets
+        // the chunk (a multiple of 64).
+        PrefillAttnParams q = p;
+        q.nc = 1;
+        q.ch = 0;
+        if (p.part && p.part_nc >= 2 && p.part_nc <= 8) {   // 8: pf_attn_merge_kernel's bound
+            const uint32_t keys = p.pos0 + p.T;
+            uint32_t ch = 128;
+            const char* ec = std::getenv("QORA_HIP_PF_ATTN_CH");
+            if (ec && *ec) ch = std::max(64u, (uint32_t)std::atoi(ec) / 64u * 64u);
+            if ((keys + ch - 1) / ch > p.part_nc) ch = ((keys + p.part_nc - 1) / p.part_nc + 63u) / 64u * 64u;
+            const uint32_t nc = (keys + ch - 1) / ch;
+            if (nc >= 2) {
+                q.nc = nc;
+                q.ch = ch;
+            }
+        }
+        const dim3 grid((p.T + qt - 1) / qt * q.nc, p.KVH);
 #define QORA_PF_ATTN(HD)                                                                                     \
     do {                                                                                                    \
-        if (p.kv_f16) hipLaunchKernelGGL((pf_attn_mfma_kernel<HD, true>), grid, dim3(256), 0, stream, p);   \
-        else hipLaunchKernelGGL((pf_attn_mfma_kernel<HD, false>), grid, dim3(256), 0, stream, p);           \
+        if (p.kv_f16) hipLaunchKernelGGL((pf_attn_mfma_kernel<HD, true>), grid, dim3(256), 0, stream, q);   \
+        else hipLaunchKernelGGL((pf_attn_mfma_kernel<HD, false>), grid, dim3(256), 0, stream, q);           \
+        if (q.nc > 1)                                                                                       \
+            hipLaunchKernelGGL((pf_attn_merge_kernel<HD>), dim3(p.T, (p.H * HD + 255) / 256), dim3(256), 0,  \
+                               stream, q);                                                                  \
     } while (0)
         if (p.hd == 128) QORA_PF_ATTN(128);
         else QORA_PF_ATTN(64);

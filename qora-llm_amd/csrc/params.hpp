@@ -208,6 +208,12 @@ struct PrefillAttnParams {
     float scale;
     float* out;                // attention output [T][qd]
     uint64_t kv_ps, kv_hs;     // cache addressing as in AttnParams (0: token-major)
+    // key-range split of the matrix-core kernel: a workspace for up to part_nc
+    // key chunks per query block (null / < 2: no split); nc and ch (keys per
+    // chunk, a multiple of 64) are set by the launcher
+    float* part;
+    uint32_t part_nc;
+    uint32_t nc, ch;
 };
 
 // On-device sampling (sample.hpp).

@@ -660,13 +660,18 @@ __global__ __launch_bounds__(256) void pf_attn_mfma_kernel(PrefillAttnParams p) 
     const uint32_t sub = wave / G;                  // query sub-tile of this wave
     const uint32_t h = kvh * G + wave % G;
     const uint32_t QT = 16u * (4u / G);             // queries per block
-    const uint32_t q0 = blockIdx.x * QT;            // chunk-relative first query of the block
+    const uint32_t nc = p.nc > 1u ? p.nc : 1u;      // key chunks per query block
+    const uint32_t q0 = (blockIdx.x / nc) * QT;     // chunk-relative first query of the block
     const uint32_t qd = p.H * HD, kvd = p.KVH * HD;
     const uint64_t cps = p.kv_ps ? p.kv_ps : kvd, chs = p.kv_ps ? p.kv_hs : HD;   // cache layout
     const uint32_t nq = min(QT, p.T - q0);
     const uint32_t last = p.pos0 + q0 + nq - 1u;    // last key any query of the block needs
     const uint32_t wq0 = q0 + sub * 16u;            // this wave's first query
     const bool wave_on = sub * 16u < nq;            // waves of a partial tile may hold no query
+    // this block's keys [kbeg, kend): all of them, or key chunk blockIdx.x % nc
+    const uint32_t kbeg = nc > 1u ? (blockIdx.x % nc) * p.ch : 0u;
+    const uint32_t kend = nc > 1u ? min(kbeg + p.ch, last + 1u) : last + 1u;
+    if (kbeg > last) return;                        // a chunk past every key of the block
 
     // Q fragment: lane holds q[wq0 + li][g4 * QS + s]
     float qf[QS];
@@ -690,7 +695,7 @@ __global__ __launch_bounds__(256) void pf_attn_mfma_kernel(PrefillAttnParams p) 
     for (int c = 0; c < OC; ++c) o[c] = f32x4v{0.f, 0.f, 0.f, 0.f};
     float* pw = ps[wave];
 
-    for (uint32_t k0 = 0; k0 <= last; k0 += KT) {
+    for (uint32_t k0 = kbeg; k0 < kend; k0 += KT) {
         __syncthreads();                            // the previous tiles are consumed
         // stage K and V rows k0 .. k0 + 63 (clamped to `last`; masked below)
         for (uint32_t e = t; e < (uint32_t)(KT * HD / 4); e += 256) {
@@ -789,6 +794,26 @@ __global__ __launch_bounds__(256) void pf_attn_mfma_kernel(PrefillAttnParams p) 
         }
     }
     if (!wave_on) return;
+    if (nc > 1u) {
+        // partial state of the chunk: unnormalised o, running max m and sum l
+        // per row, merged by pf_attn_merge_kernel
+        const uint64_t blk = (uint64_t)blockIdx.x * p.KVH + kvh;
+        float* po = p.part + (blk * 64u + wave * 16u) * HD;
+        float* pml = p.part + (uint64_t)gridDim.x * p.KVH * 64u * HD + (blk * 64u + wave * 16u) * 2u;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t row = 4u * g4 + (uint32_t)r;
+            if (wq0 + row >= q0 + nq) continue;
+#pragma unroll
+            for (int c = 0; c < OC; ++c) po[row * HD + 16 * c + li] = o[c][r];
+            if (li == 0) {
+                pml[row * 2u] = m[r];
+                pml[row * 2u + 1u] = l[r];
+            }
+        }
+        return;
+    }
+    if (!wave_on) return;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         const uint32_t qi = wq0 + 4u * g4 + (uint32_t)r;
@@ -797,6 +822,53 @@ __global__ __launch_bounds__(256) void pf_attn_mfma_kernel(PrefillAttnParams p) 
         float* out = p.out + (uint64_t)qi * qd + (uint64_t)h * HD + li;
 #pragma unroll
         for (int c = 0; c < OC; ++c) out[16 * c] = o[c][r] * inv;
+    }
+}
+
+// Merge of the key chunks of pf_attn_mfma_kernel (nc > 1): blocks of 256
+// elements of a token row; out = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c over the chunks
+// holding keys of the row's query block (a chunk with no key visible to the
+// row has m = -inf and adds nothing).
+template <int HD>
+__global__ __launch_bounds__(256) void pf_attn_merge_kernel(PrefillAttnParams p) {
+    constexpr uint32_t MC = 8;                      // most chunks (the workspace's bound)
+    const uint32_t t = blockIdx.x;
+    const uint32_t G = p.H / p.KVH, QT = 16u * (4u / G), nc = p.nc;
+    const uint32_t qb = t / QT, qloc = t % QT, sub = qloc / 16u, row = qloc % 16u;
+    const uint32_t q0 = qb * QT, nq = min(QT, p.T - q0);
+    const uint32_t last = p.pos0 + q0 + nq - 1u;
+    const uint32_t nlive = min(min(nc, MC), last / p.ch + 1u);
+    const uint64_t nblk = (uint64_t)((p.T + QT - 1u) / QT) * nc * p.KVH;
+    const float* po = p.part;
+    const float* pml = p.part + nblk * 64u * HD;
+    const uint32_t qd = p.H * HD;
+    // thread: element e = head * HD + d of the row (grid.y covers the row in
+    // 256-element pieces); every chunk's (m, l, o) requested before any is used
+    const uint32_t e = blockIdx.y * 256u + threadIdx.x;
+    if (e < qd) {
+        const uint32_t h = e / HD, d = e % HD;
+        const uint32_t kvh = h / G, wave = sub * G + h % G;
+        float mv[MC], lv[MC], ov[MC];
+#pragma unroll
+        for (uint32_t kc = 0; kc < MC; ++kc) {
+            const uint32_t kk = min(kc, nlive - 1u);
+            const uint64_t r = (((uint64_t)qb * nc + kk) * p.KVH + kvh) * 64u + wave * 16u + row;
+            mv[kc] = pml[r * 2u];
+            lv[kc] = pml[r * 2u + 1u];
+            ov[kc] = po[r * HD + d];
+        }
+        float M = mv[0];
+#pragma unroll
+        for (uint32_t kc = 1; kc < MC; ++kc) M = fmaxf(M, mv[kc]);
+        float num = 0.f, den = 0.f;
+#pragma unroll
+        for (uint32_t kc = 0; kc < MC; ++kc) {
+            if (kc >= nlive) break;
+            const float w = expf(mv[kc] - M);
+            num = fmaf(w, ov[kc], num);
+            den = fmaf(w, lv[kc], den);
+        }
+        p.out[(uint64_t)t * qd + h * HD + d] = num / den;
     }
 }
 

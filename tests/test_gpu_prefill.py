@@ -229,3 +229,35 @@ def test_row_producers_register_and_loop_bit_identical(ctx, pkg, monkeypatch, hi
     kl, vl = be.kv_layer(1)
     assert np.array_equal(reg, loop) and treg == tloop
     assert np.array_equal(kreg, kl) and np.array_equal(vreg, vl)
+
+
+@pytest.mark.parametrize("hd,kv_dtype,n,ch", [(64, 0, 150, "64"), (64, 1, 150, "64"), (128, 0, 200, "64"),
+                                               (128, 1, 130, ""), (128, 0, 256, "")])
+def test_batched_prefill_attention_key_chunks(ctx, pkg, orc, monkeypatch, hd, kv_dtype, n, ch):
+    """The prefill attention with each query block's keys split into chunks
+    (QORA_HIP_PF_ATTN_CH=64, else the default of 128 keys) and merged: logits,
+    cache and the next decode step against the oracle."""
+    print(f"case prefill key chunks hd={hd} kv={kv_dtype} n={n} ch={ch or 'default'}", flush=True)
+    if ch:
+        monkeypatch.setenv("QORA_HIP_PF_ATTN_CH", ch)
+    if hd == 64:
+        cfg = entry.smoke_config(pkg)
+    else:
+        cfg = pkg.ModelConfig(num_layers=2, vocab=1000, hidden=256, intermediate=704, num_heads=16,
+                              num_kv_heads=4, head_dim=128, rope_half_dim=64, rope_theta=5e6, rope_positions=512)
+    cfg.num_layers = 4
+    cfg.rope_positions = 512
+    w = pkg.synthetic_model(cfg, seed=4, fmt=1, rope_positions=512)
+    prompt = pkg.synth_tokens(4, 2800 + n, n, w.config.vocab)
+    be = pkg.HipBackend(ctx, w, kv_capacity=512, kv_dtype=kv_dtype)
+    om = orc.OracleModel(w, kv_capacity=512, T=4)
+    tol = REL_TOL if kv_dtype == 0 else 5e-3
+    logits, _ = be.raw_prefill(prompt)
+    assert rel_err(logits, om.prefill(prompt)) <= tol
+    for layer in (0, 3):
+        k, v = be.kv_layer(layer)
+        kr, vr = om.kv_layer(layer)
+        assert rel_err(k, kr) <= tol and rel_err(v, vr) <= tol
+    t = pkg.synth_tokens(4, 2900, 1, w.config.vocab)[0]
+    logits, _ = be.forward_decode_raw(int(t))
+    assert rel_err(logits, om.forward_decode(int(t))) <= tol
