@@ -651,7 +651,9 @@ __global__ __launch_bounds__(256) void pf_attn_mfma_kernel(PrefillAttnParams p) 
     constexpr int OC = HD / 16;                     // 16-dim output tiles
     __shared__ __align__(16) float ks[KT * KS];
     __shared__ __align__(16) float vs[KT * VS];
-    __shared__ __align__(16) float ps[4][16 * PS];
+    // P (4 waves x 16 rows x PS) reuses the K tile's space once every wave has
+    // its scores: 67 KB of LDS, two blocks per CU
+    static_assert(4 * 16 * PS <= KT * KS, "P fits in the K tile");
 
     const uint32_t t = threadIdx.x;
     const uint32_t lane = t % kWave, g4 = lane / 16u, li = lane % 16u;
@@ -693,7 +695,7 @@ __global__ __launch_bounds__(256) void pf_attn_mfma_kernel(PrefillAttnParams p) 
     for (int r = 0; r < 4; ++r) { m[r] = -INFINITY; l[r] = 0.f; }
 #pragma unroll
     for (int c = 0; c < OC; ++c) o[c] = f32x4v{0.f, 0.f, 0.f, 0.f};
-    float* pw = ps[wave];
+    float* pw = ks + wave * 16u * PS;
 
     for (uint32_t k0 = kbeg; k0 < kend; k0 += KT) {
         __syncthreads();                            // the previous tiles are consumed
@@ -721,7 +723,11 @@ __global__ __launch_bounds__(256) void pf_attn_mfma_kernel(PrefillAttnParams p) 
             vr[3] = vv.w;
         }
         __syncthreads();
-        if (!wave_on || k0 > p.pos0 + wq0 + 15u) continue;   // no key of this tile is visible to the wave
+        // a wave with no visible key in the tile skips the work, not the barriers
+        const bool active = wave_on && k0 <= p.pos0 + wq0 + 15u;
+        float f[4] = {1.f, 1.f, 1.f, 1.f};
+        float ev[4][4] = {};
+        if (active) {
         // ---- S = Q K^T: four 16 x 16 tiles ----
         f32x4v sacc[4];
 #pragma unroll
@@ -738,7 +744,6 @@ __global__ __launch_bounds__(256) void pf_attn_mfma_kernel(PrefillAttnParams p) 
             }
         }
         // ---- online softmax: lane holds rows 4 g4 + r, keys 16 c + li ----
-        float f[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const uint32_t qpos = p.pos0 + wq0 + 4u * g4 + (uint32_t)r;
@@ -761,7 +766,7 @@ __global__ __launch_bounds__(256) void pf_attn_mfma_kernel(PrefillAttnParams p) 
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
                 const float e = expf(sv[c] - mref);
-                pw[(4u * g4 + (uint32_t)r) * PS + 16u * c + li] = e;
+                ev[r][c] = e;
                 sum += e;
             }
             sum += __shfl_xor(sum, 1, kWave);
@@ -771,6 +776,13 @@ __global__ __launch_bounds__(256) void pf_attn_mfma_kernel(PrefillAttnParams p) 
             l[r] = l[r] * f[r] + sum;
             m[r] = m_new;
         }
+        }
+        __syncthreads();                            // every wave is done reading the K tile
+        if (!active) continue;
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) pw[(4u * g4 + (uint32_t)r) * PS + 16u * c + li] = ev[r][c];
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
