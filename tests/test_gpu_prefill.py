@@ -261,3 +261,18 @@ def test_batched_prefill_attention_key_chunks(ctx, pkg, orc, monkeypatch, hd, kv
     t = pkg.synth_tokens(4, 2900, 1, w.config.vocab)[0]
     logits, _ = be.forward_decode_raw(int(t))
     assert rel_err(logits, om.forward_decode(int(t))) <= tol
+
+
+def test_batched_prefill_attention_many_keys(ctx, pkg, orc):
+    """1100 tokens: the third 512-token chunk attends to 1100 keys, more than
+    8 chunks of 128, so the chunk grows to 192 keys (6 chunks)."""
+    print("case prefill key chunks 1100 tokens", flush=True)
+    w = _model(pkg, 1, layers=2, seed=8, positions=1200)
+    prompt = pkg.synth_tokens(8, 3000, 1100, w.config.vocab)
+    be = pkg.HipBackend(ctx, w, kv_capacity=1200)
+    om = orc.OracleModel(w, kv_capacity=1200, T=8)
+    logits, _ = be.raw_prefill(prompt)
+    assert rel_err(logits, om.prefill(prompt)) <= REL_TOL
+    k, v = be.kv_layer(1)
+    kr, vr = om.kv_layer(1)
+    assert rel_err(k, kr) <= REL_TOL and rel_err(v, vr) <= REL_TOL
