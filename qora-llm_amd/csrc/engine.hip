@@ -4,6 +4,8 @@
 #include "launch.hpp"
 
 #include <algorithm>
+#include <atomic>
+#include <chrono>
 #include <cstdlib>
 #include <cstring>
 #include <cstdio>
@@ -156,6 +158,7 @@ struct qora_hip_ctx {
     int32_t* h_tok = nullptr;
     int32_t* d_h_tok = nullptr;
     bool capturing = false;
+    bool tok_armed = false;              // h_tok[0] set to kTokPending for the step in flight
     std::vector<PreparedGemv> gemvs;
     ModelState m;
 };
@@ -1153,9 +1156,33 @@ void print_mk_trace(qora_hip_ctx* c) {
     std::fprintf(stderr, "\n");
 }
 
+// h_tok[0] while a step's token is outstanding (argmax_finish_kernel stores
+// the token there, a vocabulary index, never this value)
+constexpr int32_t kTokPending = INT32_MIN;
+
 int finish_step(qora_hip_ctx* c, float* logits, uint32_t* argmax) {
     ModelState& m = c->m;
     const bool mapped = c->d_h_tok != nullptr;   // argmax_finish_kernel stored the token in h_tok
+    if (mapped && c->tok_armed && !logits && !m.mk && !m.mlp) {
+        // Greedy step without logits: the token is read from the mapped word as
+        // soon as the device has stored it, without waiting for the stream's
+        // completion signal. Stream order keeps the next step's work behind
+        // this one. After 200 ms without a token (a failed launch, a fault)
+        // the stream is synchronised and its error reported.
+        c->tok_armed = false;
+        volatile int32_t* ht = c->h_tok;
+        const auto t0 = std::chrono::steady_clock::now();
+        for (uint32_t i = 1;; ++i) {
+            const int32_t tok = ht[0];
+            if (tok != kTokPending) {
+                m.dev_token = tok;
+                if (argmax) *argmax = (uint32_t)tok;
+                return QORA_HIP_OK;
+            }
+            if ((i & 1023u) == 0 && std::chrono::steady_clock::now() - t0 > std::chrono::milliseconds(200)) break;
+        }
+    }
+    c->tok_armed = false;
     if (!mapped) HIP_TRY(c, hipMemcpyAsync(&c->h_pin[16], m.d_token, 4, hipMemcpyDeviceToHost, c->stream));
     if (m.mk) HIP_TRY(c, hipMemcpyAsync(&c->h_pin[24], m.d_mk_err, 4, hipMemcpyDeviceToHost, c->stream));
     if (logits) HIP_TRY(c, hipMemcpyAsync(logits, m.d_logits, (size_t)m.vocab * 4, hipMemcpyDeviceToHost, c->stream));
@@ -1190,6 +1217,11 @@ extern "C" int qora_hip_decode(qora_hip_ctx* c, uint32_t token, float* logits, u
     if (token >= m.vocab) return fail(c, QORA_HIP_E_INVALID, "token id out of range");
     if (force_fail("launch")) return fail(c, QORA_HIP_E_DEVICE, "forced launch failure (QORA_HIP_FORCE_FAIL=launch)");
     if (int rc = put_token(c, token)) return rc;
+    if (c->h_tok) {
+        reinterpret_cast<volatile int32_t*>(c->h_tok)[0] = kTokPending;
+        std::atomic_thread_fence(std::memory_order_seq_cst);
+        c->tok_armed = true;
+    }
     if (int rc = launch_step(c, true, m.host_pos)) return rc;
     if (int rc = finish_step(c, logits, argmax)) return rc;
     m.host_pos += 1;

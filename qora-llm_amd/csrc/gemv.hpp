@@ -602,11 +602,17 @@ __global__ __launch_bounds__(256) void argmax_finish_kernel(ArgmaxFinishParams p
         // no candidate above -inf: the sampler returns index 0
         const int32_t tok = (i0 == 0xFFFFFFFFu) ? 0 : (int32_t)i0;
         *p.token_out = tok;
-        if (p.host_token) *p.host_token = tok;
         if (p.pos) {
             const int32_t ps = *p.pos;
             p.gen[ps] = tok;
             *p.pos = ps + 1;
+        }
+        if (p.host_token) {
+            // last, after the step's other stores are visible: a host that
+            // reads the token without waiting for the kernel's end finds
+            // every result of the step in place
+            __threadfence_system();
+            *p.host_token = tok;
         }
     }
 }
