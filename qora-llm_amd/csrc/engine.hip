@@ -1222,7 +1222,10 @@ extern "C" int qora_hip_decode(qora_hip_ctx* c, uint32_t token, float* logits, u
         std::atomic_thread_fence(std::memory_order_seq_cst);
         c->tok_armed = true;
     }
-    if (int rc = launch_step(c, true, m.host_pos)) return rc;
+    if (int rc = launch_step(c, true, m.host_pos)) {
+        c->tok_armed = false;
+        return rc;
+    }
     if (int rc = finish_step(c, logits, argmax)) return rc;
     m.host_pos += 1;
     return QORA_HIP_OK;
