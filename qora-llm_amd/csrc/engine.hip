@@ -2167,8 +2167,14 @@ extern "C" int qora_hip_decode_sample(qora_hip_ctx* c, uint32_t token, const uin
     if (token >= m.vocab) return fail(c, QORA_HIP_E_INVALID, "token id out of range");
     if (int rc = put_token(c, token)) return rc;
     if (int rc = launch_step(c, true, m.host_pos)) return rc;
-    uint32_t greedy = 0;
-    if (int rc = finish_step(c, logits, &greedy)) return rc;
+    if (logits || m.mk || m.mlp) {
+        uint32_t greedy = 0;
+        if (int rc = finish_step(c, logits, &greedy)) return rc;
+    } else {
+        // no wait here: the sampling kernels follow the step on the stream, and
+        // the host builds the penalty list while the step runs
+        m.dev_token = -1;
+    }
     m.host_pos += 1;
     return sample_device(c, m.d_logits, m.vocab, history, n_history, params, rng_state, token_out, c->stream);
 }
