@@ -208,3 +208,33 @@ def test_long_context_decode_matches_oracle(ctx, pkg, orc, kv_dtype, hd):
         ref = om.forward_decode(int(t))
         assert rel_err(logits, ref) <= tol
     assert be.kv_len() == n + 4
+
+
+def test_state_calls_right_after_a_logits_free_step(ctx, pkg, orc):
+    """A greedy step without logits returns once the device has stored its
+    token, before the stream reports completion. Calls made right after it
+    (cache read-back, reset, a new prompt) see the step's results complete."""
+    print("case state calls after logits-free steps", flush=True)
+    w = small_model(pkg, 1, layers=4, seed=9)
+    be = pkg.HipBackend(ctx, w, kv_capacity=128)
+    om = orc.OracleModel(w, kv_capacity=128, T=4)
+    prompt = pkg.synth_tokens(9, 2100, 12, w.config.vocab)
+    ref, _ = om.greedy(prompt, 9)
+    for _ in range(3):
+        _, tok = be.raw_prefill(prompt, want_logits=False)
+        got = [tok]
+        for _ in range(8):
+            _, tok = be.forward_decode_raw(int(tok), want_logits=False)
+            got.append(tok)
+            assert be.kv_len() == len(prompt) + len(got) - 1
+        assert got == ref
+        k, _ = be.kv_layer(2)
+        assert k.shape[0] == len(prompt) + 8
+        be.kv_reset()
+        assert be.kv_len() == 0
+    om2 = orc.OracleModel(w, kv_capacity=128, T=4)
+    om2.prefill(prompt)
+    for t in ref[:8]:
+        om2.forward_decode(int(t))
+    kr, _ = om2.kv_layer(2)
+    assert rel_err(k, kr) <= REL_TOL
