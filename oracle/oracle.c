@@ -70,33 +70,6 @@ static void init_tables(void) {
 
 float oq_h2f(uint16_t h) { init_tables(); return H2F(h); }
 
-uint16_t oq_f2h(float f) {
-    uint32_t x;
-    memcpy(&x, &f, 4);
-    const uint32_t sign = (x >> 16) & 0x8000u;
-    const uint32_t absx = x & 0x7FFFFFFFu;
-    if (absx >= 0x7F800000u) { /* inf / nan */
-        return (uint16_t)(sign | 0x7C00u | (absx > 0x7F800000u ? 0x200u | ((absx >> 13) & 0x3FFu) : 0u));
-    }
-    if (absx >= 0x477FF000u) return (uint16_t)(sign | 0x7C00u); /* rounds to inf */
-    if (absx < 0x38800000u) { /* result subnormal or zero */
-        if (absx < 0x33000000u) return (uint16_t)sign; /* < half of min subnormal */
-        /* value = m * 2^(e-150); the subnormal unit is 2^-24, so the
-         * result mantissa is m * 2^(e-126), rounded to nearest even. */
-        const uint32_t e = absx >> 23;
-        const uint32_t m = (absx & 0x7FFFFFu) | 0x800000u;
-        const uint32_t sh = 126 - e;
-        uint32_t r = m >> sh;
-        const uint32_t rem = m & ((1u << sh) - 1u);
-        const uint32_t half = 1u << (sh - 1);
-        if (rem > half || (rem == half && (r & 1u))) ++r;
-        return (uint16_t)(sign | r);
-    }
-    uint32_t r = ((absx >> 13) - (112u << 10));
-    const uint32_t rem = absx & 0x1FFFu;
-    if (rem > 0x1000u || (rem == 0x1000u && (r & 1u))) ++r;
-    return (uint16_t)(sign | r);
-}
 
 void oq_set_threads(int nthreads) { g_nthreads = nthreads; }
 

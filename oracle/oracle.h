@@ -13,13 +13,40 @@
  * the same T the oracle reproduces the reference's floating-point result
  * (the reference's own result depends on rayon's thread count T).
  *
- * Parity pins (tests/test_oracle.py): exhaustive f16 widening, exhaustive
- * nibble dequant, exact-arithmetic GEMV regimes, float64 brute force on small
- * shapes, closed forms for RMSNorm / RoPE / softmax / attention, and the
- * k-split order checked against a float32 numpy restatement of the chunked
- * sum. Parity unpinned (no reference test or import can pin it): the exact
+ * Pin of each exported function (tests/test_oracle.py unless named):
+ *   oq_h2f                  all 65536 codes vs IEEE widening (numpy)
+ *   oq_dequant_q4(_row)     all 256 bytes x every scale class vs float64;
+ *                           one-hot GEMV rows
+ *   oq_gemv_q4_rows         numpy float32 restatement of the row order
+ *   oq_gemv_q4              single pass and k-split (T = 1, 3, 12) bit-exact
+ *                           vs numpy float32 restatements; exact-arithmetic
+ *                           regime = float64; one-hot, zero, linearity
+ *   oq_fused_gate_up_q4     partials bit-exact vs restatement, SiLU vs float64
+ *   oq_gemv_f16             scalar order bit-exact (numpy float32); AVX-512
+ *                           order, single pass and k-split (T = 3, 12 at
+ *                           k*n >= 4e6), bit-exact vs an FMA restatement that
+ *                           is itself checked against libm fmaf
+ *   oq_fused_gate_up_f16    two GEMVs + SiLU vs float64
+ *   oq_lm_head_q4 / _f16    row-dot order bit-exact (numpy float32)
+ *   oq_rms_norm_f16         order bit-exact; constant-vector closed form
+ *   oq_apply_rope           identity at pos 0, pair norms, float64
+ *   oq_softmax              uniform scores, float64
+ *   oq_attention_decode     L = 1, identical keys, GQA mapping, float64
+ *   oq_argmax               first-max rules (ties, NaN, +-inf)
+ *   oq_forward_decode /     float64 restatement of the model (tests/
+ *   oq_prefill              model_f64.py), Q4 and F16 (both F16 dispatch
+ *                           orders, T = 1 and 3); greedy chain; F16 embedding
+ *                           row exact
+ *   oq_kv_*                 caches vs the float64 model's; kv_set resumes
+ *                           bit-identically
+ *   oq_set_threads          results identical for 1 and 4 threads
+ *   oq_rng_next_f32,        tests/test_sampling.py: integer xorshift
+ *   penalties, top-k        restatement, penalty semantics, one-draw cases,
+ *                           sampled frequencies vs the float64 distribution
+ * Parity unpinned (no reference test or import can pin it): the exact
  * bits of libm expf used in SiLU and softmax (glibc expf here vs the Rust
- * platform libm there), covered by tolerance only.
+ * platform libm there), covered by tolerance only; the reference's rayon
+ * thread count T, taken as a parameter.
  */
 #ifndef QORA_ORACLE_H
 #define QORA_ORACLE_H
@@ -33,8 +60,6 @@ extern "C" {
 
 /* IEEE binary16 -> binary32 widening (half 2.7.1 f16::to_f32). Exact. */
 float oq_h2f(uint16_t h);
-/* binary32 -> binary16, round to nearest even (half f16::from_f32). */
-uint16_t oq_f2h(float f);
 
 /* ---- kernels (src/gemv.rs, src/simd.rs) ---- */
 

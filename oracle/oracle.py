@@ -35,7 +35,6 @@ class OqModelDesc(ctypes.Structure):
 
 _SIGS = {
     "oq_h2f": (ctypes.c_float, [ctypes.c_uint16]),
-    "oq_f2h": (ctypes.c_uint16, [ctypes.c_float]),
     "oq_dequant_q4_row": (None, [_P, _P, _U64, _U64, _P]),
     "oq_dequant_q4": (None, [_P, _P, _U64, _U64, _P]),
     "oq_gemv_q4_rows": (None, [_P, _P, _P, _U64, _U64, _U64, _P]),

@@ -7,6 +7,7 @@ import pytest
 
 import __graft_entry__ as entry
 from helpers import REL_TOL, rel_err
+from model_f64 import F64Model
 
 pytestmark = pytest.mark.gpu
 
@@ -23,9 +24,11 @@ def test_prefill_decode_logits_and_kv_match_oracle(ctx, pkg, orc, fmt):
     prompt = pkg.synth_tokens(0, 2000, 13, w.config.vocab)
     be = pkg.HipBackend(ctx, w, kv_capacity=128)
     om = orc.OracleModel(w, kv_capacity=128, T=4)
+    truth = F64Model(w)
     logits, tok = be.raw_prefill(prompt)
     ref = om.prefill(prompt)
     assert rel_err(logits, ref) <= REL_TOL
+    assert rel_err(logits, truth.prefill(prompt)) <= 1e-4
     assert tok == orc.argmax(ref)
     assert be.kv_len() == len(prompt)
     for layer in (0, 3):
@@ -35,10 +38,14 @@ def test_prefill_decode_logits_and_kv_match_oracle(ctx, pkg, orc, fmt):
         assert rel_err(k, kr) <= REL_TOL and rel_err(v, vr) <= REL_TOL
     # teacher-forced decode: feed fixed tokens, compare every step
     feed = pkg.synth_tokens(0, 2001, 20, w.config.vocab)
-    for t in feed:
+    for i, t in enumerate(feed):
         logits, tok = be.forward_decode_raw(int(t))
         ref = om.forward_decode(int(t))
         assert rel_err(logits, ref) <= REL_TOL
+        if i % 5 == 0:
+            assert rel_err(logits, truth.step(int(t))) <= 1e-4
+        else:
+            truth.step(int(t))
         gap = orc.top2_gap(ref)
         if gap > 1e-4 * float(np.max(np.abs(ref))):
             assert tok == orc.argmax(ref)

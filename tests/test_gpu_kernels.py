@@ -200,6 +200,9 @@ def test_gate_up_f16_vs_oracle(ctx, orc, pkg):
         ctx.check(ctx.lib.qora_hip_gate_up_f16(ctx.h, d.put(gw), d.put(uw), d.put(x), out, k, n, None), "gate_up_f16")
         got = d.get(out, n, np.float32)
     assert rel_err(got, orc.fused_gate_up_f16(x, gw, uw, k, n, T=12)) <= REL_TOL
+    g = gw.view(np.float16).astype(np.float64).reshape(k, n).T @ x.astype(np.float64)
+    u = uw.view(np.float16).astype(np.float64).reshape(k, n).T @ x.astype(np.float64)
+    assert rel_err(got, g / (1 + np.exp(-g)) * u) <= 1e-5
 
 
 @pytest.mark.parametrize("rows,cols", [(32000, 2048), (1000, 256)])
@@ -211,6 +214,8 @@ def test_rowdot_f16_vs_oracle_lm_head(ctx, orc, pkg, rows, cols):
         ctx.check(ctx.lib.qora_hip_gemv_f16_rowdot(ctx.h, d.put(w), d.put(x), y, rows, cols, None), "rowdot_f16")
         got = d.get(y, rows, np.float32)
     assert rel_err(got, orc.lm_head_f16(x, w, rows, cols)) <= REL_TOL
+    truth = w.view(np.float16).astype(np.float64).reshape(rows, cols) @ x.astype(np.float64)
+    assert rel_err(got, truth) <= 1e-5
 
 
 @pytest.mark.parametrize("n", [2048, 11008, 1, 33])

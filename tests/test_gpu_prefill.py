@@ -11,6 +11,7 @@ import pytest
 
 import __graft_entry__ as entry
 from helpers import REL_TOL, dequant_np, device, exact_q4, rel_err, rng
+from model_f64 import F64Model
 
 pytestmark = pytest.mark.gpu
 
@@ -157,6 +158,8 @@ def test_batched_prefill_matches_oracle(ctx, pkg, orc, fmt, kv_dtype, n):
     ref = om.prefill(prompt)
     tol = REL_TOL if kv_dtype == 0 else 5e-3
     assert rel_err(logits, ref) <= tol
+    if kv_dtype == 0:
+        assert rel_err(logits, F64Model(w).prefill(prompt)) <= 1e-4
     if orc.top2_gap(ref) > 1e-4 * float(np.max(np.abs(ref))):
         assert tok == orc.argmax(ref)
     assert be.kv_len() == n

@@ -16,6 +16,7 @@ import numpy as np
 import pytest
 
 from helpers import dequant_np, exact_q4, random_q4, rel_err, rng
+from model_f64 import F64Model
 
 F32 = np.float32
 
@@ -234,6 +235,119 @@ def test_lm_head_q4_row_dot_order(orc, pkg):
     assert np.array_equal(orc.lm_head_q4(x, packed, scales, vocab, hidden), want)
 
 
+def fma_f32(a, b, c):
+    """Correctly rounded float32 a*b + c (an FMA), elementwise, from float64:
+    the product of two float32 values is exact in float64; TwoSum gives the
+    exact error e of s = fl64(p + c); rounding s to float32 is then correct
+    except when s lies exactly on a float32 midpoint and e != 0, where the
+    sign of e decides: the exact sum s + e lies on the side e points to."""
+    a64 = np.asarray(a, np.float64)
+    b64 = np.asarray(b, np.float64)
+    c64 = np.asarray(c, np.float64)
+    p = a64 * b64
+    s = p + c64
+    bb = s - p
+    e = (p - (s - bb)) + (c64 - bb)
+    r = s.astype(F32)
+    d = s - r.astype(np.float64)
+    nb = np.nextafter(r, np.where(d > 0, F32(np.inf), F32(-np.inf)).astype(F32))
+    mid = (d != 0) & ((r.astype(np.float64) + nb.astype(np.float64)) * 0.5 == s)
+    return np.where(mid & (e != 0) & (np.sign(e) == np.sign(d)), nb, r).astype(F32)
+
+
+def test_fma_restatement_matches_libm_fmaf():
+    """The FMA restatement against glibc's fmaf (correctly rounded), on random
+    operands and on sums built to land exactly on float32 midpoints."""
+    import ctypes
+    import ctypes.util
+    libm = ctypes.CDLL(ctypes.util.find_library("m"))
+    libm.fmaf.restype = ctypes.c_float
+    libm.fmaf.argtypes = [ctypes.c_float] * 3
+    r = rng(40)
+    a = r.normal(size=4000).astype(F32)
+    b = (r.normal(size=4000) * 0.02).astype(np.float16).astype(F32)
+    c = (r.normal(size=4000) * 10.0 ** r.integers(-3, 4, size=4000)).astype(F32)
+    # double-rounding cases: c has an odd last bit and a*b = h (1 - 2^-46),
+    # h half an ulp of c, so fl64(a*b + c) is the float32 midpoint above c
+    # (a tie that rounds to even, away from c) while the exact sum lies just
+    # below it (correct result: c)
+    cm = np.array([1 + 2.0 ** -23, 1 + 3 * 2.0 ** -23, 2 + 2.0 ** -22, 1000.0 + 2.0 ** -14], F32)
+    am = np.full(cm.size, 1 + 2.0 ** -23, F32)
+    bm = (np.spacing(cm) / 2 * (1 - 2.0 ** -23)).astype(F32)
+    assert not np.array_equal((am.astype(np.float64) * bm + cm).astype(F32), cm)   # naive rounding is off
+    for x, y, z in ((a, b, c), (am, bm, cm), (-am, bm, -cm)):
+        want = np.array([libm.fmaf(float(p), float(q), float(t)) for p, q, t in zip(x, y, z)], F32)
+        assert np.array_equal(fma_f32(x, y, z).view(np.uint32), want.view(np.uint32))
+
+
+def f16_rows_fma(x, wf, n):
+    """simd::gemv_f16_avx512 (simd.rs:151-176): rows with x == 0 skipped,
+    out = fma(x, w, out) over the 16-aligned columns, out += x * w on the tail."""
+    out = np.zeros(n, F32)
+    n16 = n // 16 * 16
+    for i in range(len(x)):
+        if x[i] == 0:
+            continue
+        out[:n16] = fma_f32(F32(x[i]), wf[i, :n16], out[:n16])
+        out[n16:] = out[n16:] + F32(x[i]) * wf[i, n16:]
+    return out
+
+
+def f16_gemv_avx(x, w, k, n, T):
+    """gemv_f16's AVX-512 arm (gemv.rs:539-556): one pass when k*n < 4e6,
+    else T partials of ceil(k/T) rows added onto zeros in thread order."""
+    wf = w.view(np.float16).astype(F32).reshape(k, n)
+    if k * n < 4_000_000:
+        return f16_rows_fma(x, wf, n)
+    chunk = -(-k // T)
+    out = np.zeros(n, F32)
+    for t in range(T):
+        ks, ke = t * chunk, min(k, (t + 1) * chunk)
+        if ks < ke:
+            out = out + f16_rows_fma(x[ks:ke], wf[ks:ke], n)
+    return out
+
+
+@pytest.mark.parametrize("k,n,T", [(96, 160, 1), (40, 72, 1), (2048, 2048, 3), (2048, 2048, 12)])
+def test_gemv_f16_avx_order_bit_exact(orc, pkg, k, n, T):
+    """The AVX-512 F16 GEMV, single pass and k-split (k*n >= 4e6), bit-exact
+    against the FMA restatement; n = 72 has a scalar tail."""
+    w = pkg.synth_f16(41, k + n, k * n, 0.02)
+    x = pkg.synth_f32(41, 2, k)
+    x[5] = 0.0                                       # a skipped row
+    want = f16_gemv_avx(x, w, k, n, T)
+    assert np.array_equal(orc.gemv_f16(x, w, k, n, T=T, avx512=True).view(np.uint32), want.view(np.uint32))
+
+
+def test_gate_up_f16_fallback(orc, pkg):
+    """fused_gate_up_gemv with F16 weights (gemv.rs:395-407): two gemv_f16
+    calls, then silu(g) * u (expf: tolerance)."""
+    k, n = 64, 96
+    gw = pkg.synth_f16(42, 1, k * n, 0.1)
+    uw = pkg.synth_f16(42, 2, k * n, 0.1)
+    x = pkg.synth_f32(42, 3, k)
+    for avx in (1, 0):
+        g = orc.gemv_f16(x, gw, k, n, T=1, avx512=avx).astype(np.float64)
+        u = orc.gemv_f16(x, uw, k, n, T=1, avx512=avx).astype(np.float64)
+        got = orc.fused_gate_up_f16(x, gw, uw, k, n, T=1, avx512=avx)
+        assert rel_err(got, g / (1 + np.exp(-g)) * u) <= 1e-6
+
+
+def test_lm_head_f16_row_dot_order(orc, pkg):
+    """lm_head_parallel_f16 (gemv.rs:805-822): per row, sum += x[j] * f32(w[j])
+    left to right (scalar multiply, then add)."""
+    vocab, hidden = 300, 96
+    w = pkg.synth_f16(43, 1, vocab * hidden, 0.02)
+    x = pkg.synth_f32(43, 2, hidden)
+    wf = w.view(np.float16).astype(F32).reshape(vocab, hidden)
+    want = np.zeros(vocab, F32)
+    for j in range(hidden):
+        want = want + F32(x[j]) * wf[:, j]
+    assert np.array_equal(orc.lm_head_f16(x, w, vocab, hidden).view(np.uint32), want.view(np.uint32))
+    truth = wf.astype(np.float64) @ x.astype(np.float64)
+    assert rel_err(orc.lm_head_f16(x, w, vocab, hidden), truth) <= 1e-6
+
+
 # ---------------------------------------------------------------------------
 # RMSNorm, RoPE, softmax, attention, argmax
 # ---------------------------------------------------------------------------
@@ -328,54 +442,10 @@ def test_argmax_first_max_rules(orc):
 # the full model: composition against a float64 restatement
 # ---------------------------------------------------------------------------
 
-def model_f64_step(w, cache, token, pos):
-    """forward_decode_raw (gemv.rs:872-1019) in float64 from the definition:
-    embed -> per layer [RMSNorm, q/k/v, RoPE on flagged layers at `pos`,
-    append K/V, GQA attention, o, residual, RMSNorm, silu(gate)*up, down,
-    residual] -> final RMSNorm -> tied lm_head."""
-    c = w.config
-    deq = lambda wt: dequant_np(wt.packed, wt.scales, wt.k, wt.n)
-    f16 = lambda a: a.view(np.float16).astype(np.float64)
-
-    def rms(x, g):
-        return x / np.sqrt(np.mean(x * x) + 1e-6) * f16(g)
-
-    def rope(v, heads):
-        v = v.reshape(heads, c.head_dim).copy()
-        half = c.rope_half_dim
-        ct = w.rope_cos[pos * half:(pos + 1) * half].astype(np.float64)
-        st = w.rope_sin[pos * half:(pos + 1) * half].astype(np.float64)
-        a, b = v[:, :half].copy(), v[:, half:2 * half].copy()
-        v[:, :half], v[:, half:2 * half] = a * ct - b * st, b * ct + a * st
-        return v.reshape(-1)
-
-    x = deq(w.embed)[token]
-    for l in range(c.num_layers):
-        Wq, Wk, Wv, Wo, Wg, Wu, Wd = (deq(t) for t in w.layers[l])
-        xn = rms(x, w.input_norm[l])
-        q, k, v = xn @ Wq, xn @ Wk, xn @ Wv
-        if w.no_rope_layers[l]:
-            q, k = rope(q, c.num_heads), rope(k, c.num_kv_heads)
-        cache[l][0].append(k)
-        cache[l][1].append(v)
-        K = np.array(cache[l][0]).reshape(-1, c.num_kv_heads, c.head_dim)
-        V = np.array(cache[l][1]).reshape(-1, c.num_kv_heads, c.head_dim)
-        att = np.zeros((c.num_heads, c.head_dim))
-        for h in range(c.num_heads):
-            sc = K[:, h // c.num_kv_groups] @ q.reshape(c.num_heads, c.head_dim)[h] / np.sqrt(c.head_dim)
-            p = np.exp(sc - sc.max())
-            att[h] = (p / p.sum()) @ V[:, h // c.num_kv_groups]
-        x = x + att.reshape(-1) @ Wo
-        xn = rms(x, w.post_attn_norm[l])
-        g, u = xn @ Wg, xn @ Wu
-        x = x + (g / (1 + np.exp(-g)) * u) @ Wd
-    return rms(x, w.final_norm) @ deq(w.embed).T
-
-
-def tiny_model(pkg):
+def tiny_model(pkg, fmt=1):
     cfg = pkg.ModelConfig(num_layers=2, vocab=50, hidden=64, intermediate=96, num_heads=4, num_kv_heads=2,
                           head_dim=16, rope_half_dim=8, rope_theta=5e6, rope_positions=32)
-    w = pkg.synthetic_model(cfg, seed=7, rope_positions=32)
+    w = pkg.synthetic_model(cfg, seed=7, fmt=fmt, rope_positions=32)
     w.no_rope_layers = np.array([0, 1], np.uint8)
     # non-trivial norms so the gamma placement is pinned too
     w.input_norm = [pkg.synth_f16(7, 3000 + l, cfg.hidden, 0.5) for l in range(2)]
@@ -385,30 +455,55 @@ def tiny_model(pkg):
     # actually change the residual stream
     for ws in w.layers:
         for wt in ws:
-            wt.scales = (wt.scales.view(np.float16).astype(np.float32) * 20).astype(np.float16).view(np.uint16)
+            if fmt == 1:
+                wt.scales = (wt.scales.view(np.float16).astype(np.float32) * 20).astype(np.float16).view(np.uint16)
+            else:
+                wt.data = (wt.data.view(np.float16).astype(np.float32) * 20).astype(np.float16).view(np.uint16)
     return w
 
 
-def test_model_decode_and_prefill_vs_float64(orc, pkg):
-    w = tiny_model(pkg)
-    om = orc.OracleModel(w, kv_capacity=32, T=1)
-    cache = [([], []) for _ in range(w.config.num_layers)]
+@pytest.mark.parametrize("fmt,T,avx512", [(1, 1, 1), (0, 1, 1), (0, 1, 0), (0, 3, 1)])
+def test_model_decode_and_prefill_vs_float64(orc, pkg, fmt, T, avx512):
+    """forward_decode_raw and raw_prefill of the oracle, Q4 and F16 (F16:
+    gemv_f16 in both dispatch orders, the two-GEMV gate/up fallback of
+    gemv.rs:395-407, the F16 embedding row of gemv.rs:515-526 and
+    lm_head_parallel_f16) against the float64 model."""
+    w = tiny_model(pkg, fmt)
+    f64 = F64Model(w)
+    om = orc.OracleModel(w, kv_capacity=32, T=T, avx512=avx512)
     toks = [3, 17, 42, 8, 29]
     for pos, t in enumerate(toks):
-        ref = model_f64_step(w, cache, t, pos)
+        ref = f64.step(t)
         got = om.forward_decode(t)
         assert rel_err(got, ref) <= 1e-4, pos
         assert np.std(ref) > 1e-3                    # the model does something
     for l in range(w.config.num_layers):
         k, v = om.kv_layer(l)
-        assert rel_err(np.ravel(k), np.ravel(cache[l][0])) <= 1e-4
-        assert rel_err(np.ravel(v), np.ravel(cache[l][1])) <= 1e-4
+        kr, vr = f64.kv_layer(l)
+        assert rel_err(np.ravel(k), np.ravel(kr)) <= 1e-4
+        assert rel_err(np.ravel(v), np.ravel(vr)) <= 1e-4
     # raw_prefill (its own GEMM order, gemv.rs:1027-1190) lands on the same state
-    om2 = orc.OracleModel(w, kv_capacity=32, T=1)
+    om2 = orc.OracleModel(w, kv_capacity=32, T=T, avx512=avx512)
     logits = om2.prefill(toks)
     assert rel_err(logits, ref) <= 1e-4
     for l in range(w.config.num_layers):
         assert rel_err(np.ravel(om2.kv_layer(l)[0]), np.ravel(om.kv_layer(l)[0])) <= 1e-5
+
+
+def test_model_f16_embedding_row_is_exact(orc, pkg):
+    """embed_lookup, F16 arm (gemv.rs:515-522): the row is widened exactly.
+    With every projection weight zero the layers add exact zeros to the
+    residual, so the logits are lm_head_f16(rms_norm(row)) bit for bit (both
+    pinned on their own above)."""
+    w = tiny_model(pkg, 0)
+    for ws in w.layers:
+        for wt in ws:
+            wt.data = np.zeros_like(wt.data)
+    om = orc.OracleModel(w, kv_capacity=32, T=1)
+    tok = 23
+    row = w.embed.data.reshape(w.config.vocab, w.config.hidden)[tok].view(np.float16).astype(np.float32)
+    want = orc.lm_head_f16(orc.rms_norm(row, w.final_norm), w.embed.data, w.config.vocab, w.config.hidden)
+    assert np.array_equal(om.forward_decode(tok), want)
 
 
 def test_model_greedy_is_argmax_chain(orc, pkg):
@@ -424,3 +519,33 @@ def test_model_greedy_is_argmax_chain(orc, pkg):
         logits = om2.forward_decode(t)
     assert toks == chain
     assert len(gaps) == 6
+
+
+def test_kv_set_resumes_like_the_built_cache(orc, pkg):
+    """oq_kv_set (a caller-built RawKvCache, gemv.rs:154-166): a cache set
+    from another model's rows continues exactly like that model."""
+    w = tiny_model(pkg)
+    a = orc.OracleModel(w, kv_capacity=32, T=1)
+    a.prefill([4, 9, 33, 2])
+    b = orc.OracleModel(w, kv_capacity=32, T=1)
+    for l in range(w.config.num_layers):
+        b.kv_set(l, *a.kv_layer(l))
+    assert b.kv_len() == 4
+    assert np.array_equal(a.forward_decode(11), b.forward_decode(11))
+
+
+def test_thread_count_does_not_change_results(orc, pkg):
+    """oq_set_threads only spreads independent items (heads, lm_head rows,
+    k-split partials) over threads; the partials are added in thread order."""
+    k, n = 2048, 2048
+    packed, scales = pkg.synth_q4(44, 1, k, n)
+    x = pkg.synth_f32(44, 2, k)
+    w = tiny_model(pkg)
+    outs = []
+    for nt in (1, 4):
+        orc.set_threads(nt)
+        om = orc.OracleModel(w, kv_capacity=32, T=3)
+        outs.append((orc.gemv_q4(x, packed, scales, k, n, T=12), om.prefill([1, 5, 7]), om.forward_decode(3)))
+    orc.set_threads(0)
+    for u, v in zip(*outs):
+        assert np.array_equal(u, v)
