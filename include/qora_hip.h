@@ -36,6 +36,11 @@ extern "C" {
 #define QORA_HIP_E_NOMEM (-3)   /* device allocation failed */
 #define QORA_HIP_E_STATE (-4)   /* wrong call order: no model, cache full ... */
 #define QORA_HIP_E_IO (-5)      /* .qora file read/parse failure */
+/* A decode step's fixed-point values left their range: a residual value of
+ * 2^25 or more, or one projection term of 2^20 or more (the reference's fp32
+ * would go on). The step's results are not valid; steps are refused until
+ * qora_hip_kv_reset, qora_hip_prefill or qora_hip_kv_upload. */
+#define QORA_HIP_E_RANGE (-6)
 
 typedef struct qora_hip_ctx qora_hip_ctx;
 
@@ -62,6 +67,10 @@ int qora_hip_upload_f16(qora_hip_ctx* ctx, const uint16_t* w, size_t len, uint64
                         uint32_t* wid);
 /* Device addresses of an uploaded weight (scales is NULL for F16). */
 int qora_hip_weight_ptrs(qora_hip_ctx* ctx, uint32_t wid, void** packed_or_data, void** scales);
+/* Frees an uploaded weight (dropping a WeightData, gemv.rs:99-102; the id is
+ * not reused). Refused with QORA_HIP_E_STATE while the initialised model
+ * uses it. */
+int qora_hip_release_weight(qora_hip_ctx* ctx, uint32_t wid);
 
 /* ---- model ---------------------------------------------------------------
  * DecodeWeights::from_parts (gemv.rs:306-337) + the per-layer config of
@@ -138,23 +147,6 @@ int qora_hip_sample(qora_hip_ctx* ctx, const float* logits, uint64_t vocab, cons
 int qora_hip_decode_sample(qora_hip_ctx* ctx, uint32_t token, const uint32_t* history, uint64_t n_history,
                            const qora_sample_params* params, uint64_t* rng_state, float* logits_or_null,
                            uint32_t* token_out);
-
-/* How decode steps run on this context (no counterpart in the reference):
- * 0 = no model, 1 = one captured graph of kernels per step (the default),
- * 2 = one persistent launch per step (opt-in, QORA_HIP_DECODE=mk at
- * model_init; Q4 weights). */
-int qora_hip_decode_mode(const qora_hip_ctx* ctx);
-
-/* 1 when the decode step runs the gate|up and down projections of each layer
- * as one launch (the down workgroups wait on arrival counts of the gate|up
- * workgroups while their weights stream in; opt-in with QORA_HIP_MLP=1 at
- * model_init, slower than two launches on MI355X), 0 when they are two
- * launches (the default; also F16 weights or a plan the fused kernel does not
- * take).
- * Either way the same accumulations (exact integer sums) give the same
- * results. The reference's decode step runs the fused gate+up GEMV and then
- * the down GEMV (gemv.rs:1002-1006 inside forward_decode_raw). */
-uint32_t qora_hip_mlp_fused(const qora_hip_ctx* ctx);
 
 /* Context bound of the fused short-context step (no counterpart in the
  * reference): graph-driven steps that append a position below it run each

@@ -25,6 +25,7 @@ QORA_HIP_E_DEVICE = -2
 QORA_HIP_E_NOMEM = -3
 QORA_HIP_E_STATE = -4
 QORA_HIP_E_IO = -5
+QORA_HIP_E_RANGE = -6
 
 FORMAT_F16 = 0
 FORMAT_Q4 = 1
@@ -74,6 +75,7 @@ SIGNATURES = {
     "qora_hip_upload_q4": (_I, [_P, _P, _SZ, _P, _SZ, _U64, _U64, ctypes.POINTER(_U32)]),
     "qora_hip_upload_f16": (_I, [_P, _P, _SZ, _U64, _U64, ctypes.POINTER(_U32)]),
     "qora_hip_weight_ptrs": (_I, [_P, _U32, ctypes.POINTER(_P), ctypes.POINTER(_P)]),
+    "qora_hip_release_weight": (_I, [_P, _U32]),
     "qora_hip_model_init": (_I, [_P, ctypes.POINTER(ModelDesc)]),
     "qora_hip_load_model": (_I, [_P, ctypes.c_char_p, _U32, _U32]),
     "qora_hip_prefill": (_I, [_P, _P, _SZ, _P, ctypes.POINTER(_U32)]),
@@ -101,9 +103,7 @@ SIGNATURES = {
     "qora_hip_gemv_prepare": (_I, [_P, _U32, _U32, _I, _P]),
     "qora_hip_gemv_run": (_I, [_P, _U32, _P, _P, _P]),
     "qora_hip_gemv_release": (_I, [_P, _U32]),
-    "qora_hip_decode_mode": (_I, [_P]),
     "qora_hip_attn_o_limit": (_U32, [_P]),
-    "qora_hip_mlp_fused": (_U32, [_P]),
     "qora_hip_lm_head_prepare": (_I, [_P, _U32, _P]),
     "qora_hip_lm_head_run": (_I, [_P, _U32, _P, _P, _P, _P]),
     "qora_hip_gemv_q4_rowdot": (_I, [_P, _P, _P, _P, _P, _U64, _U64, _P]),
@@ -555,17 +555,9 @@ class HipBackend:
     def kv_reset(self) -> None:
         self.ctx.check(self.ctx.lib.qora_hip_kv_reset(self.ctx.h), "kv_reset")
 
-    def decode_mode(self) -> int:
-        """1: one captured graph per step, 2: one persistent launch per step."""
-        return int(self.ctx.lib.qora_hip_decode_mode(self.ctx.h))
-
     def attn_o_limit(self) -> int:
         """Steps appending a position below this run attention inside the o GEMV."""
         return int(self.ctx.lib.qora_hip_attn_o_limit(self.ctx.h))
-
-    def mlp_fused(self) -> bool:
-        """Whether each layer's gate|up and down projections run as one launch."""
-        return bool(self.ctx.lib.qora_hip_mlp_fused(self.ctx.h))
 
     def kv_layer(self, layer: int):
         """(k, v) of one layer as f32 [len][kv_heads*head_dim] (RawKvCache entry)."""

@@ -113,6 +113,12 @@ __device__ __forceinline__ float from_fixed(long long a) {
     return (float)((double)a * (1.0 / kFixScale));
 }
 
+// Range guard of the fixed-point accumulators (kFixReadLimit, kFixAddLimit).
+__device__ __forceinline__ bool fix_out_of_range(long long a, long long lim) { return a >= lim || a <= -lim; }
+__device__ __forceinline__ void fix_flag(int* flag, bool bad) {
+    if (bad && flag) __hip_atomic_store(flag, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Cross-lane reductions over a wave64 with DPP (no LDS round trips): two
 // quad permutes and two row rotates give every lane the total of its
 // 16-lane row, then the four row totals are read with v_readlane and

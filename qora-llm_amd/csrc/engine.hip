@@ -46,6 +46,8 @@ struct ModelState {
     long long* d_gu_acc = nullptr;       // gate|up sums [2 inter]
     float* d_attn_part = nullptr;        // attention split partials
     float* d_ss = nullptr;               // [L][2][64] sums of squares per K slice (RMSNorm)
+    int* d_range = nullptr;              // set by the kernels when a fixed-point value leaves its range
+    bool range_bad = false;              // a step reported it: refused until the cache is reset
     float* d_logits = nullptr;
     int32_t* d_token = nullptr;
     int32_t* d_pos = nullptr;
@@ -56,16 +58,6 @@ struct ModelState {
     GemvPlan pl_qkv, pl_o, pl_gu, pl_down;
     uint32_t lm_blocks = 0;              // argmax partials of the lm_head launch
     bool lm_mfma = false;                // Q4 lm_head on the matrix cores (else the VALU row-dot)
-    // persistent decode step (decode_mk_kernel): one cooperative launch per token
-    bool mk = false;
-    uint32_t mk_blocks = 0;
-    MkParams mkp{};
-    MkParams* d_mkp[2] = {nullptr, nullptr};   // device copies: [0] prefill step, [1] with the lm_head
-    void* mk_region[2] = {nullptr, nullptr};
-    uint32_t* d_mk_err = nullptr;              // [64]: flag, report count, reports
-    unsigned long long* d_mk_trace = nullptr;  // QORA_HIP_MK_TRACE: per-phase clock stamps
-    size_t mk_region_bytes = 0;
-    ArgmaxFinishParams p_fin_mk{};
     uint32_t attn_chunk = 0, attn_s_max = 0;
     std::vector<GemvParams> p_qkv, p_o, p_gu, p_down;
     std::vector<AttnParams> p_attn;
@@ -73,10 +65,6 @@ struct ModelState {
     // steps that append a position below attn_o_max
     std::vector<AttnOParams> p_ao;
     uint32_t attn_o_max = 0;
-    // gate|up and down in one launch (gemv_q4m_mlp_kernel); done counter in
-    // the slot after the gate|up sums, wait-failure flag in the mapped h_tok[1]
-    std::vector<GemvMlpParams> p_mlp;
-    bool mlp = false;
     RowdotParams p_lm{};
     LmHeadParams p_lmq{};
     ArgmaxFinishParams p_fin{};
@@ -243,6 +231,8 @@ int ensure_pf_ws(qora_hip_ctx* c, uint64_t bytes) {
 
 void free_model(qora_hip_ctx* c) {
     ModelState& m = c->m;
+    // a greedy step without logits returns while its graph may still run
+    (void)hipStreamSynchronize(c->stream);
     if (m.g_step) (void)hipGraphExecDestroy(m.g_step);
     if (m.g_prefill) (void)hipGraphExecDestroy(m.g_prefill);
     if (m.g_step_ao) (void)hipGraphExecDestroy(m.g_step_ao);
@@ -303,12 +293,8 @@ int record_step(qora_hip_ctx* c, bool with_lm_head, bool fused) {
             HIP_TRY(c, launch_attn(m.p_attn[l], s));
             HIP_TRY(c, launch_gemv(m.fmt, m.pl_o, m.p_o[l], s));
         }
-        if (m.mlp) {
-            HIP_TRY(c, launch_gemv_mlp(m.pl_gu, m.pl_down, m.p_mlp[l], s));
-        } else {
-            HIP_TRY(c, launch_gemv(m.fmt, m.pl_gu, m.p_gu[l], s));
-            HIP_TRY(c, launch_gemv(m.fmt, m.pl_down, m.p_down[l], s));
-        }
+        HIP_TRY(c, launch_gemv(m.fmt, m.pl_gu, m.p_gu[l], s));
+        HIP_TRY(c, launch_gemv(m.fmt, m.pl_down, m.p_down[l], s));
     }
     if (with_lm_head) {
         if (m.lm_mfma) HIP_TRY(c, launch_lmhead(m.lm_blocks, m.p_lmq, s));
@@ -343,20 +329,6 @@ uint32_t attn_o_limit(const ModelState& m) {
     return n <= 0 ? 0u : (uint32_t)std::min<long>(n, (long)m.cap);
 }
 
-// int64 words after the gate|up sums: the fused MLP's count and its 32 group
-// counters, 128 bytes apart
-constexpr uint32_t kMlpCounterWords = 16 * 33;
-
-// The fused MLP launch, opt-in (QORA_HIP_MLP=1): it measures slower than the
-// two launches (938 against 1013 tok/s), the chain of arrival atomics and
-// polls costing more than the kernel boundary it removes. It needs the
-// mapped host word that reports a failed wait.
-bool mlp_enabled(const ModelState& m, const qora_hip_ctx* c) {
-    if (m.fmt != FMT_Q4 || !gemv_mlp_supported(m.pl_gu, m.pl_down) || !c->d_h_tok) return false;
-    const char* v = std::getenv("QORA_HIP_MLP");
-    return v && std::strcmp(v, "1") == 0;
-}
-
 bool eager_mode() {
     const char* v = std::getenv("QORA_HIP_EAGER");
     return v && *v && *v != '0';
@@ -365,12 +337,6 @@ bool eager_mode() {
 // pos: the position the step appends (its context length is pos + 1).
 int launch_step(qora_hip_ctx* c, bool with_lm_head, uint64_t pos) {
     ModelState& m = c->m;
-    if (m.mk) {
-        HIP_TRY(c, launch_decode_mk(m.mkp, m.d_mkp[with_lm_head ? 1 : 0], m.mk_blocks, c->stream));
-        if (with_lm_head) HIP_TRY(c, launch_argmax_finish(m.p_fin_mk, c->stream));
-        else HIP_TRY(c, launch_advance_pos(m.d_pos, c->stream));
-        return QORA_HIP_OK;
-    }
     const bool fused = pos < (uint64_t)m.attn_o_max;
     if (eager_mode()) return record_step(c, with_lm_head, fused);
     hipGraphExec_t g = fused ? (with_lm_head ? m.g_step_ao : m.g_prefill_ao) : (with_lm_head ? m.g_step : m.g_prefill);
@@ -449,7 +415,7 @@ extern "C" int qora_hip_create(int device, qora_hip_ctx** out) {
         return QORA_HIP_E_DEVICE;
     }
     if (hipHostMalloc((void**)&c->h_tok, 64, hipHostMallocMapped | hipHostMallocCoherent) == hipSuccess) {
-        std::memset(c->h_tok, 0, 64);   // [0] argmax token, [1] fused-MLP wait failure
+        std::memset(c->h_tok, 0, 64);   // [0] argmax token
         if (hipHostGetDevicePointer((void**)&c->d_h_tok, c->h_tok, 0) != hipSuccess) c->d_h_tok = nullptr;
     } else {
         c->h_tok = nullptr;
@@ -527,6 +493,21 @@ extern "C" int qora_hip_upload_f16(qora_hip_ctx* c, const uint16_t* data, size_t
     return QORA_HIP_OK;
 }
 
+extern "C" int qora_hip_release_weight(qora_hip_ctx* c, uint32_t wid) {
+    if (!c) return QORA_HIP_E_INVALID;
+    if (!get_weight(c, wid)) return fail(c, QORA_HIP_E_INVALID, "unknown weight id");
+    if (c->capturing) return fail(c, QORA_HIP_E_STATE, "release_weight frees: not allowed during capture");
+    const ModelState& m = c->m;
+    if (m.ready && (wid == m.embed_wid || std::find(m.wids.begin(), m.wids.end(), wid) != m.wids.end()))
+        return fail(c, QORA_HIP_E_STATE, "weight is part of the initialised model");
+    HIP_TRY(c, hipStreamSynchronize(c->stream));
+    DevWeight& w = c->weights[wid];
+    if (w.w) (void)hipFree(w.w);
+    if (w.scales) (void)hipFree(w.scales);
+    w = DevWeight();
+    return QORA_HIP_OK;
+}
+
 extern "C" int qora_hip_weight_ptrs(qora_hip_ctx* c, uint32_t wid, void** data, void** scales) {
     if (!c) return QORA_HIP_E_INVALID;
     const DevWeight* w = get_weight(c, wid);
@@ -540,203 +521,9 @@ extern "C" int qora_hip_weight_ptrs(qora_hip_ctx* c, uint32_t wid, void** data, 
 // model
 // ===========================================================================
 
-namespace {
-
-// GEMV plans of the persistent step: K slices of kMkKW rows, one group per wave.
-bool plan_mk_gemvs(const ModelState& m, int cus, GemvPlan pl[4]) {
-    const uint32_t qd = m.H * m.hd, kvd = m.KVH * m.hd;
-    const uint32_t gq = qd / 32, gkv = kvd / 32, gh = m.hidden / 32, gi = m.inter / 32;
-    const uint32_t qkv_groups[3] = {gq, gkv, gkv};
-    const uint32_t gu_groups[2] = {gi, gi};
-    return plan_gemv_q4m(m.hidden, qkv_groups, 3, false, cus, &pl[MK_QKV], 1, kMkKW) &&
-           plan_gemv_q4m(qd, &gh, 1, false, cus, &pl[MK_O], m.hd, kMkKW) &&
-           plan_gemv_q4m(m.hidden, gu_groups, 2, true, cus, &pl[MK_GU], 1, kMkKW) &&
-           plan_gemv_q4m(m.inter, &gh, 1, false, cus, &pl[MK_DOWN], 1, kMkKW);
-}
-
-// Grid of the persistent decode step, or 0 when the model takes the graph
-// path. The persistent step is opt-in (QORA_HIP_DECODE=mk): it is correct but
-// measured slower than the captured graph on MI355X, whose kernel boundaries
-// cost less than the producer-to-consumer round trips it replaces them with.
-// It also needs Q4 weights, a (hidden, head_dim) instance and a device that
-// holds the whole grid resident.
-uint32_t plan_mk_grid(qora_hip_ctx* c, const qora_model_desc* d) {
-    const ModelState& m = c->m;
-    const char* v = std::getenv("QORA_HIP_DECODE");
-    if (!v || std::strcmp(v, "mk") != 0) return 0;
-    if (m.fmt != FMT_Q4 || !m.lm_mfma || !decode_mk_supported(m.hidden, m.hd)) return 0;
-    if (m.groups > (uint32_t)kAttnMaxGroups || m.groups * m.KVH != m.H || m.hd % 32 != 0) return 0;
-    // one workgroup per CU: the occupancy query reports two for this kernel,
-    // but with all five waves resident a CU holds one (setup_mk measures it)
-    if (decode_mk_blocks_per_cu(m.hidden, m.hd, d->kv_dtype == 1 ? 1 : 0) < 1) return 0;
-    const uint32_t nb = (uint32_t)c->cus;
-    GemvPlan pl[4];
-    if (!plan_mk_gemvs(m, c->cus, pl)) return 0;
-    for (int i = 0; i < 4; ++i)
-        if (pl[i].gw != 1 || pl[i].kr != (uint32_t)kMkKW || pl[i].blocks() > (uint64_t)kMkSlots * nb) return 0;
-    if ((uint64_t)m.KVH * m.attn_s_max > nb) return 0;
-    return nb;
-}
-
-// Packs every layer's GEMVs for the persistent step, allocates its two
-// parity regions and writes its parameters (two device copies: prefill step
-// and decode step).
-int setup_mk(qora_hip_ctx* c, const qora_model_desc* d, const DevWeight* emb, uint32_t nb) {
-    ModelState& m = c->m;
-    GemvPlan pl[4];
-    if (!plan_mk_gemvs(m, c->cus, pl)) return fail(c, QORA_HIP_E_INVALID, "persistent step: GEMV plans");
-    MkParams& P = m.mkp;
-    P = MkParams{};
-    const uint32_t qd = m.H * m.hd, kvd = m.KVH * m.hd, qkv_n = qd + 2 * kvd;
-    const size_t kvb = m.kv_f16 ? 2 : 4;
-    std::vector<MkLayer> layers(m.L);
-    for (uint32_t l = 0; l < m.L; ++l) {
-        const DevWeight* W[7];
-        for (int j = 0; j < 7; ++j) W[j] = get_weight(c, m.wids[l * 7 + j]);
-        const uint32_t gq = qd / 32, gkv = kvd / 32, gh = m.hidden / 32, gi = m.inter / 32;
-        GemvParams g[4];
-        for (auto& x : g) x = GemvParams{};
-        g[MK_QKV].seg[0] = GemvSeg{(const uint8_t*)W[0]->w, (const uint16_t*)W[0]->scales, gq, 0, 0, 0};
-        g[MK_QKV].seg[1] = GemvSeg{(const uint8_t*)W[1]->w, (const uint16_t*)W[1]->scales, gkv, 0, 0, 0};
-        g[MK_QKV].seg[2] = GemvSeg{(const uint8_t*)W[2]->w, (const uint16_t*)W[2]->scales, gkv, 0, 0, 0};
-        g[MK_QKV].nseg = 3;
-        g[MK_QKV].k = m.hidden;
-        g[MK_O].seg[0] = GemvSeg{(const uint8_t*)W[3]->w, (const uint16_t*)W[3]->scales, gh, 0, 0, 0};
-        g[MK_O].nseg = 1;
-        g[MK_O].k = qd;
-        g[MK_GU].seg[0] = GemvSeg{(const uint8_t*)W[4]->w, (const uint16_t*)W[4]->scales, gi, 0, 0, 0};
-        g[MK_GU].seg[1] = GemvSeg{(const uint8_t*)W[5]->w, (const uint16_t*)W[5]->scales, gi, 0, 0, 0};
-        g[MK_GU].nseg = 2;
-        g[MK_GU].paired = 1;
-        g[MK_GU].k = m.hidden;
-        g[MK_DOWN].seg[0] = GemvSeg{(const uint8_t*)W[6]->w, (const uint16_t*)W[6]->scales, gh, 0, 0, 0};
-        g[MK_DOWN].nseg = 1;
-        g[MK_DOWN].k = m.inter;
-        MkLayer& ly = layers[l];
-        ly = MkLayer{};
-        for (int k = 0; k < 4; ++k) {
-            apply_plan(pl[k], &g[k]);
-            if (int rc = pack_model_gemv(c, FMT_Q4, pl[k], &g[k])) return rc;
-            ly.tw[k] = g[k].tw;
-            ly.ts[k] = g[k].ts;
-            ly.te[k] = g[k].tes;
-            if (l == 0) {
-                P.g[k] = g[k];
-                for (auto& sg : P.g[k].seg) sg.w = nullptr, sg.scales = nullptr;
-                P.g[k].tw = nullptr;
-                P.g[k].ts = nullptr;
-                P.g[k].tes = nullptr;
-            }
-        }
-        ly.gamma[0] = m.d_norms + ((size_t)l * 2 + 0) * m.hidden;
-        ly.gamma[1] = m.d_norms + ((size_t)l * 2 + 1) * m.hidden;
-        ly.kc = (uint8_t*)m.d_k + (size_t)l * m.cap * kvd * kvb;
-        ly.vc = (uint8_t*)m.d_v + (size_t)l * m.cap * kvd * kvb;
-        ly.use_rope = d->use_rope[l] ? 1 : 0;
-    }
-    void* tbl = nullptr;
-    if (int rc = model_alloc(c, layers.size() * sizeof(MkLayer), &tbl)) return rc;
-    HIP_TRY(c, hipMemcpy(tbl, layers.data(), layers.size() * sizeof(MkLayer), hipMemcpyHostToDevice));
-
-    // one region per parity: R, Q, RP, U, SS, A
-    size_t off = 0;
-    auto carve = [&](size_t bytes) {
-        off = (off + 255) & ~(size_t)255;
-        const size_t o = off;
-        off += bytes;
-        return o;
-    };
-    const size_t oR = carve((size_t)(m.L + 1) * m.hidden * 8), oQ = carve((size_t)m.L * qkv_n * 8);
-    const size_t oRP = carve((size_t)m.L * m.hidden * 8), oU = carve((size_t)m.L * 2 * m.inter * 8);
-    const size_t oSS = carve((size_t)m.L * 2 * 8), oA = carve((size_t)m.L * m.KVH * 4);
-    m.mk_region_bytes = (off + 255) & ~(size_t)255;
-    for (int i = 0; i < 2; ++i) {
-        if (int rc = model_alloc(c, m.mk_region_bytes, &m.mk_region[i])) return rc;
-        HIP_TRY(c, hipMemset(m.mk_region[i], 0, m.mk_region_bytes));
-        uint8_t* b = (uint8_t*)m.mk_region[i];
-        P.buf[i] = MkBufs{(long long*)(b + oR), (long long*)(b + oQ), (long long*)(b + oRP), (long long*)(b + oU),
-                          (long long*)(b + oSS), (uint32_t*)(b + oA)};
-        P.clear_base[i] = m.mk_region[i];
-    }
-    P.clear_n = m.mk_region_bytes / 16;
-    void* part = nullptr;
-    if (int rc = model_alloc(c, (size_t)m.KVH * m.attn_s_max * m.groups * (m.hd + 2) * 4, &part)) return rc;
-
-    P.layers = (const MkLayer*)tbl;
-    P.nl = m.L;
-    P.hidden = m.hidden;
-    P.inter = m.inter;
-    P.H = m.H;
-    P.KVH = m.KVH;
-    P.hd = m.hd;
-    P.G = m.groups;
-    P.half = m.half;
-    P.vocab = m.vocab;
-    P.chunk = m.attn_chunk;
-    P.s_max = m.attn_s_max;
-    P.kv_ps = m.hd;                      // head-major cache: [KVH][cap][hd] per layer
-    P.kv_hs = (uint64_t)m.cap * m.hd;
-    P.kv_f16 = m.kv_f16;
-    P.rope_cos = m.d_cos;
-    P.rope_sin = m.d_sin;
-    P.part = (float*)part;
-    P.pos = m.d_pos;
-    P.token = m.d_token;
-    P.prompt = m.d_prompt;
-    P.emb_w = (const uint8_t*)emb->w;
-    P.emb_s = (const uint16_t*)emb->scales;
-    P.lm = m.p_lmq;
-    void* errp = nullptr;
-    if (int rc = model_alloc(c, 1024, &errp)) return rc;
-    HIP_TRY(c, hipMemset(errp, 0, 1024));
-    m.d_mk_err = (uint32_t*)errp;
-    P.err = m.d_mk_err;
-    if (std::getenv("QORA_HIP_MK_TRACE")) {
-        void* tp = nullptr;
-        const size_t tb = (size_t)nb * (m.L * 5 + 2) * 3 * 8;
-        if (int rc = model_alloc(c, tb, &tp)) return rc;
-        HIP_TRY(c, hipMemset(tp, 0, tb));
-        m.d_mk_trace = (unsigned long long*)tp;
-    }
-    {
-        // One launch that only checks that the whole grid is resident at once
-        // (every wave waits for all workgroups to arrive, bounded); the step's
-        // waits would otherwise time out. If not, the model keeps the graph path.
-        P.residency_test = 1;
-        void* dp = nullptr;
-        if (int rc = model_alloc(c, sizeof(MkParams), &dp)) return rc;
-        HIP_TRY(c, hipMemcpy(dp, &P, sizeof(MkParams), hipMemcpyHostToDevice));
-        HIP_TRY(c, hipMemset(m.d_mk_err, 0, 1024));
-        HIP_TRY(c, hipMemset(m.d_mk_err + 202, 0xFF, 4));
-        HIP_TRY(c, launch_decode_mk(P, (const MkParams*)dp, nb, c->stream));
-        HIP_TRY(c, hipStreamSynchronize(c->stream));
-        uint32_t st[3] = {};
-        HIP_TRY(c, hipMemcpy(st, m.d_mk_err + 200, sizeof st, hipMemcpyDeviceToHost));
-        if (std::getenv("QORA_HIP_MK_RESIDENCY"))
-            std::fprintf(stderr, "persistent step residency: grid %u, started %u, fewest seen together %u\n", nb,
-                         st[0], st[2]);
-        HIP_TRY(c, hipMemset(m.d_mk_err, 0, 1024));
-        P.residency_test = 0;
-        if (st[2] < nb) return QORA_HIP_OK;   // not all resident: stay on the graph path
-    }
-    P.trace = m.d_mk_trace;
-    for (int i = 0; i < 2; ++i) {
-        P.with_lm = i;
-        void* dp = nullptr;
-        if (int rc = model_alloc(c, sizeof(MkParams), &dp)) return rc;
-        HIP_TRY(c, hipMemcpy(dp, &P, sizeof(MkParams), hipMemcpyHostToDevice));
-        m.d_mkp[i] = (MkParams*)dp;
-    }
-    m.mk_blocks = nb;
-    m.p_fin_mk = ArgmaxFinishParams{m.d_argv, m.d_argi, nb, m.d_token, m.d_pos, m.d_gen, c->d_h_tok};
-    m.mk = true;
-    return QORA_HIP_OK;
-}
-
-}  // namespace
-
 extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
     if (!c || !d) return fail(c, QORA_HIP_E_INVALID, "null argument");
+    if (c->capturing) return fail(c, QORA_HIP_E_STATE, "model_init allocates: not allowed during capture");
     HIP_TRY(c, hipSetDevice(c->device));
     free_model(c);
     if (d->num_layers == 0 || d->vocab == 0 || d->hidden == 0 || d->intermediate == 0 || d->num_heads == 0 ||
@@ -839,17 +626,17 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
     MALLOC(d_v, (size_t)m.L * m.cap * kvd * kvb);
     MALLOC(d_xacc, (size_t)m.hidden * 8);
     MALLOC(d_qkv_acc, qkv_n * 8);
-    MALLOC(d_gu_acc, ((size_t)2 * m.inter + kMlpCounterWords) * 8);   // + the fused MLP's counters
+    MALLOC(d_gu_acc, (size_t)2 * m.inter * 8);
     MALLOC(d_attn_part, (size_t)m.KVH * m.attn_s_max * m.groups * (m.hd + 2) * 4);
     MALLOC(d_ss, (size_t)m.L * 2 * kAttnMaxSplits * 4);
+    MALLOC(d_range, 64);
     MALLOC(d_logits, (size_t)m.vocab * 4);
     MALLOC(d_token, 64);
     MALLOC(d_pos, 64);
     MALLOC(d_gen, (size_t)m.cap * 4 + 64);
     MALLOC(d_prompt, (size_t)m.cap * 4 + 64);
-    const uint32_t mk_grid = plan_mk_grid(c, d);
-    MALLOC(d_argv, (size_t)std::max(m.lm_blocks, mk_grid) * 4);
-    MALLOC(d_argi, (size_t)std::max(m.lm_blocks, mk_grid) * 4);
+    MALLOC(d_argv, (size_t)m.lm_blocks * 4);
+    MALLOC(d_argi, (size_t)m.lm_blocks * 4);
 #undef MALLOC
     {
         // Cache slots past the current length are read (and skipped) by the
@@ -862,8 +649,9 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
     }
     HIP_TRY(c, hipMemset(m.d_xacc, 0, (size_t)m.hidden * 8));
     HIP_TRY(c, hipMemset(m.d_qkv_acc, 0, qkv_n * 8));
-    HIP_TRY(c, hipMemset(m.d_gu_acc, 0, ((size_t)2 * m.inter + kMlpCounterWords) * 8));
+    HIP_TRY(c, hipMemset(m.d_gu_acc, 0, (size_t)2 * m.inter * 8));
     HIP_TRY(c, hipMemset(m.d_pos, 0, 64));
+    HIP_TRY(c, hipMemset(m.d_range, 0, 64));
     HIP_TRY(c, hipMemset(m.d_token, 0, 64));
     HIP_TRY(c, hipMemset(m.d_gen, 0, (size_t)m.cap * 4 + 64));
     HIP_TRY(c, hipMemset(m.d_prompt, 0, (size_t)m.cap * 4 + 64));
@@ -895,8 +683,6 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
     m.p_attn.resize(m.L);
     m.attn_o_max = attn_o_limit(m);
     if (m.attn_o_max) m.p_ao.resize(m.L);
-    m.mlp = mlp_enabled(m, c);
-    if (m.mlp) m.p_mlp.resize(m.L);
     for (uint32_t l = 0; l < m.L; ++l) {
         const DevWeight* W[7];
         for (int j = 0; j < 7; ++j) W[j] = get_weight(c, m.wids[l * 7 + j]);
@@ -915,7 +701,8 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
         q.ss_out = m.d_ss + ((size_t)l * 2 + 0) * kAttnMaxSplits;
         q.acc = m.d_qkv_acc;
         q.zero_ptr = m.d_gu_acc;
-        q.zero_n = 2 * m.inter + kMlpCounterWords;   // the gate|up sums and the fused MLP's counters
+        q.range_flag = m.d_range;
+        q.zero_n = 2 * m.inter;
         apply_plan(m.pl_qkv, &q);
         if (int rc = pack_model_gemv(c, (int)m.fmt, m.pl_qkv, &q)) { free_model(c); return rc; }
 
@@ -958,6 +745,7 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
         o.groups = m.groups;
         o.pos = m.d_pos;
         o.acc = m.d_xacc;
+        o.range_flag = m.d_range;
         apply_plan(m.pl_o, &o);
         if (int rc = pack_model_gemv(c, (int)m.fmt, m.pl_o, &o)) { free_model(c); return rc; }
         if (m.attn_o_max) m.p_ao[l] = AttnOParams{o, a};
@@ -975,6 +763,7 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
         g.ss_out = m.d_ss + ((size_t)l * 2 + 1) * kAttnMaxSplits;
         g.acc = m.d_gu_acc;
         g.zero_ptr = m.d_qkv_acc;
+        g.range_flag = m.d_range;
         g.zero_n = (uint32_t)qkv_n;
         apply_plan(m.pl_gu, &g);
         if (int rc = pack_model_gemv(c, (int)m.fmt, m.pl_gu, &g)) { free_model(c); return rc; }
@@ -990,11 +779,9 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
         dn.ss_n = m.pl_gu.splits;
         dn.norm_n = m.hidden;
         dn.acc = m.d_xacc;
+        dn.range_flag = m.d_range;
         apply_plan(m.pl_down, &dn);
         if (int rc = pack_model_gemv(c, (int)m.fmt, m.pl_down, &dn)) { free_model(c); return rc; }
-        if (m.mlp)
-            m.p_mlp[l] = GemvMlpParams{g, dn, m.pl_gu.grid(), reinterpret_cast<uint32_t*>(m.d_gu_acc + 2 * m.inter),
-                                       c->d_h_tok + 1};
     }
     m.p_lm = RowdotParams{};
     m.p_lm.w = (const uint8_t*)emb->w;
@@ -1007,6 +794,7 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
     m.p_lm.do_argmax = 1;
     m.p_lm.part_val = m.d_argv;
     m.p_lm.part_idx = m.d_argi;
+    m.p_lm.range_flag = m.d_range;
     if (m.lm_mfma) {
         uint64_t wb = 0, sb = 0;
         lmhead_tile_bytes(m.vocab, m.hidden, &wb, &sb);
@@ -1028,15 +816,14 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
         m.p_lmq.do_argmax = 1;
         m.p_lmq.part_val = m.d_argv;
         m.p_lmq.part_idx = m.d_argi;
+        m.p_lmq.range_flag = m.d_range;
     }
-    m.p_fin = ArgmaxFinishParams{m.d_argv, m.d_argi, m.lm_blocks, m.d_token, m.d_pos, m.d_gen, c->d_h_tok};
+    m.p_fin = ArgmaxFinishParams{m.d_argv, m.d_argi, m.lm_blocks, m.d_token, m.d_pos, m.d_gen, c->d_h_tok, m.d_range};
     m.p_emb_tok = EmbedParams{(const uint8_t*)emb->w, (const uint16_t*)emb->scales, (int)m.fmt, m.hidden,
                               m.vocab, m.d_token, nullptr, m.d_xacc};
     m.p_emb_prompt = EmbedParams{(const uint8_t*)emb->w, (const uint16_t*)emb->scales, (int)m.fmt, m.hidden,
                                  m.vocab, m.d_prompt, m.d_pos, m.d_xacc};
 
-    if (mk_grid)
-        if (int rc = setup_mk(c, d, emb, mk_grid)) { free_model(c); return rc; }
     HIP_TRY(c, hipDeviceSynchronize());
     if (int rc = capture_step(c, true, false, &m.g_step)) { free_model(c); return rc; }
     if (int rc = capture_step(c, false, false, &m.g_prefill)) { free_model(c); return rc; }
@@ -1051,109 +838,37 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
 
 namespace {
 
+// Sets the device position; a new cache state also clears the range flag.
 int set_device_pos(qora_hip_ctx* c, uint64_t pos) {
-    ModelState& m = c->m;
-    if (m.mk) {
-        // the persistent step expects its parity cleared by the previous step
-        for (int i = 0; i < 2; ++i) HIP_TRY(c, hipMemsetAsync(m.mk_region[i], 0, m.mk_region_bytes, c->stream));
-        HIP_TRY(c, hipMemsetAsync(m.d_mk_err, 0, 1024, c->stream));
-    }
     c->h_pin[2] = (int32_t)pos;
     HIP_TRY(c, hipMemcpyAsync(c->m.d_pos, &c->h_pin[2], 4, hipMemcpyHostToDevice, c->stream));
+    HIP_TRY(c, hipMemsetAsync(c->m.d_range, 0, 4, c->stream));
     HIP_TRY(c, hipStreamSynchronize(c->stream));
+    if (c->h_tok) reinterpret_cast<volatile int32_t*>(c->h_tok)[1] = 0;
+    c->m.range_bad = false;
     return QORA_HIP_OK;
+}
+
+// The error of a step whose fixed-point values left their range (the flag
+// reached the host with the token); later steps are refused until the cache
+// is reset, re-filled by a prefill or uploaded.
+int range_error(qora_hip_ctx* c) {
+    c->m.range_bad = true;
+    return fail(c, QORA_HIP_E_RANGE,
+                "fixed-point range exceeded (a residual value of 2^25 or more, or a projection term of 2^20 or "
+                "more): the step's results are not valid; reset the KV cache");
 }
 
 int check_step_room(qora_hip_ctx* c, uint64_t steps) {
     ModelState& m = c->m;
     if (!m.ready) return fail(c, QORA_HIP_E_STATE, "model not initialised");
+    if (c->capturing) return fail(c, QORA_HIP_E_STATE, "decode and prefill steps are not allowed during capture");
+    if (m.range_bad) return range_error(c);
     if (m.host_pos + steps > m.cap)
         return fail(c, QORA_HIP_E_STATE, "KV cache full (capacity " + std::to_string(m.cap) + ")");
     if (m.any_rope && m.host_pos + steps > m.rope_positions)
         return fail(c, QORA_HIP_E_STATE, "position beyond the RoPE tables");
     return QORA_HIP_OK;
-}
-
-// The persistent step's error flag is read back with the token (d_mk_err[0]
-// into h_pin[24]); on an error the reports of the timed-out waits follow.
-int check_mk_error(qora_hip_ctx* c) {
-    ModelState& m = c->m;
-    if (m.mlp && reinterpret_cast<volatile int32_t*>(c->h_tok)[1] != 0) {
-        reinterpret_cast<volatile int32_t*>(c->h_tok)[1] = 0;
-        return fail(c, QORA_HIP_E_DEVICE,
-                    "decode step: the down projection's wait for the gate|up workgroups timed out; reset the KV cache");
-    }
-    if (!m.mk || c->h_pin[24] == 0) return QORA_HIP_OK;
-    uint32_t e[64] = {};
-    HIP_TRY(c, hipMemcpy(e, m.d_mk_err, sizeof e, hipMemcpyDeviceToHost));
-    std::string msg = "decode step: a wait for another workgroup's results timed out; reset the KV cache."
-                      " Waits (layer/site, workgroup, element, seen/wanted):";
-    for (uint32_t i = 0; i < std::min(e[1], 15u); ++i) {
-        const uint32_t* r = e + 2 + 4 * i;
-        char b[96];
-        std::snprintf(b, sizeof b, " [%u/0x%02x wg %u el %u %u/%u]", r[0] >> 8, r[0] & 0xFF, r[1], r[2],
-                      r[3] & 0xFFFF, r[3] >> 16);
-        msg += b;
-    }
-    uint32_t tr[64] = {};
-    HIP_TRY(c, hipMemcpy(tr, m.d_mk_err + 64, sizeof tr, hipMemcpyDeviceToHost));
-    msg += " | trace (wg: waves 0-4):";
-    for (int w = 0; w < 8; ++w) {
-        msg += " wg" + std::to_string(w) + ":";
-        for (int v = 0; v < 5; ++v) {
-            char b[16];
-            std::snprintf(b, sizeof b, "%x,", tr[w * 8 + v]);
-            msg += b;
-        }
-    }
-    uint32_t st[2] = {};
-    HIP_TRY(c, hipMemcpy(st, m.d_mk_err + 200, sizeof st, hipMemcpyDeviceToHost));
-    msg += " | workgroups started: " + std::to_string(st[1]) + " at the first timeout, " + std::to_string(st[0]) +
-           " over all launches; grid " + std::to_string(m.mk_blocks);
-    uint32_t gu[32] = {};
-    HIP_TRY(c, hipMemcpy(gu, m.d_mk_err + 128, sizeof gu, hipMemcpyDeviceToHost));
-    msg += " | gu tile-0 started:";
-    for (int i = 0; i < 16; ++i) msg += " " + std::to_string(gu[i] >> 8) + "." + std::to_string(gu[i] & 0xFF);
-    msg += " | ss added:";
-    for (int i = 0; i < 16; ++i) msg += " " + std::to_string(gu[16 + i] >> 8) + "." + std::to_string(gu[16 + i] & 0xFF);
-    return fail(c, QORA_HIP_E_DEVICE, msg);
-}
-
-// QORA_HIP_MK_TRACE: per-phase timeline of the last persistent step on stderr
-// (critical path: the last workgroup to leave a phase, relative to the last
-// workgroup to leave the previous one; and the mean time workgroups spend
-// waiting for a phase's inputs), in microseconds, averaged over the layers.
-void print_mk_trace(qora_hip_ctx* c) {
-    ModelState& m = c->m;
-    if (!m.mk || !m.d_mk_trace) return;
-    const uint32_t np = m.L * 5 + 2, nb = m.mk_blocks;
-    std::vector<unsigned long long> t((size_t)nb * np * 3);
-    if (hipMemcpy(t.data(), m.d_mk_trace, t.size() * 8, hipMemcpyDeviceToHost) != hipSuccess) return;
-    auto at = [&](uint32_t b, uint32_t ph, int k) { return t[((size_t)b * np + ph) * 3 + k]; };
-    unsigned long long t0 = ~0ull;
-    for (uint32_t b = 0; b < nb; ++b) t0 = std::min(t0, at(b, 0, 0));
-    double crit[6] = {}, wait[6] = {};
-    int cnt[6] = {};
-    unsigned long long prev_end = t0;
-    for (uint32_t ph = 1; ph < np; ++ph) {
-        const int kind = ph == np - 1 ? 5 : (int)((ph - 1) % 5);
-        unsigned long long end = 0;
-        double w = 0;
-        for (uint32_t b = 0; b < nb; ++b) {
-            end = std::max(end, at(b, ph, 2));
-            if (at(b, ph, 1)) w += (double)(at(b, ph, 1) - at(b, ph, 0));
-        }
-        if (end == 0) continue;
-        crit[kind] += (double)(end - prev_end) * 0.01;   // 100 MHz clock
-        wait[kind] += w / nb * 0.01;
-        cnt[kind] += 1;
-        prev_end = end;
-    }
-    static const char* names[6] = {"qkv", "attn", "o", "gate_up", "down", "lm_head"};
-    std::fprintf(stderr, "mk trace: total %.1f us;", (double)(prev_end - t0) * 0.01);
-    for (int k = 0; k < 6; ++k)
-        if (cnt[k]) std::fprintf(stderr, " %s %.2f (wait %.2f)", names[k], crit[k] / cnt[k], wait[k] / cnt[k]);
-    std::fprintf(stderr, "\n");
 }
 
 // h_tok[0] while a step's token is outstanding (argmax_finish_kernel stores
@@ -1163,7 +878,7 @@ constexpr int32_t kTokPending = INT32_MIN;
 int finish_step(qora_hip_ctx* c, float* logits, uint32_t* argmax) {
     ModelState& m = c->m;
     const bool mapped = c->d_h_tok != nullptr;   // argmax_finish_kernel stored the token in h_tok
-    if (mapped && c->tok_armed && !logits && !m.mk && !m.mlp) {
+    if (mapped && c->tok_armed && !logits) {
         // Greedy step without logits: the token is read from the mapped word as
         // soon as the device has stored it, without waiting for the stream's
         // completion signal. Stream order keeps the next step's work behind
@@ -1175,6 +890,7 @@ int finish_step(qora_hip_ctx* c, float* logits, uint32_t* argmax) {
         for (uint32_t i = 1;; ++i) {
             const int32_t tok = ht[0];
             if (tok != kTokPending) {
+                if (ht[1] != 0) return range_error(c);
                 m.dev_token = tok;
                 if (argmax) *argmax = (uint32_t)tok;
                 return QORA_HIP_OK;
@@ -1183,12 +899,13 @@ int finish_step(qora_hip_ctx* c, float* logits, uint32_t* argmax) {
         }
     }
     c->tok_armed = false;
-    if (!mapped) HIP_TRY(c, hipMemcpyAsync(&c->h_pin[16], m.d_token, 4, hipMemcpyDeviceToHost, c->stream));
-    if (m.mk) HIP_TRY(c, hipMemcpyAsync(&c->h_pin[24], m.d_mk_err, 4, hipMemcpyDeviceToHost, c->stream));
+    if (!mapped) {
+        HIP_TRY(c, hipMemcpyAsync(&c->h_pin[16], m.d_token, 4, hipMemcpyDeviceToHost, c->stream));
+        HIP_TRY(c, hipMemcpyAsync(&c->h_pin[17], m.d_range, 4, hipMemcpyDeviceToHost, c->stream));
+    }
     if (logits) HIP_TRY(c, hipMemcpyAsync(logits, m.d_logits, (size_t)m.vocab * 4, hipMemcpyDeviceToHost, c->stream));
     HIP_TRY(c, hipStreamSynchronize(c->stream));
-    if (int rc = check_mk_error(c)) return rc;
-    print_mk_trace(c);
+    if ((mapped ? reinterpret_cast<volatile int32_t*>(c->h_tok)[1] : c->h_pin[17]) != 0) return range_error(c);
     const int32_t tok = mapped ? *reinterpret_cast<volatile int32_t*>(c->h_tok) : c->h_pin[16];
     m.dev_token = tok;
     if (argmax) *argmax = (uint32_t)tok;
@@ -1242,9 +959,9 @@ extern "C" int qora_hip_generate_greedy(qora_hip_ctx* c, uint32_t token, uint32_
     for (uint32_t i = 0; i < steps; ++i)
         if (int rc = launch_step(c, true, m.host_pos + i)) return rc;
     HIP_TRY(c, hipMemcpyAsync(out, m.d_gen + m.host_pos, (size_t)steps * 4, hipMemcpyDeviceToHost, c->stream));
-    if (m.mk) HIP_TRY(c, hipMemcpyAsync(&c->h_pin[24], m.d_mk_err, 4, hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(c, hipMemcpyAsync(&c->h_pin[17], m.d_range, 4, hipMemcpyDeviceToHost, c->stream));
     HIP_TRY(c, hipStreamSynchronize(c->stream));
-    if (int rc = check_mk_error(c)) return rc;
+    if (c->h_pin[17] != 0) return range_error(c);
     m.dev_token = out[steps - 1];   // the last step's argmax stays in d_token
     m.host_pos += steps;
     return QORA_HIP_OK;
@@ -1463,6 +1180,7 @@ extern "C" int qora_hip_prefill(qora_hip_ctx* c, const uint32_t* ids, size_t n, 
     if (!c || !ids) return fail(c, QORA_HIP_E_INVALID, "null argument");
     ModelState& m = c->m;
     if (!m.ready) return fail(c, QORA_HIP_E_STATE, "model not initialised");
+    if (c->capturing) return fail(c, QORA_HIP_E_STATE, "decode and prefill steps are not allowed during capture");
     if (n == 0) return fail(c, QORA_HIP_E_INVALID, "empty prompt");
     for (size_t i = 0; i < n; ++i)
         if (ids[i] >= m.vocab) return fail(c, QORA_HIP_E_INVALID, "token id out of range");
@@ -1488,16 +1206,6 @@ extern "C" int qora_hip_prefill(qora_hip_ctx* c, const uint32_t* ids, size_t n, 
     return QORA_HIP_OK;
 }
 
-extern "C" int qora_hip_decode_mode(const qora_hip_ctx* c) {
-    if (!c || !c->m.ready) return 0;
-    return c->m.mk ? 2 : 1;
-}
-
-extern "C" uint32_t qora_hip_mlp_fused(const qora_hip_ctx* c) {
-    if (!c || !c->m.ready) return 0;
-    return c->m.mlp ? 1u : 0u;
-}
-
 extern "C" uint32_t qora_hip_attn_o_limit(const qora_hip_ctx* c) {
     if (!c || !c->m.ready) return 0;
     return c->m.attn_o_max;
@@ -1513,6 +1221,7 @@ extern "C" int qora_hip_kv_len(qora_hip_ctx* c, uint64_t* len) {
 extern "C" int qora_hip_kv_reset(qora_hip_ctx* c) {
     if (!c) return QORA_HIP_E_INVALID;
     if (!c->m.ready) return fail(c, QORA_HIP_E_STATE, "model not initialised");
+    if (c->capturing) return fail(c, QORA_HIP_E_STATE, "kv_reset is not allowed during capture");
     c->m.host_pos = 0;
     return set_device_pos(c, 0);
 }
@@ -1567,6 +1276,7 @@ extern "C" int qora_hip_kv_download(qora_hip_ctx* c, uint32_t layer, float* k, f
     ModelState& m = c->m;
     if (!m.ready) return fail(c, QORA_HIP_E_STATE, "model not initialised");
     if (layer >= m.L) return fail(c, QORA_HIP_E_INVALID, "layer out of range");
+    if (c->capturing) return fail(c, QORA_HIP_E_STATE, "kv_download is not allowed during capture");
     const size_t kvd = (size_t)m.KVH * m.hd;
     const size_t n = (size_t)m.host_pos;
     HIP_TRY(c, hipStreamSynchronize(c->stream));
@@ -2061,14 +1771,21 @@ namespace {
 
 // Penalty list and device scratch for one sampling call, then the kernels;
 // the token and the advanced rng state come back to the host.
-int sample_device(qora_hip_ctx* c, const float* logits, uint64_t vocab, const uint32_t* history, uint64_t n_history,
-                  const qora_sample_params* sp, uint64_t* rng_state, uint32_t* token, hipStream_t s) {
-    if (!logits || !sp || !rng_state || !token || (n_history && !history))
+// Argument checks of a sampling call, made before anything is launched.
+int sample_check(qora_hip_ctx* c, bool have_logits, uint64_t vocab, const uint32_t* history, uint64_t n_history,
+                 const qora_sample_params* sp, const uint64_t* rng_state, const uint32_t* token) {
+    if (!have_logits || !sp || !rng_state || !token || (n_history && !history))
         return fail(c, QORA_HIP_E_INVALID, "null argument");
     if (vocab == 0 || vocab > 0xFFFFFFFFull || !smp_supported((uint32_t)vocab))
         return fail(c, QORA_HIP_E_INVALID, "sampling supports vocab <= 131072");
     if (sp->top_k == 0 || sp->top_k > 64) return fail(c, QORA_HIP_E_INVALID, "top_k must be 1 .. 64");
     if (c->capturing) return fail(c, QORA_HIP_E_STATE, "sampling copies to the host: not allowed during capture");
+    return QORA_HIP_OK;
+}
+
+int sample_device(qora_hip_ctx* c, const float* logits, uint64_t vocab, const uint32_t* history, uint64_t n_history,
+                  const qora_sample_params* sp, uint64_t* rng_state, uint32_t* token, hipStream_t s) {
+    if (int rc = sample_check(c, logits != nullptr, vocab, history, n_history, sp, rng_state, token)) return rc;
     const bool greedy = !(sp->temperature > 0.0f);
     const bool rep = !greedy && sp->repetition_penalty > 1.0f;
     const bool pres = !greedy && sp->presence_penalty > 0.0f;
@@ -2161,13 +1878,19 @@ extern "C" int qora_hip_decode_sample(qora_hip_ctx* c, uint32_t token, const uin
                                       const qora_sample_params* params, uint64_t* rng_state, float* logits,
                                       uint32_t* token_out) {
     if (!c) return QORA_HIP_E_INVALID;
-    if (!params || !rng_state || !token_out) return fail(c, QORA_HIP_E_INVALID, "null argument");
     if (int rc = check_step_room(c, 1)) return rc;
     ModelState& m = c->m;
     if (token >= m.vocab) return fail(c, QORA_HIP_E_INVALID, "token id out of range");
+    // every argument is checked before the step is launched, so a refused call
+    // leaves the cache and the stream as they were
+    if (int rc = sample_check(c, true, m.vocab, history, n_history, params, rng_state, token_out)) return rc;
+    if (force_fail("launch")) return fail(c, QORA_HIP_E_DEVICE, "forced launch failure (QORA_HIP_FORCE_FAIL=launch)");
     if (int rc = put_token(c, token)) return rc;
-    if (int rc = launch_step(c, true, m.host_pos)) return rc;
-    if (logits || m.mk || m.mlp) {
+    if (int rc = launch_step(c, true, m.host_pos)) {
+        (void)hipStreamSynchronize(c->stream);
+        return rc;
+    }
+    if (logits) {
         uint32_t greedy = 0;
         if (int rc = finish_step(c, logits, &greedy)) return rc;
     } else {
@@ -2176,7 +1899,13 @@ extern "C" int qora_hip_decode_sample(qora_hip_ctx* c, uint32_t token, const uin
         m.dev_token = -1;
     }
     m.host_pos += 1;
-    return sample_device(c, m.d_logits, m.vocab, history, n_history, params, rng_state, token_out, c->stream);
+    const int rc = sample_device(c, m.d_logits, m.vocab, history, n_history, params, rng_state, token_out, c->stream);
+    if (rc) {
+        // nothing of this call stays in flight behind an error
+        (void)hipStreamSynchronize(c->stream);
+        m.dev_token = -1;
+    }
+    return rc;
 }
 
 extern "C" int qora_hip_argmax(qora_hip_ctx* c, const float* logits, uint64_t n, int32_t* out, void* stream) {

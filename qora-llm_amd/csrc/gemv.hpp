@@ -39,8 +39,12 @@
 
 namespace qora {
 
-__device__ __forceinline__ void fixed_add(long long* p, float v) {
-    atomicAdd(reinterpret_cast<unsigned long long*>(p), (unsigned long long)to_fixed(v));
+// acc += v in fixed point; a contribution of 2^20 or more (or NaN) sets *flag
+// instead of wrapping the accumulator.
+__device__ __forceinline__ void fixed_add(long long* p, float v, int* flag) {
+    const bool ok = fabsf(v) < 1048576.0f;
+    fix_flag(flag, !ok);
+    atomicAdd(reinterpret_cast<unsigned long long*>(p), (unsigned long long)(ok ? to_fixed(v) : 0LL));
 }
 
 __device__ __forceinline__ float silu_mul(float g, float u) {
@@ -284,6 +288,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
         for (int j = 0; j < RPL; ++j) {
             const bool ok = k0 + rl + j * RL < k1;
             const float xf = ok ? from_fixed(xa[j]) : 0.f;
+            fix_flag(p.range_flag, ok && fix_out_of_range(xa[j], kFixReadLimit));
             ssq += xf * xf;
             xv[j] = xf * h2f((uint16_t)gm[j]);
         }
@@ -398,7 +403,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
             lim = sg.groups * 32u;
             col0 = sg.col0;
         }
-        if (local < lim) fixed_add(p.acc + col0 + local, s);
+        if (local < lim) fixed_add(p.acc + col0 + local, s, p.range_flag);
     }
 }
 
@@ -454,6 +459,7 @@ __global__ __launch_bounds__(256) void rowdot_kernel(RowdotParams p) {
 #pragma unroll
         for (int c = 0; c < 16; ++c) {
             const longlong2 v = src[c];
+            fix_flag(p.range_flag, fix_out_of_range(v.x, kFixReadLimit) || fix_out_of_range(v.y, kFixReadLimit));
             xr[2 * c] = from_fixed(v.x);
             xr[2 * c + 1] = from_fixed(v.y);
         }
@@ -608,9 +614,11 @@ __global__ __launch_bounds__(256) void argmax_finish_kernel(ArgmaxFinishParams p
             *p.pos = ps + 1;
         }
         if (p.host_token) {
+            // the range flag of the step's fixed-point values, then the token
             // last, after the step's other stores are visible: a host that
             // reads the token without waiting for the kernel's end finds
             // every result of the step in place
+            if (p.range_flag) p.host_token[1] = *p.range_flag;
             __threadfence_system();
             *p.host_token = tok;
         }

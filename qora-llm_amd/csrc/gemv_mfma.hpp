@@ -330,7 +330,11 @@ __device__ __forceinline__ void gemv_q4m_item(const GemvParams& p, uint32_t tile
                     hi = (long long)c[2] + ((long long)c[3] << 8);
                 }
                 const long long Y = lo + (hi << 16);
-                const long long f = ((Y + rnd) >> rsh) << lsh;
+                // contributions of 2^20 or more flag the range instead of wrapping
+                const long long ay = Y < 0 ? -Y : Y;
+                const bool big = lsh >= 56 ? ay != 0 : ((ay + rnd) >> rsh) >= (kFixAddLimit >> lsh);
+                fix_flag(p.range_flag, big);
+                const long long f = big ? 0 : ((Y + rnd) >> rsh) << lsh;
                 atomicAdd(reinterpret_cast<unsigned long long*>(dst + h * 16), (unsigned long long)f);
             }
         }
@@ -358,32 +362,10 @@ struct GemvQ4mSmem {
     float aw[PRO == PRO_ATTN ? NPW * kAttnMaxSplits * MAXH : 1];
 };
 
-// Waits of a prologue wave (fused MLP step) before it reads its input rows:
-// until *ctr >= target, at most kGemvWaitSpins polls; past that it stores 1
-// to *err and goes on (the host reports the failure). The polls and the input
-// reads that follow are agent-scope atomic loads, which read past this XCD's
-// L2 without invalidating it (an acquire would invalidate the L2 on every
-// poll and stall the other XCD traffic); the producers' sums are atomics
-// and their norm sums atomic stores, all complete before the count rises.
-constexpr uint32_t kGemvWaitSpins = 1u << 20;
-
-__device__ __forceinline__ long long ld_agent(const long long* p) {
-    return __hip_atomic_load(const_cast<long long*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float ld_agent(const float* p) {
-    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-struct GemvWait {
-    uint32_t* ctr;
-    uint32_t target;
-    int32_t* err;
-};
-
 // The body of gemv_q4m_kernel for workgroup `block` of `nblocks`.
 template <int GW, int KW, int PRO, int IPW>
 __device__ __forceinline__ void gemv_q4m_body(const GemvParams& p, uint32_t block, uint32_t nblocks,
-                                              GemvQ4mSmem<GW, KW, PRO, IPW>& sm, const GemvWait* wait) {
+                                              GemvQ4mSmem<GW, KW, PRO, IPW>& sm) {
     constexpr int NW = 4;                    // matrix-core waves
     constexpr int NPW = PRO == PRO_ATTN ? 4 : 1;   // prologue waves (the attention merge gets four)
     constexpr int NT = (NW + NPW) * kWave;
@@ -416,17 +398,6 @@ __device__ __forceinline__ void gemv_q4m_body(const GemvParams& p, uint32_t bloc
     int esg[IPW][GW];
     if (wave >= NW) {
         // ---- prologue wave(s): rows [k0, k1) of the input into xs, max |x|, sum x^2 ----
-        if (wait) {
-            for (uint32_t spins = 0;; ++spins) {
-                if (__hip_atomic_load(wait->ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= wait->target) break;
-                if (spins >= kGemvWaitSpins) {
-                    if (lane == 0) *wait->err = 1;
-                    break;
-                }
-                __builtin_amdgcn_s_sleep(8);
-            }
-            asm volatile("" ::: "memory");   // the input reads stay below the wait
-        }
         // Raised issue priority: their few input loads enter the CU's memory
         // queue ahead of the weight streams of the other waves on the CU.
         __builtin_amdgcn_s_setprio(3);
@@ -461,13 +432,13 @@ __device__ __forceinline__ void gemv_q4m_body(const GemvParams& p, uint32_t bloc
                         gm[r] = p.gamma[rc];
                     }
                     if constexpr (PRO == PRO_SILU_FIXED) {
-                        xa[r] = wait ? ld_agent(p.xacc + rc) : p.xacc[rc];
-                        xb[r] = wait ? ld_agent(p.xacc + p.k + rc) : p.xacc[p.k + rc];
+                        xa[r] = p.xacc[rc];
+                        xb[r] = p.xacc[p.k + rc];
                     }
                 }
                 if constexpr (PRO == PRO_SILU_FIXED) {
                     const float* sp = p.ss_in + min((uint32_t)lane, p.ss_n - 1u);
-                    ssp = wait ? ld_agent(sp) : *sp;
+                    ssp = *sp;
                 }
                 float inv = 1.f;
                 if constexpr (PRO == PRO_SILU_FIXED)
@@ -480,6 +451,7 @@ __device__ __forceinline__ void gemv_q4m_body(const GemvParams& p, uint32_t bloc
                         x = ok ? xp[r] : 0.f;
                     } else if constexpr (PRO == PRO_GAMMA_FIXED) {
                         const float xf = ok ? from_fixed(xa[r]) : 0.f;
+                        fix_flag(p.range_flag, ok && fix_out_of_range(xa[r], kFixReadLimit));
                         ss += xf * xf;
                         x = xf * h2f(gm[r]);
                     } else {
@@ -518,7 +490,6 @@ __device__ __forceinline__ void gemv_q4m_body(const GemvParams& p, uint32_t bloc
 #pragma unroll
         for (int w = 1; w < NPW; ++w) xm = fmaxf(xm, wred[j][0][w]);
         if constexpr (PRO == PRO_GAMMA_FIXED) {
-            // an atomic store: a fused down launch reads it past this XCD's L2
             if (t == 0 && tile == 0)
                 __hip_atomic_store(p.ss_out + split, wred[j][1][0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
@@ -532,50 +503,7 @@ template <int GW, int KW, int PRO, int IPW = 1>
 __global__ __launch_bounds__(PRO == PRO_ATTN ? 512 : 320) void gemv_q4m_kernel(GemvParams p) {
     kernarg_warm(p);
     __shared__ GemvQ4mSmem<GW, KW, PRO, IPW> sm;
-    gemv_q4m_body<GW, KW, PRO, IPW>(p, blockIdx.x, gridDim.x, sm, nullptr);
-}
-
-// Fused MLP step: the gate|up GEMV (workgroups [0, gu_grid)) and the down GEMV
-// (the rest) in one launch. A gate|up workgroup whose accumulator atomics are
-// all acknowledged adds 1 to its group's counter (32 counters 128 bytes apart:
-// on one address ~1400 arrivals serialise, 4.7 ms a step); the last of a group
-// adds 1 to done[0]. The down workgroups' prologue waves poll done[0] (polling
-// all 32 counters costs more) before reading the gate|up sums, while their
-// matrix-core waves already stream the down weights. Opt-in: slower than the
-// two launches on MI355X (1.066 against 0.987 ms a decode step).
-// Workgroups are dispatched in index order, so every gate|up workgroup has
-// been placed on a CU before any down workgroup waits: the waits always end.
-constexpr uint32_t kMlpGroups = 32;        // arrival groups of gate|up workgroups
-constexpr uint32_t kMlpGroupStride = 32;   // words between counters (128 bytes)
-
-template <int GW, int KW>
-__global__ __launch_bounds__(320) void gemv_q4m_mlp_kernel(GemvMlpParams mp) {
-    __shared__ GemvQ4mSmem<GW, KW, PRO_GAMMA_FIXED, 1> sm;
-    static_assert(sizeof(GemvQ4mSmem<GW, KW, PRO_GAMMA_FIXED, 1>) == sizeof(GemvQ4mSmem<GW, KW, PRO_SILU_FIXED, 1>),
-                  "both bodies use the same LDS layout");
-    if (blockIdx.x < mp.gu_grid) {
-        kernarg_warm(mp.gu);
-        gemv_q4m_body<GW, KW, PRO_GAMMA_FIXED, 1>(mp.gu, blockIdx.x, mp.gu_grid, sm, nullptr);
-        if (threadIdx.x >= 4 * kWave) return;
-        // every wave's accumulator atomics (and norm-sum store) acknowledged first
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            // group counters (one 128-byte line each) spread the arrivals; the
-            // last of a group raises the count the down workgroups wait on
-            const uint32_t g = blockIdx.x % kMlpGroups;
-            const uint32_t size = mp.gu_grid / kMlpGroups + (g < mp.gu_grid % kMlpGroups ? 1u : 0u);
-            const uint32_t old =
-                __hip_atomic_fetch_add(mp.done + kMlpGroupStride * (1 + g), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if (old + 1u == size) __hip_atomic_fetch_add(mp.done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-    } else {
-        kernarg_warm(mp.dn);
-        const GemvWait w{mp.done, min(mp.gu_grid, kMlpGroups), mp.err};
-        gemv_q4m_body<GW, KW, PRO_SILU_FIXED, 1>(
-            mp.dn, blockIdx.x - mp.gu_grid, gridDim.x - mp.gu_grid,
-            reinterpret_cast<GemvQ4mSmem<GW, KW, PRO_SILU_FIXED, 1>&>(sm), &w);
-    }
+    gemv_q4m_body<GW, KW, PRO, IPW>(p, blockIdx.x, gridDim.x, sm);
 }
 
 }  // namespace qora

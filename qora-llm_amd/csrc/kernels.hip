@@ -3,7 +3,6 @@
 #include "gemv.hpp"
 #include "gemv_mfma.hpp"
 #include "lmhead_mfma.hpp"
-#include "decode_mk.hpp"
 #include "attn.hpp"
 #include "attn_o.hpp"
 #include "prefill.hpp"
@@ -223,19 +222,6 @@ static hipError_t launch_q4m_gw(const GemvPlan& plan, const GemvParams& p, hipSt
     }
 }
 
-bool gemv_mlp_supported(const GemvPlan& gu, const GemvPlan& dn) {
-    return gu.mfma && dn.mfma && gu.gw == 1 && dn.gw == 1 && gu.ipw == 1 && dn.ipw == 1 && gu.kr == 256 &&
-           dn.kr == 256 && gu.blocks() > 0 && dn.blocks() > 0;
-}
-
-hipError_t launch_gemv_mlp(const GemvPlan& gu, const GemvPlan& dn, const GemvMlpParams& p, hipStream_t stream) {
-    if (!gemv_mlp_supported(gu, dn) || p.gu_grid != gu.grid() || !p.done || !p.err ||
-        p.gu.pro != PRO_GAMMA_FIXED || p.dn.pro != PRO_SILU_FIXED || !p.gu.tw || !p.dn.tw)
-        return hipErrorInvalidValue;
-    hipLaunchKernelGGL((gemv_q4m_mlp_kernel<1, 256>), dim3(gu.grid() + dn.grid()), dim3(320), 0, stream, p);
-    return hipGetLastError();
-}
-
 hipError_t launch_gemv(int fmt, const GemvPlan& plan, const GemvParams& p, hipStream_t stream) {
     if (plan.blocks() == 0) return hipErrorInvalidValue;
     if (plan.mfma) {
@@ -389,37 +375,6 @@ hipError_t launch_lmhead(uint32_t blocks, const LmHeadParams& p, hipStream_t str
     }
 #undef QORA_LM_CASE
     return hipGetLastError();
-}
-
-// Instances of the persistent decode step: (hidden, head_dim) of SmolLM3-3B
-// (2048, 128) and of the small test models (256, 64), f32 or f16 KV cache.
-static const void* decode_mk_fn(uint32_t hidden, uint32_t hd, int kv_f16) {
-    if (hidden == 2048 && hd == 128)
-        return kv_f16 ? (const void*)decode_mk_kernel<32, 2, true> : (const void*)decode_mk_kernel<32, 2, false>;
-    if (hidden == 256 && hd == 64)
-        return kv_f16 ? (const void*)decode_mk_kernel<4, 1, true> : (const void*)decode_mk_kernel<4, 1, false>;
-    return nullptr;
-}
-
-bool decode_mk_supported(uint32_t hidden, uint32_t hd) {
-    return decode_mk_fn(hidden, hd, 0) != nullptr;
-}
-
-int decode_mk_blocks_per_cu(uint32_t hidden, uint32_t hd, int kv_f16) {
-    const void* fn = decode_mk_fn(hidden, hd, kv_f16);
-    int occ = 0;
-    if (!fn || hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, kMkNT, 0) != hipSuccess) return 0;
-    return occ;
-}
-
-hipError_t launch_decode_mk(const MkParams& host, const MkParams* dev, uint32_t blocks, hipStream_t stream) {
-    const void* fn = decode_mk_fn(host.hidden, host.hd, host.kv_f16);
-    if (!fn || !dev || blocks == 0) return hipErrorInvalidValue;
-    const MkParams* arg = dev;
-    void* args[] = {&arg};
-    if (env_int("QORA_HIP_MK_COOP", 1))
-        return hipLaunchCooperativeKernel(fn, dim3(blocks), dim3(kMkNT), args, 0, stream);
-    return hipLaunchKernel(fn, dim3(blocks), dim3(kMkNT), args, 0, stream);
 }
 
 hipError_t launch_argmax_finish(const ArgmaxFinishParams& p, hipStream_t stream) {

@@ -34,7 +34,7 @@ bool plan_gemv(int fmt, uint32_t k, const uint32_t* seg_groups, int nseg, bool p
 // or 4) and the deepest K slice of 256, 128 or 64 rows (QORA_GEMV_KW may
 // force one) that gives every CU a workgroup.
 // force_kw (256, 128 or 64): that K slice and one group per wave, whatever the
-// environment says (the persistent decode step needs kMkKW).
+// environment says.
 bool plan_gemv_q4m(uint32_t k, const uint32_t* seg_groups, int nseg, bool paired, int cus, GemvPlan* plan,
                    uint32_t row_align = 1, uint32_t force_kw = 0);
 
@@ -46,10 +46,6 @@ void apply_plan(const GemvPlan& plan, GemvParams* p);
 // p.tw == nullptr: reference layout, plain prologue only (kernel-level
 // entry points). Otherwise the tile layout written by launch_gemv_tile.
 hipError_t launch_gemv(int fmt, const GemvPlan& plan, const GemvParams& p, hipStream_t stream);
-// Fused gate|up + down launch: both plans on the matrix cores with one group
-// per wave, 256-row K slices and one item per workgroup.
-bool gemv_mlp_supported(const GemvPlan& gu, const GemvPlan& dn);
-hipError_t launch_gemv_mlp(const GemvPlan& gu, const GemvPlan& dn, const GemvMlpParams& p, hipStream_t stream);
 // Size of the tile layout of a planned GEMV (scales, exponent bounds: Q4 only).
 void gemv_tile_bytes(int fmt, const GemvPlan& plan, uint64_t* w_bytes, uint64_t* s_bytes, uint64_t* e_bytes);
 // Writes the tile layout of the reference-layout segments of p (after
@@ -75,12 +71,6 @@ void lmhead_tile_bytes(uint32_t rows, uint32_t cols, uint64_t* w_bytes, uint64_t
 hipError_t launch_lmhead_pack(const uint8_t* w, const uint16_t* scales, uint32_t rows, uint32_t cols, uint8_t* tw,
                               uint32_t* ts, hipStream_t stream);
 hipError_t launch_lmhead(uint32_t blocks, const LmHeadParams& p, hipStream_t stream);
-
-// Persistent decode step (one cooperative launch per token).
-bool decode_mk_supported(uint32_t hidden, uint32_t hd);
-int decode_mk_blocks_per_cu(uint32_t hidden, uint32_t hd, int kv_f16);
-// host: the parameters (for dispatch); dev: the same struct in device memory.
-hipError_t launch_decode_mk(const MkParams& host, const MkParams* dev, uint32_t blocks, hipStream_t stream);
 
 // Attention split geometry for up to `positions` positions: chunk is a
 // multiple of kAttnSub and s_max = ceil(positions / chunk) <= kAttnMaxSplits.

@@ -161,8 +161,12 @@ __global__ __launch_bounds__(256) void lmhead_q4m_kernel(LmHeadParams p) {
     for (int j = 0; j < XPT; ++j) {
         const bool ok = t + NT * j < COLS;
         float v = 0.f;
-        if constexpr (FIXED) v = ok ? from_fixed(xa[j]) : 0.f;
-        else v = ok ? xf[j] : 0.f;
+        if constexpr (FIXED) {
+            v = ok ? from_fixed(xa[j]) : 0.f;
+            fix_flag(p.range_flag, ok && fix_out_of_range(xa[j], kFixReadLimit));
+        } else {
+            v = ok ? xf[j] : 0.f;
+        }
         xv[j] = v;
         ss += v * v;
     }

@@ -21,8 +21,16 @@ enum Pro : int {
 
 // Fixed-point accumulators: value = int64 / 2^36. Integer adds are exact and
 // associative, so the split-K sums are identical whatever order the
-// workgroups finish in. Range |v| < 1.3e8, resolution 1.5e-11.
+// workgroups finish in. Resolution 1.5e-11. Range guard: a value read from
+// the residual must be below 2^25 in magnitude (|int| < 2^61) and a single
+// added contribution below 2^20 (|int| < 2^56); an accumulator takes at most
+// kFixMaxTerms contributions between two reads, so a value in range when read
+// cannot wrap before the next read. Kernels given a range_flag set it when a
+// value breaks either bound; the host reports QORA_HIP_E_RANGE.
 constexpr double kFixScale = 68719476736.0;   // 2^36
+constexpr long long kFixReadLimit = 1LL << 61;
+constexpr long long kFixAddLimit = 1LL << 56;
+constexpr uint32_t kFixMaxTerms = 64;
 
 struct GemvSeg {
     const uint8_t* w;         // Q4 packed bytes or F16 words (as bytes), reference layout
@@ -66,6 +74,7 @@ struct GemvParams {
     // Q4 on the matrix cores (gemv_q4m_kernel): per (workgroup, wave, group)
     // exponent bound of the K slice's scales, max |s| <= 2^tes.
     const int8_t* tes;
+    int* range_flag;          // optional: set when a fixed-point value leaves its range
 };
 
 struct RowdotParams {
@@ -79,6 +88,7 @@ struct RowdotParams {
     int do_argmax;
     float* part_val;           // [gridDim.x] per-workgroup best logit
     uint32_t* part_idx;
+    int* range_flag;           // optional: set when an xacc value leaves its range
 };
 
 // Row-dot Q4 GEMV on the matrix cores (lmhead_q4m_kernel): the tied lm_head,
@@ -99,59 +109,7 @@ struct LmHeadParams {
     int do_argmax;
     float* part_val;           // [gridDim.x] per-workgroup best logit
     uint32_t* part_idx;
-};
-
-// Persistent decode step (decode_mk_kernel, opt-in): every GEMV uses K slices of
-// kMkKW rows and one 32-column group per wave; a workgroup takes at most
-// kMkSlots items of a GEMV (a contiguous range of the split-major item order).
-constexpr int kMkKW = 256;
-constexpr int kMkSlots = 6;
-
-enum MkGemv : int { MK_QKV = 0, MK_O = 1, MK_GU = 2, MK_DOWN = 3 };
-
-struct MkLayer {
-    const uint8_t* tw[4];
-    const uint16_t* ts[4];
-    const int8_t* te[4];
-    const uint16_t* gamma[2];   // input norm, post-attention norm
-    uint8_t* kc;                // this layer's K cache [cap][KVH][hd]
-    uint8_t* vc;
-    int use_rope;
-    int pad_;
-};
-
-struct MkBufs {
-    long long* R;    // [nl + 1][hidden] residual entering layer l (R[nl]: final)
-    long long* Q;    // [nl][qkv_n]
-    long long* RP;   // [nl][hidden] residual after attention
-    long long* U;    // [nl][2 inter]
-    long long* SS;   // [nl][2] sums of squares of R[l] and RP[l]
-    uint32_t* A;     // [nl][KVH] attention items done
-};
-
-struct MkParams {
-    GemvParams g[4];           // shapes of the four GEMVs (K slice kMkKW, one group per wave)
-    const MkLayer* layers;
-    uint32_t nl, hidden, inter, H, KVH, hd, G, half, vocab;
-    uint32_t chunk, s_max;     // attention split geometry
-    int kv_f16;
-    const float* rope_cos;
-    const float* rope_sin;
-    float* part;               // attention partials [KVH][s_max][G][hd + 2]
-    MkBufs buf[2];
-    void* clear_base[2];       // each parity's buffers, one region (16-byte aligned)
-    uint64_t clear_n;          // 16-byte words per region
-    const int32_t* pos;
-    const int32_t* token;      // decode: the token of this step
-    const int32_t* prompt;     // prefill: prompt[pos]
-    const uint8_t* emb_w;      // reference-layout embedding (row lookup)
-    const uint16_t* emb_s;
-    int with_lm;
-    int residency_test;        // set-up check: count resident workgroups and exit
-    unsigned long long* trace; // optional: [workgroup][phase][3] clock stamps (enter, inputs ready, done)
-    LmHeadParams lm;           // tw, ts, rows, cols, tiles, gamma, y, part_val, part_idx
-    uint32_t* err;
-    uint64_t kv_ps, kv_hs;     // cache addressing as in AttnParams
+    int* range_flag;           // optional: set when an xacc value leaves its range
 };
 
 
@@ -246,6 +204,7 @@ struct ArgmaxFinishParams {
     int32_t* pos;              // if non-null: gen[pos] = token, pos += 1
     int32_t* gen;
     int32_t* host_token;       // optional: the token also stored here (mapped host memory, read after a sync)
+    const int* range_flag;     // optional: copied to host_token[1] before the token is stored
 };
 
 constexpr int kAttnSub = 32;         // positions staged in LDS at a time
@@ -277,18 +236,6 @@ struct AttnParams {
     // cache addressing: element (pos, kvh, d) at pos * kv_ps + kvh * kv_hs + d;
     // kv_ps = 0: token-major [pos][KVH][hd] (kv_ps = KVH hd, kv_hs = hd)
     uint64_t kv_ps, kv_hs;
-};
-
-// Fused gate|up + down launch (gemv_q4m_mlp_kernel). done[0]: the count the
-// down workgroups wait on; done[32 (1 + g)], g < 32: the group counters, 128
-// bytes apart. All zeroed before the launch (the q|k|v GEMV clears them with
-// the gate|up sums). err: set to 1 if a wait gave up.
-struct GemvMlpParams {
-    GemvParams gu;
-    GemvParams dn;
-    uint32_t gu_grid;
-    uint32_t* done;
-    int32_t* err;
 };
 
 // o projection with the attention of its query head computed in the

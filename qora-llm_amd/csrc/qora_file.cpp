@@ -13,6 +13,7 @@
 #include "../../include/qora_hip.h"
 
 #include <cstdio>
+#include <new>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -22,21 +23,33 @@ namespace {
 struct Reader {
     FILE* f = nullptr;
     bool ok = true;
-    explicit Reader(const char* path) : f(std::fopen(path, "rb")) { ok = f != nullptr; }
+    uint64_t left = 0;   // bytes not yet read
+    explicit Reader(const char* path) : f(std::fopen(path, "rb")) {
+        ok = f != nullptr;
+        if (ok && std::fseek(f, 0, SEEK_END) == 0) {
+            const long end = std::ftell(f);
+            ok = end >= 0 && std::fseek(f, 0, SEEK_SET) == 0;
+            left = ok ? (uint64_t)end : 0;
+        } else {
+            ok = false;
+        }
+    }
     ~Reader() { if (f) std::fclose(f); }
     bool bytes(void* dst, size_t n) {
         if (!ok) return false;
-        if (n && std::fread(dst, 1, n, f) != n) ok = false;
+        if (n > left || (n && std::fread(dst, 1, n, f) != n)) ok = false;
+        else left -= n;
         return ok;
     }
     uint32_t u32() { uint8_t b[4] = {0}; bytes(b, 4); return (uint32_t)b[0] | (uint32_t)b[1] << 8 | (uint32_t)b[2] << 16 | (uint32_t)b[3] << 24; }
     uint64_t u64() { const uint64_t lo = u32(); const uint64_t hi = u32(); return lo | hi << 32; }
     uint8_t u8() { uint8_t b = 0; bytes(&b, 1); return b; }
-    // length-prefixed vector of `elem`-byte items, bounded by `max_len`
+    // length-prefixed vector of `elem`-byte items, bounded by `max_len` and by
+    // the bytes left in the file (a corrupt length fails before any allocation)
     template <class T>
     bool vec(std::vector<T>& out, uint64_t max_len) {
         const uint64_t len = u64();
-        if (!ok || len > max_len) { ok = false; return false; }
+        if (!ok || len > max_len || len > left / sizeof(T)) { ok = false; return false; }
         out.resize(len);
         return bytes(out.data(), len * sizeof(T));
     }
@@ -71,10 +84,18 @@ int read_weight(qora_hip_ctx* ctx, Reader& r, uint8_t fmt, uint64_t* k, uint64_t
     return qora_hip_upload_q4(ctx, p.data(), p.size(), s.data(), s.size(), *k, *n, wid);
 }
 
-}  // namespace
+// Uploads of one load, released again if the load fails.
+struct Uploads {
+    qora_hip_ctx* ctx;
+    std::vector<uint32_t> wids;
+    bool keep = false;
+    ~Uploads() {
+        if (!keep)
+            for (uint32_t w : wids) (void)qora_hip_release_weight(ctx, w);
+    }
+};
 
-extern "C" int qora_hip_load_model(qora_hip_ctx* ctx, const char* path, uint32_t kv_capacity, uint32_t kv_dtype) {
-    if (!ctx || !path) return QORA_HIP_E_INVALID;
+int load_model(qora_hip_ctx* ctx, const char* path, uint32_t kv_capacity, uint32_t kv_dtype, Uploads& up) {
     Reader r(path);
     if (!r.ok) return QORA_HIP_E_IO;
     char magic[4];
@@ -97,6 +118,7 @@ extern "C" int qora_hip_load_model(qora_hip_ctx* ctx, const char* path, uint32_t
         for (int j = 0; j < 7; ++j) {
             uint64_t k, n;
             if (int rc = read_weight(ctx, r, fmt, &k, &n, &wids[(size_t)l * 7 + j])) return rc;
+            up.wids.push_back(wids[(size_t)l * 7 + j]);
             if (j == 4) inter = n;
         }
         if (!r.vec(in_norm[l], kMaxElems) || !r.vec(post_norm[l], kMaxElems)) return QORA_HIP_E_IO;
@@ -109,6 +131,7 @@ extern "C" int qora_hip_load_model(qora_hip_ctx* ctx, const char* path, uint32_t
     uint64_t ek, en;
     uint32_t embed_wid;
     if (int rc = read_weight(ctx, r, fmt, &ek, &en, &embed_wid)) return rc;
+    up.wids.push_back(embed_wid);
     std::vector<uint16_t> final_norm;
     std::vector<float> cos_t, sin_t;
     if (!r.vec(final_norm, kMaxElems) || !r.vec(cos_t, kMaxElems) || !r.vec(sin_t, kMaxElems)) return QORA_HIP_E_IO;
@@ -138,7 +161,24 @@ extern "C" int qora_hip_load_model(qora_hip_ctx* ctx, const char* path, uint32_t
     d.use_rope = flags.data();
     d.kv_capacity = kv_capacity;
     d.kv_dtype = kv_dtype;
-    return qora_hip_model_init(ctx, &d);
+    const int rc = qora_hip_model_init(ctx, &d);
+    up.keep = rc == QORA_HIP_OK;
+    return rc;
+}
+
+}  // namespace
+
+extern "C" int qora_hip_load_model(qora_hip_ctx* ctx, const char* path, uint32_t kv_capacity, uint32_t kv_dtype) {
+    if (!ctx || !path) return QORA_HIP_E_INVALID;
+    // no exception crosses the C ABI (a Rust caller would abort)
+    try {
+        Uploads up{ctx, {}, false};
+        return load_model(ctx, path, kv_capacity, kv_dtype, up);
+    } catch (const std::bad_alloc&) {
+        return QORA_HIP_E_NOMEM;
+    } catch (...) {
+        return QORA_HIP_E_IO;
+    }
 }
 
 extern "C" int qora_file_write(const char* path, const qora_host_model* m) {

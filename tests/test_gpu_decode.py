@@ -245,3 +245,84 @@ def test_state_calls_right_after_a_logits_free_step(ctx, pkg, orc):
         om2.forward_decode(int(t))
     kr, _ = om2.kv_layer(2)
     assert rel_err(k, kr) <= REL_TOL
+
+
+def test_model_reinit_right_after_a_logits_free_step(ctx, pkg, orc):
+    """model_init right after a greedy step that returned without waiting for
+    the stream: the old graphs and buffers are released only after the step
+    has finished, and the new model runs correctly."""
+    print("case model re-init after a logits-free step", flush=True)
+    w = small_model(pkg, 1, layers=4, seed=10)
+    be = pkg.HipBackend(ctx, w, kv_capacity=128)
+    prompt = pkg.synth_tokens(10, 2100, 12, w.config.vocab)
+    _, tok = be.raw_prefill(prompt, want_logits=False)
+    for _ in range(3):
+        _, tok = be.forward_decode_raw(int(tok), want_logits=False)
+    w2 = small_model(pkg, 1, layers=4, seed=11)
+    be2 = pkg.HipBackend(ctx, w2, kv_capacity=128)
+    om = orc.OracleModel(w2, kv_capacity=128, T=4)
+    ref, _ = om.greedy(prompt, 5)
+    got = pkg.generate_greedy_host(be2, prompt, 5)
+    assert got == ref
+
+
+def test_steps_refused_during_capture(ctx, pkg):
+    """Decode, prefill and state calls read results back to the host: during a
+    caller's stream capture they are refused (E_STATE) and the capture stays
+    usable."""
+    print("case steps refused during capture", flush=True)
+    w = small_model(pkg, 1, layers=2, seed=12)
+    be = pkg.HipBackend(ctx, w, kv_capacity=64)
+    prompt = pkg.synth_tokens(12, 2100, 5, w.config.vocab)
+    _, tok = be.raw_prefill(prompt, want_logits=False)
+    n0 = be.kv_len()
+    out = ctypes.c_uint32()
+    ids = np.asarray(prompt, dtype=np.uint32)
+    ctx.capture_begin()
+    try:
+        assert ctx.lib.qora_hip_decode(ctx.h, int(tok), None, ctypes.byref(out)) == -4
+        assert ctx.lib.qora_hip_prefill(ctx.h, ids.ctypes.data, ids.size, None, ctypes.byref(out)) == -4
+        assert ctx.lib.qora_hip_kv_reset(ctx.h) == -4
+    finally:
+        g = ctx.capture_end()
+        ctx.graph_destroy(g)
+    assert be.kv_len() == n0
+    _, nxt = be.forward_decode_raw(int(tok), want_logits=False)
+    assert be.kv_len() == n0 + 1
+
+
+@pytest.mark.parametrize("fmt", [1, 0])
+def test_fixed_point_range_overflow_is_reported(ctx, pkg, fmt):
+    """A down projection whose terms reach 2^20 would wrap the int64
+    residual: the step returns QORA_HIP_E_RANGE instead of logits, and steps
+    stay refused until the cache is reset."""
+    print(f"case fixed-point range fmt={fmt}", flush=True)
+    w = small_model(pkg, fmt, layers=2, seed=13)
+    gate, up, down = w.layers[0][4:7]
+    # gate == up, scaled by 100: every SwiGLU value silu(g) g = g^2 sigmoid(g)
+    # is >= 0 and about half are ~1e3; down terms of 60000 then put each K
+    # slice's sum far beyond 2^20, whatever the token
+    if fmt == 1:
+        gate.scales = (gate.scales.view(np.float16).astype(np.float32) * 100).astype(np.float16).view(np.uint16)
+        up.packed, up.scales = gate.packed.copy(), gate.scales.copy()
+        down.scales = np.full_like(down.scales, 0x7B53)          # 60000
+    else:
+        gate.data = (gate.data.view(np.float16).astype(np.float32) * 100).astype(np.float16).view(np.uint16)
+        up.data = gate.data.copy()
+        down.data = np.full_like(down.data, 0x7B53)
+    prompt = pkg.synth_tokens(13, 2100, 6, w.config.vocab)
+    be = pkg.HipBackend(ctx, w, kv_capacity=64)
+    be.raw_prefill(prompt, want_logits=False)                      # batched prefill: fp32, unguarded
+    for want in (True, False, True):
+        with pytest.raises(pkg.QoraHipError) as e:
+            be.forward_decode_raw(3, want_logits=want)
+        assert e.value.code == pkg.QORA_HIP_E_RANGE
+    be.kv_reset()
+    with pytest.raises(pkg.QoraHipError) as e:
+        be.generate_greedy(3, 4)
+    assert e.value.code == pkg.QORA_HIP_E_RANGE
+    # the same weights with the terms in range decode normally
+    w2 = small_model(pkg, fmt, layers=2, seed=13)
+    be2 = pkg.HipBackend(ctx, w2, kv_capacity=64)
+    be2.raw_prefill(prompt, want_logits=False)
+    be2.forward_decode_raw(3, want_logits=False)

@@ -1,6 +1,8 @@
 """On-device sampling (qora_hip_sample, qora_hip_decode_sample) against the
 oracle's restatement of generate.rs:38-91, 345-395 on the same logits: the
 same token and the same Rng state, draw for draw."""
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -90,3 +92,62 @@ def test_decode_sample_matches_decode_plus_oracle_sampling(ctx, pkg, orc):
         hist.append(nxt)
         st = st_new
     assert be.kv_len() == len(prompt) + 24
+
+
+def test_decode_sample_refused_call_launches_nothing(ctx, pkg, orc):
+    """decode_sample refused for its arguments (no sampling parameters) checks
+    them before the step is launched: the cache length is unchanged, and the
+    greedy steps that follow match the oracle."""
+    print("case refused decode_sample", flush=True)
+    cfg = entry.smoke_config(pkg)
+    w = pkg.synthetic_model(cfg, seed=6, rope_positions=64)
+    prompt = pkg.synth_tokens(6, 2000, 7, cfg.vocab)
+    be = pkg.HipBackend(ctx, w, kv_capacity=64)
+    om = orc.OracleModel(w, kv_capacity=64, T=4)
+    ref_toks, _ = om.greedy(prompt, 6)
+    _, tok = be.raw_prefill(prompt, want_logits=False)
+    _, tok = be.forward_decode_raw(tok, want_logits=False)     # leaves a logits-free step behind
+    got = [ref_toks[0], tok]
+    n0 = be.kv_len()
+    st = ctypes.c_uint64(7)
+    out = ctypes.c_uint32()
+    rc = ctx.lib.qora_hip_decode_sample(ctx.h, int(tok), None, 0, None, ctypes.byref(st), None, ctypes.byref(out))
+    assert rc == -1
+    assert be.kv_len() == n0 and st.value == 7
+    for _ in range(4):
+        _, tok = be.forward_decode_raw(tok, want_logits=False)
+        got.append(tok)
+    assert got == ref_toks
+
+
+@pytest.mark.parametrize("sp", [dict(temperature=0.9, top_p=0.95, top_k=20, repetition_penalty=1.1, presence_penalty=1.5),
+                                dict(temperature=1.6, top_p=1.0, top_k=64, repetition_penalty=1.0, presence_penalty=0.0)])
+def test_decode_sample_without_logits_matches_with_logits(ctx, pkg, orc, sp):
+    """The no-wait path (no logits asked for) gives the same tokens and Rng
+    states as the path that returns the logits, which the oracle's sampler
+    checks draw for draw; some sampled tokens differ from the greedy token, so
+    the next step's token upload is exercised."""
+    print(f"case decode_sample no logits t={sp['temperature']}", flush=True)
+    cfg = entry.smoke_config(pkg)
+    w = pkg.synthetic_model(cfg, seed=7, rope_positions=64)
+    prompt = pkg.synth_tokens(7, 2000, 9, cfg.vocab)
+    params = pkg.SampleParams(**sp)
+    be = pkg.HipBackend(ctx, w, kv_capacity=64)
+    runs = []
+    not_greedy = 0
+    for want in (True, False):
+        _, tok = be.raw_prefill(prompt, want_logits=False)
+        hist, st, seen = [tok], 99, []
+        for _ in range(20):
+            logits, nxt, st_new = be.decode_sample(hist[-1], hist, params, st, want_logits=want)
+            if want:
+                exp_tok, exp_st = orc.sample(logits, hist, sp["temperature"], sp["top_p"], sp["top_k"],
+                                             sp["repetition_penalty"], sp["presence_penalty"], st)
+                assert nxt == exp_tok and st_new == exp_st
+                not_greedy += int(nxt != orc.argmax(logits))
+            seen.append((nxt, st_new))
+            hist.append(nxt)
+            st = st_new
+        runs.append(seen)
+    assert runs[0] == runs[1]
+    assert not_greedy > 0
