@@ -151,9 +151,11 @@ __global__ __launch_bounds__(kFusedWaves * kWave) void gemv_q4m_attn_kernel(Attn
     uint4 wq[GW][NKB];
     uint32_t sw[(NZ + 1) / 2];
     int esg[GW];
+    GemvOut<GW> out{};
     if (wave < NW) {
         gemv_q4m_load_scales<GW, NZ>(p, (uint64_t)item * NW + wave, lane, sw, esg);
         gemv_q4m_load_weights<GW, NKB>(p, (uint64_t)item * NW + wave, lane, wq);
+        out = gemv_q4m_out<GW>(p, tile, wave);
     }
 
     if (qkv_wave) {
@@ -313,8 +315,7 @@ __global__ __launch_bounds__(kFusedWaves * kWave) void gemv_q4m_attn_kernel(Attn
         xm = fmaxf(xm, fabsf(xr[u]));
     }
     xm = wave_max(xm);
-    gemv_q4m_item<GW, KW>(p, tile, wave, lane, [&xr](int u, uint32_t) { return xr[u]; }, xm, sw, esg, wq, zl[wave],
-                          zero16);
+    gemv_q4m_item<GW, KW>(out, lane, [&xr](int u, uint32_t) { return xr[u]; }, xm, sw, esg, wq, zl[wave], zero16);
 }
 
 }  // namespace qora

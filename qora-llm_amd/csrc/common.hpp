@@ -109,8 +109,39 @@ __device__ __forceinline__ void sgpr_pin(T& v) {
     asm volatile("" : "+s"(v));
 }
 
+// A wave-uniform pointer held in scalar registers from here on: the asm
+// keeps the compiler from re-reading it from the kernel arguments later.
+// It must point to global memory (it is rebuilt as a global-address-space
+// pointer, so accesses through it stay global instructions, not flat ones).
+template <typename T>
+__device__ __forceinline__ T* sgpr_ptr(T* p) {
+    const uint64_t v = reinterpret_cast<uint64_t>(p);
+    uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v), hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    asm volatile("" : "+s"(lo), "+s"(hi));
+    using G = __attribute__((address_space(1))) T;
+    G* g = (G*)(((uint64_t)hi << 32) | lo);
+    return (T*)g;
+}
+
 __device__ __forceinline__ float from_fixed(long long a) {
     return (float)((double)a * (1.0 / kFixScale));
+}
+
+// Weight-stream loads, marked non-temporal: the weights of a decode step are
+// read once per token, so they should not push the step's small, reused
+// lines (kernel code, arguments, accumulators, KV rows) out of the L2.
+typedef unsigned int v4u32 __attribute__((ext_vector_type(4)));
+typedef unsigned int v2u32 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint4 ld_stream(const void* p) {
+    const v4u32 v = __builtin_nontemporal_load(reinterpret_cast<const v4u32*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint2 ld_stream2(const void* p) {
+    const v2u32 v = __builtin_nontemporal_load(reinterpret_cast<const v2u32*>(p));
+    return make_uint2(v.x, v.y);
+}
+__device__ __forceinline__ uint32_t ld_stream1(const void* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p));
 }
 
 // Range guard of the fixed-point accumulators (kFixReadLimit, kFixAddLimit).

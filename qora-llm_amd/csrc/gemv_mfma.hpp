@@ -127,7 +127,7 @@ __device__ __forceinline__ void gemv_q4m_load_weights(const GemvParams& p, uint6
 #pragma unroll
     for (int g = 0; g < GW; ++g)
 #pragma unroll
-        for (int kb = 0; kb < NKB; ++kb) wq[g][kb] = *reinterpret_cast<const uint4*>(src + (g * NKB + kb) * 1024);
+        for (int kb = 0; kb < NKB; ++kb) wq[g][kb] = ld_stream(src + (g * NKB + kb) * 1024);
 }
 
 // The lane's NZ scales (adjacent binary16) and the wave's exponent bounds.
@@ -141,14 +141,14 @@ __device__ __forceinline__ void gemv_q4m_load_scales(const GemvParams& p, uint64
     if constexpr (NZ >= 8) {
 #pragma unroll
         for (int h = 0; h < NZ / 8; ++h) {
-            const uint4 v = reinterpret_cast<const uint4*>(src)[h];
+            const uint4 v = ld_stream(reinterpret_cast<const uint4*>(src) + h);
             sw[4 * h] = v.x;
             sw[4 * h + 1] = v.y;
             sw[4 * h + 2] = v.z;
             sw[4 * h + 3] = v.w;
         }
     } else if constexpr (NZ == 4) {
-        const uint2 v = *reinterpret_cast<const uint2*>(src);
+        const uint2 v = ld_stream2(src);
         sw[0] = v.x;
         sw[1] = v.y;
     } else if constexpr (NZ == 2) {
@@ -240,6 +240,29 @@ __device__ __forceinline__ void attn_merge_rows_wave(const GemvParams& p, uint32
     if (lane < 32 && i < r1) xs[i] = k0 + i < k1 ? v : 0.f;
 }
 
+// Where a matrix-core wave's outputs go: per group, the accumulator of its
+// first column (nullptr for a group past its segment), and the range flag.
+// Computed when the wave starts and held in scalar registers: read at the
+// epilogue, after the weights have streamed through the caches, the kernel
+// arguments would cost a chain of dependent scalar-memory round trips.
+template <int GW>
+struct GemvOut {
+    long long* dst[GW];
+    int* flag;
+};
+
+template <int GW>
+__device__ __forceinline__ GemvOut<GW> gemv_q4m_out(const GemvParams& p, uint32_t tile, int wave) {
+    GemvOut<GW> o;
+#pragma unroll
+    for (int g = 0; g < GW; ++g) {
+        const LaneSrc src = lane_source(p, tile, wave * GW + g, 4 * GW);
+        o.dst[g] = sgpr_ptr(src.grp < src.sg.groups ? p.acc + src.sg.col0 + src.grp * 32u : nullptr);
+    }
+    o.flag = sgpr_ptr(p.range_flag);
+    return o;
+}
+
 // One work item (column tile, K slice) of one matrix-core wave, once the
 // slice's input x is known: x * s quantised to 30-bit limbs (LDS), the
 // matrix-core pass over the wave's weight fragments, and the fixed-point
@@ -247,8 +270,8 @@ __device__ __forceinline__ void attn_merge_rows_wave(const GemvParams& p, uint32
 // xval(u, r) returns x of slice row r, the lane's u-th z value (r = (lane *
 // NZ + u) % KW).
 template <int GW, int KW, typename XVal>
-__device__ __forceinline__ void gemv_q4m_item(const GemvParams& p, uint32_t tile, int wave, int lane, XVal xval,
-                                              float xm, const uint32_t (&sw)[(GW * KW / 64 + 1) / 2],
+__device__ __forceinline__ void gemv_q4m_item(const GemvOut<GW>& out, int lane, XVal xval, float xm,
+                                              const uint32_t (&sw)[(GW * KW / 64 + 1) / 2],
                                               const int (&esv)[GW], const uint4 (&wq)[GW][KW / 64],
                                               uint8_t (*zlw)[4][KW], const uint8_t* zero16) {
     constexpr int NKB = KW / 64;
@@ -311,12 +334,11 @@ __device__ __forceinline__ void gemv_q4m_item(const GemvParams& p, uint32_t tile
     if (lane < 16) {
 #pragma unroll
         for (int g = 0; g < GW; ++g) {
-            const LaneSrc src = lane_source(p, tile, wave * GW + g, 4 * GW);
-            if (src.grp >= src.sg.groups) continue;
+            if (!out.dst[g]) continue;
             const int sh = max(min(ex + esg[g] + 2, 62), -62);
             const int rsh = sh < 0 ? -sh : 0, lsh = sh > 0 ? sh : 0;
             const long long rnd = rsh > 0 ? (1LL << (rsh - 1)) : 0;
-            long long* dst = p.acc + src.sg.col0 + src.grp * 32u + (uint32_t)lane;
+            long long* dst = out.dst[g] + (uint32_t)lane;
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
                 const v4i32 c = acc[2 * g + h];
@@ -333,7 +355,7 @@ __device__ __forceinline__ void gemv_q4m_item(const GemvParams& p, uint32_t tile
                 // contributions of 2^20 or more flag the range instead of wrapping
                 const long long ay = Y < 0 ? -Y : Y;
                 const bool big = lsh >= 56 ? ay != 0 : ((ay + rnd) >> rsh) >= (kFixAddLimit >> lsh);
-                fix_flag(p.range_flag, big);
+                fix_flag(out.flag, big);
                 const long long f = big ? 0 : ((Y + rnd) >> rsh) << lsh;
                 atomicAdd(reinterpret_cast<unsigned long long*>(dst + h * 16), (unsigned long long)f);
             }
@@ -386,7 +408,9 @@ __device__ __forceinline__ void gemv_q4m_body(const GemvParams& p, uint32_t bloc
     const int lane = t & (kWave - 1);
     // wave-uniform (scalar) so segment lookups and addresses stay on the SALU
     const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
-    const uint32_t items = p.tiles * p.splits;
+    uint32_t tiles = __builtin_amdgcn_readfirstlane(p.tiles);
+    sgpr_pin(tiles);
+    const uint32_t items = tiles * p.splits;
     const uint32_t item0 = block * IPW;
     const uint32_t nit = min((uint32_t)IPW, items - item0);
 
@@ -396,6 +420,8 @@ __device__ __forceinline__ void gemv_q4m_body(const GemvParams& p, uint32_t bloc
     uint4 wq[IPW][GW][NKB];
     uint32_t sw[IPW][(NZ + 1) / 2];
     int esg[IPW][GW];
+    GemvOut<GW> out[IPW];
+    float* ss_dst = nullptr;
     if (wave >= NW) {
         // ---- prologue wave(s): rows [k0, k1) of the input into xs, max |x|, sum x^2 ----
         // Raised issue priority: their few input loads enter the CU's memory
@@ -477,6 +503,11 @@ __device__ __forceinline__ void gemv_q4m_body(const GemvParams& p, uint32_t bloc
 #pragma unroll
         for (int j = 0; j < IPW; ++j)
             if ((uint32_t)j < nit) gemv_q4m_load_weights<GW, NKB>(p, (uint64_t)(item0 + j) * NW + wave, lane, wq[j]);
+#pragma unroll
+        for (int j = 0; j < IPW; ++j) out[j] = gemv_q4m_out<GW>(p, (item0 + j) % p.tiles, wave);
+        if constexpr (PRO == PRO_GAMMA_FIXED) {
+            ss_dst = sgpr_ptr(p.ss_out);
+        }
     }
     __syncthreads();
     if (wave >= NW) return;
@@ -484,17 +515,17 @@ __device__ __forceinline__ void gemv_q4m_body(const GemvParams& p, uint32_t bloc
     for (int j = 0; j < IPW; ++j) {
         if ((uint32_t)j >= nit) break;
         const uint32_t item = item0 + j;
-        const uint32_t tile = item % p.tiles;
-        const uint32_t split = item / p.tiles;
+        const uint32_t tile = item % tiles;
+        const uint32_t split = item / tiles;
         float xm = wred[j][0][0];
 #pragma unroll
         for (int w = 1; w < NPW; ++w) xm = fmaxf(xm, wred[j][0][w]);
         if constexpr (PRO == PRO_GAMMA_FIXED) {
             if (t == 0 && tile == 0)
-                __hip_atomic_store(p.ss_out + split, wred[j][1][0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(ss_dst + split, wred[j][1][0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
         const float* xj = xs[j];
-        gemv_q4m_item<GW, KW>(p, tile, wave, lane, [xj](int, uint32_t r) { return xj[r]; }, xm, sw[j], esg[j], wq[j],
+        gemv_q4m_item<GW, KW>(out[j], lane, [xj](int, uint32_t r) { return xj[r]; }, xm, sw[j], esg[j], wq[j],
                               zl[wave], zero16);
     }
 }

@@ -149,8 +149,8 @@ __global__ __launch_bounds__(256) void lmhead_q4m_kernel(LmHeadParams p) {
         const uint32_t* sp = p.ts + (uint64_t)tl * UPT * 32u + ((uint32_t)lane & 31u);
 #pragma unroll
         for (int u = 0; u < UPT; ++u) {
-            wb[u] = *reinterpret_cast<const uint4*>(wp + u * 1024);
-            sb[u] = sp[u * 32];
+            wb[u] = ld_stream(wp + u * 1024);
+            sb[u] = ld_stream1(sp + u * 32);
         }
     }
 
@@ -218,8 +218,8 @@ __global__ __launch_bounds__(256) void lmhead_q4m_kernel(LmHeadParams p) {
         for (int u = 0; u < UPT; ++u) {
             const uint4 w = wb[u];
             const uint32_t s2 = sb[u];
-            wb[u] = *reinterpret_cast<const uint4*>(wp + u * 1024);
-            sb[u] = sp[u * 32];
+            wb[u] = ld_stream(wp + u * 1024);
+            sb[u] = ld_stream1(sp + u * 32);
             const v4i32 a0 = *reinterpret_cast<const v4i32*>(xl + (2 * u) * SLOT + ao);
             const v4i32 a1 = *reinterpret_cast<const v4i32*>(xl + (2 * u + 1) * SLOT + ao);
             const v4i32 c0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, q4_bfrag(w.x, w.y), zero, 0, 0, 0);
