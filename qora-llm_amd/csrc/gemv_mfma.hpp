@@ -368,10 +368,11 @@ __device__ __forceinline__ void gemv_q4m_item(const GemvOut<GW>& out, int lane, 
 // the slice's inputs and builds x (xs in LDS) while the matrix-core waves
 // stream their scales and weights from the first cycle; the one block
 // barrier hands x over without waiting for the weight loads.
-// IPW > 1: each workgroup takes IPW consecutive work items (column tile,
-// K slice) of the grid a one-item launch would have, with every item's
-// scales and weights requested up front: fewer, longer-lived workgroups,
-// all loads in flight from the start.
+// IPW > 1: workgroup b of a grid of G takes the work items (column tile,
+// K slice) b, b + G, ... (at most IPW), with every item's scales and weights
+// requested up front. With G = the workgroups a device holds at once, the
+// items past G go to the first workgroups instead of a second round that
+// could only start when the first round ends.
 // LDS of one gemv_q4m workgroup.
 template <int GW, int KW, int PRO, int IPW>
 struct GemvQ4mSmem {
@@ -411,8 +412,9 @@ __device__ __forceinline__ void gemv_q4m_body(const GemvParams& p, uint32_t bloc
     uint32_t tiles = __builtin_amdgcn_readfirstlane(p.tiles);
     sgpr_pin(tiles);
     const uint32_t items = tiles * p.splits;
-    const uint32_t item0 = block * IPW;
-    const uint32_t nit = min((uint32_t)IPW, items - item0);
+    // items block, block + nblocks, ... (strided, so a grid of resident
+    // workgroups spreads the items beyond it over the first workgroups)
+    const uint32_t nit = block < items ? min((uint32_t)IPW, (items - block + nblocks - 1) / nblocks) : 0u;
 
     if (p.zero_ptr)
         for (uint32_t i = block * NT + t; i < p.zero_n; i += nblocks * NT) p.zero_ptr[i] = 0;
@@ -429,8 +431,8 @@ __device__ __forceinline__ void gemv_q4m_body(const GemvParams& p, uint32_t bloc
         __builtin_amdgcn_s_setprio(3);
 #pragma unroll
         for (int j = 0; j < IPW; ++j) {
-            if ((uint32_t)j >= nit) break;
-            const uint32_t split = (item0 + j) / p.tiles;
+            if ((uint32_t)j >= nit) continue;
+            const uint32_t split = (block + (uint32_t)j * nblocks) / tiles;
             const uint32_t k0 = split * (uint32_t)KW;
             const uint32_t k1 = min(p.k, k0 + (uint32_t)KW);
             float mx = 0.f, ss = 0.f;
@@ -499,12 +501,12 @@ __device__ __forceinline__ void gemv_q4m_body(const GemvParams& p, uint32_t bloc
         // ---- matrix-core waves: every item's scales first (the quantisation needs them), then weights ----
 #pragma unroll
         for (int j = 0; j < IPW; ++j)
-            if ((uint32_t)j < nit) gemv_q4m_load_scales<GW, NZ>(p, (uint64_t)(item0 + j) * NW + wave, lane, sw[j], esg[j]);
+            if ((uint32_t)j < nit) gemv_q4m_load_scales<GW, NZ>(p, (uint64_t)(block + (uint32_t)j * nblocks) * NW + wave, lane, sw[j], esg[j]);
 #pragma unroll
         for (int j = 0; j < IPW; ++j)
-            if ((uint32_t)j < nit) gemv_q4m_load_weights<GW, NKB>(p, (uint64_t)(item0 + j) * NW + wave, lane, wq[j]);
+            if ((uint32_t)j < nit) gemv_q4m_load_weights<GW, NKB>(p, (uint64_t)(block + (uint32_t)j * nblocks) * NW + wave, lane, wq[j]);
 #pragma unroll
-        for (int j = 0; j < IPW; ++j) out[j] = gemv_q4m_out<GW>(p, (item0 + j) % p.tiles, wave);
+        for (int j = 0; j < IPW; ++j) out[j] = gemv_q4m_out<GW>(p, (block + (uint32_t)j * nblocks) % tiles, wave);
         if constexpr (PRO == PRO_GAMMA_FIXED) {
             ss_dst = sgpr_ptr(p.ss_out);
         }
@@ -513,8 +515,8 @@ __device__ __forceinline__ void gemv_q4m_body(const GemvParams& p, uint32_t bloc
     if (wave >= NW) return;
 #pragma unroll
     for (int j = 0; j < IPW; ++j) {
-        if ((uint32_t)j >= nit) break;
-        const uint32_t item = item0 + j;
+        if ((uint32_t)j >= nit) continue;
+        const uint32_t item = (block + (uint32_t)j * nblocks);
         const uint32_t tile = item % tiles;
         const uint32_t split = item / tiles;
         float xm = wred[j][0][0];
@@ -535,6 +537,115 @@ __global__ __launch_bounds__(PRO == PRO_ATTN ? 512 : 320) void gemv_q4m_kernel(G
     kernarg_warm(p);
     __shared__ GemvQ4mSmem<GW, KW, PRO, IPW> sm;
     gemv_q4m_body<GW, KW, PRO, IPW>(p, blockIdx.x, gridDim.x, sm);
+}
+
+// Four matrix-core waves and no prologue wave (PRO_PLAIN, PRO_GAMMA_FIXED,
+// PRO_SILU_FIXED). Each wave builds a quarter of the slice's input itself:
+// its input loads go out first, then its scales and weights, and loads
+// complete in issue order, so the input is in long before the weights (a
+// separate prologue wave's input loads would queue behind the other waves'
+// weight streams). A CU holds eight such 4-wave workgroups at once against
+// five 5-wave ones, so the gate|up projection's 1376 workgroups run in one
+// round instead of two.
+template <int GW, int KW, int PRO>
+__global__ __launch_bounds__(256) void gemv_q4m4_kernel(GemvParams p) {
+    constexpr int NW = 4;
+    constexpr int NKB = KW / 64, NZ = GW * KW / 64;
+    constexpr int RW = KW / NW;              // input rows per wave (16..128)
+    constexpr int RPL = (RW + kWave - 1) / kWave;
+    static_assert(KW % 64 == 0 && KW <= 512, "slice of 64..512 rows");
+    static_assert(PRO == PRO_PLAIN || PRO == PRO_GAMMA_FIXED || PRO == PRO_SILU_FIXED, "no attention merge here");
+    kernarg_warm(p);
+    __shared__ __align__(16) float xs[KW];
+    __shared__ float wred[2][NW];
+    __shared__ __align__(16) uint8_t zl[NW][GW][4][KW];
+    __shared__ __align__(16) uint8_t zero16[16];
+
+    const int t = threadIdx.x;
+    const int lane = t & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
+    uint32_t tiles = __builtin_amdgcn_readfirstlane(p.tiles);
+    sgpr_pin(tiles);
+    const uint32_t item = blockIdx.x;
+    const uint32_t tile = item % tiles, split = item / tiles;
+    const uint32_t k0 = split * (uint32_t)KW;
+    const uint32_t k1 = min(p.k, k0 + (uint32_t)KW);
+
+    if (p.zero_ptr)
+        for (uint32_t i = blockIdx.x * (NW * kWave) + t; i < p.zero_n; i += gridDim.x * (NW * kWave)) p.zero_ptr[i] = 0;
+
+    // ---- this wave's input rows [wave * RW, wave * RW + RW) of the slice ----
+    float xp[RPL], ssp = 0.f;
+    long long xa[RPL], xb[RPL];
+    uint16_t gm[RPL];
+#pragma unroll
+    for (int r = 0; r < RPL; ++r) {
+        const uint32_t row = (uint32_t)(wave * RW + lane + kWave * r);
+        const uint32_t rc = min(k0 + row, p.k - 1u);
+        if constexpr (PRO == PRO_PLAIN) xp[r] = p.x[rc];
+        if constexpr (PRO == PRO_GAMMA_FIXED) {
+            xa[r] = p.xacc[rc];
+            gm[r] = p.gamma[rc];
+        }
+        if constexpr (PRO == PRO_SILU_FIXED) {
+            xa[r] = p.xacc[rc];
+            xb[r] = p.xacc[p.k + rc];
+        }
+    }
+    if constexpr (PRO == PRO_SILU_FIXED) ssp = p.ss_in[min((uint32_t)lane, p.ss_n - 1u)];
+    __builtin_amdgcn_sched_barrier(0);   // the input loads are issued before the weight stream
+
+    // ---- then the wave's scales and weights ----
+    uint4 wq[GW][NKB];
+    uint32_t sw[(NZ + 1) / 2];
+    int esg[GW];
+    gemv_q4m_load_scales<GW, NZ>(p, (uint64_t)item * NW + wave, lane, sw, esg);
+    gemv_q4m_load_weights<GW, NKB>(p, (uint64_t)item * NW + wave, lane, wq);
+    const GemvOut<GW> out = gemv_q4m_out<GW>(p, tile, wave);
+    float* ss_dst = nullptr;
+    if constexpr (PRO == PRO_GAMMA_FIXED) ss_dst = sgpr_ptr(p.ss_out);
+
+    // ---- x of the wave's rows into LDS, max |x|, sum x^2 ----
+    float inv = 1.f;
+    if constexpr (PRO == PRO_SILU_FIXED)
+        inv = 1.0f / sqrtf(wave_sum(lane < (int)p.ss_n ? ssp : 0.f) / (float)p.norm_n + 1e-6f);
+    float mx = 0.f, ss = 0.f;
+#pragma unroll
+    for (int r = 0; r < RPL; ++r) {
+        const uint32_t lr = (uint32_t)(lane + kWave * r);
+        const uint32_t row = (uint32_t)(wave * RW) + lr;
+        const bool ok = lr < (uint32_t)RW && k0 + row < k1;
+        float x;
+        if constexpr (PRO == PRO_PLAIN) {
+            x = ok ? xp[r] : 0.f;
+        } else if constexpr (PRO == PRO_GAMMA_FIXED) {
+            const float xf = ok ? from_fixed(xa[r]) : 0.f;
+            fix_flag(out.flag, ok && fix_out_of_range(xa[r], kFixReadLimit));
+            ss += xf * xf;
+            x = xf * h2f(gm[r]);
+        } else {
+            x = ok ? silu_mul(inv * from_fixed(xa[r]), inv * from_fixed(xb[r])) : 0.f;
+        }
+        if (lr < (uint32_t)RW) xs[row] = x;
+        mx = fmaxf(mx, fabsf(x));
+    }
+    mx = wave_max(mx);
+    if constexpr (PRO == PRO_GAMMA_FIXED) ss = wave_sum(ss);
+    if (lane == 0) {
+        wred[0][wave] = mx;
+        wred[1][wave] = ss;
+    }
+    if (wave == 0 && lane < 4) reinterpret_cast<uint32_t*>(zero16)[lane] = 0u;
+    __syncthreads();
+    const float xm = fmaxf(fmaxf(wred[0][0], wred[0][1]), fmaxf(wred[0][2], wred[0][3]));
+    if constexpr (PRO == PRO_GAMMA_FIXED) {
+        // the slice's sum of squares (the waves' partials in order), for the
+        // consumer of this GEMV's output, which applies the RMSNorm factor
+        if (t == 0 && tile == 0)
+            __hip_atomic_store(ss_dst + split, ((wred[1][0] + wred[1][1]) + wred[1][2]) + wred[1][3], __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+    }
+    gemv_q4m_item<GW, KW>(out, lane, [](int, uint32_t r) { return xs[r]; }, xm, sw, esg, wq, zl[wave], zero16);
 }
 
 }  // namespace qora

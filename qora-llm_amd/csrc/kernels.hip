@@ -111,9 +111,6 @@ bool plan_gemv_q4m(uint32_t k, const uint32_t* seg_groups, int nseg, bool paired
         if (best.blocks() >= want) break;
     }
     if (!have) return false;
-    // several work items per workgroup (QORA_GEMV_IPW = 2 or 4; K slices of 256, one group per wave)
-    const int ipw = env_int("QORA_GEMV_IPW", 1);
-    if ((ipw == 2 || ipw == 4) && best.gw == 1 && best.kr == 256 && row_align == 1) best.ipw = ipw;
     *plan = best;
     return true;
 }
@@ -173,15 +170,16 @@ static hipError_t launch_gemv_gt(const GemvPlan& plan, const GemvParams& p, hipS
 
 template <int GW, int KW, int IPW>
 static hipError_t launch_q4m_ipw(const GemvPlan& plan, const GemvParams& p, hipStream_t stream) {
-    // 4 matrix-core waves + the prologue wave (four for the attention merge)
-    const dim3 grid(plan.grid()), block(320), block_attn(512);
+    // 4 matrix-core waves that build their own input rows; the attention
+    // merge keeps 4 matrix-core waves + 4 prologue waves
+    const dim3 grid(plan.grid()), block(256), block_attn(512);
     switch (p.pro) {
-    case PRO_PLAIN: hipLaunchKernelGGL((gemv_q4m_kernel<GW, KW, PRO_PLAIN, IPW>), grid, block, 0, stream, p); break;
+    case PRO_PLAIN: hipLaunchKernelGGL((gemv_q4m4_kernel<GW, KW, PRO_PLAIN>), grid, block, 0, stream, p); break;
     case PRO_GAMMA_FIXED:
-        hipLaunchKernelGGL((gemv_q4m_kernel<GW, KW, PRO_GAMMA_FIXED, IPW>), grid, block, 0, stream, p);
+        hipLaunchKernelGGL((gemv_q4m4_kernel<GW, KW, PRO_GAMMA_FIXED>), grid, block, 0, stream, p);
         break;
     case PRO_SILU_FIXED:
-        hipLaunchKernelGGL((gemv_q4m_kernel<GW, KW, PRO_SILU_FIXED, IPW>), grid, block, 0, stream, p);
+        hipLaunchKernelGGL((gemv_q4m4_kernel<GW, KW, PRO_SILU_FIXED>), grid, block, 0, stream, p);
         break;
     case PRO_ATTN:
         if constexpr (IPW == 1) {
@@ -197,14 +195,6 @@ static hipError_t launch_q4m_ipw(const GemvPlan& plan, const GemvParams& p, hipS
 
 template <int GW, int KW>
 static hipError_t launch_q4m_kw(const GemvPlan& plan, const GemvParams& p, hipStream_t stream) {
-    if constexpr (GW == 1 && KW == 256) {
-        switch (plan.ipw) {
-        case 1: return launch_q4m_ipw<GW, KW, 1>(plan, p, stream);
-        case 2: return launch_q4m_ipw<GW, KW, 2>(plan, p, stream);
-        case 4: return launch_q4m_ipw<GW, KW, 4>(plan, p, stream);
-        default: return hipErrorInvalidValue;
-        }
-    }
     if (plan.ipw != 1) return hipErrorInvalidValue;
     return launch_q4m_ipw<GW, KW, 1>(plan, p, stream);
 }
