@@ -190,6 +190,17 @@ int qora_hip_graph_destroy(qora_hip_ctx* ctx, void* graph_exec);
  * W Q4 [k][n] in the projection layout. */
 int qora_hip_gemv_q4(qora_hip_ctx* ctx, const void* packed, const void* scales, const float* x, float* y,
                      uint64_t k, uint64_t n, void* stream);
+/* No counterpart in the reference: qora_hip_gemv_q4 for callers that cannot
+ * allocate device memory (code under stream capture, tight serving loops,
+ * harnesses that forbid hipMalloc). It calls no hipMalloc, hipFree or other
+ * allocating routine: its fixed-point accumulator is a static device array
+ * of 65536 int64 words (512 KiB per device, held until the process ends), so
+ * n is limited to 65536 (larger n returns QORA_HIP_E_INVALID). Same kernels
+ * and results as qora_hip_gemv_q4. Every call on a device shares that
+ * device's array: calls that overlap on one device (two streams, two
+ * contexts) race. */
+int qora_hip_gemv_q4_noalloc(qora_hip_ctx* ctx, const void* packed, const void* scales, const float* x, float* y,
+                             uint64_t k, uint64_t n, void* stream);
 /* gemv_f16 (gemv.rs:534-567; simd.rs:151-176). */
 int qora_hip_gemv_f16(qora_hip_ctx* ctx, const void* w, const float* x, float* y, uint64_t k, uint64_t n,
                       void* stream);

@@ -96,6 +96,7 @@ SIGNATURES = {
     "qora_hip_graph_launch": (_I, [_P, _P, _U32]),
     "qora_hip_graph_destroy": (_I, [_P, _P]),
     "qora_hip_gemv_q4": (_I, [_P, _P, _P, _P, _P, _U64, _U64, _P]),
+    "qora_hip_gemv_q4_noalloc": (_I, [_P, _P, _P, _P, _P, _U64, _U64, _P]),
     "qora_hip_gemv_f16": (_I, [_P, _P, _P, _P, _U64, _U64, _P]),
     "qora_hip_gemv_q4_accumulate": (_I, [_P, _P, _P, _P, _P, _U64, _U64, _P]),
     "qora_hip_gate_up_q4_accumulate": (_I, [_P, _P, _P, _P, _P, _P, _P, _U64, _U64, _P]),

@@ -6,6 +6,7 @@
 #include <algorithm>
 #include <atomic>
 #include <chrono>
+#include <mutex>
 #include <cstdlib>
 #include <cstring>
 #include <cstdio>
@@ -14,6 +15,46 @@
 #include <vector>
 
 using namespace qora;
+
+// Scratch of the allocation-free GEMV entry (qora_hip_gemv_q4_noalloc): its
+// fixed-point accumulator, one copy on every device the library runs on,
+// held until the process ends. Host code never passes the array's name to
+// a kernel or a copy: it uses the device address that hipGetSymbolAddress
+// returns for the current device (noalloc_scratch below).
+constexpr uint64_t kNoAllocMaxN = 65536;   // outputs; int64 words of the array (512 KiB)
+static __device__ __align__(256) long long scratch[kNoAllocMaxN];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+hipError_t g_scratch_err[kMaxDevices] = {};
+bool g_scratch_done[kMaxDevices] = {};
+
+// The device address of `scratch` on `device`, looked up once per device
+// with that device current (the caller's set-up, qora_hip_create).
+hipError_t noalloc_scratch_setup(int device) {
+    if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_done[device]) {
+        void* ptr = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        g_scratch_err[device] = e;
+        g_scratch_ptr[device] = e == hipSuccess ? ptr : nullptr;
+        if (e != hipSuccess) (void)hipGetLastError();
+        g_scratch_done[device] = true;
+    }
+    return g_scratch_err[device];
+}
+
+long long* noalloc_scratch(int device) {
+    if (device < 0 || device >= kMaxDevices) return nullptr;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    return static_cast<long long*>(g_scratch_ptr[device]);
+}
+
+}  // namespace
 
 namespace {
 
@@ -409,6 +450,9 @@ extern "C" int qora_hip_create(int device, qora_hip_ctx** out) {
     int cus = 0;
     (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device);
     c->cus = cus > 0 ? cus : 256;
+    // the allocation-free entry's scratch address on this device (an error
+    // here only disables that entry, which then reports it)
+    (void)noalloc_scratch_setup(device);
     if (hipHostMalloc((void**)&c->h_pin, 128, hipHostMallocDefault) != hipSuccess) {
         (void)hipStreamDestroy(c->stream);
         delete c;
@@ -1444,6 +1488,24 @@ int rowdot_entry(qora_hip_ctx* c, int fmt, const void* w, const void* s, const f
 extern "C" int qora_hip_gemv_q4(qora_hip_ctx* c, const void* packed, const void* scales, const float* x, float* y,
                                 uint64_t k, uint64_t n, void* stream) {
     return gemv_entry(c, FMT_Q4, packed, scales, nullptr, nullptr, x, y, k, n, false, stream);
+}
+
+extern "C" int qora_hip_gemv_q4_noalloc(qora_hip_ctx* c, const void* packed, const void* scales, const float* x,
+                                        float* y, uint64_t k, uint64_t n, void* stream) {
+    if (!c) return QORA_HIP_E_INVALID;
+    if (!y) return fail(c, QORA_HIP_E_INVALID, "null argument");
+    if (n == 0 || n > kNoAllocMaxN)
+        return fail(c, QORA_HIP_E_INVALID, "gemv_q4_noalloc takes 0 < n <= " + std::to_string(kNoAllocMaxN));
+    long long* acc = noalloc_scratch(c->device);
+    if (!acc) return fail(c, QORA_HIP_E_DEVICE, "gemv_q4_noalloc: no scratch address on this device");
+    // the same kernels as qora_hip_gemv_q4, on the device's static scratch
+    // instead of the context's grown accumulator: clear (a kernel, not a
+    // memset), accumulate, convert
+    const hipStream_t s = pick_stream(c, stream);
+    HIP_TRY(c, launch_fill_zero(acc, n, s));
+    if (int rc = gemv_acc_entry(c, FMT_Q4, packed, scales, nullptr, nullptr, x, acc, k, n, false, stream)) return rc;
+    HIP_TRY(c, launch_acc_to_f32(acc, (uint32_t)n, 0, y, s));
+    return QORA_HIP_OK;
 }
 
 extern "C" int qora_hip_gemv_f16(qora_hip_ctx* c, const void* w, const float* x, float* y, uint64_t k, uint64_t n,
