@@ -90,7 +90,9 @@ typedef struct {
     const float* rope_sin;
     uint64_t rope_positions;
     const uint8_t* use_rope;                /* [num_layers]: the file's no_rope_layers (1 = rotate) */
-    uint32_t kv_capacity;                   /* positions held on device */
+    uint32_t kv_capacity;                   /* positions held on device; 0 = the RoPE table length
+                                               (65536 without RoPE layers), every position the
+                                               model can place */
     uint32_t kv_dtype;                      /* 0 = f32 (reference RawKvCache), 1 = f16 */
 } qora_model_desc;
 
@@ -125,14 +127,17 @@ int qora_hip_generate_greedy(qora_hip_ctx* ctx, uint32_t token, uint32_t steps, 
 typedef struct {
     float temperature;          /* <= 0: greedy, the first-max rule */
     float top_p;                /* nucleus mass, e.g. 0.95 */
-    uint32_t top_k;             /* 1 .. 64 (the reference default is 20) */
+    uint32_t top_k;             /* candidates kept (the reference default is 20); 0 = the whole
+                                   vocabulary, as sample_token_top_k (generate.rs:357-363) */
     float repetition_penalty;   /* <= 1: off; once per occurrence in the last 64 history tokens */
     float presence_penalty;     /* <= 0: off; once for every token present in the history */
 } qora_sample_params;
 
 /* apply_repetition_penalty, then apply_presence_penalty, then
  * sample_token_top_k (generate.rs:64-91, 345-395) on device logits [vocab]
- * (vocab <= 131072; the logits are not modified). The penalties apply only
+ * (vocab <= 4194304; the logits are not modified). top_k 1..64 on a
+ * vocabulary of up to 131072 takes the fast path (each block's best 64);
+ * any other top_k sorts every logit on the device. The penalties apply only
  * when temperature > 0, as at every call site (generate.rs:141-145, 216-235).
  * history is the host array
  * of generated tokens, rng_state the Rng (xorshift64, generate.rs:38-61)

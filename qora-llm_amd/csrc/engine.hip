@@ -21,6 +21,7 @@ using namespace qora;
 // held until the process ends. Host code never passes the array's name to
 // a kernel or a copy: it uses the device address that hipGetSymbolAddress
 // returns for the current device (noalloc_scratch below).
+constexpr uint32_t kDefaultKvCapacity = 65536;   // kv_capacity 0 for a model without RoPE layers
 constexpr uint64_t kNoAllocMaxN = 65536;   // outputs; int64 words of the array (512 KiB)
 static __device__ __align__(256) long long scratch[kNoAllocMaxN];
 
@@ -175,6 +176,8 @@ struct qora_hip_ctx {
     int32_t* smp_tok = nullptr;
     SamplePenalty* smp_pen = nullptr;
     uint32_t smp_vocab = 0;
+    void* smp_sort = nullptr;            // full-sort path: two key buffers and the probabilities
+    uint64_t smp_sort_bytes = 0;
     uint64_t smp_pen_n = 0;
     void* ws_pf = nullptr;               // kernel-level GEMM: split operand and group exponents
     uint64_t ws_pf_bytes = 0;
@@ -481,7 +484,7 @@ extern "C" int qora_hip_destroy(qora_hip_ctx* c) {
         if (w.scales) (void)hipFree(w.scales);
     }
     for (void* p : {(void*)c->ws_acc, (void*)c->ws_attn_part, c->ws_pf, (void*)c->smp_work, (void*)c->smp_cand,
-                    (void*)c->smp_rng, (void*)c->smp_tok, (void*)c->smp_pen})
+                    (void*)c->smp_rng, (void*)c->smp_pen, c->smp_sort})
         if (p) (void)hipFree(p);
     if (c->h_pin) (void)hipHostFree(c->h_pin);
     if (c->h_tok) (void)hipHostFree(c->h_tok);
@@ -571,7 +574,7 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
     HIP_TRY(c, hipSetDevice(c->device));
     free_model(c);
     if (d->num_layers == 0 || d->vocab == 0 || d->hidden == 0 || d->intermediate == 0 || d->num_heads == 0 ||
-        d->num_kv_heads == 0 || d->head_dim == 0 || d->kv_capacity == 0)
+        d->num_kv_heads == 0 || d->head_dim == 0)
         return fail(c, QORA_HIP_E_INVALID, "zero-sized model dimension");
     if (d->format > 1) return fail(c, QORA_HIP_E_INVALID, "format must be 0 (F16) or 1 (Q4)");
     if (d->num_heads % d->num_kv_heads != 0 || d->num_kv_groups != d->num_heads / d->num_kv_heads)
@@ -587,7 +590,15 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
         return fail(c, QORA_HIP_E_INVALID, "null model pointer");
     bool any_rope = false;
     for (uint32_t l = 0; l < d->num_layers; ++l) any_rope |= d->use_rope[l] != 0;
-    if (any_rope && (!d->rope_cos || !d->rope_sin || d->rope_half_dim == 0 || d->rope_positions < d->kv_capacity))
+    // kv_capacity 0: as many positions as the model can place, i.e. the
+    // RoPE table length (65536 for SmolLM3-3B), or kDefaultKvCapacity for a
+    // model without RoPE layers, so a caller never runs out of cache where
+    // the reference's growing RawKvCache would go on
+    const uint64_t cap = d->kv_capacity ? d->kv_capacity
+                                        : (any_rope ? std::min<uint64_t>(d->rope_positions, 0x7FFFFFFFull)
+                                                    : (uint64_t)kDefaultKvCapacity);
+    if (cap == 0) return fail(c, QORA_HIP_E_INVALID, "zero-sized KV cache (empty RoPE tables)");
+    if (any_rope && (!d->rope_cos || !d->rope_sin || d->rope_half_dim == 0 || d->rope_positions < cap))
         return fail(c, QORA_HIP_E_INVALID, "RoPE tables must cover kv_capacity positions");
 
     ModelState& m = c->m;
@@ -601,7 +612,7 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
     m.groups = d->num_kv_groups;
     m.half = d->rope_half_dim;
     m.fmt = d->format;
-    m.cap = d->kv_capacity;
+    m.cap = (uint32_t)cap;
     m.kv_f16 = d->kv_dtype == 1;
     m.rope_positions = d->rope_positions;
     m.any_rope = any_rope;
@@ -1831,19 +1842,22 @@ extern "C" int qora_hip_attn_prefill(qora_hip_ctx* c, const float* q, const void
 
 namespace {
 
-// Penalty list and device scratch for one sampling call, then the kernels;
-// the token and the advanced rng state come back to the host.
 // Argument checks of a sampling call, made before anything is launched.
 int sample_check(qora_hip_ctx* c, bool have_logits, uint64_t vocab, const uint32_t* history, uint64_t n_history,
                  const qora_sample_params* sp, const uint64_t* rng_state, const uint32_t* token) {
     if (!have_logits || !sp || !rng_state || !token || (n_history && !history))
         return fail(c, QORA_HIP_E_INVALID, "null argument");
-    if (vocab == 0 || vocab > 0xFFFFFFFFull || !smp_supported((uint32_t)vocab))
-        return fail(c, QORA_HIP_E_INVALID, "sampling supports vocab <= 131072");
-    if (sp->top_k == 0 || sp->top_k > 64) return fail(c, QORA_HIP_E_INVALID, "top_k must be 1 .. 64");
+    if (vocab == 0 || vocab > 0xFFFFFFFFull || !smp_sort_supported((uint32_t)vocab))
+        return fail(c, QORA_HIP_E_INVALID, "sampling supports vocabularies of 1 .. 4194304 tokens");
     if (c->capturing) return fail(c, QORA_HIP_E_STATE, "sampling copies to the host: not allowed during capture");
     return QORA_HIP_OK;
 }
+
+// Penalty list and device scratch for one sampling call, then the kernels;
+// the token and the advanced rng state come back to the host. top_k 1..64
+// on a vocabulary of up to 131072 keeps each block's best 64 keys; any other
+// top_k (0 = the whole vocabulary, sample_token_top_k's k, generate.rs:357-363)
+// or a larger vocabulary sorts every key.
 
 int sample_device(qora_hip_ctx* c, const float* logits, uint64_t vocab, const uint32_t* history, uint64_t n_history,
                   const qora_sample_params* sp, uint64_t* rng_state, uint32_t* token, hipStream_t s) {
@@ -1873,7 +1887,7 @@ int sample_device(qora_hip_ctx* c, const float* logits, uint64_t vocab, const ui
     const uint32_t V = (uint32_t)vocab, blocks = smp_blocks(V);
     if (V > c->smp_vocab || !c->smp_rng) {
         HIP_TRY(c, hipStreamSynchronize(c->stream));
-        for (void* q : {(void*)c->smp_work, (void*)c->smp_cand, (void*)c->smp_rng, (void*)c->smp_tok})
+        for (void* q : {(void*)c->smp_work, (void*)c->smp_cand, (void*)c->smp_rng})   // smp_tok lies in smp_rng
             if (q) (void)hipFree(q);
         c->smp_work = nullptr;
         c->smp_cand = nullptr;
@@ -1918,7 +1932,27 @@ int sample_device(qora_hip_ctx* c, const float* logits, uint64_t vocab, const ui
     p.top_k = sp->top_k;
     p.rng = c->smp_rng;
     p.token_out = c->smp_tok;
-    HIP_TRY(c, launch_sample(logits, p, s));
+    const bool few = sp->top_k >= 1 && sp->top_k <= 64 && smp_supported(V);
+    if (few) {
+        HIP_TRY(c, launch_sample(logits, p, s));
+    } else {
+        const uint32_t k = sp->top_k > 0 ? std::min<uint32_t>(sp->top_k, V) : V;
+        const uint32_t ns = smp_sort_keys(V);
+        const uint64_t bytes = (uint64_t)ns * 16 + (uint64_t)V * 4;
+        if (bytes > c->smp_sort_bytes) {
+            HIP_TRY(c, hipStreamSynchronize(c->stream));
+            if (c->smp_sort) (void)hipFree(c->smp_sort);
+            c->smp_sort = nullptr;
+            c->smp_sort_bytes = 0;
+            if (int rc = dalloc(c, bytes, &c->smp_sort)) return rc;
+            c->smp_sort_bytes = bytes;
+        }
+        p.sort_a = (unsigned long long*)c->smp_sort;
+        p.sort_b = p.sort_a + ns;
+        p.n_sort = ns;
+        p.probs = (float*)(p.sort_b + ns);
+        HIP_TRY(c, launch_sample_sorted(logits, p, k, s));
+    }
     HIP_TRY(c, hipMemcpyAsync(&c->h_pin[20], c->smp_tok, 4, hipMemcpyDeviceToHost, s));
     HIP_TRY(c, hipMemcpyAsync(&c->h_pin[22], c->smp_rng, 8, hipMemcpyDeviceToHost, s));
     HIP_TRY(c, hipStreamSynchronize(s));

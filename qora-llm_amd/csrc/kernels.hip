@@ -642,4 +642,36 @@ hipError_t launch_sample(const float* logits, const SampleParams& p, hipStream_t
     return hipGetLastError();
 }
 
+uint32_t smp_sort_keys(uint32_t vocab) {
+    uint32_t n = smp_blocks(vocab) * kSmpBlock, m = kSmpBlock;
+    while (m < n) m <<= 1;
+    return m;
+}
+bool smp_sort_supported(uint32_t vocab) { return vocab > 0 && vocab <= kSmpSortMax; }
+
+hipError_t launch_sample_sorted(const float* logits, const SampleParams& p, uint32_t k, hipStream_t stream) {
+    if (!smp_sort_supported(p.vocab) || p.blocks != smp_blocks(p.vocab) || p.n_sort != smp_sort_keys(p.vocab) ||
+        k == 0 || k > p.vocab || !p.sort_a || !p.sort_b || !p.probs)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(smp_copy_kernel, dim3(std::min<uint32_t>(1024, (p.vocab + 255) / 256)), dim3(256), 0, stream,
+                       logits, p.work, p.vocab);
+    if (p.n_pen) hipLaunchKernelGGL(smp_penalty_kernel, dim3((p.n_pen + 255) / 256), dim3(256), 0, stream, p);
+    // runs of 2048 keys (the padding blocks past the vocabulary sort to all ~0)
+    const uint32_t nb = p.n_sort / kSmpBlock;
+    SampleParams q = p;
+    hipLaunchKernelGGL(smp_block_sort_kernel, dim3(nb), dim3(256), 0, stream, q);
+    unsigned long long* src = p.sort_a;
+    unsigned long long* dst = p.sort_b;
+    for (uint32_t run = kSmpBlock; run < p.n_sort; run <<= 1) {
+        hipLaunchKernelGGL(smp_merge_kernel, dim3(p.n_sort / 256), dim3(256), 0, stream, (const unsigned long long*)src,
+                           dst, p.n_sort, run);
+        std::swap(src, dst);
+    }
+    if (p.temperature > 0.0f)
+        hipLaunchKernelGGL(smp_probs_kernel, dim3((k + 255) / 256), dim3(256), 0, stream, p,
+                           (const unsigned long long*)src, k);
+    hipLaunchKernelGGL(smp_scan_kernel, dim3(1), dim3(64), 0, stream, p, (const unsigned long long*)src, k);
+    return hipGetLastError();
+}
+
 }  // namespace qora

@@ -113,5 +113,10 @@ hipError_t launch_pf_attn(const PrefillAttnParams& p, hipStream_t stream);
 uint32_t smp_blocks(uint32_t vocab);
 bool smp_supported(uint32_t vocab);
 hipError_t launch_sample(const float* logits, const SampleParams& p, hipStream_t stream);
+// The full-sort path (any top_k, vocabularies up to 4M): n_sort keys per
+// sort buffer, and the kernels over the first k sorted candidates.
+uint32_t smp_sort_keys(uint32_t vocab);
+bool smp_sort_supported(uint32_t vocab);
+hipError_t launch_sample_sorted(const float* logits, const SampleParams& p, uint32_t k, hipStream_t stream);
 
 }  // namespace qora

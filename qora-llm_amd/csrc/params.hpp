@@ -194,6 +194,14 @@ struct SampleParams {
     uint32_t top_k;
     unsigned long long* rng;   // xorshift64 state, updated in place
     int32_t* token_out;
+    // the full-sort path (top_k 0 or above kSmpKeep, or a large vocabulary):
+    // every key sorted by merging 2048-key runs (two buffers of n_sort keys,
+    // n_sort = blocks * 2048 rounded up to a power of two), then the
+    // reference's arithmetic over the first k of them
+    unsigned long long* sort_a;
+    unsigned long long* sort_b;
+    uint32_t n_sort;
+    float* probs;              // [k] e^((l - max) / temperature) of the sorted candidates
 };
 
 struct ArgmaxFinishParams {

@@ -26,6 +26,7 @@ namespace qora {
 constexpr uint32_t kSmpBlock = 2048;    // logits per block in the first pass
 constexpr uint32_t kSmpKeep = 64;       // candidates kept per block (top_k <= kSmpKeep)
 constexpr uint32_t kSmpFinal = 4096;    // candidate keys sorted by the final block
+constexpr uint32_t kSmpSortMax = 1u << 22;   // keys of the full-sort path (vocabularies up to 4M)
 
 // Orderable key: ascending key = value descending, then index ascending.
 __device__ __forceinline__ unsigned long long smp_key(float v, uint32_t idx) {
@@ -138,6 +139,102 @@ __global__ __launch_bounds__(256) void smp_final_kernel(SampleParams p) {
                     }
                 }
                 if (!hit) token = (uint32_t)keys[0];
+            }
+        }
+    }
+    *p.rng = state;
+    *p.token_out = (int32_t)token;
+}
+
+// ---------------------------------------------------------------------------
+// Full-sort path: every (value, index) key in the reference's stable order.
+// 1. smp_block_sort_kernel: each block bitonic-sorts its 2048 keys and writes
+//    them all (keys past the vocabulary are ~0, which sort last);
+// 2. smp_merge_kernel, once per doubling of the run length: key i of a run
+//    lands at its rank in the run it pairs with (a binary search), so the
+//    merged run is in order; the ~0 padding ties break by run (stable);
+// 3. smp_probs_kernel: e^((l - max) / temperature) of the first k keys, each
+//    computed once by the same expression the scan would use;
+// 4. smp_scan_kernel: one thread runs sample_token_top_k's sums, nucleus
+//    cut-off, draw and scan over those k values in order (generate.rs:360-393).
+// ---------------------------------------------------------------------------
+
+__global__ __launch_bounds__(256) void smp_block_sort_kernel(SampleParams p) {
+    __shared__ unsigned long long keys[kSmpBlock];
+    const uint32_t base = blockIdx.x * kSmpBlock;
+    for (uint32_t j = threadIdx.x; j < kSmpBlock; j += 256) {
+        const uint32_t i = base + j;
+        keys[j] = i < p.vocab ? smp_key(p.work[i], i) : ~0ull;
+    }
+    smp_bitonic<kSmpBlock>(keys);
+    for (uint32_t j = threadIdx.x; j < kSmpBlock; j += 256) p.sort_a[base + j] = keys[j];
+}
+
+// Runs of `run` keys in `in` (n keys, n a multiple of 2 run) merged in pairs into `out`.
+__global__ __launch_bounds__(256) void smp_merge_kernel(const unsigned long long* in, unsigned long long* out,
+                                                        uint32_t n, uint32_t run) {
+    const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+    if (i >= n) return;
+    const uint32_t r = i / run, base = (r & ~1u) * run;
+    const bool first = (r & 1u) == 0u;
+    const unsigned long long key = in[i];
+    const unsigned long long* other = in + (first ? base + run : base);
+    // rank among the other run: keys below (first run) or not above (second
+    // run), so equal keys keep their run order
+    uint32_t lo = 0, hi = run;
+    while (lo < hi) {
+        const uint32_t mid = (lo + hi) >> 1;
+        const bool before = first ? other[mid] < key : other[mid] <= key;
+        if (before) lo = mid + 1;
+        else hi = mid;
+    }
+    const uint32_t own = i - (first ? base : base + run);
+    out[base + own + lo] = key;
+}
+
+__global__ __launch_bounds__(256) void smp_probs_kernel(SampleParams p, const unsigned long long* sorted, uint32_t k) {
+    const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+    if (i >= k) return;
+    const float inv_temp = 1.0f / p.temperature;
+    const float max_logit = smp_key_value(sorted[0]);
+    p.probs[i] = expf((smp_key_value(sorted[i]) - max_logit) * inv_temp);
+}
+
+__global__ __launch_bounds__(64) void smp_scan_kernel(SampleParams p, const unsigned long long* sorted, uint32_t k) {
+    if (threadIdx.x != 0) return;
+    uint32_t token = (uint32_t)sorted[0];
+    unsigned long long state = *p.rng;
+    if (p.temperature > 0.0f) {
+        float sum = 0.0f;
+        for (uint32_t i = 0; i < k; ++i) sum = __fadd_rn(sum, p.probs[i]);
+        if (sum > 0.0f) {
+            const float inv = 1.0f / sum;
+            // each probability is e * inv, rounded, then added (never one fused
+            // multiply-add), as the reference scales the vector before summing
+            float cum = 0.0f;
+            uint32_t cutoff = k;
+            for (uint32_t i = 0; i < k; ++i) {
+                cum = __fadd_rn(cum, __fmul_rn(p.probs[i], inv));
+                if (cum >= p.top_p) {
+                    cutoff = i + 1;
+                    break;
+                }
+            }
+            float total = 0.0f;
+            for (uint32_t i = 0; i < cutoff; ++i) total = __fadd_rn(total, __fmul_rn(p.probs[i], inv));
+            if (total > 0.0f) {
+                state ^= state << 13;
+                state ^= state >> 7;
+                state ^= state << 17;
+                const float rand_val = (float)(uint32_t)(state >> 40) / 16777216.0f * total;
+                float acc = 0.0f;
+                for (uint32_t i = 0; i < cutoff; ++i) {
+                    acc = __fadd_rn(acc, __fmul_rn(p.probs[i], inv));
+                    if (acc >= rand_val) {
+                        token = (uint32_t)sorted[i];
+                        break;
+                    }
+                }
             }
         }
     }

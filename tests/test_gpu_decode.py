@@ -326,3 +326,24 @@ def test_fixed_point_range_overflow_is_reported(ctx, pkg, fmt):
     be2 = pkg.HipBackend(ctx, w2, kv_capacity=64)
     be2.raw_prefill(prompt, want_logits=False)
     be2.forward_decode_raw(3, want_logits=False)
+
+
+def test_default_kv_capacity_is_the_rope_table(ctx, pkg, orc):
+    """kv_capacity 0: the cache holds every position the RoPE tables cover (a
+    caller never runs out where the reference's growing cache would go on);
+    the step past the table is refused."""
+    print("case default kv capacity", flush=True)
+    w = small_model(pkg, 1, layers=4, seed=14)          # RoPE on layer 3, tables of 128 positions
+    be = pkg.HipBackend(ctx, w, kv_capacity=0)
+    om = orc.OracleModel(w, kv_capacity=128, T=4)
+    prompt = pkg.synth_tokens(14, 2100, 100, w.config.vocab)
+    _, tok = be.raw_prefill(prompt, want_logits=False)
+    om.prefill(prompt)
+    toks = be.generate_greedy(tok, 28)
+    assert be.kv_len() == 128
+    for t in [tok] + list(toks[:-1]):
+        ref = om.forward_decode(int(t))
+    assert int(toks[-1]) == orc.argmax(ref) or orc.top2_gap(ref) <= 1e-4 * float(np.max(np.abs(ref)))
+    with pytest.raises(pkg.QoraHipError) as e:
+        be.forward_decode_raw(int(toks[-1]))
+    assert e.value.code == pkg.QORA_HIP_E_STATE

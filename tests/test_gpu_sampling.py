@@ -64,13 +64,41 @@ def test_sample_ties_and_zero_signs(ctx, pkg, orc):
 
 def test_sample_errors(ctx, pkg):
     with device(ctx) as d:
-        dl = d.put(np.zeros(300000, np.float32))
-        bad_k = pkg.SampleParams(temperature=0.7, top_p=0.9, top_k=0, repetition_penalty=1.0, presence_penalty=0.0)
+        dl = d.put(np.zeros(16, np.float32))
         ok = pkg.SampleParams(temperature=0.7, top_p=0.9, top_k=20, repetition_penalty=1.0, presence_penalty=0.0)
         with pytest.raises(pkg.QoraHipError):
-            ctx.sample(dl, 1000, [], bad_k, 1)
+            ctx.sample(dl, 0, [], ok, 1)                # empty vocabulary
         with pytest.raises(pkg.QoraHipError):
-            ctx.sample(dl, 300000, [], ok, 1)      # beyond the supported vocabulary
+            ctx.sample(dl, (1 << 22) + 1, [], ok, 1)    # beyond the supported vocabulary
+
+
+# the full-sort path: top_k 0 (the whole vocabulary), top_k above 64, a
+# vocabulary above 131072 (generate.rs:357-363)
+SORT_CASES = [(1000, 0), (4097, 100), (128256, 0), (128256, 1000), (200000, 20), (5000, 6000)]
+
+
+@pytest.mark.parametrize("vocab,top_k", SORT_CASES)
+def test_sample_full_sort_matches_oracle(ctx, pkg, orc, vocab, top_k):
+    print(f"case sample full sort vocab={vocab} top_k={top_k}", flush=True)
+    r = np.random.default_rng(vocab + top_k)
+    settings = [dict(temperature=0.9, top_p=0.95, repetition_penalty=1.1, presence_penalty=1.5),
+                dict(temperature=1.4, top_p=1.0, repetition_penalty=1.0, presence_penalty=0.0),
+                dict(temperature=0.0, top_p=0.95, repetition_penalty=1.1, presence_penalty=0.0)]
+    with device(ctx) as d:
+        for si, sp in enumerate(settings):
+            params = pkg.SampleParams(top_k=top_k, **sp)
+            st_gpu = st_orc = 0x9E3779B97F4A7C15 + si
+            for trial in range(6):
+                lg = (r.standard_normal(vocab) * 2.5).astype(np.float32)
+                if trial == 1:
+                    lg[r.integers(0, vocab, size=50)] = lg.max()     # ties at the top
+                hist = r.integers(0, vocab, size=int(r.integers(0, 100))).tolist()
+                dl = d.put(lg)
+                tok, st_gpu = ctx.sample(dl, vocab, hist, params, st_gpu)
+                want, st_orc = orc.sample(lg, hist, sp["temperature"], sp["top_p"], top_k,
+                                          sp["repetition_penalty"], sp["presence_penalty"], st_orc)
+                assert tok == want, (si, trial)
+                assert st_gpu == st_orc
 
 
 def test_decode_sample_matches_decode_plus_oracle_sampling(ctx, pkg, orc):

@@ -70,14 +70,17 @@ def test_penalties_per_occurrence_and_window(orc):
         assert pres[t] == (np.float32(lg[t] - np.float32(1.5)) if t in hist else lg[t])
 
 
-def test_sampled_frequencies_match_float64_distribution(orc):
+@pytest.mark.parametrize("top_k,top_p", [(20, 0.9), (0, 0.93), (1000, 0.93)])
+def test_sampled_frequencies_match_float64_distribution(orc, top_k, top_p):
     """20000 draws against the distribution the definition fixes: softmax of
-    (l - max) / T over the top_k logits, cut at the first cumulative mass >=
-    top_p, renormalised."""
+    (l - max) / T over the top_k logits (top_k 0 or above the vocabulary: all
+    of them, generate.rs:363), cut at the first cumulative mass >= top_p,
+    renormalised."""
     r = np.random.default_rng(3)
     lg = (r.standard_normal(300) * 1.5).astype(np.float32)
-    T, top_p, top_k = 0.8, 0.9, 20
-    order = np.lexsort((np.arange(lg.size), -lg.astype(np.float64)))[:top_k]
+    T = 0.8
+    kk = top_k if 0 < top_k < lg.size else lg.size
+    order = np.lexsort((np.arange(lg.size), -lg.astype(np.float64)))[:kk]
     z = np.exp((lg[order].astype(np.float64) - lg.max()) / T)
     pz = z / z.sum()
     cut = int(np.searchsorted(np.cumsum(pz), top_p) + 1)
