@@ -122,6 +122,151 @@ def prepared_time(ctx, hip, wid, wid_up, paired, nbytes, x, acc):
             ctx.gemv_release(g)
 
 
+def f16_bytes(k, n):
+    """Algorithmic bytes of one F16 GEMV: binary16 weights + f32 x + f32 y."""
+    return 2 * k * n + 4 * k + 4 * n
+
+
+def device_copies(ctx, hip, srcs, min_bytes=768 << 20, min_copies=2):
+    """Distinct device copies of the device buffers `srcs` [(ptr, nbytes)],
+    enough copies that together they span >= min_bytes. Returns the list of
+    per-copy pointer tuples and the allocations to free."""
+    per = sum(nb for _, nb in srcs)
+    copies = max(min_copies, math.ceil(min_bytes / per))
+    sets, allocs = [], []
+    try:
+        for _ in range(copies):
+            ptrs = []
+            for p, nb in srcs:
+                d = ctx.malloc(nb)
+                allocs.append(d)
+                hip.d2d(d, p, nb)
+                ptrs.append(d)
+            sets.append(tuple(ptrs))
+    except Exception:
+        for d in allocs:
+            ctx.free(d)
+        raise
+    return sets, allocs
+
+
+def copies_time(ctx, hip, srcs, launch):
+    """Average ms per launch of launch(ptr_tuple) over distinct copies of srcs."""
+    sets, allocs = device_copies(ctx, hip, srcs)
+    try:
+        return time_graph(ctx, hip, [(lambda s=s: launch(s)) for s in sets])
+    finally:
+        ctx.synchronize()
+        for d in allocs:
+            ctx.free(d)
+
+
+def valu_q4_roofline(ctx, hip, be, pkg):
+    """The VALU Q4 GEMV (gemv_kernel, the reference weight layout, one
+    launch through qora_hip_gemv_q4_accumulate / _gate_up_q4_accumulate)
+    and the VALU row-dot lm_head (qora_hip_gemv_q4_rowdot) on the shapes the
+    matrix-core kernels are timed on, for the comparison of the two."""
+    c = be.config
+    lib, h = ctx.lib, ctx.h
+    x = ctx.malloc(4 * c.intermediate)
+    acc = ctx.malloc(8 * 2 * c.intermediate)
+    ctx.h2d(x, pkg.synth_f32(0, 77, c.intermediate))
+    shapes = c.weight_shapes()
+    res = {}
+    try:
+        for j, label in ((0, "q/o 2048x2048"), (1, "k/v 2048x512"), (6, "down 11008x2048")):
+            k, n = shapes[j]
+            p, s = ctx.weight_ptrs(int(be.wids[0, j]))
+            ms = copies_time(ctx, hip, [(p, k * n // 2), (s, k * n // 16)],
+                             lambda t, k=k, n=n: ctx.check(
+                                 lib.qora_hip_gemv_q4_accumulate(h, t[0], t[1], x, acc, k, n, None), "q4_acc"))
+            res[label] = {"us": ms * 1e3, "gbps": q4_bytes(k, n) / (ms * 1e-3) / 1e9}
+        k, n = shapes[4]
+        gp, gs = ctx.weight_ptrs(int(be.wids[0, 4]))
+        up, us = ctx.weight_ptrs(int(be.wids[0, 5]))
+        ms = copies_time(ctx, hip, [(gp, k * n // 2), (gs, k * n // 16), (up, k * n // 2), (us, k * n // 16)],
+                         lambda t: ctx.check(lib.qora_hip_gate_up_q4_accumulate(h, t[0], t[1], t[2], t[3], x, acc,
+                                                                                 k, n, None), "gate_up_acc"))
+        gu_bytes = 2 * (k * n // 2 + k * n // 16) + 4 * k + 8 * n
+        res["gate+up 2048x(2x11008)"] = {"us": ms * 1e3, "gbps": gu_bytes / (ms * 1e-3) / 1e9}
+        V, Hd = c.vocab, c.hidden
+        ep, es = ctx.weight_ptrs(be.embed_wid)
+        lm = ctx.malloc(4 * V)
+        try:
+            ms = copies_time(ctx, hip, [(ep, V * Hd // 2), (es, V * Hd // 16)],
+                             lambda t: ctx.check(lib.qora_hip_gemv_q4_rowdot(h, t[0], t[1], x, lm, V, Hd, None),
+                                                 "q4_rowdot"))
+        finally:
+            ctx.free(lm)
+        res["lm_head 128256x2048"] = {"us": ms * 1e3, "gbps": q4_bytes(V, Hd) / (ms * 1e-3) / 1e9}
+    finally:
+        ctx.free(x)
+        ctx.free(acc)
+    return res
+
+
+def f16_measurements(pkg, hip, cfg, prompt, steps, warmup):
+    """The F16 weight path on its own context: decode tok/s of the
+    SmolLM3-3B architecture with seeded N(0, 0.02) binary16 weights (same
+    prompt, f32 KV cache of 2048 positions), and GB/s of its decode-step
+    GEMV (the VALU kernel on the tile layout) and row-dot lm_head on the
+    per-layer shapes, each over >= 768 MB of distinct copies."""
+    t0 = time.perf_counter()
+    w16 = pkg.synthetic_model(cfg, seed=0, fmt=pkg.FORMAT_F16, rope_positions=2048)
+    print(f"# F16 synthetic model ready in {time.perf_counter() - t0:.1f}s", file=sys.stderr, flush=True)
+    ctx = pkg.HipContext(0)
+    try:
+        be = pkg.HipBackend(ctx, w16, kv_capacity=2048, kv_dtype=pkg.KV_F32)
+        _, tok = be.raw_prefill(prompt, want_logits=False)
+        for _ in range(warmup):
+            _, tok = be.forward_decode_raw(tok, want_logits=False)
+        ctx.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            _, tok = be.forward_decode_raw(tok, want_logits=False)
+        ctx.synchronize()
+        tok_s = steps / (time.perf_counter() - t0)
+        wbytes = w16.weight_bytes_per_token()
+        roof = HBM_PEAK_GBS * 1e9 / wbytes
+        print(f"# F16 decode {tok_s:.1f} tok/s (weight roofline {roof:.0f})", file=sys.stderr, flush=True)
+        lib, h = ctx.lib, ctx.h
+        x = ctx.malloc(4 * cfg.intermediate)
+        acc = ctx.malloc(8 * 2 * cfg.intermediate)
+        ctx.h2d(x, pkg.synth_f32(0, 77, cfg.intermediate))
+        shapes = cfg.weight_shapes()
+        gemv = {}
+        try:
+            for j, label in ((0, "q/o 2048x2048"), (1, "k/v 2048x512"), (6, "down 11008x2048")):
+                k, n = shapes[j]
+                ms = prepared_time(ctx, hip, int(be.wids[0, j]), 0, False, 2 * k * n, x, acc)
+                gemv[label] = {"us": ms * 1e3, "gbps": f16_bytes(k, n) / (ms * 1e-3) / 1e9}
+            k, n = shapes[4]
+            ms = prepared_time(ctx, hip, int(be.wids[0, 4]), int(be.wids[0, 5]), True, 4 * k * n, x, acc)
+            gu_bytes = 4 * k * n + 4 * k + 8 * n
+            gemv["gate+up 2048x(2x11008)"] = {"us": ms * 1e3, "gbps": gu_bytes / (ms * 1e-3) / 1e9}
+            V, Hd = cfg.vocab, cfg.hidden
+            ep, _ = ctx.weight_ptrs(be.embed_wid)
+            lm = ctx.malloc(4 * V)
+            try:
+                ms = copies_time(ctx, hip, [(ep, 2 * V * Hd)],
+                                 lambda t: ctx.check(lib.qora_hip_gemv_f16_rowdot(h, t[0], x, lm, V, Hd, None),
+                                                     "f16_rowdot"))
+            finally:
+                ctx.free(lm)
+            gemv["lm_head 128256x2048"] = {"us": ms * 1e3, "gbps": f16_bytes(V, Hd) / (ms * 1e-3) / 1e9}
+        finally:
+            ctx.free(x)
+            ctx.free(acc)
+        for kname, v in gemv.items():
+            print(f"# F16 {kname}: {v['us']:.2f} us, {v['gbps']:.0f} GB/s", file=sys.stderr, flush=True)
+    finally:
+        ctx.close()
+    return {"tok_s": round(tok_s, 2), "weight_bytes_per_token": wbytes, "weight_roofline_tok_s": round(roof, 1),
+            "frac_of_weight_roofline": round(tok_s / roof, 4),
+            "gemv_gbps": {k2: round(v["gbps"], 1) for k2, v in gemv.items()},
+            "gemv_us": {k2: round(v["us"], 3) for k2, v in gemv.items()}}
+
+
 def gemv_roofline(ctx, hip, be, pkg):
     """Per-shape GB/s of the decode step's Q4 GEMV kernel on the model's own
     weights (tile layout, qora_hip_gemv_prepare / qora_hip_gemv_run), and of
@@ -162,10 +307,87 @@ def gemv_roofline(ctx, hip, be, pkg):
     return results
 
 
+CPU_THREADS = 16   # host threads a one-GPU job of this benchmark is given
+
+
+def host_cpu():
+    """Model name and counts of the host CPU, from /proc/cpuinfo (what lscpu
+    reports as Model name, CPU(s), Socket(s) and Core(s) per socket)."""
+    info = {"model": None, "logical_cpus": os.cpu_count(), "sockets": None, "cores_per_socket": None}
+    try:
+        info["available_cpus"] = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        info["available_cpus"] = os.cpu_count()
+    try:
+        sockets, cores = set(), None
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                key, _, val = line.partition(":")
+                key, val = key.strip(), val.strip()
+                if key == "model name" and info["model"] is None:
+                    info["model"] = val
+                elif key == "physical id":
+                    sockets.add(val)
+                elif key == "cpu cores" and cores is None:
+                    cores = int(val)
+        info["sockets"] = len(sockets) or None
+        info["cores_per_socket"] = cores
+    except (OSError, ValueError):
+        pass
+    return info
+
+
+def cpu_threads():
+    """Threads for the multi-threaded CPU baseline: every CPU this process
+    may run on, at most CPU_THREADS."""
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        avail = os.cpu_count() or 1
+    return max(1, min(CPU_THREADS, avail))
+
+
+def cpu_gemv_rates(pkg, orc, threads_list, min_bytes=1 << 30):
+    """GB/s of the reference CPU GEMVs (the oracle's AVX-512 LUT Q4 GEMV,
+    gemv.rs:646-675 / simd.rs:44-83, and the row-dot lm_head,
+    gemv.rs:825-864) on the 2048 -> 11008 gate shape (seed 0, x ~ N(0,1))
+    and the 128256 x 2048 tied lm_head, each pass over >= min_bytes of
+    distinct weight copies so the host caches cannot serve them."""
+    out = {}
+    k, n = 2048, 11008
+    p, s = pkg.synth_q4(0, 4, k, n)
+    x = pkg.synth_f32(0, 77, k)
+    copies = max(2, math.ceil(min_bytes / (p.nbytes + s.nbytes)))
+    ps = [(p.copy(), s.copy()) for _ in range(copies)]
+    for T in threads_list:
+        orc.set_threads(T)
+        orc.gemv_q4(x, ps[0][0], ps[0][1], k, n, T)
+        t0 = time.perf_counter()
+        for pp, ss in ps:
+            orc.gemv_q4(x, pp, ss, k, n, T)
+        dt = (time.perf_counter() - t0) / copies
+        out[f"gate 2048x11008 T={T}"] = {"us": round(dt * 1e6, 1), "gbps": round(q4_bytes(k, n) / dt / 1e9, 2)}
+    del ps
+    V, Hd = pkg.SMOLLM3_3B.vocab, pkg.SMOLLM3_3B.hidden
+    p, s = pkg.synth_q4(0, 1000, V, Hd)
+    x = pkg.synth_f32(0, 78, Hd)
+    copies = max(2, math.ceil(min_bytes / (p.nbytes + s.nbytes)))
+    ps = [(p, s)] + [(p.copy(), s.copy()) for _ in range(copies - 1)]
+    for T in threads_list:
+        orc.set_threads(T)
+        orc.lm_head_q4(x, ps[0][0], ps[0][1], V, Hd)
+        t0 = time.perf_counter()
+        for pp, ss in ps:
+            orc.lm_head_q4(x, pp, ss, V, Hd)
+        dt = (time.perf_counter() - t0) / copies
+        out[f"lm_head 128256x2048 T={T}"] = {"us": round(dt * 1e6, 1), "gbps": round(q4_bytes(V, Hd) / dt / 1e9, 2)}
+    return out
+
+
 def cpu_baseline(pkg, orc, w, prompt, seconds=15.0, threads=16):
     """Reference CPU algorithm (oracle) on this host: prefill 8 prompt tokens,
     then decode tokens until `seconds` of decode time have passed."""
-    threads = max(1, min(threads, os.cpu_count() or 1))
+    threads = max(1, threads)
     orc.set_threads(threads)
     om = orc.OracleModel(w, kv_capacity=1024, T=threads)
     logits = om.prefill(prompt[:8])
@@ -287,6 +509,41 @@ def long_context_rate(ctx, pkg, w, n_ctx=32768, n_tok=64):
 COPY_BYTES = 64 << 20
 
 
+def calibration_copies(ctx, hip):
+    """Three device copies of COPY_BYTES (hipMemcpy's blit kernel reads and
+    writes COPY_BYTES each): the known-size dispatches that scale the
+    FETCH_SIZE / WRITE_SIZE counters of a --pmc run to bytes."""
+    src, dst = ctx.malloc(COPY_BYTES), ctx.malloc(COPY_BYTES)
+    for _ in range(3):
+        hip.d2d(dst, src, COPY_BYTES)
+    ctx.synchronize()
+    ctx.free(src)
+    ctx.free(dst)
+
+
+def profile_decode(steps=16):
+    """The decode step's kernels, launched eagerly, for rocprofv3 --pmc
+    runs: the calibration copies, then the 64-token prompt's prefill and
+    `steps` greedy decode tokens of the SmolLM3-3B Q4 model (seed 0, f32 KV
+    cache of 2048 positions). Every layer's weights are distinct, so each
+    decode GEMV reads its weights from HBM."""
+    pkg = entry.load_package()
+    cfg = pkg.SMOLLM3_3B
+    w = pkg.synthetic_model(cfg, seed=0, rope_positions=2048)
+    prompt = pkg.synth_tokens(0, 2000, 64, cfg.vocab)
+    hip = Hip()
+    ctx = pkg.HipContext(0)
+    be = pkg.HipBackend(ctx, w, kv_capacity=2048, kv_dtype=pkg.KV_F32)
+    calibration_copies(ctx, hip)
+    _, tok = be.raw_prefill(prompt, want_logits=False)
+    for _ in range(steps):
+        _, tok = be.forward_decode_raw(tok, want_logits=False)
+    ctx.synchronize()
+    print(json.dumps({"profile_decode": {"prompt_tokens": 64, "steps": steps, "copy_bytes": COPY_BYTES,
+                                         "last_token": int(tok)}}), flush=True)
+    ctx.close()
+
+
 def profile_kernel(launches=8):
     """The dominant kernel alone, for rocprofv3 --pmc runs: three device
     copies of COPY_BYTES (hipMemcpy's blit kernel: reads and writes
@@ -305,16 +562,14 @@ def profile_kernel(launches=8):
     x = ctx.malloc(4 * k)
     acc = ctx.malloc(8 * 2 * n)
     ctx.h2d(x, pkg.synth_f32(0, 77, k))
-    src, dst = ctx.malloc(COPY_BYTES), ctx.malloc(COPY_BYTES)
-    for _ in range(3):
-        hip.d2d(dst, src, COPY_BYTES)
+    calibration_copies(ctx, hip)
     gids = [ctx.gemv_prepare(wg, wu, True) for _ in range(launches)]
     ctx.synchronize()
     for g in gids:
         ctx.check(ctx.lib.qora_hip_gemv_run(ctx.h, g, x, acc, None), "gemv_run")
     ctx.synchronize()
     gu_bytes = 2 * (k * n // 2 + k * n // 16) + 4 * k + 8 * n
-    print(json.dumps({"profile_kernel": "gemv_q4m_kernel gate|up 2048x(2x11008)", "launches": launches,
+    print(json.dumps({"profile_kernel": "gemv_q4m4_kernel gate|up 2048x(2x11008)", "launches": launches,
                       "algorithmic_bytes_per_launch": gu_bytes, "copy_bytes": COPY_BYTES}), flush=True)
     for g in gids:
         ctx.gemv_release(g)
@@ -327,6 +582,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-gemv", action="store_true")
+    ap.add_argument("--no-f16", action="store_true", help="skip the F16-weight decode and GEMV figures")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--decode-only", action="store_true",
                     help="time only the host-driven decode (skips the chained loop and the ~2048-context run)")
@@ -336,6 +592,9 @@ def main():
                     help="only the 512-token batched prefill of the SmolLM3-3B model (for rocprofv3)")
     ap.add_argument("--profile-long", action="store_true",
                     help="only the decode at ~32768 positions with an f16 KV cache (for rocprofv3)")
+    ap.add_argument("--profile-decode", action="store_true",
+                    help="only the 64-token prefill and 16 decode tokens, launched eagerly after device copies "
+                         "of known size, for hardware-counter runs")
     ap.add_argument("--profile-kernel", action="store_true",
                     help="only launch the dominant kernel (gate|up GEMV) eagerly, after a device copy of "
                          "known size, for hardware-counter runs")
@@ -351,6 +610,10 @@ def main():
     if args.profile_kernel:
         profile_kernel()
         return
+    if args.profile_decode:
+        os.environ["QORA_HIP_EAGER"] = "1"
+        profile_decode()
+        return
     if args.profile_prefill or args.profile_long:
         pkg = entry.load_package()
         cfg = pkg.SMOLLM3_3B
@@ -360,6 +623,7 @@ def main():
             be = pkg.HipBackend(ctx, w, kv_capacity=2048, kv_dtype=pkg.KV_F32)
             print(json.dumps({"profile_prefill": prefill_rate(be, ctx, pkg, cfg)}), flush=True)
         else:
+            calibration_copies(ctx, Hip())
             rate, _ = long_context_rate(ctx, pkg, w)
             print(json.dumps({"profile_long_tok_s": round(rate, 2)}), flush=True)
         ctx.close()
@@ -367,6 +631,7 @@ def main():
     prompt_len, cap = 64, 2048
     if prompt_len + args.warmup + args.steps > cap:
         sys.exit("warmup + steps exceed the 2048-position KV cache")
+    cpu_host = host_cpu()
 
     pkg = entry.load_package()
     cfg = pkg.SMOLLM3_3B
@@ -401,6 +666,10 @@ def main():
     for kname, v in gemv.items():
         print(f"# {kname}: {v['us']:.2f} us, {v['gbps']:.0f} GB/s", file=sys.stderr, flush=True)
 
+    valu = {} if args.no_gemv else valu_q4_roofline(ctx, hip, be, pkg)
+    for kname, v in valu.items():
+        print(f"# VALU Q4 {kname}: {v['us']:.2f} us, {v['gbps']:.0f} GB/s", file=sys.stderr, flush=True)
+
     long_rate = long_bytes = None
     if not args.decode_only:
         long_rate, long_bytes = long_context_rate(ctx, pkg, w)
@@ -411,16 +680,28 @@ def main():
         roofline = {"bound": "hbm", "achieved": round(gu["gbps"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                     "frac": round(gu["gbps"] / HBM_PEAK_GBS, 4),
                     "traffic": read_traffic(os.path.join(ROOT, "profiles", "gate_up_q4_2048x11008_pmc.md")),
-                    "kernel": "gemv_q4m_kernel<GW=1,KW=256,PRO_PLAIN> paired gate|up 2048->2x11008 (qora_hip_gemv_run)",
+                    "kernel": "gemv_q4m4_kernel<GW=1,KW=256,PRO_PLAIN> paired gate|up 2048->2x11008 (qora_hip_gemv_run)",
                     "algorithmic_bytes_per_launch": gu["bytes"], "avg_launch_us": round(gu["us"], 3)}
 
-    cpu = None
+    weight_bytes = w.weight_bytes_per_token()
+    ctx.close()
+    f16 = None
+    if not args.decode_only and not args.no_f16:
+        f16 = f16_measurements(pkg, hip, cfg, prompt, min(args.steps, 128), args.warmup)
+
+    cpu = cpu_t1 = cpu_gemv = None
     if not args.no_cpu_baseline:
         orc = entry.load_oracle()
-        cpu = cpu_baseline(pkg, orc, w, prompt, seconds=args.cpu_seconds)
+        T = cpu_threads()
+        cpu = cpu_baseline(pkg, orc, w, prompt, seconds=args.cpu_seconds, threads=T)
         print(f"# cpu baseline {cpu['value']:.2f} tok/s on {cpu['cores']} threads", file=sys.stderr, flush=True)
+        if not args.decode_only:
+            cpu_t1 = cpu_baseline(pkg, orc, w, prompt, seconds=min(args.cpu_seconds, 10.0), threads=1)
+            print(f"# cpu baseline {cpu_t1['value']:.2f} tok/s on 1 thread", file=sys.stderr, flush=True)
+            cpu_gemv = cpu_gemv_rates(pkg, orc, sorted({T, 1}, reverse=True))
+            for kname, v in cpu_gemv.items():
+                print(f"# cpu {kname}: {v['us']:.0f} us, {v['gbps']:.2f} GB/s", file=sys.stderr, flush=True)
 
-    weight_bytes = w.weight_bytes_per_token()
     out = {
         "metric": "decode tok/s (SmolLM3-3B Q4, bs=1) + Q4 GEMV HBM GB/s vs ~8 TB/s peak",
         "value": round(tok_s, 2),
@@ -450,9 +731,14 @@ def main():
         "frac_of_roofline_ctx32768": (round(long_rate * long_bytes / (HBM_PEAK_GBS * 1e9), 4)
                                       if long_rate else None),
         "gemv_gbps": {k2: round(v["gbps"], 1) for k2, v in gemv.items()},
+        "gemv_us": {k2: round(v["us"], 3) for k2, v in gemv.items()},
+        "gemv_gbps_valu_q4": {k2: round(v["gbps"], 1) for k2, v in valu.items()},
+        "f16": f16,
+        "cpu_host": cpu_host,
+        "cpu_baseline_t1": cpu_t1,
+        "cpu_gemv_gbps": cpu_gemv,
         "vs_baseline_ref": "reference GPU decode ~4.1 tok/s (README.md:43,157, GTX 1660 SUPER)",
     }
-    ctx.close()
     print(json.dumps(out), flush=True)
 
 
