@@ -519,8 +519,17 @@ const float* oq_kv_v(const oq_kv* kv, uint32_t layer) { return kv->v[layer]; }
  * layer, token-major [len][kv_stride]. */
 int oq_kv_set(oq_kv* kv, uint32_t layer, const float* k, const float* v, uint64_t len) {
     if (layer >= kv->num_layers || len > kv->capacity) return -1;
-    memcpy(kv->k[layer], k, len * kv->kv_stride * sizeof(float));
-    memcpy(kv->v[layer], v, len * kv->kv_stride * sizeof(float));
+    /* copied in 1 MiB pieces on every thread: the first write to fresh cache
+     * pages is what costs, and the threads take those page faults in parallel */
+    const uint64_t total = len * kv->kv_stride, piece = 1u << 18;
+    const int64_t pieces = (int64_t)((total + piece - 1) / piece);
+#pragma omp parallel for schedule(dynamic, 4) num_threads(nthreads())
+    for (int64_t i = 0; i < 2 * pieces; ++i) {
+        const uint64_t at = (uint64_t)(i % pieces) * piece;
+        const uint64_t cnt = total - at < piece ? total - at : piece;
+        if (i < pieces) memcpy(kv->k[layer] + at, k + at, cnt * sizeof(float));
+        else memcpy(kv->v[layer] + at, v + at, cnt * sizeof(float));
+    }
     kv->len[layer] = len;
     return 0;
 }

@@ -404,30 +404,6 @@ int capture_step(qora_hip_ctx* c, bool with_lm_head, bool fused, hipGraphExec_t*
     return QORA_HIP_OK;
 }
 
-float h2f_host(uint16_t h) {
-    const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
-    const uint32_t exp = (h >> 10) & 0x1Fu;
-    uint32_t mant = h & 0x3FFu;
-    uint32_t bits;
-    if (exp == 0) {
-        if (mant == 0) {
-            bits = sign;
-        } else {
-            int e = -1;
-            do { mant <<= 1; ++e; } while ((mant & 0x400u) == 0);
-            mant &= 0x3FFu;
-            bits = sign | ((uint32_t)(127 - 15 - e) << 23) | (mant << 13);
-        }
-    } else if (exp == 0x1F) {
-        bits = sign | 0x7F800000u | (mant << 13);
-    } else {
-        bits = sign | ((exp + 127 - 15) << 23) | (mant << 13);
-    }
-    float f;
-    std::memcpy(&f, &bits, 4);
-    return f;
-}
-
 }  // namespace
 
 // ===========================================================================
@@ -1293,34 +1269,22 @@ extern "C" int qora_hip_kv_upload(qora_hip_ctx* c, uint32_t layer, const float* 
     const size_t kvd = (size_t)m.KVH * m.hd;
     const size_t count = (size_t)len * kvd;
     if (count) {
-        // host: token-major [len][KVH][hd] f32; device: head-major [KVH][cap][hd]
-        const size_t row32 = (size_t)m.hd * 4;
+        // host: token-major [len][KVH][hd] f32, copied up in one piece; a kernel moves it into
+        // the head-major [KVH][cap][hd] cache (binary16 for an f16 cache)
+        void* tmp = nullptr;
+        if (int rc = dalloc(c, count * 4, &tmp)) return rc;
         const float* src[2] = {k, v};
-        if (!m.kv_f16) {
-            for (int which = 0; which < 2; ++which) {
-                uint8_t* base = (uint8_t*)(which ? m.d_v : m.d_k) + (size_t)layer * m.cap * kvd * 4;
-                for (uint32_t h = 0; h < m.KVH; ++h)
-                    HIP_TRY(c, hipMemcpy2D(base + (size_t)h * m.cap * row32, row32, (const uint8_t*)src[which] + h * row32,
-                                           kvd * 4, row32, len, hipMemcpyHostToDevice));
-            }
-        } else {
-            // head-major f32 staging [KVH][len][hd], then binary16 per head
-            void* tmp = nullptr;
-            if (int rc = dalloc(c, count * 4, &tmp)) return rc;
-            hipError_t e = hipSuccess;
-            for (int which = 0; which < 2 && e == hipSuccess; ++which) {
-                uint16_t* base = (uint16_t*)(which ? m.d_v : m.d_k) + (size_t)layer * m.cap * kvd;
-                for (uint32_t h = 0; h < m.KVH && e == hipSuccess; ++h)
-                    e = hipMemcpy2D((uint8_t*)tmp + (size_t)h * len * row32, row32,
-                                    (const uint8_t*)src[which] + h * row32, kvd * 4, row32, len, hipMemcpyHostToDevice);
-                for (uint32_t h = 0; h < m.KVH && e == hipSuccess; ++h)
-                    e = launch_f32_to_f16((const float*)tmp + (size_t)h * len * m.hd, base + (size_t)h * m.cap * m.hd,
-                                          (uint64_t)len * m.hd, c->stream);
-                if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
-            }
-            (void)hipFree(tmp);
-            if (e != hipSuccess) return fail(c, QORA_HIP_E_DEVICE, std::string("kv_upload: ") + hipGetErrorString(e));
+        const size_t eb = m.kv_f16 ? 2 : 4;
+        hipError_t e = hipSuccess;
+        for (int which = 0; which < 2 && e == hipSuccess; ++which) {
+            uint8_t* base = (uint8_t*)(which ? m.d_v : m.d_k) + (size_t)layer * m.cap * kvd * eb;
+            e = hipMemcpyAsync(tmp, src[which], count * 4, hipMemcpyHostToDevice, c->stream);
+            if (e == hipSuccess)
+                e = launch_kv_move(true, m.kv_f16 != 0, (float*)tmp, base, (uint32_t)len, m.KVH, m.hd, m.cap, c->stream);
+            if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
         }
+        (void)hipFree(tmp);
+        if (e != hipSuccess) return fail(c, QORA_HIP_E_DEVICE, std::string("kv_upload: ") + hipGetErrorString(e));
     }
     m.host_pos = len;
     return set_device_pos(c, len);
@@ -1336,22 +1300,20 @@ extern "C" int qora_hip_kv_download(qora_hip_ctx* c, uint32_t layer, float* k, f
     const size_t n = (size_t)m.host_pos;
     HIP_TRY(c, hipStreamSynchronize(c->stream));
     if (n == 0) return QORA_HIP_OK;
-    // device: head-major [KVH][cap][hd]; host: the reference's token-major [len][KVH][hd]
+    // device: head-major [KVH][cap][hd]; host: the reference's token-major [len][KVH][hd] f32,
+    // gathered on the device and copied down in one piece
+    void* tmp = nullptr;
+    if (int rc = dalloc(c, n * kvd * 4, &tmp)) return rc;
     const size_t eb = m.kv_f16 ? 2 : 4;
-    const size_t row = (size_t)m.hd * eb;
-    std::vector<uint8_t> tmp(m.kv_f16 ? n * kvd * 2 : 0);
-    for (int which = 0; which < 2; ++which) {
-        const uint8_t* base = (const uint8_t*)(which ? m.d_v : m.d_k) + (size_t)layer * m.cap * kvd * eb;
-        float* out = which ? v : k;
-        uint8_t* dst = m.kv_f16 ? tmp.data() : (uint8_t*)out;
-        for (uint32_t h = 0; h < m.KVH; ++h)
-            HIP_TRY(c, hipMemcpy2D(dst + h * row, kvd * eb, base + (size_t)h * m.cap * row, row, row, n,
-                                   hipMemcpyDeviceToHost));
-        if (m.kv_f16) {
-            const uint16_t* t16 = (const uint16_t*)tmp.data();
-            for (size_t i = 0; i < n * kvd; ++i) out[i] = h2f_host(t16[i]);
-        }
+    hipError_t e = hipSuccess;
+    for (int which = 0; which < 2 && e == hipSuccess; ++which) {
+        uint8_t* base = (uint8_t*)(which ? m.d_v : m.d_k) + (size_t)layer * m.cap * kvd * eb;
+        e = launch_kv_move(false, m.kv_f16 != 0, (float*)tmp, base, (uint32_t)n, m.KVH, m.hd, m.cap, c->stream);
+        if (e == hipSuccess) e = hipMemcpyAsync(which ? v : k, tmp, n * kvd * 4, hipMemcpyDeviceToHost, c->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
     }
+    (void)hipFree(tmp);
+    if (e != hipSuccess) return fail(c, QORA_HIP_E_DEVICE, std::string("kv_download: ") + hipGetErrorString(e));
     return QORA_HIP_OK;
 }
 

@@ -272,15 +272,40 @@ hipError_t launch_gemv_tile(int fmt, const GemvPlan& plan, const GemvParams& p, 
     return hipGetLastError();
 }
 
-__global__ __launch_bounds__(256) void f32_to_f16_kernel(const float* src, uint16_t* dst, uint64_t n) {
-    for (uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x; i < n; i += (uint64_t)gridDim.x * 256u)
-        dst[i] = f2h(src[i]);
+// Element i of the token-major rows [len][kvh][hd] sits at ((h * cap + t) * hd + d) of one
+// layer's head-major cache [kvh][cap][hd]; TO_CACHE moves rows into the cache, else back out.
+template <bool TO_CACHE, bool F16>
+__global__ __launch_bounds__(256) void kv_move_kernel(float* rows, void* cache, uint32_t len, uint32_t kvh,
+                                                      uint32_t hd, uint64_t cap) {
+    const uint64_t row = (uint64_t)kvh * hd, n = (uint64_t)len * row;
+    for (uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x; i < n; i += (uint64_t)gridDim.x * 256u) {
+        const uint64_t t = i / row;
+        const uint32_t r = (uint32_t)(i - t * row);
+        const uint32_t h = r / hd, d = r - h * hd;
+        const uint64_t o = ((uint64_t)h * cap + t) * hd + d;
+        if constexpr (TO_CACHE) {
+            if constexpr (F16) ((uint16_t*)cache)[o] = f2h(rows[i]);
+            else ((float*)cache)[o] = rows[i];
+        } else {
+            if constexpr (F16) rows[i] = h2f(((const uint16_t*)cache)[o]);
+            else rows[i] = ((const float*)cache)[o];
+        }
+    }
 }
 
-hipError_t launch_f32_to_f16(const float* src, uint16_t* dst, uint64_t n, hipStream_t stream) {
+hipError_t launch_kv_move(bool to_cache, bool f16, float* rows, void* cache, uint32_t len, uint32_t kvh, uint32_t hd,
+                          uint64_t cap, hipStream_t stream) {
+    const uint64_t n = (uint64_t)len * kvh * hd;
     if (n == 0) return hipSuccess;
-    const uint32_t blocks = (uint32_t)std::min<uint64_t>(4096, (n + 255) / 256);
-    hipLaunchKernelGGL(f32_to_f16_kernel, dim3(blocks), dim3(256), 0, stream, src, dst, n);
+    if (len > cap || hd == 0) return hipErrorInvalidValue;
+    const dim3 grid((uint32_t)std::min<uint64_t>(4096, (n + 255) / 256)), block(256);
+    if (to_cache) {
+        if (f16) hipLaunchKernelGGL((kv_move_kernel<true, true>), grid, block, 0, stream, rows, cache, len, kvh, hd, cap);
+        else hipLaunchKernelGGL((kv_move_kernel<true, false>), grid, block, 0, stream, rows, cache, len, kvh, hd, cap);
+    } else {
+        if (f16) hipLaunchKernelGGL((kv_move_kernel<false, true>), grid, block, 0, stream, rows, cache, len, kvh, hd, cap);
+        else hipLaunchKernelGGL((kv_move_kernel<false, false>), grid, block, 0, stream, rows, cache, len, kvh, hd, cap);
+    }
     return hipGetLastError();
 }
 

@@ -53,8 +53,10 @@ void gemv_tile_bytes(int fmt, const GemvPlan& plan, uint64_t* w_bytes, uint64_t*
 hipError_t launch_gemv_tile(int fmt, const GemvPlan& plan, const GemvParams& p, uint8_t* tw, uint16_t* ts,
                             int8_t* te, hipStream_t stream);
 hipError_t launch_fill_zero(long long* p, uint64_t n, hipStream_t stream);
-// dst[i] = binary16(src[i]), round to nearest even
-hipError_t launch_f32_to_f16(const float* src, uint16_t* dst, uint64_t n, hipStream_t stream);
+// One layer's KV cache [kvh][cap][hd] (f32, or binary16 rounded to nearest even) from / to the
+// token-major rows [len][kvh][hd] f32 (to_cache: rows -> cache).
+hipError_t launch_kv_move(bool to_cache, bool f16, float* rows, void* cache, uint32_t len, uint32_t kvh, uint32_t hd,
+                          uint64_t cap, hipStream_t stream);
 hipError_t launch_acc_to_f32(const long long* acc, uint32_t n, int paired, float* y, hipStream_t stream);
 
 // Row-dot GEMV (lm_head). blocks: grid size (also the argmax partial count).
