@@ -11,6 +11,12 @@
 //
 // Attention (gemv.rs:914-989, softmax_raw gemv.rs:782-793) of head h over
 // KV head h / groups, positions [0, L), L = *pos + 1:
+//   * the kernel is compiled per pass count NP (32 positions a pass, contexts
+//     32 (NP - 1) < L <= 32 NP; the host picks the variant from the position
+//     it appends), so every loop is unrolled to its live passes and only the
+//     last pass needs masks. The rows of passes 0 .. NP - 2 lie below the
+//     appended position whatever it is: their loads go out before the
+//     position arrives;
 //   * q, the appended k row and v row: RMSNorm factor of the q|k|v GEMV input
 //     applied to the fixed-point sums, q and k rotated at position L - 1
 //     (apply_rope_raw, gemv.rs:903-906); the workgroup of column tile 0 of the
@@ -18,11 +24,12 @@
 //     (gemv.rs:909-911), every workgroup uses them from LDS;
 //   * all 8 waves take positions: lane (c, j) = (lane % 16, lane / 16) of wave
 //     w holds position 32 i + 4 w + j of pass i and dims 64 u + 4 c .. + 3, so
-//     each load instruction reads four whole rows; passes are loaded in
-//     blocks of kFusedPasses (K and V together) before any arithmetic;
+//     each load instruction reads four whole rows;
 //   * a row's partial dots are summed over its 16 lanes by a DPP butterfly
-//     (every lane gets the same bits); each wave keeps its own running max,
-//     sum and p.V, merged in wave order at the end.
+//     (every lane gets the same bits); each wave takes its softmax over all
+//     its positions at once (max, then 2^(s - max) and p.V), sums its four
+//     row slots with lane-swap instructions, and the 8 waves' states are
+//     merged in wave order at the end.
 // The cache rows read are those below L - 1 (written by earlier steps), so
 // the row being appended is never read while it is written.
 #pragma once
@@ -36,24 +43,31 @@
 
 namespace qora {
 
-constexpr int kFusedWaves = 8;          // waves per workgroup, all in the attention
-constexpr uint32_t kFusedPass = 32;     // positions per pass: 8 waves x 4 row slots
-constexpr int kFusedPasses = 8;         // passes loaded together (256 positions)
-
 template <bool F16KV>
 __device__ __forceinline__ float4 kv_word_f32(typename std::conditional<F16KV, uint2, float4>::type w) {
     if constexpr (F16KV) return kv_words_f32(w);
     else return w;
 }
 
-template <int HD, bool F16KV>
+// Sum of v over lanes l, l ^ 16, l ^ 32 and l ^ 48 (the four row slots of a
+// wave), the same bits in all four: each lane-swap instruction leaves lane l's
+// partner value in one of its two results, so their sum is v[l] + v[l ^ 16]
+// (then ^ 32) in every lane.
+__device__ __forceinline__ float sum_row_slots(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+template <int HD, bool F16KV, int NP>
 __global__ __launch_bounds__(kFusedWaves * kWave) void gemv_q4m_attn_kernel(AttnOParams ap) {
     constexpr int GW = 1, NW = 4;
     constexpr int KW = HD;                  // one query head per K slice
     constexpr int NKB = KW / 64, NZ = GW * KW / 64;
     constexpr int NQ = HD / 64;             // dim quads per lane
-    constexpr int PB = kFusedPasses;
     static_assert(HD == 64 || HD == 128, "head_dim 64 or 128");
+    static_assert(NP >= 1 && NP <= kFusedMaxPasses, "1 to 8 passes");
     using W = typename std::conditional<F16KV, uint2, float4>::type;
     kernarg_warm(ap);
     const GemvParams& p = ap.g;
@@ -81,56 +95,60 @@ __global__ __launch_bounds__(kFusedWaves * kWave) void gemv_q4m_attn_kernel(Attn
     const uint32_t qd = a.H * HD, kvd = a.KVH * HD;
     const uint64_t cps = kv_pos_stride(a), coff = kv_head_off(a, kvh);
 
-    // ---- the position first: every cache address depends on it ----
-    int32_t pos_raw = __builtin_amdgcn_readfirstlane(*a.pos);
-    sgpr_pin(pos_raw);
-    const uint32_t L = (uint32_t)pos_raw + 1u;
-    const uint32_t cur = L - 1u;                       // position appended this step
-
-    // ---- cache rows of the first block's live passes, then the q|k|v sums
-    // and (matrix-core waves) the work item's scales and weights: loads
-    // complete in issue order, and the rows are needed first ----
     const uint32_t c = (uint32_t)lane % 16, j = (uint32_t)lane / 16;
-    const uint32_t slot = 4u * (uint32_t)wave + j;     // position of pass i: b0 + 32 i + slot
+    const uint32_t slot = 4u * (uint32_t)wave + j;     // position of pass i: 32 i + slot
     const uint8_t* kcache = reinterpret_cast<const uint8_t*>(a.kc);
     const uint8_t* vcache = reinterpret_cast<const uint8_t*>(a.vc);
     constexpr uint32_t EB = F16KV ? 2u : 4u;
-    W kr[PB][NQ], vr[PB][NQ];
-    // passes of the block at b0 holding positions below L (wave-uniform)
-    auto live_passes = [&](uint32_t b0) { return min((uint32_t)PB, (L - b0 + kFusedPass - 1) / kFusedPass); };
-    // Register slot i holds pass (i + rot) mod np: the workgroups of an XCD
-    // read the same rows, and staggering their order spreads the requests
-    // over the L2 channels instead of all asking for the same lines at once.
-    const uint32_t rot = blockIdx.x / 8u;
-    auto pass_base = [&](uint32_t b0, uint32_t i, uint32_t np) { return b0 + kFusedPass * ((i + rot) % np); };
-    auto load_block = [&](uint32_t b0) {
-        // rows >= cur are not read (clamped to cur - 1, discarded below); none when cur == 0
-        const uint32_t np = cur == 0 ? 0u : live_passes(b0);
+    W kr[NP][NQ], vr[NP][NQ];
+    auto load_row = [&](int i, uint32_t pos) {
 #pragma unroll
-        for (int i = 0; i < PB; ++i) {
-            if ((uint32_t)i < np) {
-                const uint32_t pos = min(pass_base(b0, (uint32_t)i, np) + slot, cur - 1u);
-#pragma unroll
-                for (int u = 0; u < NQ; ++u) {
-                    const uint64_t off = ((uint64_t)pos * cps + coff + 64u * (uint32_t)u + 4u * c) * EB;
-                    kr[i][u] = *reinterpret_cast<const W*>(kcache + off);
-                    vr[i][u] = *reinterpret_cast<const W*>(vcache + off);
-                }
-            } else {
-#pragma unroll
-                for (int u = 0; u < NQ; ++u) {
-                    kr[i][u] = W{};
-                    vr[i][u] = W{};
-                }
-            }
+        for (int u = 0; u < NQ; ++u) {
+            const uint64_t off = ((uint64_t)pos * cps + coff + 64u * (uint32_t)u + 4u * c) * EB;
+            kr[i][u] = *reinterpret_cast<const W*>(kcache + off);
+            vr[i][u] = *reinterpret_cast<const W*>(vcache + off);
         }
     };
-    load_block(0);
-    // ---- q|k|v sums of the head (waves NW.., one dim per thread): issued
-    // after the cache rows, so their arithmetic waits for both at once ----
+    // ---- passes 0 .. NP-2: positions below 32 (NP - 1) <= L - 1, cached
+    // rows whose addresses do not depend on the position ----
+#pragma unroll
+    for (int i = 0; i < NP - 1; ++i) load_row(i, kFusedPass * (uint32_t)i + slot);
+
     const bool qkv_wave = wave >= NW && wave < NW + HD / kWave;
     const uint32_t d = (uint32_t)(t - NW * kWave) % HD;
     const uint32_t pd = rope_partner(d, a.half);
+
+    // ---- the position, then the last pass: rows at or past the appended
+    // position are not read (address clamped below it, or to row 0 when it
+    // is 0; those values are replaced or masked below) ----
+    int32_t pos_raw = ld_scalar_i32(a.pos);
+    sgpr_pin(pos_raw);
+    const uint32_t L = (uint32_t)pos_raw + 1u;
+    const uint32_t cur = L - 1u;                       // position appended this step
+    const uint32_t plast = kFusedPass * (uint32_t)(NP - 1) + slot;
+    load_row(NP - 1, cur == 0u ? 0u : min(plast, cur - 1u));
+    float rc = 1.f, rs = 0.f;
+    if (qkv_wave && a.use_rope && d < 2 * a.half) {
+        const uint32_t td = d < a.half ? d : d - a.half;
+        rc = a.rope_cos[(uint64_t)cur * a.half + td];
+        rs = a.rope_sin[(uint64_t)cur * a.half + td];
+    }
+
+    // ---- the matrix-core waves' scales and weights. Waves NW.. issue the
+    // same loads as wave - NW (the lines are already in flight): every wave
+    // then has the same loads outstanding after its cache rows, so its first
+    // use of the rows waits for the rows alone, not for these ----
+    uint4 wq[GW][NKB];
+    uint32_t sw[(NZ + 1) / 2];
+    int esg[GW];
+    const uint32_t mwave = (uint32_t)wave % NW;
+    gemv_q4m_load_scales<GW, NZ>(p, (uint64_t)item * NW + mwave, lane, sw, esg);
+    gemv_q4m_load_weights<GW, NKB>(p, (uint64_t)item * NW + mwave, lane, wq);
+    GemvOut<GW> out{};
+    if (wave < NW) out = gemv_q4m_out<GW>(p, tile, wave);
+    __builtin_amdgcn_sched_barrier(0);
+    // ---- q|k|v sums of the head (waves NW.., one dim per thread), issued
+    // last: their arithmetic then waits for every load above at once ----
     long long qa = 0, qb = 0, ka = 0, kb = 0, va = 0;
     float ssp = 0.f;
     if (qkv_wave) {
@@ -140,22 +158,6 @@ __global__ __launch_bounds__(kFusedWaves * kWave) void gemv_q4m_attn_kernel(Attn
         kb = a.qkv_acc[qd + (uint64_t)kvh * HD + pd];
         va = a.qkv_acc[qd + kvd + (uint64_t)kvh * HD + d];
         ssp = a.ss_in[min((uint32_t)lane, a.ss_n - 1u)];
-    }
-    float rc = 1.f, rs = 0.f;
-    if (qkv_wave && a.use_rope && d < 2 * a.half) {
-        const uint32_t td = d < a.half ? d : d - a.half;
-        rc = a.rope_cos[(uint64_t)cur * a.half + td];
-        rs = a.rope_sin[(uint64_t)cur * a.half + td];
-    }
-
-    uint4 wq[GW][NKB];
-    uint32_t sw[(NZ + 1) / 2];
-    int esg[GW];
-    GemvOut<GW> out{};
-    if (wave < NW) {
-        gemv_q4m_load_scales<GW, NZ>(p, (uint64_t)item * NW + wave, lane, sw, esg);
-        gemv_q4m_load_weights<GW, NKB>(p, (uint64_t)item * NW + wave, lane, wq);
-        out = gemv_q4m_out<GW>(p, tile, wave);
     }
 
     if (qkv_wave) {
@@ -198,96 +200,73 @@ __global__ __launch_bounds__(kFusedWaves * kWave) void gemv_q4m_attn_kernel(Attn
         q[u][2] = v.z;
         q[u][3] = v.w;
     }
+    // ---- scores of the lane's positions, in log2 units (scale * log2 e):
+    // the weights 2^(s - m) equal e^(s' - m') of the natural-log scores. In
+    // the last pass the appended position takes its k row from LDS and the
+    // positions past it are masked ----
     const float scale2 = a.scale * 1.4426950408889634f;   // log2(e)
-    float m_w = -INFINITY, l_w = 0.f;
+    const bool last_cur = plast == cur, last_live = plast <= cur;
+    float s[NP];
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+        float dot = 0.f;
+#pragma unroll
+        for (int u = 0; u < NQ; ++u) {
+            float4 k = kv_word_f32<F16KV>(kr[i][u]);
+            if (i == NP - 1 && last_cur) k = *reinterpret_cast<const float4*>(kn + 64 * u + 4 * c);
+            dot = fmaf(q[u][0], k.x, dot);
+            dot = fmaf(q[u][1], k.y, dot);
+            dot = fmaf(q[u][2], k.z, dot);
+            dot = fmaf(q[u][3], k.w, dot);
+        }
+        dot = row16_sum(dot) * scale2;
+        s[i] = (i < NP - 1 || last_live) ? dot : -INFINITY;
+    }
+    // ---- the wave's softmax over its positions and p.V (a wave with no
+    // live position keeps m = -inf, l = 0, p.V = 0) ----
+    float mx = s[0];
+#pragma unroll
+    for (int i = 1; i < NP; ++i) mx = fmaxf(mx, s[i]);
+    mx = wave_max(mx);
+    const float mref = mx == -INFINITY ? 0.f : mx;
+    float sum = 0.f;
     float o[NQ][4];
 #pragma unroll
     for (int u = 0; u < NQ; ++u)
 #pragma unroll
         for (int e = 0; e < 4; ++e) o[u][e] = 0.f;
-
-    for (uint32_t b0 = 0; b0 < L; b0 += kFusedPass * PB) {
-        if (b0 > 0) load_block(b0);
-        const uint32_t np = live_passes(b0);
-        // ---- scores of the lane's positions, in log2 units (scale * log2 e):
-        // the weights 2^(s - m) equal e^(s' - m') of the natural-log scores.
-        // A pass wholly below cur reads only cached rows; the pass holding
-        // cur (and any rows past L) takes the selects ----
-        float s[PB];
 #pragma unroll
-        for (int i = 0; i < PB; ++i) {
-            s[i] = -INFINITY;
-            if ((uint32_t)i >= np) continue;
-            const uint32_t base = pass_base(b0, (uint32_t)i, np);
-            const uint32_t pos = base + slot;
-            const bool plain = base + kFusedPass <= cur;   // wave-uniform
-            float dot = 0.f;
+    for (int i = 0; i < NP; ++i) {
+        const float p_i = exp2f(s[i] - mref);      // 0 where masked
+        sum += p_i;
 #pragma unroll
-            for (int u = 0; u < NQ; ++u) {
-                float4 k = kv_word_f32<F16KV>(kr[i][u]);
-                if (!plain && pos == cur) k = *reinterpret_cast<const float4*>(kn + 64 * u + 4 * c);
-                dot = fmaf(q[u][0], k.x, dot);
-                dot = fmaf(q[u][1], k.y, dot);
-                dot = fmaf(q[u][2], k.z, dot);
-                dot = fmaf(q[u][3], k.w, dot);
+        for (int u = 0; u < NQ; ++u) {
+            float4 v = kv_word_f32<F16KV>(vr[i][u]);
+            if (i == NP - 1) {
+                if (last_cur) v = *reinterpret_cast<const float4*>(vn + 64 * u + 4 * c);
+                if (!last_live) v = make_float4(0.f, 0.f, 0.f, 0.f);   // select: stale bits never reach the sum
             }
-            dot = row16_sum(dot) * scale2;
-            s[i] = (plain || pos < L) ? dot : -INFINITY;
+            o[u][0] = fmaf(p_i, v.x, o[u][0]);
+            o[u][1] = fmaf(p_i, v.y, o[u][1]);
+            o[u][2] = fmaf(p_i, v.z, o[u][2]);
+            o[u][3] = fmaf(p_i, v.w, o[u][3]);
         }
-        // ---- the wave's running softmax state and p.V ----
-        float mx = s[0];
-#pragma unroll
-        for (int i = 1; i < PB; ++i) mx = fmaxf(mx, s[i]);
-        mx = wave_max(mx);
-        if (mx == -INFINITY) continue;                 // no position of this wave in the block
-        const float m_new = fmaxf(m_w, mx);
-        const float f = exp2f(m_w - m_new);            // 0 while m_w = -inf
-        float sum = 0.f;
-#pragma unroll
-        for (int u = 0; u < NQ; ++u)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) o[u][e] *= f;
-#pragma unroll
-        for (int i = 0; i < PB; ++i) {
-            if ((uint32_t)i >= np) continue;
-            const uint32_t base = pass_base(b0, (uint32_t)i, np);
-            const uint32_t pos = base + slot;
-            const bool plain = base + kFusedPass <= cur;   // wave-uniform
-            const float p_i = (plain || pos < L) ? exp2f(s[i] - m_new) : 0.f;
-            sum += p_i;
-#pragma unroll
-            for (int u = 0; u < NQ; ++u) {
-                float4 v = kv_word_f32<F16KV>(vr[i][u]);
-                if (!plain) {
-                    if (pos == cur) v = *reinterpret_cast<const float4*>(vn + 64 * u + 4 * c);
-                    if (pos >= L) v = make_float4(0.f, 0.f, 0.f, 0.f);   // select: stale bits never reach the sum
-                }
-                o[u][0] = fmaf(p_i, v.x, o[u][0]);
-                o[u][1] = fmaf(p_i, v.y, o[u][1]);
-                o[u][2] = fmaf(p_i, v.z, o[u][2]);
-                o[u][3] = fmaf(p_i, v.w, o[u][3]);
-            }
-        }
-        // each row slot counted once (its 16 lanes hold the same weights)
-        l_w = l_w * f + wave_sum(c == 0 ? sum : 0.f);
-        m_w = m_new;
     }
+    // each row slot counted once (its 16 lanes hold the same weights)
+    const float l_w = wave_sum(c == 0 ? sum : 0.f);
 
     // ---- merge: the wave's 4 row slots, then the 8 waves in order ----
 #pragma unroll
     for (int u = 0; u < NQ; ++u)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            o[u][e] += __shfl_xor(o[u][e], 16, kWave);
-            o[u][e] += __shfl_xor(o[u][e], 32, kWave);
-        }
+        for (int e = 0; e < 4; ++e) o[u][e] = sum_row_slots(o[u][e]);
     if (j == 0) {
 #pragma unroll
         for (int u = 0; u < NQ; ++u)
             *reinterpret_cast<float4*>(&accs[wave][64 * u + 4 * c]) = make_float4(o[u][0], o[u][1], o[u][2], o[u][3]);
     }
     if (lane == 0) {
-        mls[wave][0] = m_w;
+        mls[wave][0] = mx;
         mls[wave][1] = l_w;
     }
     __syncthreads();

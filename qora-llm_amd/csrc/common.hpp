@@ -123,6 +123,15 @@ __device__ __forceinline__ T* sgpr_ptr(T* p) {
     return (T*)g;
 }
 
+// A wave-uniform int32 read with a scalar load (through the constant address
+// space): its wait counts scalar loads only, so vector loads issued before it
+// stay in flight while it is waited for. The value must not change while the
+// kernel runs (the scalar cache is invalidated at each kernel start).
+__device__ __forceinline__ int32_t ld_scalar_i32(const int32_t* p) {
+    using C = const __attribute__((address_space(4))) int32_t;
+    return *(C*)reinterpret_cast<uint64_t>(p);
+}
+
 __device__ __forceinline__ float from_fixed(long long a) {
     return (float)((double)a * (1.0 / kFixScale));
 }

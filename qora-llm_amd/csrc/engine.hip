@@ -113,8 +113,10 @@ struct ModelState {
     EmbedParams p_emb_tok{}, p_emb_prompt{};
     hipGraphExec_t g_step = nullptr;
     hipGraphExec_t g_prefill = nullptr;
-    hipGraphExec_t g_step_ao = nullptr;      // the same steps with the fused attention + o kernel
-    hipGraphExec_t g_prefill_ao = nullptr;
+    // the same steps with the fused attention + o kernel, one per pass count
+    // (index np - 1: contexts of 32 (np - 1) < L <= 32 np positions)
+    hipGraphExec_t g_step_ao[kFusedMaxPasses] = {};
+    hipGraphExec_t g_prefill_ao[kFusedMaxPasses] = {};
     uint64_t host_pos = 0;
     // token id that d_token holds once the queued work is done (-1: not known):
     // a decode call passing that id skips the upload
@@ -279,8 +281,10 @@ void free_model(qora_hip_ctx* c) {
     (void)hipStreamSynchronize(c->stream);
     if (m.g_step) (void)hipGraphExecDestroy(m.g_step);
     if (m.g_prefill) (void)hipGraphExecDestroy(m.g_prefill);
-    if (m.g_step_ao) (void)hipGraphExecDestroy(m.g_step_ao);
-    if (m.g_prefill_ao) (void)hipGraphExecDestroy(m.g_prefill_ao);
+    for (hipGraphExec_t g : m.g_step_ao)
+        if (g) (void)hipGraphExecDestroy(g);
+    for (hipGraphExec_t g : m.g_prefill_ao)
+        if (g) (void)hipGraphExecDestroy(g);
     for (void* p : m.allocs) (void)hipFree(p);
     m = ModelState();
 }
@@ -324,15 +328,16 @@ int pack_model_gemv(qora_hip_ctx* c, int fmt, const GemvPlan& pl, GemvParams* p)
     return QORA_HIP_OK;
 }
 
-// fused: attention inside the o GEMV (short contexts, see attn_o_max)
-int record_step(qora_hip_ctx* c, bool with_lm_head, bool fused) {
+// np > 0: attention inside the o GEMV for contexts of at most 32 np
+// positions (short contexts, see attn_o_max); np = 0: split attention
+int record_step(qora_hip_ctx* c, bool with_lm_head, uint32_t np) {
     ModelState& m = c->m;
     const hipStream_t s = c->stream;
     HIP_TRY(c, launch_embed(with_lm_head ? m.p_emb_tok : m.p_emb_prompt, s));
     for (uint32_t l = 0; l < m.L; ++l) {
         HIP_TRY(c, launch_gemv(m.fmt, m.pl_qkv, m.p_qkv[l], s));
-        if (fused) {
-            HIP_TRY(c, launch_attn_o(m.pl_o, m.p_ao[l], s));
+        if (np) {
+            HIP_TRY(c, launch_attn_o(m.pl_o, m.p_ao[l], np, s));
         } else {
             HIP_TRY(c, launch_attn(m.p_attn[l], s));
             HIP_TRY(c, launch_gemv(m.fmt, m.pl_o, m.p_o[l], s));
@@ -362,15 +367,22 @@ uint32_t attn_nsg(uint32_t max_chunk) {
 
 // Steps that append a position below this bound run attention inside the o
 // GEMV (gemv_q4m_attn_kernel): every workgroup reads its head's whole
-// context, so the fused step pays off only while the context is short.
-// QORA_HIP_ATTN_O overrides the bound (0: never fused).
-constexpr uint32_t kAttnODefaultMax = 256;
+// context, so the fused step pays off only while the context is short; the
+// kernel takes at most kFusedMaxPasses passes of 32 positions. QORA_HIP_ATTN_O
+// lowers the bound (0: never fused).
+constexpr uint32_t kAttnODefaultMax = kFusedPass * kFusedMaxPasses;
 
 uint32_t attn_o_limit(const ModelState& m) {
     if (m.fmt != FMT_Q4 || !attn_o_supported(m.pl_o, m.hd, m.H, m.groups)) return 0;
     const char* v = std::getenv("QORA_HIP_ATTN_O");
     const long n = (v && *v) ? std::atol(v) : (long)kAttnODefaultMax;
-    return n <= 0 ? 0u : (uint32_t)std::min<long>(n, (long)m.cap);
+    return n <= 0 ? 0u : (uint32_t)std::min<long>(std::min<long>(n, (long)kAttnODefaultMax), (long)m.cap);
+}
+
+// Pass count of the fused kernel for the step that appends `pos` (its context
+// is pos + 1 positions), 0 for the split attention.
+uint32_t fused_passes(const ModelState& m, uint64_t pos) {
+    return pos < (uint64_t)m.attn_o_max ? (uint32_t)(pos / kFusedPass) + 1u : 0u;
 }
 
 bool eager_mode() {
@@ -381,16 +393,17 @@ bool eager_mode() {
 // pos: the position the step appends (its context length is pos + 1).
 int launch_step(qora_hip_ctx* c, bool with_lm_head, uint64_t pos) {
     ModelState& m = c->m;
-    const bool fused = pos < (uint64_t)m.attn_o_max;
-    if (eager_mode()) return record_step(c, with_lm_head, fused);
-    hipGraphExec_t g = fused ? (with_lm_head ? m.g_step_ao : m.g_prefill_ao) : (with_lm_head ? m.g_step : m.g_prefill);
+    const uint32_t np = fused_passes(m, pos);
+    if (eager_mode()) return record_step(c, with_lm_head, np);
+    hipGraphExec_t g = np ? (with_lm_head ? m.g_step_ao[np - 1] : m.g_prefill_ao[np - 1])
+                          : (with_lm_head ? m.g_step : m.g_prefill);
     HIP_TRY(c, hipGraphLaunch(g, c->stream));
     return QORA_HIP_OK;
 }
 
-int capture_step(qora_hip_ctx* c, bool with_lm_head, bool fused, hipGraphExec_t* out) {
+int capture_step(qora_hip_ctx* c, bool with_lm_head, uint32_t np, hipGraphExec_t* out) {
     HIP_TRY(c, hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
-    const int rc = record_step(c, with_lm_head, fused);
+    const int rc = record_step(c, with_lm_head, np);
     hipGraph_t g = nullptr;
     const hipError_t e = hipStreamEndCapture(c->stream, &g);
     if (rc) {
@@ -856,11 +869,12 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
                                  m.vocab, m.d_prompt, m.d_pos, m.d_xacc};
 
     HIP_TRY(c, hipDeviceSynchronize());
-    if (int rc = capture_step(c, true, false, &m.g_step)) { free_model(c); return rc; }
-    if (int rc = capture_step(c, false, false, &m.g_prefill)) { free_model(c); return rc; }
-    if (m.attn_o_max) {
-        if (int rc = capture_step(c, true, true, &m.g_step_ao)) { free_model(c); return rc; }
-        if (int rc = capture_step(c, false, true, &m.g_prefill_ao)) { free_model(c); return rc; }
+    if (int rc = capture_step(c, true, 0, &m.g_step)) { free_model(c); return rc; }
+    if (int rc = capture_step(c, false, 0, &m.g_prefill)) { free_model(c); return rc; }
+    // one fused variant per pass count a step below attn_o_max can need
+    for (uint32_t np = 1; m.attn_o_max && np <= (m.attn_o_max - 1) / kFusedPass + 1; ++np) {
+        if (int rc = capture_step(c, true, np, &m.g_step_ao[np - 1])) { free_model(c); return rc; }
+        if (int rc = capture_step(c, false, np, &m.g_prefill_ao[np - 1])) { free_model(c); return rc; }
     }
     m.host_pos = 0;
     m.ready = true;

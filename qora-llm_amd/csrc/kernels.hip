@@ -433,17 +433,30 @@ bool attn_o_supported(const GemvPlan& pl, uint32_t hd, uint32_t H, uint32_t grou
            groups >= 1 && groups <= (uint32_t)kAttnMaxGroups;
 }
 
-hipError_t launch_attn_o(const GemvPlan& pl, const AttnOParams& p, hipStream_t stream) {
-    if (p.g.zero_ptr) return hipErrorInvalidValue;   // the fused kernel clears nothing
+template <int HD, bool F16KV>
+static hipError_t launch_attn_o_hd(const GemvPlan& pl, const AttnOParams& p, uint32_t np, hipStream_t stream) {
     const dim3 grid(pl.blocks()), block(kFusedWaves * kWave);
-    if (p.a.hd == 128) {
-        if (p.a.kv_f16) hipLaunchKernelGGL((gemv_q4m_attn_kernel<128, true>), grid, block, 0, stream, p);
-        else hipLaunchKernelGGL((gemv_q4m_attn_kernel<128, false>), grid, block, 0, stream, p);
-    } else {
-        if (p.a.kv_f16) hipLaunchKernelGGL((gemv_q4m_attn_kernel<64, true>), grid, block, 0, stream, p);
-        else hipLaunchKernelGGL((gemv_q4m_attn_kernel<64, false>), grid, block, 0, stream, p);
+    switch (np) {
+    case 1: hipLaunchKernelGGL((gemv_q4m_attn_kernel<HD, F16KV, 1>), grid, block, 0, stream, p); break;
+    case 2: hipLaunchKernelGGL((gemv_q4m_attn_kernel<HD, F16KV, 2>), grid, block, 0, stream, p); break;
+    case 3: hipLaunchKernelGGL((gemv_q4m_attn_kernel<HD, F16KV, 3>), grid, block, 0, stream, p); break;
+    case 4: hipLaunchKernelGGL((gemv_q4m_attn_kernel<HD, F16KV, 4>), grid, block, 0, stream, p); break;
+    case 5: hipLaunchKernelGGL((gemv_q4m_attn_kernel<HD, F16KV, 5>), grid, block, 0, stream, p); break;
+    case 6: hipLaunchKernelGGL((gemv_q4m_attn_kernel<HD, F16KV, 6>), grid, block, 0, stream, p); break;
+    case 7: hipLaunchKernelGGL((gemv_q4m_attn_kernel<HD, F16KV, 7>), grid, block, 0, stream, p); break;
+    case 8: hipLaunchKernelGGL((gemv_q4m_attn_kernel<HD, F16KV, 8>), grid, block, 0, stream, p); break;
+    default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
+}
+
+hipError_t launch_attn_o(const GemvPlan& pl, const AttnOParams& p, uint32_t np, hipStream_t stream) {
+    if (p.g.zero_ptr) return hipErrorInvalidValue;   // the fused kernel clears nothing
+    if (p.a.hd == 128) {
+        return p.a.kv_f16 ? launch_attn_o_hd<128, true>(pl, p, np, stream)
+                          : launch_attn_o_hd<128, false>(pl, p, np, stream);
+    }
+    return p.a.kv_f16 ? launch_attn_o_hd<64, true>(pl, p, np, stream) : launch_attn_o_hd<64, false>(pl, p, np, stream);
 }
 
 hipError_t launch_attn_combine(const AttnCombineParams& p, hipStream_t stream) {

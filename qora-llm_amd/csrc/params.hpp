@@ -219,6 +219,11 @@ constexpr int kAttnSub = 32;         // positions staged in LDS at a time
 constexpr int kAttnMaxHd = 128;
 constexpr int kAttnMaxGroups = 4;
 constexpr int kAttnMaxSplits = 64;
+// fused short-context attention + o (gemv_q4m_attn_kernel): 32-position
+// passes, 8 waves x 4 row slots, at most 8 passes (256 positions)
+constexpr int kFusedWaves = 8;
+constexpr uint32_t kFusedPass = 32;
+constexpr int kFusedMaxPasses = 8;
 
 struct AttnParams {
     const float* q;            // kernel-level: q [H*hd] fp32, already rotated

@@ -2,8 +2,8 @@
 computed inside the o-projection kernel (gemv_q4m_attn_kernel) for steps that
 append a position below qora_hip_attn_o_limit, the split attention kernel
 above it. Both against the oracle (gemv.rs:914-989 inside forward_decode_raw,
-gemv.rs:872-1019), across the bound, from the first position, over several
-256-position blocks, and with f32 and f16 caches."""
+gemv.rs:872-1019), across the bound, from the first position, at every
+compiled pass count, and with f32 and f16 caches."""
 import numpy as np
 import pytest
 
@@ -35,6 +35,8 @@ def test_limit_policy(ctx, pkg, monkeypatch):
     assert pkg.HipBackend(ctx, w, kv_capacity=128).attn_o_limit() == 0
     monkeypatch.setenv("QORA_HIP_ATTN_O", "40")
     assert pkg.HipBackend(ctx, _model(pkg, 128), kv_capacity=128).attn_o_limit() == 40
+    monkeypatch.setenv("QORA_HIP_ATTN_O", "640")                # the kernel takes at most 256 positions
+    assert pkg.HipBackend(ctx, _model(pkg, 128), kv_capacity=1024).attn_o_limit() == 256
     monkeypatch.delenv("QORA_HIP_ATTN_O")
     # F16 weights run the VALU GEMVs: no fused step
     assert pkg.HipBackend(ctx, _model(pkg, 64, fmt=0), kv_capacity=128).attn_o_limit() == 0
@@ -88,42 +90,47 @@ def test_fused_from_the_first_position(ctx, pkg, orc, monkeypatch, hd):
 
 
 @pytest.mark.parametrize("kv_dtype", [0, 1])
-def test_fused_over_several_blocks(ctx, pkg, orc, monkeypatch, kv_dtype):
-    """Bound raised to 640: contexts of 501..504 positions take two 256-position
-    blocks per workgroup, the appended row in the second."""
-    print(f"case attn_o blocks kv={kv_dtype}", flush=True)
-    monkeypatch.setenv("QORA_HIP_ATTN_O", "640")
-    cap, n = 640, 500
+def test_fused_every_pass_count(ctx, pkg, orc, kv_dtype):
+    """The fused kernel is compiled per count of 32-position passes (1..8).
+    Caches of n uploaded positions, then two steps appending n and n + 1,
+    for n around every pass boundary: each pass count, the appended row as
+    the first, a middle and the last position of its pass, and the step from
+    the last fused position (255) to the split kernel (256)."""
+    print(f"case attn_o pass counts kv={kv_dtype}", flush=True)
+    cap = 320
     w = _model(pkg, 128, positions=cap, seed=5)
     be = pkg.HipBackend(ctx, w, kv_capacity=cap, kv_dtype=kv_dtype)
-    assert be.attn_o_limit() == 640
+    assert be.attn_o_limit() == 256
     om = orc.OracleModel(w, kv_capacity=cap, T=4)
     r = np.random.default_rng(21)
     kvd = w.config.num_kv_heads * w.config.head_dim
-    for layer in range(w.config.num_layers):
-        k = r.standard_normal((n, kvd), dtype=np.float32)
-        v = r.standard_normal((n, kvd), dtype=np.float32)
-        if kv_dtype:
-            k, v = k.astype(np.float16).astype(np.float32), v.astype(np.float16).astype(np.float32)
-        be.kv_upload(layer, k, v)
-        om.kv_set(layer, k, v)
     tol = REL_TOL if kv_dtype == 0 else 5e-3
-    for t in pkg.synth_tokens(5, 2001, 4, w.config.vocab):
-        logits, _ = be.forward_decode_raw(int(t))
-        assert rel_err(logits, om.forward_decode(int(t))) <= tol
-    k, v = be.kv_layer(2)
-    kr, vr = om.kv_layer(2)
-    assert rel_err(k, kr) <= tol and rel_err(v, vr) <= tol
+    for n in (0, 1, 30, 31, 32, 45, 63, 64, 95, 96, 127, 150, 159, 191, 192, 223, 224, 240, 254, 255):
+        for layer in range(w.config.num_layers):
+            k = r.standard_normal((n, kvd), dtype=np.float32)
+            v = r.standard_normal((n, kvd), dtype=np.float32)
+            if kv_dtype:
+                k, v = k.astype(np.float16).astype(np.float32), v.astype(np.float16).astype(np.float32)
+            be.kv_upload(layer, k, v)
+            om.kv_set(layer, k, v)
+        for t in pkg.synth_tokens(5, 2001 + n, 2, w.config.vocab):
+            logits, _ = be.forward_decode_raw(int(t))
+            assert rel_err(logits, om.forward_decode(int(t))) <= tol, n
+        k, v = be.kv_layer(2)
+        kr, vr = om.kv_layer(2)
+        assert rel_err(k, kr) <= tol and rel_err(v, vr) <= tol, n
 
 
-def test_device_chained_greedy_crosses_the_bound(ctx, pkg, orc, monkeypatch):
+@pytest.mark.parametrize("bound,prompt_len", [(30, 10), (256, 25)])
+def test_device_chained_greedy_crosses_the_bound(ctx, pkg, orc, monkeypatch, bound, prompt_len):
     """generate_greedy launches every step from the host in one call; each
-    picks its graph by the position it appends."""
-    monkeypatch.setenv("QORA_HIP_ATTN_O", "30")
+    picks its graph by the position it appends: across the fused/split bound
+    (30), and across the fused kernel's pass counts (positions 25..64)."""
+    monkeypatch.setenv("QORA_HIP_ATTN_O", str(bound))
     w = _model(pkg, 128, positions=128, seed=6)
     be = pkg.HipBackend(ctx, w, kv_capacity=128)
     om = orc.OracleModel(w, kv_capacity=128, T=4)
-    prompt = pkg.synth_tokens(6, 2000, 10, w.config.vocab)
+    prompt = pkg.synth_tokens(6, 2000, prompt_len, w.config.vocab)
     ref, _ = om.greedy(prompt, 40)
     _, first = be.raw_prefill(prompt, want_logits=False)
     assert [first] + be.generate_greedy(first, 39).tolist() == ref
