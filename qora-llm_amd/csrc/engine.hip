@@ -12,6 +12,7 @@
 #include <cstdio>
 #include <string>
 #include <unordered_map>
+#include <initializer_list>
 #include <vector>
 
 using namespace qora;
@@ -137,6 +138,11 @@ struct ModelState {
     float* d_pf_part = nullptr;          // split-K partials of the GEMMs
     float* d_pf_apart = nullptr;         // key-chunk partials of the prefill attention
     std::vector<int8_t*> pf_wf;          // [L][7] Q4 group exponents
+    // Q4 weights packed for pf_gemm2_kernel ([L][7]), when every projection
+    // has k % 32 == 0 and n % 128 == 0; else the prefill runs pf_gemm_kernel
+    bool pf2 = false;
+    std::vector<uint2*> pf_wq;
+    std::vector<uint16_t*> pf_sc;
     LmHeadParams p_lmq_pf{};
     RowdotParams p_lm_pf{};
     ArgmaxFinishParams p_fin_pf{};
@@ -1062,6 +1068,19 @@ int pf_setup(qora_hip_ctx* c) {
                 if (sh.splits > 1) pb = std::max<uint64_t>(pb, (uint64_t)sh.splits * t * w->n * 4);
             }
         }
+        // the fused launches of the packed-weight GEMM: q|k|v, o, gate|up, down
+        m.pf2 = m.fmt == FMT_Q4 && pf_gemm2_supported(m.hidden, qd) && pf_gemm2_supported(m.hidden, kvd) &&
+                pf_gemm2_supported(qd, m.hidden) && pf_gemm2_supported(m.hidden, m.inter) &&
+                pf_gemm2_supported(m.inter, m.hidden);
+        if (m.pf2) {
+            const uint32_t shapes[4][2] = {{m.hidden, qd + 2 * kvd}, {qd, m.hidden}, {m.hidden, 2 * m.inter},
+                                           {m.inter, m.hidden}};
+            for (const auto& kn : shapes)
+                for (uint32_t t = 1; t <= tc; ++t) {
+                    const PfGemm2Shape sh = pf_gemm2_shape(t, kn[0], kn[1], c->cus);
+                    if (sh.splits > 1) pb = std::max<uint64_t>(pb, (uint64_t)sh.splits * t * kn[1] * 4);
+                }
+        }
         PF_ALLOC(d_pf_part, pb);
     }
 #undef PF_ALLOC
@@ -1085,6 +1104,22 @@ int pf_setup(qora_hip_ctx* c) {
                 m.pf_wf[(size_t)l * 7 + j] = (int8_t*)ptr;
                 HIP_TRY(c, launch_pf_weight_exp((const uint16_t*)w->scales, (uint32_t)w->k, groups, (int8_t*)ptr,
                                                 scratch, c->stream));
+            }
+    }
+    if (m.pf2) {
+        m.pf_wq.assign((size_t)m.L * 7, nullptr);
+        m.pf_sc.assign((size_t)m.L * 7, nullptr);
+        for (uint32_t l = 0; l < m.L; ++l)
+            for (int j = 0; j < 7; ++j) {
+                const DevWeight* w = get_weight(c, m.wids[(size_t)l * 7 + j]);
+                if (!w) return fail(c, QORA_HIP_E_STATE, "model weight released");
+                if (int rc = model_alloc(c, w->k * w->n / 2, &ptr)) return rc;
+                m.pf_wq[(size_t)l * 7 + j] = (uint2*)ptr;
+                if (int rc = model_alloc(c, w->k * w->n / 16, &ptr)) return rc;
+                m.pf_sc[(size_t)l * 7 + j] = (uint16_t*)ptr;
+                HIP_TRY(c, launch_pf_pack_q4((const uint8_t*)w->w, (const uint16_t*)w->scales, (uint32_t)w->k,
+                                             (uint32_t)w->n, m.pf_wq[(size_t)l * 7 + j], m.pf_sc[(size_t)l * 7 + j],
+                                             c->stream));
             }
     }
     // the lm_head of the last prompt row reads the final-normed fp32 row
@@ -1128,6 +1163,42 @@ int pf_gemm(qora_hip_ctx* c, uint32_t l, int j, uint32_t T, float* y, uint32_t l
     return QORA_HIP_OK;
 }
 
+// One launch of the packed-weight GEMM over the projections js of layer l
+// (their columns side by side), each written to its own rows ys[i] (row
+// stride ldy) or added to them.
+int pf_gemm2(qora_hip_ctx* c, uint32_t l, std::initializer_list<int> js, uint32_t T, std::initializer_list<float*> ys,
+             uint32_t ldy, bool accumulate) {
+    ModelState& m = c->m;
+    PfGemm2Params g{};
+    g.xh = m.d_pf_xh;
+    g.xl = m.d_pf_xl;
+    g.xe = m.d_pf_xe;
+    g.T = T;
+    auto yi = ys.begin();
+    for (int j : js) {
+        const size_t wi = (size_t)l * 7 + (size_t)j;
+        const DevWeight* w = get_weight(c, m.wids[wi]);
+        if (!w) return fail(c, QORA_HIP_E_STATE, "model weight released");
+        PfGemm2Seg& sg = g.seg[g.nseg++];
+        sg.wq = m.pf_wq[wi];
+        sg.sc = m.pf_sc[wi];
+        sg.wf = m.pf_wf[wi];
+        sg.n = (uint32_t)w->n;
+        sg.nb0 = g.ntot / 128u;
+        sg.y = *yi++;
+        sg.ldy = ldy;
+        sg.accumulate = accumulate ? 1 : 0;
+        g.k = (uint32_t)w->k;
+        g.ntot += (uint32_t)w->n;
+    }
+    const PfGemm2Shape sh = pf_gemm2_shape(T, g.k, g.ntot, c->cus);
+    g.splits = sh.splits;
+    g.kper = sh.kper;
+    g.part = m.d_pf_part;
+    HIP_TRY(c, launch_pf_gemm2(sh.bm, g, c->stream));
+    return QORA_HIP_OK;
+}
+
 // raw_prefill (gemv.rs:1027-1190) over the prompt in chunks of pf_tc tokens:
 // every layer runs on the whole chunk (GEMMs on the matrix cores, causal
 // attention over the cache rows written so far), then the last row's final
@@ -1161,9 +1232,15 @@ int prefill_batched(qora_hip_ctx* c, size_t n, float* logits, uint32_t* argmax) 
             nr.xl = m.d_pf_xl;
             nr.xe = m.d_pf_xe;
             HIP_TRY(c, launch_pf_rows(PF_ROW_RMSNORM, nr, T, s));
-            if (int rc = pf_gemm(c, l, 0, T, m.d_pf_qkv, qkvn, false)) return rc;
-            if (int rc = pf_gemm(c, l, 1, T, m.d_pf_qkv + qd, qkvn, false)) return rc;
-            if (int rc = pf_gemm(c, l, 2, T, m.d_pf_qkv + qd + kvd, qkvn, false)) return rc;
+            if (m.pf2) {
+                if (int rc = pf_gemm2(c, l, {0, 1, 2}, T, {m.d_pf_qkv, m.d_pf_qkv + qd, m.d_pf_qkv + qd + kvd},
+                                      qkvn, false))
+                    return rc;
+            } else {
+                if (int rc = pf_gemm(c, l, 0, T, m.d_pf_qkv, qkvn, false)) return rc;
+                if (int rc = pf_gemm(c, l, 1, T, m.d_pf_qkv + qd, qkvn, false)) return rc;
+                if (int rc = pf_gemm(c, l, 2, T, m.d_pf_qkv + qd + kvd, qkvn, false)) return rc;
+            }
             PrefillAttnParams a{};
             a.qkv = m.d_pf_qkv;
             a.q = m.d_pf_q;
@@ -1194,11 +1271,18 @@ int prefill_batched(qora_hip_ctx* c, size_t n, float* logits, uint32_t* argmax) 
             sr.xl = m.d_pf_xl;
             sr.xe = m.d_pf_xe;
             HIP_TRY(c, launch_pf_rows(PF_ROW_SPLIT, sr, T, s));
-            if (int rc = pf_gemm(c, l, 3, T, m.d_pf_x, m.hidden, true)) return rc;
+            if (int rc = m.pf2 ? pf_gemm2(c, l, {3}, T, {m.d_pf_x}, m.hidden, true)
+                               : pf_gemm(c, l, 3, T, m.d_pf_x, m.hidden, true))
+                return rc;
             nr.gamma = m.d_norms + ((size_t)l * 2 + 1) * m.hidden;
             HIP_TRY(c, launch_pf_rows(PF_ROW_RMSNORM, nr, T, s));
-            if (int rc = pf_gemm(c, l, 4, T, m.d_pf_gu, 2 * m.inter, false)) return rc;
-            if (int rc = pf_gemm(c, l, 5, T, m.d_pf_gu + m.inter, 2 * m.inter, false)) return rc;
+            if (m.pf2) {
+                if (int rc = pf_gemm2(c, l, {4, 5}, T, {m.d_pf_gu, m.d_pf_gu + m.inter}, 2 * m.inter, false))
+                    return rc;
+            } else {
+                if (int rc = pf_gemm(c, l, 4, T, m.d_pf_gu, 2 * m.inter, false)) return rc;
+                if (int rc = pf_gemm(c, l, 5, T, m.d_pf_gu + m.inter, 2 * m.inter, false)) return rc;
+            }
             PrefillRowParams gr{};
             gr.x = m.d_pf_gu;
             gr.u = m.d_pf_gu + m.inter;
@@ -1208,7 +1292,9 @@ int prefill_batched(qora_hip_ctx* c, size_t n, float* logits, uint32_t* argmax) 
             gr.xl = m.d_pf_xl;
             gr.xe = m.d_pf_xe;
             HIP_TRY(c, launch_pf_rows(PF_ROW_SILU, gr, T, s));
-            if (int rc = pf_gemm(c, l, 6, T, m.d_pf_x, m.hidden, true)) return rc;
+            if (int rc = m.pf2 ? pf_gemm2(c, l, {6}, T, {m.d_pf_x}, m.hidden, true)
+                               : pf_gemm(c, l, 6, T, m.d_pf_x, m.hidden, true))
+                return rc;
         }
     }
     HIP_TRY(c, launch_rmsnorm(m.d_pf_x + (size_t)(T - 1) * m.hidden, m.d_final, m.hidden, m.d_pf_xn, s));
@@ -1753,42 +1839,70 @@ extern "C" int qora_hip_gemm(qora_hip_ctx* c, uint32_t wid, const float* x, floa
     if (!w) return fail(c, QORA_HIP_E_INVALID, "unknown weight id");
     if (T == 0 || T > 0x7FFFFFFFull) return fail(c, QORA_HIP_E_INVALID, "bad row count");
     if (!pf_gemm_supported((uint32_t)w->k, (uint32_t)w->n)) return fail(c, QORA_HIP_E_INVALID, "k must be a multiple of 32");
-    // scratch: xh, xl [T][k] binary16, xe [T], wf [n/32], exponent partials (each 256-byte aligned)
+    const uint32_t K = (uint32_t)w->k, N = (uint32_t)w->n;
+    // Q4 with n % 128 == 0 runs the prefill's packed-weight GEMM (the weight
+    // packed into the workspace for this call), anything else pf_gemm_kernel
+    const bool packed = w->fmt == FMT_Q4 && pf_gemm2_supported(K, N);
+    // scratch: xh, xl [T][k] binary16, xe [T], wf [n/32], exponent partials,
+    // then the packed weight (wq, sc) or nothing, then the split-K partials
+    // (each part 256-byte aligned)
     auto al = [](uint64_t b) { return (b + 255) & ~uint64_t(255); };
-    const uint64_t bx = al(T * w->k * 2), be = al(T * 4), bf = al(w->n / 32 + 1);
-    const uint64_t bs = al(pf_weight_exp_scratch((uint32_t)w->k, (uint32_t)(w->n / 32)));
-    const PfGemmShape sh = pf_gemm_shape((uint32_t)T, (uint32_t)w->k, (uint32_t)w->n, c->cus);
-    const uint64_t bp = sh.splits > 1 ? al((uint64_t)sh.splits * T * w->n * 4) : 0;
-    if (int rc = ensure_pf_ws(c, 2 * bx + be + bf + bs + bp)) return rc;
+    const uint64_t bx = al(T * K * 2), be = al(T * 4), bf = al(N / 32 + 1);
+    const uint64_t bs = al(pf_weight_exp_scratch(K, N / 32));
+    const uint64_t bq = packed ? al((uint64_t)K * N / 2) : 0, bc = packed ? al((uint64_t)K * N / 16) : 0;
+    const PfGemmShape sh = pf_gemm_shape((uint32_t)T, K, N, c->cus);
+    const PfGemm2Shape s2 = packed ? pf_gemm2_shape((uint32_t)T, K, N, c->cus) : PfGemm2Shape{};
+    const uint32_t splits = packed ? s2.splits : sh.splits;
+    const uint64_t bp = splits > 1 ? al((uint64_t)splits * T * N * 4) : 0;
+    if (int rc = ensure_pf_ws(c, 2 * bx + be + bf + bs + bq + bc + bp)) return rc;
     uint8_t* base = (uint8_t*)c->ws_pf;
+    uint8_t* wq = base + 2 * bx + be + bf + bs;
+    float* part = splits > 1 ? (float*)(wq + bq + bc) : nullptr;
     const hipStream_t s = pick_stream(c, stream);
     PrefillRowParams r{};
     r.x = const_cast<float*>(x);
-    r.n = (uint32_t)w->k;
+    r.n = K;
     r.xh = (uint16_t*)base;
     r.xl = (uint16_t*)(base + bx);
     r.xe = (int32_t*)(base + 2 * bx);
     HIP_TRY(c, launch_pf_rows(PF_ROW_SPLIT, r, (uint32_t)T, s));
+    int8_t* wf = (int8_t*)(base + 2 * bx + be);
+    if (w->fmt == FMT_Q4)
+        HIP_TRY(c, launch_pf_weight_exp((const uint16_t*)w->scales, K, N / 32, wf, (uint32_t*)(base + 2 * bx + be + bf), s));
+    if (packed) {
+        HIP_TRY(c, launch_pf_pack_q4((const uint8_t*)w->w, (const uint16_t*)w->scales, K, N, (uint2*)wq,
+                                     (uint16_t*)(wq + bq), s));
+        PfGemm2Params h{};
+        h.xh = r.xh;
+        h.xl = r.xl;
+        h.xe = r.xe;
+        h.T = (uint32_t)T;
+        h.k = K;
+        h.nseg = 1;
+        h.ntot = N;
+        h.seg[0] = PfGemm2Seg{(const uint2*)wq, (const uint16_t*)(wq + bq), wf, N, 0, y, N, 0};
+        h.splits = s2.splits;
+        h.kper = s2.kper;
+        h.part = part;
+        HIP_TRY(c, launch_pf_gemm2(s2.bm, h, s));
+        return QORA_HIP_OK;
+    }
     PrefillGemmParams g{};
     g.xh = r.xh;
     g.xl = r.xl;
     g.xe = r.xe;
     g.T = (uint32_t)T;
-    g.k = (uint32_t)w->k;
-    g.n = (uint32_t)w->n;
+    g.k = K;
+    g.n = N;
     g.w = (const uint8_t*)w->w;
     g.scales = (const uint16_t*)w->scales;
-    if (w->fmt == FMT_Q4) {
-        g.wf = (const int8_t*)(base + 2 * bx + be);
-        HIP_TRY(c, launch_pf_weight_exp(g.scales, g.k, g.n / 32, const_cast<int8_t*>(g.wf),
-                                        (uint32_t*)(base + 2 * bx + be + bf), s));
-    }
+    g.wf = w->fmt == FMT_Q4 ? wf : nullptr;
     g.y = y;
-    g.ldy = g.n;
+    g.ldy = N;
     g.nt = sh.nt;
     g.splits = sh.splits;
     g.kper = sh.kper;
-    g.part = sh.splits > 1 ? (float*)(base + 2 * bx + be + bf + bs) : nullptr;
+    g.part = part;
     HIP_TRY(c, launch_pf_gemm(w->fmt, g, s));
     return QORA_HIP_OK;
 }

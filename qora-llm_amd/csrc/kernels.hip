@@ -611,6 +611,57 @@ hipError_t launch_pf_gemm(int fmt, const PrefillGemmParams& p, hipStream_t strea
     return hipGetLastError();
 }
 
+bool pf_gemm2_supported(uint32_t k, uint32_t n) { return k > 0 && k % 32 == 0 && n > 0 && n % 128 == 0; }
+
+hipError_t launch_pf_pack_q4(const uint8_t* w, const uint16_t* scales, uint32_t k, uint32_t n, uint2* wq,
+                             uint16_t* sc, hipStream_t stream) {
+    if (!pf_gemm2_supported(k, n)) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(pf_pack_q4_kernel, dim3(n / 128, k / 32), dim3(256), 0, stream, w, scales, k, n, wq, sc);
+    return hipGetLastError();
+}
+
+// 128-token tiles from 128 tokens up; then split K until the blocks cover
+// the CUs once (each block's K loop is bound by its matrix-core work, and a
+// block's LDS leaves room for one more on its CU).
+PfGemm2Shape pf_gemm2_shape(uint32_t T, uint32_t k, uint32_t ntot, int cus) {
+    PfGemm2Shape sh{};
+    sh.bm = T >= 128 ? 128u : 64u;
+    const char* eb = std::getenv("QORA_HIP_PF_BM");
+    if (eb && *eb) sh.bm = std::atoi(eb) == 64 ? 64u : 128u;
+    const uint64_t blocks = std::max<uint64_t>(1, (uint64_t)(ntot / 128u) * ((T + sh.bm - 1) / sh.bm));
+    const uint32_t steps = k / 32u;
+    uint32_t splits = (uint32_t)std::max<uint64_t>(1, ((uint64_t)std::max(1, cus) + blocks - 1) / blocks);
+    const char* es = std::getenv("QORA_HIP_PF_SPLITS");
+    if (es && *es) splits = std::max(1, std::atoi(es));
+    splits = std::min(splits, std::max(1u, steps / 8u));   // at least 8 steps (256 rows) a split
+    const uint32_t per = (steps + splits - 1) / splits;
+    sh.kper = per * 32u;
+    sh.splits = (steps + per - 1) / per;
+    return sh;
+}
+
+hipError_t launch_pf_gemm2(uint32_t bm, const PfGemm2Params& p, hipStream_t stream) {
+    if (p.T == 0 || p.k % 32 != 0 || p.nseg < 1 || p.nseg > 3 || p.ntot % 128 != 0 || p.splits == 0 ||
+        p.kper % 32 != 0 || (uint64_t)p.splits * p.kper < p.k || (p.splits > 1 && !p.part))
+        return hipErrorInvalidValue;
+    uint32_t nb = 0;
+    for (int i = 0; i < p.nseg; ++i) {
+        if (p.seg[i].nb0 != nb || p.seg[i].n % 128 != 0 || !p.seg[i].wq || !p.seg[i].sc || !p.seg[i].wf) return hipErrorInvalidValue;
+        nb += p.seg[i].n / 128;
+    }
+    if (nb * 128u != p.ntot) return hipErrorInvalidValue;
+    const dim3 grid(nb, (p.T + bm - 1) / bm, p.splits);
+    if (bm == 128) hipLaunchKernelGGL((pf_gemm2_kernel<128>), grid, dim3(256), 0, stream, p);
+    else if (bm == 64) hipLaunchKernelGGL((pf_gemm2_kernel<64>), grid, dim3(256), 0, stream, p);
+    else return hipErrorInvalidValue;
+    if (p.splits > 1) {
+        const uint64_t total = (uint64_t)p.T * p.ntot;
+        const uint32_t blocks = (uint32_t)std::min<uint64_t>(4096, (total + 255) / 256);
+        hipLaunchKernelGGL(pf_splitk_reduce2_kernel, dim3(blocks), dim3(256), 0, stream, p);
+    }
+    return hipGetLastError();
+}
+
 hipError_t launch_pf_rope_cache(const PrefillAttnParams& p, hipStream_t stream) {
     if (p.T == 0) return hipSuccess;
     if (p.kv_f16) hipLaunchKernelGGL((pf_rope_cache_kernel<true>), dim3(p.T), dim3(256), 0, stream, p);

@@ -109,6 +109,18 @@ struct PfGemmShape {
 PfGemmShape pf_gemm_shape(uint32_t T, uint32_t k, uint32_t n, int cus);
 // p.nt, p.splits, p.kper from pf_gemm_shape; p.part holds splits * T * n floats when splits > 1
 hipError_t launch_pf_gemm(int fmt, const PrefillGemmParams& p, hipStream_t stream);
+// Prefill GEMM on pre-packed Q4 weights (pf_gemm2_kernel). pack: the packed
+// copy of a Q4 weight [k][n] (k % 32 == 0, n % 128 == 0) into wq (k n / 2
+// bytes) and sc (k n / 16 bytes).
+bool pf_gemm2_supported(uint32_t k, uint32_t n);
+hipError_t launch_pf_pack_q4(const uint8_t* w, const uint16_t* scales, uint32_t k, uint32_t n, uint2* wq,
+                             uint16_t* sc, hipStream_t stream);
+struct PfGemm2Shape {
+    uint32_t bm, splits, kper;
+};
+PfGemm2Shape pf_gemm2_shape(uint32_t T, uint32_t k, uint32_t ntot, int cus);
+// p.splits, p.kper from pf_gemm2_shape (bm too); p.part holds splits * T * ntot floats when splits > 1
+hipError_t launch_pf_gemm2(uint32_t bm, const PfGemm2Params& p, hipStream_t stream);
 hipError_t launch_pf_rope_cache(const PrefillAttnParams& p, hipStream_t stream);
 hipError_t launch_pf_attn(const PrefillAttnParams& p, hipStream_t stream);
 

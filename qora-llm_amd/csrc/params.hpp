@@ -150,6 +150,37 @@ struct PrefillGemmParams {
     uint32_t nt;               // column tile (64 or 128), from pf_gemm_shape
 };
 
+// Pre-packed Q4 weight of the prefill GEMM (pf_gemm2_kernel): column block
+// nb (128 columns), K step ks (32 rows), thread t = 64 rg + bc of a 256-thread
+// block: wq[(nb * KS + ks) * 256 + t] holds 8 bytes, byte r = the two
+// nibbles of columns 2 bc, 2 bc + 1 of row 32 ks + 8 rg + r (the reference
+// byte); sc[((nb * KS + ks) * 4 + g) * 32 + r] the f16 scale of row 32 ks + r,
+// group g of the block. KS = k / 32.
+struct PfGemm2Seg {
+    const uint2* wq;
+    const uint16_t* sc;
+    const int8_t* wf;          // per-group exponents [n/32]
+    uint32_t n;                // columns (multiple of 128)
+    uint32_t nb0;              // first column block of the segment in the grid
+    float* y;                  // [T][ldy]
+    uint32_t ldy;
+    int accumulate;            // 1: y += result (residual add)
+};
+
+struct PfGemm2Params {
+    const uint16_t* xh;
+    const uint16_t* xl;
+    const int32_t* xe;
+    uint32_t T, k;
+    PfGemm2Seg seg[3];
+    int nseg;
+    uint32_t ntot;             // columns of all segments
+    // split K: grid.z = splits, split z takes rows [z kper, (z + 1) kper) and
+    // writes part[z][T][ntot]; pf_splitk_reduce2_kernel sums them in split order
+    uint32_t splits, kper;
+    float* part;
+};
+
 struct PrefillAttnParams {
     const float* qkv;          // GEMM output rows [T][qd + 2 kvd]
     float* q;                  // rotated q [T][qd]

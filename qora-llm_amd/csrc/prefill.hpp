@@ -465,6 +465,219 @@ __global__ __launch_bounds__(256) void pf_gemm_kernel(PrefillGemmParams p) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Prefill GEMM on pre-packed Q4 weights (the same numerics as pf_gemm_kernel:
+// y = x' w' 2^(e_t + f_g), three f16 products per pair xh wh + xl wh + xh wl
+// accumulated in fp32, in that order, per 32-deep K step).
+// Block: 256 threads (2 x 2 waves) over BM tokens x 128 columns; each wave
+// holds (BM / 2) x 64 of the output as (BM / 32) x 4 MFMA tiles. Per K step
+// a thread loads its x' row piece (both parts), 8 bytes of packed weights
+// (16 values) and 16 bytes of their scales; the next step's loads are in
+// flight while the current step's operands go through the matrix cores, and
+// the LDS is double-buffered (one barrier per step). Up to three weight
+// segments share the launch (q|k|v, gate|up): column block b belongs to the
+// segment whose blocks start at or below it.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void pf_pack_q4_kernel(const uint8_t* w, const uint16_t* scales, uint32_t k,
+                                                         uint32_t n, uint2* wq, uint16_t* sc) {
+    // block (nb, ks): thread t packs its 8 bytes and, for t < 128, one scale row
+    const uint32_t nb = blockIdx.x, ks = blockIdx.y, KS = k / 32u;
+    const uint32_t t = threadIdx.x, bc = t % 64u, rg = t / 64u;
+    const uint32_t col = nb * 128u + 2u * bc;
+    uint32_t lo = 0, hi = 0;
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+        const uint32_t row = ks * 32u + rg * 8u + (uint32_t)r;
+        const uint32_t b = w[(uint64_t)row * (n / 2u) + col / 2u];
+        if (r < 4) lo |= b << (8 * r);
+        else hi |= b << (8 * (r - 4));
+    }
+    wq[((uint64_t)nb * KS + ks) * 256u + t] = make_uint2(lo, hi);
+    if (t < 128u) {
+        const uint32_t g = t / 32u, r = t % 32u;
+        sc[(((uint64_t)nb * KS + ks) * 4u + g) * 32u + r] =
+            scales[(uint64_t)(ks * 32u + r) * (n / 32u) + nb * 4u + g];
+    }
+}
+
+template <int BM>
+__global__ __launch_bounds__(256) void pf_gemm2_kernel(PfGemm2Params p) {
+    constexpr int BN = 128, KC = 32;
+    constexpr int XS = KC + 8;                      // LDS row stride in halves (80 B)
+    constexpr int WM = BM / 2, TM = WM / 16, TN = 4;
+    constexpr int XT = 256 / BM;                    // threads per x' row (2 or 4)
+    constexpr int XH = KC / XT;                     // halves of a row per thread (16 or 8)
+    constexpr int XV = XH / 8;                      // 16-byte loads per part (2 or 1)
+    static_assert(BM == 64 || BM == 128, "64- or 128-token tiles");
+    __shared__ __align__(16) _Float16 xs[2][2][BM * XS];
+    __shared__ __align__(16) _Float16 ws[2][2][BN * XS];
+    kernarg_warm(p);
+
+    const int t = threadIdx.x;
+    const int lane = t & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
+    const int wm = wave >> 1, wn = wave & 1;
+    const uint32_t nb = blockIdx.x;
+    // the segment of this column block (wave-uniform: whole-struct selects, no
+    // indexing of the argument block)
+    PfGemm2Seg sg = p.seg[0];
+    if (p.nseg > 1 && nb >= p.seg[1].nb0) sg = p.seg[1];
+    if (p.nseg > 2 && nb >= p.seg[2].nb0) sg = p.seg[2];
+    const uint32_t lnb = nb - sg.nb0;               // column block within the segment
+    const uint32_t m0 = blockIdx.y * (uint32_t)BM;
+    const uint32_t K = p.k, KS = K / 32u;
+    const uint32_t kb = blockIdx.z * p.kper;
+    const uint32_t steps = (min(K, kb + p.kper) - kb) / (uint32_t)KC;
+
+    // x' rows: thread t loads XH halves of row t / XT (rows past T read row T - 1, masked at the end)
+    const uint32_t xr = (uint32_t)t / XT, xq = (uint32_t)t % XT;
+    const uint64_t xoff = (uint64_t)min(m0 + xr, p.T - 1u) * K + xq * XH;
+    // weights: columns 2 bc, 2 bc + 1 of the block, rows 8 rg .. 8 rg + 7 of the step
+    const uint32_t bc = (uint32_t)t % 64u, rg = (uint32_t)t / 64u;
+    const uint32_t g = bc / 16u;                    // 32-column group in the block
+    const float wscale = ldexpf(1.0f, -(int)sg.wf[lnb * 4u + g]);
+    const uint2* wqp = sg.wq + (uint64_t)lnb * KS * 256u + (uint32_t)t;
+    const uint16_t* scp = sg.sc + ((uint64_t)lnb * KS * 4u + g) * 32u + rg * 8u;
+
+    // (native vector types: the compiler keeps these in registers)
+    struct Slice {
+        v4u32 xh0, xh1, xl0, xl1;                   // x' pieces (xh1, xl1: 128-token tiles only)
+        v2u32 wq;
+        v4u32 sc;                                   // 8 f16 scales, rows 8 rg .. + 7
+    };
+    auto load_slice = [&](Slice& q, uint32_t s) {
+        const uint32_t k0 = kb + s * (uint32_t)KC;
+        q.xh0 = *reinterpret_cast<const v4u32*>(p.xh + xoff + k0);
+        q.xl0 = *reinterpret_cast<const v4u32*>(p.xl + xoff + k0);
+        if constexpr (XV == 2) {
+            q.xh1 = *reinterpret_cast<const v4u32*>(p.xh + xoff + k0 + 8u);
+            q.xl1 = *reinterpret_cast<const v4u32*>(p.xl + xoff + k0 + 8u);
+        }
+        const uint32_t ks = k0 / 32u;
+        q.wq = *reinterpret_cast<const v2u32*>(wqp + (uint64_t)ks * 256u);
+        q.sc = *reinterpret_cast<const v4u32*>(scp + (uint64_t)ks * 128u);
+    };
+    auto store_slice = [&](const Slice& q, int buf) {
+        *reinterpret_cast<v4u32*>(&xs[buf][0][xr * XS + xq * XH]) = q.xh0;
+        *reinterpret_cast<v4u32*>(&xs[buf][1][xr * XS + xq * XH]) = q.xl0;
+        if constexpr (XV == 2) {
+            *reinterpret_cast<v4u32*>(&xs[buf][0][xr * XS + xq * XH + 8]) = q.xh1;
+            *reinterpret_cast<v4u32*>(&xs[buf][1][xr * XS + xq * XH + 8]) = q.xl1;
+        }
+        _Float16 h0[8], h1[8], l0[8], l1[8];
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+            const uint32_t byte = (q.wq[r / 4] >> (8 * (r & 3))) & 0xFFu;
+            const uint32_t sw2 = q.sc[r / 2];
+            const uint16_t sb = (uint16_t)((r & 1) ? (sw2 >> 16) : (sw2 & 0xFFFFu));
+            const float sv = h2f(sb) * wscale;      // exact: power-of-two scaling
+            const float w0 = sv * (float)((int)(byte & 0xFu) - 8);
+            const float w1 = sv * (float)((int)(byte >> 4) - 8);
+            h0[r] = (_Float16)w0;
+            h1[r] = (_Float16)w1;
+            l0[r] = (_Float16)(w0 - (float)h0[r]);
+            l1[r] = (_Float16)(w1 - (float)h1[r]);
+        }
+        const uint32_t c0 = (2u * bc) * XS + rg * 8u, c1 = (2u * bc + 1u) * XS + rg * 8u;
+        *reinterpret_cast<half8v*>(&ws[buf][0][c0]) = half8v{h0[0], h0[1], h0[2], h0[3], h0[4], h0[5], h0[6], h0[7]};
+        *reinterpret_cast<half8v*>(&ws[buf][0][c1]) = half8v{h1[0], h1[1], h1[2], h1[3], h1[4], h1[5], h1[6], h1[7]};
+        *reinterpret_cast<half8v*>(&ws[buf][1][c0]) = half8v{l0[0], l0[1], l0[2], l0[3], l0[4], l0[5], l0[6], l0[7]};
+        *reinterpret_cast<half8v*>(&ws[buf][1][c1]) = half8v{l1[0], l1[1], l1[2], l1[3], l1[4], l1[5], l1[6], l1[7]};
+    };
+
+    f32x4v acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = f32x4v{0.f, 0.f, 0.f, 0.f};
+    const uint32_t li = (uint32_t)lane % 16u, kq = (uint32_t)lane / 16u;
+    auto compute = [&](int buf) {
+        half8v ah[TM], al[TM], bh[TN], bl[TN];
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+            const uint32_t row = (uint32_t)wm * WM + (uint32_t)i * 16u + li;
+            ah[i] = *reinterpret_cast<const half8v*>(&xs[buf][0][row * XS + kq * 8u]);
+            al[i] = *reinterpret_cast<const half8v*>(&xs[buf][1][row * XS + kq * 8u]);
+        }
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const uint32_t c = (uint32_t)wn * 64u + (uint32_t)j * 16u + li;
+            bh[j] = *reinterpret_cast<const half8v*>(&ws[buf][0][c * XS + kq * 8u]);
+            bl[j] = *reinterpret_cast<const half8v*>(&ws[buf][1][c * XS + kq * 8u]);
+        }
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int i = 0; i < TM; ++i) {
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], bh[j], acc[i][j], 0, 0, 0);
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], bh[j], acc[i][j], 0, 0, 0);
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], bl[j], acc[i][j], 0, 0, 0);
+            }
+    };
+
+    // global loads run two steps ahead of the matrix cores: slice se holds the
+    // even steps, so the odd ones; the LDS buffer of step s is s & 1
+    Slice se, so;
+    if (steps > 0) load_slice(se, 0);
+    if (steps > 1) load_slice(so, 1);
+    if (steps > 0) store_slice(se, 0);
+    __syncthreads();
+    for (uint32_t s = 0; s < steps; s += 2) {
+        if (s + 2 < steps) load_slice(se, s + 2);
+        compute(0);
+        if (s + 1 < steps) store_slice(so, 1);
+        __syncthreads();
+        if (s + 1 < steps) {
+            if (s + 3 < steps) load_slice(so, s + 3);
+            compute(1);
+            if (s + 2 < steps) store_slice(se, 0);
+            __syncthreads();
+        }
+    }
+
+    // epilogue: y = acc * 2^(e_t + f_g), stored, added, or kept as this split's partial
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const uint32_t cl = (uint32_t)wn * 64u + (uint32_t)j * 16u + li;   // column in the block
+            const uint32_t c = lnb * (uint32_t)BN + cl;                        // column in the segment
+            const int fg = (int)sg.wf[c / 32u];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t row = m0 + (uint32_t)wm * WM + (uint32_t)i * 16u + kq * 4u + (uint32_t)r;
+                if (row >= p.T) continue;
+                const float v = ldexpf(acc[i][j][r], p.xe[row] + fg);
+                if (p.splits > 1) {
+                    p.part[((uint64_t)blockIdx.z * p.T + row) * p.ntot + nb * (uint32_t)BN + cl] = v;
+                } else {
+                    float* y = sg.y + (uint64_t)row * sg.ldy + c;
+                    if (sg.accumulate) *y += v;
+                    else *y = v;
+                }
+            }
+        }
+    }
+}
+
+// Split-K partials of pf_gemm2_kernel summed in split order, stored or added
+// into each segment's rows.
+__global__ __launch_bounds__(256) void pf_splitk_reduce2_kernel(PfGemm2Params p) {
+    const uint64_t total = (uint64_t)p.T * p.ntot;
+    for (uint64_t e = (uint64_t)blockIdx.x * 256u + threadIdx.x; e < total; e += (uint64_t)gridDim.x * 256u) {
+        float v = p.part[e];
+        for (uint32_t z = 1; z < p.splits; ++z) v += p.part[(uint64_t)z * total + e];
+        const uint32_t row = (uint32_t)(e / p.ntot), c = (uint32_t)(e % p.ntot);
+        const uint32_t b = c / 128u;
+        PfGemm2Seg sg = p.seg[0];
+        if (p.nseg > 1 && b >= p.seg[1].nb0) sg = p.seg[1];
+        if (p.nseg > 2 && b >= p.seg[2].nb0) sg = p.seg[2];
+        float* y = sg.y + (uint64_t)row * sg.ldy + (c - sg.nb0 * 128u);
+        if (sg.accumulate) *y += v;
+        else *y = v;
+    }
+}
+
 // Split-K partials summed in split order (deterministic), stored or added.
 __global__ __launch_bounds__(256) void pf_splitk_reduce_kernel(PrefillGemmParams p) {
     const uint64_t total = (uint64_t)p.T * p.n;
