@@ -139,17 +139,26 @@ __device__ __forceinline__ LaneSrc lane_source(const GemvParams& p, uint32_t til
         sidx = 0;
         if (p.nseg > 1 && tile >= p.seg[1].tile0) sidx = 1;
         if (p.nseg > 2 && tile >= p.seg[2].tile0) sidx = 2;
-        const uint32_t t0 = sidx == 0 ? p.seg[0].tile0 : (sidx == 1 ? p.seg[1].tile0 : p.seg[2].tile0);
+        uint32_t t00 = p.seg[0].tile0, t01 = p.seg[1].tile0, t02 = p.seg[2].tile0;
+        asm volatile("" : "+s"(t00), "+s"(t01), "+s"(t02));
+        const uint32_t t0 = sidx == 0 ? t00 : (sidx == 1 ? t01 : t02);
         grp = (tile - t0) * (uint32_t)gt + (uint32_t)gi;
     }
     // Per-field selects over the kernarg values (a per-lane index into
     // p.seg would fetch the struct with a vector load before any weight load).
+    // Each candidate is read into a scalar register first (the empty asm):
+    // otherwise the compiler folds the select chain into an indexed load of
+    // the argument block, which makes it copy the whole block to scratch.
+    auto pick = [&](auto v0, auto v1, auto v2) {
+        asm volatile("" : "+s"(v0), "+s"(v1), "+s"(v2));
+        return sidx == 0 ? v0 : (sidx == 1 ? v1 : v2);
+    };
     LaneSrc s;
-    s.sg.w = sidx == 0 ? p.seg[0].w : (sidx == 1 ? p.seg[1].w : p.seg[2].w);
-    s.sg.scales = sidx == 0 ? p.seg[0].scales : (sidx == 1 ? p.seg[1].scales : p.seg[2].scales);
-    s.sg.groups = sidx == 0 ? p.seg[0].groups : (sidx == 1 ? p.seg[1].groups : p.seg[2].groups);
-    s.sg.tile0 = sidx == 0 ? p.seg[0].tile0 : (sidx == 1 ? p.seg[1].tile0 : p.seg[2].tile0);
-    s.sg.col0 = sidx == 0 ? p.seg[0].col0 : (sidx == 1 ? p.seg[1].col0 : p.seg[2].col0);
+    s.sg.w = pick(p.seg[0].w, p.seg[1].w, p.seg[2].w);
+    s.sg.scales = pick(p.seg[0].scales, p.seg[1].scales, p.seg[2].scales);
+    s.sg.groups = pick(p.seg[0].groups, p.seg[1].groups, p.seg[2].groups);
+    s.sg.tile0 = pick(p.seg[0].tile0, p.seg[1].tile0, p.seg[2].tile0);
+    s.sg.col0 = pick(p.seg[0].col0, p.seg[1].col0, p.seg[2].col0);
     s.sg.tiles = 0;
     s.grp = grp;
     s.grp_c = grp < s.sg.groups ? grp : 0u;
