@@ -49,6 +49,12 @@ __device__ __forceinline__ float4 kv_word_f32(typename std::conditional<F16KV, u
     else return w;
 }
 
+// c ? a : b per component (a select of the vector objects themselves can be
+// lowered through scratch memory)
+__device__ __forceinline__ float4 sel4(bool c, float4 a, float4 b) {
+    return make_float4(c ? a.x : b.x, c ? a.y : b.y, c ? a.z : b.z, c ? a.w : b.w);
+}
+
 // Sum of v over lanes l, l ^ 16, l ^ 32 and l ^ 48 (the four row slots of a
 // wave), the same bits in all four: each lane-swap instruction leaves lane l's
 // partner value in one of its two results, so their sum is v[l] + v[l ^ 16]
@@ -101,43 +107,65 @@ __global__ __launch_bounds__(kFusedWaves * kWave) void gemv_q4m_attn_kernel(Attn
     const uint8_t* vcache = reinterpret_cast<const uint8_t*>(a.vc);
     constexpr uint32_t EB = F16KV ? 2u : 4u;
     W kr[NP][NQ], vr[NP][NQ];
-    auto load_row = [&](int i, uint32_t pos) {
-#pragma unroll
-        for (int u = 0; u < NQ; ++u) {
-            const uint64_t off = ((uint64_t)pos * cps + coff + 64u * (uint32_t)u + 4u * c) * EB;
-            kr[i][u] = *reinterpret_cast<const W*>(kcache + off);
-            vr[i][u] = *reinterpret_cast<const W*>(vcache + off);
-        }
+    auto row_off = [&](uint32_t pos, int u) {
+        return ((uint64_t)pos * cps + coff + 64u * (uint32_t)u + 4u * c) * EB;
     };
-    // ---- passes 0 .. NP-2: positions below 32 (NP - 1) <= L - 1, cached
-    // rows whose addresses do not depend on the position ----
+    auto load_k = [&](int i, uint32_t pos) {
 #pragma unroll
-    for (int i = 0; i < NP - 1; ++i) load_row(i, kFusedPass * (uint32_t)i + slot);
+        for (int u = 0; u < NQ; ++u) kr[i][u] = *reinterpret_cast<const W*>(kcache + row_off(pos, u));
+    };
+    auto load_v = [&](int i, uint32_t pos) {
+#pragma unroll
+        for (int u = 0; u < NQ; ++u) vr[i][u] = *reinterpret_cast<const W*>(vcache + row_off(pos, u));
+    };
+    // ---- K rows of passes 0 .. NP-2: positions below 32 (NP - 1) <= L - 1,
+    // cached rows whose addresses do not depend on the position ----
+#pragma unroll
+    for (int i = 0; i < NP - 1; ++i) load_k(i, kFusedPass * (uint32_t)i + slot);
 
     const bool qkv_wave = wave >= NW && wave < NW + HD / kWave;
     const uint32_t d = (uint32_t)(t - NW * kWave) % HD;
     const uint32_t pd = rope_partner(d, a.half);
 
-    // ---- the position, then the last pass: rows at or past the appended
-    // position are not read (address clamped below it, or to row 0 when it
-    // is 0; those values are replaced or masked below) ----
+    // ---- the position, then the last pass's K rows: rows at or past the
+    // appended position are not read (address clamped below it, or to row 0
+    // when it is 0; those values are replaced or masked below) ----
     int32_t pos_raw = ld_scalar_i32(a.pos);
     sgpr_pin(pos_raw);
     const uint32_t L = (uint32_t)pos_raw + 1u;
     const uint32_t cur = L - 1u;                       // position appended this step
     const uint32_t plast = kFusedPass * (uint32_t)(NP - 1) + slot;
-    load_row(NP - 1, cur == 0u ? 0u : min(plast, cur - 1u));
-    float rc = 1.f, rs = 0.f;
-    if (qkv_wave && a.use_rope && d < 2 * a.half) {
-        const uint32_t td = d < a.half ? d : d - a.half;
-        rc = a.rope_cos[(uint64_t)cur * a.half + td];
-        rs = a.rope_sin[(uint64_t)cur * a.half + td];
+    const uint32_t plast_rd = cur == 0u ? 0u : min(plast, cur - 1u);
+    load_k(NP - 1, plast_rd);
+
+    // ---- the q|k|v sums of the head and its RoPE row (waves NW.., one dim
+    // per thread), after the K rows and before the V rows: q is ready while
+    // the V rows stream in, and the scores need only q and K ----
+    long long qa = 0, qb = 0, ka = 0, kb = 0, va = 0;
+    float ssp = 0.f, rc = 1.f, rs = 0.f;
+    if (qkv_wave) {
+        if (a.use_rope && d < 2 * a.half) {
+            const uint32_t td = d < a.half ? d : d - a.half;
+            rc = a.rope_cos[(uint64_t)cur * a.half + td];
+            rs = a.rope_sin[(uint64_t)cur * a.half + td];
+        }
+        qa = a.qkv_acc[(uint64_t)h * HD + d];
+        qb = a.qkv_acc[(uint64_t)h * HD + pd];
+        ka = a.qkv_acc[qd + (uint64_t)kvh * HD + d];
+        kb = a.qkv_acc[qd + (uint64_t)kvh * HD + pd];
+        va = a.qkv_acc[qd + kvd + (uint64_t)kvh * HD + d];
+        ssp = a.ss_in[min((uint32_t)lane, a.ss_n - 1u)];
     }
+
+    // ---- V rows of every pass ----
+#pragma unroll
+    for (int i = 0; i < NP - 1; ++i) load_v(i, kFusedPass * (uint32_t)i + slot);
+    load_v(NP - 1, plast_rd);
 
     // ---- the matrix-core waves' scales and weights. Waves NW.. issue the
     // same loads as wave - NW (the lines are already in flight): every wave
-    // then has the same loads outstanding after its cache rows, so its first
-    // use of the rows waits for the rows alone, not for these ----
+    // then has the same loads outstanding after its V rows, so its first use
+    // of the rows waits for the rows alone, not for these ----
     uint4 wq[GW][NKB];
     uint32_t sw[(NZ + 1) / 2];
     int esg[GW];
@@ -147,20 +175,11 @@ __global__ __launch_bounds__(kFusedWaves * kWave) void gemv_q4m_attn_kernel(Attn
     GemvOut<GW> out{};
     if (wave < NW) out = gemv_q4m_out<GW>(p, tile, wave);
     __builtin_amdgcn_sched_barrier(0);
-    // ---- q|k|v sums of the head (waves NW.., one dim per thread), issued
-    // last: their arithmetic then waits for every load above at once ----
-    long long qa = 0, qb = 0, ka = 0, kb = 0, va = 0;
-    float ssp = 0.f;
-    if (qkv_wave) {
-        qa = a.qkv_acc[(uint64_t)h * HD + d];
-        qb = a.qkv_acc[(uint64_t)h * HD + pd];
-        ka = a.qkv_acc[qd + (uint64_t)kvh * HD + d];
-        kb = a.qkv_acc[qd + (uint64_t)kvh * HD + pd];
-        va = a.qkv_acc[qd + kvd + (uint64_t)kvh * HD + d];
-        ssp = a.ss_in[min((uint32_t)lane, a.ss_n - 1u)];
-    }
 
     if (qkv_wave) {
+        // the sums and the RoPE row are waited for here, after the V rows and
+        // the weights have been issued
+        asm volatile("" : "+v"(qa), "+v"(qb), "+v"(ka), "+v"(kb), "+v"(va), "+v"(ssp), "+v"(rc), "+v"(rs));
         // the q|k|v GEMV ran on x * gamma; its RMSNorm factor is applied here
         const float inv = 1.0f / sqrtf(wave_sum(lane < (int)a.ss_n ? ssp : 0.f) / (float)a.norm_n + 1e-6f);
         const bool rot = a.use_rope != 0 && d < 2 * a.half;
@@ -213,7 +232,11 @@ __global__ __launch_bounds__(kFusedWaves * kWave) void gemv_q4m_attn_kernel(Attn
 #pragma unroll
         for (int u = 0; u < NQ; ++u) {
             float4 k = kv_word_f32<F16KV>(kr[i][u]);
-            if (i == NP - 1 && last_cur) k = *reinterpret_cast<const float4*>(kn + 64 * u + 4 * c);
+            if (i == NP - 1) {
+                // selects, not a masked write into the loaded registers
+                const float4 kc4 = *reinterpret_cast<const float4*>(kn + 64 * u + 4 * c);
+                k = sel4(last_cur, kc4, k);
+            }
             dot = fmaf(q[u][0], k.x, dot);
             dot = fmaf(q[u][1], k.y, dot);
             dot = fmaf(q[u][2], k.z, dot);
@@ -229,6 +252,8 @@ __global__ __launch_bounds__(kFusedWaves * kWave) void gemv_q4m_attn_kernel(Attn
     for (int i = 1; i < NP; ++i) mx = fmaxf(mx, s[i]);
     mx = wave_max(mx);
     const float mref = mx == -INFINITY ? 0.f : mx;
+    // the V rows are first needed below: keep their uses after the softmax
+    __builtin_amdgcn_sched_barrier(0);
     float sum = 0.f;
     float o[NQ][4];
 #pragma unroll
@@ -243,8 +268,9 @@ __global__ __launch_bounds__(kFusedWaves * kWave) void gemv_q4m_attn_kernel(Attn
         for (int u = 0; u < NQ; ++u) {
             float4 v = kv_word_f32<F16KV>(vr[i][u]);
             if (i == NP - 1) {
-                if (last_cur) v = *reinterpret_cast<const float4*>(vn + 64 * u + 4 * c);
-                if (!last_live) v = make_float4(0.f, 0.f, 0.f, 0.f);   // select: stale bits never reach the sum
+                const float4 vc4 = *reinterpret_cast<const float4*>(vn + 64 * u + 4 * c);
+                v = sel4(last_cur, vc4, v);
+                v = sel4(last_live, v, make_float4(0.f, 0.f, 0.f, 0.f));   // select: stale bits never reach the sum
             }
             o[u][0] = fmaf(p_i, v.x, o[u][0]);
             o[u][1] = fmaf(p_i, v.y, o[u][1]);
