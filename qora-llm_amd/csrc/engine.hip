@@ -1117,9 +1117,9 @@ int pf_setup(qora_hip_ctx* c) {
                 m.pf_wq[(size_t)l * 7 + j] = (uint2*)ptr;
                 if (int rc = model_alloc(c, w->k * w->n / 16, &ptr)) return rc;
                 m.pf_sc[(size_t)l * 7 + j] = (uint16_t*)ptr;
-                HIP_TRY(c, launch_pf_pack_q4((const uint8_t*)w->w, (const uint16_t*)w->scales, (uint32_t)w->k,
-                                             (uint32_t)w->n, m.pf_wq[(size_t)l * 7 + j], m.pf_sc[(size_t)l * 7 + j],
-                                             c->stream));
+                HIP_TRY(c, launch_pf_pack_q4((const uint8_t*)w->w, (const uint16_t*)w->scales,
+                                             m.pf_wf[(size_t)l * 7 + j], (uint32_t)w->k, (uint32_t)w->n,
+                                             m.pf_wq[(size_t)l * 7 + j], m.pf_sc[(size_t)l * 7 + j], c->stream));
             }
     }
     // the lm_head of the last prompt row reads the final-normed fp32 row
@@ -1870,7 +1870,7 @@ extern "C" int qora_hip_gemm(qora_hip_ctx* c, uint32_t wid, const float* x, floa
     if (w->fmt == FMT_Q4)
         HIP_TRY(c, launch_pf_weight_exp((const uint16_t*)w->scales, K, N / 32, wf, (uint32_t*)(base + 2 * bx + be + bf), s));
     if (packed) {
-        HIP_TRY(c, launch_pf_pack_q4((const uint8_t*)w->w, (const uint16_t*)w->scales, K, N, (uint2*)wq,
+        HIP_TRY(c, launch_pf_pack_q4((const uint8_t*)w->w, (const uint16_t*)w->scales, wf, K, N, (uint2*)wq,
                                      (uint16_t*)(wq + bq), s));
         PfGemm2Params h{};
         h.xh = r.xh;

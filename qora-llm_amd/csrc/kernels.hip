@@ -613,27 +613,46 @@ hipError_t launch_pf_gemm(int fmt, const PrefillGemmParams& p, hipStream_t strea
 
 bool pf_gemm2_supported(uint32_t k, uint32_t n) { return k > 0 && k % 32 == 0 && n > 0 && n % 128 == 0; }
 
-hipError_t launch_pf_pack_q4(const uint8_t* w, const uint16_t* scales, uint32_t k, uint32_t n, uint2* wq,
-                             uint16_t* sc, hipStream_t stream) {
-    if (!pf_gemm2_supported(k, n)) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(pf_pack_q4_kernel, dim3(n / 128, k / 32), dim3(256), 0, stream, w, scales, k, n, wq, sc);
+hipError_t launch_pf_pack_q4(const uint8_t* w, const uint16_t* scales, const int8_t* wf, uint32_t k, uint32_t n,
+                             uint2* wq, uint16_t* sc, hipStream_t stream) {
+    if (!pf_gemm2_supported(k, n) || !wf) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(pf_pack_q4_kernel, dim3(n / 128, k / 32), dim3(256), 0, stream, w, scales, wf, k, n, wq, sc);
     return hipGetLastError();
 }
 
-// 128-token tiles from 128 tokens up; then split K until the blocks cover
-// the CUs once (each block's K loop is bound by its matrix-core work, and a
-// block's LDS leaves room for one more on its CU).
+// 128-token tiles from 128 tokens up; then the K split (512 tokens on 256
+// CUs: q|k|v 5, o 8, gate|up 1, down 8).
 PfGemm2Shape pf_gemm2_shape(uint32_t T, uint32_t k, uint32_t ntot, int cus) {
     PfGemm2Shape sh{};
     sh.bm = T >= 128 ? 128u : 64u;
     const char* eb = std::getenv("QORA_HIP_PF_BM");
     if (eb && *eb) sh.bm = std::atoi(eb) == 64 ? 64u : 128u;
-    const uint64_t blocks = std::max<uint64_t>(1, (uint64_t)(ntot / 128u) * ((T + sh.bm - 1) / sh.bm));
+    const uint64_t tiles = std::max<uint64_t>(1, (uint64_t)(ntot / 128u) * ((T + sh.bm - 1) / sh.bm));
     const uint32_t steps = k / 32u;
-    uint32_t splits = (uint32_t)std::max<uint64_t>(1, ((uint64_t)std::max(1, cus) + blocks - 1) / blocks);
+    // K is split only when the tiles leave the CUs' block slots (two per CU:
+    // 80 KB of LDS and ~220 registers a thread each) partly empty: beyond one
+    // round of blocks a split adds partial-sum traffic and no speed. The
+    // splits are of equal length (at least 8 steps each, at most 16 splits),
+    // and the count is the one whose blocks fill their rounds best (fewer
+    // splits unless more fill them better by 2% or more).
+    const uint64_t slots = 2u * (uint64_t)std::max(1, cus);
+    const uint32_t smax = tiles >= slots ? 1u
+                                         : (uint32_t)std::min<uint64_t>({16u, std::max(1u, steps / 8u),
+                                                                         (slots + tiles - 1) / tiles});
+    uint32_t splits = 1;
+    double best = -1.0;
+    for (uint32_t s = 1; s <= smax; ++s) {
+        const uint32_t per = (steps + s - 1) / s;
+        if ((steps + per - 1) / per != s) continue;
+        const uint64_t blocks = tiles * s, rounds = (blocks + slots - 1) / slots;
+        const double fill = (double)blocks / (double)(rounds * slots);
+        if (fill > best + 0.02) {
+            best = fill;
+            splits = s;
+        }
+    }
     const char* es = std::getenv("QORA_HIP_PF_SPLITS");
-    if (es && *es) splits = std::max(1, std::atoi(es));
-    splits = std::min(splits, std::max(1u, steps / 8u));   // at least 8 steps (256 rows) a split
+    if (es && *es) splits = std::min(std::max(1, std::atoi(es)), (int)std::max(1u, steps / 8u));
     const uint32_t per = (steps + splits - 1) / splits;
     sh.kper = per * 32u;
     sh.splits = (steps + per - 1) / per;

@@ -111,10 +111,11 @@ PfGemmShape pf_gemm_shape(uint32_t T, uint32_t k, uint32_t n, int cus);
 hipError_t launch_pf_gemm(int fmt, const PrefillGemmParams& p, hipStream_t stream);
 // Prefill GEMM on pre-packed Q4 weights (pf_gemm2_kernel). pack: the packed
 // copy of a Q4 weight [k][n] (k % 32 == 0, n % 128 == 0) into wq (k n / 2
-// bytes) and sc (k n / 16 bytes).
+// bytes) and sc (k n / 16 bytes, the scales times 2^-wf[group]); wf from
+// launch_pf_weight_exp.
 bool pf_gemm2_supported(uint32_t k, uint32_t n);
-hipError_t launch_pf_pack_q4(const uint8_t* w, const uint16_t* scales, uint32_t k, uint32_t n, uint2* wq,
-                             uint16_t* sc, hipStream_t stream);
+hipError_t launch_pf_pack_q4(const uint8_t* w, const uint16_t* scales, const int8_t* wf, uint32_t k, uint32_t n,
+                             uint2* wq, uint16_t* sc, hipStream_t stream);
 struct PfGemm2Shape {
     uint32_t bm, splits, kper;
 };

@@ -477,26 +477,42 @@ __global__ __launch_bounds__(256) void pf_gemm_kernel(PrefillGemmParams p) {
 // the LDS is double-buffered (one barrier per step). Up to three weight
 // segments share the launch (q|k|v, gate|up): column block b belongs to the
 // segment whose blocks start at or below it.
+//
+// Packed layout (pf_pack_q4_kernel), per 128-column block nb and 32-row step
+// ks: thread t = 64 rg + bc owns columns 2 bc, 2 bc + 1 and rows 8 rg .. 8 rg + 7.
+// Word c of its uint2 holds column 2 bc + c: row 8 rg + 2 j in nibble j and row
+// 8 rg + 2 j + 1 in nibble j + 4, so (word >> 4 j) & 0x000F000F is the pair of
+// rows (2 j, 2 j + 1) in the low bits of two binary16 halves. The scales are
+// stored as binary16 s' = s 2^-f_g (|s'| < 2^12), row-major per group:
+// sc[((nb KS + ks) 4 + g) 32 + r]; s' is exact unless a group's scales span
+// more than 2^26, where it rounds to the binary16 subnormal grid (an error
+// below 2^-37 of the group's largest weight).
+// Dequantisation in packed binary16: (0x6400 | q) is 1024 + q, minus 1032 is
+// q - 8 (exact), times s' gives wh = f16(q' s') (one rounding of the exact
+// 15-bit product, as f32 then f16 would give), and fma(q', s', -wh) gives
+// wl = f16(q' s' - wh): the same wh, wl as the fp32 path, two rows at a time.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void pf_pack_q4_kernel(const uint8_t* w, const uint16_t* scales, uint32_t k,
-                                                         uint32_t n, uint2* wq, uint16_t* sc) {
-    // block (nb, ks): thread t packs its 8 bytes and, for t < 128, one scale row
+__global__ __launch_bounds__(256) void pf_pack_q4_kernel(const uint8_t* w, const uint16_t* scales, const int8_t* wf,
+                                                         uint32_t k, uint32_t n, uint2* wq, uint16_t* sc) {
+    // block (nb, ks): thread t packs its 16 nibbles and, for t < 128, one scale row
     const uint32_t nb = blockIdx.x, ks = blockIdx.y, KS = k / 32u;
     const uint32_t t = threadIdx.x, bc = t % 64u, rg = t / 64u;
     const uint32_t col = nb * 128u + 2u * bc;
-    uint32_t lo = 0, hi = 0;
+    uint32_t w0 = 0, w1 = 0;
 #pragma unroll
     for (int r = 0; r < 8; ++r) {
         const uint32_t row = ks * 32u + rg * 8u + (uint32_t)r;
         const uint32_t b = w[(uint64_t)row * (n / 2u) + col / 2u];
-        if (r < 4) lo |= b << (8 * r);
-        else hi |= b << (8 * (r - 4));
+        const int slot = (r >> 1) + 4 * (r & 1);
+        w0 |= (b & 0xFu) << (4 * slot);
+        w1 |= (b >> 4) << (4 * slot);
     }
-    wq[((uint64_t)nb * KS + ks) * 256u + t] = make_uint2(lo, hi);
+    wq[((uint64_t)nb * KS + ks) * 256u + t] = make_uint2(w0, w1);
     if (t < 128u) {
         const uint32_t g = t / 32u, r = t % 32u;
-        sc[(((uint64_t)nb * KS + ks) * 4u + g) * 32u + r] =
-            scales[(uint64_t)(ks * 32u + r) * (n / 32u) + nb * 4u + g];
+        const uint16_t s = scales[(uint64_t)(ks * 32u + r) * (n / 32u) + nb * 4u + g];
+        const _Float16 sv = (_Float16)(h2f(s) * ldexpf(1.0f, -(int)wf[nb * 4u + g]));
+        sc[(((uint64_t)nb * KS + ks) * 4u + g) * 32u + r] = __builtin_bit_cast(uint16_t, sv);
     }
 }
 
@@ -535,7 +551,6 @@ __global__ __launch_bounds__(256) void pf_gemm2_kernel(PfGemm2Params p) {
     // weights: columns 2 bc, 2 bc + 1 of the block, rows 8 rg .. 8 rg + 7 of the step
     const uint32_t bc = (uint32_t)t % 64u, rg = (uint32_t)t / 64u;
     const uint32_t g = bc / 16u;                    // 32-column group in the block
-    const float wscale = ldexpf(1.0f, -(int)sg.wf[lnb * 4u + g]);
     const uint2* wqp = sg.wq + (uint64_t)lnb * KS * 256u + (uint32_t)t;
     const uint16_t* scp = sg.sc + ((uint64_t)lnb * KS * 4u + g) * 32u + rg * 8u;
 
@@ -543,7 +558,7 @@ __global__ __launch_bounds__(256) void pf_gemm2_kernel(PfGemm2Params p) {
     struct Slice {
         v4u32 xh0, xh1, xl0, xl1;                   // x' pieces (xh1, xl1: 128-token tiles only)
         v2u32 wq;
-        v4u32 sc;                                   // 8 f16 scales, rows 8 rg .. + 7
+        v4u32 sc;                                   // 8 binary16 s', rows 8 rg .. + 7 (pairs)
     };
     auto load_slice = [&](Slice& q, uint32_t s) {
         const uint32_t k0 = kb + s * (uint32_t)KC;
@@ -564,25 +579,28 @@ __global__ __launch_bounds__(256) void pf_gemm2_kernel(PfGemm2Params p) {
             *reinterpret_cast<v4u32*>(&xs[buf][0][xr * XS + xq * XH + 8]) = q.xh1;
             *reinterpret_cast<v4u32*>(&xs[buf][1][xr * XS + xq * XH + 8]) = q.xl1;
         }
-        _Float16 h0[8], h1[8], l0[8], l1[8];
+        // wh, wl of columns 2 bc, 2 bc + 1, two rows per binary16 pair
+        const half2v bias = {(_Float16)1032.0f, (_Float16)1032.0f};
+        v4u32 wh[2], wl[2];
 #pragma unroll
-        for (int r = 0; r < 8; ++r) {
-            const uint32_t byte = (q.wq[r / 4] >> (8 * (r & 3))) & 0xFFu;
-            const uint32_t sw2 = q.sc[r / 2];
-            const uint16_t sb = (uint16_t)((r & 1) ? (sw2 >> 16) : (sw2 & 0xFFFFu));
-            const float sv = h2f(sb) * wscale;      // exact: power-of-two scaling
-            const float w0 = sv * (float)((int)(byte & 0xFu) - 8);
-            const float w1 = sv * (float)((int)(byte >> 4) - 8);
-            h0[r] = (_Float16)w0;
-            h1[r] = (_Float16)w1;
-            l0[r] = (_Float16)(w0 - (float)h0[r]);
-            l1[r] = (_Float16)(w1 - (float)h1[r]);
+        for (int c = 0; c < 2; ++c) {
+            const uint32_t wv = q.wq[c];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const half2v qv = __builtin_bit_cast(half2v, ((wv >> (4 * j)) & 0x000F000Fu) | 0x64006400u) - bias;
+                const uint32_t sj = q.sc[j];        // (a bit_cast of a vector element would read element 0)
+                const half2v sv = __builtin_bit_cast(half2v, sj);
+                const half2v h = qv * sv;
+                const half2v l = __builtin_elementwise_fma(qv, sv, -h);
+                wh[c][j] = __builtin_bit_cast(uint32_t, h);
+                wl[c][j] = __builtin_bit_cast(uint32_t, l);
+            }
         }
         const uint32_t c0 = (2u * bc) * XS + rg * 8u, c1 = (2u * bc + 1u) * XS + rg * 8u;
-        *reinterpret_cast<half8v*>(&ws[buf][0][c0]) = half8v{h0[0], h0[1], h0[2], h0[3], h0[4], h0[5], h0[6], h0[7]};
-        *reinterpret_cast<half8v*>(&ws[buf][0][c1]) = half8v{h1[0], h1[1], h1[2], h1[3], h1[4], h1[5], h1[6], h1[7]};
-        *reinterpret_cast<half8v*>(&ws[buf][1][c0]) = half8v{l0[0], l0[1], l0[2], l0[3], l0[4], l0[5], l0[6], l0[7]};
-        *reinterpret_cast<half8v*>(&ws[buf][1][c1]) = half8v{l1[0], l1[1], l1[2], l1[3], l1[4], l1[5], l1[6], l1[7]};
+        *reinterpret_cast<v4u32*>(&ws[buf][0][c0]) = wh[0];
+        *reinterpret_cast<v4u32*>(&ws[buf][0][c1]) = wh[1];
+        *reinterpret_cast<v4u32*>(&ws[buf][1][c0]) = wl[0];
+        *reinterpret_cast<v4u32*>(&ws[buf][1][c1]) = wl[1];
     };
 
     f32x4v acc[TM][TN];
