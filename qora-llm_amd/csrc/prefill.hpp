@@ -479,10 +479,13 @@ __global__ __launch_bounds__(256) void pf_gemm_kernel(PrefillGemmParams p) {
 // segment whose blocks start at or below it.
 //
 // Packed layout (pf_pack_q4_kernel), per 128-column block nb and 32-row step
-// ks: thread t = 64 rg + bc owns columns 2 bc, 2 bc + 1 and rows 8 rg .. 8 rg + 7.
-// Word c of its uint2 holds column 2 bc + c: row 8 rg + 2 j in nibble j and row
-// 8 rg + 2 j + 1 in nibble j + 4, so (word >> 4 j) & 0x000F000F is the pair of
-// rows (2 j, 2 j + 1) in the low bits of two binary16 halves. The scales are
+// ks: thread t = 64 rg + bc owns columns c0 = 32 (bc / 16) + bc % 16 and
+// c0 + 16 (one 32-column group, so one set of scales) and rows 8 rg .. 8 rg + 7;
+// consecutive lanes own consecutive columns, so their LDS stores (80-byte
+// column stride) fall in distinct banks. Word c of its uint2 holds column
+// c0 + 16 c: row 8 rg + 2 j in nibble j and row 8 rg + 2 j + 1 in nibble j + 4,
+// so (word >> 4 j) & 0x000F000F is the pair of rows (2 j, 2 j + 1) in the low
+// bits of two binary16 halves. The scales are
 // stored as binary16 s' = s 2^-f_g (|s'| < 2^12), row-major per group:
 // sc[((nb KS + ks) 4 + g) 32 + r]; s' is exact unless a group's scales span
 // more than 2^26, where it rounds to the binary16 subnormal grid (an error
@@ -497,15 +500,16 @@ __global__ __launch_bounds__(256) void pf_pack_q4_kernel(const uint8_t* w, const
     // block (nb, ks): thread t packs its 16 nibbles and, for t < 128, one scale row
     const uint32_t nb = blockIdx.x, ks = blockIdx.y, KS = k / 32u;
     const uint32_t t = threadIdx.x, bc = t % 64u, rg = t / 64u;
-    const uint32_t col = nb * 128u + 2u * bc;
+    const uint32_t c0 = nb * 128u + (bc / 16u) * 32u + bc % 16u, c1 = c0 + 16u;
     uint32_t w0 = 0, w1 = 0;
 #pragma unroll
     for (int r = 0; r < 8; ++r) {
         const uint32_t row = ks * 32u + rg * 8u + (uint32_t)r;
-        const uint32_t b = w[(uint64_t)row * (n / 2u) + col / 2u];
+        const uint32_t b0 = w[(uint64_t)row * (n / 2u) + c0 / 2u], b1 = w[(uint64_t)row * (n / 2u) + c1 / 2u];
         const int slot = (r >> 1) + 4 * (r & 1);
-        w0 |= (b & 0xFu) << (4 * slot);
-        w1 |= (b >> 4) << (4 * slot);
+        // column c is the low nibble of byte c / 2 when c is even
+        w0 |= ((c0 & 1u) ? (b0 >> 4) : (b0 & 0xFu)) << (4 * slot);
+        w1 |= ((c1 & 1u) ? (b1 >> 4) : (b1 & 0xFu)) << (4 * slot);
     }
     wq[((uint64_t)nb * KS + ks) * 256u + t] = make_uint2(w0, w1);
     if (t < 128u) {
@@ -548,8 +552,9 @@ __global__ __launch_bounds__(256) void pf_gemm2_kernel(PfGemm2Params p) {
     // x' rows: thread t loads XH halves of row t / XT (rows past T read row T - 1, masked at the end)
     const uint32_t xr = (uint32_t)t / XT, xq = (uint32_t)t % XT;
     const uint64_t xoff = (uint64_t)min(m0 + xr, p.T - 1u) * K + xq * XH;
-    // weights: columns 2 bc, 2 bc + 1 of the block, rows 8 rg .. 8 rg + 7 of the step
+    // weights: columns cw, cw + 16 of the block, rows 8 rg .. 8 rg + 7 of the step
     const uint32_t bc = (uint32_t)t % 64u, rg = (uint32_t)t / 64u;
+    const uint32_t cw = (bc / 16u) * 32u + bc % 16u;
     const uint32_t g = bc / 16u;                    // 32-column group in the block
     const uint2* wqp = sg.wq + (uint64_t)lnb * KS * 256u + (uint32_t)t;
     const uint16_t* scp = sg.sc + ((uint64_t)lnb * KS * 4u + g) * 32u + rg * 8u;
@@ -579,7 +584,7 @@ __global__ __launch_bounds__(256) void pf_gemm2_kernel(PfGemm2Params p) {
             *reinterpret_cast<v4u32*>(&xs[buf][0][xr * XS + xq * XH + 8]) = q.xh1;
             *reinterpret_cast<v4u32*>(&xs[buf][1][xr * XS + xq * XH + 8]) = q.xl1;
         }
-        // wh, wl of columns 2 bc, 2 bc + 1, two rows per binary16 pair
+        // wh, wl of columns cw, cw + 16, two rows per binary16 pair
         const half2v bias = {(_Float16)1032.0f, (_Float16)1032.0f};
         v4u32 wh[2], wl[2];
 #pragma unroll
@@ -596,7 +601,7 @@ __global__ __launch_bounds__(256) void pf_gemm2_kernel(PfGemm2Params p) {
                 wl[c][j] = __builtin_bit_cast(uint32_t, l);
             }
         }
-        const uint32_t c0 = (2u * bc) * XS + rg * 8u, c1 = (2u * bc + 1u) * XS + rg * 8u;
+        const uint32_t c0 = cw * XS + rg * 8u, c1 = (cw + 16u) * XS + rg * 8u;
         *reinterpret_cast<v4u32*>(&ws[buf][0][c0]) = wh[0];
         *reinterpret_cast<v4u32*>(&ws[buf][0][c1]) = wh[1];
         *reinterpret_cast<v4u32*>(&ws[buf][1][c0]) = wl[0];
@@ -634,22 +639,33 @@ __global__ __launch_bounds__(256) void pf_gemm2_kernel(PfGemm2Params p) {
     };
 
     // global loads run two steps ahead of the matrix cores: slice se holds the
-    // even steps, so the odd ones; the LDS buffer of step s is s & 1
+    // even steps, so the odd ones; the LDS buffer of step s is s & 1. The
+    // steady-state loop has no branches, so the compiler interleaves one
+    // step's matrix-core work with the dequantisation and LDS stores of the
+    // next (loads of a clamped step index past the end stay in bounds and are
+    // not used).
     Slice se, so;
-    if (steps > 0) load_slice(se, 0);
-    if (steps > 1) load_slice(so, 1);
-    if (steps > 0) store_slice(se, 0);
-    __syncthreads();
-    for (uint32_t s = 0; s < steps; s += 2) {
-        if (s + 2 < steps) load_slice(se, s + 2);
-        compute(0);
-        if (s + 1 < steps) store_slice(so, 1);
+    if (steps > 0) {
+        load_slice(se, 0);
+        load_slice(so, min(1u, steps - 1u));
+        store_slice(se, 0);
         __syncthreads();
-        if (s + 1 < steps) {
-            if (s + 3 < steps) load_slice(so, s + 3);
-            compute(1);
-            if (s + 2 < steps) store_slice(se, 0);
+        uint32_t s = 0;
+        for (; s + 2 < steps; s += 2) {
+            load_slice(se, s + 2);
+            compute(0);
+            store_slice(so, 1);
             __syncthreads();
+            load_slice(so, min(s + 3u, steps - 1u));
+            compute(1);
+            store_slice(se, 0);
+            __syncthreads();
+        }
+        compute(0);
+        if (s + 1 < steps) {
+            store_slice(so, 1);
+            __syncthreads();
+            compute(1);
         }
     }
 
