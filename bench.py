@@ -575,6 +575,71 @@ def profile_kernel(launches=8):
         ctx.gemv_release(g)
 
 
+def probe_residency(pkg, hip, cfg, prompt, steps=128, warmup=8):
+    """What bounds the decode step besides HBM bandwidth: the per-launch floor
+    of a captured graph of dependent launches (the smallest GEMV, 256 -> 128),
+    one GEMV launched on a single prepared copy (L2- and Infinity-Cache-resident)
+    against 8 and 64 rotating copies, and decode with every layer on layer 0's
+    weights (44 MB resident) against the model's own 1.7 GB."""
+    out = {}
+    w = pkg.synthetic_model(cfg, seed=0, rope_positions=2048)
+    ctx = pkg.HipContext(0)
+    try:
+        be = pkg.HipBackend(ctx, w, kv_capacity=2048, kv_dtype=pkg.KV_F32)
+        c = be.config
+        x = ctx.malloc(4 * c.intermediate)
+        acc = ctx.malloc(8 * 2 * c.intermediate)
+        ctx.h2d(x, pkg.synth_f32(0, 77, c.intermediate))
+        packed, scales = pkg.synth_q4(0, 99, 256, 128)
+        tiny = ctx.upload(pkg.Weight(k=256, n=128, packed=packed, scales=scales))
+        g = ctx.gemv_prepare(tiny)
+        run = lambda g=g: ctx.check(ctx.lib.qora_hip_gemv_run(ctx.h, g, x, acc, None), "gemv_run")
+        out["launch_floor_us_gemv_256x128"] = round(time_graph(ctx, hip, [run] * 200) * 1e3, 3)
+        ctx.gemv_release(g)
+        shapes = c.weight_shapes()
+        res = {}
+        for label, j, paired in (("q/o 2048x2048", 0, False), ("down 11008x2048", 6, False),
+                                 ("gate+up 2048x(2x11008)", 4, True)):
+            k, n = shapes[j]
+            nb = (k * n // 2 + k * n // 16) * (2 if paired else 1)
+            per = {}
+            for copies in (1, 8, 64):
+                gids = [ctx.gemv_prepare(int(be.wids[0, j]), int(be.wids[0, 5]) if paired else 0, paired)
+                        for _ in range(copies)]
+                fns = [(lambda g=g: ctx.check(ctx.lib.qora_hip_gemv_run(ctx.h, g, x, acc, None), "gemv_run"))
+                       for g in gids] * max(1, 64 // copies)
+                ms = time_graph(ctx, hip, fns)
+                for g in gids:
+                    ctx.gemv_release(g)
+                per[f"{copies} copies ({copies * nb / 2**20:.0f} MiB)"] = round(ms * 1e3, 3)
+            res[label] = per
+        out["gemv_us_by_copies"] = res
+        ctx.free(x)
+        ctx.free(acc)
+    finally:
+        ctx.close()
+
+    def decode_rate(shared):
+        ctx = pkg.HipContext(0)
+        try:
+            be = pkg.HipBackend(ctx, w, kv_capacity=2048, kv_dtype=pkg.KV_F32, shared_layers=shared)
+            _, tok = be.raw_prefill(prompt, want_logits=False)
+            for _ in range(warmup):
+                _, tok = be.forward_decode_raw(tok, want_logits=False)
+            ctx.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                _, tok = be.forward_decode_raw(tok, want_logits=False)
+            ctx.synchronize()
+            return steps / (time.perf_counter() - t0)
+        finally:
+            ctx.close()
+
+    out["decode_tok_s_own_weights"] = round(decode_rate(False), 1)
+    out["decode_tok_s_layer0_weights_everywhere"] = round(decode_rate(True), 1)
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -595,6 +660,8 @@ def main():
     ap.add_argument("--profile-decode", action="store_true",
                     help="only the 64-token prefill and 16 decode tokens, launched eagerly after device copies "
                          "of known size, for hardware-counter runs")
+    ap.add_argument("--probe-residency", action="store_true",
+                    help="only the launch-floor and cache-residency probes of the decode step")
     ap.add_argument("--profile-kernel", action="store_true",
                     help="only launch the dominant kernel (gate|up GEMV) eagerly, after a device copy of "
                          "known size, for hardware-counter runs")
@@ -609,6 +676,12 @@ def main():
         sys.exit(2)
     if args.profile_kernel:
         profile_kernel()
+        return
+    if args.probe_residency:
+        pkg = entry.load_package()
+        cfg = pkg.SMOLLM3_3B
+        prompt = pkg.synth_tokens(0, 2000, 64, cfg.vocab)
+        print(json.dumps({"probe_residency": probe_residency(pkg, Hip(), cfg, prompt)}), flush=True)
         return
     if args.profile_decode:
         os.environ["QORA_HIP_EAGER"] = "1"

@@ -503,14 +503,20 @@ class HipBackend:
     Mirrors the reference's decode API (gemv.rs:872-876, 1027-1030) with the
     RawKvCache held on the device inside the context."""
 
-    def __init__(self, ctx: HipContext, weights: DecodeWeights, kv_capacity: int = 2048, kv_dtype: int = KV_F32):
+    def __init__(self, ctx: HipContext, weights: DecodeWeights, kv_capacity: int = 2048, kv_dtype: int = KV_F32,
+                 shared_layers: bool = False):
+        """shared_layers: every layer uses layer 0's uploaded weights (one layer's
+        bytes on the device: a cache-residency probe, not a model)."""
         self.ctx = ctx
         self.weights = weights
         c = weights.config
         self.config = c
         self.kv_capacity = kv_capacity
         self.kv_dtype = kv_dtype
-        wids = np.array([ctx.upload(w) for ws in weights.layers for w in ws], dtype=np.uint32)
+        if shared_layers:
+            wids = np.array([ctx.upload(w) for w in weights.layers[0]] * c.num_layers, dtype=np.uint32)
+        else:
+            wids = np.array([ctx.upload(w) for ws in weights.layers for w in ws], dtype=np.uint32)
         embed_wid = ctx.upload(weights.embed)
         self._keep = [wids]
         in_ptrs = (ctypes.c_void_p * c.num_layers)(*[_ptr(g) for g in weights.input_norm])
