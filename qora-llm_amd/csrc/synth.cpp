@@ -4,9 +4,12 @@
 //   key  = mix64(seed ^ mix64(tensor_id + C))
 //   r_i  = mix64(key + (i + 1) * 0x9E3779B97F4A7C15)   (splitmix64 output i)
 // so tensors can be generated in parallel, in any order, bit for bit.
-// Normals are the sum of the four 16-bit lanes of r_i, centred and scaled to
-// unit variance (an Irwin-Hall approximation computed exactly in float64), so
-// the numpy restatement used by the tests reproduces every byte.
+// Normals are Box-Muller draws: u1, u2 = the high and low 32 bits of r_i
+// (+ 1/2, times 2^-32), z = sqrt(-2 ln u1) cos(2 pi (u2 - 1/2)) (tails to
+// 6.8 sigma). ln and cos are evaluated here from + - * / and sqrt alone
+// (frexp, an atanh series for ln, a halved-angle Taylor series for cos), all
+// correctly rounded in float64, so the numpy restatement used by the tests
+// reproduces every byte.
 #include "../../include/qora_hip.h"
 
 #include <algorithm>
@@ -31,13 +34,45 @@ inline uint64_t stream_key(uint64_t seed, uint64_t tensor_id) {
 
 inline uint64_t draw(uint64_t key, uint64_t i) { return mix64(key + (i + 1) * kGolden); }
 
-// 4 * var(U{0..65535}) = 4 * (65536^2 - 1) / 12
-const double kInvStd = 1.0 / std::sqrt(1431655765.0);
+// ln u for 0 < u <= 1: u = m 2^e with m in [sqrt(1/2), sqrt(2)), ln m =
+// 2 atanh(t) = 2 t sum_k t^(2k) / (2k + 1), t = (m - 1) / (m + 1), |t| < 0.172
+// (terms to t^22).
+inline double ln_unit(double u) {
+    int e = 0;
+    double m = std::frexp(u, &e);                  // u = m 2^e, m in [1/2, 1)
+    if (m < 0.70710678118654752) {
+        m = m * 2.0;
+        e = e - 1;
+    }
+    const double t = (m - 1.0) / (m + 1.0), t2 = t * t;
+    double s = 1.0 / 23.0;
+    for (int k = 10; k >= 0; --k) s = s * t2 + 1.0 / (2.0 * k + 1.0);
+    return (double)e * 0.6931471805599453 + 2.0 * t * s;
+}
+
+// (-1)^k / (2k)!, k = 0..12, by repeated division
+struct CosCoef {
+    double c[13];
+    CosCoef() {
+        c[0] = 1.0;
+        for (int k = 1; k <= 12; ++k) c[k] = -c[k - 1] / ((2.0 * k - 1.0) * (2.0 * k));
+    }
+};
+const CosCoef kCos;
+
+// cos x for |x| <= pi: cos x = 2 cos^2(x / 2) - 1, cos(x / 2) by its Taylor
+// series to (x / 2)^24.
+inline double cos_pm_pi(double x) {
+    const double h = 0.5 * x, h2 = h * h;
+    double c = kCos.c[12];
+    for (int k = 11; k >= 0; --k) c = c * h2 + kCos.c[k];
+    return 2.0 * c * c - 1.0;
+}
 
 inline double normal_of(uint64_t r) {
-    const double s = (double)(r & 0xFFFFu) + (double)((r >> 16) & 0xFFFFu) + (double)((r >> 32) & 0xFFFFu) +
-                     (double)(r >> 48);
-    return (s - 131070.0) * kInvStd;
+    const double u1 = ((double)(r >> 32) + 0.5) * 2.3283064365386963e-10;          // 2^-32
+    const double u2 = ((double)(r & 0xFFFFFFFFull) + 0.5) * 2.3283064365386963e-10;
+    return std::sqrt(-2.0 * ln_unit(u1)) * cos_pm_pi(6.283185307179586 * (u2 - 0.5));
 }
 
 // binary32 -> binary16, round to nearest even.
