@@ -474,7 +474,8 @@ __global__ __launch_bounds__(256) void pf_gemm_kernel(PrefillGemmParams p) {
 // a thread loads its x' row piece (both parts), 8 bytes of packed weights
 // (16 values) and 16 bytes of their scales; the next step's loads are in
 // flight while the current step's operands go through the matrix cores, and
-// the LDS is double-buffered (one barrier per step). Up to three weight
+// the LDS is double-buffered (one barrier per step; 64 KB a block at 128
+// tokens, two blocks per CU). Up to three weight
 // segments share the launch (q|k|v, gate|up): column block b belongs to the
 // segment whose blocks start at or below it.
 //
@@ -523,7 +524,11 @@ __global__ __launch_bounds__(256) void pf_pack_q4_kernel(const uint8_t* w, const
 template <int BM>
 __global__ __launch_bounds__(256) void pf_gemm2_kernel(PfGemm2Params p) {
     constexpr int BN = 128, KC = 32;
-    constexpr int XS = KC + 8;                      // LDS row stride in halves (80 B)
+    // LDS rows of 64 B (32 halves, no padding); the 16-byte chunk c of row r
+    // sits at chunk c ^ ((r >> 1) & 3), which leaves the fragment reads, the
+    // x' stores (two or four threads a row) and the weight stores (lanes on
+    // consecutive columns) free of bank conflicts
+    constexpr int XS = KC;
     constexpr int WM = BM / 2, TM = WM / 16, TN = 4;
     constexpr int XT = 256 / BM;                    // threads per x' row (2 or 4)
     constexpr int XH = KC / XT;                     // halves of a row per thread (16 or 8)
@@ -578,11 +583,13 @@ __global__ __launch_bounds__(256) void pf_gemm2_kernel(PfGemm2Params p) {
         q.sc = *reinterpret_cast<const v4u32*>(scp + (uint64_t)ks * 128u);
     };
     auto store_slice = [&](const Slice& q, int buf) {
-        *reinterpret_cast<v4u32*>(&xs[buf][0][xr * XS + xq * XH]) = q.xh0;
-        *reinterpret_cast<v4u32*>(&xs[buf][1][xr * XS + xq * XH]) = q.xl0;
+        const uint32_t xsw = (xr >> 1) & 3u;
+        const uint32_t xc0 = xr * XS + ((xq * XV) ^ xsw) * 8u, xc1 = xr * XS + ((xq * XV + 1u) ^ xsw) * 8u;
+        *reinterpret_cast<v4u32*>(&xs[buf][0][xc0]) = q.xh0;
+        *reinterpret_cast<v4u32*>(&xs[buf][1][xc0]) = q.xl0;
         if constexpr (XV == 2) {
-            *reinterpret_cast<v4u32*>(&xs[buf][0][xr * XS + xq * XH + 8]) = q.xh1;
-            *reinterpret_cast<v4u32*>(&xs[buf][1][xr * XS + xq * XH + 8]) = q.xl1;
+            *reinterpret_cast<v4u32*>(&xs[buf][0][xc1]) = q.xh1;
+            *reinterpret_cast<v4u32*>(&xs[buf][1][xc1]) = q.xl1;
         }
         // wh, wl of columns cw, cw + 16, two rows per binary16 pair
         const half2v bias = {(_Float16)1032.0f, (_Float16)1032.0f};
@@ -601,7 +608,8 @@ __global__ __launch_bounds__(256) void pf_gemm2_kernel(PfGemm2Params p) {
                 wl[c][j] = __builtin_bit_cast(uint32_t, l);
             }
         }
-        const uint32_t c0 = cw * XS + rg * 8u, c1 = (cw + 16u) * XS + rg * 8u;
+        const uint32_t wsw = (cw >> 1) & 3u;               // the same for cw + 16
+        const uint32_t c0 = cw * XS + (rg ^ wsw) * 8u, c1 = (cw + 16u) * XS + (rg ^ wsw) * 8u;
         *reinterpret_cast<v4u32*>(&ws[buf][0][c0]) = wh[0];
         *reinterpret_cast<v4u32*>(&ws[buf][0][c1]) = wh[1];
         *reinterpret_cast<v4u32*>(&ws[buf][1][c0]) = wl[0];
@@ -619,14 +627,16 @@ __global__ __launch_bounds__(256) void pf_gemm2_kernel(PfGemm2Params p) {
 #pragma unroll
         for (int i = 0; i < TM; ++i) {
             const uint32_t row = (uint32_t)wm * WM + (uint32_t)i * 16u + li;
-            ah[i] = *reinterpret_cast<const half8v*>(&xs[buf][0][row * XS + kq * 8u]);
-            al[i] = *reinterpret_cast<const half8v*>(&xs[buf][1][row * XS + kq * 8u]);
+            const uint32_t ch = kq ^ ((li >> 1) & 3u);     // row % 16 == li
+            ah[i] = *reinterpret_cast<const half8v*>(&xs[buf][0][row * XS + ch * 8u]);
+            al[i] = *reinterpret_cast<const half8v*>(&xs[buf][1][row * XS + ch * 8u]);
         }
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
             const uint32_t c = (uint32_t)wn * 64u + (uint32_t)j * 16u + li;
-            bh[j] = *reinterpret_cast<const half8v*>(&ws[buf][0][c * XS + kq * 8u]);
-            bl[j] = *reinterpret_cast<const half8v*>(&ws[buf][1][c * XS + kq * 8u]);
+            const uint32_t ch = kq ^ ((li >> 1) & 3u);     // c % 16 == li
+            bh[j] = *reinterpret_cast<const half8v*>(&ws[buf][0][c * XS + ch * 8u]);
+            bl[j] = *reinterpret_cast<const half8v*>(&ws[buf][1][c * XS + ch * 8u]);
         }
 #pragma unroll
         for (int j = 0; j < TN; ++j)
