@@ -821,6 +821,9 @@ __global__ __launch_bounds__(512) void attn_decode_direct_kernel(AttnParams p) {
     for (int g = 0; g < G4; ++g)
 #pragma unroll
         for (int d = 0; d < VD; ++d) qv[g][d] = (uint32_t)g < G ? qs[g * HD + vc * VD + d] : 0.f;
+    // scores in log2 units (scale * log2 e): the weights 2^(s - m) are e^(s' - m')
+    // of the natural-log scores, one v_exp_f32 each; m goes out as m ln 2
+    const float scale2 = p.scale * 1.4426950408889634f;
     float m[G4], l[G4], o[G4][VD];
 #pragma unroll
     for (int g = 0; g < G4; ++g) {
@@ -867,7 +870,7 @@ __global__ __launch_bounds__(512) void attn_decode_direct_kernel(AttnParams p) {
 #pragma unroll
                 for (int d = 0; d < VD; ++d) a = fmaf(qv[g][d], k[d], a);
                 a = row16_sum(a);
-                s[i][g] = 4u * i + vj < cn ? a * p.scale : -INFINITY;
+                s[i][g] = 4u * i + vj < cn ? a * scale2 : -INFINITY;
             }
         }
         load_rows(kr, kc, p0 + pn * PP);
@@ -881,11 +884,13 @@ __global__ __launch_bounds__(512) void attn_decode_direct_kernel(AttnParams p) {
             mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
             mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
             const float m_new = fmaxf(m[g], mx);
-            f[g] = expf(m[g] - m_new);              // 0 on the first pass
+            // v_exp_f32 itself: arguments <= 0, and weights below 2^-126 (flushed
+            // to zero) cannot reach a sum that holds the maximum's 1
+            f[g] = __builtin_amdgcn_exp2f(m[g] - m_new);   // 0 on the first pass
             float sum = 0.f;
 #pragma unroll
             for (int i = 0; i < NI; ++i) {
-                const float e = 4u * i + vj < cn ? expf(s[i][g] - m_new) : 0.f;
+                const float e = 4u * i + vj < cn ? __builtin_amdgcn_exp2f(s[i][g] - m_new) : 0.f;
                 s[i][g] = e;
                 sum += e;
             }
@@ -960,14 +965,14 @@ __global__ __launch_bounds__(512) void attn_decode_direct_kernel(AttnParams p) {
     for (int w = 0; w < NWV; ++w) mx = fmaxf(mx, red_m[w][g]);
     float acc = 0.f, lt = 0.f;
     for (int w = 0; w < NWV; ++w) {
-        const float wt = expf(red_m[w][g] - mx);   // 0 for a wave without passes
+        const float wt = exp2f(red_m[w][g] - mx);  // 0 for a wave without passes
         acc = fmaf(red_o[w][g][d], wt, acc);
         lt = fmaf(red_l[w][g], wt, lt);
     }
     float* part = p.part + (((uint64_t)kvh * p.s_max + split) * G + g) * (hd + 2);
     part[d] = acc;
     if (d == 0) {
-        part[hd] = mx;
+        part[hd] = mx * 0.6931471805599453f;       // natural-log units for the merge
         part[hd + 1] = lt;
     }
 }
