@@ -738,12 +738,13 @@ __global__ __launch_bounds__(512) void attn_decode_direct_kernel(AttnParams p) {
     const uint16_t* kc = reinterpret_cast<const uint16_t*>(p.kc);
     const uint16_t* vcache = reinterpret_cast<const uint16_t*>(p.vc);
     VW kr[NI], vr[NI];
+    auto load_row = [&](VW& dst, const uint16_t* src, uint32_t c0, int i) {
+        const uint64_t off = (uint64_t)min(c0 + 4u * i + vj, p1 - 1u) * cps + coff + vc * VD;
+        dst = *reinterpret_cast<const VW*>(src + off);
+    };
     auto load_rows = [&](VW (&dst)[NI], const uint16_t* src, uint32_t c0) {
 #pragma unroll
-        for (int i = 0; i < NI; ++i) {
-            const uint64_t off = (uint64_t)min(c0 + 4u * i + vj, p1 - 1u) * cps + coff + vc * VD;
-            dst[i] = *reinterpret_cast<const VW*>(src + off);
-        }
+        for (int i = 0; i < NI; ++i) load_row(dst[i], src, c0, i);
     };
     constexpr uint32_t QPT = G4 * HD / 256;          // q values per set-up thread
     const bool qset = t < 256 && model;
@@ -832,9 +833,10 @@ __global__ __launch_bounds__(512) void attn_decode_direct_kernel(AttnParams p) {
 #pragma unroll
         for (int d = 0; d < VD; ++d) o[g][d] = 0.f;
     }
-    // Each wave's passes: wave, wave + NWV, ... The next pass's K rows go into
-    // the K registers as soon as the scores are done, its V rows into the V
-    // registers after p.V, so one pass's loads overlap the other's arithmetic.
+    // Each wave's passes: wave, wave + NWV, ... Row i of the next pass goes
+    // into the K registers as soon as row i's scores are done, and into the V
+    // registers after row i's p.V, so one pass's loads overlap the other's
+    // arithmetic.
     for (uint32_t pi = wave; pi < npass; pi += NWV) {
         const uint32_t c0 = p0 + pi * PP;
         const uint32_t cn = min((uint32_t)PP, p1 - c0);
@@ -872,8 +874,8 @@ __global__ __launch_bounds__(512) void attn_decode_direct_kernel(AttnParams p) {
                 a = row16_sum(a);
                 s[i][g] = 4u * i + vj < cn ? a * scale2 : -INFINITY;
             }
+            load_row(kr[i], kc, p0 + pn * PP, i);     // row i of the next pass, as soon as it is free
         }
-        load_rows(kr, kc, p0 + pn * PP);
         // ---- online softmax per head over the pass ----
         float f[G4];
 #pragma unroll
@@ -906,7 +908,7 @@ __global__ __launch_bounds__(512) void attn_decode_direct_kernel(AttnParams p) {
             for (int d = 0; d < VD; ++d) o[g][d] *= f[g];
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
-            if (4u * i + vj >= cn) continue;
+            if (4u * i + vj < cn) {
             float v[VD];
             if constexpr (VD == 8) {
                 const uint32_t w4[4] = {vr[i].x, vr[i].y, vr[i].z, vr[i].w};
@@ -931,8 +933,9 @@ __global__ __launch_bounds__(512) void attn_decode_direct_kernel(AttnParams p) {
             for (int g = 0; g < G4; ++g)
 #pragma unroll
                 for (int d = 0; d < VD; ++d) o[g][d] = fmaf(s[i][g], v[d], o[g][d]);
+            }
+            load_row(vr[i], vcache, p0 + pn * PP, i);
         }
-        load_rows(vr, vcache, p0 + pn * PP);
     }
     // ---- this wave's totals: sum the four position phases (lanes c, c + 16, c + 32, c + 48) ----
 #pragma unroll
