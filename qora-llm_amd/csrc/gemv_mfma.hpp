@@ -168,12 +168,10 @@ __device__ __forceinline__ void gemv_q4m_load_scales(const GemvParams& p, uint64
 // Slots past the active splits are skipped by selection, so stale bits never
 // reach the sum. aw: LDS of kAttnMaxSplits floats per head, private to the
 // calling wave.
-// Latency: the number of active splits depends on the position, so the
-// loads that do not are issued with the position load: the running max and
-// sum of every split (lane s: split s) and the rows of the first
-// kMergeSpec splits, which cover every split of a short context; longer
-// contexts fetch the remaining rows after the position arrives.
-constexpr uint32_t kMergeSpec = 4;
+// Latency: every load is issued with the position load, before the number
+// of active splits is known: the running max and sum of every split (lane s:
+// split s) and the row of every split up to the launch's split count (slots
+// past the active splits are read but never selected).
 
 __device__ __forceinline__ void attn_merge_rows_wave(const GemvParams& p, uint32_t k0, uint32_t r0, uint32_t r1,
                                                      uint32_t k1, float* xs, float* aw) {
@@ -205,17 +203,11 @@ __device__ __forceinline__ void attn_merge_rows_wave(const GemvParams& p, uint32
     }
     float pv[kAttnMaxSplits / 2];
 #pragma unroll
-    for (uint32_t j = 0; j < kMergeSpec / 2; ++j)
+    for (uint32_t j = 0; j < kAttnMaxSplits / 2; ++j)
         pv[j] = rbase[(uint64_t)min(par + 2u * j, p.attn_s_max - 1u) * sstride];
     const uint32_t L = (uint32_t)pos_raw + 1u;
     const uint32_t chunk = p.attn_chunk ? p.attn_chunk : attn_chunk_for(L);
     const uint32_t s_act = min(p.attn_s_max, (L + chunk - 1) / chunk);
-    // ---- the remaining rows of a longer context ----
-    if (s_act > kMergeSpec) {
-#pragma unroll
-        for (uint32_t j = kMergeSpec / 2; j < kAttnMaxSplits / 2; ++j)
-            pv[j] = rbase[(uint64_t)min(par + 2u * j, s_act - 1u) * sstride];
-    }
     const bool ok = (uint32_t)lane < s_act;
 #pragma unroll
     for (uint32_t q = 0; q < 2; ++q) {
@@ -234,7 +226,7 @@ __device__ __forceinline__ void attn_merge_rows_wave(const GemvParams& p, uint32
 #pragma unroll
     for (uint32_t j = 0; j < kAttnMaxSplits / 2; ++j) {
         const uint32_t sj = par + 2u * j;
-        if (j < kMergeSpec / 2 || s_act > kMergeSpec) v = sj < s_act ? fmaf(pv[j], wrow[sj], v) : v;
+        v = sj < s_act ? fmaf(pv[j], wrow[sj], v) : v;
     }
     v += __shfl_xor(v, 32, kWave);
     if (lane < 32 && i < r1) xs[i] = k0 + i < k1 ? v : 0.f;
