@@ -620,21 +620,22 @@ hipError_t launch_pf_pack_q4(const uint8_t* w, const uint16_t* scales, const int
     return hipGetLastError();
 }
 
-// 128-token tiles from 128 tokens up; then the K split (512 tokens on 256
-// CUs: q|k|v 5, o 8, gate|up 1, down 8).
+// 64-token tiles (three blocks per CU; 128-token tiles, two per CU, measured
+// 2.7% slower over a 512-token prefill), then the K split.
 PfGemm2Shape pf_gemm2_shape(uint32_t T, uint32_t k, uint32_t ntot, int cus) {
     PfGemm2Shape sh{};
-    sh.bm = T >= 128 ? 128u : 64u;
+    sh.bm = 64u;
     const char* eb = std::getenv("QORA_HIP_PF_BM");
     if (eb && *eb) sh.bm = std::atoi(eb) == 64 ? 64u : 128u;
     const uint64_t tiles = std::max<uint64_t>(1, (uint64_t)(ntot / 128u) * ((T + sh.bm - 1) / sh.bm));
     const uint32_t steps = k / 32u;
-    // K is split only when the tiles leave the CUs' block slots (two per CU:
-    // 80 KB of LDS and ~220 registers a thread each) partly empty: beyond one
-    // round of blocks a split adds partial-sum traffic and no speed. The
-    // splits are of equal length (at least 8 steps each, at most 16 splits),
-    // and the count is the one whose blocks fill their rounds best (fewer
-    // splits unless more fill them better by 2% or more).
+    // K is split only when the tiles leave two block slots per CU partly
+    // empty: beyond that a split's partial-sum traffic costs more than it
+    // gains (with 64-token tiles three blocks fit a CU, but splitting for the
+    // third measured slower). The splits are of equal length (at least 8
+    // steps each, at most 16 splits), and the count is the one whose blocks
+    // fill their rounds best (fewer splits unless more fill them better by 2%
+    // or more): 512 tokens on 256 CUs, q|k|v 2, o 4, gate|up 1, down 4.
     const uint64_t slots = 2u * (uint64_t)std::max(1, cus);
     const uint32_t smax = tiles >= slots ? 1u
                                          : (uint32_t)std::min<uint64_t>({16u, std::max(1u, steps / 8u),
