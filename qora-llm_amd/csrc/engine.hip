@@ -1166,8 +1166,18 @@ int pf_gemm(qora_hip_ctx* c, uint32_t l, int j, uint32_t T, float* y, uint32_t l
 // One launch of the packed-weight GEMM over the projections js of layer l
 // (their columns side by side), each written to its own rows ys[i] (row
 // stride ldy) or added to them.
+// Split-K partials left for the next row kernel (the residual add of an o or
+// down GEMM summed by the norm that follows it); part == nullptr: none.
+struct PfDeferred {
+    const float* part = nullptr;
+    uint32_t splits = 0;
+    uint64_t stride = 0;
+};
+
+// defer: when set and the launch splits K over one accumulating segment whose
+// rows are ldy == ntot wide, the partials are left for the caller
 int pf_gemm2(qora_hip_ctx* c, uint32_t l, std::initializer_list<int> js, uint32_t T, std::initializer_list<float*> ys,
-             uint32_t ldy, bool accumulate) {
+             uint32_t ldy, bool accumulate, PfDeferred* defer = nullptr) {
     ModelState& m = c->m;
     PfGemm2Params g{};
     g.xh = m.d_pf_xh;
@@ -1195,7 +1205,9 @@ int pf_gemm2(qora_hip_ctx* c, uint32_t l, std::initializer_list<int> js, uint32_
     g.splits = sh.splits;
     g.kper = sh.kper;
     g.part = m.d_pf_part;
-    HIP_TRY(c, launch_pf_gemm2(sh.bm, g, c->stream));
+    const bool leave = defer && g.splits > 1 && g.nseg == 1 && accumulate && ldy == g.ntot;
+    HIP_TRY(c, launch_pf_gemm2(sh.bm, g, c->stream, !leave));
+    if (defer) *defer = leave ? PfDeferred{g.part, g.splits, (uint64_t)T * g.ntot} : PfDeferred{};
     return QORA_HIP_OK;
 }
 
@@ -1223,6 +1235,7 @@ int prefill_batched(qora_hip_ctx* c, size_t n, float* logits, uint32_t* argmax) 
         r.x = m.d_pf_x;
         r.n = m.hidden;
         HIP_TRY(c, launch_pf_rows(PF_ROW_EMBED, r, T, s));
+        PfDeferred pend;   // the previous layer's down partials, summed by this layer's first norm
         for (uint32_t l = 0; l < m.L; ++l) {
             PrefillRowParams nr{};
             nr.x = m.d_pf_x;
@@ -1231,6 +1244,9 @@ int prefill_batched(qora_hip_ctx* c, size_t n, float* logits, uint32_t* argmax) 
             nr.xh = m.d_pf_xh;
             nr.xl = m.d_pf_xl;
             nr.xe = m.d_pf_xe;
+            nr.part = pend.part;
+            nr.splits = pend.splits;
+            nr.part_stride = pend.stride;
             HIP_TRY(c, launch_pf_rows(PF_ROW_RMSNORM, nr, T, s));
             if (m.pf2) {
                 if (int rc = pf_gemm2(c, l, {0, 1, 2}, T, {m.d_pf_qkv, m.d_pf_qkv + qd, m.d_pf_qkv + qd + kvd},
@@ -1271,10 +1287,14 @@ int prefill_batched(qora_hip_ctx* c, size_t n, float* logits, uint32_t* argmax) 
             sr.xl = m.d_pf_xl;
             sr.xe = m.d_pf_xe;
             HIP_TRY(c, launch_pf_rows(PF_ROW_SPLIT, sr, T, s));
-            if (int rc = m.pf2 ? pf_gemm2(c, l, {3}, T, {m.d_pf_x}, m.hidden, true)
+            PfDeferred od;     // the o GEMM's partials, summed by the second norm
+            if (int rc = m.pf2 ? pf_gemm2(c, l, {3}, T, {m.d_pf_x}, m.hidden, true, &od)
                                : pf_gemm(c, l, 3, T, m.d_pf_x, m.hidden, true))
                 return rc;
             nr.gamma = m.d_norms + ((size_t)l * 2 + 1) * m.hidden;
+            nr.part = od.part;
+            nr.splits = od.splits;
+            nr.part_stride = od.stride;
             HIP_TRY(c, launch_pf_rows(PF_ROW_RMSNORM, nr, T, s));
             if (m.pf2) {
                 if (int rc = pf_gemm2(c, l, {4, 5}, T, {m.d_pf_gu, m.d_pf_gu + m.inter}, 2 * m.inter, false))
@@ -1292,7 +1312,10 @@ int prefill_batched(qora_hip_ctx* c, size_t n, float* logits, uint32_t* argmax) 
             gr.xl = m.d_pf_xl;
             gr.xe = m.d_pf_xe;
             HIP_TRY(c, launch_pf_rows(PF_ROW_SILU, gr, T, s));
-            if (int rc = m.pf2 ? pf_gemm2(c, l, {6}, T, {m.d_pf_x}, m.hidden, true)
+            // the last layer's down GEMM is reduced in place: the final norm
+            // reads the residual rows
+            pend = PfDeferred{};
+            if (int rc = m.pf2 ? pf_gemm2(c, l, {6}, T, {m.d_pf_x}, m.hidden, true, l + 1 < m.L ? &pend : nullptr)
                                : pf_gemm(c, l, 6, T, m.d_pf_x, m.hidden, true))
                 return rc;
         }

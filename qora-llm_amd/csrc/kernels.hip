@@ -660,7 +660,7 @@ PfGemm2Shape pf_gemm2_shape(uint32_t T, uint32_t k, uint32_t ntot, int cus) {
     return sh;
 }
 
-hipError_t launch_pf_gemm2(uint32_t bm, const PfGemm2Params& p, hipStream_t stream) {
+hipError_t launch_pf_gemm2(uint32_t bm, const PfGemm2Params& p, hipStream_t stream, bool reduce) {
     if (p.T == 0 || p.k % 32 != 0 || p.nseg < 1 || p.nseg > 3 || p.ntot % 128 != 0 || p.splits == 0 ||
         p.kper % 32 != 0 || (uint64_t)p.splits * p.kper < p.k || (p.splits > 1 && !p.part))
         return hipErrorInvalidValue;
@@ -674,7 +674,7 @@ hipError_t launch_pf_gemm2(uint32_t bm, const PfGemm2Params& p, hipStream_t stre
     if (bm == 128) hipLaunchKernelGGL((pf_gemm2_kernel<128>), grid, dim3(256), 0, stream, p);
     else if (bm == 64) hipLaunchKernelGGL((pf_gemm2_kernel<64>), grid, dim3(256), 0, stream, p);
     else return hipErrorInvalidValue;
-    if (p.splits > 1) {
+    if (p.splits > 1 && reduce) {
         const uint64_t total = (uint64_t)p.T * p.ntot;
         const uint32_t blocks = (uint32_t)std::min<uint64_t>(4096, (total + 255) / 256);
         hipLaunchKernelGGL(pf_splitk_reduce2_kernel, dim3(blocks), dim3(256), 0, stream, p);

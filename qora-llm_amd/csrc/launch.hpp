@@ -120,8 +120,9 @@ struct PfGemm2Shape {
     uint32_t bm, splits, kper;
 };
 PfGemm2Shape pf_gemm2_shape(uint32_t T, uint32_t k, uint32_t ntot, int cus);
-// p.splits, p.kper from pf_gemm2_shape (bm too); p.part holds splits * T * ntot floats when splits > 1
-hipError_t launch_pf_gemm2(uint32_t bm, const PfGemm2Params& p, hipStream_t stream);
+// p.splits, p.kper from pf_gemm2_shape (bm too); p.part holds splits * T * ntot floats when splits > 1.
+// reduce = false leaves the split partials for the consumer to sum (pf_rmsnorm_split_reg_kernel).
+hipError_t launch_pf_gemm2(uint32_t bm, const PfGemm2Params& p, hipStream_t stream, bool reduce = true);
 hipError_t launch_pf_rope_cache(const PrefillAttnParams& p, hipStream_t stream);
 hipError_t launch_pf_attn(const PrefillAttnParams& p, hipStream_t stream);
 

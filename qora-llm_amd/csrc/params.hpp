@@ -129,6 +129,12 @@ struct PrefillRowParams {
     uint16_t* xh;
     uint16_t* xl;
     int32_t* xe;
+    // pf_rmsnorm_split_reg_kernel: optional split-K partials of the GEMM that
+    // produced x's increment, part[z][T][n] (z < splits, z-stride part_stride):
+    // x += sum over z in split order (stored back), then the norm
+    const float* part;
+    uint32_t splits;
+    uint64_t part_stride;
 };
 
 struct PrefillGemmParams {

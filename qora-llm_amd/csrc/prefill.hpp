@@ -91,7 +91,17 @@ __global__ __launch_bounds__(256) void pf_embed_kernel(PrefillRowParams p) {
 __global__ __launch_bounds__(256) void pf_rmsnorm_split_kernel(PrefillRowParams p) {
     __shared__ float red[4];
     const uint32_t t = blockIdx.x;
-    const float* x = p.x + (uint64_t)t * p.n;
+    float* x = p.x + (uint64_t)t * p.n;
+    if (p.part) {
+        // split-K partials of the preceding residual add, summed in split order
+        const float* pr = p.part + (uint64_t)t * p.n;
+        for (uint32_t j = threadIdx.x; j < p.n; j += 256) {
+            float a = pr[j];
+            for (uint32_t z = 1; z < p.splits; ++z) a += pr[(uint64_t)z * p.part_stride + j];
+            x[j] += a;
+        }
+        __syncthreads();
+    }
     float ss = 0.f;
     for (uint32_t j = threadIdx.x; j < p.n; j += 256) ss = fmaf(x[j], x[j], ss);
     ss = block_sum<256>(ss, red);
@@ -148,7 +158,7 @@ template <int EPT>
 __global__ __launch_bounds__(256) void pf_rmsnorm_split_reg_kernel(PrefillRowParams p) {
     __shared__ float red[4];
     const uint32_t t = blockIdx.x;
-    const float* x = p.x + (uint64_t)t * p.n;
+    float* x = p.x + (uint64_t)t * p.n;
     float v[EPT];
     float gm[EPT];
     float ss = 0.f;
@@ -157,8 +167,42 @@ __global__ __launch_bounds__(256) void pf_rmsnorm_split_reg_kernel(PrefillRowPar
         const uint32_t j = threadIdx.x + 256u * (uint32_t)i;
         v[i] = j < p.n ? x[j] : 0.f;
         gm[i] = j < p.n ? h2f(p.gamma[j]) : 0.f;
-        ss = fmaf(v[i], v[i], ss);
     }
+    if (p.part) {
+        // the residual add of the split-K GEMM before this norm, in the
+        // order pf_splitk_reduce2_kernel sums: x += ((p0 + p1) + p2) + ...
+        // Partials are loaded four splits at a time, all of a group's loads
+        // issued before its adds (indexes clamped to the last split; the
+        // extra values are not added).
+        const float* pr = p.part + (uint64_t)t * p.n;
+        float a[EPT];
+        for (uint32_t z = 0; z < p.splits; z += 4) {
+            float q[4][EPT];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const uint64_t zo = (uint64_t)min(z + (uint32_t)u, p.splits - 1u) * p.part_stride;
+#pragma unroll
+                for (int i = 0; i < EPT; ++i) {
+                    const uint32_t j = min(threadIdx.x + 256u * (uint32_t)i, p.n - 1u);
+                    q[u][i] = pr[zo + j];
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+#pragma unroll
+                for (int i = 0; i < EPT; ++i)
+                    if (z + (uint32_t)u < p.splits) a[i] = (z == 0 && u == 0) ? q[0][i] : a[i] + q[u][i];
+        }
+#pragma unroll
+        for (int i = 0; i < EPT; ++i) {
+            const uint32_t j = threadIdx.x + 256u * (uint32_t)i;
+            if (j >= p.n) continue;
+            v[i] += a[i];
+            x[j] = v[i];
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < EPT; ++i) ss = fmaf(v[i], v[i], ss);
     ss = block_sum<256>(ss, red);
     const float inv = 1.0f / sqrtf(ss / (float)p.n + 1e-6f);
     float amax = 0.f;
