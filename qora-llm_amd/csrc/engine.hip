@@ -1174,8 +1174,9 @@ struct PfDeferred {
     uint64_t stride = 0;
 };
 
-// defer: when set and the launch splits K over one accumulating segment whose
-// rows are ldy == ntot wide, the partials are left for the caller
+// defer: when set and the launch splits K, with the segments' rows side by
+// side in one output (row stride ldy == ntot), the partials are left for the
+// caller, who sums them in split order (and adds them when accumulating)
 int pf_gemm2(qora_hip_ctx* c, uint32_t l, std::initializer_list<int> js, uint32_t T, std::initializer_list<float*> ys,
              uint32_t ldy, bool accumulate, PfDeferred* defer = nullptr) {
     ModelState& m = c->m;
@@ -1205,7 +1206,9 @@ int pf_gemm2(qora_hip_ctx* c, uint32_t l, std::initializer_list<int> js, uint32_
     g.splits = sh.splits;
     g.kper = sh.kper;
     g.part = m.d_pf_part;
-    const bool leave = defer && g.splits > 1 && g.nseg == 1 && accumulate && ldy == g.ntot;
+    bool side = ldy == g.ntot;
+    for (int i = 0; i < g.nseg; ++i) side = side && g.seg[i].y == g.seg[0].y + (size_t)g.seg[i].nb0 * 128u;
+    const bool leave = defer && g.splits > 1 && side;
     HIP_TRY(c, launch_pf_gemm2(sh.bm, g, c->stream, !leave));
     if (defer) *defer = leave ? PfDeferred{g.part, g.splits, (uint64_t)T * g.ntot} : PfDeferred{};
     return QORA_HIP_OK;
@@ -1248,9 +1251,10 @@ int prefill_batched(qora_hip_ctx* c, size_t n, float* logits, uint32_t* argmax) 
             nr.splits = pend.splits;
             nr.part_stride = pend.stride;
             HIP_TRY(c, launch_pf_rows(PF_ROW_RMSNORM, nr, T, s));
+            PfDeferred qd_def;   // the q|k|v GEMM's partials, summed by the RoPE / cache kernel
             if (m.pf2) {
                 if (int rc = pf_gemm2(c, l, {0, 1, 2}, T, {m.d_pf_qkv, m.d_pf_qkv + qd, m.d_pf_qkv + qd + kvd},
-                                      qkvn, false))
+                                      qkvn, false, qkvn <= kPfRopeRowMax ? &qd_def : nullptr))
                     return rc;
             } else {
                 if (int rc = pf_gemm(c, l, 0, T, m.d_pf_qkv, qkvn, false)) return rc;
@@ -1278,7 +1282,11 @@ int prefill_batched(qora_hip_ctx* c, size_t n, float* logits, uint32_t* argmax) 
             a.kv_hs = (uint64_t)m.cap * m.hd;
             a.part = m.d_pf_apart;
             a.part_nc = kPfAttnChunks;
+            a.qkv_part = qd_def.part;
+            a.qkv_splits = qd_def.splits;
+            a.qkv_part_stride = qd_def.stride;
             HIP_TRY(c, launch_pf_rope_cache(a, s));
+            a.qkv_part = nullptr;
             HIP_TRY(c, launch_pf_attn(a, s));
             PrefillRowParams sr{};
             sr.x = m.d_pf_ao;

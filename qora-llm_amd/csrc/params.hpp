@@ -209,7 +209,14 @@ struct PrefillAttnParams {
     float* part;
     uint32_t part_nc;
     uint32_t nc, ch;
+    // pf_rope_cache_kernel: optional split-K partials of the q|k|v GEMM,
+    // qkv_part[z][T][qd + 2 kvd] (z-stride qkv_part_stride), summed in split
+    // order in place of the qkv rows (rows of at most kPfRopeRowMax floats)
+    const float* qkv_part;
+    uint32_t qkv_splits;
+    uint64_t qkv_part_stride;
 };
+constexpr uint32_t kPfRopeRowMax = 8192;
 
 // On-device sampling (sample.hpp).
 struct SamplePenalty {

@@ -786,11 +786,24 @@ __global__ __launch_bounds__(256) void pf_splitk_reduce_kernel(PrefillGemmParams
 // ---------------------------------------------------------------------------
 template <bool F16KV>
 __global__ __launch_bounds__(256) void pf_rope_cache_kernel(PrefillAttnParams p) {
+    __shared__ float rs[kPfRopeRowMax];
     const uint32_t t = blockIdx.x;
     const uint32_t pos = p.pos0 + t;
     const uint32_t hd = p.hd, half = p.half;
-    const uint32_t qd = p.H * hd, kvd = p.KVH * hd;
-    const float* row = p.qkv + (uint64_t)t * (qd + 2 * kvd);
+    const uint32_t qd = p.H * hd, kvd = p.KVH * hd, qkvn = qd + 2 * kvd;
+    const float* row = p.qkv + (uint64_t)t * qkvn;
+    if (p.qkv_part) {
+        // the q|k|v row from the GEMM's split-K partials, summed in split order
+        // (as pf_splitk_reduce2_kernel would store it)
+        const float* pr = p.qkv_part + (uint64_t)t * qkvn;
+        for (uint32_t i = threadIdx.x; i < qkvn; i += 256) {
+            float a = pr[i];
+            for (uint32_t z = 1; z < p.qkv_splits; ++z) a += pr[(uint64_t)z * p.qkv_part_stride + i];
+            rs[i] = a;
+        }
+        __syncthreads();
+        row = rs;
+    }
     const float* ct = p.rope_cos + (uint64_t)pos * half;
     const float* st = p.rope_sin + (uint64_t)pos * half;
     const bool rot = p.use_rope != 0;
