@@ -1287,14 +1287,11 @@ int prefill_batched(qora_hip_ctx* c, size_t n, float* logits, uint32_t* argmax) 
             a.qkv_part_stride = qd_def.stride;
             HIP_TRY(c, launch_pf_rope_cache(a, s));
             a.qkv_part = nullptr;
+            // the attention output comes back split for the o GEMM
+            a.xh = m.d_pf_xh;
+            a.xl = m.d_pf_xl;
+            a.xe = m.d_pf_xe;
             HIP_TRY(c, launch_pf_attn(a, s));
-            PrefillRowParams sr{};
-            sr.x = m.d_pf_ao;
-            sr.n = qd;
-            sr.xh = m.d_pf_xh;
-            sr.xl = m.d_pf_xl;
-            sr.xe = m.d_pf_xe;
-            HIP_TRY(c, launch_pf_rows(PF_ROW_SPLIT, sr, T, s));
             PfDeferred od;     // the o GEMM's partials, summed by the second norm
             if (int rc = m.pf2 ? pf_gemm2(c, l, {3}, T, {m.d_pf_x}, m.hidden, true, &od)
                                : pf_gemm(c, l, 3, T, m.d_pf_x, m.hidden, true))

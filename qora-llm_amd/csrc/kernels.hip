@@ -689,6 +689,17 @@ hipError_t launch_pf_rope_cache(const PrefillAttnParams& p, hipStream_t stream) 
     return hipGetLastError();
 }
 
+// The attention output rows (p.out) split into the o GEMM's operand.
+static hipError_t launch_pf_attn_split(const PrefillAttnParams& p, hipStream_t stream) {
+    PrefillRowParams r{};
+    r.x = p.out;
+    r.n = p.H * p.hd;
+    r.xh = p.xh;
+    r.xl = p.xl;
+    r.xe = p.xe;
+    return launch_pf_rows(PF_ROW_SPLIT, r, p.T, stream);
+}
+
 hipError_t launch_pf_attn(const PrefillAttnParams& p, hipStream_t stream) {
     if (p.T == 0) return hipSuccess;
     if (p.hd > (uint32_t)kAttnMaxHd || p.hd % 8 != 0 || p.H % p.KVH != 0) return hipErrorInvalidValue;
@@ -716,22 +727,28 @@ hipError_t launch_pf_attn(const PrefillAttnParams& p, hipStream_t stream) {
             }
         }
         const dim3 grid((p.T + qt - 1) / qt * q.nc, p.KVH);
+        // with split outputs and chunks, the merge writes the o GEMM's operand itself
+        const bool merge_split = p.xh && q.nc > 1 && p.H * p.hd <= 2048u;
 #define QORA_PF_ATTN(HD)                                                                                     \
     do {                                                                                                    \
         if (p.kv_f16) hipLaunchKernelGGL((pf_attn_mfma_kernel<HD, true>), grid, dim3(256), 0, stream, q);   \
         else hipLaunchKernelGGL((pf_attn_mfma_kernel<HD, false>), grid, dim3(256), 0, stream, q);           \
-        if (q.nc > 1)                                                                                       \
+        if (merge_split)                                                                                    \
+            hipLaunchKernelGGL((pf_attn_merge_split_kernel<HD>), dim3(p.T), dim3(256), 0, stream, q);        \
+        else if (q.nc > 1)                                                                                  \
             hipLaunchKernelGGL((pf_attn_merge_kernel<HD>), dim3(p.T, (p.H * HD + 255) / 256), dim3(256), 0,  \
                                stream, q);                                                                  \
     } while (0)
         if (p.hd == 128) QORA_PF_ATTN(128);
         else QORA_PF_ATTN(64);
 #undef QORA_PF_ATTN
+        if (p.xh && !merge_split) return launch_pf_attn_split(p, stream);
         return hipGetLastError();
     }
     const dim3 grid((p.T + 31) / 32, p.H);
     if (p.kv_f16) hipLaunchKernelGGL((pf_attn_vec_kernel<true>), grid, dim3(256), 0, stream, p);
     else hipLaunchKernelGGL((pf_attn_vec_kernel<false>), grid, dim3(256), 0, stream, p);
+    if (p.xh) return launch_pf_attn_split(p, stream);
     return hipGetLastError();
 }
 

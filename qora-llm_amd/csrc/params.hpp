@@ -215,6 +215,12 @@ struct PrefillAttnParams {
     const float* qkv_part;
     uint32_t qkv_splits;
     uint64_t qkv_part_stride;
+    // optional: the attention output written as the o GEMM's operand (two
+    // binary16 parts and a row exponent, as pf_split_kernel makes them)
+    // instead of the fp32 rows in out
+    uint16_t* xh;
+    uint16_t* xl;
+    int32_t* xe;
 };
 constexpr uint32_t kPfRopeRowMax = 8192;
 

@@ -1198,4 +1198,68 @@ __global__ __launch_bounds__(256) void pf_attn_merge_kernel(PrefillAttnParams p)
     }
 }
 
+// pf_attn_merge_kernel and pf_split_kernel in one pass: block t merges row
+// t's key chunks (thread: 8 consecutive dims of one head; the same per-element
+// arithmetic, in the same chunk order) and splits the row for the o GEMM.
+template <int HD>
+__global__ __launch_bounds__(256) void pf_attn_merge_split_kernel(PrefillAttnParams p) {
+    constexpr uint32_t MC = 8;                      // most chunks (the workspace's bound)
+    constexpr uint32_t DPT = 8;                     // dims per thread
+    __shared__ float red[4];
+    const uint32_t t = blockIdx.x;
+    const uint32_t G = p.H / p.KVH, QT = 16u * (4u / G), nc = p.nc;
+    const uint32_t qb = t / QT, qloc = t % QT, sub = qloc / 16u, row = qloc % 16u;
+    const uint32_t q0 = qb * QT, nq = min(QT, p.T - q0);
+    const uint32_t last = p.pos0 + q0 + nq - 1u;
+    const uint32_t nlive = min(min(nc, MC), last / p.ch + 1u);
+    const uint64_t nblk = (uint64_t)((p.T + QT - 1u) / QT) * nc * p.KVH;
+    const float* po = p.part;
+    const float* pml = p.part + nblk * 64u * HD;
+    const uint32_t qd = p.H * HD;
+    const uint32_t e0 = threadIdx.x * DPT;          // first element of the row (qd <= 256 DPT)
+    const bool on = e0 < qd;
+    const uint32_t h = min(e0, qd - 1u) / HD, d0 = min(e0, qd - 1u) % HD;
+    const uint32_t kvh = h / G, wave = sub * G + h % G;
+    float mv[MC], lv[MC], ov[MC][DPT];
+#pragma unroll
+    for (uint32_t kc = 0; kc < MC; ++kc) {
+        const uint32_t kk = min(kc, nlive - 1u);
+        const uint64_t r = (((uint64_t)qb * nc + kk) * p.KVH + kvh) * 64u + wave * 16u + row;
+        mv[kc] = pml[r * 2u];
+        lv[kc] = pml[r * 2u + 1u];
+        const float4 a = *reinterpret_cast<const float4*>(po + r * HD + d0);
+        const float4 b = *reinterpret_cast<const float4*>(po + r * HD + d0 + 4u);
+        ov[kc][0] = a.x; ov[kc][1] = a.y; ov[kc][2] = a.z; ov[kc][3] = a.w;
+        ov[kc][4] = b.x; ov[kc][5] = b.y; ov[kc][6] = b.z; ov[kc][7] = b.w;
+    }
+    float M = mv[0];
+#pragma unroll
+    for (uint32_t kc = 1; kc < MC; ++kc) M = fmaxf(M, mv[kc]);
+    float num[DPT], den = 0.f;
+#pragma unroll
+    for (uint32_t i = 0; i < DPT; ++i) num[i] = 0.f;
+#pragma unroll
+    for (uint32_t kc = 0; kc < MC; ++kc) {
+        if (kc >= nlive) break;
+        const float w = expf(mv[kc] - M);
+#pragma unroll
+        for (uint32_t i = 0; i < DPT; ++i) num[i] = fmaf(w, ov[kc][i], num[i]);
+        den = fmaf(w, lv[kc], den);
+    }
+    float v[DPT], amax = 0.f;
+#pragma unroll
+    for (uint32_t i = 0; i < DPT; ++i) {
+        v[i] = num[i] / den;
+        amax = on ? fmaxf(amax, fabsf(v[i])) : amax;
+    }
+    const int e = pf_row_exponent(pf_block_max<256>(amax, red));
+    if (on) {
+        _Float16* xh = reinterpret_cast<_Float16*>(p.xh) + (uint64_t)t * qd + e0;
+        _Float16* xl = reinterpret_cast<_Float16*>(p.xl) + (uint64_t)t * qd + e0;
+#pragma unroll
+        for (uint32_t i = 0; i < DPT; ++i) pf_split(v[i], e, xh + i, xl + i);
+    }
+    if (threadIdx.x == 0) p.xe[t] = e;
+}
+
 }  // namespace qora
