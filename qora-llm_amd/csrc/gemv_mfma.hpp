@@ -563,8 +563,9 @@ __global__ __launch_bounds__(256) void gemv_q4m4_kernel(GemvParams p) {
     const uint32_t k0 = split * (uint32_t)KW;
     const uint32_t k1 = min(p.k, k0 + (uint32_t)KW);
 
-    if (p.zero_ptr)
-        for (uint32_t i = blockIdx.x * (NW * kWave) + t; i < p.zero_n; i += gridDim.x * (NW * kWave)) p.zero_ptr[i] = 0;
+    // (the accumulator this launch clears is cleared at the end: on gfx9 a
+    // store counts in vmcnt like a load, so stores issued first would hold
+    // up every wait for the input rows and weights)
 
     // ---- this wave's input rows [wave * RW, wave * RW + RW) of the slice ----
     float xp[RPL], ssp = 0.f;
@@ -638,6 +639,8 @@ __global__ __launch_bounds__(256) void gemv_q4m4_kernel(GemvParams p) {
                                __HIP_MEMORY_SCOPE_AGENT);
     }
     gemv_q4m_item<GW, KW>(out, lane, [](int, uint32_t r) { return xs[r]; }, xm, sw, esg, wq, zl[wave], zero16);
+    if (p.zero_ptr)
+        for (uint32_t i = blockIdx.x * (NW * kWave) + t; i < p.zero_n; i += gridDim.x * (NW * kWave)) p.zero_ptr[i] = 0;
 }
 
 }  // namespace qora
