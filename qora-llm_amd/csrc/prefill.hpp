@@ -943,31 +943,41 @@ __global__ __launch_bounds__(256) void pf_attn_vec_kernel(PrefillAttnParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// Causal prefill attention on the fp32 matrix cores (v_mfma_f32_16x16x4_f32:
-// exact products, fp32 accumulation). Block (query tile, KV head), 4 waves;
-// wave w takes query head kvh * G + w % G for 16 queries (sub-tile w / G), so
-// the G heads sharing a KV head share each K/V tile staged in LDS (64 keys
-// per step). Per wave and key tile: S = Q K^T (16 x 64, Q held in registers),
-// online softmax in registers, P through LDS into the A layout, O += P V
-// (16 x HD). The contraction index of step s in lane group g = l / 16 is
-// d = g HD/4 + s for Q K^T and key = 16 g + s for P V, so each lane reads its
-// operands as contiguous 16-byte runs.
-// Operand layouts of v_mfma_f32_16x16x4_f32 (lane l): A[i = l % 16][k = l / 16],
-// B[k = l / 16][j = l % 16], C[i = 4 (l / 16) + r][j = l % 16] in register r.
+// Causal prefill attention on the matrix cores. Block (query tile, KV head),
+// 4 waves; wave w takes query head kvh * G + w % G for 16 queries (sub-tile
+// w / G), so the G heads sharing a KV head share each K/V tile staged in LDS
+// (64 keys per step). Per wave and key tile:
+//   * S^T = K Q^T on the fp32 matrix cores (v_mfma_f32_16x16x4_f32: exact
+//     products, fp32 accumulation), K from LDS as the A operand and Q held
+//     in registers as B. The contraction index of step s in lane group
+//     g = l / 16 is d = g HD/4 + s, so each lane reads contiguous 16-byte runs.
+//     Lane (g, i) then holds the scores of query i for keys 16 c + 4 g + r
+//     (c, r < 4): the online softmax of a query runs in its own four lanes
+//     and its probabilities never leave them;
+//   * O^T += V^T P^T on the f16 matrix cores (v_mfma_f32_16x16x32_f16), both
+//     operands split into two binary16 parts, three products (vh ph + vl ph +
+//     vh pl) accumulated in fp32. The contraction runs over the 32 keys of a
+//     half tile in the order lane group g holds them: position 8 g + b is key
+//     16 (b / 4) + 4 g + b % 4, so P^T comes straight from the lane's
+//     probabilities and V is staged as VT[s][g][d][8] binary16 (the 8 keys a
+//     lane needs for dim d, contiguous).
+// Precision: products of the f16 parts are exact; p and v are held to 22
+// bits above 2^-14 (below, to an absolute 2^-25: p <= 1, and a value that
+// small moves the sum by less than fp32 rounding of the larger terms).
+// Operand layouts (lane l): 16x16x4 f32: A[i = l % 16][k = l / 16],
+// B[k = l / 16][j = l % 16]; 16x16x32 f16: A[i = l % 16][k = 8 (l / 16) + b],
+// B[k = 8 (l / 16) + b][j = l % 16]; C[i = 4 (l / 16) + r][j = l % 16] in
+// register r for both.
 // ---------------------------------------------------------------------------
 template <int HD, bool F16KV>
-__global__ __launch_bounds__(256) void pf_attn_mfma_kernel(PrefillAttnParams p) {
+__global__ __launch_bounds__(256, 2) void pf_attn_mfma_kernel(PrefillAttnParams p) {
     constexpr int KT = 64;                          // keys per step
     constexpr int KS = HD + 4;                      // K row stride (floats)
-    constexpr int VS = HD + 1;                      // V row stride
-    constexpr int PS = KT + 4;                      // P row stride
-    constexpr int QS = HD / 4;                      // contraction steps of Q K^T
+    constexpr int QS = HD / 4;                      // contraction steps of K Q^T
     constexpr int OC = HD / 16;                     // 16-dim output tiles
     __shared__ __align__(16) float ks[KT * KS];
-    __shared__ __align__(16) float vs[KT * VS];
-    // P (4 waves x 16 rows x PS) reuses the K tile's space once every wave has
-    // its scores: 67 KB of LDS, two blocks per CU
-    static_assert(4 * 16 * PS <= KT * KS, "P fits in the K tile");
+    // V of the tile: vt[part][half s][lane group g][dim d][8 keys], binary16
+    __shared__ __align__(16) _Float16 vt[2][2 * 4 * HD * 8];
 
     const uint32_t t = threadIdx.x;
     const uint32_t lane = t % kWave, g4 = lane / 16u, li = lane % 16u;
@@ -989,7 +999,7 @@ __global__ __launch_bounds__(256) void pf_attn_mfma_kernel(PrefillAttnParams p) 
     const uint32_t kend = nc > 1u ? min(kbeg + p.ch, last + 1u) : last + 1u;
     if (kbeg > last) return;                        // a chunk past every key of the block
 
-    // Q fragment: lane holds q[wq0 + li][g4 * QS + s]
+    // Q fragment (B operand): lane holds q[wq0 + li][g4 * QS + s]
     float qf[QS];
     {
         const uint32_t qi = min(wq0 + li, p.T - 1u);
@@ -1003,46 +1013,86 @@ __global__ __launch_bounds__(256) void pf_attn_mfma_kernel(PrefillAttnParams p) 
             qf[4 * s4 + 3] = v.w;
         }
     }
-    float m[4], l[4];
+    const uint32_t qpos = p.pos0 + wq0 + li;        // this lane's query position
+    float m = -INFINITY, l = 0.f;
     f32x4v o[OC];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) { m[r] = -INFINITY; l[r] = 0.f; }
-#pragma unroll
     for (int c = 0; c < OC; ++c) o[c] = f32x4v{0.f, 0.f, 0.f, 0.f};
-    float* pw = ks + wave * 16u * PS;
 
-    for (uint32_t k0 = kbeg; k0 < kend; k0 += KT) {
-        __syncthreads();                            // the previous tiles are consumed
-        // stage K and V rows k0 .. k0 + 63 (clamped to `last`; masked below)
-        for (uint32_t e = t; e < (uint32_t)(KT * HD / 4); e += 256) {
+    // A tile's K and V are loaded into registers one tile ahead (thread e of
+    // the K load: key e / (HD/4), dims 4 (e % (HD/4)) ..; of the V load: dim
+    // e % HD, keys 4 (e / HD) .. + 3), then staged in LDS.
+    constexpr int KE = KT * HD / 4 / 256;           // K float4s per thread
+    constexpr int VE = HD * KT / 4 / 256;           // V key quads per thread
+    float4 kreg[KE];
+    float vreg[VE][4];
+    auto load_tile = [&](uint32_t k0) {
+#pragma unroll
+        for (int u = 0; u < KE; ++u) {
+            const uint32_t e = t + 256u * (uint32_t)u;
             const uint32_t r = e / (HD / 4), c4 = e % (HD / 4);
             const uint64_t idx = (uint64_t)min(k0 + r, last) * cps + (uint64_t)kvh * chs + 4u * c4;
-            float4 kv, vv;
             if constexpr (F16KV) {
                 const uint2 a = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(p.kc) + idx);
-                const uint2 b = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(p.vc) + idx);
-                kv = make_float4(h2f((uint16_t)(a.x & 0xFFFFu)), h2f((uint16_t)(a.x >> 16)),
-                                 h2f((uint16_t)(a.y & 0xFFFFu)), h2f((uint16_t)(a.y >> 16)));
-                vv = make_float4(h2f((uint16_t)(b.x & 0xFFFFu)), h2f((uint16_t)(b.x >> 16)),
-                                 h2f((uint16_t)(b.y & 0xFFFFu)), h2f((uint16_t)(b.y >> 16)));
+                kreg[u] = make_float4(__uint_as_float(a.x), __uint_as_float(a.y), 0.f, 0.f);   // raw words
             } else {
-                kv = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(p.kc) + idx);
-                vv = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(p.vc) + idx);
+                kreg[u] = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(p.kc) + idx);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < VE; ++u) {
+            const uint32_t e = t + 256u * (uint32_t)u;
+            const uint32_t d = e % HD, quad = e / HD;
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+                const uint64_t idx = (uint64_t)min(k0 + 4u * quad + (uint32_t)rr, last) * cps + (uint64_t)kvh * chs + d;
+                if constexpr (F16KV) vreg[u][rr] = __uint_as_float((uint32_t)reinterpret_cast<const uint16_t*>(p.vc)[idx]);
+                else vreg[u][rr] = reinterpret_cast<const float*>(p.vc)[idx];
+            }
+        }
+    };
+    auto store_tile = [&]() {
+#pragma unroll
+        for (int u = 0; u < KE; ++u) {
+            const uint32_t e = t + 256u * (uint32_t)u;
+            const uint32_t r = e / (HD / 4), c4 = e % (HD / 4);
+            float4 kv = kreg[u];
+            if constexpr (F16KV) {
+                const uint32_t ax = __float_as_uint(kv.x), ay = __float_as_uint(kv.y);
+                kv = make_float4(h2f((uint16_t)(ax & 0xFFFFu)), h2f((uint16_t)(ax >> 16)),
+                                 h2f((uint16_t)(ay & 0xFFFFu)), h2f((uint16_t)(ay >> 16)));
             }
             *reinterpret_cast<float4*>(&ks[r * KS + 4 * c4]) = kv;
-            float* vr = &vs[r * VS + 4 * c4];
-            vr[0] = vv.x;
-            vr[1] = vv.y;
-            vr[2] = vv.z;
-            vr[3] = vv.w;
         }
+        typedef _Float16 half4v __attribute__((ext_vector_type(4)));
+#pragma unroll
+        for (int u = 0; u < VE; ++u) {
+            const uint32_t e = t + 256u * (uint32_t)u;
+            const uint32_t d = e % HD, quad = e / HD;   // keys 4 quad .. 4 quad + 3
+            const uint32_t hs = quad / 8u, cq = (quad % 8u) / 4u, gq = quad % 4u;
+            _Float16 vh[4], vl[4];
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+                const float v = F16KV ? h2f((uint16_t)__float_as_uint(vreg[u][rr])) : vreg[u][rr];
+                vh[rr] = (_Float16)v;
+                vl[rr] = (_Float16)(v - (float)vh[rr]);
+            }
+            const uint32_t o8 = ((hs * 4u + gq) * (uint32_t)HD + d) * 8u + cq * 4u;
+            *reinterpret_cast<half4v*>(&vt[0][o8]) = half4v{vh[0], vh[1], vh[2], vh[3]};
+            *reinterpret_cast<half4v*>(&vt[1][o8]) = half4v{vl[0], vl[1], vl[2], vl[3]};
+        }
+    };
+
+    load_tile(kbeg);
+    for (uint32_t k0 = kbeg; k0 < kend; k0 += KT) {
+        __syncthreads();                            // the previous tiles are consumed
+        store_tile();
         __syncthreads();
+        // the next tile's loads (clamped: past the last key they re-read it)
+        load_tile(k0 + KT < kend ? k0 + KT : k0);
         // a wave with no visible key in the tile skips the work, not the barriers
-        const bool active = wave_on && k0 <= p.pos0 + wq0 + 15u;
-        float f[4] = {1.f, 1.f, 1.f, 1.f};
-        float ev[4][4] = {};
-        if (active) {
-        // ---- S = Q K^T: four 16 x 16 tiles ----
+        if (!(wave_on && k0 <= p.pos0 + wq0 + 15u)) continue;
+        // ---- S^T = K Q^T: four 16-key x 16-query tiles ----
         f32x4v sacc[4];
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
@@ -1051,104 +1101,87 @@ __global__ __launch_bounds__(256) void pf_attn_mfma_kernel(PrefillAttnParams p) 
 #pragma unroll
             for (int s4 = 0; s4 < QS / 4; ++s4) {
                 const float4 kb = *reinterpret_cast<const float4*>(krow + 4 * s4);
-                sacc[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(qf[4 * s4], kb.x, sacc[c], 0, 0, 0);
-                sacc[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(qf[4 * s4 + 1], kb.y, sacc[c], 0, 0, 0);
-                sacc[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(qf[4 * s4 + 2], kb.z, sacc[c], 0, 0, 0);
-                sacc[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(qf[4 * s4 + 3], kb.w, sacc[c], 0, 0, 0);
+                sacc[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(kb.x, qf[4 * s4], sacc[c], 0, 0, 0);
+                sacc[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(kb.y, qf[4 * s4 + 1], sacc[c], 0, 0, 0);
+                sacc[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(kb.z, qf[4 * s4 + 2], sacc[c], 0, 0, 0);
+                sacc[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(kb.w, qf[4 * s4 + 3], sacc[c], 0, 0, 0);
             }
         }
-        // ---- online softmax: lane holds rows 4 g4 + r, keys 16 c + li ----
+        // ---- online softmax of query li over keys 16 c + 4 g4 + r ----
+        float sv[4][4];
+        float mx = -INFINITY;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const uint32_t qpos = p.pos0 + wq0 + 4u * g4 + (uint32_t)r;
-            float sv[4];
-            float mx = -INFINITY;
+        for (int c = 0; c < 4; ++c)
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const uint32_t kp = k0 + 16u * c + li;
-                sv[c] = kp <= qpos ? sacc[c][r] * p.scale : -INFINITY;
-                mx = fmaxf(mx, sv[c]);
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t kp = k0 + 16u * c + 4u * g4 + (uint32_t)r;
+                sv[c][r] = kp <= qpos ? sacc[c][r] * p.scale : -INFINITY;
+                mx = fmaxf(mx, sv[c][r]);
             }
-            mx = fmaxf(mx, __shfl_xor(mx, 1, kWave));
-            mx = fmaxf(mx, __shfl_xor(mx, 2, kWave));
-            mx = fmaxf(mx, __shfl_xor(mx, 4, kWave));
-            mx = fmaxf(mx, __shfl_xor(mx, 8, kWave));
-            const float m_new = fmaxf(m[r], mx);
-            const float mref = m_new == -INFINITY ? 0.f : m_new;   // a row with no visible key yet
-            f[r] = expf(m[r] - mref);
-            float sum = 0.f;
+        mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+        const float m_new = fmaxf(m, mx);
+        const float mref = m_new == -INFINITY ? 0.f : m_new;   // a query with no visible key yet
+        const float f = expf(m - mref);
+        float sum = 0.f;
+        half8v ph[2], pl[2];
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const float e = expf(sv[c] - mref);
-                ev[r][c] = e;
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float e = expf(sv[c][r] - mref);
                 sum += e;
+                const _Float16 eh = (_Float16)e;
+                ph[c / 2][(c % 2) * 4 + r] = eh;
+                pl[c / 2][(c % 2) * 4 + r] = (_Float16)(e - (float)eh);
             }
-            sum += __shfl_xor(sum, 1, kWave);
-            sum += __shfl_xor(sum, 2, kWave);
-            sum += __shfl_xor(sum, 4, kWave);
-            sum += __shfl_xor(sum, 8, kWave);
-            l[r] = l[r] * f[r] + sum;
-            m[r] = m_new;
-        }
-        }
-        __syncthreads();                            // every wave is done reading the K tile
-        if (!active) continue;
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-#pragma unroll
-            for (int c = 0; c < 4; ++c) pw[(4u * g4 + (uint32_t)r) * PS + 16u * c + li] = ev[r][c];
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        sum += __shfl_xor(sum, 16, kWave);
+        sum += __shfl_xor(sum, 32, kWave);
+        l = l * f + sum;
+        m = m_new;
+        // ---- O^T = O^T f + V^T P^T: dim tiles of 16, two half tiles of 32 keys ----
 #pragma unroll
         for (int c = 0; c < OC; ++c)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) o[c][r] *= f[r];
-        // ---- O += P V: A = P[li][16 g4 + s], B = V[16 g4 + s][16 c + li] ----
-        const float* prow = &pw[li * PS + 16u * g4];
+            for (int r = 0; r < 4; ++r) o[c][r] *= f;
 #pragma unroll
-        for (int s4 = 0; s4 < 4; ++s4) {
-            const float4 pa = *reinterpret_cast<const float4*>(prow + 4 * s4);
-            const float pav[4] = {pa.x, pa.y, pa.z, pa.w};
+        for (int hs = 0; hs < 2; ++hs) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const float* vrow = &vs[(16u * g4 + 4u * s4 + (uint32_t)j) * VS + li];
-#pragma unroll
-                for (int c = 0; c < OC; ++c)
-                    o[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(pav[j], vrow[16 * c], o[c], 0, 0, 0);
+            for (int c = 0; c < OC; ++c) {
+                const uint32_t o8 = (((uint32_t)hs * 4u + g4) * (uint32_t)HD + 16u * c + li) * 8u;
+                const half8v ah = *reinterpret_cast<const half8v*>(&vt[0][o8]);
+                const half8v al = *reinterpret_cast<const half8v*>(&vt[1][o8]);
+                o[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, ph[hs], o[c], 0, 0, 0);
+                o[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, ph[hs], o[c], 0, 0, 0);
+                o[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, pl[hs], o[c], 0, 0, 0);
             }
         }
     }
     if (!wave_on) return;
+    // lane (g4, li): O^T[dims 16 c + 4 g4 + r][query li]
+    const uint32_t row = li;                        // query within the wave's 16
+    if (wq0 + row >= q0 + nq) return;
     if (nc > 1u) {
         // partial state of the chunk: unnormalised o, running max m and sum l
-        // per row, merged by pf_attn_merge_kernel
+        // per row, merged by pf_attn_merge_kernel / pf_attn_merge_split_kernel
         const uint64_t blk = (uint64_t)blockIdx.x * p.KVH + kvh;
         float* po = p.part + (blk * 64u + wave * 16u) * HD;
         float* pml = p.part + (uint64_t)gridDim.x * p.KVH * 64u * HD + (blk * 64u + wave * 16u) * 2u;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const uint32_t row = 4u * g4 + (uint32_t)r;
-            if (wq0 + row >= q0 + nq) continue;
-#pragma unroll
-            for (int c = 0; c < OC; ++c) po[row * HD + 16 * c + li] = o[c][r];
-            if (li == 0) {
-                pml[row * 2u] = m[r];
-                pml[row * 2u + 1u] = l[r];
-            }
+        for (int c = 0; c < OC; ++c)
+            *reinterpret_cast<float4*>(&po[row * HD + 16 * c + 4 * g4]) = make_float4(o[c][0], o[c][1], o[c][2], o[c][3]);
+        if (g4 == 0) {
+            pml[row * 2u] = m;
+            pml[row * 2u + 1u] = l;
         }
         return;
     }
-    if (!wave_on) return;
+    const float inv = 1.0f / l;
+    float* out = p.out + (uint64_t)(wq0 + row) * qd + (uint64_t)h * HD;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const uint32_t qi = wq0 + 4u * g4 + (uint32_t)r;
-        if (qi >= q0 + nq) continue;
-        const float inv = 1.0f / l[r];
-        float* out = p.out + (uint64_t)qi * qd + (uint64_t)h * HD + li;
-#pragma unroll
-        for (int c = 0; c < OC; ++c) out[16 * c] = o[c][r] * inv;
-    }
+    for (int c = 0; c < OC; ++c)
+        *reinterpret_cast<float4*>(&out[16 * c + 4 * g4]) =
+            make_float4(o[c][0] * inv, o[c][1] * inv, o[c][2] * inv, o[c][3] * inv);
 }
 
 // Merge of the key chunks of pf_attn_mfma_kernel (nc > 1): blocks of 256
