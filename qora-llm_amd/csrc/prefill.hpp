@@ -947,13 +947,13 @@ __global__ __launch_bounds__(256) void pf_attn_vec_kernel(PrefillAttnParams p) {
 // 4 waves; wave w takes query head kvh * G + w % G for 16 queries (sub-tile
 // w / G), so the G heads sharing a KV head share each K/V tile staged in LDS
 // (64 keys per step). Per wave and key tile:
-//   * S^T = K Q^T on the fp32 matrix cores (v_mfma_f32_16x16x4_f32: exact
-//     products, fp32 accumulation), K from LDS as the A operand and Q held
-//     in registers as B. The contraction index of step s in lane group
-//     g = l / 16 is d = g HD/4 + s, so each lane reads contiguous 16-byte runs.
-//     Lane (g, i) then holds the scores of query i for keys 16 c + 4 g + r
-//     (c, r < 4): the online softmax of a query runs in its own four lanes
-//     and its probabilities never leave them;
+//   * S^T = K Q^T on the f16 matrix cores (v_mfma_f32_16x16x32_f16), K from
+//     LDS as the A operand and Q held in registers as B, each split into two
+//     binary16 parts on a power-of-two scale (per key row, per query: as the
+//     prefill GEMM splits its operands; 22-bit products, fp32 accumulation),
+//     the dot then scaled back exactly. Lane (g, i) holds the scores of
+//     query i for keys 16 c + 4 g + r (c, r < 4): the online softmax of a
+//     query runs in its own four lanes and its probabilities never leave them;
 //   * O^T += V^T P^T on the f16 matrix cores (v_mfma_f32_16x16x32_f16), both
 //     operands split into two binary16 parts, three products (vh ph + vl ph +
 //     vh pl) accumulated in fp32. The contraction runs over the 32 keys of a
@@ -964,18 +964,19 @@ __global__ __launch_bounds__(256) void pf_attn_vec_kernel(PrefillAttnParams p) {
 // Precision: products of the f16 parts are exact; p and v are held to 22
 // bits above 2^-14 (below, to an absolute 2^-25: p <= 1, and a value that
 // small moves the sum by less than fp32 rounding of the larger terms).
-// Operand layouts (lane l): 16x16x4 f32: A[i = l % 16][k = l / 16],
-// B[k = l / 16][j = l % 16]; 16x16x32 f16: A[i = l % 16][k = 8 (l / 16) + b],
-// B[k = 8 (l / 16) + b][j = l % 16]; C[i = 4 (l / 16) + r][j = l % 16] in
-// register r for both.
+// Operand layouts of v_mfma_f32_16x16x32_f16 (lane l): A[i = l % 16][k =
+// 8 (l / 16) + b], B[k = 8 (l / 16) + b][j = l % 16], C[i = 4 (l / 16) + r]
+// [j = l % 16] in register r.
 // ---------------------------------------------------------------------------
 template <int HD, bool F16KV>
 __global__ __launch_bounds__(256, 2) void pf_attn_mfma_kernel(PrefillAttnParams p) {
     constexpr int KT = 64;                          // keys per step
-    constexpr int KS = HD + 4;                      // K row stride (floats)
-    constexpr int QS = HD / 4;                      // contraction steps of K Q^T
+    constexpr int QC = HD / 32;                     // 32-deep contraction steps of K Q^T
     constexpr int OC = HD / 16;                     // 16-dim output tiles
-    __shared__ __align__(16) float ks[KT * KS];
+    // K of the tile: kt[part][step st][key][32 dims] binary16 (dims 32 st ..),
+    // 16-byte chunk c of key r at chunk c ^ ((r >> 1) & 3); ksc[key] = 2^e_k
+    __shared__ __align__(16) _Float16 kt[2][QC][KT * 32];
+    __shared__ __align__(16) float ksc[KT];
     // V of the tile: vt[part][half s][lane group g][dim d][8 keys], binary16
     __shared__ __align__(16) _Float16 vt[2][2 * 4 * HD * 8];
 
@@ -999,19 +1000,38 @@ __global__ __launch_bounds__(256, 2) void pf_attn_mfma_kernel(PrefillAttnParams 
     const uint32_t kend = nc > 1u ? min(kbeg + p.ch, last + 1u) : last + 1u;
     if (kbeg > last) return;                        // a chunk past every key of the block
 
-    // Q fragment (B operand): lane holds q[wq0 + li][g4 * QS + s]
-    float qf[QS];
+    // Q fragment (B operand of K Q^T): lane holds q[wq0 + li][32 st + 8 g4 + b]
+    // times 2^-e_q (e_q from the query's max |q|: the lane's four-lane group)
+    // as two binary16 parts
+    half8v qh[QC], ql[QC];
+    float sq;                                       // 2^e_q
     {
         const uint32_t qi = min(wq0 + li, p.T - 1u);
-        const float* qrow = p.q + (uint64_t)qi * qd + (uint64_t)h * HD + g4 * QS;
+        const float* qrow = p.q + (uint64_t)qi * qd + (uint64_t)h * HD + 8u * g4;
+        float qv[QC][8];
+        float amax = 0.f;
 #pragma unroll
-        for (int s4 = 0; s4 < QS / 4; ++s4) {
-            const float4 v = *reinterpret_cast<const float4*>(qrow + 4 * s4);
-            qf[4 * s4] = v.x;
-            qf[4 * s4 + 1] = v.y;
-            qf[4 * s4 + 2] = v.z;
-            qf[4 * s4 + 3] = v.w;
+        for (int st = 0; st < QC; ++st) {
+            const float4 a = *reinterpret_cast<const float4*>(qrow + 32 * st);
+            const float4 b = *reinterpret_cast<const float4*>(qrow + 32 * st + 4);
+            qv[st][0] = a.x; qv[st][1] = a.y; qv[st][2] = a.z; qv[st][3] = a.w;
+            qv[st][4] = b.x; qv[st][5] = b.y; qv[st][6] = b.z; qv[st][7] = b.w;
+#pragma unroll
+            for (int b8 = 0; b8 < 8; ++b8) amax = fmaxf(amax, fabsf(qv[st][b8]));
         }
+        amax = fmaxf(amax, __shfl_xor(amax, 16, kWave));
+        amax = fmaxf(amax, __shfl_xor(amax, 32, kWave));
+        const int eq = pf_row_exponent(amax);
+        sq = ldexpf(1.0f, eq);
+#pragma unroll
+        for (int st = 0; st < QC; ++st)
+#pragma unroll
+            for (int b8 = 0; b8 < 8; ++b8) {
+                const float v = ldexpf(qv[st][b8], -eq);
+                const _Float16 hv = (_Float16)v;
+                qh[st][b8] = hv;
+                ql[st][b8] = (_Float16)(v - (float)hv);
+            }
     }
     const uint32_t qpos = p.pos0 + wq0 + li;        // this lane's query position
     float m = -INFINITY, l = 0.f;
@@ -1051,7 +1071,10 @@ __global__ __launch_bounds__(256, 2) void pf_attn_mfma_kernel(PrefillAttnParams 
             }
         }
     };
+    typedef _Float16 half4v __attribute__((ext_vector_type(4)));
     auto store_tile = [&]() {
+        // K: key r's HD/4 threads (consecutive lanes) share its exponent e_k
+        // (max |k| of the row, butterfly over those lanes), then two binary16 parts
 #pragma unroll
         for (int u = 0; u < KE; ++u) {
             const uint32_t e = t + 256u * (uint32_t)u;
@@ -1062,9 +1085,23 @@ __global__ __launch_bounds__(256, 2) void pf_attn_mfma_kernel(PrefillAttnParams 
                 kv = make_float4(h2f((uint16_t)(ax & 0xFFFFu)), h2f((uint16_t)(ax >> 16)),
                                  h2f((uint16_t)(ay & 0xFFFFu)), h2f((uint16_t)(ay >> 16)));
             }
-            *reinterpret_cast<float4*>(&ks[r * KS + 4 * c4]) = kv;
+            float amax = fmaxf(fmaxf(fabsf(kv.x), fabsf(kv.y)), fmaxf(fabsf(kv.z), fabsf(kv.w)));
+#pragma unroll
+            for (int w = 1; w < HD / 4; w *= 2) amax = fmaxf(amax, __shfl_xor(amax, w, kWave));
+            const int ek = pf_row_exponent(amax);
+            const float kin[4] = {ldexpf(kv.x, -ek), ldexpf(kv.y, -ek), ldexpf(kv.z, -ek), ldexpf(kv.w, -ek)};
+            _Float16 kh[4], kl[4];
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4) {
+                kh[q4] = (_Float16)kin[q4];
+                kl[q4] = (_Float16)(kin[q4] - (float)kh[q4]);
+            }
+            const uint32_t st = c4 / 8u, ch = ((c4 % 8u) / 2u) ^ ((r >> 1) & 3u);
+            const uint32_t o4 = r * 32u + ch * 8u + (c4 % 2u) * 4u;
+            *reinterpret_cast<half4v*>(&kt[0][st][o4]) = half4v{kh[0], kh[1], kh[2], kh[3]};
+            *reinterpret_cast<half4v*>(&kt[1][st][o4]) = half4v{kl[0], kl[1], kl[2], kl[3]};
+            if (c4 == 0) ksc[r] = ldexpf(1.0f, ek);
         }
-        typedef _Float16 half4v __attribute__((ext_vector_type(4)));
 #pragma unroll
         for (int u = 0; u < VE; ++u) {
             const uint32_t e = t + 256u * (uint32_t)u;
@@ -1092,32 +1129,37 @@ __global__ __launch_bounds__(256, 2) void pf_attn_mfma_kernel(PrefillAttnParams 
         load_tile(k0 + KT < kend ? k0 + KT : k0);
         // a wave with no visible key in the tile skips the work, not the barriers
         if (!(wave_on && k0 <= p.pos0 + wq0 + 15u)) continue;
-        // ---- S^T = K Q^T: four 16-key x 16-query tiles ----
+        // ---- S^T = K Q^T: four 16-key x 16-query tiles, three binary16 products
+        // (kh qh + kl qh + kh ql) per 32-deep step ----
         f32x4v sacc[4];
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
             sacc[c] = f32x4v{0.f, 0.f, 0.f, 0.f};
-            const float* krow = &ks[(16u * c + li) * KS + g4 * QS];
+            const uint32_t o8 = (16u * c + li) * 32u + (g4 ^ ((li >> 1) & 3u)) * 8u;
 #pragma unroll
-            for (int s4 = 0; s4 < QS / 4; ++s4) {
-                const float4 kb = *reinterpret_cast<const float4*>(krow + 4 * s4);
-                sacc[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(kb.x, qf[4 * s4], sacc[c], 0, 0, 0);
-                sacc[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(kb.y, qf[4 * s4 + 1], sacc[c], 0, 0, 0);
-                sacc[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(kb.z, qf[4 * s4 + 2], sacc[c], 0, 0, 0);
-                sacc[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(kb.w, qf[4 * s4 + 3], sacc[c], 0, 0, 0);
+            for (int st = 0; st < QC; ++st) {
+                const half8v kh = *reinterpret_cast<const half8v*>(&kt[0][st][o8]);
+                const half8v kl = *reinterpret_cast<const half8v*>(&kt[1][st][o8]);
+                sacc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qh[st], sacc[c], 0, 0, 0);
+                sacc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl, qh[st], sacc[c], 0, 0, 0);
+                sacc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, ql[st], sacc[c], 0, 0, 0);
             }
         }
         // ---- online softmax of query li over keys 16 c + 4 g4 + r ----
         float sv[4][4];
         float mx = -INFINITY;
 #pragma unroll
-        for (int c = 0; c < 4; ++c)
+        for (int c = 0; c < 4; ++c) {
+            const float4 kf = *reinterpret_cast<const float4*>(&ksc[16u * c + 4u * g4]);
+            const float kfa[4] = {kf.x, kf.y, kf.z, kf.w};
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const uint32_t kp = k0 + 16u * c + 4u * g4 + (uint32_t)r;
-                sv[c][r] = kp <= qpos ? sacc[c][r] * p.scale : -INFINITY;
+                // the dot at its own scale (times 2^(e_k + e_q), exact), then the softmax scale
+                sv[c][r] = kp <= qpos ? (sacc[c][r] * (kfa[r] * sq)) * p.scale : -INFINITY;
                 mx = fmaxf(mx, sv[c][r]);
             }
+        }
         mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
         mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
         const float m_new = fmaxf(m, mx);
