@@ -513,21 +513,26 @@ __global__ __launch_bounds__(256) void pf_gemm_kernel(PrefillGemmParams p) {
 // Prefill GEMM on pre-packed Q4 weights (the same numerics as pf_gemm_kernel:
 // y = x' w' 2^(e_t + f_g), three f16 products per pair xh wh + xl wh + xh wl
 // accumulated in fp32, in that order, per 32-deep K step).
-// Block: 256 threads (2 x 2 waves) over BM tokens x 128 columns; each wave
-// holds (BM / 2) x 64 of the output as (BM / 32) x 4 MFMA tiles. Per K step
-// a thread loads its x' row piece (both parts), 8 bytes of packed weights
-// (16 values) and 16 bytes of their scales; the next step's loads are in
-// flight while the current step's operands go through the matrix cores, and
-// the LDS is double-buffered (one barrier per step; 64 KB a block at 128
-// tokens, two blocks per CU). Up to three weight
+// Block: 256 threads (4 waves) over BM tokens x 128 columns; wave w holds
+// the BM x 32 output of the 32-column group w as (BM / 16) x 2 MFMA tiles.
+// Only x' goes through LDS (shared by the four waves): each wave loads the
+// packed weights and scales of its own columns straight into registers (a
+// lane's 8 bytes are its B fragments for two tiles: 8 rows of 2 columns) and
+// dequantises them there, so weights cost no LDS traffic and no second
+// dequantisation (against 2 x 2 waves of BM / 2 x 64 with the weights staged
+// in LDS: 72 KB of LDS traffic per block step at 64 tokens against 40 KB, and
+// 20 % less time). Per K step a thread loads its x' row piece (both parts)
+// and its wave's weights; loads run two steps ahead of the matrix cores,
+// weights are dequantised one step ahead, and the x' LDS is double-buffered
+// (one barrier per step; 16 KB a block at 64 tokens). Up to three weight
 // segments share the launch (q|k|v, gate|up): column block b belongs to the
 // segment whose blocks start at or below it.
 //
 // Packed layout (pf_pack_q4_kernel), per 128-column block nb and 32-row step
-// ks: thread t = 64 rg + bc owns columns c0 = 32 (bc / 16) + bc % 16 and
+// ks: entry t = 64 rg + bc holds columns c0 = 32 (bc / 16) + bc % 16 and
 // c0 + 16 (one 32-column group, so one set of scales) and rows 8 rg .. 8 rg + 7;
-// consecutive lanes own consecutive columns, so their LDS stores (80-byte
-// column stride) fall in distinct banks. Word c of its uint2 holds column
+// lane l = 16 rg + i of the wave of group g reads entry 64 rg + 16 g + i, the
+// rows and columns of its B fragments. Word c of the uint2 holds column
 // c0 + 16 c: row 8 rg + 2 j in nibble j and row 8 rg + 2 j + 1 in nibble j + 4,
 // so (word >> 4 j) & 0x000F000F is the pair of rows (2 j, 2 j + 1) in the low
 // bits of two binary16 halves. The scales are
@@ -566,26 +571,23 @@ __global__ __launch_bounds__(256) void pf_pack_q4_kernel(const uint8_t* w, const
 }
 
 template <int BM>
-__global__ __launch_bounds__(256) void pf_gemm2_kernel(PfGemm2Params p) {
+__global__ __launch_bounds__(256, 2) void pf_gemm2_kernel(PfGemm2Params p) {
     constexpr int BN = 128, KC = 32;
     // LDS rows of 64 B (32 halves, no padding); the 16-byte chunk c of row r
-    // sits at chunk c ^ ((r >> 1) & 3), which leaves the fragment reads, the
-    // x' stores (two or four threads a row) and the weight stores (lanes on
-    // consecutive columns) free of bank conflicts
+    // sits at chunk c ^ ((r >> 1) & 3), which leaves the fragment reads and the
+    // x' stores (two or four threads a row) free of bank conflicts
     constexpr int XS = KC;
-    constexpr int WM = BM / 2, TM = WM / 16, TN = 4;
-    constexpr int XT = 256 / BM;                    // threads per x' row (2 or 4)
-    constexpr int XH = KC / XT;                     // halves of a row per thread (16 or 8)
-    constexpr int XV = XH / 8;                      // 16-byte loads per part (2 or 1)
+    constexpr int TM = BM / 16, TN = 2;
+    constexpr int XT = 256 / BM;                    // threads per x' row (4 or 2)
+    constexpr int XH = KC / XT;                     // halves of a row per thread (8 or 16)
+    constexpr int XV = XH / 8;                      // 16-byte loads per part (1 or 2)
     static_assert(BM == 64 || BM == 128, "64- or 128-token tiles");
     __shared__ __align__(16) _Float16 xs[2][2][BM * XS];
-    __shared__ __align__(16) _Float16 ws[2][2][BN * XS];
     kernarg_warm(p);
 
     const int t = threadIdx.x;
     const int lane = t & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
-    const int wm = wave >> 1, wn = wave & 1;
     const uint32_t nb = blockIdx.x;
     // the segment of this column block (wave-uniform: whole-struct selects, no
     // indexing of the argument block)
@@ -601,18 +603,17 @@ __global__ __launch_bounds__(256) void pf_gemm2_kernel(PfGemm2Params p) {
     // x' rows: thread t loads XH halves of row t / XT (rows past T read row T - 1, masked at the end)
     const uint32_t xr = (uint32_t)t / XT, xq = (uint32_t)t % XT;
     const uint64_t xoff = (uint64_t)min(m0 + xr, p.T - 1u) * K + xq * XH;
-    // weights: columns cw, cw + 16 of the block, rows 8 rg .. 8 rg + 7 of the step
-    const uint32_t bc = (uint32_t)t % 64u, rg = (uint32_t)t / 64u;
-    const uint32_t cw = (bc / 16u) * 32u + bc % 16u;
-    const uint32_t g = bc / 16u;                    // 32-column group in the block
-    const uint2* wqp = sg.wq + (uint64_t)lnb * KS * 256u + (uint32_t)t;
-    const uint16_t* scp = sg.sc + ((uint64_t)lnb * KS * 4u + g) * 32u + rg * 8u;
+    // weights: lane (kq, li) of wave w holds rows 8 kq .. 8 kq + 7 of columns
+    // 32 w + li and 32 w + 16 + li, with their 8 scales
+    const uint32_t li = (uint32_t)lane % 16u, kq = (uint32_t)lane / 16u;
+    const uint2* wqp = sg.wq + (uint64_t)lnb * KS * 256u + 64u * kq + 16u * (uint32_t)wave + li;
+    const uint16_t* scp = sg.sc + ((uint64_t)lnb * KS * 4u + (uint32_t)wave) * 32u + 8u * kq;
 
     // (native vector types: the compiler keeps these in registers)
     struct Slice {
         v4u32 xh0, xh1, xl0, xl1;                   // x' pieces (xh1, xl1: 128-token tiles only)
         v2u32 wq;
-        v4u32 sc;                                   // 8 binary16 s', rows 8 rg .. + 7 (pairs)
+        v4u32 sc;                                   // 8 binary16 s', rows 8 kq .. + 7 (pairs)
     };
     auto load_slice = [&](Slice& q, uint32_t s) {
         const uint32_t k0 = kb + s * (uint32_t)KC;
@@ -626,7 +627,7 @@ __global__ __launch_bounds__(256) void pf_gemm2_kernel(PfGemm2Params p) {
         q.wq = *reinterpret_cast<const v2u32*>(wqp + (uint64_t)ks * 256u);
         q.sc = *reinterpret_cast<const v4u32*>(scp + (uint64_t)ks * 128u);
     };
-    auto store_slice = [&](const Slice& q, int buf) {
+    auto store_x = [&](const Slice& q, int buf) {
         const uint32_t xsw = (xr >> 1) & 3u;
         const uint32_t xc0 = xr * XS + ((xq * XV) ^ xsw) * 8u, xc1 = xr * XS + ((xq * XV + 1u) ^ xsw) * 8u;
         *reinterpret_cast<v4u32*>(&xs[buf][0][xc0]) = q.xh0;
@@ -635,12 +636,15 @@ __global__ __launch_bounds__(256) void pf_gemm2_kernel(PfGemm2Params p) {
             *reinterpret_cast<v4u32*>(&xs[buf][0][xc1]) = q.xh1;
             *reinterpret_cast<v4u32*>(&xs[buf][1][xc1]) = q.xl1;
         }
-        // wh, wl of columns cw, cw + 16, two rows per binary16 pair
+    };
+    // wh, wl of the lane's two columns, two rows per binary16 pair: the B
+    // fragments (k = 8 kq + b, column li) of tiles 0 and 1
+    auto dequant = [&](const Slice& q, half8v* bh, half8v* bl) {
         const half2v bias = {(_Float16)1032.0f, (_Float16)1032.0f};
-        v4u32 wh[2], wl[2];
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
             const uint32_t wv = q.wq[c];
+            v4u32 wh, wl;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const half2v qv = __builtin_bit_cast(half2v, ((wv >> (4 * j)) & 0x000F000Fu) | 0x64006400u) - bias;
@@ -648,16 +652,12 @@ __global__ __launch_bounds__(256) void pf_gemm2_kernel(PfGemm2Params p) {
                 const half2v sv = __builtin_bit_cast(half2v, sj);
                 const half2v h = qv * sv;
                 const half2v l = __builtin_elementwise_fma(qv, sv, -h);
-                wh[c][j] = __builtin_bit_cast(uint32_t, h);
-                wl[c][j] = __builtin_bit_cast(uint32_t, l);
+                wh[j] = __builtin_bit_cast(uint32_t, h);
+                wl[j] = __builtin_bit_cast(uint32_t, l);
             }
+            bh[c] = __builtin_bit_cast(half8v, wh);
+            bl[c] = __builtin_bit_cast(half8v, wl);
         }
-        const uint32_t wsw = (cw >> 1) & 3u;               // the same for cw + 16
-        const uint32_t c0 = cw * XS + (rg ^ wsw) * 8u, c1 = (cw + 16u) * XS + (rg ^ wsw) * 8u;
-        *reinterpret_cast<v4u32*>(&ws[buf][0][c0]) = wh[0];
-        *reinterpret_cast<v4u32*>(&ws[buf][0][c1]) = wh[1];
-        *reinterpret_cast<v4u32*>(&ws[buf][1][c0]) = wl[0];
-        *reinterpret_cast<v4u32*>(&ws[buf][1][c1]) = wl[1];
     };
 
     f32x4v acc[TM][TN];
@@ -665,22 +665,14 @@ __global__ __launch_bounds__(256) void pf_gemm2_kernel(PfGemm2Params p) {
     for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = f32x4v{0.f, 0.f, 0.f, 0.f};
-    const uint32_t li = (uint32_t)lane % 16u, kq = (uint32_t)lane / 16u;
-    auto compute = [&](int buf) {
-        half8v ah[TM], al[TM], bh[TN], bl[TN];
+    auto compute = [&](int buf, const half8v* bh, const half8v* bl) {
+        half8v ah[TM], al[TM];
 #pragma unroll
         for (int i = 0; i < TM; ++i) {
-            const uint32_t row = (uint32_t)wm * WM + (uint32_t)i * 16u + li;
+            const uint32_t row = (uint32_t)i * 16u + li;
             const uint32_t ch = kq ^ ((li >> 1) & 3u);     // row % 16 == li
             ah[i] = *reinterpret_cast<const half8v*>(&xs[buf][0][row * XS + ch * 8u]);
             al[i] = *reinterpret_cast<const half8v*>(&xs[buf][1][row * XS + ch * 8u]);
-        }
-#pragma unroll
-        for (int j = 0; j < TN; ++j) {
-            const uint32_t c = (uint32_t)wn * 64u + (uint32_t)j * 16u + li;
-            const uint32_t ch = kq ^ ((li >> 1) & 3u);     // c % 16 == li
-            bh[j] = *reinterpret_cast<const half8v*>(&ws[buf][0][c * XS + ch * 8u]);
-            bl[j] = *reinterpret_cast<const half8v*>(&ws[buf][1][c * XS + ch * 8u]);
         }
 #pragma unroll
         for (int j = 0; j < TN; ++j)
@@ -693,33 +685,38 @@ __global__ __launch_bounds__(256) void pf_gemm2_kernel(PfGemm2Params p) {
     };
 
     // global loads run two steps ahead of the matrix cores: slice se holds the
-    // even steps, so the odd ones; the LDS buffer of step s is s & 1. The
-    // steady-state loop has no branches, so the compiler interleaves one
-    // step's matrix-core work with the dequantisation and LDS stores of the
-    // next (loads of a clamped step index past the end stay in bounds and are
-    // not used).
+    // even steps, so the odd ones; the LDS buffer and weight registers of step
+    // s are s & 1. The steady-state loop has no branches, so the compiler
+    // interleaves one step's matrix-core work with the dequantisation and LDS
+    // stores of the next (loads of a clamped step index past the end stay in
+    // bounds and are not used).
     Slice se, so;
+    half8v bhE[TN], blE[TN], bhO[TN], blO[TN];
     if (steps > 0) {
         load_slice(se, 0);
         load_slice(so, min(1u, steps - 1u));
-        store_slice(se, 0);
+        store_x(se, 0);
+        dequant(se, bhE, blE);
         __syncthreads();
         uint32_t s = 0;
         for (; s + 2 < steps; s += 2) {
             load_slice(se, s + 2);
-            compute(0);
-            store_slice(so, 1);
+            compute(0, bhE, blE);
+            store_x(so, 1);
+            dequant(so, bhO, blO);
             __syncthreads();
             load_slice(so, min(s + 3u, steps - 1u));
-            compute(1);
-            store_slice(se, 0);
+            compute(1, bhO, blO);
+            store_x(se, 0);
+            dequant(se, bhE, blE);
             __syncthreads();
         }
-        compute(0);
+        compute(0, bhE, blE);
         if (s + 1 < steps) {
-            store_slice(so, 1);
+            store_x(so, 1);
+            dequant(so, bhO, blO);
             __syncthreads();
-            compute(1);
+            compute(1, bhO, blO);
         }
     }
 
@@ -728,12 +725,12 @@ __global__ __launch_bounds__(256) void pf_gemm2_kernel(PfGemm2Params p) {
     for (int i = 0; i < TM; ++i) {
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
-            const uint32_t cl = (uint32_t)wn * 64u + (uint32_t)j * 16u + li;   // column in the block
+            const uint32_t cl = (uint32_t)wave * 32u + (uint32_t)j * 16u + li;  // column in the block
             const uint32_t c = lnb * (uint32_t)BN + cl;                        // column in the segment
             const int fg = (int)sg.wf[c / 32u];
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const uint32_t row = m0 + (uint32_t)wm * WM + (uint32_t)i * 16u + kq * 4u + (uint32_t)r;
+                const uint32_t row = m0 + (uint32_t)i * 16u + kq * 4u + (uint32_t)r;
                 if (row >= p.T) continue;
                 const float v = ldexpf(acc[i][j][r], p.xe[row] + fg);
                 if (p.splits > 1) {
