@@ -63,6 +63,83 @@ __device__ __forceinline__ float pf_block_max(float v, float* red) {
     return m;
 }
 
+// Row chunks of the register-cached producers: thread t of NT owns the runs
+// of four consecutive elements starting at 4 (t + NT i). A row whose length,
+// stride and pointers are multiples of four elements (16 bytes of fp32, 8 of
+// binary16) moves as vectors (VEC); any other row element by element, with
+// the same values. Elements past the row end read as 0 and are not written.
+// Loads are branch-free (indexes clamped into the row, the value then
+// selected), so all of a thread's loads are in flight together.
+__device__ __forceinline__ bool pf_al(const void* a, uintptr_t m) { return ((uintptr_t)a & (m - 1)) == 0; }
+
+template <bool VEC>
+__device__ __forceinline__ void pf_load4(const float* x, uint32_t j, uint32_t n, float* v) {
+    if constexpr (VEC) {                            // n is a positive multiple of 4
+        const float4 a = *reinterpret_cast<const float4*>(x + min(j, n - 4u));
+        const bool in = j < n;
+        v[0] = in ? a.x : 0.f;
+        v[1] = in ? a.y : 0.f;
+        v[2] = in ? a.z : 0.f;
+        v[3] = in ? a.w : 0.f;
+    } else {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const float a = x[min(j + (uint32_t)c, n - 1u)];
+            v[c] = j + c < n ? a : 0.f;
+        }
+    }
+}
+
+template <bool VEC>
+__device__ __forceinline__ void pf_gamma4(const uint16_t* g, uint32_t j, uint32_t n, float* v) {
+    if constexpr (VEC) {
+        const uint2 a = *reinterpret_cast<const uint2*>(g + min(j, n - 4u));
+        const bool in = j < n;
+        v[0] = in ? h2f((uint16_t)(a.x & 0xFFFFu)) : 0.f;
+        v[1] = in ? h2f((uint16_t)(a.x >> 16)) : 0.f;
+        v[2] = in ? h2f((uint16_t)(a.y & 0xFFFFu)) : 0.f;
+        v[3] = in ? h2f((uint16_t)(a.y >> 16)) : 0.f;
+    } else {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const float a = h2f(g[min(j + (uint32_t)c, n - 1u)]);
+            v[c] = j + c < n ? a : 0.f;
+        }
+    }
+}
+
+template <bool VEC>
+__device__ __forceinline__ void pf_store4(float* x, uint32_t j, uint32_t n, const float* v) {
+    if constexpr (VEC) {
+        if (j < n) *reinterpret_cast<float4*>(x + j) = make_float4(v[0], v[1], v[2], v[3]);
+    } else {
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+            if (j + c < n) x[j + c] = v[c];
+    }
+}
+
+template <bool VEC>
+__device__ __forceinline__ void pf_split4(const float* v, int e, _Float16* xh, _Float16* xl, uint32_t j, uint32_t n) {
+    typedef _Float16 half4v __attribute__((ext_vector_type(4)));
+    if constexpr (VEC) {
+        if (j >= n) return;
+        half4v h, l;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const float sv = ldexpf(v[c], -e);
+            h[c] = (_Float16)sv;
+            l[c] = (_Float16)(sv - (float)h[c]);
+        }
+        *reinterpret_cast<half4v*>(xh + j) = h;
+        *reinterpret_cast<half4v*>(xl + j) = l;
+    } else {
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+            if (j + c < n) pf_split(v[c], e, xh + j + c, xl + j + c);
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Row producers: one block of 256 threads per token row. Each writes the
 // split GEMM operand (xh, xl: [T][k] binary16, xe[T] exponents).
@@ -102,8 +179,11 @@ __global__ __launch_bounds__(256) void pf_rmsnorm_split_kernel(PrefillRowParams 
         }
         __syncthreads();
     }
+    // sum of squares in the order of the register-cached kernel: thread t
+    // takes the runs 4 t + 1024 i, each in element order
     float ss = 0.f;
-    for (uint32_t j = threadIdx.x; j < p.n; j += 256) ss = fmaf(x[j], x[j], ss);
+    for (uint32_t b0 = 4u * threadIdx.x; b0 < p.n; b0 += 1024u)
+        for (uint32_t j = b0; j < min(b0 + 4u, p.n); ++j) ss = fmaf(x[j], x[j], ss);
     ss = block_sum<256>(ss, red);
     const float inv = 1.0f / sqrtf(ss / (float)p.n + 1e-6f);
     float amax = 0.f;
@@ -151,121 +231,142 @@ __global__ __launch_bounds__(256) void pf_silu_split_kernel(PrefillRowParams p) 
     if (threadIdx.x == 0) p.xe[t] = e;
 }
 
-// The same three producers with the row held in registers (thread t keeps
-// elements t + NT i, i < EPT, NT = 256 unless stated): each element is read once instead of two or
-// three times, with the same arithmetic. For rows of at most 256 * EPT.
-template <int EPT>
-__global__ __launch_bounds__(256) void pf_rmsnorm_split_reg_kernel(PrefillRowParams p) {
-    __shared__ float red[4];
+// The same three producers with the row held in registers: each element is
+// read once instead of two or three times, with the same arithmetic. The
+// norm and the split keep the runs of four elements at 4 (t + 256 i) (as
+// pf_load4 describes; the norm's sum of squares runs in that order in the
+// multi-pass kernel too). For rows of at most 256 * EPT (SwiGLU: NT * EPT).
+template <int EPT, bool VEC>
+__device__ __forceinline__ void pf_rmsnorm_split_row(const PrefillRowParams& p, float* red) {
+    constexpr int C = EPT / 4;
     const uint32_t t = blockIdx.x;
     float* x = p.x + (uint64_t)t * p.n;
-    float v[EPT];
-    float gm[EPT];
-    float ss = 0.f;
+    float v[C][4];
+    float gm[C][4];
 #pragma unroll
-    for (int i = 0; i < EPT; ++i) {
-        const uint32_t j = threadIdx.x + 256u * (uint32_t)i;
-        v[i] = j < p.n ? x[j] : 0.f;
-        gm[i] = j < p.n ? h2f(p.gamma[j]) : 0.f;
+    for (int i = 0; i < C; ++i) {
+        const uint32_t j = 4u * (threadIdx.x + 256u * (uint32_t)i);
+        pf_load4<VEC>(x, j, p.n, v[i]);
+        pf_gamma4<VEC>(p.gamma, j, p.n, gm[i]);
     }
     if (p.part) {
         // the residual add of the split-K GEMM before this norm, in the
         // order pf_splitk_reduce2_kernel sums: x += ((p0 + p1) + p2) + ...
         // Partials are loaded four splits at a time, all of a group's loads
-        // issued before its adds (indexes clamped to the last split; the
-        // extra values are not added).
+        // issued before its adds (split indexes clamped to the last split;
+        // the extra values are not added).
         const float* pr = p.part + (uint64_t)t * p.n;
-        float a[EPT];
+        float a[C][4];
         for (uint32_t z = 0; z < p.splits; z += 4) {
-            float q[4][EPT];
+            float q[4][C][4];
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
                 const uint64_t zo = (uint64_t)min(z + (uint32_t)u, p.splits - 1u) * p.part_stride;
 #pragma unroll
-                for (int i = 0; i < EPT; ++i) {
-                    const uint32_t j = min(threadIdx.x + 256u * (uint32_t)i, p.n - 1u);
-                    q[u][i] = pr[zo + j];
-                }
+                for (int i = 0; i < C; ++i) pf_load4<VEC>(pr + zo, 4u * (threadIdx.x + 256u * (uint32_t)i), p.n, q[u][i]);
             }
 #pragma unroll
             for (int u = 0; u < 4; ++u)
 #pragma unroll
-                for (int i = 0; i < EPT; ++i)
-                    if (z + (uint32_t)u < p.splits) a[i] = (z == 0 && u == 0) ? q[0][i] : a[i] + q[u][i];
+                for (int i = 0; i < C; ++i)
+#pragma unroll
+                    for (int c = 0; c < 4; ++c)
+                        if (z + (uint32_t)u < p.splits) a[i][c] = (z == 0 && u == 0) ? q[0][i][c] : a[i][c] + q[u][i][c];
         }
 #pragma unroll
-        for (int i = 0; i < EPT; ++i) {
-            const uint32_t j = threadIdx.x + 256u * (uint32_t)i;
-            if (j >= p.n) continue;
-            v[i] += a[i];
-            x[j] = v[i];
+        for (int i = 0; i < C; ++i) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) v[i][c] += a[i][c];
+            pf_store4<VEC>(x, 4u * (threadIdx.x + 256u * (uint32_t)i), p.n, v[i]);
         }
     }
+    // (elements past the row end are 0 and leave the sum unchanged)
+    float ss = 0.f;
 #pragma unroll
-    for (int i = 0; i < EPT; ++i) ss = fmaf(v[i], v[i], ss);
+    for (int i = 0; i < C; ++i)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) ss = fmaf(v[i][c], v[i][c], ss);
     ss = block_sum<256>(ss, red);
     const float inv = 1.0f / sqrtf(ss / (float)p.n + 1e-6f);
     float amax = 0.f;
 #pragma unroll
-    for (int i = 0; i < EPT; ++i) {
-        v[i] = (v[i] * inv) * gm[i];
-        amax = fmaxf(amax, fabsf(v[i]));
+    for (int i = 0; i < C; ++i)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            v[i][c] = (v[i][c] * inv) * gm[i][c];
+            amax = fmaxf(amax, fabsf(v[i][c]));
+        }
+    const int e = pf_row_exponent(pf_block_max<256>(amax, red));
+    _Float16* xh = reinterpret_cast<_Float16*>(p.xh) + (uint64_t)t * p.n;
+    _Float16* xl = reinterpret_cast<_Float16*>(p.xl) + (uint64_t)t * p.n;
+#pragma unroll
+    for (int i = 0; i < C; ++i) pf_split4<VEC>(v[i], e, xh, xl, 4u * (threadIdx.x + 256u * (uint32_t)i), p.n);
+    if (threadIdx.x == 0) p.xe[t] = e;
+}
+
+template <int EPT>
+__global__ __launch_bounds__(256) void pf_rmsnorm_split_reg_kernel(PrefillRowParams p) {
+    __shared__ float red[4];
+    if (p.n % 4u == 0 && pf_al(p.x, 16) && pf_al(p.gamma, 8) && pf_al(p.xh, 8) && pf_al(p.xl, 8) &&
+        (!p.part || (pf_al(p.part, 16) && p.part_stride % 4u == 0)))
+        pf_rmsnorm_split_row<EPT, true>(p, red);
+    else
+        pf_rmsnorm_split_row<EPT, false>(p, red);
+}
+
+template <int EPT, bool VEC>
+__device__ __forceinline__ void pf_split_row(const PrefillRowParams& p, float* red) {
+    constexpr int C = EPT / 4;
+    const uint32_t t = blockIdx.x;
+    const float* x = p.x + (uint64_t)t * p.n;
+    float v[C][4];
+    float amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < C; ++i) {
+        pf_load4<VEC>(x, 4u * (threadIdx.x + 256u * (uint32_t)i), p.n, v[i]);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) amax = fmaxf(amax, fabsf(v[i][c]));
     }
     const int e = pf_row_exponent(pf_block_max<256>(amax, red));
     _Float16* xh = reinterpret_cast<_Float16*>(p.xh) + (uint64_t)t * p.n;
     _Float16* xl = reinterpret_cast<_Float16*>(p.xl) + (uint64_t)t * p.n;
 #pragma unroll
-    for (int i = 0; i < EPT; ++i) {
-        const uint32_t j = threadIdx.x + 256u * (uint32_t)i;
-        if (j < p.n) pf_split(v[i], e, xh + j, xl + j);
-    }
+    for (int i = 0; i < C; ++i) pf_split4<VEC>(v[i], e, xh, xl, 4u * (threadIdx.x + 256u * (uint32_t)i), p.n);
     if (threadIdx.x == 0) p.xe[t] = e;
 }
 
 template <int EPT>
 __global__ __launch_bounds__(256) void pf_split_reg_kernel(PrefillRowParams p) {
     __shared__ float red[4];
-    const uint32_t t = blockIdx.x;
-    const float* x = p.x + (uint64_t)t * p.n;
-    float v[EPT];
-    float amax = 0.f;
-#pragma unroll
-    for (int i = 0; i < EPT; ++i) {
-        const uint32_t j = threadIdx.x + 256u * (uint32_t)i;
-        v[i] = j < p.n ? x[j] : 0.f;
-        amax = fmaxf(amax, fabsf(v[i]));
-    }
-    const int e = pf_row_exponent(pf_block_max<256>(amax, red));
-    _Float16* xh = reinterpret_cast<_Float16*>(p.xh) + (uint64_t)t * p.n;
-    _Float16* xl = reinterpret_cast<_Float16*>(p.xl) + (uint64_t)t * p.n;
-#pragma unroll
-    for (int i = 0; i < EPT; ++i) {
-        const uint32_t j = threadIdx.x + 256u * (uint32_t)i;
-        if (j < p.n) pf_split(v[i], e, xh + j, xl + j);
-    }
-    if (threadIdx.x == 0) p.xe[t] = e;
+    if (p.n % 4u == 0 && pf_al(p.x, 16) && pf_al(p.xh, 8) && pf_al(p.xl, 8))
+        pf_split_row<EPT, true>(p, red);
+    else
+        pf_split_row<EPT, false>(p, red);
 }
 
-// NT threads per row: the row's maximum does not depend on the thread count,
-// so any NT gives the same values (1024 for 11008-wide rows: 16 waves a row).
+// SwiGLU rows on NT threads, thread t holding the elements t + NT i (the
+// row's maximum does not depend on the thread count or order, so any NT and
+// mapping give the same values; 1024 threads for 11008-wide rows: 16 waves a
+// row). Loads are branch-free (indexes clamped into the row).
 template <int NT, int EPT>
 __global__ __launch_bounds__(NT) void pf_silu_split_reg_kernel(PrefillRowParams p) {
     __shared__ float red[NT / kWave];
     const uint32_t t = blockIdx.x;
     const float* g = p.x + (uint64_t)t * p.ld;
     const float* u = p.u + (uint64_t)t * p.ld;
-    float v[EPT];
+    float gv[EPT], uv[EPT];
+#pragma unroll
+    for (int i = 0; i < EPT; ++i) {
+        const uint32_t j = min(threadIdx.x + (uint32_t)NT * (uint32_t)i, p.n - 1u);
+        gv[i] = g[j];
+        uv[i] = u[j];
+    }
     float amax = 0.f;
 #pragma unroll
     for (int i = 0; i < EPT; ++i) {
         const uint32_t j = threadIdx.x + (uint32_t)NT * (uint32_t)i;
-        float h = 0.f;
-        if (j < p.n) {
-            const float gv = g[j];
-            h = (gv / (1.0f + expf(-gv))) * u[j];
-        }
-        v[i] = h;
-        amax = fmaxf(amax, fabsf(h));
+        gv[i] = j < p.n ? (gv[i] / (1.0f + expf(-gv[i]))) * uv[i] : 0.f;
+        amax = fmaxf(amax, fabsf(gv[i]));
     }
     const int e = pf_row_exponent(pf_block_max<NT>(amax, red));
     _Float16* xh = reinterpret_cast<_Float16*>(p.xh) + (uint64_t)t * p.n;
@@ -273,7 +374,7 @@ __global__ __launch_bounds__(NT) void pf_silu_split_reg_kernel(PrefillRowParams 
 #pragma unroll
     for (int i = 0; i < EPT; ++i) {
         const uint32_t j = threadIdx.x + (uint32_t)NT * (uint32_t)i;
-        if (j < p.n) pf_split(v[i], e, xh + j, xl + j);
+        if (j < p.n) pf_split(gv[i], e, xh + j, xl + j);
     }
     if (threadIdx.x == 0) p.xe[t] = e;
 }
@@ -792,11 +893,29 @@ __global__ __launch_bounds__(256) void pf_rope_cache_kernel(PrefillAttnParams p)
     if (p.qkv_part) {
         // the q|k|v row from the GEMM's split-K partials, summed in split order
         // (as pf_splitk_reduce2_kernel would store it)
+        // Four elements (i0 + 256 c) and four splits at a time, all of a
+        // group's loads issued before its adds (indexes clamped into the row
+        // and to the last split; the extra values are not used).
         const float* pr = p.qkv_part + (uint64_t)t * qkvn;
-        for (uint32_t i = threadIdx.x; i < qkvn; i += 256) {
-            float a = pr[i];
-            for (uint32_t z = 1; z < p.qkv_splits; ++z) a += pr[(uint64_t)z * p.qkv_part_stride + i];
-            rs[i] = a;
+        for (uint32_t i0 = threadIdx.x; i0 < qkvn; i0 += 1024u) {
+            float a[4];
+            for (uint32_t z = 0; z < p.qkv_splits; z += 4) {
+                float q[4][4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const uint64_t zo = (uint64_t)min(z + (uint32_t)u, p.qkv_splits - 1u) * p.qkv_part_stride;
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) q[u][c] = pr[zo + min(i0 + 256u * (uint32_t)c, qkvn - 1u)];
+                }
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+#pragma unroll
+                    for (int c = 0; c < 4; ++c)
+                        if (z + (uint32_t)u < p.qkv_splits) a[c] = (z == 0 && u == 0) ? q[0][c] : a[c] + q[u][c];
+            }
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+                if (i0 + 256u * (uint32_t)c < qkvn) rs[i0 + 256u * c] = a[c];
         }
         __syncthreads();
         row = rs;
@@ -1328,8 +1447,20 @@ __global__ __launch_bounds__(256) void pf_attn_merge_split_kernel(PrefillAttnPar
     if (on) {
         _Float16* xh = reinterpret_cast<_Float16*>(p.xh) + (uint64_t)t * qd + e0;
         _Float16* xl = reinterpret_cast<_Float16*>(p.xl) + (uint64_t)t * qd + e0;
+        if (pf_al(xh, 16) && pf_al(xl, 16)) {
+            half8v hv, lv8;
 #pragma unroll
-        for (uint32_t i = 0; i < DPT; ++i) pf_split(v[i], e, xh + i, xl + i);
+            for (uint32_t i = 0; i < DPT; ++i) {
+                const float sv = ldexpf(v[i], -e);
+                hv[i] = (_Float16)sv;
+                lv8[i] = (_Float16)(sv - (float)hv[i]);
+            }
+            *reinterpret_cast<half8v*>(xh) = hv;
+            *reinterpret_cast<half8v*>(xl) = lv8;
+        } else {
+#pragma unroll
+            for (uint32_t i = 0; i < DPT; ++i) pf_split(v[i], e, xh + i, xl + i);
+        }
     }
     if (threadIdx.x == 0) p.xe[t] = e;
 }
