@@ -136,6 +136,7 @@ struct ModelState {
     int32_t* d_pf_xe = nullptr;          // [tc]
     uint32_t* d_pf_ids = nullptr;        // [cap]
     float* d_pf_part = nullptr;          // split-K partials of the GEMMs
+    uint64_t pf_part_bytes = 0;          // its size (the largest split set at set-up)
     float* d_pf_apart = nullptr;         // key-chunk partials of the prefill attention
     std::vector<int8_t*> pf_wf;          // [L][7] Q4 group exponents
     // Q4 weights packed for pf_gemm2_kernel ([L][7]), when every projection
@@ -1082,6 +1083,7 @@ int pf_setup(qora_hip_ctx* c) {
                 }
         }
         PF_ALLOC(d_pf_part, pb);
+        m.pf_part_bytes = pb;
     }
 #undef PF_ALLOC
     m.pf_wf.assign((size_t)m.L * 7, nullptr);
@@ -1154,7 +1156,11 @@ int pf_gemm(qora_hip_ctx* c, uint32_t l, int j, uint32_t T, float* y, uint32_t l
     g.y = y;
     g.ldy = ldy;
     g.accumulate = accumulate ? 1 : 0;
-    const PfGemmShape sh = pf_gemm_shape(T, g.k, g.n, c->cus);
+    PfGemmShape sh = pf_gemm_shape(T, g.k, g.n, c->cus);
+    if (sh.splits > 1 && (uint64_t)sh.splits * T * g.n * 4 > m.pf_part_bytes) {
+        sh.splits = 1;   // (as in pf_gemm2 below)
+        sh.kper = g.k;
+    }
     g.nt = sh.nt;
     g.splits = sh.splits;
     g.kper = sh.kper;
@@ -1202,7 +1208,13 @@ int pf_gemm2(qora_hip_ctx* c, uint32_t l, std::initializer_list<int> js, uint32_
         g.k = (uint32_t)w->k;
         g.ntot += (uint32_t)w->n;
     }
-    const PfGemm2Shape sh = pf_gemm2_shape(T, g.k, g.ntot, c->cus);
+    PfGemm2Shape sh = pf_gemm2_shape(T, g.k, g.ntot, c->cus);
+    // (a split set larger than the buffer sized at set-up, as the tuning
+    // variables read at each call could ask for, runs unsplit)
+    if (sh.splits > 1 && (uint64_t)sh.splits * T * g.ntot * 4 > m.pf_part_bytes) {
+        sh.splits = 1;
+        sh.kper = g.k;
+    }
     g.splits = sh.splits;
     g.kper = sh.kper;
     g.part = m.d_pf_part;

@@ -624,19 +624,29 @@ hipError_t launch_pf_pack_q4(const uint8_t* w, const uint16_t* scales, const int
 // 2.7% slower over a 512-token prefill), then the K split.
 PfGemm2Shape pf_gemm2_shape(uint32_t T, uint32_t k, uint32_t ntot, int cus) {
     PfGemm2Shape sh{};
-    sh.bm = 64u;
-    const char* eb = std::getenv("QORA_HIP_PF_BM");
-    if (eb && *eb) sh.bm = std::atoi(eb) == 64 ? 64u : 128u;
-    const uint64_t tiles = std::max<uint64_t>(1, (uint64_t)(ntot / 128u) * ((T + sh.bm - 1) / sh.bm));
     const uint32_t steps = k / 32u;
-    // K is split only when the tiles leave two block slots per CU partly
-    // empty: beyond that a split's partial-sum traffic costs more than it
-    // gains (with 64-token tiles three blocks fit a CU, but splitting for the
-    // third measured slower). The splits are of equal length (at least 8
-    // steps each, at most 16 splits), and the count is the one whose blocks
-    // fill their rounds best (fewer splits unless more fill them better by 2%
-    // or more): 512 tokens on 256 CUs, q|k|v 2, o 4, gate|up 1, down 4.
-    const uint64_t slots = 2u * (uint64_t)std::max(1, cus);
+    const uint64_t cu = (uint64_t)std::max(1, cus);
+    // 64-token tiles; 32-token tiles where K is short (at most 4096) and the
+    // 64-token tiles leave two block slots per CU partly empty: twice the
+    // blocks without more split partials (512 tokens on 256 CUs: q|k|v and o;
+    // a long K such as down's 11008 streams twice the weights through the L2
+    // with 32-token tiles and measured slower)
+    sh.bm = 64u;
+    if (k <= 4096u && (uint64_t)(ntot / 128u) * ((T + 63u) / 64u) < 2u * cu) sh.bm = 32u;
+    const char* eb = std::getenv("QORA_HIP_PF_BM");
+    if (eb && *eb) {
+        const int v = std::atoi(eb);
+        sh.bm = v == 32 ? 32u : v == 64 ? 64u : 128u;
+    }
+    const uint64_t tiles = std::max<uint64_t>(1, (uint64_t)(ntot / 128u) * ((T + sh.bm - 1) / sh.bm));
+    // K is split only when the tiles leave the block slots partly empty (two
+    // per CU; three for the lighter 32-token blocks): beyond that a split's
+    // partial-sum traffic costs more than it gains. The splits are of equal
+    // length (at least 8 steps each, at most 16 splits), and the count is the
+    // one whose blocks fill their rounds best (fewer splits unless more fill
+    // them better by 2% or more): 512 tokens on 256 CUs, q|k|v 2 and o 3 with
+    // 32-token tiles, gate|up 1 and down 4 with 64-token tiles.
+    const uint64_t slots = (sh.bm == 32u ? 3u : 2u) * cu;
     const uint32_t smax = tiles >= slots ? 1u
                                          : (uint32_t)std::min<uint64_t>({16u, std::max(1u, steps / 8u),
                                                                          (slots + tiles - 1) / tiles});
@@ -673,6 +683,7 @@ hipError_t launch_pf_gemm2(uint32_t bm, const PfGemm2Params& p, hipStream_t stre
     const dim3 grid(nb, (p.T + bm - 1) / bm, p.splits);
     if (bm == 128) hipLaunchKernelGGL((pf_gemm2_kernel<128>), grid, dim3(256), 0, stream, p);
     else if (bm == 64) hipLaunchKernelGGL((pf_gemm2_kernel<64>), grid, dim3(256), 0, stream, p);
+    else if (bm == 32) hipLaunchKernelGGL((pf_gemm2_kernel<32>), grid, dim3(256), 0, stream, p);
     else return hipErrorInvalidValue;
     if (p.splits > 1 && reduce) {
         const uint64_t total = (uint64_t)p.T * p.ntot;

@@ -679,10 +679,10 @@ __global__ __launch_bounds__(256, 2) void pf_gemm2_kernel(PfGemm2Params p) {
     // x' stores (two or four threads a row) free of bank conflicts
     constexpr int XS = KC;
     constexpr int TM = BM / 16, TN = 2;
-    constexpr int XT = 256 / BM;                    // threads per x' row (4 or 2)
-    constexpr int XH = KC / XT;                     // halves of a row per thread (8 or 16)
-    constexpr int XV = XH / 8;                      // 16-byte loads per part (1 or 2)
-    static_assert(BM == 64 || BM == 128, "64- or 128-token tiles");
+    constexpr int XT = 256 / BM;                    // threads per x' row (8, 4 or 2)
+    constexpr int XH = KC / XT;                     // halves of a row per thread (4, 8 or 16)
+    constexpr int XV = XH / 8;                      // 16-byte loads per part (0: one 8-byte load, 1 or 2)
+    static_assert(BM == 32 || BM == 64 || BM == 128, "32-, 64- or 128-token tiles");
     __shared__ __align__(16) _Float16 xs[2][2][BM * XS];
     kernarg_warm(p);
 
@@ -712,14 +712,22 @@ __global__ __launch_bounds__(256, 2) void pf_gemm2_kernel(PfGemm2Params p) {
 
     // (native vector types: the compiler keeps these in registers)
     struct Slice {
-        v4u32 xh0, xh1, xl0, xl1;                   // x' pieces (xh1, xl1: 128-token tiles only)
+        v4u32 xh0, xh1, xl0, xl1;                   // x' pieces (xh1, xl1: 128-token tiles only;
+                                                    // 32-token tiles use the first two words)
         v2u32 wq;
         v4u32 sc;                                   // 8 binary16 s', rows 8 kq .. + 7 (pairs)
     };
     auto load_slice = [&](Slice& q, uint32_t s) {
         const uint32_t k0 = kb + s * (uint32_t)KC;
-        q.xh0 = *reinterpret_cast<const v4u32*>(p.xh + xoff + k0);
-        q.xl0 = *reinterpret_cast<const v4u32*>(p.xl + xoff + k0);
+        if constexpr (XV == 0) {
+            const v2u32 h2 = *reinterpret_cast<const v2u32*>(p.xh + xoff + k0);
+            const v2u32 l2 = *reinterpret_cast<const v2u32*>(p.xl + xoff + k0);
+            q.xh0 = v4u32{h2[0], h2[1], 0u, 0u};
+            q.xl0 = v4u32{l2[0], l2[1], 0u, 0u};
+        } else {
+            q.xh0 = *reinterpret_cast<const v4u32*>(p.xh + xoff + k0);
+            q.xl0 = *reinterpret_cast<const v4u32*>(p.xl + xoff + k0);
+        }
         if constexpr (XV == 2) {
             q.xh1 = *reinterpret_cast<const v4u32*>(p.xh + xoff + k0 + 8u);
             q.xl1 = *reinterpret_cast<const v4u32*>(p.xl + xoff + k0 + 8u);
@@ -729,6 +737,13 @@ __global__ __launch_bounds__(256, 2) void pf_gemm2_kernel(PfGemm2Params p) {
         q.sc = *reinterpret_cast<const v4u32*>(scp + (uint64_t)ks * 128u);
     };
     auto store_x = [&](const Slice& q, int buf) {
+        if constexpr (XV == 0) {
+            // half a 16-byte chunk: thread xq fills halves (xq % 2) 4 .. + 3 of chunk xq / 2
+            const uint32_t xo = xr * XS + ((xq / 2u) ^ ((xr >> 1) & 3u)) * 8u + (xq % 2u) * 4u;
+            *reinterpret_cast<v2u32*>(&xs[buf][0][xo]) = v2u32{q.xh0[0], q.xh0[1]};
+            *reinterpret_cast<v2u32*>(&xs[buf][1][xo]) = v2u32{q.xl0[0], q.xl0[1]};
+            return;
+        }
         const uint32_t xsw = (xr >> 1) & 3u;
         const uint32_t xc0 = xr * XS + ((xq * XV) ^ xsw) * 8u, xc1 = xr * XS + ((xq * XV + 1u) ^ xsw) * 8u;
         *reinterpret_cast<v4u32*>(&xs[buf][0][xc0]) = q.xh0;
