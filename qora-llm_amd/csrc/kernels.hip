@@ -620,8 +620,7 @@ hipError_t launch_pf_pack_q4(const uint8_t* w, const uint16_t* scales, const int
     return hipGetLastError();
 }
 
-// 64-token tiles (three blocks per CU; 128-token tiles, two per CU, measured
-// 2.7% slower over a 512-token prefill), then the K split.
+// Tile height (32 or 64 tokens), then the K split.
 PfGemm2Shape pf_gemm2_shape(uint32_t T, uint32_t k, uint32_t ntot, int cus) {
     PfGemm2Shape sh{};
     const uint32_t steps = k / 32u;
@@ -634,10 +633,7 @@ PfGemm2Shape pf_gemm2_shape(uint32_t T, uint32_t k, uint32_t ntot, int cus) {
     sh.bm = 64u;
     if (k <= 4096u && (uint64_t)(ntot / 128u) * ((T + 63u) / 64u) < 2u * cu) sh.bm = 32u;
     const char* eb = std::getenv("QORA_HIP_PF_BM");
-    if (eb && *eb) {
-        const int v = std::atoi(eb);
-        sh.bm = v == 32 ? 32u : v == 64 ? 64u : 128u;
-    }
+    if (eb && *eb) sh.bm = std::atoi(eb) == 32 ? 32u : 64u;     // tuning and tests: force 32 or 64
     const uint64_t tiles = std::max<uint64_t>(1, (uint64_t)(ntot / 128u) * ((T + sh.bm - 1) / sh.bm));
     // K is split only when the tiles leave the block slots partly empty (two
     // per CU; three for the lighter 32-token blocks): beyond that a split's
@@ -681,8 +677,7 @@ hipError_t launch_pf_gemm2(uint32_t bm, const PfGemm2Params& p, hipStream_t stre
     }
     if (nb * 128u != p.ntot) return hipErrorInvalidValue;
     const dim3 grid(nb, (p.T + bm - 1) / bm, p.splits);
-    if (bm == 128) hipLaunchKernelGGL((pf_gemm2_kernel<128>), grid, dim3(256), 0, stream, p);
-    else if (bm == 64) hipLaunchKernelGGL((pf_gemm2_kernel<64>), grid, dim3(256), 0, stream, p);
+    if (bm == 64) hipLaunchKernelGGL((pf_gemm2_kernel<64>), grid, dim3(256), 0, stream, p);
     else if (bm == 32) hipLaunchKernelGGL((pf_gemm2_kernel<32>), grid, dim3(256), 0, stream, p);
     else return hipErrorInvalidValue;
     if (p.splits > 1 && reduce) {

@@ -676,13 +676,13 @@ __global__ __launch_bounds__(256, 2) void pf_gemm2_kernel(PfGemm2Params p) {
     constexpr int BN = 128, KC = 32;
     // LDS rows of 64 B (32 halves, no padding); the 16-byte chunk c of row r
     // sits at chunk c ^ ((r >> 1) & 3), which leaves the fragment reads and the
-    // x' stores (two or four threads a row) free of bank conflicts
+    // x' stores (four or eight threads a row) free of bank conflicts
     constexpr int XS = KC;
     constexpr int TM = BM / 16, TN = 2;
-    constexpr int XT = 256 / BM;                    // threads per x' row (8, 4 or 2)
-    constexpr int XH = KC / XT;                     // halves of a row per thread (4, 8 or 16)
-    constexpr int XV = XH / 8;                      // 16-byte loads per part (0: one 8-byte load, 1 or 2)
-    static_assert(BM == 32 || BM == 64 || BM == 128, "32-, 64- or 128-token tiles");
+    constexpr int XT = 256 / BM;                    // threads per x' row (8 or 4)
+    constexpr int XH = KC / XT;                     // halves of a row per thread (4 or 8)
+    constexpr int XV = XH / 8;                      // 16-byte loads per part (0: one 8-byte load, or 1)
+    static_assert(BM == 32 || BM == 64, "32- or 64-token tiles");
     __shared__ __align__(16) _Float16 xs[2][2][BM * XS];
     kernarg_warm(p);
 
@@ -712,8 +712,7 @@ __global__ __launch_bounds__(256, 2) void pf_gemm2_kernel(PfGemm2Params p) {
 
     // (native vector types: the compiler keeps these in registers)
     struct Slice {
-        v4u32 xh0, xh1, xl0, xl1;                   // x' pieces (xh1, xl1: 128-token tiles only;
-                                                    // 32-token tiles use the first two words)
+        v4u32 xh0, xl0;                             // x' pieces (32-token tiles use the first two words)
         v2u32 wq;
         v4u32 sc;                                   // 8 binary16 s', rows 8 kq .. + 7 (pairs)
     };
@@ -728,10 +727,6 @@ __global__ __launch_bounds__(256, 2) void pf_gemm2_kernel(PfGemm2Params p) {
             q.xh0 = *reinterpret_cast<const v4u32*>(p.xh + xoff + k0);
             q.xl0 = *reinterpret_cast<const v4u32*>(p.xl + xoff + k0);
         }
-        if constexpr (XV == 2) {
-            q.xh1 = *reinterpret_cast<const v4u32*>(p.xh + xoff + k0 + 8u);
-            q.xl1 = *reinterpret_cast<const v4u32*>(p.xl + xoff + k0 + 8u);
-        }
         const uint32_t ks = k0 / 32u;
         q.wq = *reinterpret_cast<const v2u32*>(wqp + (uint64_t)ks * 256u);
         q.sc = *reinterpret_cast<const v4u32*>(scp + (uint64_t)ks * 128u);
@@ -744,14 +739,9 @@ __global__ __launch_bounds__(256, 2) void pf_gemm2_kernel(PfGemm2Params p) {
             *reinterpret_cast<v2u32*>(&xs[buf][1][xo]) = v2u32{q.xl0[0], q.xl0[1]};
             return;
         }
-        const uint32_t xsw = (xr >> 1) & 3u;
-        const uint32_t xc0 = xr * XS + ((xq * XV) ^ xsw) * 8u, xc1 = xr * XS + ((xq * XV + 1u) ^ xsw) * 8u;
+        const uint32_t xc0 = xr * XS + (xq ^ ((xr >> 1) & 3u)) * 8u;
         *reinterpret_cast<v4u32*>(&xs[buf][0][xc0]) = q.xh0;
         *reinterpret_cast<v4u32*>(&xs[buf][1][xc0]) = q.xl0;
-        if constexpr (XV == 2) {
-            *reinterpret_cast<v4u32*>(&xs[buf][0][xc1]) = q.xh1;
-            *reinterpret_cast<v4u32*>(&xs[buf][1][xc1]) = q.xl1;
-        }
     };
     // wh, wl of the lane's two columns, two rows per binary16 pair: the B
     // fragments (k = 8 kq + b, column li) of tiles 0 and 1

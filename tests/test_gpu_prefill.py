@@ -214,6 +214,25 @@ def test_gemm_loop_modes_bit_identical(ctx, pkg, monkeypatch, k, n, T):
     assert np.array_equal(y0, y1)
 
 
+@pytest.mark.parametrize("k,n,T", [(2048, 3072, 200), (11008, 2048, 77), (512, 1024, 33)])
+def test_gemm2_tile_heights_bit_identical(ctx, pkg, monkeypatch, k, n, T):
+    """32- and 64-token tiles of the packed-weight GEMM issue the same products
+    per output element in the same order (K unsplit in both)."""
+    print(f"case gemm2 tile heights k={k} n={n} T={T}", flush=True)
+    packed, scales = pkg.synth_q4(36, k + n, k, n)
+    x = (rng(T + 5).standard_normal((T, k)) * 2).astype(np.float32)
+    wid = ctx.upload(pkg.Weight(k=k, n=n, packed=packed, scales=scales))
+    monkeypatch.setenv("QORA_HIP_PF_SPLITS", "1")
+    with device(ctx) as d:
+        monkeypatch.setenv("QORA_HIP_PF_BM", "64")
+        y64 = _gemm(ctx, d, wid, x, T, n)
+        monkeypatch.setenv("QORA_HIP_PF_BM", "32")
+        y32 = _gemm(ctx, d, wid, x, T, n)
+    assert np.array_equal(y32, y64)
+    W = dequant_np(packed, scales, k, n)
+    assert rel_err(y32, x.astype(np.float64) @ W) <= TRUTH_TOL
+
+
 @pytest.mark.parametrize("hidden,inter,heads", [(2048, 11008, 16), (512, 3008, 4)])
 def test_row_producers_register_and_loop_bit_identical(ctx, pkg, monkeypatch, hidden, inter, heads):
     """The register-cached row producers (rows up to 2048, 4096 and 12288 wide)
