@@ -676,7 +676,7 @@ __global__ __launch_bounds__(256, 2) void pf_gemm2_kernel(PfGemm2Params p) {
     constexpr int BN = 128, KC = 32;
     // LDS rows of 64 B (32 halves, no padding); the 16-byte chunk c of row r
     // sits at chunk c ^ ((r >> 1) & 3), which leaves the fragment reads and the
-    // x' stores (four or eight threads a row) free of bank conflicts
+    // 64-token tiles' x' stores (four threads a row) free of bank conflicts
     constexpr int XS = KC;
     constexpr int TM = BM / 16, TN = 2;
     constexpr int XT = 256 / BM;                    // threads per x' row (8 or 4)
