@@ -55,17 +55,6 @@ __device__ __forceinline__ float4 sel4(bool c, float4 a, float4 b) {
     return make_float4(c ? a.x : b.x, c ? a.y : b.y, c ? a.z : b.z, c ? a.w : b.w);
 }
 
-// Sum of v over lanes l, l ^ 16, l ^ 32 and l ^ 48 (the four row slots of a
-// wave), the same bits in all four: each lane-swap instruction leaves lane l's
-// partner value in one of its two results, so their sum is v[l] + v[l ^ 16]
-// (then ^ 32) in every lane.
-__device__ __forceinline__ float sum_row_slots(float v) {
-    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
-    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
-}
-
 template <int HD, bool F16KV, int NP>
 __global__ __launch_bounds__(kFusedWaves * kWave) void gemv_q4m_attn_kernel(AttnOParams ap) {
     constexpr int GW = 1, NW = 4;

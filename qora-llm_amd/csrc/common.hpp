@@ -199,6 +199,42 @@ __device__ __forceinline__ float row16_sum(float v) {
     return v;
 }
 
+// Sum of v over lanes l, l ^ 16, l ^ 32 and l ^ 48 (the four row slots of a
+// wave), the same bits in all four: each lane-swap instruction leaves lane l's
+// partner value in one of its two results, so their sum is v[l] + v[l ^ 16]
+// (then ^ 32) in every lane.
+__device__ __forceinline__ float sum_row_slots(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+// The same for the maximum.
+__device__ __forceinline__ float max_row_slots(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+// Maximum over each aligned group of N lanes (N = 16: a row; 32: two rows),
+// every lane of the group receiving it: the row16_sum butterfly with fmaxf,
+// then the lane-swap of rows l and l ^ 16. All 64 lanes must be active.
+template <int N>
+__device__ __forceinline__ float group_max(float v) {
+    static_assert(N == 16 || N == 32, "16- or 32-lane groups");
+    v = fmaxf(v, dpp_f32<0xB1>(v));    // quad_perm [1,0,3,2]
+    v = fmaxf(v, dpp_f32<0x4E>(v));    // quad_perm [2,3,0,1]
+    v = fmaxf(v, dpp_f32<0x141>(v));   // row_half_mirror
+    v = fmaxf(v, dpp_f32<0x140>(v));   // row_mirror
+    if constexpr (N == 32) {
+        const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    }
+    return v;
+}
+
 __device__ __forceinline__ float wave_max(float v) {
     v = fmaxf(v, dpp_f32<0xB1>(v));
     v = fmaxf(v, dpp_f32<0x4E>(v));

@@ -1140,8 +1140,7 @@ __global__ __launch_bounds__(256, 2) void pf_attn_mfma_kernel(PrefillAttnParams 
 #pragma unroll
             for (int b8 = 0; b8 < 8; ++b8) amax = fmaxf(amax, fabsf(qv[st][b8]));
         }
-        amax = fmaxf(amax, __shfl_xor(amax, 16, kWave));
-        amax = fmaxf(amax, __shfl_xor(amax, 32, kWave));
+        amax = max_row_slots(amax);
         const int eq = pf_row_exponent(amax);
         sq = ldexpf(1.0f, eq);
 #pragma unroll
@@ -1155,6 +1154,9 @@ __global__ __launch_bounds__(256, 2) void pf_attn_mfma_kernel(PrefillAttnParams 
             }
     }
     const uint32_t qpos = p.pos0 + wq0 + li;        // this lane's query position
+    // scores in log2 units: dot * 2^(e_k + e_q) * scale * log2(e), so the
+    // softmax runs on v_exp_f32 (2^x) directly; m leaves as m ln 2
+    const float qf = sq * p.scale * 1.4426950408889634f;
     float m = -INFINITY, l = 0.f;
     f32x4v o[OC];
 #pragma unroll
@@ -1167,7 +1169,42 @@ __global__ __launch_bounds__(256, 2) void pf_attn_mfma_kernel(PrefillAttnParams 
     constexpr int VE = HD * KT / 4 / 256;           // V key quads per thread
     float4 kreg[KE];
     float vreg[VE][4];
+    // Cache rows addressed from the KV head's base (uniform) by 32-bit byte
+    // offsets row * row_bytes + column bytes (24-bit multiplies) when every
+    // offset of the block fits; 64-bit element indexes otherwise.
+    constexpr uint32_t ES = F16KV ? 2u : 4u;
+    const bool off32 = last < (1u << 24) && cps * ES < (1u << 24) &&
+                       ((uint64_t)last + 1u) * cps * ES + (uint64_t)HD * ES < (1ull << 31);
+    const char* kbase = reinterpret_cast<const char*>(p.kc) + (uint64_t)kvh * chs * ES;
+    const char* vbase = reinterpret_cast<const char*>(p.vc) + (uint64_t)kvh * chs * ES;
+    const uint32_t rowb = (uint32_t)(cps * ES);
     auto load_tile = [&](uint32_t k0) {
+        if (off32) {
+#pragma unroll
+            for (int u = 0; u < KE; ++u) {
+                const uint32_t e = t + 256u * (uint32_t)u;
+                const uint32_t r = e / (HD / 4), c4 = e % (HD / 4);
+                const uint32_t o = __umul24(min(k0 + r, last), rowb) + 4u * c4 * ES;
+                if constexpr (F16KV) {
+                    const uint2 a = *reinterpret_cast<const uint2*>(kbase + o);
+                    kreg[u] = make_float4(__uint_as_float(a.x), __uint_as_float(a.y), 0.f, 0.f);   // raw words
+                } else {
+                    kreg[u] = *reinterpret_cast<const float4*>(kbase + o);
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < VE; ++u) {
+                const uint32_t e = t + 256u * (uint32_t)u;
+                const uint32_t d = e % HD, quad = e / HD;
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr) {
+                    const uint32_t o = __umul24(min(k0 + 4u * quad + (uint32_t)rr, last), rowb) + d * ES;
+                    if constexpr (F16KV) vreg[u][rr] = __uint_as_float((uint32_t)*reinterpret_cast<const uint16_t*>(vbase + o));
+                    else vreg[u][rr] = *reinterpret_cast<const float*>(vbase + o);
+                }
+            }
+            return;
+        }
 #pragma unroll
         for (int u = 0; u < KE; ++u) {
             const uint32_t e = t + 256u * (uint32_t)u;
@@ -1206,9 +1243,7 @@ __global__ __launch_bounds__(256, 2) void pf_attn_mfma_kernel(PrefillAttnParams 
                 kv = make_float4(h2f((uint16_t)(ax & 0xFFFFu)), h2f((uint16_t)(ax >> 16)),
                                  h2f((uint16_t)(ay & 0xFFFFu)), h2f((uint16_t)(ay >> 16)));
             }
-            float amax = fmaxf(fmaxf(fabsf(kv.x), fabsf(kv.y)), fmaxf(fabsf(kv.z), fabsf(kv.w)));
-#pragma unroll
-            for (int w = 1; w < HD / 4; w *= 2) amax = fmaxf(amax, __shfl_xor(amax, w, kWave));
+            const float amax = group_max<HD / 4>(fmaxf(fmaxf(fabsf(kv.x), fabsf(kv.y)), fmaxf(fabsf(kv.z), fabsf(kv.w))));
             const int ek = pf_row_exponent(amax);
             const float kin[4] = {ldexpf(kv.x, -ek), ldexpf(kv.y, -ek), ldexpf(kv.z, -ek), ldexpf(kv.w, -ek)};
             _Float16 kh[4], kl[4];
@@ -1276,30 +1311,27 @@ __global__ __launch_bounds__(256, 2) void pf_attn_mfma_kernel(PrefillAttnParams 
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const uint32_t kp = k0 + 16u * c + 4u * g4 + (uint32_t)r;
-                // the dot at its own scale (times 2^(e_k + e_q), exact), then the softmax scale
-                sv[c][r] = kp <= qpos ? (sacc[c][r] * (kfa[r] * sq)) * p.scale : -INFINITY;
+                sv[c][r] = kp <= qpos ? sacc[c][r] * (kfa[r] * qf) : -INFINITY;
                 mx = fmaxf(mx, sv[c][r]);
             }
         }
-        mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+        mx = max_row_slots(mx);
         const float m_new = fmaxf(m, mx);
         const float mref = m_new == -INFINITY ? 0.f : m_new;   // a query with no visible key yet
-        const float f = expf(m - mref);
+        const float f = __builtin_amdgcn_exp2f(m - mref);
         float sum = 0.f;
         half8v ph[2], pl[2];
 #pragma unroll
         for (int c = 0; c < 4; ++c)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const float e = expf(sv[c][r] - mref);
+                const float e = __builtin_amdgcn_exp2f(sv[c][r] - mref);
                 sum += e;
                 const _Float16 eh = (_Float16)e;
                 ph[c / 2][(c % 2) * 4 + r] = eh;
                 pl[c / 2][(c % 2) * 4 + r] = (_Float16)(e - (float)eh);
             }
-        sum += __shfl_xor(sum, 16, kWave);
-        sum += __shfl_xor(sum, 32, kWave);
+        sum = sum_row_slots(sum);
         l = l * f + sum;
         m = m_new;
         // ---- O^T = O^T f + V^T P^T: dim tiles of 16, two half tiles of 32 keys ----
@@ -1334,7 +1366,7 @@ __global__ __launch_bounds__(256, 2) void pf_attn_mfma_kernel(PrefillAttnParams 
         for (int c = 0; c < OC; ++c)
             *reinterpret_cast<float4*>(&po[row * HD + 16 * c + 4 * g4]) = make_float4(o[c][0], o[c][1], o[c][2], o[c][3]);
         if (g4 == 0) {
-            pml[row * 2u] = m;
+            pml[row * 2u] = m * 0.6931471805599453f;   // natural units for the merge
             pml[row * 2u + 1u] = l;
         }
         return;
