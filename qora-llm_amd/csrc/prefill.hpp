@@ -771,7 +771,12 @@ __global__ __launch_bounds__(256, 2) void pf_gemm2_kernel(PfGemm2Params p) {
     for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = f32x4v{0.f, 0.f, 0.f, 0.f};
+    // A wave raises its issue priority while it reads its fragments and issues
+    // its MFMAs (64-token tiles: 3-4% faster on the large shapes, same output;
+    // no effect on 32-token tiles), so the matrix cores are fed ahead of the
+    // other waves' dequantisation.
     auto compute = [&](int buf, const half8v* bh, const half8v* bl) {
+        if constexpr (BM == 64) __builtin_amdgcn_s_setprio(1);
         half8v ah[TM], al[TM];
 #pragma unroll
         for (int i = 0; i < TM; ++i) {
@@ -788,6 +793,7 @@ __global__ __launch_bounds__(256, 2) void pf_gemm2_kernel(PfGemm2Params p) {
                 acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], bh[j], acc[i][j], 0, 0, 0);
                 acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], bl[j], acc[i][j], 0, 0, 0);
             }
+        if constexpr (BM == 64) __builtin_amdgcn_s_setprio(0);
     };
 
     // global loads run two steps ahead of the matrix cores: slice se holds the
