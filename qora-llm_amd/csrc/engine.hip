@@ -1183,8 +1183,12 @@ struct PfDeferred {
 // defer: when set and the launch splits K, with the segments' rows side by
 // side in one output (row stride ldy == ntot), the partials are left for the
 // caller, who sums them in split order (and adds them when accumulating)
+// swiglu: when set (gate, up: two segments of equal width, not accumulated)
+// and the launch runs K unsplit, the GEMM writes h = SiLU(gate) * up to
+// ys[0] (row stride n) instead of gate and up, and *swiglu stays true;
+// otherwise it is cleared and gate and up are written as usual.
 int pf_gemm2(qora_hip_ctx* c, uint32_t l, std::initializer_list<int> js, uint32_t T, std::initializer_list<float*> ys,
-             uint32_t ldy, bool accumulate, PfDeferred* defer = nullptr) {
+             uint32_t ldy, bool accumulate, PfDeferred* defer = nullptr, bool* swiglu = nullptr) {
     ModelState& m = c->m;
     PfGemm2Params g{};
     g.xh = m.d_pf_xh;
@@ -1218,6 +1222,13 @@ int pf_gemm2(qora_hip_ctx* c, uint32_t l, std::initializer_list<int> js, uint32_
     g.splits = sh.splits;
     g.kper = sh.kper;
     g.part = m.d_pf_part;
+    if (swiglu) {
+        *swiglu = *swiglu && g.nseg == 2 && g.seg[0].n == g.seg[1].n && g.splits == 1 && !accumulate;
+        if (*swiglu) {
+            g.swiglu = 1;
+            g.seg[0].ldy = g.seg[0].n;
+        }
+    }
     bool side = ldy == g.ntot;
     for (int i = 0; i < g.nseg; ++i) side = side && g.seg[i].y == g.seg[0].y + (size_t)g.seg[i].nb0 * 128u;
     const bool leave = defer && g.splits > 1 && side;
@@ -1313,8 +1324,10 @@ int prefill_batched(qora_hip_ctx* c, size_t n, float* logits, uint32_t* argmax) 
             nr.splits = od.splits;
             nr.part_stride = od.stride;
             HIP_TRY(c, launch_pf_rows(PF_ROW_RMSNORM, nr, T, s));
+            bool swiglu = m.pf2;           // SiLU(g) * u formed by the gate|up GEMM when it runs unsplit
             if (m.pf2) {
-                if (int rc = pf_gemm2(c, l, {4, 5}, T, {m.d_pf_gu, m.d_pf_gu + m.inter}, 2 * m.inter, false))
+                if (int rc = pf_gemm2(c, l, {4, 5}, T, {m.d_pf_gu, m.d_pf_gu + m.inter}, 2 * m.inter, false, nullptr,
+                                      &swiglu))
                     return rc;
             } else {
                 if (int rc = pf_gemm(c, l, 4, T, m.d_pf_gu, 2 * m.inter, false)) return rc;
@@ -1322,8 +1335,8 @@ int prefill_batched(qora_hip_ctx* c, size_t n, float* logits, uint32_t* argmax) 
             }
             PrefillRowParams gr{};
             gr.x = m.d_pf_gu;
-            gr.u = m.d_pf_gu + m.inter;
-            gr.ld = 2 * m.inter;
+            gr.u = swiglu ? nullptr : m.d_pf_gu + m.inter;
+            gr.ld = swiglu ? m.inter : 2 * m.inter;
             gr.n = m.inter;
             gr.xh = m.d_pf_xh;
             gr.xl = m.d_pf_xl;

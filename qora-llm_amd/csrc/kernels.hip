@@ -676,6 +676,8 @@ hipError_t launch_pf_gemm2(uint32_t bm, const PfGemm2Params& p, hipStream_t stre
         nb += p.seg[i].n / 128;
     }
     if (nb * 128u != p.ntot) return hipErrorInvalidValue;
+    if (p.swiglu && (p.nseg != 2 || p.seg[0].n != p.seg[1].n || p.splits != 1 || !p.seg[0].y || p.seg[0].accumulate))
+        return hipErrorInvalidValue;
     const dim3 grid(nb, (p.T + bm - 1) / bm, p.splits);
     if (bm == 64) hipLaunchKernelGGL((pf_gemm2_kernel<64>), grid, dim3(256), 0, stream, p);
     else if (bm == 32) hipLaunchKernelGGL((pf_gemm2_kernel<32>), grid, dim3(256), 0, stream, p);

@@ -185,6 +185,10 @@ struct PfGemm2Params {
     // writes part[z][T][ntot]; pf_splitk_reduce2_kernel sums them in split order
     uint32_t splits, kper;
     float* part;
+    // SwiGLU pairing (gate|up): seg[0] = gate, seg[1] = up, both n wide, K
+    // unsplit; column block b computes gate and up columns [64 b, 64 b + 64)
+    // and writes h = SiLU(gate) * up to seg[0].y (row stride seg[0].ldy)
+    int swiglu;
 };
 
 struct PrefillAttnParams {

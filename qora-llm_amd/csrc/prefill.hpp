@@ -211,23 +211,24 @@ __global__ __launch_bounds__(256) void pf_split_kernel(PrefillRowParams p) {
 
 // SwiGLU (gemv.rs:1160-1166): v = (g / (1 + exp(-g))) * u over the gate and up
 // rows, then split (the down projection's input).
+// p.u null: the rows already hold SiLU(g) * u (the gate|up GEMM's SwiGLU
+// pairing), only split.
 __global__ __launch_bounds__(256) void pf_silu_split_kernel(PrefillRowParams p) {
     __shared__ float red[4];
     const uint32_t t = blockIdx.x;
+    const bool swiglu = p.u != nullptr;
     const float* g = p.x + (uint64_t)t * p.ld;
-    const float* u = p.u + (uint64_t)t * p.ld;
-    float amax = 0.f;
-    for (uint32_t j = threadIdx.x; j < p.n; j += 256) {
+    const float* u = swiglu ? p.u + (uint64_t)t * p.ld : g;
+    auto h = [&](uint32_t j) {
         const float gv = g[j];
-        amax = fmaxf(amax, fabsf((gv / (1.0f + expf(-gv))) * u[j]));
-    }
+        return swiglu ? (gv / (1.0f + expf(-gv))) * u[j] : gv;
+    };
+    float amax = 0.f;
+    for (uint32_t j = threadIdx.x; j < p.n; j += 256) amax = fmaxf(amax, fabsf(h(j)));
     const int e = pf_row_exponent(pf_block_max<256>(amax, red));
     _Float16* xh = reinterpret_cast<_Float16*>(p.xh) + (uint64_t)t * p.n;
     _Float16* xl = reinterpret_cast<_Float16*>(p.xl) + (uint64_t)t * p.n;
-    for (uint32_t j = threadIdx.x; j < p.n; j += 256) {
-        const float gv = g[j];
-        pf_split((gv / (1.0f + expf(-gv))) * u[j], e, xh + j, xl + j);
-    }
+    for (uint32_t j = threadIdx.x; j < p.n; j += 256) pf_split(h(j), e, xh + j, xl + j);
     if (threadIdx.x == 0) p.xe[t] = e;
 }
 
@@ -352,20 +353,24 @@ template <int NT, int EPT>
 __global__ __launch_bounds__(NT) void pf_silu_split_reg_kernel(PrefillRowParams p) {
     __shared__ float red[NT / kWave];
     const uint32_t t = blockIdx.x;
+    // p.u null: the rows already hold SiLU(g) * u (the gate|up GEMM's SwiGLU
+    // pairing), only split
+    const bool swiglu = p.u != nullptr;
     const float* g = p.x + (uint64_t)t * p.ld;
-    const float* u = p.u + (uint64_t)t * p.ld;
+    const float* u = swiglu ? p.u + (uint64_t)t * p.ld : g;
     float gv[EPT], uv[EPT];
 #pragma unroll
     for (int i = 0; i < EPT; ++i) {
         const uint32_t j = min(threadIdx.x + (uint32_t)NT * (uint32_t)i, p.n - 1u);
         gv[i] = g[j];
-        uv[i] = u[j];
+        if (swiglu) uv[i] = u[j];
     }
     float amax = 0.f;
 #pragma unroll
     for (int i = 0; i < EPT; ++i) {
         const uint32_t j = threadIdx.x + (uint32_t)NT * (uint32_t)i;
-        gv[i] = j < p.n ? (gv[i] / (1.0f + expf(-gv[i]))) * uv[i] : 0.f;
+        const float h = swiglu ? (gv[i] / (1.0f + expf(-gv[i]))) * uv[i] : gv[i];
+        gv[i] = j < p.n ? h : 0.f;
         amax = fmaxf(amax, fabsf(gv[i]));
     }
     const int e = pf_row_exponent(pf_block_max<NT>(amax, red));
@@ -691,11 +696,19 @@ __global__ __launch_bounds__(256, 2) void pf_gemm2_kernel(PfGemm2Params p) {
     const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
     const uint32_t nb = blockIdx.x;
     // the segment of this column block (wave-uniform: whole-struct selects, no
-    // indexing of the argument block)
+    // indexing of the argument block); with SwiGLU pairing, waves 0, 1 take
+    // gate and waves 2, 3 up, each the 32-column group grp of packed block
+    // lnb (h columns 64 nb + 32 (wave % 2) ..)
+    const bool pair = p.swiglu != 0;
     PfGemm2Seg sg = p.seg[0];
-    if (p.nseg > 1 && nb >= p.seg[1].nb0) sg = p.seg[1];
-    if (p.nseg > 2 && nb >= p.seg[2].nb0) sg = p.seg[2];
-    const uint32_t lnb = nb - sg.nb0;               // column block within the segment
+    if (pair) {
+        if (wave >= 2) sg = p.seg[1];
+    } else {
+        if (p.nseg > 1 && nb >= p.seg[1].nb0) sg = p.seg[1];
+        if (p.nseg > 2 && nb >= p.seg[2].nb0) sg = p.seg[2];
+    }
+    const uint32_t lnb = pair ? nb / 2u : nb - sg.nb0;  // column block within the segment
+    const uint32_t grp = pair ? 2u * (nb % 2u) + (uint32_t)wave % 2u : (uint32_t)wave;   // 32-column group in it
     const uint32_t m0 = blockIdx.y * (uint32_t)BM;
     const uint32_t K = p.k, KS = K / 32u;
     const uint32_t kb = blockIdx.z * p.kper;
@@ -707,8 +720,8 @@ __global__ __launch_bounds__(256, 2) void pf_gemm2_kernel(PfGemm2Params p) {
     // weights: lane (kq, li) of wave w holds rows 8 kq .. 8 kq + 7 of columns
     // 32 w + li and 32 w + 16 + li, with their 8 scales
     const uint32_t li = (uint32_t)lane % 16u, kq = (uint32_t)lane / 16u;
-    const uint2* wqp = sg.wq + (uint64_t)lnb * KS * 256u + 64u * kq + 16u * (uint32_t)wave + li;
-    const uint16_t* scp = sg.sc + ((uint64_t)lnb * KS * 4u + (uint32_t)wave) * 32u + 8u * kq;
+    const uint2* wqp = sg.wq + (uint64_t)lnb * KS * 256u + 64u * kq + 16u * grp + li;
+    const uint16_t* scp = sg.sc + ((uint64_t)lnb * KS * 4u + grp) * 32u + 8u * kq;
 
     // (native vector types: the compiler keeps these in registers)
     struct Slice {
@@ -830,6 +843,50 @@ __global__ __launch_bounds__(256, 2) void pf_gemm2_kernel(PfGemm2Params p) {
             __syncthreads();
             compute(1, bhO, blO);
         }
+    }
+
+    if (pair) {
+        // gate waves leave their values in LDS (the x' buffers, free once
+        // every wave is past its last step); up waves form h = SiLU(g) * u
+        // (gemv.rs:1160-1166, the arithmetic of pf_silu_split_kernel)
+        float* gt = reinterpret_cast<float*>(&xs[0][0][0]);     // [BM][64]
+        static_assert(sizeof(xs) >= (size_t)BM * 64u * 4u, "gate tile fits the x' buffers");
+        __syncthreads();
+        if (wave < 2) {
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j) {
+                    const uint32_t c = lnb * (uint32_t)BN + grp * 32u + (uint32_t)j * 16u + li;
+                    const int fg = (int)sg.wf[c / 32u];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const uint32_t rl = (uint32_t)i * 16u + kq * 4u + (uint32_t)r;
+                        const uint32_t row = min(m0 + rl, p.T - 1u);
+                        gt[rl * 64u + (uint32_t)wave * 32u + (uint32_t)j * 16u + li] = ldexpf(acc[i][j][r], p.xe[row] + fg);
+                    }
+                }
+        }
+        __syncthreads();
+        if (wave < 2) return;
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                const uint32_t c = lnb * (uint32_t)BN + grp * 32u + (uint32_t)j * 16u + li;
+                const int fg = (int)sg.wf[c / 32u];
+                const uint32_t hc = 64u * nb + ((uint32_t)wave - 2u) * 32u + (uint32_t)j * 16u + li;   // h column
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const uint32_t rl = (uint32_t)i * 16u + kq * 4u + (uint32_t)r;
+                    const uint32_t row = m0 + rl;
+                    if (row >= p.T) continue;
+                    const float u = ldexpf(acc[i][j][r], p.xe[row] + fg);
+                    const float g = gt[rl * 64u + ((uint32_t)wave - 2u) * 32u + (uint32_t)j * 16u + li];
+                    p.seg[0].y[(uint64_t)row * p.seg[0].ldy + hc] = (g / (1.0f + expf(-g))) * u;
+                }
+            }
+        return;
     }
 
     // epilogue: y = acc * 2^(e_t + f_g), stored, added, or kept as this split's partial
