@@ -787,9 +787,13 @@ __global__ __launch_bounds__(256, 2) void pf_gemm2_kernel(PfGemm2Params p) {
     // A wave raises its issue priority while it reads its fragments and issues
     // its MFMAs (64-token tiles: 3-4% faster on the large shapes, same output;
     // no effect on 32-token tiles), so the matrix cores are fed ahead of the
-    // other waves' dequantisation.
+    // other waves' dequantisation; the compiler's MFMA/VALU interleave
+    // strategy 0 adds ~1.7% there.
     auto compute = [&](int buf, const half8v* bh, const half8v* bl) {
-        if constexpr (BM == 64) __builtin_amdgcn_s_setprio(1);
+        if constexpr (BM == 64) {
+            __builtin_amdgcn_s_setprio(1);
+            __builtin_amdgcn_iglp_opt(0);
+        }
         half8v ah[TM], al[TM];
 #pragma unroll
         for (int i = 0; i < TM; ++i) {
