@@ -288,7 +288,8 @@ int qora_hip_argmax(qora_hip_ctx* ctx, const float* logits, uint64_t n, int32_t*
  *   q4  : v = U{-7..7}, stored q = v + 8; scale = f16(|z| * 0.02 / 7)
  *   f16 : f16(z * std)
  *   f32 : z
- * z is a sum-of-four-uniforms normal approximation (exactly reproducible). */
+ * z is a Box-Muller normal draw from two 32-bit uniforms, with ln and cos
+ * evaluated from correctly rounded float64 operations (exactly reproducible). */
 void qora_synth_q4(uint64_t seed, uint64_t tensor_id, uint64_t k, uint64_t n, uint8_t* packed,
                    uint16_t* scales);
 void qora_synth_f16(uint64_t seed, uint64_t tensor_id, uint64_t count, float stddev, uint16_t* out);

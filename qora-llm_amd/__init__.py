@@ -527,9 +527,15 @@ class HipBackend:
                       ctypes.cast(in_ptrs, ctypes.c_void_p).value, ctypes.cast(post_ptrs, ctypes.c_void_p).value,
                       embed_wid, _ptr(weights.final_norm), _ptr(weights.rope_cos), _ptr(weights.rope_sin),
                       weights.rope_cos.size // c.rope_half_dim, _ptr(weights.no_rope_layers), kv_capacity, kv_dtype)
-        ctx.check(ctx.lib.qora_hip_model_init(ctx.h, ctypes.byref(d)), "model_init")
+        self._desc = d
+        self.model_init()
         self.wids = wids.reshape(c.num_layers, 7)
         self.embed_wid = embed_wid
+
+    def model_init(self) -> None:
+        """(Re)builds the device model from the uploaded weights
+        (qora_hip_model_init); the KV cache starts empty."""
+        self.ctx.check(self.ctx.lib.qora_hip_model_init(self.ctx.h, ctypes.byref(self._desc)), "model_init")
 
     def forward_decode_raw(self, token_id: int, want_logits: bool = True):
         """One decode step; returns (logits or None, greedy token)."""

@@ -17,12 +17,13 @@
 
 using namespace qora;
 
+constexpr uint32_t kDefaultKvCapacity = 65536;   // kv_capacity 0 for a model without RoPE layers
+
 // Scratch of the allocation-free GEMV entry (qora_hip_gemv_q4_noalloc): its
 // fixed-point accumulator, one copy on every device the library runs on,
 // held until the process ends. Host code never passes the array's name to
 // a kernel or a copy: it uses the device address that hipGetSymbolAddress
 // returns for the current device (noalloc_scratch below).
-constexpr uint32_t kDefaultKvCapacity = 65536;   // kv_capacity 0 for a model without RoPE layers
 constexpr uint64_t kNoAllocMaxN = 65536;   // outputs; int64 words of the array (512 KiB)
 static __device__ __align__(256) long long scratch[kNoAllocMaxN];
 
@@ -367,7 +368,7 @@ int record_step(qora_hip_ctx* c, bool with_lm_head, uint32_t np) {
 // Attention subgroups per block (1 or 4): by default 4 when a split can hold
 // more than one 32-position pass; QORA_HIP_ATTN_NSG overrides.
 uint32_t attn_nsg(uint32_t max_chunk) {
-    const char* v = std::getenv("QORA_HIP_ATTN_NSG");
+    const char* v = tuning_env("QORA_HIP_ATTN_NSG");
     if (v && *v) return std::atoi(v) > 1 ? 4u : 1u;
     return max_chunk > (uint32_t)kAttnSub ? 4u : 1u;
 }
@@ -654,7 +655,17 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
         free_model(c);
         return fail(c, QORA_HIP_E_INVALID, "RMSNorm input split into more than 64 K slices");
     }
-    m.lm_mfma = m.fmt == FMT_Q4 && lmhead_supported(m.hidden) && !std::getenv("QORA_HIP_LM_ROWDOT");
+    // The fixed-point range guard (params.hpp) holds while an accumulator
+    // takes at most kFixMaxTerms terms between two reads: the residual takes
+    // the o or the down projection's split-K terms, the other accumulators
+    // start from zero.
+    for (const GemvPlan* pl : {&m.pl_qkv, &m.pl_o, &m.pl_gu, &m.pl_down})
+        if (pl->splits > kFixMaxTerms) {
+            free_model(c);
+            return fail(c, QORA_HIP_E_INVALID, "a projection's contraction is split into more than " +
+                                                   std::to_string(kFixMaxTerms) + " K slices");
+        }
+    m.lm_mfma = m.fmt == FMT_Q4 && lmhead_supported(m.hidden) && !tuning_env("QORA_HIP_LM_ROWDOT");
     m.lm_blocks = m.lm_mfma ? lmhead_blocks(m.vocab, c->cus) : rowdot_blocks(m.vocab, m.hidden, c->cus);
     attn_geometry(m.cap, &m.attn_chunk, &m.attn_s_max);
 
@@ -693,7 +704,7 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
         // Cache slots past the current length are read (and skipped) by the
         // attention kernel; they start as zeros, or as NaN bit patterns with
         // QORA_HIP_KV_FILL=nan (a test of that skipping).
-        const char* fill = std::getenv("QORA_HIP_KV_FILL");
+        const char* fill = tuning_env("QORA_HIP_KV_FILL");
         const int byte = (fill && std::strcmp(fill, "nan") == 0) ? 0xFF : 0;
         HIP_TRY(c, hipMemset(m.d_k, byte, (size_t)m.L * m.cap * kvd * kvb));
         HIP_TRY(c, hipMemset(m.d_v, byte, (size_t)m.L * m.cap * kvd * kvb));
@@ -1545,10 +1556,11 @@ extern "C" int qora_hip_graph_destroy(qora_hip_ctx* c, void* graph_exec) {
 
 namespace {
 
-// acc[0:n] (+ acc[n:2n] when paired) += W x, one launch of the model's GEMV
-// kernel with the plain-vector prologue.
-int gemv_acc_entry(qora_hip_ctx* c, int fmt, const void* w0, const void* s0, const void* w1, const void* s1,
-                   const float* x, long long* acc, uint64_t k, uint64_t n, bool paired, void* stream) {
+// Argument checks and launch plan of acc[0:n] (+ acc[n:2n] when paired) +=
+// W x; nothing is launched, so a refused call leaves the device untouched.
+int gemv_acc_prepare(qora_hip_ctx* c, int fmt, const void* w0, const void* s0, const void* w1, const void* s1,
+                     const float* x, long long* acc, uint64_t k, uint64_t n, bool paired, GemvPlan* plan,
+                     GemvParams* params) {
     if (!c) return QORA_HIP_E_INVALID;
     if (!w0 || !x || !acc || (fmt == FMT_Q4 && !s0) || (paired && (!w1 || (fmt == FMT_Q4 && !s1))))
         return fail(c, QORA_HIP_E_INVALID, "null argument");
@@ -1572,6 +1584,18 @@ int gemv_acc_entry(qora_hip_ctx* c, int fmt, const void* w0, const void* s0, con
     p.x = x;
     p.acc = acc;
     apply_plan(pl, &p);
+    *plan = pl;
+    *params = p;
+    return QORA_HIP_OK;
+}
+
+// acc[0:n] (+ acc[n:2n] when paired) += W x, one launch of the model's GEMV
+// kernel with the plain-vector prologue.
+int gemv_acc_entry(qora_hip_ctx* c, int fmt, const void* w0, const void* s0, const void* w1, const void* s1,
+                   const float* x, long long* acc, uint64_t k, uint64_t n, bool paired, void* stream) {
+    GemvPlan pl;
+    GemvParams p{};
+    if (int rc = gemv_acc_prepare(c, fmt, w0, s0, w1, s1, x, acc, k, n, paired, &pl, &p)) return rc;
     HIP_TRY(c, launch_gemv(fmt, pl, p, pick_stream(c, stream)));
     return QORA_HIP_OK;
 }
@@ -1627,9 +1651,15 @@ extern "C" int qora_hip_gemv_q4_noalloc(qora_hip_ctx* c, const void* packed, con
     // the same kernels as qora_hip_gemv_q4, on the device's static scratch
     // instead of the context's grown accumulator: clear (a kernel, not a
     // memset), accumulate, convert
+    // every argument is checked before the first launch: a refused call
+    // writes nothing to the device-wide scratch
+    GemvPlan pl;
+    GemvParams p{};
+    if (int rc = gemv_acc_prepare(c, FMT_Q4, packed, scales, nullptr, nullptr, x, acc, k, n, false, &pl, &p))
+        return rc;
     const hipStream_t s = pick_stream(c, stream);
     HIP_TRY(c, launch_fill_zero(acc, n, s));
-    if (int rc = gemv_acc_entry(c, FMT_Q4, packed, scales, nullptr, nullptr, x, acc, k, n, false, stream)) return rc;
+    HIP_TRY(c, launch_gemv(FMT_Q4, pl, p, s));
     HIP_TRY(c, launch_acc_to_f32(acc, (uint32_t)n, 0, y, s));
     return QORA_HIP_OK;
 }
@@ -2143,8 +2173,23 @@ extern "C" int qora_hip_decode_sample(qora_hip_ctx* c, uint32_t token, const uin
         // nothing of this call stays in flight behind an error
         (void)hipStreamSynchronize(c->stream);
         m.dev_token = -1;
+        return rc;
     }
-    return rc;
+    if (!logits) {
+        // The step's range flag (finish_step reads it when logits are asked
+        // for). sample_device has synchronised the stream, so the step's
+        // argmax_finish_kernel has copied the flag to the mapped word.
+        int32_t bad;
+        if (c->d_h_tok) {
+            bad = reinterpret_cast<volatile int32_t*>(c->h_tok)[1];
+        } else {
+            HIP_TRY(c, hipMemcpyAsync(&c->h_pin[17], m.d_range, 4, hipMemcpyDeviceToHost, c->stream));
+            HIP_TRY(c, hipStreamSynchronize(c->stream));
+            bad = c->h_pin[17];
+        }
+        if (bad) return range_error(c);
+    }
+    return QORA_HIP_OK;
 }
 
 extern "C" int qora_hip_argmax(qora_hip_ctx* c, const float* logits, uint64_t n, int32_t* out, void* stream) {

@@ -14,9 +14,16 @@
 
 namespace qora {
 
-static int env_int(const char* name, int dflt) {
+const char* tuning_env(const char* name) {
+    const char* on = std::getenv("QORA_HIP_TUNING");
+    if (!on || std::strcmp(on, "1") != 0) return nullptr;
     const char* v = std::getenv(name);
-    return (v && *v) ? std::atoi(v) : dflt;
+    return (v && *v) ? v : nullptr;
+}
+
+static int env_int(const char* name, int dflt) {
+    const char* v = tuning_env(name);
+    return v ? std::atoi(v) : dflt;
 }
 
 bool plan_gemv(int fmt, uint32_t k, const uint32_t* seg_groups, int nseg, bool paired, int cus,
@@ -104,6 +111,9 @@ bool plan_gemv_q4m(uint32_t k, const uint32_t* seg_groups, int nseg, bool paired
         }
         pl.kr = kw;
         pl.splits = (k + pl.kr - 1) / pl.kr;
+        // an accumulator takes at most kFixMaxTerms split-K terms between two
+        // reads (the fixed-point range guard, params.hpp)
+        if (pl.splits > kFixMaxTerms) continue;
         if (!have || (best.blocks() < want && pl.blocks() > best.blocks())) {
             best = pl;
             have = true;
@@ -408,7 +418,7 @@ hipError_t launch_attn(const AttnParams& p, hipStream_t stream) {
     const dim3 grid(p.s_max, p.KVH);
     const bool lng = p.nsg > 1;
     if (lng && p.kv_f16 && (p.hd == 128 || p.hd == 64) && p.groups <= (uint32_t)kAttnMaxGroups &&
-        !std::getenv("QORA_HIP_ATTN_STAGED")) {
+        !tuning_env("QORA_HIP_ATTN_STAGED")) {
         const dim3 grid_t(p.KVH, p.s_max);
         if (p.hd == 128) hipLaunchKernelGGL((attn_decode_direct_kernel<128>), grid_t, dim3(512), 0, stream, p);
         else hipLaunchKernelGGL((attn_decode_direct_kernel<64>), grid_t, dim3(512), 0, stream, p);
@@ -529,7 +539,7 @@ static bool pf_rows_reg(int kind, const PrefillRowParams& p, uint32_t T, hipStre
 hipError_t launch_pf_rows(int kind, const PrefillRowParams& p, uint32_t T, hipStream_t stream) {
     if (T == 0) return hipSuccess;
     // QORA_HIP_PF_ROWS=loop keeps every row on the multi-pass kernels
-    const char* er = std::getenv("QORA_HIP_PF_ROWS");
+    const char* er = tuning_env("QORA_HIP_PF_ROWS");
     const bool loop = er && std::strcmp(er, "loop") == 0;
     if (!loop && pf_rows_reg(kind, p, T, stream)) return hipGetLastError();
     switch (kind) {
@@ -565,13 +575,13 @@ bool pf_gemm_supported(uint32_t k, uint32_t n) { return k > 0 && k % 32 == 0 && 
 PfGemmShape pf_gemm_shape(uint32_t T, uint32_t k, uint32_t n, int cus) {
     PfGemmShape sh{};
     const uint32_t mt = (T + 63) / 64;
-    const char* ev = std::getenv("QORA_HIP_PF_NT");
+    const char* ev = tuning_env("QORA_HIP_PF_NT");
     bool wide = n % 128 == 0 && (uint64_t)(n / 128) * mt >= (uint64_t)cus;
     if (ev && *ev) wide = std::atoi(ev) == 128 && n % 128 == 0;
     sh.nt = wide ? 128 : 64;
     const uint64_t blocks = (uint64_t)((n + sh.nt - 1) / sh.nt) * mt;
     uint32_t splits = (uint32_t)std::min<uint64_t>(std::max<uint64_t>(1, (4ull * cus) / blocks), std::max(1u, k / 256));
-    const char* es = std::getenv("QORA_HIP_PF_SPLITS");
+    const char* es = tuning_env("QORA_HIP_PF_SPLITS");
     if (es && *es) splits = std::max(1, std::atoi(es));
     const uint32_t steps = k / 32;
     splits = std::min(splits, steps);
@@ -588,7 +598,7 @@ hipError_t launch_pf_gemm(int fmt, const PrefillGemmParams& p, hipStream_t strea
     const uint32_t nt = (p.n % 128 == 0 && p.nt == 128) ? 128 : 64;
     const dim3 grid((p.n + nt - 1) / nt, (p.T + 63) / 64, p.splits);
     // QORA_HIP_PF_MODE=0 selects the double-buffered K loop (pf_gemm_kernel MODE 0)
-    const char* em = std::getenv("QORA_HIP_PF_MODE");
+    const char* em = tuning_env("QORA_HIP_PF_MODE");
     const int mode = (em && *em && std::atoi(em) == 0) ? 0 : 1;
 #define QORA_PF_GEMM(NT_, Q4_)                                                                              \
     do {                                                                                                   \
@@ -632,7 +642,7 @@ PfGemm2Shape pf_gemm2_shape(uint32_t T, uint32_t k, uint32_t ntot, int cus) {
     // with 32-token tiles and measured slower)
     sh.bm = 64u;
     if (k <= 4096u && (uint64_t)(ntot / 128u) * ((T + 63u) / 64u) < 2u * cu) sh.bm = 32u;
-    const char* eb = std::getenv("QORA_HIP_PF_BM");
+    const char* eb = tuning_env("QORA_HIP_PF_BM");
     if (eb && *eb) sh.bm = std::atoi(eb) == 32 ? 32u : 64u;     // tuning and tests: force 32 or 64
     const uint64_t tiles = std::max<uint64_t>(1, (uint64_t)(ntot / 128u) * ((T + sh.bm - 1) / sh.bm));
     // K is split only when the tiles leave the block slots partly empty (two
@@ -658,7 +668,7 @@ PfGemm2Shape pf_gemm2_shape(uint32_t T, uint32_t k, uint32_t ntot, int cus) {
             splits = s;
         }
     }
-    const char* es = std::getenv("QORA_HIP_PF_SPLITS");
+    const char* es = tuning_env("QORA_HIP_PF_SPLITS");
     if (es && *es) splits = std::min(std::max(1, std::atoi(es)), (int)std::max(1u, steps / 8u));
     const uint32_t per = (steps + splits - 1) / splits;
     sh.kper = per * 32u;
@@ -725,7 +735,7 @@ hipError_t launch_pf_attn(const PrefillAttnParams& p, hipStream_t stream) {
         if (p.part && p.part_nc >= 2 && p.part_nc <= 8) {   // 8: pf_attn_merge_kernel's bound
             const uint32_t keys = p.pos0 + p.T;
             uint32_t ch = 128;
-            const char* ec = std::getenv("QORA_HIP_PF_ATTN_CH");
+            const char* ec = tuning_env("QORA_HIP_PF_ATTN_CH");
             if (ec && *ec) ch = std::max(64u, (uint32_t)std::atoi(ec) / 64u * 64u);
             if ((keys + ch - 1) / ch > p.part_nc) ch = ((keys + p.part_nc - 1) / p.part_nc + 63u) / 64u * 64u;
             const uint32_t nc = (keys + ch - 1) / ch;

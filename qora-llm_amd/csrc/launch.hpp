@@ -8,6 +8,11 @@
 
 namespace qora {
 
+// Value of a tuning or test variable (launch-shape overrides, test hooks):
+// read only when QORA_HIP_TUNING=1 is set, so a host that inherits such a
+// variable does not change the kernels by accident; nullptr otherwise.
+const char* tuning_env(const char* name);
+
 // Launch shape of one split-K GEMV call site.
 struct GemvPlan {
     int gt = 8;           // groups per column tile

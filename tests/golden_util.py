@@ -20,7 +20,15 @@ def model_of(pkg, fx):
                           intermediate=c["intermediate"], num_heads=c["num_heads"], num_kv_heads=c["num_kv_heads"],
                           head_dim=c["head_dim"], rope_half_dim=c["rope_half_dim"], rope_theta=c["rope_theta"],
                           rope_positions=fx["rope_positions"])
-    return pkg.synthetic_model(cfg, seed=fx["seed"], rope_positions=fx["rope_positions"])
+    w = pkg.synthetic_model(cfg, seed=fx["seed"], rope_positions=fx["rope_positions"])
+    mult = fx.get("proj_scale", 1.0)
+    if mult != 1.0:
+        # every projection's Q4 group scales times mult, rounded to binary16
+        for ws in w.layers:
+            for wt in ws:
+                wt.scales = (wt.scales.view(np.float16).astype(np.float32) * np.float32(mult)).astype(
+                    np.float16).view(np.uint16)
+    return w
 
 
 def weights_sha256(w):

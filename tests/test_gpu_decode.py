@@ -57,6 +57,7 @@ def test_stale_nan_cache_slots_never_reach_the_output(ctx, pkg, orc, monkeypatch
     """The attention kernel reads cache slots at and past the appended
     position before they are written; they must be skipped, not multiplied
     by a zero weight (0 * NaN = NaN). The cache starts as NaN bit patterns."""
+    monkeypatch.setenv("QORA_HIP_TUNING", "1")   # the library reads tuning variables only then
     monkeypatch.setenv("QORA_HIP_KV_FILL", "nan")
     w = small_model(pkg, 1)
     prompt = pkg.synth_tokens(0, 2000, 13, w.config.vocab)
@@ -75,11 +76,18 @@ def test_stale_nan_cache_slots_never_reach_the_output(ctx, pkg, orc, monkeypatch
 
 
 def test_greedy_tokens_match_oracle_small(ctx, pkg, orc):
-    w = small_model(pkg, 1, layers=8, seed=3)
-    prompt = pkg.synth_tokens(3, 2000, 16, w.config.vocab)
+    """64 greedy steps of an 8-layer model whose projection scales are x8, so
+    that its greedy path visits many distinct tokens (48 of 64)."""
+    w = small_model(pkg, 1, layers=8, seed=0)
+    for ws in w.layers:
+        for wt in ws:
+            wt.scales = (wt.scales.view(np.float16).astype(np.float32) * np.float32(8)).astype(
+                np.float16).view(np.uint16)
+    prompt = pkg.synth_tokens(0, 2000, 16, w.config.vocab)
     be = pkg.HipBackend(ctx, w, kv_capacity=128)
     om = orc.OracleModel(w, kv_capacity=128, T=4)
     ref, gaps = om.greedy(prompt, 64)
+    assert len(set(ref)) >= 32
     got = pkg.generate_greedy_host(be, prompt, 64)
     assert got == ref
     # the device-chained loop produces the same sequence
@@ -321,6 +329,18 @@ def test_fixed_point_range_overflow_is_reported(ctx, pkg, fmt):
     with pytest.raises(pkg.QoraHipError) as e:
         be.generate_greedy(3, 4)
     assert e.value.code == pkg.QORA_HIP_E_RANGE
+    # the sampled step, with and without logits: the flag is reported there
+    # too, and the next step is refused
+    sp = pkg.SampleParams(temperature=0.8, top_k=40, top_p=0.9, repetition_penalty=1.1, presence_penalty=0.0)
+    for want in (False, True, False):
+        be.kv_reset()
+        be.raw_prefill(prompt, want_logits=False)
+        with pytest.raises(pkg.QoraHipError) as e:
+            be.decode_sample(3, list(prompt), sp, 12345, want_logits=want)
+        assert e.value.code == pkg.QORA_HIP_E_RANGE
+        with pytest.raises(pkg.QoraHipError) as e:
+            be.decode_sample(3, list(prompt), sp, 12345, want_logits=False)
+        assert e.value.code == pkg.QORA_HIP_E_RANGE
     # the same weights with the terms in range decode normally
     w2 = small_model(pkg, fmt, layers=2, seed=13)
     be2 = pkg.HipBackend(ctx, w2, kv_capacity=64)
@@ -347,3 +367,69 @@ def test_default_kv_capacity_is_the_rope_table(ctx, pkg, orc):
     with pytest.raises(pkg.QoraHipError) as e:
         be.forward_decode_raw(int(toks[-1]))
     assert e.value.code == pkg.QORA_HIP_E_STATE
+
+
+def test_forced_failures_leave_the_context_usable(ctx, pkg, orc, monkeypatch):
+    """The reference sends any Err of the GPU backend to the CPU path
+    (main.rs:143-151, gpu_inference.rs:518-562), so a failed call must come
+    back as a clean error code and leave the context usable:
+    QORA_HIP_FORCE_FAIL=alloc fails every device allocation (model set-up,
+    the prefill's first buffers) and =launch every step before it launches.
+    A refused step leaves the cache as it was, a refused prefill leaves it
+    empty, a refused model_init leaves no model; the next call after the
+    variable is cleared matches the oracle."""
+    print("case forced alloc/launch failures", flush=True)
+    w = small_model(pkg, 1, layers=4, seed=21)
+    prompt = pkg.synth_tokens(21, 2000, 11, w.config.vocab)
+    be = pkg.HipBackend(ctx, w, kv_capacity=64)
+    om = orc.OracleModel(w, kv_capacity=64, T=4)
+
+    # alloc: the batched prefill's buffers are allocated by its first call
+    monkeypatch.setenv("QORA_HIP_FORCE_FAIL", "alloc")
+    with pytest.raises(pkg.QoraHipError) as e:
+        be.raw_prefill(prompt)
+    assert e.value.code == pkg.QORA_HIP_E_NOMEM
+    assert be.kv_len() == 0
+    monkeypatch.delenv("QORA_HIP_FORCE_FAIL")
+    logits, tok = be.raw_prefill(prompt)
+    assert rel_err(logits, om.prefill(prompt)) <= REL_TOL
+
+    # launch: decode, device-chained greedy, sampled decode and prefill
+    sp = pkg.SampleParams(**pkg.DEFAULT_SAMPLING)
+    monkeypatch.setenv("QORA_HIP_FORCE_FAIL", "launch")
+    for call in (lambda: be.forward_decode_raw(tok), lambda: be.forward_decode_raw(tok, want_logits=False),
+                 lambda: be.generate_greedy(tok, 3), lambda: be.decode_sample(tok, list(prompt), sp, 99)):
+        with pytest.raises(pkg.QoraHipError) as e:
+            call()
+        assert e.value.code == pkg.QORA_HIP_E_DEVICE
+        assert be.kv_len() == len(prompt)
+    monkeypatch.delenv("QORA_HIP_FORCE_FAIL")
+    for t in (tok, 5, 17):
+        logits, _ = be.forward_decode_raw(int(t))
+        assert rel_err(logits, om.forward_decode(int(t))) <= REL_TOL
+    monkeypatch.setenv("QORA_HIP_FORCE_FAIL", "launch")
+    with pytest.raises(pkg.QoraHipError) as e:
+        be.raw_prefill(prompt)
+    assert e.value.code == pkg.QORA_HIP_E_DEVICE
+    assert be.kv_len() == 0
+    monkeypatch.delenv("QORA_HIP_FORCE_FAIL")
+    om = orc.OracleModel(w, kv_capacity=64, T=4)
+    logits, tok = be.raw_prefill(prompt)
+    assert rel_err(logits, om.prefill(prompt)) <= REL_TOL
+
+    # alloc during model_init: no model is left, steps are refused, and the
+    # next model_init builds it again
+    monkeypatch.setenv("QORA_HIP_FORCE_FAIL", "alloc")
+    with pytest.raises(pkg.QoraHipError) as e:
+        be.model_init()
+    assert e.value.code == pkg.QORA_HIP_E_NOMEM
+    monkeypatch.delenv("QORA_HIP_FORCE_FAIL")
+    with pytest.raises(pkg.QoraHipError) as e:
+        be.forward_decode_raw(tok)
+    assert e.value.code == pkg.QORA_HIP_E_STATE
+    be.model_init()
+    om = orc.OracleModel(w, kv_capacity=64, T=4)
+    logits, tok = be.raw_prefill(prompt)
+    assert rel_err(logits, om.prefill(prompt)) <= REL_TOL
+    logits, _ = be.forward_decode_raw(tok)
+    assert rel_err(logits, om.forward_decode(tok)) <= REL_TOL

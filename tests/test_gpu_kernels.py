@@ -205,8 +205,11 @@ def test_gate_up_f16_vs_oracle(ctx, orc, pkg):
     assert rel_err(got, g / (1 + np.exp(-g)) * u) <= 1e-5
 
 
-@pytest.mark.parametrize("rows,cols", [(32000, 2048), (1000, 256)])
+@pytest.mark.parametrize("rows,cols", [(128256, 2048), (32000, 2048), (1000, 256)])
 def test_rowdot_f16_vs_oracle_lm_head(ctx, orc, pkg, rows, cols):
+    """The F16 tied lm_head (row-dot, gemv.rs:805-822), up to the model's
+    full 128256 x 2048 vocabulary."""
+    print(f"case rowdot f16 rows={rows} cols={cols}", flush=True)
     w = pkg.synth_f16(4, 1000, rows * cols, 0.02)
     x = pkg.synth_f32(4, 94, cols)
     with device(ctx) as d:
@@ -214,7 +217,9 @@ def test_rowdot_f16_vs_oracle_lm_head(ctx, orc, pkg, rows, cols):
         ctx.check(ctx.lib.qora_hip_gemv_f16_rowdot(ctx.h, d.put(w), d.put(x), y, rows, cols, None), "rowdot_f16")
         got = d.get(y, rows, np.float32)
     assert rel_err(got, orc.lm_head_f16(x, w, rows, cols)) <= REL_TOL
-    truth = w.view(np.float16).astype(np.float64).reshape(rows, cols) @ x.astype(np.float64)
+    wm = w.view(np.float16).reshape(rows, cols)
+    x64 = x.astype(np.float64)
+    truth = np.concatenate([wm[r:r + 16384].astype(np.float64) @ x64 for r in range(0, rows, 16384)])
     assert rel_err(got, truth) <= 1e-5
 
 

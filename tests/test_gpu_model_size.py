@@ -3,7 +3,8 @@ the oracle: the 36-layer SmolLM3-3B architecture with seeded random Q4
 weights (seed 1), a batched prefill of 512 seeded random token ids
 (raw_prefill, gemv.rs:1027-1190), then decode steps with every layer's
 binary16 KV cache filled to 32,700 positions (forward_decode_raw,
-gemv.rs:872-1019).
+gemv.rs:872-1019), and decode steps over an f32 cache filled to 1990
+positions (the 2048-context workload's split attention).
 
 The filled cache rows are seeded N(0, 1) values rounded to binary16 (one
 pool of rows, each layer's window starting one row further on) and set in
@@ -106,5 +107,47 @@ def test_decode_over_32700_positions_f16_cache_matches_oracle(pkg, orc, model):
             kr, vr = om.kv_layer(l)
             assert np.array_equal(k[:FILL], kr[:FILL]) and np.array_equal(v[:FILL], vr[:FILL]), l
             assert rel_err(k[FILL:], kr[FILL:]) <= REL_TOL and rel_err(v[FILL:], vr[FILL:]) <= REL_TOL, l
+    finally:
+        ctx.close()
+
+
+def test_decode_over_1990_positions_f32_cache_matches_oracle(pkg, orc, model):
+    """The 2048-context workload's decode path at model size: every layer's
+    f32 cache filled to 1990 positions (the split attention past 256
+    positions, 63 splits of 32), then 6 decode steps against the oracle at
+    REL_TOL, logits and the appended cache rows; greedy tokens compared
+    wherever the oracle's top-2 gap exceeds 1e-4 of its largest logit."""
+    print("case decode at 1990 positions, f32 KV, SmolLM3-3B seed 1", flush=True)
+    c = model.config
+    kvd = c.num_kv_heads * c.head_dim
+    fill, cap = 1990, 2048
+    orc.set_threads(THREADS)
+    om = orc.OracleModel(model, kv_capacity=cap, T=THREADS)
+    ctx = pkg.HipContext(0)
+    try:
+        be = pkg.HipBackend(ctx, model, kv_capacity=cap, kv_dtype=pkg.KV_F32)
+        pool = np.random.default_rng(fill).standard_normal((2, fill + c.num_layers, kvd), dtype=np.float32)
+        for layer in range(c.num_layers):
+            k, v = pool[0, layer:layer + fill], pool[1, layer:layer + fill]
+            be.kv_upload(layer, k, v)
+            om.kv_set(layer, k, v)
+        del pool
+        assert be.kv_len() == fill
+        compared = 0
+        for t in pkg.synth_tokens(1, 2502, 6, c.vocab):
+            logits, tok = be.forward_decode_raw(int(t))
+            ref = om.forward_decode(int(t))
+            err = rel_err(logits, ref)
+            print(f"  step token {int(t)}: rel err {err:.2e}", flush=True)
+            assert err <= REL_TOL, int(t)
+            if orc.top2_gap(ref) > 1e-4 * np.max(np.abs(ref)):
+                assert tok == orc.argmax(ref)
+                compared += 1
+        assert compared >= 3
+        for l in (0, 17, c.num_layers - 1):
+            k, v = be.kv_layer(l)
+            kr, vr = om.kv_layer(l)
+            assert np.array_equal(k[:fill], kr[:fill]) and np.array_equal(v[:fill], vr[:fill]), l
+            assert rel_err(k[fill:], kr[fill:]) <= REL_TOL and rel_err(v[fill:], vr[fill:]) <= REL_TOL, l
     finally:
         ctx.close()

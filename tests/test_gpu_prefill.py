@@ -209,6 +209,7 @@ def test_gemm_loop_modes_bit_identical(ctx, pkg, monkeypatch, k, n, T):
     wid = ctx.upload(pkg.Weight(k=k, n=n, packed=packed, scales=scales))
     with device(ctx) as d:
         y1 = _gemm(ctx, d, wid, x, T, n)
+        monkeypatch.setenv("QORA_HIP_TUNING", "1")   # the library reads tuning variables only then
         monkeypatch.setenv("QORA_HIP_PF_MODE", "0")
         y0 = _gemm(ctx, d, wid, x, T, n)
     assert np.array_equal(y0, y1)
@@ -222,6 +223,7 @@ def test_gemm2_tile_heights_bit_identical(ctx, pkg, monkeypatch, k, n, T):
     packed, scales = pkg.synth_q4(36, k + n, k, n)
     x = (rng(T + 5).standard_normal((T, k)) * 2).astype(np.float32)
     wid = ctx.upload(pkg.Weight(k=k, n=n, packed=packed, scales=scales))
+    monkeypatch.setenv("QORA_HIP_TUNING", "1")   # the library reads tuning variables only then
     monkeypatch.setenv("QORA_HIP_PF_SPLITS", "1")
     with device(ctx) as d:
         monkeypatch.setenv("QORA_HIP_PF_BM", "64")
@@ -246,6 +248,7 @@ def test_row_producers_register_and_loop_bit_identical(ctx, pkg, monkeypatch, hi
     reg, treg = be.raw_prefill(prompt)
     kreg, vreg = be.kv_layer(1)
     be.kv_reset()
+    monkeypatch.setenv("QORA_HIP_TUNING", "1")   # the library reads tuning variables only then
     monkeypatch.setenv("QORA_HIP_PF_ROWS", "loop")
     loop, tloop = be.raw_prefill(prompt)
     kl, vl = be.kv_layer(1)
@@ -261,6 +264,7 @@ def test_batched_prefill_attention_key_chunks(ctx, pkg, orc, monkeypatch, hd, kv
     cache and the next decode step against the oracle."""
     print(f"case prefill key chunks hd={hd} kv={kv_dtype} n={n} ch={ch or 'default'}", flush=True)
     if ch:
+        monkeypatch.setenv("QORA_HIP_TUNING", "1")   # the library reads tuning variables only then
         monkeypatch.setenv("QORA_HIP_PF_ATTN_CH", ch)
     if hd == 64:
         cfg = entry.smoke_config(pkg)

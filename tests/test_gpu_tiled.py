@@ -125,8 +125,13 @@ def test_prepared_q4_scale_extremes(ctx, pkg, k, n):
     assert err <= 2e-5
 
 
-@pytest.mark.parametrize("k,n", [(2048, 2048), (300, 352), (2048, 512)])
+# F16 fp32 accumulation of k terms against the float64 truth (normwise)
+F16_TRUTH_TOL = 1e-5
+
+
+@pytest.mark.parametrize("k,n", [(2048, 2048), (300, 352), (2048, 512), (11008, 2048), (2048, 11008)])
 def test_prepared_f16_vs_oracle(ctx, orc, pkg, k, n):
+    print(f"case prepared f16 k={k} n={n}", flush=True)
     w = pkg.synth_f16(13, 1, k * n, 0.02)
     x = pkg.synth_f32(13, 2, k)
     wid = ctx.upload(pkg.Weight(k=k, n=n, data=w))
@@ -144,6 +149,31 @@ def test_prepared_f16_vs_oracle(ctx, orc, pkg, k, n):
     assert np.array_equal((acc / FIX).astype(np.float32), y_ref_layout)
     for avx in (False, True):
         assert rel_err(acc / FIX, orc.gemv_f16(x, w, k, n, avx512=avx)) <= REL_TOL
+    truth = w.view(np.float16).astype(np.float64).reshape(k, n).T @ x.astype(np.float64)
+    assert rel_err(acc / FIX, truth) <= F16_TRUTH_TOL
+
+
+@pytest.mark.parametrize("k,n", [(2048, 11008), (37, 224)])
+def test_prepared_f16_gate_up_vs_oracle_and_truth(ctx, orc, pkg, k, n):
+    """The paired F16 GEMV of the decode step's gate|up launch (gate at
+    acc[0:n], up at acc[n:2n]) at the model's 2048 -> 2 x 11008 shape."""
+    print(f"case prepared f16 gate_up k={k} n={n}", flush=True)
+    gw = pkg.synth_f16(17, 1, k * n, 0.02)
+    uw = pkg.synth_f16(17, 2, k * n, 0.02)
+    x = pkg.synth_f32(17, 3, k)
+    gid = ctx.gemv_prepare(ctx.upload(pkg.Weight(k=k, n=n, data=gw)), ctx.upload(pkg.Weight(k=k, n=n, data=uw)),
+                           paired=True)
+    try:
+        with device(ctx) as d:
+            acc = _run_prepared(ctx, d, gid, x, 2 * n)
+    finally:
+        ctx.gemv_release(gid)
+    for half, wh in enumerate((gw, uw)):
+        y = acc[half * n:(half + 1) * n] / FIX
+        for avx in (False, True):
+            assert rel_err(y, orc.gemv_f16(x, wh, k, n, avx512=avx)) <= REL_TOL
+        truth = wh.view(np.float16).astype(np.float64).reshape(k, n).T @ x.astype(np.float64)
+        assert rel_err(y, truth) <= F16_TRUTH_TOL
 
 
 def test_prepared_graph_replay(ctx, pkg):

@@ -45,3 +45,25 @@ def test_noalloc_gemv_refuses_sizes_beyond_its_scratch(ctx, pkg):
         want = _run(ctx, d, ctx.lib.qora_hip_gemv_q4, packed2, scales2, x, k, n2)
         got = _run(ctx, d, ctx.lib.qora_hip_gemv_q4_noalloc, packed2, scales2, x, k, n2)
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_noalloc_gemv_refused_call_launches_nothing(ctx, pkg):
+    """Arguments are checked before the first launch: a refused call (n not a
+    multiple of 32, a null input) returns QORA_HIP_E_INVALID and enqueues no
+    write to the shared scratch, so a result computed around it is intact."""
+    print("case gemv_q4_noalloc refused calls", flush=True)
+    k, n = 2048, 2048
+    packed, scales = pkg.synth_q4(63, 1, k, n)
+    x = pkg.synth_f32(63, 2, k)
+    with device(ctx) as d:
+        want = _run(ctx, d, ctx.lib.qora_hip_gemv_q4, packed, scales, x, k, n)
+        pk, sc, xd = d.put(packed), d.put(scales), d.put(x)
+        y = d.empty(n * 4)
+        ctx.check(ctx.lib.qora_hip_gemv_q4_noalloc(ctx.h, pk, sc, xd, y, k, n, None), "noalloc")
+        # queued behind the valid call on the same stream, before its result is read
+        assert ctx.lib.qora_hip_gemv_q4_noalloc(ctx.h, pk, sc, xd, d.empty(48 * 4), k, 48, None) == \
+            pkg.QORA_HIP_E_INVALID
+        assert ctx.lib.qora_hip_gemv_q4_noalloc(ctx.h, pk, sc, None, d.empty(64 * 4), k, 64, None) == \
+            pkg.QORA_HIP_E_INVALID
+        got = d.get(y, n, np.float32)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
