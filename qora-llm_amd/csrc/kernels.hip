@@ -53,6 +53,9 @@ bool plan_gemv(int fmt, uint32_t k, const uint32_t* seg_groups, int nseg, bool p
         forced_rpl <= max_rpl)
         rpl = forced_rpl;
     while (rpl < max_rpl && ((rl * (uint32_t)rpl) % row_align) != 0) rpl *= 2;
+    // at most kFixMaxTerms split-K terms per accumulator between two reads
+    // (the fixed-point range guard, params.hpp)
+    while (rpl < max_rpl && (k + rl * (uint32_t)rpl - 1) / (rl * (uint32_t)rpl) > kFixMaxTerms) rpl *= 2;
     if ((rl * (uint32_t)rpl) % row_align != 0) return false;
     pl.rpl = rpl;
     pl.kr = rl * (uint32_t)rpl;

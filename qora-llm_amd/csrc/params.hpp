@@ -24,13 +24,14 @@ enum Pro : int {
 // workgroups finish in. Resolution 1.5e-11. Range guard: a value read from
 // the residual must be below 2^25 in magnitude (|int| < 2^61) and a single
 // added contribution below 2^20 (|int| < 2^56); an accumulator takes at most
-// kFixMaxTerms contributions between two reads, so a value in range when read
-// cannot wrap before the next read. Kernels given a range_flag set it when a
+// kFixMaxTerms contributions between two reads (the launch planners enforce
+// it), so a value in range when read cannot wrap before the next read:
+// |int| < 2^61 + 96 * 2^56 = 2^63. Kernels given a range_flag set it when a
 // value breaks either bound; the host reports QORA_HIP_E_RANGE.
 constexpr double kFixScale = 68719476736.0;   // 2^36
 constexpr long long kFixReadLimit = 1LL << 61;
 constexpr long long kFixAddLimit = 1LL << 56;
-constexpr uint32_t kFixMaxTerms = 64;
+constexpr uint32_t kFixMaxTerms = 96;
 
 struct GemvSeg {
     const uint8_t* w;         // Q4 packed bytes or F16 words (as bytes), reference layout
