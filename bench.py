@@ -521,16 +521,18 @@ def calibration_copies(ctx, hip):
     ctx.free(dst)
 
 
-def profile_decode(steps=16):
+def profile_decode(steps=16, prompt_len=64):
     """The decode step's kernels, launched eagerly, for rocprofv3 --pmc
-    runs: the calibration copies, then the 64-token prompt's prefill and
-    `steps` greedy decode tokens of the SmolLM3-3B Q4 model (seed 0, f32 KV
-    cache of 2048 positions). Every layer's weights are distinct, so each
-    decode GEMV reads its weights from HBM."""
+    runs: the calibration copies, then the prompt's prefill (64 tokens, or
+    the 2048-context workload's 1920) and `steps` greedy decode tokens of the
+    SmolLM3-3B Q4 model (seed 0, f32 KV cache of 2048 positions). Every
+    layer's weights are distinct, so each decode GEMV reads its weights from
+    HBM."""
     pkg = entry.load_package()
     cfg = pkg.SMOLLM3_3B
     w = pkg.synthetic_model(cfg, seed=0, rope_positions=2048)
-    prompt = pkg.synth_tokens(0, 2000, 64, cfg.vocab)
+    prompt = (pkg.synth_tokens(0, 2000, 64, cfg.vocab) if prompt_len == 64
+              else pkg.synth_tokens(0, 2002, prompt_len, cfg.vocab))
     hip = Hip()
     ctx = pkg.HipContext(0)
     be = pkg.HipBackend(ctx, w, kv_capacity=2048, kv_dtype=pkg.KV_F32)
@@ -539,7 +541,7 @@ def profile_decode(steps=16):
     for _ in range(steps):
         _, tok = be.forward_decode_raw(tok, want_logits=False)
     ctx.synchronize()
-    print(json.dumps({"profile_decode": {"prompt_tokens": 64, "steps": steps, "copy_bytes": COPY_BYTES,
+    print(json.dumps({"profile_decode": {"prompt_tokens": len(prompt), "steps": steps, "copy_bytes": COPY_BYTES,
                                          "last_token": int(tok)}}), flush=True)
     ctx.close()
 
@@ -660,6 +662,8 @@ def main():
     ap.add_argument("--profile-decode", action="store_true",
                     help="only the 64-token prefill and 16 decode tokens, launched eagerly after device copies "
                          "of known size, for hardware-counter runs")
+    ap.add_argument("--profile-prompt", type=int, default=64, choices=[64, 1920],
+                    help="prompt length of --profile-decode: 64, or 1920 for the 2048-context workload")
     ap.add_argument("--probe-residency", action="store_true",
                     help="only the launch-floor and cache-residency probes of the decode step")
     ap.add_argument("--profile-kernel", action="store_true",
@@ -685,7 +689,7 @@ def main():
         return
     if args.profile_decode:
         os.environ["QORA_HIP_EAGER"] = "1"
-        profile_decode()
+        profile_decode(prompt_len=args.profile_prompt)
         return
     if args.profile_prefill or args.profile_long:
         pkg = entry.load_package()

@@ -668,6 +668,11 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
     m.lm_mfma = m.fmt == FMT_Q4 && lmhead_supported(m.hidden) && !tuning_env("QORA_HIP_LM_ROWDOT");
     m.lm_blocks = m.lm_mfma ? lmhead_blocks(m.vocab, c->cus) : rowdot_blocks(m.vocab, m.hidden, c->cus);
     attn_geometry(m.cap, &m.attn_chunk, &m.attn_s_max);
+    // The step's split length follows the live context (attn_chunk_for(L):
+    // 32 positions up to L = 2048), so a context shorter than the capacity
+    // can need more splits than the capacity's own geometry has: launch
+    // enough for every L <= cap (splits past L exit at once).
+    m.attn_s_max = std::min<uint32_t>((uint32_t)kAttnMaxSplits, (m.cap + kAttnSub - 1) / kAttnSub);
 
     // device buffers
     void* p = nullptr;

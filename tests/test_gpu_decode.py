@@ -225,6 +225,32 @@ def test_long_context_decode_matches_oracle(ctx, pkg, orc, kv_dtype, hd):
     assert be.kv_len() == n + 4
 
 
+@pytest.mark.parametrize("cap,n", [(2100, 1500), (3000, 2040), (2100, 2095)])
+def test_split_count_covers_contexts_below_an_odd_capacity(ctx, pkg, orc, cap, n):
+    """The split length follows the live context (32 positions up to 2048),
+    so at a capacity whose own split length is longer (2100: 64 positions)
+    a context of 1500 needs 47 splits where the capacity's geometry has 33:
+    the step launches enough splits for every context up to the capacity,
+    and no position goes unattended."""
+    print(f"case split count cap={cap} n={n}", flush=True)
+    cfg = pkg.ModelConfig(num_layers=2, vocab=1000, hidden=256, intermediate=704, num_heads=4,
+                          num_kv_heads=2, head_dim=64, rope_half_dim=32, rope_theta=5e6, rope_positions=cap)
+    w = pkg.synthetic_model(cfg, seed=8, rope_positions=cap)
+    be = pkg.HipBackend(ctx, w, kv_capacity=cap)
+    om = orc.OracleModel(w, kv_capacity=cap, T=4)
+    r = np.random.default_rng(cap + n)
+    kvd = cfg.num_kv_heads * cfg.head_dim
+    for layer in range(cfg.num_layers):
+        # keys that make the late positions matter: scores grow with position
+        k = r.standard_normal((n, kvd), dtype=np.float32) * np.linspace(0.5, 3, n, dtype=np.float32)[:, None]
+        v = r.standard_normal((n, kvd), dtype=np.float32)
+        be.kv_upload(layer, k, v)
+        om.kv_set(layer, k, v)
+    for t in pkg.synth_tokens(8, 2001, 3, cfg.vocab):
+        logits, _ = be.forward_decode_raw(int(t))
+        assert rel_err(logits, om.forward_decode(int(t))) <= REL_TOL, int(t)
+
+
 def test_state_calls_right_after_a_logits_free_step(ctx, pkg, orc):
     """A greedy step without logits returns once the device has stored its
     token, before the stream reports completion. Calls made right after it
