@@ -451,7 +451,18 @@ def extra_decode_rates(be, ctx, pkg, cfg, prompt, cap, steps):
         hist.append(tok)
     sampled = steps / (time.perf_counter() - t0)
     print(f"# sampled decode (device top-k/top-p + penalties): {sampled:.1f} tok/s", file=sys.stderr, flush=True)
-    return chained, tok_s_2048, sampled
+    # top_k 0 (every token a candidate, sample_token_top_k's k = vocab): the
+    # full device sort and the sequential scan over all 128256 probabilities
+    params0 = pkg.SampleParams(**dict(pkg.DEFAULT_SAMPLING, top_k=0))
+    n0 = 16
+    ctx.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(n0):
+        _, tok, st = be.decode_sample(hist[-1], hist, params0, st)
+        hist.append(tok)
+    sampled_k0 = n0 / (time.perf_counter() - t0)
+    print(f"# sampled decode, top_k 0 (full sort): {sampled_k0:.1f} tok/s", file=sys.stderr, flush=True)
+    return chained, tok_s_2048, sampled, sampled_k0
 
 
 def prefill_rate(be, ctx, pkg, cfg, n=512, reps=3):
@@ -733,9 +744,9 @@ def main():
     tok_s = args.steps / dt
     print(f"# decode {tok_s:.1f} tok/s ({dt / args.steps * 1e3:.3f} ms/token)", file=sys.stderr, flush=True)
 
-    chained = tok_s_2048 = sampled = None
+    chained = tok_s_2048 = sampled = sampled_k0 = None
     if not args.decode_only:
-        chained, tok_s_2048, sampled = extra_decode_rates(be, ctx, pkg, cfg, prompt, cap, args.steps)
+        chained, tok_s_2048, sampled, sampled_k0 = extra_decode_rates(be, ctx, pkg, cfg, prompt, cap, args.steps)
 
     prefill = None if args.decode_only else prefill_rate(be, ctx, pkg, cfg)
 
@@ -803,6 +814,7 @@ def main():
         "tok_s_device_chained": round(chained, 2) if chained else None,
         "tok_s_ctx2048": round(tok_s_2048, 2) if tok_s_2048 else None,
         "tok_s_sampled": round(sampled, 2) if sampled else None,
+        "tok_s_sampled_top_k0": round(sampled_k0, 2) if sampled_k0 else None,
         "tok_s_ctx32768_f16kv": round(long_rate, 2) if long_rate else None,
         "prefill_512": prefill,
         "frac_of_roofline_ctx32768": (round(long_rate * long_bytes / (HBM_PEAK_GBS * 1e9), 4)

@@ -817,7 +817,7 @@ hipError_t launch_sample_sorted(const float* logits, const SampleParams& p, uint
     if (p.temperature > 0.0f)
         hipLaunchKernelGGL(smp_probs_kernel, dim3((k + 255) / 256), dim3(256), 0, stream, p,
                            (const unsigned long long*)src, k);
-    hipLaunchKernelGGL(smp_scan_kernel, dim3(1), dim3(64), 0, stream, p, (const unsigned long long*)src, k);
+    hipLaunchKernelGGL(smp_scan_kernel, dim3(1), dim3(256), 0, stream, p, (const unsigned long long*)src, k);
     return hipGetLastError();
 }
 

@@ -155,8 +155,10 @@ __global__ __launch_bounds__(256) void smp_final_kernel(SampleParams p) {
 //    merged run is in order; the ~0 padding ties break by run (stable);
 // 3. smp_probs_kernel: e^((l - max) / temperature) of the first k keys, each
 //    computed once by the same expression the scan would use;
-// 4. smp_scan_kernel: one thread runs sample_token_top_k's sums, nucleus
-//    cut-off, draw and scan over those k values in order (generate.rs:360-393).
+// 4. smp_scan_kernel: sample_token_top_k's sums, nucleus cut-off, draw and
+//    scan over those k values (generate.rs:360-393), the sums in the
+//    reference's order on one lane over LDS-staged values, the draw's scan as
+//    a parallel search of the running sums (below).
 // ---------------------------------------------------------------------------
 
 __global__ __launch_bounds__(256) void smp_block_sort_kernel(SampleParams p) {
@@ -200,46 +202,180 @@ __global__ __launch_bounds__(256) void smp_probs_kernel(SampleParams p, const un
     p.probs[i] = expf((smp_key_value(sorted[i]) - max_logit) * inv_temp);
 }
 
-__global__ __launch_bounds__(64) void smp_scan_kernel(SampleParams p, const unsigned long long* sorted, uint32_t k) {
-    if (threadIdx.x != 0) return;
+// The scan of sample_token_top_k (generate.rs:360-393) over the k sorted
+// candidates, bit for bit in the reference's float order. Two sequential
+// passes run on lane 0 of wave 0 over values staged in LDS (waves 1..3 load
+// the next 4096-value chunk while lane 0 works on the current one, so lane 0
+// never waits on global memory):
+//   A. sum = e_0 + e_1 + ... (left to right), inv = 1 / sum;
+//   B. cum_i = cum_{i-1} + e_i * inv, each written back over e_i, up to the
+//      first cum_i >= top_p (the cut-off; every value when none reaches it).
+// The reference's `total` over the cut-off is the same left-to-right sum of
+// the same rounded products, i.e. the last cum_i of pass B, and its draw
+// loop recomputes the same running sums: the token is the first candidate
+// i < cut-off with cum_i >= rand_val, found by all 256 threads at once.
+constexpr uint32_t kScanChunk = 4096;
+
+__device__ __forceinline__ void smp_scan_stage(const float* src, uint32_t c, uint32_t n, float* dst) {
+    for (uint32_t i = threadIdx.x - 64u; i < kScanChunk; i += 192u) {
+        const uint32_t j = c * kScanChunk + i;
+        dst[i] = j < n ? src[j] : 0.f;
+    }
+}
+
+__device__ __forceinline__ void smp_scan_unstage(const float* srcb, uint32_t c, uint32_t n, float* dst) {
+    for (uint32_t i = threadIdx.x - 64u; i < kScanChunk; i += 192u) {
+        const uint32_t j = c * kScanChunk + i;
+        if (j < n) dst[j] = srcb[i];
+    }
+}
+
+// One pass over v[0, n) in order on thread 0, 16 values at a time from LDS:
+// `block(x[16], cnt)` runs the pass's arithmetic over x[0, cnt) in order (it
+// may rewrite them) and returns the index of its stop within the block, or
+// 16 for none. writeback: the (rewritten) values go back to v. Returns
+// i + 1 of the stop, or 0 when the pass ran to n. (Staged chunks are padded
+// with zeros past n, so 16-value reads stay inside the buffer.)
+template <bool WRITEBACK, typename Block>
+__device__ __forceinline__ uint32_t smp_scan_pass(float* v, uint32_t n, float (*buf)[kScanChunk], uint32_t* s_stop,
+                                                  Block block) {
+    const uint32_t t = threadIdx.x;
+    const uint32_t nch = (n + kScanChunk - 1) / kScanChunk;
+    __syncthreads();   // every thread has read the previous pass's stop
+    if (t == 0) *s_stop = 0;
+    if (t >= 64 && nch) smp_scan_stage(v, 0, n, buf[0]);
+    __syncthreads();
+    uint32_t c = 0;
+    for (; c < nch; ++c) {
+        if (t >= 64) {
+            // chunk c - 1 (done) goes back, then chunk c + 1 comes into its buffer
+            if (WRITEBACK && c > 0) smp_scan_unstage(buf[(c - 1) & 1u], c - 1, n, v);
+            if (c + 1 < nch) smp_scan_stage(v, c + 1, n, buf[(c + 1) & 1u]);
+        }
+        if (t == 0) {
+            float4* b4 = reinterpret_cast<float4*>(buf[c & 1u]);
+            const uint32_t i0 = c * kScanChunk, cnt = min(kScanChunk, n - i0);
+            for (uint32_t j = 0; j < cnt; j += 16) {
+                float x[16];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const float4 f = b4[j / 4 + q];
+                    x[4 * q] = f.x;
+                    x[4 * q + 1] = f.y;
+                    x[4 * q + 2] = f.z;
+                    x[4 * q + 3] = f.w;
+                }
+                const uint32_t at = block(x, min(16u, cnt - j));
+                if (WRITEBACK) {
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) b4[j / 4 + q] = make_float4(x[4 * q], x[4 * q + 1], x[4 * q + 2], x[4 * q + 3]);
+                }
+                if (at < 16u) {
+                    *s_stop = i0 + j + at + 1;
+                    break;
+                }
+            }
+        }
+        __syncthreads();
+        if (*s_stop) break;
+    }
+    if (WRITEBACK && nch && t >= 64) smp_scan_unstage(buf[min(c, nch - 1) & 1u], min(c, nch - 1), n, v);
+    return *s_stop;
+}
+
+__global__ __launch_bounds__(256) void smp_scan_kernel(SampleParams p, const unsigned long long* sorted, uint32_t k) {
+    __shared__ __align__(16) float buf[2][kScanChunk];
+    __shared__ uint32_t s_stop;
+    __shared__ float s_val[2];
+    __shared__ uint32_t s_hit[4];
+    const uint32_t t = threadIdx.x;
     uint32_t token = (uint32_t)sorted[0];
     unsigned long long state = *p.rng;
     if (p.temperature > 0.0f) {
         float sum = 0.0f;
-        for (uint32_t i = 0; i < k; ++i) sum = __fadd_rn(sum, p.probs[i]);
-        if (sum > 0.0f) {
-            const float inv = 1.0f / sum;
+        smp_scan_pass<false>(p.probs, k, buf, &s_stop, [&](float (&x)[16], uint32_t cnt) {
+            if (cnt == 16u) {
+#pragma unroll
+                for (int j = 0; j < 16; ++j) sum = __fadd_rn(sum, x[j]);
+            } else {
+                for (uint32_t j = 0; j < cnt; ++j) sum = __fadd_rn(sum, x[j]);
+            }
+            return 16u;
+        });
+        if (t == 0) s_val[0] = sum;
+        __syncthreads();
+        if (s_val[0] > 0.0f) {
+            const float inv = 1.0f / s_val[0];
             // each probability is e * inv, rounded, then added (never one fused
             // multiply-add), as the reference scales the vector before summing
             float cum = 0.0f;
-            uint32_t cutoff = k;
-            for (uint32_t i = 0; i < k; ++i) {
-                cum = __fadd_rn(cum, __fmul_rn(p.probs[i], inv));
-                if (cum >= p.top_p) {
-                    cutoff = i + 1;
-                    break;
+            const float top_p = p.top_p;
+            // the running sums of a block first (the sums never decrease, but a
+            // NaN could break that, so every one is tested), then the first stop
+            const uint32_t stop = smp_scan_pass<true>(p.probs, k, buf, &s_stop, [&](float (&x)[16], uint32_t cnt) {
+                if (cnt == 16u) {
+#pragma unroll
+                    for (int j = 0; j < 16; ++j) {
+                        cum = __fadd_rn(cum, __fmul_rn(x[j], inv));
+                        x[j] = cum;
+                    }
+                } else {
+                    for (uint32_t j = 0; j < cnt; ++j) {
+                        cum = __fadd_rn(cum, __fmul_rn(x[j], inv));
+                        x[j] = cum;
+                    }
                 }
-            }
-            float total = 0.0f;
-            for (uint32_t i = 0; i < cutoff; ++i) total = __fadd_rn(total, __fmul_rn(p.probs[i], inv));
+                // the running sums never decrease unless a NaN enters, which
+                // then stays to the block's end: with the last sum below top_p
+                // (a false comparison for NaN) no sum of the block reached it
+                if (cum < top_p) return 16u;
+                uint32_t at = 0;
+                while (at < cnt && !(x[at] >= top_p)) ++at;
+                if (at < cnt) cum = x[at];   // the reference's cumsum at its cut-off
+                return at < cnt ? at : 16u;
+            });
+            const uint32_t cutoff = stop ? stop : k;
+            if (t == 0) s_val[1] = cum;   // total over the cut-off
+            __syncthreads();
+            const float total = s_val[1];
             if (total > 0.0f) {
                 state ^= state << 13;
                 state ^= state >> 7;
                 state ^= state << 17;
                 const float rand_val = (float)(uint32_t)(state >> 40) / 16777216.0f * total;
-                float acc = 0.0f;
-                for (uint32_t i = 0; i < cutoff; ++i) {
-                    acc = __fadd_rn(acc, __fmul_rn(p.probs[i], inv));
-                    if (acc >= rand_val) {
-                        token = (uint32_t)sorted[i];
-                        break;
-                    }
+                // C: first i < cutoff with cum_i >= rand_val, a staged chunk at a
+                // time, every thread testing its values of the chunk (the cum_i
+                // are this block's own stores, ordered by the barriers)
+                const uint32_t nch = (cutoff + kScanChunk - 1) / kScanChunk;
+                if (t >= 64) smp_scan_stage(p.probs, 0, cutoff, buf[0]);
+                __syncthreads();
+                uint32_t first = 0xFFFFFFFFu;
+                for (uint32_t c = 0; c < nch; ++c) {
+                    if (t >= 64 && c + 1 < nch) smp_scan_stage(p.probs, c + 1, cutoff, buf[(c + 1) & 1u]);
+                    const float* b = buf[c & 1u];
+                    const uint32_t i0 = c * kScanChunk, cnt = min(kScanChunk, cutoff - i0);
+                    uint32_t f = 0xFFFFFFFFu;
+                    for (uint32_t j = t; j < cnt; j += 256)
+                        if (b[j] >= rand_val) {
+                            f = i0 + j;
+                            break;
+                        }
+#pragma unroll
+                    for (int off = 32; off >= 1; off >>= 1) f = min(f, (uint32_t)__shfl_xor((int)f, off, kWave));
+                    if ((t & 63u) == 0) s_hit[t / 64] = f;
+                    __syncthreads();
+                    first = min(min(s_hit[0], s_hit[1]), min(s_hit[2], s_hit[3]));
+                    __syncthreads();   // s_hit is rewritten next chunk
+                    if (first != 0xFFFFFFFFu) break;
                 }
+                if (first != 0xFFFFFFFFu) token = (uint32_t)sorted[first];
             }
         }
     }
-    *p.rng = state;
-    *p.token_out = (int32_t)token;
+    if (t == 0) {
+        *p.rng = state;
+        *p.token_out = (int32_t)token;
+    }
 }
 
 }  // namespace qora
