@@ -285,7 +285,15 @@ __global__ __launch_bounds__(kFusedWaves * kWave) void gemv_q4m_attn_kernel(Attn
         mls[wave][1] = l_w;
     }
     __syncthreads();
-    if (wave >= NW) return;
+    if (wave >= NW) {
+        // the accumulator this launch clears (the next GEMV's), while the
+        // matrix-core waves run their pass
+        if (p.zero_ptr) {
+            const uint32_t tq = (uint32_t)(t - NW * kWave), nq = (kFusedWaves - NW) * kWave;
+            for (uint32_t i = blockIdx.x * nq + tq; i < p.zero_n; i += gridDim.x * nq) p.zero_ptr[i] = 0;
+        }
+        return;
+    }
     // ---- each matrix-core wave merges the 8 waves' states for the rows its
     // lanes quantise (lane l: rows l * NQ + u), in wave order ----
     float M = mls[0][0];

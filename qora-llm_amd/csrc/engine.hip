@@ -739,8 +739,9 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
     //   xacc --RMSNorm+q|k|v GEMV--> qkv_acc --attention(RoPE, K/V append)-->
     //   partials --merge+o GEMV--> xacc (+=) --RMSNorm+gate|up GEMV--> gu_acc
     //   --silu*up+down GEMV--> xacc (+=)
-    // qkv_acc is cleared by the gate|up kernel and gu_acc by the next q|k|v
-    // kernel, each after its last reader has finished. Below attn_o_max
+    // qkv_acc is cleared by the gate|up kernel and gu_acc by the o kernel
+    // (the waves it has left over), each after its last reader has finished
+    // and before its next writer starts. Below attn_o_max
     // positions, attention and the o GEMV run as one kernel
     // (gemv_q4m_attn_kernel) that reads qkv_acc itself.
     m.p_qkv.resize(m.L);
@@ -767,9 +768,7 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
         q.gamma = m.d_norms + ((size_t)l * 2 + 0) * m.hidden;
         q.ss_out = m.d_ss + ((size_t)l * 2 + 0) * kAttnMaxSplits;
         q.acc = m.d_qkv_acc;
-        q.zero_ptr = m.d_gu_acc;
         q.range_flag = m.d_range;
-        q.zero_n = 2 * m.inter;
         apply_plan(m.pl_qkv, &q);
         if (int rc = pack_model_gemv(c, (int)m.fmt, m.pl_qkv, &q)) { free_model(c); return rc; }
 
@@ -813,6 +812,8 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
         o.pos = m.d_pos;
         o.acc = m.d_xacc;
         o.range_flag = m.d_range;
+        o.zero_ptr = m.d_gu_acc;      // cleared by the attention + o launch's idle waves
+        o.zero_n = 2 * m.inter;
         apply_plan(m.pl_o, &o);
         if (int rc = pack_model_gemv(c, (int)m.fmt, m.pl_o, &o)) { free_model(c); return rc; }
         if (m.attn_o_max) m.p_ao[l] = AttnOParams{o, a};

@@ -408,9 +408,6 @@ __device__ __forceinline__ void gemv_q4m_body(const GemvParams& p, uint32_t bloc
     // workgroups spreads the items beyond it over the first workgroups)
     const uint32_t nit = block < items ? min((uint32_t)IPW, (items - block + nblocks - 1) / nblocks) : 0u;
 
-    if (p.zero_ptr)
-        for (uint32_t i = block * NT + t; i < p.zero_n; i += nblocks * NT) p.zero_ptr[i] = 0;
-
     uint4 wq[IPW][GW][NKB];
     uint32_t sw[IPW][(NZ + 1) / 2];
     int esg[IPW][GW];
@@ -504,7 +501,15 @@ __device__ __forceinline__ void gemv_q4m_body(const GemvParams& p, uint32_t bloc
         }
     }
     __syncthreads();
-    if (wave >= NW) return;
+    if (wave >= NW) {
+        // the accumulator this launch clears, by the prologue waves once
+        // their input is handed over
+        if (p.zero_ptr) {
+            const uint32_t tq = (uint32_t)(t - NW * kWave), nq = NPW * kWave;
+            for (uint32_t i = block * nq + tq; i < p.zero_n; i += nblocks * nq) p.zero_ptr[i] = 0;
+        }
+        return;
+    }
 #pragma unroll
     for (int j = 0; j < IPW; ++j) {
         if ((uint32_t)j >= nit) continue;

@@ -464,7 +464,6 @@ static hipError_t launch_attn_o_hd(const GemvPlan& pl, const AttnOParams& p, uin
 }
 
 hipError_t launch_attn_o(const GemvPlan& pl, const AttnOParams& p, uint32_t np, hipStream_t stream) {
-    if (p.g.zero_ptr) return hipErrorInvalidValue;   // the fused kernel clears nothing
     if (p.a.hd == 128) {
         return p.a.kv_f16 ? launch_attn_o_hd<128, true>(pl, p, np, stream)
                           : launch_attn_o_hd<128, false>(pl, p, np, stream);
