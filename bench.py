@@ -282,8 +282,11 @@ def gemv_roofline(ctx, hip, be, pkg):
         k, n = shapes[j]
         ms = prepared_time(ctx, hip, int(be.wids[0, j]), 0, False, k * n // 2 + k * n // 16, x, acc)
         results[label] = {"us": ms * 1e3, "gbps": q4_bytes(k, n) / (ms * 1e-3) / 1e9}
-    # fused gate+up (the dominant kernel)
+    # the single 2048 -> 11008 gate projection (the one-GEMV workload's shape)
     k, n = shapes[4]
+    ms = prepared_time(ctx, hip, int(be.wids[0, 4]), 0, False, k * n // 2 + k * n // 16, x, acc)
+    results["gate 2048x11008"] = {"us": ms * 1e3, "gbps": q4_bytes(k, n) / (ms * 1e-3) / 1e9}
+    # fused gate+up (the dominant kernel)
     gu_w = 2 * (k * n // 2 + k * n // 16)
     ms = prepared_time(ctx, hip, int(be.wids[0, 4]), int(be.wids[0, 5]), True, gu_w, x, acc)
     gu_bytes = gu_w + 4 * k + 8 * n
@@ -557,12 +560,13 @@ def profile_decode(steps=16, prompt_len=64):
     ctx.close()
 
 
-def profile_kernel(launches=8):
+def profile_kernel(launches=8, shape="gate_up"):
     """The dominant kernel alone, for rocprofv3 --pmc runs: three device
     copies of COPY_BYTES (hipMemcpy's blit kernel: reads and writes
     COPY_BYTES each, the counter calibration), then `launches` launches of
-    the gate|up GEMV (2048 -> 2 x 11008, SmolLM3-3B layer 0 weights) on
-    distinct packed copies, so each launch reads its weights from HBM."""
+    the gate|up GEMV (2048 -> 2 x 11008, SmolLM3-3B layer 0 weights), or of
+    the single gate GEMV (shape "gate": 2048 -> 11008), on distinct packed
+    copies, so each launch reads its weights from HBM."""
     pkg = entry.load_package()
     cfg = pkg.SMOLLM3_3B
     hip = Hip()
@@ -576,14 +580,17 @@ def profile_kernel(launches=8):
     acc = ctx.malloc(8 * 2 * n)
     ctx.h2d(x, pkg.synth_f32(0, 77, k))
     calibration_copies(ctx, hip)
-    gids = [ctx.gemv_prepare(wg, wu, True) for _ in range(launches)]
+    paired = shape == "gate_up"
+    gids = [ctx.gemv_prepare(wg, wu if paired else 0, paired) for _ in range(launches)]
     ctx.synchronize()
     for g in gids:
         ctx.check(ctx.lib.qora_hip_gemv_run(ctx.h, g, x, acc, None), "gemv_run")
     ctx.synchronize()
-    gu_bytes = 2 * (k * n // 2 + k * n // 16) + 4 * k + 8 * n
-    print(json.dumps({"profile_kernel": "gemv_q4m4_kernel gate|up 2048x(2x11008)", "launches": launches,
-                      "algorithmic_bytes_per_launch": gu_bytes, "copy_bytes": COPY_BYTES}), flush=True)
+    nbytes = 2 * (k * n // 2 + k * n // 16) + 4 * k + 8 * n if paired else q4_bytes(k, n)
+    print(json.dumps({"profile_kernel": "gemv_q4m4_kernel " + ("gate|up 2048x(2x11008)" if paired else
+                                                               "gate 2048x11008"),
+                      "launches": launches, "algorithmic_bytes_per_launch": nbytes, "copy_bytes": COPY_BYTES}),
+          flush=True)
     for g in gids:
         ctx.gemv_release(g)
 
@@ -673,6 +680,8 @@ def main():
     ap.add_argument("--profile-decode", action="store_true",
                     help="only the 64-token prefill and 16 decode tokens, launched eagerly after device copies "
                          "of known size, for hardware-counter runs")
+    ap.add_argument("--profile-shape", default="gate_up", choices=["gate_up", "gate"],
+                    help="GEMV of --profile-kernel: the paired gate|up (default) or the single gate projection")
     ap.add_argument("--profile-prompt", type=int, default=64, choices=[64, 1920],
                     help="prompt length of --profile-decode: 64, or 1920 for the 2048-context workload")
     ap.add_argument("--probe-residency", action="store_true",
@@ -690,7 +699,7 @@ def main():
                           "n_gpus": args.gpus}))
         sys.exit(2)
     if args.profile_kernel:
-        profile_kernel()
+        profile_kernel(shape=args.profile_shape)
         return
     if args.probe_residency:
         pkg = entry.load_package()

@@ -17,11 +17,14 @@
 //   So the result is fp32 accumulation of (nearly) exact products: it differs
 //   from the reference only in summation order and in the last bits of x.
 //
-// The GEMM block is 256 threads (2 x 2 waves) over 64 tokens x NT columns;
-// each step stages a 32-deep K slice of x' (both parts, from the split
-// buffers) and of w' (dequantised from the reference-layout weights) in LDS,
-// double-buffered, with the next slice's global loads in flight during the
-// current slice's MFMAs.
+// Two GEMM kernels share these numerics:
+//   * pf_gemm2_kernel (every Q4 projection whose width is a multiple of
+//     128): weights pre-packed once at set-up, 4 waves over BM tokens x 128
+//     columns, only x' in LDS, each wave dequantising its own weights in
+//     registers (its comment below has the details);
+//   * pf_gemm_kernel (F16 weights and other widths): the reference layout
+//     read directly, 2 x 2 waves over 64 tokens x NT columns, each 32-deep K
+//     slice of x' and w' (dequantised) staged in LDS.
 //
 // Operand layouts of v_mfma_f32_16x16x32_f16 (lane l, element b = 0..7):
 //   A[i = l % 16][k = 8 (l / 16) + b], B[k = 8 (l / 16) + b][j = l % 16],
