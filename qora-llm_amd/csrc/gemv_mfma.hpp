@@ -232,6 +232,17 @@ __device__ __forceinline__ void attn_merge_rows_wave(const GemvParams& p, uint32
     if (lane < 32 && i < r1) xs[i] = k0 + i < k1 ? v : 0.f;
 }
 
+// The item of workgroup b of a G-workgroup launch in XCD order. Workgroups
+// go to the 8 XCDs in turn (b to XCD (b + r) mod 8, r fixed for the launch),
+// so XCD x holds the workgroups b = x mod 8; they take the contiguous items
+// [x q + min(x, G mod 8), ...) with q = G / 8, and the K slices whose inputs
+// an XCD's L2 fetches are a few instead of all of them. A permutation of
+// [0, G) for every G.
+__device__ __forceinline__ uint32_t xcd_item(uint32_t b, uint32_t G) {
+    const uint32_t q = G >> 3, rem = G & 7u, x = b & 7u;
+    return x * q + min(x, rem) + (b >> 3);
+}
+
 // Where a matrix-core wave's outputs go: per group, the accumulator of its
 // first column (nullptr for a group past its segment), and the range flag.
 // Computed when the wave starts and held in scalar registers: read at the
@@ -533,7 +544,8 @@ template <int GW, int KW, int PRO, int IPW = 1>
 __global__ __launch_bounds__(PRO == PRO_ATTN ? 512 : 320) void gemv_q4m_kernel(GemvParams p) {
     kernarg_warm(p);
     __shared__ GemvQ4mSmem<GW, KW, PRO, IPW> sm;
-    gemv_q4m_body<GW, KW, PRO, IPW>(p, blockIdx.x, gridDim.x, sm);
+    const uint32_t b = IPW == 1 && p.xcd_order ? xcd_item(blockIdx.x, gridDim.x) : blockIdx.x;
+    gemv_q4m_body<GW, KW, PRO, IPW>(p, b, gridDim.x, sm);
 }
 
 // Four matrix-core waves and no prologue wave (PRO_PLAIN, PRO_GAMMA_FIXED,
@@ -563,7 +575,7 @@ __global__ __launch_bounds__(256) void gemv_q4m4_kernel(GemvParams p) {
     const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
     uint32_t tiles = __builtin_amdgcn_readfirstlane(p.tiles);
     sgpr_pin(tiles);
-    const uint32_t item = blockIdx.x;
+    const uint32_t item = p.xcd_order ? xcd_item(blockIdx.x, gridDim.x) : blockIdx.x;
     const uint32_t tile = item % tiles, split = item / tiles;
     const uint32_t k0 = split * (uint32_t)KW;
     const uint32_t k1 = min(p.k, k0 + (uint32_t)KW);

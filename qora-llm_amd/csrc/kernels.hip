@@ -140,6 +140,13 @@ void apply_plan(const GemvPlan& plan, GemvParams* p) {
     p->tiles = plan.tiles;
     p->splits = plan.splits;
     p->rows_per_split = plan.kr;
+    // XCD order for the prologues that read a previous kernel's output (bit
+    // = prologue): each XCD's L2 then fetches the inputs of its own K slices
+    // only. The plain prologue's input is one small vector; it keeps launch
+    // order, which streams its weights a little faster.
+    static const int xcd_mask = env_int("QORA_HIP_XCD_ORDER",
+                                        (1 << PRO_GAMMA_FIXED) | (1 << PRO_SILU_FIXED) | (1 << PRO_ATTN));
+    p->xcd_order = (uint32_t)(xcd_mask >> p->pro) & 1u;
 }
 
 template <int FMT, int GT, int PRO, bool TILED>

@@ -76,6 +76,9 @@ struct GemvParams {
     // exponent bound of the K slice's scales, max |s| <= 2^tes.
     const int8_t* tes;
     int* range_flag;          // optional: set when a fixed-point value leaves its range
+    // 1: the matrix-core kernels run item xcd_item(b, G) in workgroup b
+    // (each XCD takes a contiguous run of items); 0: item b
+    uint32_t xcd_order;
 };
 
 struct RowdotParams {
