@@ -279,17 +279,4 @@ __device__ __forceinline__ bool argmax_better(float va, uint32_t ia, float vb, u
     return va > vb || (va == vb && ia < ib);
 }
 
-// Device-scope release/acquire around the "last workgroup finishes the
-// reduction" pattern. Workgroups of one launch run on different XCDs with
-// separate L2s; the agent-scope fences write back / invalidate so the
-// partials written by one XCD are visible to another.
-__device__ __forceinline__ uint32_t arrive_counter(uint32_t* counter) {
-    __threadfence();
-    return __hip_atomic_fetch_add(counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ __forceinline__ void store_u32_release(uint32_t* p, uint32_t v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
-}
-
 }  // namespace qora

@@ -394,7 +394,6 @@ __device__ __forceinline__ void gemv_q4m_body(const GemvParams& p, uint32_t bloc
                                               GemvQ4mSmem<GW, KW, PRO, IPW>& sm) {
     constexpr int NW = 4;                    // matrix-core waves
     constexpr int NPW = PRO == PRO_ATTN ? 4 : 1;   // prologue waves (the attention merge gets four)
-    constexpr int NT = (NW + NPW) * kWave;
     constexpr int NKB = KW / 64;            // K blocks (one MFMA each) per slice
     constexpr int NZ = GW * KW / 64;        // z values per lane
     constexpr int RPW = KW / 64;            // prologue rows per lane
