@@ -222,11 +222,18 @@ __device__ __forceinline__ void attn_merge_rows_wave(const GemvParams& p, uint32
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     const float* wrow = aw + hh * kAttnMaxSplits;
+    // every weight is read unconditionally (sj < kAttnMaxSplits), so the
+    // reads go out together and the inactive splits are a select: a read
+    // under the condition became a branch and an LDS round trip per split
+    float wj[kAttnMaxSplits / 2];
+#pragma unroll
+    for (uint32_t j = 0; j < kAttnMaxSplits / 2; ++j) wj[j] = wrow[par + 2u * j];
     float v = 0.f;
 #pragma unroll
     for (uint32_t j = 0; j < kAttnMaxSplits / 2; ++j) {
         const uint32_t sj = par + 2u * j;
-        v = sj < s_act ? fmaf(pv[j], wrow[sj], v) : v;
+        const float t = fmaf(pv[j], wj[j], v);
+        v = sj < s_act ? t : v;
     }
     v += __shfl_xor(v, 32, kWave);
     if (lane < 32 && i < r1) xs[i] = k0 + i < k1 ? v : 0.f;
