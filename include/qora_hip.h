@@ -160,6 +160,15 @@ int qora_hip_decode_sample(qora_hip_ctx* ctx, uint32_t token, const uint32_t* hi
  * kernel does not cover, or QORA_HIP_ATTN_O=0 at model_init). */
 uint32_t qora_hip_attn_o_limit(const qora_hip_ctx* ctx);
 
+/* Context bound of the chunked step (no counterpart in the reference):
+ * graph-driven steps that append a position from qora_hip_attn_o_limit up to
+ * below this bound keep attention and the o projection in one kernel, each
+ * column-tile workgroup of a head attending over its own chunk of the
+ * positions; longer contexts take the split attention kernel. 0 = never (no
+ * fused step, a shape or device the chunked kernel does not cover, or
+ * QORA_HIP_ATTN_CHUNK=0 at model_init). */
+uint32_t qora_hip_attn_chunk_limit(const qora_hip_ctx* ctx);
+
 /* RawKvCache access (gemv.rs:154-166): current length, reset to empty, and a
  * copy of one layer's [len][kv_heads][head_dim] K and V as f32. */
 int qora_hip_kv_len(qora_hip_ctx* ctx, uint64_t* len);

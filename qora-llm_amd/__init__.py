@@ -105,6 +105,7 @@ SIGNATURES = {
     "qora_hip_gemv_run": (_I, [_P, _U32, _P, _P, _P]),
     "qora_hip_gemv_release": (_I, [_P, _U32]),
     "qora_hip_attn_o_limit": (_U32, [_P]),
+    "qora_hip_attn_chunk_limit": (_U32, [_P]),
     "qora_hip_lm_head_prepare": (_I, [_P, _U32, _P]),
     "qora_hip_lm_head_run": (_I, [_P, _U32, _P, _P, _P, _P]),
     "qora_hip_gemv_q4_rowdot": (_I, [_P, _P, _P, _P, _P, _U64, _U64, _P]),
@@ -571,6 +572,11 @@ class HipBackend:
     def attn_o_limit(self) -> int:
         """Steps appending a position below this run attention inside the o GEMV."""
         return int(self.ctx.lib.qora_hip_attn_o_limit(self.ctx.h))
+
+    def attn_chunk_limit(self) -> int:
+        """Steps appending a position from attn_o_limit() up to below this run
+        the chunked attention + o step."""
+        return int(self.ctx.lib.qora_hip_attn_chunk_limit(self.ctx.h))
 
     def kv_layer(self, layer: int):
         """(k, v) of one layer as f32 [len][kv_heads*head_dim] (RawKvCache entry)."""

@@ -55,7 +55,80 @@ __device__ __forceinline__ float4 sel4(bool c, float4 a, float4 b) {
     return make_float4(c ? a.x : b.x, c ? a.y : b.y, c ? a.z : b.z, c ? a.w : b.w);
 }
 
-template <int HD, bool F16KV, int NP>
+// The chunked step's exchange for workgroup (head h, column tile j), in two
+// halves around a block barrier. chunk_publish (wave 0): the chunk's
+// un-normalised state (acc = xr, m = M, l = den) goes to a.part at [h][j]
+// and is counted in the head's counter; then lane 0 waits until the head's
+// `tiles` states are counted (bounded: past kChunkSpin polls the step is
+// flagged through the range flag and its output is not valid). The states
+// are written and read with device-scope atomic stores and loads, and the
+// count is raised only once the last store of the wave has returned (an
+// exchange whose result the increment depends on), so a counted state is in
+// place. Each head's counter has a 128-byte line of its own, and one lane a
+// workgroup polls it. chunk_merge (each matrix-core wave, after the
+// barrier): the head's states merged in chunk order into M, den and xr of
+// the wave's rows (lane * NQ + u).
+template <int HD, int NQ>
+__device__ __forceinline__ void chunk_publish(const AttnOParams& ap, uint32_t h, uint32_t tile, int lane, float M,
+                                              float den, const float (&xr)[NQ]) {
+    constexpr uint32_t SR = HD + 2;                     // floats per state: acc[HD], m, l
+    float* st = ap.a.part + ((uint64_t)h * ap.g.tiles + tile) * SR;
+    uint32_t* count = ap.ch_count + h * kChunkCountStride;
+#pragma unroll
+    for (int u = 0; u < NQ; ++u)
+        __hip_atomic_store(st + lane * NQ + u, xr[u], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    float prev = 0.f;
+    if (lane == 0) {
+        __hip_atomic_store(st + HD + 1, den, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        prev = __hip_atomic_exchange(st + HD, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    uint32_t one = 1u;
+    asm volatile("" : "+v"(one) : "v"(prev));
+    if (lane == 0) {
+        __hip_atomic_fetch_add(count, one, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        uint32_t n = 0;
+        for (uint32_t it = 0; it < kChunkSpin; ++it) {
+            n = __hip_atomic_load(count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (n >= ap.g.tiles) break;
+            __builtin_amdgcn_s_sleep(2);
+        }
+        fix_flag(ap.g.range_flag, n < ap.g.tiles);
+    }
+}
+
+template <int HD, int NQ>
+__device__ __forceinline__ void chunk_merge(const AttnOParams& ap, uint32_t h, int lane, float& M, float& den,
+                                            float (&xr)[NQ]) {
+    constexpr uint32_t SR = HD + 2;
+    const uint32_t tiles = ap.g.tiles;
+    const float* base = ap.a.part + (uint64_t)h * tiles * SR;
+    // (m, l) of chunk `lane`, the wave's rows of every chunk (indexes
+    // clamped into [0, tiles); weights past `tiles` are zero)
+    const uint32_t jl = min((uint32_t)lane, tiles - 1u);
+    const float mj = __hip_atomic_load(base + (uint64_t)jl * SR + HD, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const float lj = __hip_atomic_load(base + (uint64_t)jl * SR + HD + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    float ac[kChunkMaxTiles][NQ];
+#pragma unroll
+    for (uint32_t jj = 0; jj < kChunkMaxTiles; ++jj)
+#pragma unroll
+        for (int u = 0; u < NQ; ++u)
+            ac[jj][u] = __hip_atomic_load(base + (uint64_t)min(jj, tiles - 1u) * SR + lane * NQ + u, __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT);
+    const bool live = (uint32_t)lane < tiles && mj != -INFINITY;
+    M = wave_max(live ? mj : -INFINITY);
+    const float wl = live ? exp2f(mj - M) : 0.f;
+    den = wave_sum(live ? lj * wl : 0.f);
+#pragma unroll
+    for (int u = 0; u < NQ; ++u) xr[u] = 0.f;
+#pragma unroll
+    for (uint32_t jj = 0; jj < kChunkMaxTiles; ++jj) {
+        const float wj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wl), (int)jj));
+#pragma unroll
+        for (int u = 0; u < NQ; ++u) xr[u] = fmaf(ac[jj][u], wj, xr[u]);
+    }
+}
+
+template <int HD, bool F16KV, int NP, bool CH = false>
 __global__ __launch_bounds__(kFusedWaves * kWave) void gemv_q4m_attn_kernel(AttnOParams ap) {
     constexpr int GW = 1, NW = 4;
     constexpr int KW = HD;                  // one query head per K slice
@@ -91,7 +164,10 @@ __global__ __launch_bounds__(kFusedWaves * kWave) void gemv_q4m_attn_kernel(Attn
     const uint64_t cps = kv_pos_stride(a), coff = kv_head_off(a, kvh);
 
     const uint32_t c = (uint32_t)lane % 16, j = (uint32_t)lane / 16;
-    const uint32_t slot = 4u * (uint32_t)wave + j;     // position of pass i: 32 i + slot
+    // position of pass i: P0 + 32 i + slot (CH: chunk `tile` of 32 NP
+    // positions; otherwise every position from 0)
+    const uint32_t P0 = CH ? tile * (kFusedPass * (uint32_t)NP) : 0u;
+    const uint32_t slot = P0 + 4u * (uint32_t)wave + j;
     const uint8_t* kcache = reinterpret_cast<const uint8_t*>(a.kc);
     const uint8_t* vcache = reinterpret_cast<const uint8_t*>(a.vc);
     constexpr uint32_t EB = F16KV ? 2u : 4u;
@@ -108,9 +184,12 @@ __global__ __launch_bounds__(kFusedWaves * kWave) void gemv_q4m_attn_kernel(Attn
         for (int u = 0; u < NQ; ++u) vr[i][u] = *reinterpret_cast<const W*>(vcache + row_off(pos, u));
     };
     // ---- K rows of passes 0 .. NP-2: positions below 32 (NP - 1) <= L - 1,
-    // cached rows whose addresses do not depend on the position ----
+    // cached rows whose addresses do not depend on the position (CH: every
+    // pass waits for the position) ----
+    if constexpr (!CH) {
 #pragma unroll
-    for (int i = 0; i < NP - 1; ++i) load_k(i, kFusedPass * (uint32_t)i + slot);
+        for (int i = 0; i < NP - 1; ++i) load_k(i, kFusedPass * (uint32_t)i + slot);
+    }
 
     const bool qkv_wave = wave >= NW && wave < NW + HD / kWave;
     const uint32_t d = (uint32_t)(t - NW * kWave) % HD;
@@ -124,8 +203,16 @@ __global__ __launch_bounds__(kFusedWaves * kWave) void gemv_q4m_attn_kernel(Attn
     const uint32_t L = (uint32_t)pos_raw + 1u;
     const uint32_t cur = L - 1u;                       // position appended this step
     const uint32_t plast = kFusedPass * (uint32_t)(NP - 1) + slot;
-    const uint32_t plast_rd = cur == 0u ? 0u : min(plast, cur - 1u);
-    load_k(NP - 1, plast_rd);
+    // the row read for position x: rows at or past the appended one are not
+    // read (their values are replaced from LDS or masked)
+    auto rd = [&](uint32_t x) { return cur == 0u ? 0u : min(x, cur - 1u); };
+    const uint32_t plast_rd = rd(plast);
+    if constexpr (CH) {
+#pragma unroll
+        for (int i = 0; i < NP; ++i) load_k(i, rd(kFusedPass * (uint32_t)i + slot));
+    } else {
+        load_k(NP - 1, plast_rd);
+    }
 
     // ---- the q|k|v sums of the head and its RoPE row (waves NW.., one dim
     // per thread), after the K rows and before the V rows: q is ready while
@@ -147,9 +234,14 @@ __global__ __launch_bounds__(kFusedWaves * kWave) void gemv_q4m_attn_kernel(Attn
     }
 
     // ---- V rows of every pass ----
+    if constexpr (CH) {
 #pragma unroll
-    for (int i = 0; i < NP - 1; ++i) load_v(i, kFusedPass * (uint32_t)i + slot);
-    load_v(NP - 1, plast_rd);
+        for (int i = 0; i < NP; ++i) load_v(i, rd(kFusedPass * (uint32_t)i + slot));
+    } else {
+#pragma unroll
+        for (int i = 0; i < NP - 1; ++i) load_v(i, kFusedPass * (uint32_t)i + slot);
+        load_v(NP - 1, plast_rd);
+    }
 
     // ---- the matrix-core waves' scales and weights. Waves NW.. issue the
     // same loads as wave - NW (the lines are already in flight): every wave
@@ -213,7 +305,10 @@ __global__ __launch_bounds__(kFusedWaves * kWave) void gemv_q4m_attn_kernel(Attn
     // the last pass the appended position takes its k row from LDS and the
     // positions past it are masked ----
     const float scale2 = a.scale * 1.4426950408889634f;   // log2(e)
-    const bool last_cur = plast == cur, last_live = plast <= cur;
+    // pass i holds the appended position / a live one (CH: any pass; else
+    // only the last, whose earlier passes lie below the appended position)
+    auto is_cur = [&](int i) { return kFusedPass * (uint32_t)i + slot == cur; };
+    auto is_live = [&](int i) { return kFusedPass * (uint32_t)i + slot <= cur; };
     float s[NP];
 #pragma unroll
     for (int i = 0; i < NP; ++i) {
@@ -221,10 +316,10 @@ __global__ __launch_bounds__(kFusedWaves * kWave) void gemv_q4m_attn_kernel(Attn
 #pragma unroll
         for (int u = 0; u < NQ; ++u) {
             float4 k = kv_word_f32<F16KV>(kr[i][u]);
-            if (i == NP - 1) {
+            if (CH || i == NP - 1) {
                 // selects, not a masked write into the loaded registers
                 const float4 kc4 = *reinterpret_cast<const float4*>(kn + 64 * u + 4 * c);
-                k = sel4(last_cur, kc4, k);
+                k = sel4(is_cur(i), kc4, k);
             }
             dot = fmaf(q[u][0], k.x, dot);
             dot = fmaf(q[u][1], k.y, dot);
@@ -232,7 +327,7 @@ __global__ __launch_bounds__(kFusedWaves * kWave) void gemv_q4m_attn_kernel(Attn
             dot = fmaf(q[u][3], k.w, dot);
         }
         dot = row16_sum(dot) * scale2;
-        s[i] = (i < NP - 1 || last_live) ? dot : -INFINITY;
+        s[i] = ((!CH && i < NP - 1) || is_live(i)) ? dot : -INFINITY;
     }
     // ---- the wave's softmax over its positions and p.V (a wave with no
     // live position keeps m = -inf, l = 0, p.V = 0) ----
@@ -256,10 +351,10 @@ __global__ __launch_bounds__(kFusedWaves * kWave) void gemv_q4m_attn_kernel(Attn
 #pragma unroll
         for (int u = 0; u < NQ; ++u) {
             float4 v = kv_word_f32<F16KV>(vr[i][u]);
-            if (i == NP - 1) {
+            if (CH || i == NP - 1) {
                 const float4 vc4 = *reinterpret_cast<const float4*>(vn + 64 * u + 4 * c);
-                v = sel4(last_cur, vc4, v);
-                v = sel4(last_live, v, make_float4(0.f, 0.f, 0.f, 0.f));   // select: stale bits never reach the sum
+                v = sel4(is_cur(i), vc4, v);
+                v = sel4(is_live(i), v, make_float4(0.f, 0.f, 0.f, 0.f));   // select: stale bits never reach the sum
             }
             o[u][0] = fmaf(p_i, v.x, o[u][0]);
             o[u][1] = fmaf(p_i, v.y, o[u][1]);
@@ -292,7 +387,7 @@ __global__ __launch_bounds__(kFusedWaves * kWave) void gemv_q4m_attn_kernel(Attn
             const uint32_t tq = (uint32_t)(t - NW * kWave), nq = (kFusedWaves - NW) * kWave;
             for (uint32_t i = blockIdx.x * nq + tq; i < p.zero_n; i += gridDim.x * nq) p.zero_ptr[i] = 0;
         }
-        return;
+        if constexpr (!CH) return;
     }
     // ---- each matrix-core wave merges the 8 waves' states for the rows its
     // lanes quantise (lane l: rows l * NQ + u), in wave order ----
@@ -309,6 +404,12 @@ __global__ __launch_bounds__(kFusedWaves * kWave) void gemv_q4m_attn_kernel(Attn
         den = fmaf(mls[w][1], sc, den);
 #pragma unroll
         for (int u = 0; u < NQ; ++u) xr[u] = fmaf(accs[w][lane * NQ + u], sc, xr[u]);
+    }
+    if constexpr (CH) {
+        if (wave == 0) chunk_publish<HD, NQ>(ap, h, tile, lane, M, den, xr);
+        __syncthreads();                               // the head's states are counted
+        if (wave >= NW) return;
+        chunk_merge<HD, NQ>(ap, h, lane, M, den, xr);
     }
     float xm = 0.f;
 #pragma unroll

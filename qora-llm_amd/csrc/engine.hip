@@ -109,6 +109,9 @@ struct ModelState {
     // steps that append a position below attn_o_max
     std::vector<AttnOParams> p_ao;
     uint32_t attn_o_max = 0;
+    // steps that append a position in [attn_o_max, attn_ch_max) run the
+    // chunked step (gemv_q4m_attn_kernel with CH); ch_np_max passes at most
+    uint32_t attn_ch_max = 0, ch_np_max = 0;
     RowdotParams p_lm{};
     LmHeadParams p_lmq{};
     ArgmaxFinishParams p_fin{};
@@ -119,6 +122,8 @@ struct ModelState {
     // (index np - 1: contexts of 32 (np - 1) < L <= 32 np positions)
     hipGraphExec_t g_step_ao[kFusedMaxPasses] = {};
     hipGraphExec_t g_prefill_ao[kFusedMaxPasses] = {};
+    hipGraphExec_t g_step_ch[kFusedMaxPasses] = {};
+    hipGraphExec_t g_prefill_ch[kFusedMaxPasses] = {};
     uint64_t host_pos = 0;
     // token id that d_token holds once the queued work is done (-1: not known):
     // a decode call passing that id skips the upload
@@ -293,6 +298,10 @@ void free_model(qora_hip_ctx* c) {
         if (g) (void)hipGraphExecDestroy(g);
     for (hipGraphExec_t g : m.g_prefill_ao)
         if (g) (void)hipGraphExecDestroy(g);
+    for (hipGraphExec_t g : m.g_step_ch)
+        if (g) (void)hipGraphExecDestroy(g);
+    for (hipGraphExec_t g : m.g_prefill_ch)
+        if (g) (void)hipGraphExecDestroy(g);
     for (void* p : m.allocs) (void)hipFree(p);
     m = ModelState();
 }
@@ -337,15 +346,16 @@ int pack_model_gemv(qora_hip_ctx* c, int fmt, const GemvPlan& pl, GemvParams* p)
 }
 
 // np > 0: attention inside the o GEMV for contexts of at most 32 np
-// positions (short contexts, see attn_o_max); np = 0: split attention
-int record_step(qora_hip_ctx* c, bool with_lm_head, uint32_t np) {
+// positions (short contexts, see attn_o_max), or with chunked, the chunked
+// step whose column tiles take 32 np positions each; np = 0: split attention
+int record_step(qora_hip_ctx* c, bool with_lm_head, uint32_t np, bool chunked = false) {
     ModelState& m = c->m;
     const hipStream_t s = c->stream;
     HIP_TRY(c, launch_embed(with_lm_head ? m.p_emb_tok : m.p_emb_prompt, s));
     for (uint32_t l = 0; l < m.L; ++l) {
         HIP_TRY(c, launch_gemv(m.fmt, m.pl_qkv, m.p_qkv[l], s));
         if (np) {
-            HIP_TRY(c, launch_attn_o(m.pl_o, m.p_ao[l], np, s));
+            HIP_TRY(c, launch_attn_o(m.pl_o, m.p_ao[l], np, chunked, s));
         } else {
             HIP_TRY(c, launch_attn(m.p_attn[l], s));
             HIP_TRY(c, launch_gemv(m.fmt, m.pl_o, m.p_o[l], s));
@@ -387,10 +397,40 @@ uint32_t attn_o_limit(const ModelState& m) {
     return n <= 0 ? 0u : (uint32_t)std::min<long>(std::min<long>(n, (long)kAttnODefaultMax), (long)m.cap);
 }
 
-// Pass count of the fused kernel for the step that appends `pos` (its context
-// is pos + 1 positions), 0 for the split attention.
-uint32_t fused_passes(const ModelState& m, uint64_t pos) {
-    return pos < (uint64_t)m.attn_o_max ? (uint32_t)(pos / kFusedPass) + 1u : 0u;
+// Steps that append a position in [attn_o_max, this bound) run the chunked
+// step: the column tiles of a head each attend over a chunk of 32 np
+// positions (tiles * 32 np >= the context) and exchange their states, so a
+// layer's attention and o projection stay one launch without each workgroup
+// reading the whole context. The exchange costs a few microseconds of
+// device-coherent stores, polls and loads, and every query head re-reads its
+// KV head's rows, so the step beats the split attention only while each
+// column tile holds few positions: by default up to kChunkDefaultPerTile per
+// tile (measured on SmolLM3-3B: +4.4% at 300-500 positions, +2.8% at ~730,
+// -0.8% at ~990). QORA_HIP_ATTN_CHUNK sets the bound (0: never chunked), up
+// to kFusedMaxPasses passes a tile.
+constexpr uint32_t kChunkDefaultPerTile = 48;
+
+uint32_t attn_ch_limit(const ModelState& m, int cus) {
+    if (m.fmt != FMT_Q4 || !attn_chunk_supported(m.pl_o, m.hd, m.H, m.groups, m.attn_s_max, cus)) return 0;
+    const uint64_t top = std::min<uint64_t>((uint64_t)kFusedPass * kFusedMaxPasses * m.pl_o.tiles, m.cap);
+    const char* v = std::getenv("QORA_HIP_ATTN_CHUNK");
+    const long long n = (v && *v) ? std::atoll(v) : (long long)kChunkDefaultPerTile * m.pl_o.tiles;
+    const uint64_t lim = n <= 0 ? 0u : std::min<uint64_t>((uint64_t)n, top);
+    return lim > m.attn_o_max ? (uint32_t)lim : 0u;
+}
+
+// Attention of the step that appends `pos` (its context is pos + 1
+// positions): the fused kernel's pass count, or the chunked step's passes per
+// chunk (chunked), or np = 0 for the split attention.
+struct StepAttn {
+    uint32_t np;
+    bool chunked;
+};
+
+StepAttn step_attn(const ModelState& m, uint64_t pos) {
+    if (pos < (uint64_t)m.attn_o_max) return {(uint32_t)(pos / kFusedPass) + 1u, false};
+    if (pos < (uint64_t)m.attn_ch_max) return {(uint32_t)(pos / ((uint64_t)kFusedPass * m.pl_o.tiles)) + 1u, true};
+    return {0u, false};
 }
 
 bool eager_mode() {
@@ -401,17 +441,18 @@ bool eager_mode() {
 // pos: the position the step appends (its context length is pos + 1).
 int launch_step(qora_hip_ctx* c, bool with_lm_head, uint64_t pos) {
     ModelState& m = c->m;
-    const uint32_t np = fused_passes(m, pos);
-    if (eager_mode()) return record_step(c, with_lm_head, np);
-    hipGraphExec_t g = np ? (with_lm_head ? m.g_step_ao[np - 1] : m.g_prefill_ao[np - 1])
-                          : (with_lm_head ? m.g_step : m.g_prefill);
+    const StepAttn sa = step_attn(m, pos);
+    if (eager_mode()) return record_step(c, with_lm_head, sa.np, sa.chunked);
+    hipGraphExec_t g = !sa.np       ? (with_lm_head ? m.g_step : m.g_prefill)
+                       : sa.chunked ? (with_lm_head ? m.g_step_ch[sa.np - 1] : m.g_prefill_ch[sa.np - 1])
+                                    : (with_lm_head ? m.g_step_ao[sa.np - 1] : m.g_prefill_ao[sa.np - 1]);
     HIP_TRY(c, hipGraphLaunch(g, c->stream));
     return QORA_HIP_OK;
 }
 
-int capture_step(qora_hip_ctx* c, bool with_lm_head, uint32_t np, hipGraphExec_t* out) {
+int capture_step(qora_hip_ctx* c, bool with_lm_head, uint32_t np, hipGraphExec_t* out, bool chunked = false) {
     HIP_TRY(c, hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
-    const int rc = record_step(c, with_lm_head, np);
+    const int rc = record_step(c, with_lm_head, np, chunked);
     hipGraph_t g = nullptr;
     const hipError_t e = hipStreamEndCapture(c->stream, &g);
     if (rc) {
@@ -692,7 +733,8 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
     MALLOC(d_k, (size_t)m.L * m.cap * kvd * kvb);
     MALLOC(d_v, (size_t)m.L * m.cap * kvd * kvb);
     MALLOC(d_xacc, (size_t)m.hidden * 8);
-    MALLOC(d_qkv_acc, qkv_n * 8);
+    // q|k|v sums, then the chunked step's per-head counters (cleared with them)
+    MALLOC(d_qkv_acc, (qkv_n + kChunkCountWords) * 8);
     MALLOC(d_gu_acc, (size_t)2 * m.inter * 8);
     MALLOC(d_attn_part, (size_t)m.KVH * m.attn_s_max * m.groups * (m.hd + 2) * 4);
     MALLOC(d_ss, (size_t)m.L * 2 * kAttnMaxSplits * 4);
@@ -715,7 +757,7 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
         HIP_TRY(c, hipMemset(m.d_v, byte, (size_t)m.L * m.cap * kvd * kvb));
     }
     HIP_TRY(c, hipMemset(m.d_xacc, 0, (size_t)m.hidden * 8));
-    HIP_TRY(c, hipMemset(m.d_qkv_acc, 0, qkv_n * 8));
+    HIP_TRY(c, hipMemset(m.d_qkv_acc, 0, (qkv_n + kChunkCountWords) * 8));
     HIP_TRY(c, hipMemset(m.d_gu_acc, 0, (size_t)2 * m.inter * 8));
     HIP_TRY(c, hipMemset(m.d_pos, 0, 64));
     HIP_TRY(c, hipMemset(m.d_range, 0, 64));
@@ -739,18 +781,22 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
     //   xacc --RMSNorm+q|k|v GEMV--> qkv_acc --attention(RoPE, K/V append)-->
     //   partials --merge+o GEMV--> xacc (+=) --RMSNorm+gate|up GEMV--> gu_acc
     //   --silu*up+down GEMV--> xacc (+=)
-    // qkv_acc is cleared by the gate|up kernel and gu_acc by the o kernel
-    // (the waves it has left over), each after its last reader has finished
-    // and before its next writer starts. Below attn_o_max
-    // positions, attention and the o GEMV run as one kernel
-    // (gemv_q4m_attn_kernel) that reads qkv_acc itself.
+    // qkv_acc (with the chunked step's counters behind it) is cleared by the
+    // gate|up kernel and gu_acc by the o kernel (the waves it has left over),
+    // each after its last reader has finished and before its next writer
+    // starts. Below attn_ch_max positions attention and the o GEMV run as one
+    // kernel (gemv_q4m_attn_kernel) that reads qkv_acc itself: below
+    // attn_o_max every workgroup over the whole context, above it each over
+    // its chunk (the chunked step).
     m.p_qkv.resize(m.L);
     m.p_o.resize(m.L);
     m.p_gu.resize(m.L);
     m.p_down.resize(m.L);
     m.p_attn.resize(m.L);
     m.attn_o_max = attn_o_limit(m);
-    if (m.attn_o_max) m.p_ao.resize(m.L);
+    m.attn_ch_max = attn_ch_limit(m, c->cus);
+    m.ch_np_max = m.attn_ch_max ? (uint32_t)((m.attn_ch_max - 1u) / ((uint64_t)kFusedPass * m.pl_o.tiles)) + 1u : 0u;
+    if (m.attn_o_max || m.attn_ch_max) m.p_ao.resize(m.L);
     for (uint32_t l = 0; l < m.L; ++l) {
         const DevWeight* W[7];
         for (int j = 0; j < 7; ++j) W[j] = get_weight(c, m.wids[l * 7 + j]);
@@ -816,7 +862,8 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
         o.zero_n = 2 * m.inter;
         apply_plan(m.pl_o, &o);
         if (int rc = pack_model_gemv(c, (int)m.fmt, m.pl_o, &o)) { free_model(c); return rc; }
-        if (m.attn_o_max) m.p_ao[l] = AttnOParams{o, a};
+        if (m.attn_o_max || m.attn_ch_max)
+            m.p_ao[l] = AttnOParams{o, a, reinterpret_cast<uint32_t*>(m.d_qkv_acc + qkv_n)};
 
         GemvParams& g = m.p_gu[l];
         g = GemvParams{};
@@ -832,7 +879,7 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
         g.acc = m.d_gu_acc;
         g.zero_ptr = m.d_qkv_acc;
         g.range_flag = m.d_range;
-        g.zero_n = (uint32_t)qkv_n;
+        g.zero_n = (uint32_t)(qkv_n + kChunkCountWords);   // with the chunked step's counters
         apply_plan(m.pl_gu, &g);
         if (int rc = pack_model_gemv(c, (int)m.fmt, m.pl_gu, &g)) { free_model(c); return rc; }
 
@@ -899,6 +946,11 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
     for (uint32_t np = 1; m.attn_o_max && np <= (m.attn_o_max - 1) / kFusedPass + 1; ++np) {
         if (int rc = capture_step(c, true, np, &m.g_step_ao[np - 1])) { free_model(c); return rc; }
         if (int rc = capture_step(c, false, np, &m.g_prefill_ao[np - 1])) { free_model(c); return rc; }
+    }
+    // one chunked variant per passes-per-chunk count
+    for (uint32_t np = 1; np <= m.ch_np_max; ++np) {
+        if (int rc = capture_step(c, true, np, &m.g_step_ch[np - 1], true)) { free_model(c); return rc; }
+        if (int rc = capture_step(c, false, np, &m.g_prefill_ch[np - 1], true)) { free_model(c); return rc; }
     }
     m.host_pos = 0;
     m.ready = true;
@@ -1410,6 +1462,11 @@ extern "C" int qora_hip_prefill(qora_hip_ctx* c, const uint32_t* ids, size_t n, 
 extern "C" uint32_t qora_hip_attn_o_limit(const qora_hip_ctx* c) {
     if (!c || !c->m.ready) return 0;
     return c->m.attn_o_max;
+}
+
+extern "C" uint32_t qora_hip_attn_chunk_limit(const qora_hip_ctx* c) {
+    if (!c || !c->m.ready) return 0;
+    return c->m.attn_ch_max;
 }
 
 extern "C" int qora_hip_kv_len(qora_hip_ctx* c, uint64_t* len) {

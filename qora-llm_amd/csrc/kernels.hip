@@ -453,29 +453,55 @@ bool attn_o_supported(const GemvPlan& pl, uint32_t hd, uint32_t H, uint32_t grou
            groups >= 1 && groups <= (uint32_t)kAttnMaxGroups;
 }
 
-template <int HD, bool F16KV>
+template <int HD, bool F16KV, bool CH>
 static hipError_t launch_attn_o_hd(const GemvPlan& pl, const AttnOParams& p, uint32_t np, hipStream_t stream) {
     const dim3 grid(pl.blocks()), block(kFusedWaves * kWave);
     switch (np) {
-    case 1: hipLaunchKernelGGL((gemv_q4m_attn_kernel<HD, F16KV, 1>), grid, block, 0, stream, p); break;
-    case 2: hipLaunchKernelGGL((gemv_q4m_attn_kernel<HD, F16KV, 2>), grid, block, 0, stream, p); break;
-    case 3: hipLaunchKernelGGL((gemv_q4m_attn_kernel<HD, F16KV, 3>), grid, block, 0, stream, p); break;
-    case 4: hipLaunchKernelGGL((gemv_q4m_attn_kernel<HD, F16KV, 4>), grid, block, 0, stream, p); break;
-    case 5: hipLaunchKernelGGL((gemv_q4m_attn_kernel<HD, F16KV, 5>), grid, block, 0, stream, p); break;
-    case 6: hipLaunchKernelGGL((gemv_q4m_attn_kernel<HD, F16KV, 6>), grid, block, 0, stream, p); break;
-    case 7: hipLaunchKernelGGL((gemv_q4m_attn_kernel<HD, F16KV, 7>), grid, block, 0, stream, p); break;
-    case 8: hipLaunchKernelGGL((gemv_q4m_attn_kernel<HD, F16KV, 8>), grid, block, 0, stream, p); break;
+    case 1: hipLaunchKernelGGL((gemv_q4m_attn_kernel<HD, F16KV, 1, CH>), grid, block, 0, stream, p); break;
+    case 2: hipLaunchKernelGGL((gemv_q4m_attn_kernel<HD, F16KV, 2, CH>), grid, block, 0, stream, p); break;
+    case 3: hipLaunchKernelGGL((gemv_q4m_attn_kernel<HD, F16KV, 3, CH>), grid, block, 0, stream, p); break;
+    case 4: hipLaunchKernelGGL((gemv_q4m_attn_kernel<HD, F16KV, 4, CH>), grid, block, 0, stream, p); break;
+    case 5: hipLaunchKernelGGL((gemv_q4m_attn_kernel<HD, F16KV, 5, CH>), grid, block, 0, stream, p); break;
+    case 6: hipLaunchKernelGGL((gemv_q4m_attn_kernel<HD, F16KV, 6, CH>), grid, block, 0, stream, p); break;
+    case 7: hipLaunchKernelGGL((gemv_q4m_attn_kernel<HD, F16KV, 7, CH>), grid, block, 0, stream, p); break;
+    case 8: hipLaunchKernelGGL((gemv_q4m_attn_kernel<HD, F16KV, 8, CH>), grid, block, 0, stream, p); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
 }
 
-hipError_t launch_attn_o(const GemvPlan& pl, const AttnOParams& p, uint32_t np, hipStream_t stream) {
+hipError_t launch_attn_o(const GemvPlan& pl, const AttnOParams& p, uint32_t np, bool chunked, hipStream_t stream) {
+    if (chunked && !p.ch_count) return hipErrorInvalidValue;
     if (p.a.hd == 128) {
-        return p.a.kv_f16 ? launch_attn_o_hd<128, true>(pl, p, np, stream)
-                          : launch_attn_o_hd<128, false>(pl, p, np, stream);
+        if (chunked)
+            return p.a.kv_f16 ? launch_attn_o_hd<128, true, true>(pl, p, np, stream)
+                              : launch_attn_o_hd<128, false, true>(pl, p, np, stream);
+        return p.a.kv_f16 ? launch_attn_o_hd<128, true, false>(pl, p, np, stream)
+                          : launch_attn_o_hd<128, false, false>(pl, p, np, stream);
     }
-    return p.a.kv_f16 ? launch_attn_o_hd<64, true>(pl, p, np, stream) : launch_attn_o_hd<64, false>(pl, p, np, stream);
+    if (chunked)
+        return p.a.kv_f16 ? launch_attn_o_hd<64, true, true>(pl, p, np, stream)
+                          : launch_attn_o_hd<64, false, true>(pl, p, np, stream);
+    return p.a.kv_f16 ? launch_attn_o_hd<64, true, false>(pl, p, np, stream)
+                      : launch_attn_o_hd<64, false, false>(pl, p, np, stream);
+}
+
+bool attn_chunk_supported(const GemvPlan& pl, uint32_t hd, uint32_t H, uint32_t groups, uint32_t s_max, int cus) {
+    if (!attn_o_supported(pl, hd, H, groups) || pl.tiles > kChunkMaxTiles || H > kChunkHeads || pl.tiles > s_max)
+        return false;
+    // every workgroup of a launch waits for the other column tiles of its
+    // head: the grid must be resident at once
+    int per_cu = 0;
+    const hipError_t e =
+        hd == 128 ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, gemv_q4m_attn_kernel<128, false, 8, true>,
+                                                                 kFusedWaves * kWave, 0)
+                  : hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, gemv_q4m_attn_kernel<64, false, 8, true>,
+                                                                 kFusedWaves * kWave, 0);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    return (uint64_t)pl.blocks() <= (uint64_t)per_cu * (uint64_t)std::max(cus, 1);
 }
 
 hipError_t launch_attn_combine(const AttnCombineParams& p, hipStream_t stream) {

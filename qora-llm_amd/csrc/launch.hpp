@@ -88,8 +88,12 @@ hipError_t launch_attn_combine(const AttnCombineParams& p, hipStream_t stream);
 // prologue (gemv_q4m_attn_kernel). The o plan must be an MFMA plan with one
 // group per wave and K slices of exactly one head (kr = hd, splits = H).
 bool attn_o_supported(const GemvPlan& pl, uint32_t hd, uint32_t H, uint32_t groups);
-// The fused short-context step for contexts of 32 (np - 1) < L <= 32 np positions, np in 1..8.
-hipError_t launch_attn_o(const GemvPlan& pl, const AttnOParams& p, uint32_t np, hipStream_t stream);
+// The fused short-context step for contexts of 32 (np - 1) < L <= 32 np positions, np in 1..8;
+// chunked: the chunked step, each column tile over 32 np positions (tiles * 32 np >= L).
+hipError_t launch_attn_o(const GemvPlan& pl, const AttnOParams& p, uint32_t np, bool chunked, hipStream_t stream);
+// The chunked step on this plan: at most kChunkMaxTiles column tiles, a.part
+// large enough for H * tiles states (tiles <= s_max), the grid resident at once.
+bool attn_chunk_supported(const GemvPlan& pl, uint32_t hd, uint32_t H, uint32_t groups, uint32_t s_max, int cus);
 
 hipError_t launch_embed(const EmbedParams& p, hipStream_t stream);
 hipError_t launch_dequant_q4(const uint8_t* packed, const uint16_t* scales, uint64_t k, uint64_t n,

@@ -282,6 +282,15 @@ constexpr int kAttnMaxSplits = 64;
 constexpr int kFusedWaves = 8;
 constexpr uint32_t kFusedPass = 32;
 constexpr int kFusedMaxPasses = 8;
+// chunked step: at most this many column tiles (position chunks) per head,
+// and the polls of a workgroup waiting for its head's chunk states before
+// it gives up and flags the step (the states of every workgroup of a launch
+// are in place within microseconds when the grid is resident at once)
+constexpr uint32_t kChunkMaxTiles = 16;
+constexpr uint32_t kChunkHeads = 64;
+constexpr uint32_t kChunkSpin = 1u << 20;
+constexpr uint32_t kChunkCountStride = 32;   // u32 counters 128 bytes apart: [kChunkHeads][32]
+constexpr uint32_t kChunkCountWords = kChunkHeads * kChunkCountStride / 2;   // as int64 words
 
 struct AttnParams {
     const float* q;            // kernel-level: q [H*hd] fp32, already rotated
@@ -315,6 +324,12 @@ struct AttnParams {
 struct AttnOParams {
     GemvParams g;
     AttnParams a;
+    // chunked step (gemv_q4m_attn_kernel with CH): workgroup (head h, column
+    // tile j) attends over positions [32 NP j, 32 NP (j + 1)) and leaves its
+    // state (acc[hd], m, l) in a.part at [h][j]; ch_count[h * 32] counts the
+    // states in place. The counters are zero when the launch starts (the
+    // next launch that clears this accumulator region clears them again).
+    uint32_t* ch_count;
 };
 
 struct AttnCombineParams {

@@ -1,8 +1,11 @@
-"""The fused short-context decode step on the GPU: each layer's attention
-computed inside the o-projection kernel (gemv_q4m_attn_kernel) for steps that
-append a position below qora_hip_attn_o_limit, the split attention kernel
-above it. Both against the oracle (gemv.rs:914-989 inside forward_decode_raw,
-gemv.rs:872-1019), across the bound, from the first position, at every
+"""The fused decode steps on the GPU: each layer's attention computed inside
+the o-projection kernel (gemv_q4m_attn_kernel) for steps that append a
+position below qora_hip_attn_o_limit (every workgroup over the whole
+context), the chunked step up to qora_hip_attn_chunk_limit (each column-tile
+workgroup of a head over its own chunk of positions, the chunk states
+exchanged between the workgroups), and the split attention kernel above.
+Against the oracle (gemv.rs:914-989 inside forward_decode_raw,
+gemv.rs:872-1019), across the bounds, from the first position, at every
 compiled pass count, and with f32 and f16 caches."""
 import numpy as np
 import pytest
@@ -40,17 +43,46 @@ def test_limit_policy(ctx, pkg, monkeypatch):
     monkeypatch.delenv("QORA_HIP_ATTN_O")
     # F16 weights run the VALU GEMVs: no fused step
     assert pkg.HipBackend(ctx, _model(pkg, 64, fmt=0), kv_capacity=128).attn_o_limit() == 0
+    assert pkg.HipBackend(ctx, _model(pkg, 64, fmt=0), kv_capacity=128).attn_chunk_limit() == 0
 
 
+def test_chunk_limit_policy(ctx, pkg, monkeypatch):
+    """The chunked step covers [attn_o_limit, attn_chunk_limit): by default
+    48 positions per column tile, at most 8 passes of 32 positions per tile,
+    never above the capacity, and never at or below the fused bound;
+    QORA_HIP_ATTN_CHUNK sets it."""
+    w = _model(pkg, 128, positions=4096)
+    monkeypatch.setenv("QORA_HIP_ATTN_CHUNK", "1000000")
+    top = pkg.HipBackend(ctx, w, kv_capacity=4096).attn_chunk_limit()
+    assert top > 256 and top % 256 == 0                 # 8 passes x 32 positions x the column tiles
+    tiles = top // 256
+    monkeypatch.delenv("QORA_HIP_ATTN_CHUNK")
+    dflt = 48 * tiles if 48 * tiles > 256 else 0        # none when at or below the fused bound
+    assert pkg.HipBackend(ctx, w, kv_capacity=4096).attn_chunk_limit() == dflt
+    assert pkg.HipBackend(ctx, w, kv_capacity=300).attn_chunk_limit() == (300 if dflt else 0)
+    assert pkg.HipBackend(ctx, w, kv_capacity=256).attn_chunk_limit() == 0   # all fused
+    monkeypatch.setenv("QORA_HIP_ATTN_CHUNK", "0")
+    assert pkg.HipBackend(ctx, w, kv_capacity=1024).attn_chunk_limit() == 0
+    monkeypatch.setenv("QORA_HIP_ATTN_CHUNK", "600")
+    assert pkg.HipBackend(ctx, w, kv_capacity=1024).attn_chunk_limit() == min(600, top)
+    monkeypatch.setenv("QORA_HIP_ATTN_O", "0")          # chunked from the first position
+    be = pkg.HipBackend(ctx, w, kv_capacity=1024)
+    assert be.attn_o_limit() == 0 and be.attn_chunk_limit() == min(600, top)
+
+
+@pytest.mark.parametrize("after", ["split", "chunked"])
 @pytest.mark.parametrize("hd,kv_dtype", [(64, 0), (128, 0), (128, 1), (64, 1)])
-def test_steps_across_the_bound_match_oracle(ctx, pkg, orc, monkeypatch, hd, kv_dtype):
+def test_steps_across_the_bound_match_oracle(ctx, pkg, orc, monkeypatch, hd, kv_dtype, after):
     """Bound 24: a 12-token prompt, then 24 teacher-forced steps appending
-    positions 12..35 (fused up to 23, split from 24 on)."""
-    print(f"case attn_o across bound hd={hd} kv={kv_dtype}", flush=True)
+    positions 12..35 (fused up to 23, split or chunked from 24 on)."""
+    print(f"case attn_o across bound hd={hd} kv={kv_dtype} then {after}", flush=True)
     monkeypatch.setenv("QORA_HIP_ATTN_O", "24")
+    if after == "split":
+        monkeypatch.setenv("QORA_HIP_ATTN_CHUNK", "0")
     w = _model(pkg, hd, positions=128)
     be = pkg.HipBackend(ctx, w, kv_capacity=128, kv_dtype=kv_dtype)
     assert be.attn_o_limit() == 24
+    assert (be.attn_chunk_limit() == 0) == (after == "split")
     om = orc.OracleModel(w, kv_capacity=128, T=4)
     tol = REL_TOL if kv_dtype == 0 else 5e-3
     prompt = pkg.synth_tokens(hd, 2000, 12, w.config.vocab)
@@ -95,7 +127,7 @@ def test_fused_every_pass_count(ctx, pkg, orc, kv_dtype):
     Caches of n uploaded positions, then two steps appending n and n + 1,
     for n around every pass boundary: each pass count, the appended row as
     the first, a middle and the last position of its pass, and the step from
-    the last fused position (255) to the split kernel (256)."""
+    the last fused position (255) to the step kind above the bound (256)."""
     print(f"case attn_o pass counts kv={kv_dtype}", flush=True)
     cap = 320
     w = _model(pkg, 128, positions=cap, seed=5)
@@ -121,12 +153,16 @@ def test_fused_every_pass_count(ctx, pkg, orc, kv_dtype):
         assert rel_err(k, kr) <= tol and rel_err(v, vr) <= tol, n
 
 
-@pytest.mark.parametrize("bound,prompt_len", [(30, 10), (256, 25)])
-def test_device_chained_greedy_crosses_the_bound(ctx, pkg, orc, monkeypatch, bound, prompt_len):
+@pytest.mark.parametrize("bound,prompt_len,chunk", [(30, 10, "0"), (30, 10, None), (256, 25, None), (0, 40, None)])
+def test_device_chained_greedy_crosses_the_bound(ctx, pkg, orc, monkeypatch, bound, prompt_len, chunk):
     """generate_greedy launches every step from the host in one call; each
-    picks its graph by the position it appends: across the fused/split bound
-    (30), and across the fused kernel's pass counts (positions 25..64)."""
+    picks its graph by the position it appends: across the fused/split and
+    fused/chunked bounds (30), across the fused kernel's pass counts
+    (positions 25..64), and across the chunked step's (bound 0: chunked from
+    the prompt, positions 40..79)."""
     monkeypatch.setenv("QORA_HIP_ATTN_O", str(bound))
+    if chunk is not None:
+        monkeypatch.setenv("QORA_HIP_ATTN_CHUNK", chunk)
     w = _model(pkg, 128, positions=128, seed=6)
     be = pkg.HipBackend(ctx, w, kv_capacity=128)
     om = orc.OracleModel(w, kv_capacity=128, T=4)
@@ -134,3 +170,50 @@ def test_device_chained_greedy_crosses_the_bound(ctx, pkg, orc, monkeypatch, bou
     ref, _ = om.greedy(prompt, 40)
     _, first = be.raw_prefill(prompt, want_logits=False)
     assert [first] + be.generate_greedy(first, 39).tolist() == ref
+
+
+@pytest.mark.parametrize("mode,kv_dtype", [("chunked", 0), ("chunked", 1), ("split", 0)])
+def test_chunked_every_pass_count(ctx, pkg, orc, monkeypatch, mode, kv_dtype):
+    """The chunked step is compiled per count of 32-position passes per
+    column tile (1..8); with the fused step off it runs from the first
+    position. Caches of n uploaded positions, then two steps appending n and
+    n + 1, for n around every chunk and pass-count boundary of the model's
+    column tiles (chunks wholly past the context, the appended row as the
+    first and last position of a chunk, the last position below the bound);
+    the same positions through the split attention kernel (mode split)."""
+    print(f"case chunked pass counts {mode} kv={kv_dtype}", flush=True)
+    monkeypatch.setenv("QORA_HIP_ATTN_O", "0")
+    monkeypatch.setenv("QORA_HIP_ATTN_CHUNK", "0" if mode == "split" else "1000000")
+    w = _model(pkg, 128, positions=4096, seed=7)
+    probe = pkg.HipBackend(ctx, w, kv_capacity=4096)
+    top = probe.attn_chunk_limit()
+    del probe
+    if mode == "split":
+        assert top == 0
+        top = 512
+    cap = top
+    tiles = top // 256                                   # chunk of np passes: 32 np positions per column tile
+    be = pkg.HipBackend(ctx, w, kv_capacity=cap, kv_dtype=kv_dtype)
+    assert be.attn_o_limit() == 0
+    assert be.attn_chunk_limit() == (cap if mode == "chunked" else 0)
+    om = orc.OracleModel(w, kv_capacity=cap, T=4)
+    r = np.random.default_rng(22)
+    kvd = w.config.num_kv_heads * w.config.head_dim
+    tol = REL_TOL if kv_dtype == 0 else 5e-3
+    step = 32 * tiles                                    # positions per pass count
+    ns = {0, 1, 31, 32, 33, 63, 64, step - 2, step - 1, step, step + 1, 2 * step - 1, 2 * step + 31,
+          3 * step + 64, 4 * step - 1, 5 * step + 7, 6 * step - 32, 7 * step, 8 * step - 3, cap - 2}
+    for n in sorted(x for x in ns if 0 <= x <= cap - 2):
+        for layer in range(w.config.num_layers):
+            k = r.standard_normal((n, kvd), dtype=np.float32)
+            v = r.standard_normal((n, kvd), dtype=np.float32)
+            if kv_dtype:
+                k, v = k.astype(np.float16).astype(np.float32), v.astype(np.float16).astype(np.float32)
+            be.kv_upload(layer, k, v)
+            om.kv_set(layer, k, v)
+        for t in pkg.synth_tokens(7, 3001 + n, 2, w.config.vocab):
+            logits, _ = be.forward_decode_raw(int(t))
+            assert rel_err(logits, om.forward_decode(int(t))) <= tol, n
+        k, v = be.kv_layer(3)
+        kr, vr = om.kv_layer(3)
+        assert rel_err(k, kr) <= tol and rel_err(v, vr) <= tol, n
