@@ -146,8 +146,9 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnParams p) {
     const uint64_t cps = kv_pos_stride(p), coff = kv_head_off(p, kvh);   // cache layout
     const uint32_t nq = G * hd;
 
-    // ---- position-independent loads, in flight with the position ----
-    const int32_t pos_raw = p.pos ? *p.pos : (int32_t)p.L - 1;
+    // ---- position-independent loads, in flight with the position (a scalar
+    // load: waiting for it does not wait for the vector loads) ----
+    const int32_t pos_raw = p.pos ? ld_scalar_i32(p.pos) : (int32_t)p.L - 1;
     long long qa[2] = {0, 0}, qb[2] = {0, 0};
     long long ka = 0, kb = 0, va = 0;
     float ssp = 0.f;
@@ -170,7 +171,13 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnParams p) {
     const uint32_t L = (uint32_t)pos_raw + 1u;
     const uint32_t chunk = p.chunk ? p.chunk : attn_chunk_for(L);
     const uint32_t p0 = split * chunk;
-    if (p0 >= L) return;
+    if (p0 >= L) {
+        // the loads above are used on this path too, so the compiler issues
+        // them before the position is known instead of sinking them past
+        // this branch (behind a wait for the position)
+        asm volatile("" ::"v"(qa[0]), "v"(qa[1]), "v"(qb[0]), "v"(qb[1]), "v"(ka), "v"(kb), "v"(va), "v"(ssp));
+        return;
+    }
     const uint32_t p1 = min(L, p0 + chunk);
     const uint32_t cur = L - 1;                        // position appended this step
     const bool has_new = model && cur >= p0 && cur < p1;
@@ -440,8 +447,9 @@ __global__ __launch_bounds__(256 * kAttnLongNsg) void attn_decode_long_kernel(At
     const uint64_t cps = kv_pos_stride(p), coff = kv_head_off(p, kvh);   // cache layout
     const uint32_t nq = G * hd;
 
-    // ---- position-independent loads, in flight with the position ----
-    const int32_t pos_raw = p.pos ? *p.pos : (int32_t)p.L - 1;
+    // ---- position-independent loads, in flight with the position (a scalar
+    // load: waiting for it does not wait for the vector loads) ----
+    const int32_t pos_raw = p.pos ? ld_scalar_i32(p.pos) : (int32_t)p.L - 1;
     long long qa[2] = {0, 0}, qb[2] = {0, 0};
     long long ka = 0, kb = 0, va = 0;
     float ssp = 0.f;
@@ -464,7 +472,11 @@ __global__ __launch_bounds__(256 * kAttnLongNsg) void attn_decode_long_kernel(At
     const uint32_t L = (uint32_t)pos_raw + 1u;
     const uint32_t chunk = p.chunk ? p.chunk : attn_chunk_for(L);
     const uint32_t p0 = split * chunk;
-    if (p0 >= L) return;                               // whole block: no barrier reached yet
+    if (p0 >= L) {                                     // whole block: no barrier reached yet
+        // used on this path too: the loads above go out before the position
+        asm volatile("" ::"v"(qa[0]), "v"(qa[1]), "v"(qb[0]), "v"(qb[1]), "v"(ka), "v"(kb), "v"(va), "v"(ssp));
+        return;
+    }
     const uint32_t p1 = min(L, p0 + chunk);
     const uint32_t cur = L - 1;                        // position appended this step
     const bool has_new = model && cur >= p0 && cur < p1;
