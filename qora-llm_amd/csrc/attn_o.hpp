@@ -59,7 +59,7 @@ __device__ __forceinline__ float4 sel4(bool c, float4 a, float4 b) {
 // halves around a block barrier. chunk_publish (wave 0): the chunk's
 // un-normalised state (acc = xr, m = M, l = den) goes to a.part at [h][j]
 // and is counted in the head's counter; then lane 0 waits until the head's
-// `tiles` states are counted (bounded: past kChunkSpin polls the step is
+// `tiles` states are counted (bounded: past ch_spin polls the step is
 // flagged through the range flag and its output is not valid). The states
 // are written and read with device-scope atomic stores and loads, and the
 // count is raised only once the last store of the wave has returned (an
@@ -87,7 +87,7 @@ __device__ __forceinline__ void chunk_publish(const AttnOParams& ap, uint32_t h,
     if (lane == 0) {
         __hip_atomic_fetch_add(count, one, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         uint32_t n = 0;
-        for (uint32_t it = 0; it < kChunkSpin; ++it) {
+        for (uint32_t it = 0; it < ap.ch_spin; ++it) {
             n = __hip_atomic_load(count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             if (n >= ap.g.tiles) break;
             __builtin_amdgcn_s_sleep(2);

@@ -862,8 +862,13 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
         o.zero_n = 2 * m.inter;
         apply_plan(m.pl_o, &o);
         if (int rc = pack_model_gemv(c, (int)m.fmt, m.pl_o, &o)) { free_model(c); return rc; }
-        if (m.attn_o_max || m.attn_ch_max)
-            m.p_ao[l] = AttnOParams{o, a, reinterpret_cast<uint32_t*>(m.d_qkv_acc + qkv_n)};
+        if (m.attn_o_max || m.attn_ch_max) {
+            // the chunked step's bounded wait; QORA_HIP_CHUNK_SPIN (a test
+            // hook) shortens it, 0 forcing the timeout path
+            const char* spin = tuning_env("QORA_HIP_CHUNK_SPIN");
+            m.p_ao[l] = AttnOParams{o, a, reinterpret_cast<uint32_t*>(m.d_qkv_acc + qkv_n),
+                                    spin ? (uint32_t)std::strtoul(spin, nullptr, 10) : kChunkSpin};
+        }
 
         GemvParams& g = m.p_gu[l];
         g = GemvParams{};

@@ -330,6 +330,7 @@ struct AttnOParams {
     // states in place. The counters are zero when the launch starts (the
     // next launch that clears this accumulator region clears them again).
     uint32_t* ch_count;
+    uint32_t ch_spin;          // polls before a workgroup gives up waiting (kChunkSpin)
 };
 
 struct AttnCombineParams {

@@ -217,3 +217,34 @@ def test_chunked_every_pass_count(ctx, pkg, orc, monkeypatch, mode, kv_dtype):
         k, v = be.kv_layer(3)
         kr, vr = om.kv_layer(3)
         assert rel_err(k, kr) <= tol and rel_err(v, vr) <= tol, n
+
+
+def test_chunked_wait_timeout_is_reported(ctx, pkg, orc, monkeypatch):
+    """The chunked step's workgroups wait a bounded number of polls for their
+    head's chunk states; one that gives up flags the step, which then
+    returns QORA_HIP_E_RANGE instead of results, and later steps are refused
+    until the cache is reset. Forced from the host with a spin limit of 0
+    (every workgroup gives up at once; all its accesses stay in bounds), then
+    the same model with the normal limit decodes as the oracle does."""
+    print("case chunked wait timeout", flush=True)
+    monkeypatch.setenv("QORA_HIP_ATTN_O", "0")
+    monkeypatch.setenv("QORA_HIP_ATTN_CHUNK", "1000000")
+    monkeypatch.setenv("QORA_HIP_TUNING", "1")
+    monkeypatch.setenv("QORA_HIP_CHUNK_SPIN", "0")
+    w = _model(pkg, 128, positions=256, seed=8)
+    prompt = pkg.synth_tokens(8, 2200, 20, w.config.vocab)
+    be = pkg.HipBackend(ctx, w, kv_capacity=256)
+    assert be.attn_chunk_limit() > 0
+    be.raw_prefill(prompt, want_logits=False)                # batched prefill: no chunked step
+    for want in (True, False):
+        with pytest.raises(pkg.QoraHipError) as e:
+            be.forward_decode_raw(5, want_logits=want)
+        assert e.value.code == pkg.QORA_HIP_E_RANGE
+    monkeypatch.delenv("QORA_HIP_CHUNK_SPIN")
+    be = pkg.HipBackend(ctx, w, kv_capacity=256)
+    om = orc.OracleModel(w, kv_capacity=256, T=4)
+    logits, _ = be.raw_prefill(prompt)
+    assert rel_err(logits, om.prefill(prompt)) <= REL_TOL
+    for t in (5, 9):
+        logits, _ = be.forward_decode_raw(t)
+        assert rel_err(logits, om.forward_decode(t)) <= REL_TOL
