@@ -9,6 +9,12 @@
 // items, same packed weights). The 16 column tiles of a head repeat its
 // attention; at a short context that costs less than a launch.
 //
+// Chunked (CH, mid contexts): the column tiles of a head split its context
+// instead, tile j attending over positions [32 NP j, 32 NP (j + 1)); each
+// leaves its chunk's softmax state in global memory, counts it in the head's
+// counter, waits (bounded) for the head's other chunks and merges them in
+// chunk order before its matrix-core pass (chunk_publish, chunk_merge).
+//
 // Attention (gemv.rs:914-989, softmax_raw gemv.rs:782-793) of head h over
 // KV head h / groups, positions [0, L), L = *pos + 1:
 //   * the kernel is compiled per pass count NP (32 positions a pass, contexts
