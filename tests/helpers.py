@@ -15,6 +15,18 @@ def rel_err(a, b) -> float:
     return float(np.max(np.abs(a - b))) / denom if a.size else 0.0
 
 
+def elem_err(a, b, mag) -> float:
+    """max_j |a_j - b_j| / mag_j, each output's error against its own scale
+    mag_j = sum_k |x_k w_kj| (what the rounding error of a sum of products is
+    proportional to). Unlike rel_err, which measures every error against the
+    largest output, this bounds the small outputs too; an output whose terms
+    are all zero (mag_j = 0) must be exact."""
+    a = np.asarray(a, dtype=np.float64)
+    b = np.asarray(b, dtype=np.float64)
+    m = np.asarray(mag, dtype=np.float64)
+    return float(np.max(np.abs(a - b) / (m + 1e-300))) if a.size else 0.0
+
+
 def rng(seed):
     return np.random.default_rng(seed)
 

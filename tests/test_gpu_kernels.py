@@ -8,7 +8,7 @@ import ctypes
 import numpy as np
 import pytest
 
-from helpers import REL_TOL, device, dequant_np, exact_q4, random_q4, rel_err, rng
+from helpers import REL_TOL, dequant_np, device, elem_err, exact_q4, random_q4, rel_err, rng
 
 pytestmark = pytest.mark.gpu
 
@@ -47,8 +47,10 @@ def test_gemv_q4_random_vs_oracle(ctx, orc, pkg, k, n):
     for T in (1, 12):
         ref = orc.gemv_q4(x, packed, scales, k, n, T=T)
         assert rel_err(y, ref) <= REL_TOL, (T, rel_err(y, ref))
-    truth = dequant_np(packed, scales, k, n).T @ x.astype(np.float64)
+    wd = dequant_np(packed, scales, k, n)
+    truth = wd.T @ x.astype(np.float64)
     assert rel_err(y, truth) <= 1e-5
+    assert elem_err(y, truth, np.abs(wd).T @ np.abs(x.astype(np.float64))) <= 1e-5
 
 
 def test_gemv_q4_one_hot_is_dequant_row(ctx, orc):
@@ -140,8 +142,10 @@ def test_rowdot_q4_vs_oracle_lm_head(ctx, orc, pkg, rows, cols):
         got = d.get(y, rows, np.float32)
     ref = orc.lm_head_q4(x, packed, scales, rows, cols)
     assert rel_err(got, ref) <= REL_TOL
-    truth = dequant_np(packed, scales, rows, cols) @ x.astype(np.float64)
+    wd = dequant_np(packed, scales, rows, cols)
+    truth = wd @ x.astype(np.float64)
     assert rel_err(got, truth) <= 1e-5
+    assert elem_err(got, truth, np.abs(wd) @ np.abs(x.astype(np.float64))) <= 1e-5
 
 
 def test_rowdot_q4_exact_regime(ctx, orc):

@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 
 import __graft_entry__ as entry
-from helpers import REL_TOL, dequant_np, device, exact_q4, rel_err, rng
+from helpers import REL_TOL, dequant_np, device, elem_err, exact_q4, rel_err, rng
 from model_f64 import F64Model
 
 pytestmark = pytest.mark.gpu
@@ -38,6 +38,7 @@ def test_gemm_q4_vs_oracle_and_truth(ctx, orc, pkg, k, n, T):
     W = dequant_np(packed, scales, k, n)
     truth = x.astype(np.float64) @ W
     assert rel_err(y, truth) <= TRUTH_TOL
+    assert elem_err(y, truth, np.abs(x.astype(np.float64)) @ np.abs(W)) <= TRUTH_TOL
     for t in sorted({0, T // 2, T - 1}):
         ref = orc.gemv_q4(x[t], packed, scales, k, n, T=1)
         assert rel_err(y[t], ref) <= REL_TOL
@@ -51,8 +52,10 @@ def test_gemm_f16_vs_oracle_and_truth(ctx, orc, pkg, k, n, T):
     wid = ctx.upload(pkg.Weight(k=k, n=n, data=w))
     with device(ctx) as d:
         y = _gemm(ctx, d, wid, x, T, n)
-    truth = x.astype(np.float64) @ w.view(np.float16).astype(np.float64).reshape(k, n)
+    W = w.view(np.float16).astype(np.float64).reshape(k, n)
+    truth = x.astype(np.float64) @ W
     assert rel_err(y, truth) <= TRUTH_TOL
+    assert elem_err(y, truth, np.abs(x.astype(np.float64)) @ np.abs(W)) <= TRUTH_TOL
     for t in (0, T - 1):
         assert rel_err(y[t], orc.gemv_f16(x[t], w, k, n, T=1)) <= REL_TOL
 

@@ -10,7 +10,7 @@ sums are compared bit-exactly with the reference-layout entry point."""
 import numpy as np
 import pytest
 
-from helpers import REL_TOL, device, dequant_np, exact_q4, rel_err
+from helpers import REL_TOL, device, dequant_np, elem_err, exact_q4, rel_err
 
 pytestmark = pytest.mark.gpu
 
@@ -46,10 +46,15 @@ def test_prepared_q4_vs_oracle_and_truth(ctx, orc, pkg, k, n):
     finally:
         ctx.gemv_release(gid)
     y = acc / FIX
+    wd = dequant_np(packed, scales, k, n)
+    mag = np.abs(wd).T @ np.abs(x.astype(np.float64))     # each output's own scale
     for T in (1, 12):
-        assert rel_err(y, orc.gemv_q4(x, packed, scales, k, n, T=T)) <= REL_TOL
-    truth = dequant_np(packed, scales, k, n).T @ x.astype(np.float64)
+        ref = orc.gemv_q4(x, packed, scales, k, n, T=T)
+        assert rel_err(y, ref) <= REL_TOL
+        assert elem_err(y, ref, mag) <= REL_TOL
+    truth = wd.T @ x.astype(np.float64)
     assert rel_err(y, truth) <= TRUTH_TOL
+    assert elem_err(y, truth, mag) <= TRUTH_TOL
 
 
 @pytest.mark.parametrize("k,n", [(2048, 2048), (37, 224), (4097, 1056)])
@@ -149,8 +154,10 @@ def test_prepared_f16_vs_oracle(ctx, orc, pkg, k, n):
     assert np.array_equal((acc / FIX).astype(np.float32), y_ref_layout)
     for avx in (False, True):
         assert rel_err(acc / FIX, orc.gemv_f16(x, w, k, n, avx512=avx)) <= REL_TOL
-    truth = w.view(np.float16).astype(np.float64).reshape(k, n).T @ x.astype(np.float64)
+    wd = w.view(np.float16).astype(np.float64).reshape(k, n)
+    truth = wd.T @ x.astype(np.float64)
     assert rel_err(acc / FIX, truth) <= F16_TRUTH_TOL
+    assert elem_err(acc / FIX, truth, np.abs(wd).T @ np.abs(x.astype(np.float64))) <= F16_TRUTH_TOL
 
 
 @pytest.mark.parametrize("k,n", [(2048, 11008), (37, 224)])
