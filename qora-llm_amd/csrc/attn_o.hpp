@@ -257,8 +257,8 @@ __global__ __launch_bounds__(kFusedWaves * kWave) void gemv_q4m_attn_kernel(Attn
     uint32_t sw[(NZ + 1) / 2];
     int esg[GW];
     const uint32_t mwave = (uint32_t)wave % NW;
-    gemv_q4m_load_scales<GW, NZ>(p, (uint64_t)item * NW + mwave, lane, sw, esg);
-    gemv_q4m_load_weights<GW, NKB>(p, (uint64_t)item * NW + mwave, lane, wq);
+    gemv_q4m_load_scales<GW, NZ>(p.ts, p.tes, (uint64_t)item * NW + mwave, lane, sw, esg);
+    gemv_q4m_load_weights<GW, NKB>(p.tw, (uint64_t)item * NW + mwave, lane, wq);
     GemvOut<GW> out{};
     if (wave < NW) out = gemv_q4m_out<GW>(p, tile, wave);
     __builtin_amdgcn_sched_barrier(0);

@@ -122,8 +122,8 @@ __device__ __forceinline__ v4i32 q4_bfrag(uint32_t w0, uint32_t w1) {
 
 // Weight fragments of one wave: [group][K block] x 16 B per lane.
 template <int GW, int NKB>
-__device__ __forceinline__ void gemv_q4m_load_weights(const GemvParams& p, uint64_t bw, int lane, uint4 (&wq)[GW][NKB]) {
-    const uint8_t* src = p.tw + bw * (uint64_t)(GW * NKB * 1024) + (uint32_t)lane * 16u;
+__device__ __forceinline__ void gemv_q4m_load_weights(const uint8_t* tw, uint64_t bw, int lane, uint4 (&wq)[GW][NKB]) {
+    const uint8_t* src = tw + bw * (uint64_t)(GW * NKB * 1024) + (uint32_t)lane * 16u;
 #pragma unroll
     for (int g = 0; g < GW; ++g)
 #pragma unroll
@@ -135,9 +135,9 @@ __device__ __forceinline__ void gemv_q4m_load_weights(const GemvParams& p, uint6
 // quantisation reads them: taking them to a scalar here would wait for the
 // load before the weight loads are issued.
 template <int GW, int NZ>
-__device__ __forceinline__ void gemv_q4m_load_scales(const GemvParams& p, uint64_t bw, int lane,
+__device__ __forceinline__ void gemv_q4m_load_scales(const uint16_t* ts, const int8_t* tes, uint64_t bw, int lane,
                                                      uint32_t (&sw)[(NZ + 1) / 2], int (&esg)[GW]) {
-    const uint16_t* src = p.ts + (bw * 64u + (uint32_t)lane) * NZ;
+    const uint16_t* src = ts + (bw * 64u + (uint32_t)lane) * NZ;
     if constexpr (NZ >= 8) {
 #pragma unroll
         for (int h = 0; h < NZ / 8; ++h) {
@@ -157,7 +157,7 @@ __device__ __forceinline__ void gemv_q4m_load_scales(const GemvParams& p, uint64
         sw[0] = src[0];
     }
 #pragma unroll
-    for (int g = 0; g < GW; ++g) esg[g] = (int)p.tes[bw * GW + g];
+    for (int g = 0; g < GW; ++g) esg[g] = (int)tes[bw * GW + g];
 }
 
 
@@ -507,10 +507,10 @@ __device__ __forceinline__ void gemv_q4m_body(const GemvParams& p, uint32_t bloc
         // ---- matrix-core waves: every item's scales first (the quantisation needs them), then weights ----
 #pragma unroll
         for (int j = 0; j < IPW; ++j)
-            if ((uint32_t)j < nit) gemv_q4m_load_scales<GW, NZ>(p, (uint64_t)(block + (uint32_t)j * nblocks) * NW + wave, lane, sw[j], esg[j]);
+            if ((uint32_t)j < nit) gemv_q4m_load_scales<GW, NZ>(p.ts, p.tes, (uint64_t)(block + (uint32_t)j * nblocks) * NW + wave, lane, sw[j], esg[j]);
 #pragma unroll
         for (int j = 0; j < IPW; ++j)
-            if ((uint32_t)j < nit) gemv_q4m_load_weights<GW, NKB>(p, (uint64_t)(block + (uint32_t)j * nblocks) * NW + wave, lane, wq[j]);
+            if ((uint32_t)j < nit) gemv_q4m_load_weights<GW, NKB>(p.tw, (uint64_t)(block + (uint32_t)j * nblocks) * NW + wave, lane, wq[j]);
 #pragma unroll
         for (int j = 0; j < IPW; ++j) out[j] = gemv_q4m_out<GW>(p, (block + (uint32_t)j * nblocks) % tiles, wave);
         if constexpr (PRO == PRO_GAMMA_FIXED) {
@@ -562,15 +562,29 @@ __global__ __launch_bounds__(PRO == PRO_ATTN ? 512 : 320) void gemv_q4m_kernel(G
 // weight streams). A CU holds eight such 4-wave workgroups at once against
 // five 5-wave ones, so the gate|up projection's 1376 workgroups run in one
 // round instead of two.
+//
+// Arguments: what the first loads need comes first and is preloaded into
+// scalar registers at wave launch (the first 14 argument words, built with
+// -amdgpu-kernarg-preload-count): weights, scales, exponent bounds, the input
+// (x, or the accumulator) and its second operand (gamma, or the SiLU norm
+// partials), K, the tile count, the item count with the XCD-order flag in
+// bit 31, and ss_n | norm_n << 8. The rest is read from the GemvParams block,
+// whose loads go out behind the input loads and are first waited for after
+// the weights have been issued (no kernarg_warm here: its wait would come
+// first). The item mapping is branch-free, which keeps the compiler from
+// hoisting the block's loads, and a wait for them, above the first loads.
 template <int GW, int KW, int PRO>
-__global__ __launch_bounds__(256) void gemv_q4m4_kernel(GemvParams p) {
+__global__ __launch_bounds__(256) void gemv_q4m4_kernel(const uint8_t* tw, const uint16_t* ts, const int8_t* tes,
+                                                        const void* xin, const void* xaux, uint32_t k, uint32_t tiles_a,
+                                                        uint32_t items_x, uint32_t ss_nn, GemvParams p) {
     constexpr int NW = 4;
     constexpr int NKB = KW / 64, NZ = GW * KW / 64;
     constexpr int RW = KW / NW;              // input rows per wave (16..128)
     constexpr int RPL = (RW + kWave - 1) / kWave;
     static_assert(KW % 64 == 0 && KW <= 512, "slice of 64..512 rows");
     static_assert(PRO == PRO_PLAIN || PRO == PRO_GAMMA_FIXED || PRO == PRO_SILU_FIXED, "no attention merge here");
-    kernarg_warm(p);
+    const long long* xacc = static_cast<const long long*>(xin);
+    const uint32_t ss_n = ss_nn & 0xFFu, norm_n = ss_nn >> 8;
     __shared__ __align__(16) float xs[KW];
     __shared__ float wred[2][NW];
     __shared__ __align__(16) uint8_t zl[NW][GW][4][KW];
@@ -579,12 +593,12 @@ __global__ __launch_bounds__(256) void gemv_q4m4_kernel(GemvParams p) {
     const int t = threadIdx.x;
     const int lane = t & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
-    uint32_t tiles = __builtin_amdgcn_readfirstlane(p.tiles);
+    uint32_t tiles = __builtin_amdgcn_readfirstlane(tiles_a);
     sgpr_pin(tiles);
-    const uint32_t item = p.xcd_order ? xcd_item(blockIdx.x, gridDim.x) : blockIdx.x;
+    const uint32_t item = blockIdx.x + (items_x >> 31) * (xcd_item(blockIdx.x, items_x & 0x7FFFFFFFu) - blockIdx.x);
     const uint32_t tile = item % tiles, split = item / tiles;
     const uint32_t k0 = split * (uint32_t)KW;
-    const uint32_t k1 = min(p.k, k0 + (uint32_t)KW);
+    const uint32_t k1 = min(k, k0 + (uint32_t)KW);
 
     // (the accumulator this launch clears is cleared at the end: on gfx9 a
     // store counts in vmcnt like a load, so stores issued first would hold
@@ -597,26 +611,27 @@ __global__ __launch_bounds__(256) void gemv_q4m4_kernel(GemvParams p) {
 #pragma unroll
     for (int r = 0; r < RPL; ++r) {
         const uint32_t row = (uint32_t)(wave * RW + lane + kWave * r);
-        const uint32_t rc = min(k0 + row, p.k - 1u);
-        if constexpr (PRO == PRO_PLAIN) xp[r] = p.x[rc];
+        const uint32_t rc = min(k0 + row, k - 1u);
+        if constexpr (PRO == PRO_PLAIN) xp[r] = static_cast<const float*>(xin)[rc];
         if constexpr (PRO == PRO_GAMMA_FIXED) {
-            xa[r] = p.xacc[rc];
-            gm[r] = p.gamma[rc];
+            xa[r] = xacc[rc];
+            gm[r] = static_cast<const uint16_t*>(xaux)[rc];
         }
         if constexpr (PRO == PRO_SILU_FIXED) {
-            xa[r] = p.xacc[rc];
-            xb[r] = p.xacc[p.k + rc];
+            xa[r] = xacc[rc];
+            xb[r] = xacc[k + rc];
         }
     }
-    if constexpr (PRO == PRO_SILU_FIXED) ssp = p.ss_in[min((uint32_t)lane, p.ss_n - 1u)];
+    if constexpr (PRO == PRO_SILU_FIXED) ssp = static_cast<const float*>(xaux)[min((uint32_t)lane, ss_n - 1u)];
     __builtin_amdgcn_sched_barrier(0);   // the input loads are issued before the weight stream
 
     // ---- then the wave's scales and weights ----
     uint4 wq[GW][NKB];
     uint32_t sw[(NZ + 1) / 2];
     int esg[GW];
-    gemv_q4m_load_scales<GW, NZ>(p, (uint64_t)item * NW + wave, lane, sw, esg);
-    gemv_q4m_load_weights<GW, NKB>(p, (uint64_t)item * NW + wave, lane, wq);
+    gemv_q4m_load_scales<GW, NZ>(ts, tes, (uint64_t)item * NW + wave, lane, sw, esg);
+    gemv_q4m_load_weights<GW, NKB>(tw, (uint64_t)item * NW + wave, lane, wq);
+    __builtin_amdgcn_sched_barrier(0);
     const GemvOut<GW> out = gemv_q4m_out<GW>(p, tile, wave);
     float* ss_dst = nullptr;
     if constexpr (PRO == PRO_GAMMA_FIXED) ss_dst = sgpr_ptr(p.ss_out);
@@ -624,7 +639,7 @@ __global__ __launch_bounds__(256) void gemv_q4m4_kernel(GemvParams p) {
     // ---- x of the wave's rows into LDS, max |x|, sum x^2 ----
     float inv = 1.f;
     if constexpr (PRO == PRO_SILU_FIXED)
-        inv = 1.0f / sqrtf(wave_sum(lane < (int)p.ss_n ? ssp : 0.f) / (float)p.norm_n + 1e-6f);
+        inv = 1.0f / sqrtf(wave_sum(lane < (int)ss_n ? ssp : 0.f) / (float)norm_n + 1e-6f);
     float mx = 0.f, ss = 0.f;
 #pragma unroll
     for (int r = 0; r < RPL; ++r) {

@@ -193,13 +193,25 @@ static hipError_t launch_q4m_ipw(const GemvPlan& plan, const GemvParams& p, hipS
     // 4 matrix-core waves that build their own input rows; the attention
     // merge keeps 4 matrix-core waves + 4 prologue waves
     const dim3 grid(plan.grid()), block(256), block_attn(512);
+    // the 4-wave kernel takes the item count (bit 31: XCD order) and
+    // ss_n | norm_n << 8 in single argument words
+    if (plan.grid() >= 0x80000000u || (p.pro == PRO_SILU_FIXED && (p.ss_n > 0xFFu || p.norm_n >= (1u << 24))))
+        return hipErrorInvalidValue;
     switch (p.pro) {
-    case PRO_PLAIN: hipLaunchKernelGGL((gemv_q4m4_kernel<GW, KW, PRO_PLAIN>), grid, block, 0, stream, p); break;
+    case PRO_PLAIN:
+        hipLaunchKernelGGL((gemv_q4m4_kernel<GW, KW, PRO_PLAIN>), grid, block, 0, stream, p.tw, p.ts, p.tes,
+                           static_cast<const void*>(p.x), static_cast<const void*>(nullptr), p.k, p.tiles,
+                           plan.grid() | (p.xcd_order ? 0x80000000u : 0u), p.ss_n | (p.norm_n << 8), p);
+        break;
     case PRO_GAMMA_FIXED:
-        hipLaunchKernelGGL((gemv_q4m4_kernel<GW, KW, PRO_GAMMA_FIXED>), grid, block, 0, stream, p);
+        hipLaunchKernelGGL((gemv_q4m4_kernel<GW, KW, PRO_GAMMA_FIXED>), grid, block, 0, stream, p.tw, p.ts, p.tes,
+                           static_cast<const void*>(p.xacc), static_cast<const void*>(p.gamma), p.k, p.tiles,
+                           plan.grid() | (p.xcd_order ? 0x80000000u : 0u), p.ss_n | (p.norm_n << 8), p);
         break;
     case PRO_SILU_FIXED:
-        hipLaunchKernelGGL((gemv_q4m4_kernel<GW, KW, PRO_SILU_FIXED>), grid, block, 0, stream, p);
+        hipLaunchKernelGGL((gemv_q4m4_kernel<GW, KW, PRO_SILU_FIXED>), grid, block, 0, stream, p.tw, p.ts, p.tes,
+                           static_cast<const void*>(p.xacc), static_cast<const void*>(p.ss_in), p.k, p.tiles,
+                           plan.grid() | (p.xcd_order ? 0x80000000u : 0u), p.ss_n | (p.norm_n << 8), p);
         break;
     case PRO_ATTN:
         if constexpr (IPW == 1) {
