@@ -120,8 +120,14 @@ __device__ __forceinline__ void attn_store_tile(const KvTileRegs<TL>& r, uint32_
 // within kAttnMaxSplits at every context length). Contexts whose splits hold
 // many passes take attn_decode_long_kernel instead.
 template <int DPL, bool F16KV>
-__global__ __launch_bounds__(256) void attn_decode_kernel(AttnParams p) {
-    kernarg_warm(p);
+__global__ __launch_bounds__(256) void attn_decode_kernel(const int32_t* pos_p, const long long* qkv,
+                                                          const float* ssin, const float* rcos, const float* rsin,
+                                                          uint32_t shape, uint32_t hh, uint32_t snn, uint32_t chunk_a,
+                                                          AttnParams p) {
+    // (first-load arguments preloaded; see launch_attn)
+    const uint32_t half = (hh >> 16) & 0x7FFFu, H = hh & 0xFFFFu, KVH = shape >> 20;
+    const bool use_rope = (hh >> 31) != 0u;
+    const uint32_t ss_n = snn & 0xFFu, norm_n = snn >> 8;
     constexpr int NT = 256;
     constexpr int SUB = kAttnSub;                    // positions per pass (32)
     constexpr int HDM = 64 * DPL;                    // head_dim bound of this instance
@@ -139,37 +145,37 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnParams p) {
     const int wave = t / kWave;
     const uint32_t split = blockIdx.x;
     const uint32_t kvh = blockIdx.y;
-    const uint32_t hd = p.hd, G = p.groups;
-    const bool model = p.qkv_acc != nullptr;
-    const uint64_t kv_stride = (uint64_t)p.KVH * hd;    // q|k|v accumulator layout
+    const uint32_t hd = shape & 0x3FFu, G = (shape >> 10) & 0x3FFu;
+    const bool model = qkv != nullptr;
+    const uint64_t kv_stride = (uint64_t)KVH * hd;    // q|k|v accumulator layout
     const uint64_t head_off = (uint64_t)kvh * hd;
-    const uint64_t cps = kv_pos_stride(p), coff = kv_head_off(p, kvh);   // cache layout
+    const uint64_t cps = p.kv_ps ? p.kv_ps : kv_stride, coff = (uint64_t)kvh * (p.kv_ps ? p.kv_hs : (uint64_t)hd);   // cache layout
     const uint32_t nq = G * hd;
 
     // ---- position-independent loads, in flight with the position (a scalar
     // load: waiting for it does not wait for the vector loads) ----
-    const int32_t pos_raw = p.pos ? ld_scalar_i32(p.pos) : (int32_t)p.L - 1;
+    const int32_t pos_raw = pos_p ? ld_scalar_i32(pos_p) : (int32_t)p.L - 1;
     long long qa[2] = {0, 0}, qb[2] = {0, 0};
     long long ka = 0, kb = 0, va = 0;
     float ssp = 0.f;
     const uint32_t dn = min((uint32_t)t, hd - 1u);
     if (model) {
-        const uint32_t qd = p.H * hd;
+        const uint32_t qd = H * hd;
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
             const uint32_t i = min((uint32_t)t + (uint32_t)u * NT, nq - 1u);
             const uint32_t d = i % hd;
-            qa[u] = p.qkv_acc[(uint64_t)kvh * G * hd + i];
-            qb[u] = p.qkv_acc[(uint64_t)kvh * G * hd + (i - d) + rope_partner(d, p.half)];
+            qa[u] = qkv[(uint64_t)kvh * G * hd + i];
+            qb[u] = qkv[(uint64_t)kvh * G * hd + (i - d) + rope_partner(d, half)];
         }
-        ka = p.qkv_acc[qd + head_off + dn];
-        kb = p.qkv_acc[qd + head_off + rope_partner(dn, p.half)];
-        va = p.qkv_acc[qd + kv_stride + head_off + dn];
-        ssp = p.ss_in[min((uint32_t)lane, p.ss_n - 1u)];
+        ka = qkv[qd + head_off + dn];
+        kb = qkv[qd + head_off + rope_partner(dn, half)];
+        va = qkv[qd + kv_stride + head_off + dn];
+        ssp = ssin[min((uint32_t)lane, ss_n - 1u)];
     }
 
     const uint32_t L = (uint32_t)pos_raw + 1u;
-    const uint32_t chunk = p.chunk ? p.chunk : attn_chunk_for(L);
+    const uint32_t chunk = chunk_a ? chunk_a : attn_chunk_for(L);
     const uint32_t p0 = split * chunk;
     if (p0 >= L) {
         // the loads above are used on this path too, so the compiler issues
@@ -186,17 +192,17 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnParams p) {
 
     // ---- position-dependent loads: RoPE entries of `cur`, first cache tile ----
     float qc[2] = {1.f, 1.f}, qsn[2] = {0.f, 0.f}, kc_ = 1.f, ks_ = 0.f;
-    if (model && p.use_rope) {
-        const float* ct = p.rope_cos + (uint64_t)cur * p.half;
-        const float* st = p.rope_sin + (uint64_t)cur * p.half;
+    if (model && use_rope) {
+        const float* ct = rcos + (uint64_t)cur * half;
+        const float* st = rsin + (uint64_t)cur * half;
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
             const uint32_t d = min((uint32_t)t + (uint32_t)u * NT, nq - 1u) % hd;
-            const uint32_t td = d < p.half ? d : (d < 2 * p.half ? d - p.half : 0u);
+            const uint32_t td = d < half ? d : (d < 2 * half ? d - half : 0u);
             qc[u] = ct[td];
             qsn[u] = st[td];
         }
-        const uint32_t td = dn < p.half ? dn : (dn < 2 * p.half ? dn - p.half : 0u);
+        const uint32_t td = dn < half ? dn : (dn < 2 * half ? dn - half : 0u);
         kc_ = ct[td];
         ks_ = st[td];
     }
@@ -211,8 +217,8 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnParams p) {
     float k_app = 0.f, v_app = 0.f;                   // thread t < hd: dim t of the appended row
     if (model) {
         // the q|k|v GEMV ran on x * gamma; its RMSNorm factor is applied here
-        const float inv = 1.0f / sqrtf(wave_sum(lane < (int)p.ss_n ? ssp : 0.f) / (float)p.norm_n + 1e-6f);
-        const bool rot = p.use_rope != 0;
+        const float inv = 1.0f / sqrtf(wave_sum(lane < (int)ss_n ? ssp : 0.f) / (float)norm_n + 1e-6f);
+        const bool rot = use_rope != 0;
         // padding dims [hd, HDM) of each q row are zero
         for (uint32_t i = t; i < G * HDM; i += NT)
             if (i % HDM >= hd) qs[i] = 0.f;
@@ -224,14 +230,14 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnParams p) {
                 const uint32_t d = i % hd;
                 const float a = inv * from_fixed(qa[u]), b = inv * from_fixed(qb[u]);
                 // rotate_half: the first half takes -partner * sin, the second +partner * sin
-                qs[(i / hd) * HDM + d] = (rot && d < 2 * p.half) ? (d < p.half ? a * qc[u] - b * qsn[u]
+                qs[(i / hd) * HDM + d] = (rot && d < 2 * half) ? (d < half ? a * qc[u] - b * qsn[u]
                                                                                  : a * qc[u] + b * qsn[u])
                                                                   : a;
             }
         }
         if (has_new && (uint32_t)t < hd) {
             const float a = inv * from_fixed(ka), b = inv * from_fixed(kb);
-            float kv = (rot && dn < 2 * p.half) ? (dn < p.half ? a * kc_ - b * ks_ : a * kc_ + b * ks_) : a;
+            float kv = (rot && dn < 2 * half) ? (dn < half ? a * kc_ - b * ks_ : a * kc_ + b * ks_) : a;
             float vv = inv * from_fixed(va);
             const uint64_t idx = (uint64_t)cur * cps + coff + dn;
             if constexpr (F16KV) {

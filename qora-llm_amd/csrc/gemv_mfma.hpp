@@ -173,10 +173,22 @@ __device__ __forceinline__ void gemv_q4m_load_scales(const uint16_t* ts, const i
 // split s) and the row of every split up to the launch's split count (slots
 // past the active splits are read but never selected).
 
-__device__ __forceinline__ void attn_merge_rows_wave(const GemvParams& p, uint32_t k0, uint32_t r0, uint32_t r1,
-                                                     uint32_t k1, float* xs, float* aw) {
+// The arguments gemv_q4m_kernel's first loads need, preloaded into scalar
+// registers at wave launch (leading kernel arguments); the rest comes from
+// the GemvParams block.
+struct GemvFirst {
+    const uint8_t* tw;
+    const uint16_t* ts;
+    const int8_t* tes;
+    const float* attn_part;
+    const int32_t* pos;
+    uint32_t k, tiles, hd, groups, s_max;
+};
+
+__device__ __forceinline__ void attn_merge_rows_wave(const GemvParams& p, const GemvFirst& f, uint32_t k0, uint32_t r0,
+                                                     uint32_t r1, uint32_t k1, float* xs, float* aw) {
     const int lane = threadIdx.x & (kWave - 1);
-    const uint32_t hd = p.head_dim, G = p.groups;
+    const uint32_t hd = f.hd, G = f.groups, s_max = f.s_max;
     const uint64_t sstride = (uint64_t)G * (hd + 2);
     const uint32_t a0 = k0 + r0, a1 = min(k0 + r1, k1);      // absolute rows
     if (a0 >= a1) {
@@ -189,25 +201,25 @@ __device__ __forceinline__ void attn_merge_rows_wave(const GemvParams& p, uint32
     const uint32_t par = (uint32_t)lane / 32;
     const uint32_t r = min(k0 + i, a1 - 1u);
     const uint32_t h = r / hd, d = r % hd, hh = h - h0;
-    const float* rbase = p.attn_part + ((uint64_t)(h / G) * p.attn_s_max * G + (h % G)) * (hd + 2) + d;
+    const float* rbase = f.attn_part + ((uint64_t)(h / G) * s_max * G + (h % G)) * (hd + 2) + d;
     // ---- issued together: position, every split's (m, l), the first rows ----
-    const int32_t pos_raw = *p.pos;
-    const uint32_t sl = min((uint32_t)lane, p.attn_s_max - 1u);
+    const int32_t pos_raw = *f.pos;
+    const uint32_t sl = min((uint32_t)lane, s_max - 1u);
     float ms[2], ls[2];
 #pragma unroll
     for (uint32_t q = 0; q < 2; ++q) {
         const uint32_t hq = h0 + min(q, nh - 1u);
-        const float* base = p.attn_part + ((uint64_t)(hq / G) * p.attn_s_max * G + hq % G) * (hd + 2);
+        const float* base = f.attn_part + ((uint64_t)(hq / G) * s_max * G + hq % G) * (hd + 2);
         ms[q] = base[(uint64_t)sl * sstride + hd];
         ls[q] = base[(uint64_t)sl * sstride + hd + 1];
     }
     float pv[kAttnMaxSplits / 2];
 #pragma unroll
     for (uint32_t j = 0; j < kAttnMaxSplits / 2; ++j)
-        pv[j] = rbase[(uint64_t)min(par + 2u * j, p.attn_s_max - 1u) * sstride];
+        pv[j] = rbase[(uint64_t)min(par + 2u * j, s_max - 1u) * sstride];
     const uint32_t L = (uint32_t)pos_raw + 1u;
     const uint32_t chunk = p.attn_chunk ? p.attn_chunk : attn_chunk_for(L);
-    const uint32_t s_act = min(p.attn_s_max, (L + chunk - 1) / chunk);
+    const uint32_t s_act = min(s_max, (L + chunk - 1) / chunk);
     const bool ok = (uint32_t)lane < s_act;
 #pragma unroll
     for (uint32_t q = 0; q < 2; ++q) {
@@ -397,8 +409,8 @@ struct GemvQ4mSmem {
 
 // The body of gemv_q4m_kernel for workgroup `block` of `nblocks`.
 template <int GW, int KW, int PRO, int IPW>
-__device__ __forceinline__ void gemv_q4m_body(const GemvParams& p, uint32_t block, uint32_t nblocks,
-                                              GemvQ4mSmem<GW, KW, PRO, IPW>& sm) {
+__device__ __forceinline__ void gemv_q4m_body(const GemvParams& p, const GemvFirst& f, uint32_t block,
+                                              uint32_t nblocks, GemvQ4mSmem<GW, KW, PRO, IPW>& sm) {
     constexpr int NW = 4;                    // matrix-core waves
     constexpr int NPW = PRO == PRO_ATTN ? 4 : 1;   // prologue waves (the attention merge gets four)
     constexpr int NKB = KW / 64;            // K blocks (one MFMA each) per slice
@@ -418,12 +430,16 @@ __device__ __forceinline__ void gemv_q4m_body(const GemvParams& p, uint32_t bloc
     const int lane = t & (kWave - 1);
     // wave-uniform (scalar) so segment lookups and addresses stay on the SALU
     const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
-    uint32_t tiles = __builtin_amdgcn_readfirstlane(p.tiles);
+    uint32_t tiles = __builtin_amdgcn_readfirstlane(f.tiles);
     sgpr_pin(tiles);
-    const uint32_t items = tiles * p.splits;
     // items block, block + nblocks, ... (strided, so a grid of resident
-    // workgroups spreads the items beyond it over the first workgroups)
-    const uint32_t nit = block < items ? min((uint32_t)IPW, (items - block + nblocks - 1) / nblocks) : 0u;
+    // workgroups spreads the items beyond it over the first workgroups); one
+    // item per workgroup: the grid is the item count
+    uint32_t nit = 1u;
+    if constexpr (IPW > 1) {
+        const uint32_t items = tiles * p.splits;
+        nit = block < items ? min((uint32_t)IPW, (items - block + nblocks - 1) / nblocks) : 0u;
+    }
 
     uint4 wq[IPW][GW][NKB];
     uint32_t sw[IPW][(NZ + 1) / 2];
@@ -440,14 +456,14 @@ __device__ __forceinline__ void gemv_q4m_body(const GemvParams& p, uint32_t bloc
             if ((uint32_t)j >= nit) continue;
             const uint32_t split = (block + (uint32_t)j * nblocks) / tiles;
             const uint32_t k0 = split * (uint32_t)KW;
-            const uint32_t k1 = min(p.k, k0 + (uint32_t)KW);
+            const uint32_t k1 = min(f.k, k0 + (uint32_t)KW);
             float mx = 0.f, ss = 0.f;
             if constexpr (kAttn) {
                 const uint32_t pw = (uint32_t)(wave - NW);
                 constexpr uint32_t RW = KW / NPW;   // rows per prologue wave (<= 64)
 #pragma unroll
                 for (uint32_t c = 0; c < RW; c += 32)
-                    attn_merge_rows_wave(p, k0, pw * RW + c, pw * RW + min(c + 32, RW), k1, xs[j],
+                    attn_merge_rows_wave(p, f, k0, pw * RW + c, pw * RW + min(c + 32, RW), k1, xs[j],
                                          aw + pw * kAttnMaxSplits * MAXH);
                 __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
                 __builtin_amdgcn_wave_barrier();
@@ -459,7 +475,7 @@ __device__ __forceinline__ void gemv_q4m_body(const GemvParams& p, uint32_t bloc
                 uint16_t gm[RPW];
 #pragma unroll
                 for (int r = 0; r < RPW; ++r) {
-                    const uint32_t rc = min(k0 + (uint32_t)(lane + 64 * r), p.k - 1u);
+                    const uint32_t rc = min(k0 + (uint32_t)(lane + 64 * r), f.k - 1u);
                     if constexpr (PRO == PRO_PLAIN) xp[r] = p.x[rc];
                     if constexpr (PRO == PRO_GAMMA_FIXED) {
                         xa[r] = p.xacc[rc];
@@ -507,10 +523,10 @@ __device__ __forceinline__ void gemv_q4m_body(const GemvParams& p, uint32_t bloc
         // ---- matrix-core waves: every item's scales first (the quantisation needs them), then weights ----
 #pragma unroll
         for (int j = 0; j < IPW; ++j)
-            if ((uint32_t)j < nit) gemv_q4m_load_scales<GW, NZ>(p.ts, p.tes, (uint64_t)(block + (uint32_t)j * nblocks) * NW + wave, lane, sw[j], esg[j]);
+            if ((uint32_t)j < nit) gemv_q4m_load_scales<GW, NZ>(f.ts, f.tes, (uint64_t)(block + (uint32_t)j * nblocks) * NW + wave, lane, sw[j], esg[j]);
 #pragma unroll
         for (int j = 0; j < IPW; ++j)
-            if ((uint32_t)j < nit) gemv_q4m_load_weights<GW, NKB>(p.tw, (uint64_t)(block + (uint32_t)j * nblocks) * NW + wave, lane, wq[j]);
+            if ((uint32_t)j < nit) gemv_q4m_load_weights<GW, NKB>(f.tw, (uint64_t)(block + (uint32_t)j * nblocks) * NW + wave, lane, wq[j]);
 #pragma unroll
         for (int j = 0; j < IPW; ++j) out[j] = gemv_q4m_out<GW>(p, (block + (uint32_t)j * nblocks) % tiles, wave);
         if constexpr (PRO == PRO_GAMMA_FIXED) {
@@ -546,12 +562,21 @@ __device__ __forceinline__ void gemv_q4m_body(const GemvParams& p, uint32_t bloc
     }
 }
 
+// Arguments: what the first loads need comes first and is preloaded into
+// scalar registers at wave launch (14 words): weights, scales, exponent
+// bounds, the attention partials and the position, K, the tile count, the
+// item count with the XCD-order flag in bit 31, and head_dim | groups << 10 |
+// s_max << 20; the rest comes from the GemvParams block, read where it is
+// used (no kernarg_warm, whose wait would come before the first loads).
 template <int GW, int KW, int PRO, int IPW = 1>
-__global__ __launch_bounds__(PRO == PRO_ATTN ? 512 : 320) void gemv_q4m_kernel(GemvParams p) {
-    kernarg_warm(p);
+__global__ __launch_bounds__(PRO == PRO_ATTN ? 512 : 320) void gemv_q4m_kernel(
+    const uint8_t* tw, const uint16_t* ts, const int8_t* tes, const float* attn_part, const int32_t* pos, uint32_t k,
+    uint32_t tiles, uint32_t items_x, uint32_t hgs, GemvParams p) {
     __shared__ GemvQ4mSmem<GW, KW, PRO, IPW> sm;
-    const uint32_t b = IPW == 1 && p.xcd_order ? xcd_item(blockIdx.x, gridDim.x) : blockIdx.x;
-    gemv_q4m_body<GW, KW, PRO, IPW>(p, b, gridDim.x, sm);
+    const GemvFirst f{tw, ts, tes, attn_part, pos, k, tiles, hgs & 0x3FFu, (hgs >> 10) & 0x3FFu, hgs >> 20};
+    const uint32_t n = items_x & 0x7FFFFFFFu;
+    const uint32_t b = IPW == 1 ? blockIdx.x + (items_x >> 31) * (xcd_item(blockIdx.x, n) - blockIdx.x) : blockIdx.x;
+    gemv_q4m_body<GW, KW, PRO, IPW>(p, f, b, IPW == 1 ? n : gridDim.x, sm);
 }
 
 // Four matrix-core waves and no prologue wave (PRO_PLAIN, PRO_GAMMA_FIXED,

@@ -215,7 +215,10 @@ static hipError_t launch_q4m_ipw(const GemvPlan& plan, const GemvParams& p, hipS
         break;
     case PRO_ATTN:
         if constexpr (IPW == 1) {
-            hipLaunchKernelGGL((gemv_q4m_kernel<GW, KW, PRO_ATTN, 1>), grid, block_attn, 0, stream, p);
+            if (p.head_dim > 0x3FFu || p.groups > 0x3FFu || p.attn_s_max > 0xFFFu) return hipErrorInvalidValue;
+            hipLaunchKernelGGL((gemv_q4m_kernel<GW, KW, PRO_ATTN, 1>), grid, block_attn, 0, stream, p.tw, p.ts, p.tes,
+                               p.attn_part, p.pos, p.k, p.tiles, plan.grid() | (p.xcd_order ? 0x80000000u : 0u),
+                               p.head_dim | (p.groups << 10) | (p.attn_s_max << 20), p);
             break;
         } else {
             return hipErrorInvalidValue;
@@ -447,12 +450,26 @@ hipError_t launch_attn(const AttnParams& p, hipStream_t stream) {
         return hipGetLastError();
     }
     const dim3 block(lng ? 256 * kAttnLongNsg : 256);
+    // attn_decode_kernel takes the arguments of its first loads ahead of the
+    // parameter block (preloaded into scalar registers at wave launch), the
+    // small ones packed: hd | groups << 10 | KVH << 20, H | half << 16 |
+    // use_rope << 31, ss_n | norm_n << 8
+    if (!lng && (p.hd > 0x3FFu || p.groups > 0x3FFu || p.KVH > 0xFFFu || p.H > 0xFFFFu || p.half > 0x7FFFu ||
+                 p.ss_n > 0xFFu || p.norm_n >= (1u << 24)))
+        return hipErrorInvalidValue;
+    const uint32_t shape = p.hd | (p.groups << 10) | (p.KVH << 20);
+    const uint32_t hh = p.H | (p.half << 16) | (p.use_rope ? 0x80000000u : 0u);
+    const uint32_t snn = p.ss_n | (p.norm_n << 8);
 #define QORA_ATTN(DPL)                                                                                   \
     do {                                                                                                \
         if (lng && p.kv_f16) hipLaunchKernelGGL((attn_decode_long_kernel<DPL, true>), grid, block, 0, stream, p); \
         else if (lng) hipLaunchKernelGGL((attn_decode_long_kernel<DPL, false>), grid, block, 0, stream, p); \
-        else if (p.kv_f16) hipLaunchKernelGGL((attn_decode_kernel<DPL, true>), grid, block, 0, stream, p); \
-        else hipLaunchKernelGGL((attn_decode_kernel<DPL, false>), grid, block, 0, stream, p);          \
+        else if (p.kv_f16)                                                                              \
+            hipLaunchKernelGGL((attn_decode_kernel<DPL, true>), grid, block, 0, stream, p.pos, p.qkv_acc, p.ss_in, \
+                               p.rope_cos, p.rope_sin, shape, hh, snn, p.chunk, p);                    \
+        else                                                                                            \
+            hipLaunchKernelGGL((attn_decode_kernel<DPL, false>), grid, block, 0, stream, p.pos, p.qkv_acc, p.ss_in, \
+                               p.rope_cos, p.rope_sin, shape, hh, snn, p.chunk, p);                    \
     } while (0)
     if (p.hd <= 64) QORA_ATTN(1);
     else QORA_ATTN(2);
