@@ -23,6 +23,11 @@
 //     last pass needs masks. The rows of passes 0 .. NP - 2 lie below the
 //     appended position whatever it is: their loads go out before the
 //     position arrives;
+//   * the arguments of the first loads (cache, position, q|k|v sums, norm
+//     partials, shape and strides) come ahead of the parameter block and are
+//     preloaded into scalar registers at wave launch: the K rows go out at
+//     once, the parameter block's lines with the position, and the RoPE row
+//     (whose table pointers are in the block) after the V rows;
 //   * q, the appended k row and v row: RMSNorm factor of the q|k|v GEMV input
 //     applied to the fixed-point sums, q and k rotated at position L - 1
 //     (apply_rope_raw, gemv.rs:903-906); the workgroup of column tile 0 of the
@@ -135,7 +140,10 @@ __device__ __forceinline__ void chunk_merge(const AttnOParams& ap, uint32_t h, i
 }
 
 template <int HD, bool F16KV, int NP, bool CH = false>
-__global__ __launch_bounds__(kFusedWaves * kWave) void gemv_q4m_attn_kernel(AttnOParams ap) {
+__global__ __launch_bounds__(kFusedWaves * kWave) void gemv_q4m_attn_kernel(const void* kc_a, const void* vc_a, const int32_t* pos_a,
+                                                                         const long long* qkv_a, const float* ssin_a,
+                                                                         uint32_t tg, uint32_t khs, uint32_t cps_a,
+                                                                         uint32_t hs_a, AttnOParams ap) {
     constexpr int GW = 1, NW = 4;
     constexpr int KW = HD;                  // one query head per K slice
     constexpr int NKB = KW / 64, NZ = GW * KW / 64;
@@ -143,7 +151,6 @@ __global__ __launch_bounds__(kFusedWaves * kWave) void gemv_q4m_attn_kernel(Attn
     static_assert(HD == 64 || HD == 128, "head_dim 64 or 128");
     static_assert(NP >= 1 && NP <= kFusedMaxPasses, "1 to 8 passes");
     using W = typename std::conditional<F16KV, uint2, float4>::type;
-    kernarg_warm(ap);
     const GemvParams& p = ap.g;
     const AttnParams& a = ap.a;
     __shared__ __align__(16) float qs[HD];
@@ -162,20 +169,25 @@ __global__ __launch_bounds__(kFusedWaves * kWave) void gemv_q4m_attn_kernel(Attn
     // each XCD consecutive items, i.e. the column tiles of two query heads of
     // one KV head at the model shape, so an XCD's L2 serves one KV head's
     // rows to all of its workgroups.
-    const uint32_t item = gridDim.x % 8u == 0u ? (blockIdx.x % 8u) * (gridDim.x / 8u) + blockIdx.x / 8u : blockIdx.x;
-    const uint32_t tile = item % p.tiles;
-    const uint32_t h = item / p.tiles;                 // K slice = query head
-    const uint32_t kvh = h / a.groups;
-    const uint32_t qd = a.H * HD, kvd = a.KVH * HD;
-    const uint64_t cps = kv_pos_stride(a), coff = kv_head_off(a, kvh);
+    // (the leading arguments are preloaded: tg = tiles | groups << 16, khs =
+    // KVH | half << 12 | ss_n << 24, the cache's position and head strides)
+    const uint32_t tiles = tg & 0xFFFFu, groups = tg >> 16;
+    const uint32_t KVH = khs & 0xFFFu, half = (khs >> 12) & 0xFFFu, ss_n = khs >> 24;
+    const uint32_t grid = tiles * KVH * groups;
+    const uint32_t item = grid % 8u == 0u ? (blockIdx.x % 8u) * (grid / 8u) + blockIdx.x / 8u : blockIdx.x;
+    const uint32_t tile = item % tiles;
+    const uint32_t h = item / tiles;                   // K slice = query head
+    const uint32_t kvh = h / groups;
+    const uint32_t qd = KVH * groups * HD, kvd = KVH * HD;
+    const uint64_t cps = cps_a, coff = (uint64_t)kvh * hs_a;
 
     const uint32_t c = (uint32_t)lane % 16, j = (uint32_t)lane / 16;
     // position of pass i: P0 + 32 i + slot (CH: chunk `tile` of 32 NP
     // positions; otherwise every position from 0)
     const uint32_t P0 = CH ? tile * (kFusedPass * (uint32_t)NP) : 0u;
     const uint32_t slot = P0 + 4u * (uint32_t)wave + j;
-    const uint8_t* kcache = reinterpret_cast<const uint8_t*>(a.kc);
-    const uint8_t* vcache = reinterpret_cast<const uint8_t*>(a.vc);
+    const uint8_t* kcache = reinterpret_cast<const uint8_t*>(kc_a);
+    const uint8_t* vcache = reinterpret_cast<const uint8_t*>(vc_a);
     constexpr uint32_t EB = F16KV ? 2u : 4u;
     W kr[NP][NQ], vr[NP][NQ];
     auto row_off = [&](uint32_t pos, int u) {
@@ -199,12 +211,15 @@ __global__ __launch_bounds__(kFusedWaves * kWave) void gemv_q4m_attn_kernel(Attn
 
     const bool qkv_wave = wave >= NW && wave < NW + HD / kWave;
     const uint32_t d = (uint32_t)(t - NW * kWave) % HD;
-    const uint32_t pd = rope_partner(d, a.half);
+    const uint32_t pd = rope_partner(d, half);
 
     // ---- the position, then the last pass's K rows: rows at or past the
     // appended position are not read (address clamped below it, or to row 0
     // when it is 0; those values are replaced or masked below) ----
-    int32_t pos_raw = ld_scalar_i32(a.pos);
+    int32_t pos_raw = ld_scalar_i32(pos_a);
+    // the parameter block's lines, read while the position is in flight (the
+    // position's wait covers them)
+    kernarg_warm(ap);
     sgpr_pin(pos_raw);
     const uint32_t L = (uint32_t)pos_raw + 1u;
     const uint32_t cur = L - 1u;                       // position appended this step
@@ -226,17 +241,12 @@ __global__ __launch_bounds__(kFusedWaves * kWave) void gemv_q4m_attn_kernel(Attn
     long long qa = 0, qb = 0, ka = 0, kb = 0, va = 0;
     float ssp = 0.f, rc = 1.f, rs = 0.f;
     if (qkv_wave) {
-        if (a.use_rope && d < 2 * a.half) {
-            const uint32_t td = d < a.half ? d : d - a.half;
-            rc = a.rope_cos[(uint64_t)cur * a.half + td];
-            rs = a.rope_sin[(uint64_t)cur * a.half + td];
-        }
-        qa = a.qkv_acc[(uint64_t)h * HD + d];
-        qb = a.qkv_acc[(uint64_t)h * HD + pd];
-        ka = a.qkv_acc[qd + (uint64_t)kvh * HD + d];
-        kb = a.qkv_acc[qd + (uint64_t)kvh * HD + pd];
-        va = a.qkv_acc[qd + kvd + (uint64_t)kvh * HD + d];
-        ssp = a.ss_in[min((uint32_t)lane, a.ss_n - 1u)];
+        qa = qkv_a[(uint64_t)h * HD + d];
+        qb = qkv_a[(uint64_t)h * HD + pd];
+        ka = qkv_a[qd + (uint64_t)kvh * HD + d];
+        kb = qkv_a[qd + (uint64_t)kvh * HD + pd];
+        va = qkv_a[qd + kvd + (uint64_t)kvh * HD + d];
+        ssp = ssin_a[min((uint32_t)lane, ss_n - 1u)];
     }
 
     // ---- V rows of every pass ----
@@ -253,6 +263,14 @@ __global__ __launch_bounds__(kFusedWaves * kWave) void gemv_q4m_attn_kernel(Attn
     // same loads as wave - NW (the lines are already in flight): every wave
     // then has the same loads outstanding after its V rows, so its first use
     // of the rows waits for the rows alone, not for these ----
+    // ---- the RoPE row of the appended position: its table pointers come
+    // from the parameter block, so these loads follow the rows ----
+    if (qkv_wave && a.use_rope && d < 2 * half) {
+        const uint32_t td = d < half ? d : d - half;
+        rc = a.rope_cos[(uint64_t)cur * half + td];
+        rs = a.rope_sin[(uint64_t)cur * half + td];
+    }
+
     uint4 wq[GW][NKB];
     uint32_t sw[(NZ + 1) / 2];
     int esg[GW];
@@ -268,16 +286,16 @@ __global__ __launch_bounds__(kFusedWaves * kWave) void gemv_q4m_attn_kernel(Attn
         // the weights have been issued
         asm volatile("" : "+v"(qa), "+v"(qb), "+v"(ka), "+v"(kb), "+v"(va), "+v"(ssp), "+v"(rc), "+v"(rs));
         // the q|k|v GEMV ran on x * gamma; its RMSNorm factor is applied here
-        const float inv = 1.0f / sqrtf(wave_sum(lane < (int)a.ss_n ? ssp : 0.f) / (float)a.norm_n + 1e-6f);
-        const bool rot = a.use_rope != 0 && d < 2 * a.half;
+        const float inv = 1.0f / sqrtf(wave_sum(lane < (int)ss_n ? ssp : 0.f) / (float)a.norm_n + 1e-6f);
+        const bool rot = a.use_rope != 0 && d < 2 * half;
         auto rotate = [&](long long x, long long y) {
             const float u = inv * from_fixed(x), v = inv * from_fixed(y);
-            return rot ? (d < a.half ? u * rc - v * rs : u * rc + v * rs) : u;
+            return rot ? (d < half ? u * rc - v * rs : u * rc + v * rs) : u;
         };
         qs[d] = rotate(qa, qb);
         float kv = rotate(ka, kb);
         float vv = inv * from_fixed(va);
-        const bool owner = tile == 0 && h % a.groups == 0;
+        const bool owner = tile == 0 && h % groups == 0;
         const uint64_t idx = (uint64_t)cur * cps + coff + d;
         if constexpr (F16KV) {
             const uint16_t kh = f2h(kv), vh = f2h(vv);

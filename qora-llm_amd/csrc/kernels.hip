@@ -485,17 +485,29 @@ bool attn_o_supported(const GemvPlan& pl, uint32_t hd, uint32_t H, uint32_t grou
 template <int HD, bool F16KV, bool CH>
 static hipError_t launch_attn_o_hd(const GemvPlan& pl, const AttnOParams& p, uint32_t np, hipStream_t stream) {
     const dim3 grid(pl.blocks()), block(kFusedWaves * kWave);
+    // the first loads' arguments go ahead of the parameter block (preloaded
+    // into scalar registers at wave launch): the cache, the position, the
+    // q|k|v sums and norm partials, tiles | groups << 16, KVH | half << 12 |
+    // ss_n << 24 and the cache's position and head strides (in elements)
+    const AttnParams& a = p.a;
+    const uint64_t cps = a.kv_ps ? a.kv_ps : (uint64_t)a.KVH * a.hd, hs = a.kv_ps ? a.kv_hs : (uint64_t)a.hd;
+    if (p.g.tiles > 0xFFFFu || a.groups > 0xFFFFu || a.KVH > 0xFFFu || a.half > 0xFFFu || a.ss_n > 0xFFu ||
+        a.H != a.KVH * a.groups || pl.blocks() != p.g.tiles * a.H || cps > 0xFFFFFFFFull || hs > 0xFFFFFFFFull)
+        return hipErrorInvalidValue;
+    const uint32_t tg = p.g.tiles | (a.groups << 16), khs = a.KVH | (a.half << 12) | (a.ss_n << 24);
+#define QORA_AO_ARGS p.a.kc, p.a.vc, p.a.pos, p.a.qkv_acc, p.a.ss_in, tg, khs, (uint32_t)cps, (uint32_t)hs, p
     switch (np) {
-    case 1: hipLaunchKernelGGL((gemv_q4m_attn_kernel<HD, F16KV, 1, CH>), grid, block, 0, stream, p); break;
-    case 2: hipLaunchKernelGGL((gemv_q4m_attn_kernel<HD, F16KV, 2, CH>), grid, block, 0, stream, p); break;
-    case 3: hipLaunchKernelGGL((gemv_q4m_attn_kernel<HD, F16KV, 3, CH>), grid, block, 0, stream, p); break;
-    case 4: hipLaunchKernelGGL((gemv_q4m_attn_kernel<HD, F16KV, 4, CH>), grid, block, 0, stream, p); break;
-    case 5: hipLaunchKernelGGL((gemv_q4m_attn_kernel<HD, F16KV, 5, CH>), grid, block, 0, stream, p); break;
-    case 6: hipLaunchKernelGGL((gemv_q4m_attn_kernel<HD, F16KV, 6, CH>), grid, block, 0, stream, p); break;
-    case 7: hipLaunchKernelGGL((gemv_q4m_attn_kernel<HD, F16KV, 7, CH>), grid, block, 0, stream, p); break;
-    case 8: hipLaunchKernelGGL((gemv_q4m_attn_kernel<HD, F16KV, 8, CH>), grid, block, 0, stream, p); break;
+    case 1: hipLaunchKernelGGL((gemv_q4m_attn_kernel<HD, F16KV, 1, CH>), grid, block, 0, stream, QORA_AO_ARGS); break;
+    case 2: hipLaunchKernelGGL((gemv_q4m_attn_kernel<HD, F16KV, 2, CH>), grid, block, 0, stream, QORA_AO_ARGS); break;
+    case 3: hipLaunchKernelGGL((gemv_q4m_attn_kernel<HD, F16KV, 3, CH>), grid, block, 0, stream, QORA_AO_ARGS); break;
+    case 4: hipLaunchKernelGGL((gemv_q4m_attn_kernel<HD, F16KV, 4, CH>), grid, block, 0, stream, QORA_AO_ARGS); break;
+    case 5: hipLaunchKernelGGL((gemv_q4m_attn_kernel<HD, F16KV, 5, CH>), grid, block, 0, stream, QORA_AO_ARGS); break;
+    case 6: hipLaunchKernelGGL((gemv_q4m_attn_kernel<HD, F16KV, 6, CH>), grid, block, 0, stream, QORA_AO_ARGS); break;
+    case 7: hipLaunchKernelGGL((gemv_q4m_attn_kernel<HD, F16KV, 7, CH>), grid, block, 0, stream, QORA_AO_ARGS); break;
+    case 8: hipLaunchKernelGGL((gemv_q4m_attn_kernel<HD, F16KV, 8, CH>), grid, block, 0, stream, QORA_AO_ARGS); break;
     default: return hipErrorInvalidValue;
     }
+#undef QORA_AO_ARGS
     return hipGetLastError();
 }
 
