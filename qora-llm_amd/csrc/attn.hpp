@@ -714,7 +714,11 @@ __global__ __launch_bounds__(256 * kAttnLongNsg) void attn_decode_long_kernel(At
 // row (model mode) comes from LDS, and positions at or past the split's end
 // never reach a sum (selection, not a zero weight: stale slots may hold NaN).
 template <int HD>
-__global__ __launch_bounds__(512) void attn_decode_direct_kernel(AttnParams p) {
+__global__ __launch_bounds__(512) void attn_decode_direct_kernel(const int32_t* pos_a, AttnParams p) {
+    // the position's pointer is preloaded into scalar registers at wave
+    // launch: its load goes out with the parameter block's lines, and one
+    // wait covers both
+    const int32_t pos_ld = pos_a ? ld_scalar_i32(pos_a) : 0;
     kernarg_warm(p);
     constexpr int NWV = 8;                           // waves per block
     constexpr int PP = 32;                           // positions per pass
@@ -738,7 +742,7 @@ __global__ __launch_bounds__(512) void attn_decode_direct_kernel(AttnParams p) {
     const uint64_t head_off = (uint64_t)kvh * HD;
     const uint64_t cps = kv_pos_stride(p), coff = kv_head_off(p, kvh);   // cache layout
 
-    const int32_t pos_raw = p.pos ? *p.pos : (int32_t)p.L - 1;
+    const int32_t pos_raw = pos_a ? pos_ld : (int32_t)p.L - 1;
     const uint32_t L = (uint32_t)pos_raw + 1u;
     const uint32_t chunk = p.chunk ? p.chunk : attn_chunk_for(L);
     const uint32_t p0 = split * chunk;

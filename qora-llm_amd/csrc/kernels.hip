@@ -445,8 +445,8 @@ hipError_t launch_attn(const AttnParams& p, hipStream_t stream) {
     if (lng && p.kv_f16 && (p.hd == 128 || p.hd == 64) && p.groups <= (uint32_t)kAttnMaxGroups &&
         !tuning_env("QORA_HIP_ATTN_STAGED")) {
         const dim3 grid_t(p.KVH, p.s_max);
-        if (p.hd == 128) hipLaunchKernelGGL((attn_decode_direct_kernel<128>), grid_t, dim3(512), 0, stream, p);
-        else hipLaunchKernelGGL((attn_decode_direct_kernel<64>), grid_t, dim3(512), 0, stream, p);
+        if (p.hd == 128) hipLaunchKernelGGL((attn_decode_direct_kernel<128>), grid_t, dim3(512), 0, stream, p.pos, p);
+        else hipLaunchKernelGGL((attn_decode_direct_kernel<64>), grid_t, dim3(512), 0, stream, p.pos, p);
         return hipGetLastError();
     }
     const dim3 block(lng ? 256 * kAttnLongNsg : 256);
