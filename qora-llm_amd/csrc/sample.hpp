@@ -7,15 +7,20 @@
 //    each distinct history token, the repetition penalty once per occurrence in
 //    the last 64 tokens (x / p for x > 0, else x * p, in sequence) and then
 //    the presence penalty once if the token occurs anywhere.
-// 2. smp_block_topk_kernel: each block sorts 2048 (value, index) keys in LDS
-//    (bitonic) and keeps its best kSmpKeep. Keys order by value descending,
-//    then index ascending: the order of the reference's stable sort_by on
-//    partial_cmp. NaN ranks last.
-// 3. smp_final_kernel: one block sorts the blocks' candidates, keeps top_k,
-//    and one thread runs the reference's arithmetic in the reference's order
-//    (softmax over the top k against the global max, nucleus cut-off, one
-//    xorshift64 draw, linear scan). Greedy (temperature <= 0) takes the first
-//    candidate: the first-max rule.
+// 2. smp_block_topk_kernel: each block keeps the best kSmpKeep of its 2048
+//    (value, index) keys. Keys order by value descending, then index
+//    ascending: the order of the reference's stable sort_by on partial_cmp.
+//    NaN ranks last. Each wave sorts runs of 64 keys, one key per lane, with
+//    cross-lane exchanges (a bitonic network in registers), and sorted runs
+//    are merged pairwise keeping the 64 smallest keys (smp_wave_merge_low).
+// 3. smp_final_kernel: one block merges the blocks' sorted candidate runs the
+//    same way down to the best 64; the softmax terms of the top k are computed
+//    one per lane, and one thread runs the reference's sums in the reference's
+//    order (softmax normaliser, nucleus cut-off, one xorshift64 draw, linear
+//    scan). Greedy (temperature <= 0) takes the first candidate: the
+//    first-max rule.
+// The keys are distinct (the index is in the low word), so any correct
+// sorting network yields the same order.
 #pragma once
 
 #include "common.hpp"
@@ -63,6 +68,67 @@ __device__ __forceinline__ void smp_bitonic(unsigned long long* keys) {
     __syncthreads();
 }
 
+// One 64-bit key per lane, exchanged with lane ^ m.
+__device__ __forceinline__ unsigned long long smp_shfl_xor(unsigned long long v, int m) {
+    const int lo = __shfl_xor((int)(uint32_t)v, m, kWave);
+    const int hi = __shfl_xor((int)(uint32_t)(v >> 32), m, kWave);
+    return ((unsigned long long)(uint32_t)hi << 32) | (uint32_t)lo;
+}
+
+// The wave's 64 keys (one per lane) sorted ascending in lane order: a
+// bitonic network whose exchanges are cross-lane shuffles (no LDS round
+// trip, no barrier). Lane i keeps the smaller key when it is the lower lane
+// of an ascending block or the upper lane of a descending one.
+__device__ __forceinline__ unsigned long long smp_wave_sort(unsigned long long v) {
+    const uint32_t lane = threadIdx.x & (kWave - 1);
+#pragma unroll
+    for (uint32_t size = 2; size <= 64; size <<= 1) {
+#pragma unroll
+        for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
+            const unsigned long long o = smp_shfl_xor(v, (int)stride);
+            const bool keep_min = ((lane & stride) == 0) == ((lane & size) == 0);
+            const unsigned long long lo = o < v ? o : v, hi = o < v ? v : o;
+            v = keep_min ? lo : hi;
+        }
+    }
+    return v;
+}
+
+// The 64 smallest keys of two ascending runs a and b, ascending (lane i
+// passes a[i] and b[63 - i]): a followed by b reversed is bitonic, so
+// min(a[i], b[63 - i]) holds the 64 smallest as a bitonic sequence, which
+// the half-cleaners of strides 32 .. 1 sort.
+__device__ __forceinline__ unsigned long long smp_wave_merge_low(unsigned long long a, unsigned long long brev) {
+    const uint32_t lane = threadIdx.x & (kWave - 1);
+    unsigned long long v = brev < a ? brev : a;
+#pragma unroll
+    for (uint32_t stride = 32; stride > 0; stride >>= 1) {
+        const unsigned long long o = smp_shfl_xor(v, (int)stride);
+        const unsigned long long lo = o < v ? o : v, hi = o < v ? v : o;
+        v = (lane & stride) == 0 ? lo : hi;
+    }
+    return v;
+}
+
+// Runs [0, n) of 64 ascending keys in runs[src] merged pairwise (run 2j with
+// 2j + 1 into run j of the other buffer, keeping the 64 smallest) until one
+// is left, by the block's NWV waves; returns the buffer that holds it.
+template <uint32_t N, uint32_t NWV>
+__device__ __forceinline__ uint32_t smp_merge_runs(unsigned long long (*runs)[N], uint32_t n, uint32_t src) {
+    const uint32_t lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    for (; n > 1; n >>= 1) {
+        __syncthreads();
+        for (uint32_t j = wave; j < n / 2; j += NWV) {
+            const unsigned long long a = runs[src][(2 * j) * 64 + lane];
+            const unsigned long long b = runs[src][(2 * j + 1) * 64 + 63 - lane];
+            runs[src ^ 1][j * 64 + lane] = smp_wave_merge_low(a, b);
+        }
+        src ^= 1;
+    }
+    __syncthreads();
+    return src;
+}
+
 __global__ __launch_bounds__(256) void smp_copy_kernel(const float* in, float* out, uint32_t n) {
     for (uint32_t i = blockIdx.x * 256u + threadIdx.x; i < n; i += gridDim.x * 256u) out[i] = in[i];
 }
@@ -78,38 +144,57 @@ __global__ __launch_bounds__(256) void smp_penalty_kernel(SampleParams p) {
 }
 
 __global__ __launch_bounds__(256) void smp_block_topk_kernel(SampleParams p) {
-    __shared__ unsigned long long keys[kSmpBlock];
+    static_assert(kSmpKeep == 64 && kSmpBlock % (4 * 64) == 0, "64-key runs, four waves");
+    constexpr uint32_t NR = kSmpBlock / 64, RPW = NR / 4;     // runs, runs per wave
+    __shared__ unsigned long long runs[2][kSmpBlock];
+    const uint32_t lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
     const uint32_t base = blockIdx.x * kSmpBlock;
-    for (uint32_t j = threadIdx.x; j < kSmpBlock; j += 256) {
-        const uint32_t i = base + j;
-        keys[j] = i < p.vocab ? smp_key(p.work[i], i) : ~0ull;
+    // every load of the wave's runs first, then each run sorted across the lanes
+    unsigned long long v[RPW];
+#pragma unroll
+    for (uint32_t q = 0; q < RPW; ++q) {
+        const uint32_t i = base + (wave + 4 * q) * 64 + lane;
+        v[q] = i < p.vocab ? smp_key(p.work[min(i, p.vocab - 1)], i) : ~0ull;
     }
-    smp_bitonic<kSmpBlock>(keys);
-    for (uint32_t j = threadIdx.x; j < kSmpKeep; j += 256) p.cand[blockIdx.x * kSmpKeep + j] = keys[j];
+#pragma unroll
+    for (uint32_t q = 0; q < RPW; ++q) runs[0][(wave + 4 * q) * 64 + lane] = smp_wave_sort(v[q]);
+    const uint32_t src = smp_merge_runs<kSmpBlock, 4>(runs, NR, 0);
+    if (wave == 0) p.cand[blockIdx.x * kSmpKeep + lane] = runs[src][lane];
 }
 
 __global__ __launch_bounds__(256) void smp_final_kernel(SampleParams p) {
-    __shared__ unsigned long long keys[kSmpFinal];
+    static_assert(kSmpFinal % 64 == 0 && kSmpKeep == 64, "64-key runs");
+    __shared__ unsigned long long runs[2][kSmpFinal];
+    __shared__ float prob[kSmpKeep];
+    __shared__ float s_inv;
+    // the blocks' candidate runs (each ascending), then runs of ~0 padding
     const uint32_t nc = p.blocks * kSmpKeep;
-    for (uint32_t j = threadIdx.x; j < kSmpFinal; j += 256) keys[j] = j < nc ? p.cand[j] : ~0ull;
-    smp_bitonic<kSmpFinal>(keys);
-    if (threadIdx.x != 0) return;
+    for (uint32_t j = threadIdx.x; j < kSmpFinal; j += 256) runs[0][j] = j < nc ? p.cand[j] : ~0ull;
+    const uint32_t src = smp_merge_runs<kSmpFinal, 4>(runs, kSmpFinal / 64, 0);
+    const unsigned long long* keys = runs[src];
     const uint32_t k = min(p.top_k, min(p.vocab, kSmpKeep));
+    const float inv_temp = p.temperature > 0.0f ? 1.0f / p.temperature : 0.0f;
+    // the softmax terms of the top k (generate.rs:360-366), one per lane of
+    // wave 0, each the expression the reference evaluates for it
+    if (p.temperature > 0.0f && threadIdx.x < k)
+        prob[threadIdx.x] = expf((smp_key_value(keys[threadIdx.x]) - smp_key_value(keys[0])) * inv_temp);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float sum = 0.0f;
+        if (p.temperature > 0.0f)
+            for (uint32_t i = 0; i < k; ++i) sum += prob[i];
+        s_inv = sum > 0.0f ? 1.0f / sum : 0.0f;
+    }
+    __syncthreads();
+    if (p.temperature > 0.0f && threadIdx.x < k && s_inv > 0.0f) prob[threadIdx.x] *= s_inv;
+    __syncthreads();
+    if (threadIdx.x != 0) return;
     uint32_t token = (uint32_t)keys[0];
     unsigned long long state = *p.rng;
     if (p.temperature > 0.0f) {
-        // softmax over the top k (generate.rs:360-370)
-        const float inv_temp = 1.0f / p.temperature;
-        const float max_logit = smp_key_value(keys[0]);
-        float prob[kSmpKeep];
-        float sum = 0.0f;
-        for (uint32_t i = 0; i < k; ++i) {
-            prob[i] = expf((smp_key_value(keys[i]) - max_logit) * inv_temp);
-            sum += prob[i];
-        }
-        if (sum > 0.0f) {
-            const float inv = 1.0f / sum;
-            for (uint32_t i = 0; i < k; ++i) prob[i] *= inv;
+        // softmax over the top k (generate.rs:360-370): the terms and their
+        // normalised values are in prob[]; the sum above ran in index order
+        if (s_inv > 0.0f) {
             // nucleus cut-off (generate.rs:372-380)
             float cum = 0.0f;
             uint32_t cutoff = k;
