@@ -68,11 +68,31 @@ __device__ __forceinline__ void smp_bitonic(unsigned long long* keys) {
     __syncthreads();
 }
 
+// A word from lane ^ m (m a power of two below 64, a constant once the
+// caller's loops are unrolled): DPP lane moves inside the VALU for 1, 2, 4
+// and 8 (quad permutes; a row rotate by 8; rows shifted by 4 either way and
+// the lane's direction selected), ds_swizzle for 16, ds_bpermute only for 32.
+// (row_shl:n gives lane i the value of lane i + n, row_shr:n of lane i - n.)
+__device__ __forceinline__ uint32_t smp_xor_lane(uint32_t x, uint32_t m) {
+    const int xi = (int)x;
+    switch (m) {
+    case 1: return (uint32_t)__builtin_amdgcn_mov_dpp(xi, 0xB1, 0xF, 0xF, false);    // quad_perm [1,0,3,2]
+    case 2: return (uint32_t)__builtin_amdgcn_mov_dpp(xi, 0x4E, 0xF, 0xF, false);    // quad_perm [2,3,0,1]
+    case 4: {
+        const int up = __builtin_amdgcn_mov_dpp(xi, 0x104, 0xF, 0xF, false);        // row_shl:4
+        const int dn = __builtin_amdgcn_mov_dpp(xi, 0x114, 0xF, 0xF, false);        // row_shr:4
+        return (uint32_t)((threadIdx.x & 4u) ? dn : up);
+    }
+    case 8: return (uint32_t)__builtin_amdgcn_mov_dpp(xi, 0x128, 0xF, 0xF, false);   // row_ror:8
+    case 16: return (uint32_t)__builtin_amdgcn_ds_swizzle(xi, (16 << 10) | 0x1F);    // xor 16 in 32-lane halves
+    default: return (uint32_t)__shfl_xor(xi, (int)m, kWave);
+    }
+}
+
 // One 64-bit key per lane, exchanged with lane ^ m.
-__device__ __forceinline__ unsigned long long smp_shfl_xor(unsigned long long v, int m) {
-    const int lo = __shfl_xor((int)(uint32_t)v, m, kWave);
-    const int hi = __shfl_xor((int)(uint32_t)(v >> 32), m, kWave);
-    return ((unsigned long long)(uint32_t)hi << 32) | (uint32_t)lo;
+__device__ __forceinline__ unsigned long long smp_shfl_xor(unsigned long long v, uint32_t m) {
+    const uint32_t lo = smp_xor_lane((uint32_t)v, m), hi = smp_xor_lane((uint32_t)(v >> 32), m);
+    return ((unsigned long long)hi << 32) | lo;
 }
 
 // The wave's 64 keys (one per lane) sorted ascending in lane order: a
@@ -85,10 +105,11 @@ __device__ __forceinline__ unsigned long long smp_wave_sort(unsigned long long v
     for (uint32_t size = 2; size <= 64; size <<= 1) {
 #pragma unroll
         for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
-            const unsigned long long o = smp_shfl_xor(v, (int)stride);
+            const unsigned long long o = smp_shfl_xor(v, stride);
             const bool keep_min = ((lane & stride) == 0) == ((lane & size) == 0);
-            const unsigned long long lo = o < v ? o : v, hi = o < v ? v : o;
-            v = keep_min ? lo : hi;
+            // the keys differ (equal ones are interchangeable), so the lane
+            // takes its partner's key exactly when that one belongs here
+            v = (o < v) == keep_min ? o : v;
         }
     }
     return v;
@@ -103,9 +124,8 @@ __device__ __forceinline__ unsigned long long smp_wave_merge_low(unsigned long l
     unsigned long long v = brev < a ? brev : a;
 #pragma unroll
     for (uint32_t stride = 32; stride > 0; stride >>= 1) {
-        const unsigned long long o = smp_shfl_xor(v, (int)stride);
-        const unsigned long long lo = o < v ? o : v, hi = o < v ? v : o;
-        v = (lane & stride) == 0 ? lo : hi;
+        const unsigned long long o = smp_shfl_xor(v, stride);
+        v = (o < v) == ((lane & stride) == 0) ? o : v;
     }
     return v;
 }
