@@ -148,7 +148,10 @@ int qora_hip_sample(qora_hip_ctx* ctx, const float* logits, uint64_t vocab, cons
                     void* stream);
 
 /* qora_hip_decode followed by qora_hip_sample on the step's logits, which
- * stay on the device (copied out only if logits_or_null is given). */
+ * stay on the device (copied out only if logits_or_null is given). The
+ * sampled token is also left on the device as the next step's input, so a
+ * following qora_hip_decode / qora_hip_decode_sample with that token uploads
+ * nothing. */
 int qora_hip_decode_sample(qora_hip_ctx* ctx, uint32_t token, const uint32_t* history, uint64_t n_history,
                            const qora_sample_params* params, uint64_t* rng_state, float* logits_or_null,
                            uint32_t* token_out);

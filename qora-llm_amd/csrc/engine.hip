@@ -190,6 +190,8 @@ struct qora_hip_ctx {
     unsigned long long* smp_rng = nullptr;
     int32_t* smp_tok = nullptr;
     SamplePenalty* smp_pen = nullptr;
+    SamplePenalty* h_pen = nullptr;      // pinned staging of the penalty list
+    uint64_t h_pen_n = 0;
     uint32_t smp_vocab = 0;
     void* smp_sort = nullptr;            // full-sort path: two key buffers and the probabilities
     uint64_t smp_sort_bytes = 0;
@@ -525,6 +527,7 @@ extern "C" int qora_hip_destroy(qora_hip_ctx* c) {
                     (void*)c->smp_rng, (void*)c->smp_pen, c->smp_sort})
         if (p) (void)hipFree(p);
     if (c->h_pin) (void)hipHostFree(c->h_pin);
+    if (c->h_pen) (void)hipHostFree(c->h_pen);
     if (c->h_tok) (void)hipHostFree(c->h_tok);
     (void)hipStreamDestroy(c->stream);
     delete c;
@@ -2100,8 +2103,14 @@ int sample_check(qora_hip_ctx* c, bool have_logits, uint64_t vocab, const uint32
 // top_k (0 = the whole vocabulary, sample_token_top_k's k, generate.rs:357-363)
 // or a larger vocabulary sorts every key.
 
+// dev_token (optional): the token is also stored there on the device (a
+// decode step's input slot). With mapped host memory the token and state are
+// read from it as soon as the kernel has stored them, without waiting for the
+// stream (as a greedy step's token is); the list's copy and the kernels have
+// then finished reading their inputs.
 int sample_device(qora_hip_ctx* c, const float* logits, uint64_t vocab, const uint32_t* history, uint64_t n_history,
-                  const qora_sample_params* sp, uint64_t* rng_state, uint32_t* token, hipStream_t s) {
+                  const qora_sample_params* sp, uint64_t* rng_state, uint32_t* token, hipStream_t s,
+                  int32_t* dev_token = nullptr) {
     if (int rc = sample_check(c, logits != nullptr, vocab, history, n_history, sp, rng_state, token)) return rc;
     const bool greedy = !(sp->temperature > 0.0f);
     const bool rep = !greedy && sp->repetition_penalty > 1.0f;
@@ -2156,10 +2165,32 @@ int sample_device(qora_hip_ctx* c, const float* logits, uint64_t vocab, const ui
         c->smp_pen = (SamplePenalty*)q;
         c->smp_pen_n = n;
     }
-    if (!pen.empty()) HIP_TRY(c, hipMemcpyAsync(c->smp_pen, pen.data(), pen.size() * sizeof(SamplePenalty),
-                                                hipMemcpyHostToDevice, s));
-    HIP_TRY(c, hipMemcpyAsync(c->smp_rng, rng_state, 8, hipMemcpyHostToDevice, s));
+    if (pen.size() > c->h_pen_n) {
+        HIP_TRY(c, hipStreamSynchronize(s));
+        if (c->h_pen) (void)hipHostFree(c->h_pen);
+        c->h_pen = nullptr;
+        c->h_pen_n = 0;
+        const uint64_t n = std::max<uint64_t>(pen.size(), 1024);
+        if (hipHostMalloc((void**)&c->h_pen, n * sizeof(SamplePenalty), hipHostMallocDefault) != hipSuccess) {
+            c->h_pen = nullptr;
+            return fail(c, QORA_HIP_E_NOMEM, "pinned penalty buffer");
+        }
+        c->h_pen_n = n;
+    }
+    if (!pen.empty()) {
+        // through pinned memory: the copy may run after this call returns
+        std::memcpy(c->h_pen, pen.data(), pen.size() * sizeof(SamplePenalty));
+        HIP_TRY(c, hipMemcpyAsync(c->smp_pen, c->h_pen, pen.size() * sizeof(SamplePenalty), hipMemcpyHostToDevice, s));
+    }
+    volatile int32_t* ho = c->d_h_tok ? c->h_tok + 4 : nullptr;   // [0] token, [2..3] state
+    if (ho) {
+        ho[0] = kTokPending;
+        std::atomic_thread_fence(std::memory_order_seq_cst);
+    }
     SampleParams p{};
+    p.rng_in = *rng_state;
+    p.host_out = ho ? c->d_h_tok + 4 : nullptr;
+    p.dev_token = dev_token;
     p.work = c->smp_work;
     p.vocab = V;
     p.pen = c->smp_pen;
@@ -2193,6 +2224,25 @@ int sample_device(qora_hip_ctx* c, const float* logits, uint64_t vocab, const ui
         p.n_sort = ns;
         p.probs = (float*)(p.sort_b + ns);
         HIP_TRY(c, launch_sample_sorted(logits, p, k, s));
+    }
+    if (ho) {
+        // the token word, stored last by the kernel; after 200 ms without it
+        // (a failed launch, a fault) the stream is synchronised and its error
+        // reported
+        const auto t0 = std::chrono::steady_clock::now();
+        bool seen = false;
+        for (uint32_t i = 1; !seen; ++i) {
+            seen = ho[0] != kTokPending;
+            if (!seen && (i & 1023u) == 0 && std::chrono::steady_clock::now() - t0 > std::chrono::milliseconds(200))
+                break;
+        }
+        if (!seen) {
+            HIP_TRY(c, hipStreamSynchronize(s));
+            if (ho[0] == kTokPending) return fail(c, QORA_HIP_E_DEVICE, "sampling kernel did not store its token");
+        }
+        *token = (uint32_t)ho[0];
+        *rng_state = (uint64_t)(uint32_t)ho[2] | ((uint64_t)(uint32_t)ho[3] << 32);
+        return QORA_HIP_OK;
     }
     HIP_TRY(c, hipMemcpyAsync(&c->h_pin[20], c->smp_tok, 4, hipMemcpyDeviceToHost, s));
     HIP_TRY(c, hipMemcpyAsync(&c->h_pin[22], c->smp_rng, 8, hipMemcpyDeviceToHost, s));
@@ -2236,17 +2286,20 @@ extern "C" int qora_hip_decode_sample(qora_hip_ctx* c, uint32_t token, const uin
         m.dev_token = -1;
     }
     m.host_pos += 1;
-    const int rc = sample_device(c, m.d_logits, m.vocab, history, n_history, params, rng_state, token_out, c->stream);
+    const int rc =
+        sample_device(c, m.d_logits, m.vocab, history, n_history, params, rng_state, token_out, c->stream, m.d_token);
     if (rc) {
         // nothing of this call stays in flight behind an error
         (void)hipStreamSynchronize(c->stream);
         m.dev_token = -1;
         return rc;
     }
+    m.dev_token = (int64_t)*token_out;   // the sampling kernel stored it as the next step's input
     if (!logits) {
         // The step's range flag (finish_step reads it when logits are asked
-        // for). sample_device has synchronised the stream, so the step's
-        // argmax_finish_kernel has copied the flag to the mapped word.
+        // for). The sampling kernels ran after the step's argmax_finish_kernel,
+        // which stored the flag to the mapped word before them (system-scope
+        // fence), so the flag is in place once the sampled token is.
         int32_t bad;
         if (c->d_h_tok) {
             bad = reinterpret_cast<volatile int32_t*>(c->h_tok)[1];

@@ -854,11 +854,11 @@ bool smp_supported(uint32_t vocab) { return vocab > 0 && smp_blocks(vocab) * kSm
 hipError_t launch_sample(const float* logits, const SampleParams& p, hipStream_t stream) {
     if (!smp_supported(p.vocab) || p.blocks != smp_blocks(p.vocab) || p.top_k == 0 || p.top_k > kSmpKeep)
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL(smp_copy_kernel, dim3(std::min<uint32_t>(1024, (p.vocab + 255) / 256)), dim3(256), 0, stream,
-                       logits, p.work, p.vocab);
-    if (p.n_pen) hipLaunchKernelGGL(smp_penalty_kernel, dim3((p.n_pen + 255) / 256), dim3(256), 0, stream, p);
-    hipLaunchKernelGGL(smp_block_topk_kernel, dim3(p.blocks), dim3(256), 0, stream, p);
-    hipLaunchKernelGGL(smp_final_kernel, dim3(1), dim3(256), 0, stream, p);
+    // the block kernel reads the logits and applies the penalties itself
+    SampleParams q = p;
+    q.logits = logits;
+    hipLaunchKernelGGL(smp_block_topk_kernel, dim3(p.blocks), dim3(256), 0, stream, q);
+    hipLaunchKernelGGL(smp_final_kernel, dim3(1), dim3(256), 0, stream, q);
     return hipGetLastError();
 }
 

@@ -250,8 +250,12 @@ struct SampleParams {
     uint32_t blocks;
     float temperature, top_p;
     uint32_t top_k;
-    unsigned long long* rng;   // xorshift64 state, updated in place
+    unsigned long long rng_in; // xorshift64 state before the draw
+    unsigned long long* rng;   // the state after it
     int32_t* token_out;
+    const float* logits;       // top_k 1..64: the logits, penalised as they are read (no copy)
+    int32_t* host_out;         // optional (mapped host memory): [2..3] the state, then [0] the token
+    int32_t* dev_token;        // optional: the token also stored here (a decode step's next input)
     // the full-sort path (top_k 0 or above kSmpKeep, or a large vocabulary):
     // every key sorted by merging 2048-key runs (two buffers of n_sort keys,
     // n_sort = blocks * 2048 rounded up to a power of two), then the

@@ -3,10 +3,12 @@
 // sample_token_top_k 345-395, Rng 38-61) on the step's logits, so a sampled
 // decode step returns a token instead of the 513 KB logits vector.
 //
-// 1. smp_copy_kernel + smp_penalty_kernel: a scratch copy of the logits; for
-//    each distinct history token, the repetition penalty once per occurrence in
-//    the last 64 tokens (x / p for x > 0, else x * p, in sequence) and then
-//    the presence penalty once if the token occurs anywhere.
+// 1. The penalties: for each distinct history token, the repetition penalty
+//    once per occurrence in the last 64 tokens (x / p for x > 0, else x * p,
+//    in sequence) and then the presence penalty once if the token occurs
+//    anywhere. top_k 1..64 applies them as the first kernel reads the logits;
+//    the full-sort path writes a penalised copy (smp_copy_kernel +
+//    smp_penalty_kernel).
 // 2. smp_block_topk_kernel: each block keeps the best kSmpKeep of its 2048
 //    (value, index) keys. Keys order by value descending, then index
 //    ascending: the order of the reference's stable sort_by on partial_cmp.
@@ -149,6 +151,29 @@ __device__ __forceinline__ uint32_t smp_merge_runs(unsigned long long (*runs)[N]
     return src;
 }
 
+// The draw's results: the state and the token in device memory, the token
+// also as the next decode step's input when asked, and in mapped host memory
+// the state and then, after a system-scope fence, the token (the host reads
+// the token as soon as it appears, without waiting for the stream).
+__device__ __forceinline__ void smp_publish(const SampleParams& p, uint32_t token, unsigned long long state) {
+    *p.rng = state;
+    *p.token_out = (int32_t)token;
+    if (p.dev_token) *p.dev_token = (int32_t)token;
+    if (p.host_out) {
+        p.host_out[2] = (int32_t)(uint32_t)state;
+        p.host_out[3] = (int32_t)(uint32_t)(state >> 32);
+        __threadfence_system();
+        __hip_atomic_store(p.host_out, (int32_t)token, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+}
+
+// One penalty entry applied to x (smp_penalty_kernel's arithmetic).
+__device__ __forceinline__ float smp_penalise(const SampleParams& p, const SamplePenalty& e, float x) {
+    for (uint32_t r = 0; r < e.rep_count; ++r) x = x > 0.0f ? x / p.repetition : x * p.repetition;
+    if (e.seen) x -= p.presence;
+    return x;
+}
+
 __global__ __launch_bounds__(256) void smp_copy_kernel(const float* in, float* out, uint32_t n) {
     for (uint32_t i = blockIdx.x * 256u + threadIdx.x; i < n; i += gridDim.x * 256u) out[i] = in[i];
 }
@@ -157,10 +182,7 @@ __global__ __launch_bounds__(256) void smp_penalty_kernel(SampleParams p) {
     const uint32_t i = blockIdx.x * 256u + threadIdx.x;
     if (i >= p.n_pen) return;
     const SamplePenalty e = p.pen[i];
-    float x = p.work[e.token];
-    for (uint32_t r = 0; r < e.rep_count; ++r) x = x > 0.0f ? x / p.repetition : x * p.repetition;
-    if (e.seen) x -= p.presence;
-    p.work[e.token] = x;
+    p.work[e.token] = smp_penalise(p, e, p.work[e.token]);
 }
 
 __global__ __launch_bounds__(256) void smp_block_topk_kernel(SampleParams p) {
@@ -169,12 +191,31 @@ __global__ __launch_bounds__(256) void smp_block_topk_kernel(SampleParams p) {
     __shared__ unsigned long long runs[2][kSmpBlock];
     const uint32_t lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
     const uint32_t base = blockIdx.x * kSmpBlock;
-    // every load of the wave's runs first, then each run sorted across the lanes
+    // every load of the wave's runs first (the logits themselves), the
+    // penalties of the block's tokens applied through LDS, then each run
+    // sorted across the lanes
+    float x[RPW];
+#pragma unroll
+    for (uint32_t q = 0; q < RPW; ++q) x[q] = p.logits[min(base + (wave + 4 * q) * 64 + lane, p.vocab - 1)];
+    if (p.n_pen) {
+        float* xs = reinterpret_cast<float*>(runs[1]);
+#pragma unroll
+        for (uint32_t q = 0; q < RPW; ++q) xs[(wave + 4 * q) * 64 + lane] = x[q];
+        __syncthreads();
+        for (uint32_t j = threadIdx.x; j < p.n_pen; j += 256) {
+            const SamplePenalty e = p.pen[j];
+            if (e.token >= base && e.token - base < kSmpBlock) xs[e.token - base] = smp_penalise(p, e, xs[e.token - base]);
+        }
+        __syncthreads();
+#pragma unroll
+        for (uint32_t q = 0; q < RPW; ++q) x[q] = xs[(wave + 4 * q) * 64 + lane];
+        __syncthreads();   // runs[1] is the merge buffer below
+    }
     unsigned long long v[RPW];
 #pragma unroll
     for (uint32_t q = 0; q < RPW; ++q) {
         const uint32_t i = base + (wave + 4 * q) * 64 + lane;
-        v[q] = i < p.vocab ? smp_key(p.work[min(i, p.vocab - 1)], i) : ~0ull;
+        v[q] = i < p.vocab ? smp_key(x[q], i) : ~0ull;
     }
 #pragma unroll
     for (uint32_t q = 0; q < RPW; ++q) runs[0][(wave + 4 * q) * 64 + lane] = smp_wave_sort(v[q]);
@@ -210,7 +251,7 @@ __global__ __launch_bounds__(256) void smp_final_kernel(SampleParams p) {
     __syncthreads();
     if (threadIdx.x != 0) return;
     uint32_t token = (uint32_t)keys[0];
-    unsigned long long state = *p.rng;
+    unsigned long long state = p.rng_in;
     if (p.temperature > 0.0f) {
         // softmax over the top k (generate.rs:360-370): the terms and their
         // normalised values are in prob[]; the sum above ran in index order
@@ -247,8 +288,7 @@ __global__ __launch_bounds__(256) void smp_final_kernel(SampleParams p) {
             }
         }
     }
-    *p.rng = state;
-    *p.token_out = (int32_t)token;
+    smp_publish(p, token, state);
 }
 
 // ---------------------------------------------------------------------------
@@ -395,7 +435,7 @@ __global__ __launch_bounds__(256) void smp_scan_kernel(SampleParams p, const uns
     __shared__ uint32_t s_hit[4];
     const uint32_t t = threadIdx.x;
     uint32_t token = (uint32_t)sorted[0];
-    unsigned long long state = *p.rng;
+    unsigned long long state = p.rng_in;
     if (p.temperature > 0.0f) {
         float sum = 0.0f;
         smp_scan_pass<false>(p.probs, k, buf, &s_stop, [&](float (&x)[16], uint32_t cnt) {
@@ -477,10 +517,7 @@ __global__ __launch_bounds__(256) void smp_scan_kernel(SampleParams p, const uns
             }
         }
     }
-    if (t == 0) {
-        *p.rng = state;
-        *p.token_out = (int32_t)token;
-    }
+    if (t == 0) smp_publish(p, token, state);
 }
 
 }  // namespace qora
