@@ -368,117 +368,185 @@ __device__ __forceinline__ void smp_scan_stage(const float* src, uint32_t c, uin
     }
 }
 
-__device__ __forceinline__ void smp_scan_unstage(const float* srcb, uint32_t c, uint32_t n, float* dst) {
-    for (uint32_t i = threadIdx.x - 64u; i < kScanChunk; i += 192u) {
-        const uint32_t j = c * kScanChunk + i;
-        if (j < n) dst[j] = srcb[i];
+// The reference's running fp32 sum over x_0 .. x_{n-1}, s_i = fl(s_{i-1} + x_i)
+// from s_{-1} = 0, bit for bit, by all 256 threads. While s stays in one
+// binade [2^E, 2^(E+1)) (or below 2^-126), every sum lies on the grid
+// u = 2^(E-23) (2^-149 below): s + x rounds to s + RNE(x / u) grid units as
+// long as that stays below the binade's end, and RNE(x / u) of a value that
+// is not exactly half a unit off the grid does not depend on s. So each
+// thread classifies its values against the grid (integer arithmetic on their
+// bits), a saturating prefix sum of the units gives every running sum of a
+// 4096-value chunk at once, and a block minimum finds the first event: a tie
+// (half a unit: the result's parity decides), a sum reaching the binade's end,
+// a value that is not a finite number >= 0, or (STOP) a sum >= stop. The sums
+// before the event are exact grid values; the event's value is added with one
+// fp32 addition, the reference's own operation, and the chunk restarts after
+// it. Events are rare: a binade crossing per doubling of the sum, a tie only
+// when a value's bits end exactly half a unit off the grid.
+// Returns the sum (with STOP: the sum at the first s_i >= stop, and
+// *stop_at = i + 1; 0 when no sum reaches it). WRITE: s_i goes to out[i] for
+// every i up to the stop (or n).
+constexpr uint32_t kExactJ = 16;                       // values per thread per chunk
+constexpr uint32_t kExactChunk = 256 * kExactJ;
+constexpr uint32_t kExactCap = 1u << 25;               // saturation of the unit sums (above every binade's end)
+constexpr uint32_t kExactNone = 0xFFFFFFFFu;
+
+struct SmpExactShared {
+    uint32_t wtot[4], wmin[4];
+    float s;
+    uint32_t base, stop_at, done;
+};
+
+__device__ __forceinline__ uint32_t smp_sat_add(uint32_t a, uint32_t b) { return min(a + b, kExactCap); }
+
+// Units of x on the grid 2^eu, rounded to nearest, and whether x is an event
+// by itself (exactly half a unit off the grid, not a finite number >= 0).
+__device__ __forceinline__ uint32_t smp_grid_units(float x, int eu, bool& ev) {
+    const uint32_t b = __float_as_uint(x);
+    ev = false;
+    if (b == 0u || b == 0x80000000u) return 0u;        // +-0
+    if (b >= 0x7F800000u) {                            // inf, NaN, or a negative value
+        ev = true;
+        return 0u;
     }
+    const uint32_t ef = b >> 23, mx = ef ? ((b & 0x7FFFFFu) | 0x800000u) : b;
+    const int sh = (ef ? (int)ef - 150 : -149) - eu;   // x = mx * 2^(eu + sh)
+    if (sh >= 0) return sh >= 8 ? kExactCap : min(mx << sh, kExactCap);
+    const int d = -sh;
+    if (d > 25) return 0u;                             // below a quarter unit
+    const uint32_t q = mx >> d, rem = mx & ((1u << d) - 1u), half = 1u << (d - 1);
+    ev = rem == half;
+    return q + (rem > half ? 1u : 0u);
 }
 
-// One pass over v[0, n) in order on thread 0, 16 values at a time from LDS:
-// `block(x[16], cnt)` runs the pass's arithmetic over x[0, cnt) in order (it
-// may rewrite them) and returns the index of its stop within the block, or
-// 16 for none. writeback: the (rewritten) values go back to v. Returns
-// i + 1 of the stop, or 0 when the pass ran to n. (Staged chunks are padded
-// with zeros past n, so 16-value reads stay inside the buffer.)
-template <bool WRITEBACK, typename Block>
-__device__ __forceinline__ uint32_t smp_scan_pass(float* v, uint32_t n, float (*buf)[kScanChunk], uint32_t* s_stop,
-                                                  Block block) {
-    const uint32_t t = threadIdx.x;
-    const uint32_t nch = (n + kScanChunk - 1) / kScanChunk;
-    __syncthreads();   // every thread has read the previous pass's stop
-    if (t == 0) *s_stop = 0;
-    if (t >= 64 && nch) smp_scan_stage(v, 0, n, buf[0]);
+template <bool STOP, bool WRITE, typename Val>
+__device__ float smp_exact_sum(uint32_t n, Val val, float stop, float* out, uint32_t* stop_at, SmpExactShared& sh) {
+    const uint32_t t = threadIdx.x, lane = t & (kWave - 1), wave = t / kWave;
+    if (t == 0) {
+        sh.s = 0.0f;
+        sh.base = 0;
+        sh.stop_at = 0;
+        sh.done = 0;
+    }
     __syncthreads();
-    uint32_t c = 0;
-    for (; c < nch; ++c) {
-        if (t >= 64) {
-            // chunk c - 1 (done) goes back, then chunk c + 1 comes into its buffer
-            if (WRITEBACK && c > 0) smp_scan_unstage(buf[(c - 1) & 1u], c - 1, n, v);
-            if (c + 1 < nch) smp_scan_stage(v, c + 1, n, buf[(c + 1) & 1u]);
+    for (;;) {
+        const float s = sh.s;
+        const uint32_t base = sh.base;
+        if (sh.done || base >= n) break;
+        // the binade of s: grid 2^eu, s = M units, its end at `bound` units
+        const uint32_t sb = __float_as_uint(s);
+        const int eu = sb < 0x00800000u ? -149 : (int)(sb >> 23) - 150;
+        const uint32_t M = sb < 0x00800000u ? sb : ((sb & 0x7FFFFFu) | 0x800000u);
+        const uint32_t bound = sb < 0x00800000u ? (1u << 23) : (1u << 24);
+        const uint32_t i0 = base + t * kExactJ;
+        float x[kExactJ];
+        uint32_t loc[kExactJ];
+        uint32_t evm = 0;                              // bit j: value j is an event by itself
+        uint32_t acc = 0;
+#pragma unroll
+        for (uint32_t j = 0; j < kExactJ; ++j) x[j] = i0 + j < n ? val(i0 + j) : 0.0f;
+#pragma unroll
+        for (uint32_t j = 0; j < kExactJ; ++j) {
+            bool ev;
+            const uint32_t r = smp_grid_units(x[j], eu, ev);
+            evm |= (ev ? 1u : 0u) << j;
+            acc = smp_sat_add(acc, r);
+            loc[j] = acc;
         }
-        if (t == 0) {
-            float4* b4 = reinterpret_cast<float4*>(buf[c & 1u]);
-            const uint32_t i0 = c * kScanChunk, cnt = min(kScanChunk, n - i0);
-            for (uint32_t j = 0; j < cnt; j += 16) {
-                float x[16];
+        // exclusive prefix of the threads' totals (saturating)
+        uint32_t inc = acc;
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const float4 f = b4[j / 4 + q];
-                    x[4 * q] = f.x;
-                    x[4 * q + 1] = f.y;
-                    x[4 * q + 2] = f.z;
-                    x[4 * q + 3] = f.w;
-                }
-                const uint32_t at = block(x, min(16u, cnt - j));
-                if (WRITEBACK) {
+        for (int d = 1; d < kWave; d <<= 1) {
+            const uint32_t o = (uint32_t)__shfl_up((int)inc, (unsigned)d, kWave);
+            if (lane >= (uint32_t)d) inc = smp_sat_add(inc, o);
+        }
+        // the lane's exclusive prefix is the previous lane's inclusive one (not
+        // inc - acc: a saturated inc has lost it)
+        const uint32_t exw = (uint32_t)__shfl_up((int)inc, 1u, kWave);
+        if (lane == kWave - 1) sh.wtot[wave] = inc;
+        __syncthreads();
+        uint32_t prev = 0;
+        for (uint32_t w = 0; w < wave; ++w) prev = smp_sat_add(prev, sh.wtot[w]);
+        const uint32_t excl = smp_sat_add(prev, lane ? exw : 0u);
+        // this thread's first event (chunk index), then the block's
+        uint32_t fe = kExactNone;
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) b4[j / 4 + q] = make_float4(x[4 * q], x[4 * q + 1], x[4 * q + 2], x[4 * q + 3]);
-                }
-                if (at < 16u) {
-                    *s_stop = i0 + j + at + 1;
-                    break;
-                }
+        for (uint32_t j = kExactJ; j-- > 0;) {
+            const uint32_t P = smp_sat_add(excl, loc[j]);
+            bool e = ((evm >> j) & 1u) != 0u || M + P >= bound;
+            if (STOP && !e) e = ldexpf((float)(M + P), eu) >= stop;
+            if (e && i0 + j < n) fe = t * kExactJ + j;
+        }
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) fe = min(fe, (uint32_t)__shfl_xor((int)fe, off, kWave));
+        if (lane == 0) sh.wmin[wave] = fe;
+        __syncthreads();
+        const uint32_t first = min(min(sh.wmin[0], sh.wmin[1]), min(sh.wmin[2], sh.wmin[3]));
+        // the exact sums before the event (or the chunk's end)
+        if (WRITE) {
+#pragma unroll
+            for (uint32_t j = 0; j < kExactJ; ++j)
+                if (i0 + j < n && t * kExactJ + j < first) out[i0 + j] = ldexpf((float)(M + smp_sat_add(excl, loc[j])), eu);
+        }
+        if (first == kExactNone) {
+            if (t == 0) {
+                uint32_t tot = 0;
+                for (uint32_t w = 0; w < 4; ++w) tot = smp_sat_add(tot, sh.wtot[w]);
+                sh.s = ldexpf((float)(M + tot), eu);
+                sh.base = min(n, base + kExactChunk);
+            }
+        } else if (t == first / kExactJ) {
+            // the event's value, added to the exact sum before it
+            const uint32_t j = first % kExactJ;
+            float xe = x[0];
+            uint32_t before = excl;
+#pragma unroll
+            for (uint32_t q = 0; q < kExactJ; ++q)
+                if (q == j) xe = x[q];
+#pragma unroll
+            for (uint32_t q = 0; q < kExactJ; ++q)
+                if (q + 1 == j) before = smp_sat_add(excl, loc[q]);
+            const float sn = __fadd_rn(ldexpf((float)(M + before), eu), xe);
+            const uint32_t gi = base + first;
+            if (WRITE) out[gi] = sn;
+            sh.s = sn;
+            sh.base = gi + 1;
+            if (STOP && sn >= stop) {
+                sh.stop_at = gi + 1;
+                sh.done = 1;
+            } else if (!(sn <= 3.402823466e38f)) {
+                sh.done = 1;                           // NaN (or inf): every later sum stays so
             }
         }
         __syncthreads();
-        if (*s_stop) break;
     }
-    if (WRITEBACK && nch && t >= 64) smp_scan_unstage(buf[min(c, nch - 1) & 1u], min(c, nch - 1), n, v);
-    return *s_stop;
+    const float r = sh.s;
+    if (STOP) *stop_at = sh.stop_at;
+    __syncthreads();                                   // sh is reused by the next call
+    return r;
 }
 
 __global__ __launch_bounds__(256) void smp_scan_kernel(SampleParams p, const unsigned long long* sorted, uint32_t k) {
     __shared__ __align__(16) float buf[2][kScanChunk];
-    __shared__ uint32_t s_stop;
+    __shared__ SmpExactShared sx;
     __shared__ float s_val[2];
     __shared__ uint32_t s_hit[4];
     const uint32_t t = threadIdx.x;
     uint32_t token = (uint32_t)sorted[0];
     unsigned long long state = p.rng_in;
     if (p.temperature > 0.0f) {
-        float sum = 0.0f;
-        smp_scan_pass<false>(p.probs, k, buf, &s_stop, [&](float (&x)[16], uint32_t cnt) {
-            if (cnt == 16u) {
-#pragma unroll
-                for (int j = 0; j < 16; ++j) sum = __fadd_rn(sum, x[j]);
-            } else {
-                for (uint32_t j = 0; j < cnt; ++j) sum = __fadd_rn(sum, x[j]);
-            }
-            return 16u;
-        });
+        const float* probs = p.probs;
+        const float sum = smp_exact_sum<false, false>(k, [probs](uint32_t i) { return probs[i]; }, 0.0f, nullptr,
+                                                      nullptr, sx);
         if (t == 0) s_val[0] = sum;
         __syncthreads();
         if (s_val[0] > 0.0f) {
             const float inv = 1.0f / s_val[0];
             // each probability is e * inv, rounded, then added (never one fused
             // multiply-add), as the reference scales the vector before summing
-            float cum = 0.0f;
-            const float top_p = p.top_p;
-            // the running sums of a block first (the sums never decrease, but a
-            // NaN could break that, so every one is tested), then the first stop
-            const uint32_t stop = smp_scan_pass<true>(p.probs, k, buf, &s_stop, [&](float (&x)[16], uint32_t cnt) {
-                if (cnt == 16u) {
-#pragma unroll
-                    for (int j = 0; j < 16; ++j) {
-                        cum = __fadd_rn(cum, __fmul_rn(x[j], inv));
-                        x[j] = cum;
-                    }
-                } else {
-                    for (uint32_t j = 0; j < cnt; ++j) {
-                        cum = __fadd_rn(cum, __fmul_rn(x[j], inv));
-                        x[j] = cum;
-                    }
-                }
-                // the running sums never decrease unless a NaN enters, which
-                // then stays to the block's end: with the last sum below top_p
-                // (a false comparison for NaN) no sum of the block reached it
-                if (cum < top_p) return 16u;
-                uint32_t at = 0;
-                while (at < cnt && !(x[at] >= top_p)) ++at;
-                if (at < cnt) cum = x[at];   // the reference's cumsum at its cut-off
-                return at < cnt ? at : 16u;
-            });
+            uint32_t stop = 0;
+            const float cum = smp_exact_sum<true, true>(
+                k, [probs, inv](uint32_t i) { return __fmul_rn(probs[i], inv); }, p.top_p, p.probs, &stop, sx);
             const uint32_t cutoff = stop ? stop : k;
             if (t == 0) s_val[1] = cum;   // total over the cut-off
             __syncthreads();

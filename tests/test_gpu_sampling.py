@@ -88,8 +88,15 @@ def test_sample_full_sort_matches_oracle(ctx, pkg, orc, vocab, top_k):
         for si, sp in enumerate(settings):
             params = pkg.SampleParams(top_k=top_k, **sp)
             st_gpu = st_orc = 0x9E3779B97F4A7C15 + si
-            for trial in range(6):
+            for trial in range(8):
                 lg = (r.standard_normal(vocab) * 2.5).astype(np.float32)
+                if trial == 6:
+                    # every logit equal: the sums are whole numbers, crossing a
+                    # binade at every power of two
+                    lg[:] = 0.5
+                if trial == 7:
+                    # two levels: long runs of equal terms
+                    lg = np.where(r.random(vocab) < 0.3, 1.0, -2.0).astype(np.float32)
                 if trial == 1:
                     lg[r.integers(0, vocab, size=50)] = lg.max()     # ties at the top
                 if trial in (2, 3):
