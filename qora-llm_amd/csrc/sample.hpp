@@ -402,21 +402,21 @@ __device__ __forceinline__ uint32_t smp_sat_add(uint32_t a, uint32_t b) { return
 // Units of x on the grid 2^eu, rounded to nearest, and whether x is an event
 // by itself (exactly half a unit off the grid, not a finite number >= 0).
 __device__ __forceinline__ uint32_t smp_grid_units(float x, int eu, bool& ev) {
+    // every case computed and selected (no branches: 16 values a thread)
     const uint32_t b = __float_as_uint(x);
-    ev = false;
-    if (b == 0u || b == 0x80000000u) return 0u;        // +-0
-    if (b >= 0x7F800000u) {                            // inf, NaN, or a negative value
-        ev = true;
-        return 0u;
-    }
-    const uint32_t ef = b >> 23, mx = ef ? ((b & 0x7FFFFFu) | 0x800000u) : b;
+    const bool zero = (b & 0x7FFFFFFFu) == 0u;         // +-0
+    const bool bad = !zero && b >= 0x7F800000u;        // inf, NaN, or a negative value
+    const uint32_t ef = (b >> 23) & 0xFFu;
+    const uint32_t mx = ef ? ((b & 0x7FFFFFu) | 0x800000u) : (b & 0x7FFFFFu);
     const int sh = (ef ? (int)ef - 150 : -149) - eu;   // x = mx * 2^(eu + sh)
-    if (sh >= 0) return sh >= 8 ? kExactCap : min(mx << sh, kExactCap);
-    const int d = -sh;
-    if (d > 25) return 0u;                             // below a quarter unit
-    const uint32_t q = mx >> d, rem = mx & ((1u << d) - 1u), half = 1u << (d - 1);
-    ev = rem == half;
-    return q + (rem > half ? 1u : 0u);
+    // sh >= 0: whole units (at least 2^31 beyond 7: saturated)
+    const uint32_t up = sh >= 8 ? kExactCap : min(mx << (uint32_t)min(max(sh, 0), 7), kExactCap);
+    // sh < 0: rounded to nearest; below a quarter unit (d > 25) nothing, and no tie
+    const uint32_t d = (uint32_t)min(max(-sh, 1), 26);
+    const uint32_t rem = mx & ((1u << d) - 1u), half = 1u << (d - 1u);
+    const uint32_t dn = (mx >> d) + (rem > half ? 1u : 0u);
+    ev = bad || (!zero && sh < 0 && rem == half);
+    return zero || bad ? 0u : (sh >= 0 ? up : dn);
 }
 
 template <bool STOP, bool WRITE, typename Val>
@@ -429,26 +429,49 @@ __device__ float smp_exact_sum(uint32_t n, Val val, float stop, float* out, uint
         sh.done = 0;
     }
     __syncthreads();
-    for (;;) {
+    // windows of 4096 values, each loaded once (the next one in flight while
+    // this one is worked on); an event restarts within the window, the values
+    // before the restart masked out
+    // (loads are unconditional, at an index clamped into the values, and the
+    // values past n then replaced: no branch per value)
+    float xn[kExactJ];
+#pragma unroll
+    for (uint32_t j = 0; j < kExactJ; ++j) {
+        const uint32_t in = t * kExactJ + j;
+        const float v = val(min(in, n - 1u));
+        xn[j] = in < n ? v : 0.0f;
+    }
+    for (uint32_t w0 = 0; w0 < n; w0 += kExactChunk) {
+      const uint32_t i0 = w0 + t * kExactJ;
+      float x[kExactJ];
+#pragma unroll
+      for (uint32_t j = 0; j < kExactJ; ++j) {
+          x[j] = xn[j];
+          const uint32_t in = i0 + kExactChunk + j;
+          const float v = val(min(in, n - 1u));
+          xn[j] = in < n ? v : 0.0f;
+      }
+      for (;;) {
         const float s = sh.s;
         const uint32_t base = sh.base;
-        if (sh.done || base >= n) break;
+        if (sh.done || base >= n || base >= w0 + kExactChunk) break;
         // the binade of s: grid 2^eu, s = M units, its end at `bound` units
         const uint32_t sb = __float_as_uint(s);
         const int eu = sb < 0x00800000u ? -149 : (int)(sb >> 23) - 150;
         const uint32_t M = sb < 0x00800000u ? sb : ((sb & 0x7FFFFFu) | 0x800000u);
         const uint32_t bound = sb < 0x00800000u ? (1u << 23) : (1u << 24);
-        const uint32_t i0 = base + t * kExactJ;
-        float x[kExactJ];
         uint32_t loc[kExactJ];
         uint32_t evm = 0;                              // bit j: value j is an event by itself
         uint32_t acc = 0;
-#pragma unroll
-        for (uint32_t j = 0; j < kExactJ; ++j) x[j] = i0 + j < n ? val(i0 + j) : 0.0f;
+        // bit j: value j lies in [base, n)
+        const uint32_t lo = (uint32_t)min(max((int)(base - i0), 0), (int)kExactJ);
+        const uint32_t hi = (uint32_t)min(max((int)(n - i0), 0), (int)kExactJ);
+        const uint32_t liveb = ((1u << hi) - 1u) & ~((1u << lo) - 1u);
 #pragma unroll
         for (uint32_t j = 0; j < kExactJ; ++j) {
+            const bool live = (liveb >> j) & 1u;
             bool ev;
-            const uint32_t r = smp_grid_units(x[j], eu, ev);
+            const uint32_t r = smp_grid_units(live ? x[j] : 0.0f, eu, ev);
             evm |= (ev ? 1u : 0u) << j;
             acc = smp_sat_add(acc, r);
             loc[j] = acc;
@@ -469,14 +492,16 @@ __device__ float smp_exact_sum(uint32_t n, Val val, float stop, float* out, uint
         for (uint32_t w = 0; w < wave; ++w) prev = smp_sat_add(prev, sh.wtot[w]);
         const uint32_t excl = smp_sat_add(prev, lane ? exw : 0u);
         // this thread's first event (chunk index), then the block's
-        uint32_t fe = kExactNone;
+        uint32_t eb = evm;
 #pragma unroll
-        for (uint32_t j = kExactJ; j-- > 0;) {
+        for (uint32_t j = 0; j < kExactJ; ++j) {
             const uint32_t P = smp_sat_add(excl, loc[j]);
-            bool e = ((evm >> j) & 1u) != 0u || M + P >= bound;
-            if (STOP && !e) e = ldexpf((float)(M + P), eu) >= stop;
-            if (e && i0 + j < n) fe = t * kExactJ + j;
+            bool e = M + P >= bound;
+            if (STOP) e = e || ldexpf((float)(M + P), eu) >= stop;
+            eb |= (e ? 1u : 0u) << j;
         }
+        eb &= liveb;
+        uint32_t fe = eb ? t * kExactJ + (uint32_t)__builtin_ctz(eb) : kExactNone;
 #pragma unroll
         for (int off = 32; off >= 1; off >>= 1) fe = min(fe, (uint32_t)__shfl_xor((int)fe, off, kWave));
         if (lane == 0) sh.wmin[wave] = fe;
@@ -486,14 +511,15 @@ __device__ float smp_exact_sum(uint32_t n, Val val, float stop, float* out, uint
         if (WRITE) {
 #pragma unroll
             for (uint32_t j = 0; j < kExactJ; ++j)
-                if (i0 + j < n && t * kExactJ + j < first) out[i0 + j] = ldexpf((float)(M + smp_sat_add(excl, loc[j])), eu);
+                if (((liveb >> j) & 1u) && t * kExactJ + j < first)
+                    out[i0 + j] = ldexpf((float)(M + smp_sat_add(excl, loc[j])), eu);
         }
         if (first == kExactNone) {
             if (t == 0) {
                 uint32_t tot = 0;
                 for (uint32_t w = 0; w < 4; ++w) tot = smp_sat_add(tot, sh.wtot[w]);
                 sh.s = ldexpf((float)(M + tot), eu);
-                sh.base = min(n, base + kExactChunk);
+                sh.base = min(n, w0 + kExactChunk);
             }
         } else if (t == first / kExactJ) {
             // the event's value, added to the exact sum before it
@@ -507,7 +533,7 @@ __device__ float smp_exact_sum(uint32_t n, Val val, float stop, float* out, uint
             for (uint32_t q = 0; q < kExactJ; ++q)
                 if (q + 1 == j) before = smp_sat_add(excl, loc[q]);
             const float sn = __fadd_rn(ldexpf((float)(M + before), eu), xe);
-            const uint32_t gi = base + first;
+            const uint32_t gi = w0 + first;
             if (WRITE) out[gi] = sn;
             sh.s = sn;
             sh.base = gi + 1;
@@ -519,6 +545,8 @@ __device__ float smp_exact_sum(uint32_t n, Val val, float stop, float* out, uint
             }
         }
         __syncthreads();
+      }
+      if (sh.done) break;
     }
     const float r = sh.s;
     if (STOP) *stop_at = sh.stop_at;
