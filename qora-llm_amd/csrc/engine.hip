@@ -407,10 +407,11 @@ uint32_t attn_o_limit(const ModelState& m) {
 // device-coherent stores, polls and loads, and every query head re-reads its
 // KV head's rows, so the step beats the split attention only while each
 // column tile holds few positions: by default up to kChunkDefaultPerTile per
-// tile (measured on SmolLM3-3B: +4.4% at 300-500 positions, +2.8% at ~730,
-// -0.8% at ~990). QORA_HIP_ATTN_CHUNK sets the bound (0: never chunked), up
-// to kFusedMaxPasses passes a tile.
-constexpr uint32_t kChunkDefaultPerTile = 48;
+// tile (measured on SmolLM3-3B against the split attention: +2.2% at 280-340
+// positions, even at 480-540, -2.1% at 680-740 and at 900-960).
+// QORA_HIP_ATTN_CHUNK sets the bound (0: never chunked), up to
+// kFusedMaxPasses passes a tile.
+constexpr uint32_t kChunkDefaultPerTile = 32;
 
 uint32_t attn_ch_limit(const ModelState& m, int cus) {
     if (m.fmt != FMT_Q4 || !attn_chunk_supported(m.pl_o, m.hd, m.H, m.groups, m.attn_s_max, cus)) return 0;

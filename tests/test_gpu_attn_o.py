@@ -48,7 +48,7 @@ def test_limit_policy(ctx, pkg, monkeypatch):
 
 def test_chunk_limit_policy(ctx, pkg, monkeypatch):
     """The chunked step covers [attn_o_limit, attn_chunk_limit): by default
-    48 positions per column tile, at most 8 passes of 32 positions per tile,
+    32 positions per column tile, at most 8 passes of 32 positions per tile,
     never above the capacity, and never at or below the fused bound;
     QORA_HIP_ATTN_CHUNK sets it."""
     w = _model(pkg, 128, positions=4096)
@@ -57,7 +57,7 @@ def test_chunk_limit_policy(ctx, pkg, monkeypatch):
     assert top > 256 and top % 256 == 0                 # 8 passes x 32 positions x the column tiles
     tiles = top // 256
     monkeypatch.delenv("QORA_HIP_ATTN_CHUNK")
-    dflt = 48 * tiles if 48 * tiles > 256 else 0        # none when at or below the fused bound
+    dflt = 32 * tiles if 32 * tiles > 256 else 0        # none when at or below the fused bound
     assert pkg.HipBackend(ctx, w, kv_capacity=4096).attn_chunk_limit() == dflt
     assert pkg.HipBackend(ctx, w, kv_capacity=300).attn_chunk_limit() == (300 if dflt else 0)
     assert pkg.HipBackend(ctx, w, kv_capacity=256).attn_chunk_limit() == 0   # all fused
