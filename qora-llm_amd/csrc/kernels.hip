@@ -857,8 +857,8 @@ hipError_t launch_sample(const float* logits, const SampleParams& p, hipStream_t
     // the block kernel reads the logits and applies the penalties itself
     SampleParams q = p;
     q.logits = logits;
-    hipLaunchKernelGGL(smp_block_topk_kernel, dim3(p.blocks), dim3(256), 0, stream, q);
-    hipLaunchKernelGGL(smp_final_kernel, dim3(1), dim3(256), 0, stream, q);
+    hipLaunchKernelGGL(smp_block_topk_kernel, dim3(p.blocks), dim3(kSmpTopkThreads), 0, stream, q);
+    hipLaunchKernelGGL(smp_final_kernel, dim3(1), dim3(kSmpFinalThreads), 0, stream, q);
     return hipGetLastError();
 }
 

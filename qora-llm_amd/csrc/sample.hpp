@@ -33,6 +33,8 @@ namespace qora {
 constexpr uint32_t kSmpBlock = 2048;    // logits per block in the first pass
 constexpr uint32_t kSmpKeep = 64;       // candidates kept per block (top_k <= kSmpKeep)
 constexpr uint32_t kSmpFinal = 4096;    // candidate keys sorted by the final block
+constexpr uint32_t kSmpTopkThreads = 512;    // 8 waves: 4 runs of 64 keys each
+constexpr uint32_t kSmpFinalThreads = 1024;  // 16 waves: two merges each in the first round
 constexpr uint32_t kSmpSortMax = 1u << 22;   // keys of the full-sort path (vocabularies up to 4M)
 
 // Orderable key: ascending key = value descending, then index ascending.
@@ -185,9 +187,10 @@ __global__ __launch_bounds__(256) void smp_penalty_kernel(SampleParams p) {
     p.work[e.token] = smp_penalise(p, e, p.work[e.token]);
 }
 
-__global__ __launch_bounds__(256) void smp_block_topk_kernel(SampleParams p) {
-    static_assert(kSmpKeep == 64 && kSmpBlock % (4 * 64) == 0, "64-key runs, four waves");
-    constexpr uint32_t NR = kSmpBlock / 64, RPW = NR / 4;     // runs, runs per wave
+__global__ __launch_bounds__(kSmpTopkThreads) void smp_block_topk_kernel(SampleParams p) {
+    constexpr uint32_t NWV = kSmpTopkThreads / kWave;
+    static_assert(kSmpKeep == 64 && kSmpBlock % (NWV * 64) == 0, "64-key runs, NWV waves");
+    constexpr uint32_t NR = kSmpBlock / 64, RPW = NR / NWV;   // runs, runs per wave
     __shared__ unsigned long long runs[2][kSmpBlock];
     const uint32_t lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
     const uint32_t base = blockIdx.x * kSmpBlock;
@@ -196,42 +199,42 @@ __global__ __launch_bounds__(256) void smp_block_topk_kernel(SampleParams p) {
     // sorted across the lanes
     float x[RPW];
 #pragma unroll
-    for (uint32_t q = 0; q < RPW; ++q) x[q] = p.logits[min(base + (wave + 4 * q) * 64 + lane, p.vocab - 1)];
+    for (uint32_t q = 0; q < RPW; ++q) x[q] = p.logits[min(base + (wave + NWV * q) * 64 + lane, p.vocab - 1)];
     if (p.n_pen) {
         float* xs = reinterpret_cast<float*>(runs[1]);
 #pragma unroll
-        for (uint32_t q = 0; q < RPW; ++q) xs[(wave + 4 * q) * 64 + lane] = x[q];
+        for (uint32_t q = 0; q < RPW; ++q) xs[(wave + NWV * q) * 64 + lane] = x[q];
         __syncthreads();
-        for (uint32_t j = threadIdx.x; j < p.n_pen; j += 256) {
+        for (uint32_t j = threadIdx.x; j < p.n_pen; j += kSmpTopkThreads) {
             const SamplePenalty e = p.pen[j];
             if (e.token >= base && e.token - base < kSmpBlock) xs[e.token - base] = smp_penalise(p, e, xs[e.token - base]);
         }
         __syncthreads();
 #pragma unroll
-        for (uint32_t q = 0; q < RPW; ++q) x[q] = xs[(wave + 4 * q) * 64 + lane];
+        for (uint32_t q = 0; q < RPW; ++q) x[q] = xs[(wave + NWV * q) * 64 + lane];
         __syncthreads();   // runs[1] is the merge buffer below
     }
     unsigned long long v[RPW];
 #pragma unroll
     for (uint32_t q = 0; q < RPW; ++q) {
-        const uint32_t i = base + (wave + 4 * q) * 64 + lane;
+        const uint32_t i = base + (wave + NWV * q) * 64 + lane;
         v[q] = i < p.vocab ? smp_key(x[q], i) : ~0ull;
     }
 #pragma unroll
-    for (uint32_t q = 0; q < RPW; ++q) runs[0][(wave + 4 * q) * 64 + lane] = smp_wave_sort(v[q]);
-    const uint32_t src = smp_merge_runs<kSmpBlock, 4>(runs, NR, 0);
+    for (uint32_t q = 0; q < RPW; ++q) runs[0][(wave + NWV * q) * 64 + lane] = smp_wave_sort(v[q]);
+    const uint32_t src = smp_merge_runs<kSmpBlock, NWV>(runs, NR, 0);
     if (wave == 0) p.cand[blockIdx.x * kSmpKeep + lane] = runs[src][lane];
 }
 
-__global__ __launch_bounds__(256) void smp_final_kernel(SampleParams p) {
+__global__ __launch_bounds__(kSmpFinalThreads) void smp_final_kernel(SampleParams p) {
     static_assert(kSmpFinal % 64 == 0 && kSmpKeep == 64, "64-key runs");
     __shared__ unsigned long long runs[2][kSmpFinal];
     __shared__ float prob[kSmpKeep];
     __shared__ float s_inv;
     // the blocks' candidate runs (each ascending), then runs of ~0 padding
     const uint32_t nc = p.blocks * kSmpKeep;
-    for (uint32_t j = threadIdx.x; j < kSmpFinal; j += 256) runs[0][j] = j < nc ? p.cand[j] : ~0ull;
-    const uint32_t src = smp_merge_runs<kSmpFinal, 4>(runs, kSmpFinal / 64, 0);
+    for (uint32_t j = threadIdx.x; j < kSmpFinal; j += kSmpFinalThreads) runs[0][j] = j < nc ? p.cand[j] : ~0ull;
+    const uint32_t src = smp_merge_runs<kSmpFinal, kSmpFinalThreads / kWave>(runs, kSmpFinal / 64, 0);
     const unsigned long long* keys = runs[src];
     const uint32_t k = min(p.top_k, min(p.vocab, kSmpKeep));
     const float inv_temp = p.temperature > 0.0f ? 1.0f / p.temperature : 0.0f;
