@@ -32,7 +32,7 @@ namespace qora {
 
 constexpr uint32_t kSmpBlock = 2048;    // logits per block in the first pass
 constexpr uint32_t kSmpKeep = 64;       // candidates kept per block (top_k <= kSmpKeep)
-constexpr uint32_t kSmpFinal = 4096;    // candidate keys sorted by the final block
+constexpr uint32_t kSmpFinal = 4096;    // candidate keys merged by the final block (64 runs of 64)
 constexpr uint32_t kSmpTopkThreads = 512;    // 8 waves: 4 runs of 64 keys each
 constexpr uint32_t kSmpFinalThreads = 1024;  // 16 waves: two merges each in the first round
 constexpr uint32_t kSmpSortMax = 1u << 22;   // keys of the full-sort path (vocabularies up to 4M)
