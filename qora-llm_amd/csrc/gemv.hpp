@@ -190,7 +190,15 @@ __global__ __launch_bounds__(256) void gemv_tile_kernel(GemvParams p, int gt, in
 }
 
 template <int FMT, int GT, int RPL, int PRO, bool TILED>
-__global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
+__global__ __launch_bounds__(256) void gemv_kernel(const uint8_t* tw, const uint16_t* ts, const void* xin,
+                                                   const void* xaux, uint32_t k, uint32_t tiles_a, uint32_t rps,
+                                                   uint32_t ss_nn, GemvParams p) {
+    // (the arguments of the first loads come ahead of the parameter block and
+    // are preloaded into scalar registers at wave launch: tile-layout
+    // weights and scales, the input and its second operand, K, the tile
+    // count, the rows per K slice, ss_n | norm_n << 8)
+    const uint32_t ss_n = ss_nn & 0xFFu, norm_n = ss_nn >> 8;
+    const long long* xacc = static_cast<const long long*>(xin);
     constexpr int NT = 256;
     constexpr int RL = NT / GT;          // row lanes
     constexpr int COLS = GT * 32;        // columns per tile
@@ -208,14 +216,13 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
     const int t = threadIdx.x;
     const int gi = t % GT;
     const int rl = t / GT;
-    const uint32_t tile = blockIdx.x % p.tiles;
-    const uint32_t split = blockIdx.x / p.tiles;
-    const uint32_t k0 = split * p.rows_per_split;
-    const uint32_t k1 = min(p.k, k0 + p.rows_per_split);
-    const uint32_t klast = p.k - 1u;
-
-    if (p.zero_ptr)
-        for (uint32_t i = blockIdx.x * NT + t; i < p.zero_n; i += gridDim.x * NT) p.zero_ptr[i] = 0;
+    const uint32_t tile = blockIdx.x % tiles_a;
+    const uint32_t split = blockIdx.x / tiles_a;
+    const uint32_t k0 = split * rps;
+    const uint32_t k1 = min(k, k0 + rps);
+    const uint32_t klast = k - 1u;
+    // (the accumulator this launch clears is cleared at the end: stores issued
+    // first would count in vmcnt ahead of the input and weight loads)
 
     // ---- which segment / group this lane reads ----
     const LaneSrc src = lane_source(p, tile, gi, GT);
@@ -234,18 +241,18 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
 #pragma unroll
     for (int j = 0; j < RPL; ++j) {
         const uint32_t rc = min(k0 + rl + j * RL, klast);
-        if constexpr (PRO == PRO_PLAIN) xv[j] = p.x[rc];
+        if constexpr (PRO == PRO_PLAIN) xv[j] = static_cast<const float*>(xin)[rc];
         if constexpr (PRO == PRO_GAMMA_FIXED) {
-            xa[j] = p.xacc[rc];
-            gm[j] = p.gamma[rc];
+            xa[j] = xacc[rc];
+            gm[j] = static_cast<const uint16_t*>(xaux)[rc];
         }
         if constexpr (PRO == PRO_SILU_FIXED) {
-            xa[j] = p.xacc[rc];
-            ua[j] = p.xacc[p.k + rc];
+            xa[j] = xacc[rc];
+            ua[j] = xacc[k + rc];
         }
     }
     float ss_part = 0.f;
-    if constexpr (PRO == PRO_SILU_FIXED) ss_part = p.ss_in[min((uint32_t)(t & (kWave - 1)), p.ss_n - 1u)];
+    if constexpr (PRO == PRO_SILU_FIXED) ss_part = static_cast<const float*>(xaux)[min((uint32_t)(t & (kWave - 1)), ss_n - 1u)];
 
     // ---- 2. weight loads ----
     float acc[32];
@@ -255,11 +262,11 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
     uint32_t sq[FMT == FMT_Q4 ? RPL : 1];
     if constexpr (FMT == FMT_Q4 && TILED) {
         // one contiguous block per workgroup: step j reads 4 KB, lane t 16 B
-        const uint8_t* bw = p.tw + (uint64_t)blockIdx.x * (RPL * 4096u) + (uint32_t)t * 16u;
+        const uint8_t* bw = tw + (uint64_t)blockIdx.x * (RPL * 4096u) + (uint32_t)t * 16u;
 #pragma unroll
         for (int j = 0; j < RPL; ++j) wq[j] = *reinterpret_cast<const uint4*>(bw + j * 4096u);
         // the lane's RPL scales are adjacent
-        const uint16_t* bs = p.ts + ((uint64_t)blockIdx.x * 256u + (uint32_t)t) * RPL;
+        const uint16_t* bs = ts + ((uint64_t)blockIdx.x * 256u + (uint32_t)t) * RPL;
         if constexpr (RPL >= 8) {
 #pragma unroll
             for (int h = 0; h < RPL / 8; ++h) {
@@ -302,7 +309,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
             xv[j] = xf * h2f((uint16_t)gm[j]);
         }
     } else if constexpr (PRO == PRO_SILU_FIXED) {
-        const float inv = 1.0f / sqrtf(wave_sum(t % kWave < (int)p.ss_n ? ss_part : 0.f) / (float)p.norm_n + 1e-6f);
+        const float inv = 1.0f / sqrtf(wave_sum(t % kWave < (int)ss_n ? ss_part : 0.f) / (float)norm_n + 1e-6f);
 #pragma unroll
         for (int j = 0; j < RPL; ++j) {
             const bool ok = k0 + rl + j * RL < k1;
@@ -345,7 +352,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
 #pragma unroll
             for (int j = 0; j < B; ++j) {
                 if constexpr (TILED) {
-                    const uint8_t* bw = p.tw + ((uint64_t)blockIdx.x * RPL + (uint32_t)(j0 + j)) * 16384u +
+                    const uint8_t* bw = tw + ((uint64_t)blockIdx.x * RPL + (uint32_t)(j0 + j)) * 16384u +
                                         (uint32_t)t * 16u;
 #pragma unroll
                     for (int v = 0; v < 4; ++v) wv[j][v] = *reinterpret_cast<const uint4*>(bw + v * 4096u);
@@ -414,6 +421,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
         }
         if (local < lim) fixed_add(p.acc + col0 + local, s, p.range_flag);
     }
+    // the accumulator this launch clears (for a later kernel), after the
+    // launch's own loads
+    if (p.zero_ptr)
+        for (uint32_t i = blockIdx.x * NT + t; i < p.zero_n; i += gridDim.x * NT) p.zero_ptr[i] = 0;
 }
 
 // acc (fixed point) -> y (fp32); paired: y[j] = silu(acc[j]) * acc[n + j].

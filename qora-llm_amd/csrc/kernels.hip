@@ -152,19 +152,28 @@ void apply_plan(const GemvPlan& plan, GemvParams* p) {
 template <int FMT, int GT, int PRO, bool TILED>
 static hipError_t launch_gemv_pro(const GemvPlan& plan, const GemvParams& p, hipStream_t stream) {
     const dim3 grid(plan.blocks()), block(256);
+    // the first loads' arguments ahead of the parameter block (preloaded into
+    // scalar registers at wave launch); ss_n | norm_n << 8 in one word
+    if (p.ss_n > 0xFFu || p.norm_n >= (1u << 24)) return hipErrorInvalidValue;
+    const void* xin = PRO == PRO_PLAIN ? static_cast<const void*>(p.x) : static_cast<const void*>(p.xacc);
+    const void* xaux = PRO == PRO_GAMMA_FIXED ? static_cast<const void*>(p.gamma)
+                                              : static_cast<const void*>(p.ss_in);
+    const uint32_t ss_nn = p.ss_n | (p.norm_n << 8);
+#define QORA_GEMV_ARGS p.tw, p.ts, xin, xaux, p.k, p.tiles, p.rows_per_split, ss_nn, p
     switch (plan.rpl) {
-    case 1: hipLaunchKernelGGL((gemv_kernel<FMT, GT, 1, PRO, TILED>), grid, block, 0, stream, p); break;
-    case 2: hipLaunchKernelGGL((gemv_kernel<FMT, GT, 2, PRO, TILED>), grid, block, 0, stream, p); break;
-    case 4: hipLaunchKernelGGL((gemv_kernel<FMT, GT, 4, PRO, TILED>), grid, block, 0, stream, p); break;
-    case 8: hipLaunchKernelGGL((gemv_kernel<FMT, GT, 8, PRO, TILED>), grid, block, 0, stream, p); break;
+    case 1: hipLaunchKernelGGL((gemv_kernel<FMT, GT, 1, PRO, TILED>), grid, block, 0, stream, QORA_GEMV_ARGS); break;
+    case 2: hipLaunchKernelGGL((gemv_kernel<FMT, GT, 2, PRO, TILED>), grid, block, 0, stream, QORA_GEMV_ARGS); break;
+    case 4: hipLaunchKernelGGL((gemv_kernel<FMT, GT, 4, PRO, TILED>), grid, block, 0, stream, QORA_GEMV_ARGS); break;
+    case 8: hipLaunchKernelGGL((gemv_kernel<FMT, GT, 8, PRO, TILED>), grid, block, 0, stream, QORA_GEMV_ARGS); break;
     case 16:
         if constexpr (FMT == FMT_Q4) {
-            hipLaunchKernelGGL((gemv_kernel<FMT, GT, 16, PRO, TILED>), grid, block, 0, stream, p);
+            hipLaunchKernelGGL((gemv_kernel<FMT, GT, 16, PRO, TILED>), grid, block, 0, stream, QORA_GEMV_ARGS);
             break;
         }
         return hipErrorInvalidValue;
     default: return hipErrorInvalidValue;
     }
+#undef QORA_GEMV_ARGS
     return hipGetLastError();
 }
 
