@@ -261,3 +261,45 @@ def test_bench_refuses_more_than_one_gpu():
                        text=True, timeout=120)
     assert r.returncode == 2
     assert "one GPU" in r.stdout
+
+
+def _header_params():
+    """{function: parameter count} of include/qora_hip.h."""
+    text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    out = {}
+    for name, args in re.findall(r"\b(qora_[a-z0-9_]+)\s*\(([^;{]*?)\)\s*;", text):
+        args = args.strip()
+        out[name] = 0 if args in ("", "void") else args.count(",") + 1
+    return out
+
+
+def _header_struct_fields(name):
+    text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    body = re.search(r"typedef struct \{([^}]*)\}\s*" + name + r"\s*;", text).group(1)
+    fields = []
+    for decl in body.split(";"):
+        decl = decl.strip()
+        if decl:
+            head, *rest = [p.strip() for p in decl.split(",")]
+            fields.append(re.findall(r"(\w+)\s*$", head)[0])
+            fields.extend(rest)
+    return fields
+
+
+def test_rust_binding_matches_the_header():
+    """qora-llm_amd/rust/qora-hip-sys/src/lib.rs (the FFI crate a Rust host links)
+    declares every header function with the same number of arguments, and its
+    #[repr(C)] structs have the header's fields in the header's order."""
+    src = open(os.path.join(ROOT, "qora-llm_amd", "rust", "qora-hip-sys", "src", "lib.rs")).read()
+    src = re.sub(r"//[^\n]*", "", src)
+    rust = {}
+    for name, args in re.findall(r"pub fn (qora_[a-z0-9_]+)\s*\(([^)]*)\)", src):
+        args = args.strip().rstrip(",")
+        rust[name] = 0 if not args else args.count(",") + 1
+    want = _header_params()
+    assert set(rust) == set(want), (sorted(set(want) - set(rust)), sorted(set(rust) - set(want)))
+    assert {n: rust[n] for n in want if rust[n] != want[n]} == {}
+    for struct in ("qora_model_desc", "qora_sample_params", "qora_host_model"):
+        body = re.search(r"pub struct " + struct + r"\s*\{([^}]*)\}", src).group(1)
+        rfields = re.findall(r"pub (\w+)\s*:", body)
+        assert rfields == _header_struct_fields(struct), struct
