@@ -595,6 +595,83 @@ def profile_kernel(launches=8, shape="gate_up"):
         ctx.gemv_release(g)
 
 
+def probe_overlap(pkg, hip, cfg, stream_counts=(1, 2, 4, 8)):
+    """The decode step's GEMV kernel with its launch boundaries overlapped:
+    independent launches over >= 768 MB of distinct packed copies, spread
+    round-robin over N streams forked from the context stream inside one
+    captured graph (streams and events are created before the capture), so
+    a launch's ramp and tail can overlap the next one's. Average microseconds
+    per launch and GB/s of algorithmic bytes, per shape and N."""
+    import dataclasses
+    h = hip.h
+    h.hipStreamCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+    h.hipStreamDestroy.argtypes = [ctypes.c_void_p]
+    h.hipStreamWaitEvent.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint]
+    w = pkg.synthetic_model(dataclasses.replace(cfg, num_layers=1, vocab=1000), seed=0, rope_positions=2048)
+    ctx = pkg.HipContext(0)
+    out = {}
+    try:
+        be = pkg.HipBackend(ctx, w, kv_capacity=2048, kv_dtype=pkg.KV_F32)
+        c = be.config
+        x = ctx.malloc(4 * c.intermediate)
+        acc = ctx.malloc(8 * 2 * c.intermediate)
+        ctx.h2d(x, pkg.synth_f32(0, 77, c.intermediate))
+        shapes = c.weight_shapes()
+        for label, j, paired in (("down 11008x2048", 6, False), ("gate 2048x11008", 4, False),
+                                 ("gate+up 2048x(2x11008)", 4, True)):
+            k, n = shapes[j]
+            nb = (k * n // 2 + k * n // 16) * (2 if paired else 1)
+            algo = nb + 4 * k + (8 if paired else 4) * n
+            per = {}
+            for ns in stream_counts:
+                gids = [ctx.gemv_prepare(int(be.wids[0, j]), int(be.wids[0, 5]) if paired else 0, paired)
+                        for _ in range(max(8, math.ceil((768 << 20) / nb)))]
+                streams = []
+                for _ in range(ns):
+                    s = ctypes.c_void_p()
+                    assert h.hipStreamCreate(ctypes.byref(s)) == 0
+                    streams.append(s.value)
+                fork, joins = hip.event(), [hip.event() for _ in streams]
+                try:
+                    for g in gids[:2]:
+                        ctx.check(ctx.lib.qora_hip_gemv_run(ctx.h, g, x, acc, None), "gemv_run")
+                    ctx.synchronize()
+                    ctx.capture_begin()
+                    hip.record(fork, ctx.stream)
+                    for s in streams:
+                        assert h.hipStreamWaitEvent(s, fork, 0) == 0
+                    for i, g in enumerate(gids):
+                        ctx.check(ctx.lib.qora_hip_gemv_run(ctx.h, g, x, acc, ctypes.c_void_p(streams[i % ns])),
+                                  "gemv_run")
+                    for s, e in zip(streams, joins):
+                        hip.record(e, s)
+                        assert h.hipStreamWaitEvent(ctx.stream, e, 0) == 0
+                    gr = ctx.capture_end()
+                    try:
+                        ctx.graph_launch(gr, 1)
+                        ctx.synchronize()
+                        a, b, reps = hip.event(), hip.event(), 3
+                        hip.record(a, ctx.stream)
+                        ctx.graph_launch(gr, reps)
+                        hip.record(b, ctx.stream)
+                        ms = hip.elapsed_ms(a, b) / (reps * len(gids))
+                    finally:
+                        ctx.graph_destroy(gr)
+                finally:
+                    ctx.synchronize()
+                    for s in streams:
+                        h.hipStreamDestroy(s)
+                    for g in gids:
+                        ctx.gemv_release(g)
+                per[f"{ns} streams"] = {"us": round(ms * 1e3, 3), "gbps": round(algo / (ms * 1e-3) / 1e9, 1)}
+            out[label] = per
+        ctx.free(x)
+        ctx.free(acc)
+    finally:
+        ctx.close()
+    return out
+
+
 def probe_residency(pkg, hip, cfg, prompt, steps=128, warmup=8):
     """What bounds the decode step besides HBM bandwidth: the per-launch floor
     of a captured graph of dependent launches (the smallest GEMV, 256 -> 128),
@@ -686,6 +763,8 @@ def main():
                     help="prompt length of --profile-decode: 64, or 1920 for the 2048-context workload")
     ap.add_argument("--probe-residency", action="store_true",
                     help="only the launch-floor and cache-residency probes of the decode step")
+    ap.add_argument("--probe-overlap", action="store_true",
+                    help="only the GEMV kernel with independent launches overlapped on 1, 2, 4 and 8 streams")
     ap.add_argument("--profile-kernel", action="store_true",
                     help="only launch the dominant kernel (gate|up GEMV) eagerly, after a device copy of "
                          "known size, for hardware-counter runs")
@@ -700,6 +779,10 @@ def main():
         sys.exit(2)
     if args.profile_kernel:
         profile_kernel(shape=args.profile_shape)
+        return
+    if args.probe_overlap:
+        pkg = entry.load_package()
+        print(json.dumps({"probe_overlap": probe_overlap(pkg, Hip(), pkg.SMOLLM3_3B)}), flush=True)
         return
     if args.probe_residency:
         pkg = entry.load_package()
