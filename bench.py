@@ -595,6 +595,50 @@ def profile_kernel(launches=8, shape="gate_up"):
         ctx.gemv_release(g)
 
 
+def probe_context(pkg, cfg, n_tok=32):
+    """Host-driven greedy decode rate against the KV cache length: every layer's
+    cache is filled with seeded random K/V rows (qora_hip_kv_upload) up to the
+    context, then n_tok tokens are timed. An f32 cache of 2048 positions (the
+    fused attention + o step below 256 positions, the chunked step below 512,
+    the split attention above), and an f16 cache of 32768 positions."""
+    import dataclasses
+    out = {}
+    kvd = cfg.num_kv_heads * cfg.head_dim
+    r = np.random.default_rng(7)
+    for cap, kv_dtype, label, ctxs in ((2048, pkg.KV_F32, "f32 cache, capacity 2048",
+                                        (64, 128, 192, 256, 320, 448, 512, 768, 1024, 1536, 2000)),
+                                       (32768, pkg.KV_F16, "f16 cache, capacity 32768",
+                                        (512, 1024, 2000, 2048, 3000, 4096, 8192, 16384, 24576, 32700))):
+        cos_t, sin_t = pkg.rope_tables(cap, cfg.rope_half_dim, cfg.rope_theta)
+        w = dataclasses.replace(pkg.synthetic_model(cfg, seed=0, rope_positions=64), rope_cos=cos_t, rope_sin=sin_t)
+        ctx = pkg.HipContext(0)
+        try:
+            be = pkg.HipBackend(ctx, w, kv_capacity=cap, kv_dtype=kv_dtype)
+            per = {}
+            for n_ctx in ctxs:
+                fill = n_ctx - 4
+                k = r.standard_normal((fill, kvd), dtype=np.float32)
+                v = r.standard_normal((fill, kvd), dtype=np.float32)
+                for layer in range(cfg.num_layers):
+                    be.kv_upload(layer, k, v)
+                del k, v
+                tok = 1
+                for _ in range(4):
+                    _, tok = be.forward_decode_raw(tok, want_logits=False)
+                ctx.synchronize()
+                t0 = time.perf_counter()
+                for _ in range(n_tok):
+                    _, tok = be.forward_decode_raw(tok, want_logits=False)
+                ctx.synchronize()
+                per[f"{n_ctx}..{n_ctx + n_tok - 1}"] = round(n_tok / (time.perf_counter() - t0), 1)
+                print(f"# {label}: positions {n_ctx}..{n_ctx + n_tok - 1}: {per[f'{n_ctx}..{n_ctx + n_tok - 1}']} tok/s",
+                      file=sys.stderr, flush=True)
+            out[label] = {"attn_o_limit": be.attn_o_limit(), "attn_chunk_limit": be.attn_chunk_limit(), "tok_s": per}
+        finally:
+            ctx.close()
+    return out
+
+
 def probe_overlap(pkg, hip, cfg, stream_counts=(1, 2, 4, 8)):
     """The decode step's GEMV kernel with its launch boundaries overlapped:
     independent launches over >= 768 MB of distinct packed copies, spread
@@ -763,6 +807,8 @@ def main():
                     help="prompt length of --profile-decode: 64, or 1920 for the 2048-context workload")
     ap.add_argument("--probe-residency", action="store_true",
                     help="only the launch-floor and cache-residency probes of the decode step")
+    ap.add_argument("--probe-context", action="store_true",
+                    help="only the decode rate against the KV cache length (f32 up to 2048, f16 up to 32768)")
     ap.add_argument("--probe-overlap", action="store_true",
                     help="only the GEMV kernel with independent launches overlapped on 1, 2, 4 and 8 streams")
     ap.add_argument("--profile-kernel", action="store_true",
@@ -779,6 +825,10 @@ def main():
         sys.exit(2)
     if args.profile_kernel:
         profile_kernel(shape=args.profile_shape)
+        return
+    if args.probe_context:
+        pkg = entry.load_package()
+        print(json.dumps({"probe_context": probe_context(pkg, pkg.SMOLLM3_3B)}), flush=True)
         return
     if args.probe_overlap:
         pkg = entry.load_package()

@@ -118,6 +118,13 @@ struct ModelState {
     EmbedParams p_emb_tok{}, p_emb_prompt{};
     hipGraphExec_t g_step = nullptr;
     hipGraphExec_t g_prefill = nullptr;
+    // split steps that append a position below split_short_max run the
+    // one-subgroup split attention (p_attn_ss) although the capacity's split
+    // length would pick the long-context kernel (0: no separate variant)
+    uint32_t split_short_max = 0;
+    std::vector<AttnParams> p_attn_ss;
+    hipGraphExec_t g_step_ss = nullptr;
+    hipGraphExec_t g_prefill_ss = nullptr;
     // the same steps with the fused attention + o kernel, one per pass count
     // (index np - 1: contexts of 32 (np - 1) < L <= 32 np positions)
     hipGraphExec_t g_step_ao[kFusedMaxPasses] = {};
@@ -296,6 +303,8 @@ void free_model(qora_hip_ctx* c) {
     (void)hipStreamSynchronize(c->stream);
     if (m.g_step) (void)hipGraphExecDestroy(m.g_step);
     if (m.g_prefill) (void)hipGraphExecDestroy(m.g_prefill);
+    if (m.g_step_ss) (void)hipGraphExecDestroy(m.g_step_ss);
+    if (m.g_prefill_ss) (void)hipGraphExecDestroy(m.g_prefill_ss);
     for (hipGraphExec_t g : m.g_step_ao)
         if (g) (void)hipGraphExecDestroy(g);
     for (hipGraphExec_t g : m.g_prefill_ao)
@@ -350,7 +359,7 @@ int pack_model_gemv(qora_hip_ctx* c, int fmt, const GemvPlan& pl, GemvParams* p)
 // np > 0: attention inside the o GEMV for contexts of at most 32 np
 // positions (short contexts, see attn_o_max), or with chunked, the chunked
 // step whose column tiles take 32 np positions each; np = 0: split attention
-int record_step(qora_hip_ctx* c, bool with_lm_head, uint32_t np, bool chunked = false) {
+int record_step(qora_hip_ctx* c, bool with_lm_head, uint32_t np, bool chunked = false, bool split_short = false) {
     ModelState& m = c->m;
     const hipStream_t s = c->stream;
     HIP_TRY(c, launch_embed(with_lm_head ? m.p_emb_tok : m.p_emb_prompt, s));
@@ -359,7 +368,7 @@ int record_step(qora_hip_ctx* c, bool with_lm_head, uint32_t np, bool chunked = 
         if (np) {
             HIP_TRY(c, launch_attn_o(m.pl_o, m.p_ao[l], np, chunked, s));
         } else {
-            HIP_TRY(c, launch_attn(m.p_attn[l], s));
+            HIP_TRY(c, launch_attn(split_short ? m.p_attn_ss[l] : m.p_attn[l], s));
             HIP_TRY(c, launch_gemv(m.fmt, m.pl_o, m.p_o[l], s));
         }
         HIP_TRY(c, launch_gemv(m.fmt, m.pl_gu, m.p_gu[l], s));
@@ -379,6 +388,8 @@ int record_step(qora_hip_ctx* c, bool with_lm_head, uint32_t np, bool chunked = 
 // replaying the captured graph (for profilers that do not follow graphs).
 // Attention subgroups per block (1 or 4): by default 4 when a split can hold
 // more than one 32-position pass; QORA_HIP_ATTN_NSG overrides.
+constexpr uint32_t kSplitShortMax = 4096;   // see split_short_max
+
 uint32_t attn_nsg(uint32_t max_chunk) {
     const char* v = tuning_env("QORA_HIP_ATTN_NSG");
     if (v && *v) return std::atoi(v) > 1 ? 4u : 1u;
@@ -428,12 +439,13 @@ uint32_t attn_ch_limit(const ModelState& m, int cus) {
 struct StepAttn {
     uint32_t np;
     bool chunked;
+    bool split_short;           // np = 0: the one-subgroup split attention (p_attn_ss)
 };
 
 StepAttn step_attn(const ModelState& m, uint64_t pos) {
-    if (pos < (uint64_t)m.attn_o_max) return {(uint32_t)(pos / kFusedPass) + 1u, false};
-    if (pos < (uint64_t)m.attn_ch_max) return {(uint32_t)(pos / ((uint64_t)kFusedPass * m.pl_o.tiles)) + 1u, true};
-    return {0u, false};
+    if (pos < (uint64_t)m.attn_o_max) return {(uint32_t)(pos / kFusedPass) + 1u, false, false};
+    if (pos < (uint64_t)m.attn_ch_max) return {(uint32_t)(pos / ((uint64_t)kFusedPass * m.pl_o.tiles)) + 1u, true, false};
+    return {0u, false, pos < (uint64_t)m.split_short_max};
 }
 
 bool eager_mode() {
@@ -445,17 +457,19 @@ bool eager_mode() {
 int launch_step(qora_hip_ctx* c, bool with_lm_head, uint64_t pos) {
     ModelState& m = c->m;
     const StepAttn sa = step_attn(m, pos);
-    if (eager_mode()) return record_step(c, with_lm_head, sa.np, sa.chunked);
-    hipGraphExec_t g = !sa.np       ? (with_lm_head ? m.g_step : m.g_prefill)
+    if (eager_mode()) return record_step(c, with_lm_head, sa.np, sa.chunked, sa.split_short);
+    hipGraphExec_t g = !sa.np ? (sa.split_short ? (with_lm_head ? m.g_step_ss : m.g_prefill_ss)
+                                                : (with_lm_head ? m.g_step : m.g_prefill))
                        : sa.chunked ? (with_lm_head ? m.g_step_ch[sa.np - 1] : m.g_prefill_ch[sa.np - 1])
                                     : (with_lm_head ? m.g_step_ao[sa.np - 1] : m.g_prefill_ao[sa.np - 1]);
     HIP_TRY(c, hipGraphLaunch(g, c->stream));
     return QORA_HIP_OK;
 }
 
-int capture_step(qora_hip_ctx* c, bool with_lm_head, uint32_t np, hipGraphExec_t* out, bool chunked = false) {
+int capture_step(qora_hip_ctx* c, bool with_lm_head, uint32_t np, hipGraphExec_t* out, bool chunked = false,
+                 bool split_short = false) {
     HIP_TRY(c, hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
-    const int rc = record_step(c, with_lm_head, np, chunked);
+    const int rc = record_step(c, with_lm_head, np, chunked, split_short);
     hipGraph_t g = nullptr;
     const hipError_t e = hipStreamEndCapture(c->stream, &g);
     if (rc) {
@@ -907,6 +921,19 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
         apply_plan(m.pl_down, &dn);
         if (int rc = pack_model_gemv(c, (int)m.fmt, m.pl_down, &dn)) { free_model(c); return rc; }
     }
+    // A capacity whose split length exceeds one 32-position pass gives every
+    // split step the long-context attention (four subgroups a split, or the
+    // direct kernel for an f16 cache), built for splits of many passes. Below
+    // kSplitShortMax positions (splits of at most two passes) the
+    // one-subgroup split attention is faster (SmolLM3-3B, f16 cache of 32768
+    // positions: 1106 against 984 tok/s at ~1000 positions, 972 against 963 at
+    // ~4000; the long kernels win from ~8000 on): those steps take their own
+    // graph.
+    if (!m.p_attn.empty() && m.p_attn[0].nsg > 1 && !tuning_env("QORA_HIP_ATTN_NSG")) {
+        m.split_short_max = std::min<uint32_t>(kSplitShortMax, m.cap);
+        m.p_attn_ss = m.p_attn;
+        for (AttnParams& a : m.p_attn_ss) a.nsg = 1;
+    }
     m.p_lm = RowdotParams{};
     m.p_lm.w = (const uint8_t*)emb->w;
     m.p_lm.scales = (const uint16_t*)emb->scales;
@@ -951,6 +978,10 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
     HIP_TRY(c, hipDeviceSynchronize());
     if (int rc = capture_step(c, true, 0, &m.g_step)) { free_model(c); return rc; }
     if (int rc = capture_step(c, false, 0, &m.g_prefill)) { free_model(c); return rc; }
+    if (m.split_short_max) {
+        if (int rc = capture_step(c, true, 0, &m.g_step_ss, false, true)) { free_model(c); return rc; }
+        if (int rc = capture_step(c, false, 0, &m.g_prefill_ss, false, true)) { free_model(c); return rc; }
+    }
     // one fused variant per pass count a step below attn_o_max can need
     for (uint32_t np = 1; m.attn_o_max && np <= (m.attn_o_max - 1) / kFusedPass + 1; ++np) {
         if (int rc = capture_step(c, true, np, &m.g_step_ao[np - 1])) { free_model(c); return rc; }

@@ -225,6 +225,36 @@ def test_long_context_decode_matches_oracle(ctx, pkg, orc, kv_dtype, hd):
     assert be.kv_len() == n + 4
 
 
+@pytest.mark.parametrize("kv_dtype,n", [(0, 2999), (1, 2999), (1, 4090), (0, 600)])
+def test_split_steps_below_4096_positions_at_a_large_capacity(ctx, pkg, orc, kv_dtype, n):
+    """A capacity of 8192 splits into 128-position pieces, so its split steps
+    would run the long-context attention; steps that append a position below
+    4096 run the one-subgroup split attention from their own graph instead
+    (64-position splits past 2048: two passes a split). Logits against the
+    oracle, the steps crossing from one graph to the other at 4096."""
+    cap = 8192
+    print(f"case split steps below 4096 kv_dtype={kv_dtype} n={n}", flush=True)
+    cfg = pkg.ModelConfig(num_layers=3, vocab=1000, hidden=256, intermediate=704, num_heads=4,
+                          num_kv_heads=2, head_dim=64, rope_half_dim=32, rope_theta=5e6, rope_positions=cap)
+    w = pkg.synthetic_model(cfg, seed=12, rope_positions=cap)
+    be = pkg.HipBackend(ctx, w, kv_capacity=cap, kv_dtype=kv_dtype)
+    om = orc.OracleModel(w, kv_capacity=cap, T=4)
+    r = np.random.default_rng(n)
+    kvd = cfg.num_kv_heads * cfg.head_dim
+    for layer in range(cfg.num_layers):
+        k = r.standard_normal((n, kvd), dtype=np.float32) * np.linspace(0.5, 3, n, dtype=np.float32)[:, None]
+        v = r.standard_normal((n, kvd), dtype=np.float32)
+        if kv_dtype:
+            k, v = k.astype(np.float16).astype(np.float32), v.astype(np.float16).astype(np.float32)
+        be.kv_upload(layer, k, v)
+        om.kv_set(layer, k, v)
+    tol = REL_TOL if kv_dtype == 0 else 5e-3
+    for t in pkg.synth_tokens(12, 2001, 10, cfg.vocab):
+        logits, _ = be.forward_decode_raw(int(t))
+        assert rel_err(logits, om.forward_decode(int(t))) <= tol, (be.kv_len(), int(t))
+    assert be.kv_len() == n + 10
+
+
 @pytest.mark.parametrize("cap,n", [(2100, 1500), (3000, 2040), (2100, 2095)])
 def test_split_count_covers_contexts_below_an_odd_capacity(ctx, pkg, orc, cap, n):
     """The split length follows the live context (32 positions up to 2048),
