@@ -195,14 +195,16 @@ def test_kv_upload_errors(ctx, pkg):
     assert e.value.code == pkg.QORA_HIP_E_STATE
 
 
-@pytest.mark.parametrize("kv_dtype,hd", [(0, 128), (1, 128), (1, 64)])
-def test_long_context_decode_matches_oracle(ctx, pkg, orc, kv_dtype, hd):
+@pytest.mark.parametrize("kv_dtype,hd,cap,n", [(0, 128, 8192, 6001), (1, 128, 8192, 6001), (1, 64, 8192, 6001),
+                                               (1, 128, 16384, 9001), (1, 64, 16384, 9001)])
+def test_long_context_decode_matches_oracle(ctx, pkg, orc, kv_dtype, hd, cap, n):
     """Decode over a cache of ~6000 uploaded positions (capacity 8192): the
     split length follows the context (96 positions per split here) and each
     attention block runs four subgroups; the appended row lands in a pass
-    owned by a later subgroup."""
+    owned by a later subgroup. With an f16 cache, steps from 4096 to 8191
+    positions run the kernel that stages rows in LDS, steps from 8192 on
+    (~9000 positions, capacity 16384) the direct kernel."""
     heads, kvh = (16, 4) if hd == 128 else (4, 2)
-    cap, n = 8192, 6001
     cfg = pkg.ModelConfig(num_layers=4, vocab=1000, hidden=256, intermediate=704, num_heads=heads,
                           num_kv_heads=kvh, head_dim=hd, rope_half_dim=hd // 2, rope_theta=5e6, rope_positions=cap)
     w = pkg.synthetic_model(cfg, seed=4, rope_positions=cap)
@@ -225,13 +227,15 @@ def test_long_context_decode_matches_oracle(ctx, pkg, orc, kv_dtype, hd):
     assert be.kv_len() == n + 4
 
 
-@pytest.mark.parametrize("kv_dtype,n", [(0, 2999), (1, 2999), (1, 4090), (0, 600)])
+@pytest.mark.parametrize("kv_dtype,n", [(0, 2999), (1, 2999), (1, 4090), (0, 600), (1, 8180)])
 def test_split_steps_below_4096_positions_at_a_large_capacity(ctx, pkg, orc, kv_dtype, n):
     """A capacity of 8192 splits into 128-position pieces, so its split steps
     would run the long-context attention; steps that append a position below
     4096 run the one-subgroup split attention from their own graph instead
     (64-position splits past 2048: two passes a split). Logits against the
-    oracle, the steps crossing from one graph to the other at 4096."""
+    oracle, the steps crossing from one graph to the other at 4096. With an
+    f16 cache the steps from 4096 on run the staged four-subgroup kernel
+    from a third graph, up to the capacity here."""
     cap = 8192
     print(f"case split steps below 4096 kv_dtype={kv_dtype} n={n}", flush=True)
     cfg = pkg.ModelConfig(num_layers=3, vocab=1000, hidden=256, intermediate=704, num_heads=4,
