@@ -493,3 +493,34 @@ def test_forced_failures_leave_the_context_usable(ctx, pkg, orc, monkeypatch):
     assert rel_err(logits, om.prefill(prompt)) <= REL_TOL
     logits, _ = be.forward_decode_raw(tok)
     assert rel_err(logits, om.forward_decode(tok)) <= REL_TOL
+
+
+@pytest.mark.parametrize("kv_dtype", [0, 1])
+def test_eager_launches_match_the_captured_graphs(ctx, pkg, monkeypatch, kv_dtype):
+    """QORA_HIP_EAGER=1 launches a step kernel by kernel (for profilers that
+    do not follow graphs): the same kernels and arguments as the graph the
+    host picks for the step, so the logits are bit-identical. Steps from each
+    attention variant of a capacity of 8192: fused (below 256 positions),
+    chunked (below 512), one-subgroup split (below 4096), the long-context
+    kernels above (staged for an f16 cache below 8192)."""
+    cap = 8192
+    cfg = pkg.ModelConfig(num_layers=2, vocab=1000, hidden=256, intermediate=704, num_heads=4,
+                          num_kv_heads=2, head_dim=64, rope_half_dim=32, rope_theta=5e6, rope_positions=cap)
+    w = pkg.synthetic_model(cfg, seed=21, rope_positions=cap)
+    be = pkg.HipBackend(ctx, w, kv_capacity=cap, kv_dtype=kv_dtype)
+    kvd = cfg.num_kv_heads * cfg.head_dim
+    toks = [int(t) for t in pkg.synth_tokens(21, 2001, 3, cfg.vocab)]
+    for n in (100, 300, 3000, 5000, 8100):
+        print(f"case eager vs graph kv_dtype={kv_dtype} n={n}", flush=True)
+        r = np.random.default_rng(n)
+        cache = [(r.standard_normal((n, kvd), dtype=np.float32), r.standard_normal((n, kvd), dtype=np.float32))
+                 for _ in range(cfg.num_layers)]
+        runs = []
+        for eager in ("0", "1"):
+            monkeypatch.setenv("QORA_HIP_EAGER", eager)
+            for layer, (k, v) in enumerate(cache):
+                be.kv_upload(layer, k, v)
+            runs.append([be.forward_decode_raw(t)[0].copy() for t in toks])
+            assert be.kv_len() == n + len(toks)
+        for a, b in zip(*runs):
+            assert np.array_equal(a, b), n
