@@ -227,17 +227,18 @@ def test_long_context_decode_matches_oracle(ctx, pkg, orc, kv_dtype, hd, cap, n)
     assert be.kv_len() == n + 4
 
 
-@pytest.mark.parametrize("kv_dtype,n", [(0, 2999), (1, 2999), (1, 4090), (0, 600), (1, 8180)])
-def test_split_steps_below_4096_positions_at_a_large_capacity(ctx, pkg, orc, kv_dtype, n):
+@pytest.mark.parametrize("kv_dtype,n,cap", [(0, 2999, 8192), (1, 2999, 8192), (1, 4090, 8192), (0, 600, 8192),
+                                             (1, 8180, 8192), (1, 8188, 16384), (0, 8188, 16384)])
+def test_split_steps_below_4096_positions_at_a_large_capacity(ctx, pkg, orc, kv_dtype, n, cap):
     """A capacity of 8192 splits into 128-position pieces, so its split steps
     would run the long-context attention; steps that append a position below
     4096 run the one-subgroup split attention from their own graph instead
     (64-position splits past 2048: two passes a split). Logits against the
     oracle, the steps crossing from one graph to the other at 4096. With an
     f16 cache the steps from 4096 on run the staged four-subgroup kernel
-    from a third graph, up to the capacity here."""
-    cap = 8192
-    print(f"case split steps below 4096 kv_dtype={kv_dtype} n={n}", flush=True)
+    from a third graph, up to the capacity at 8192, and from 8192 on (a
+    capacity of 16384) the direct kernel, the steps crossing at 8192."""
+    print(f"case split steps below 4096 kv_dtype={kv_dtype} n={n} cap={cap}", flush=True)
     cfg = pkg.ModelConfig(num_layers=3, vocab=1000, hidden=256, intermediate=704, num_heads=4,
                           num_kv_heads=2, head_dim=64, rope_half_dim=32, rope_theta=5e6, rope_positions=cap)
     w = pkg.synthetic_model(cfg, seed=12, rope_positions=cap)
