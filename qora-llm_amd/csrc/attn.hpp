@@ -702,10 +702,13 @@ __global__ __launch_bounds__(256 * kAttnLongNsg) void attn_decode_long_kernel(At
 }
 
 // Long contexts with an f16 cache: no LDS staging of the cache. Block (KV
-// head, split) of NWV waves; wave w takes the 32-position passes w, w + NWV,
-// ... of the split. Every lane works on the same slice of the row throughout:
-// lane (c, j) = (l % 16, l / 16) holds dims [c HD/16, (c + 1) HD/16) of
-// positions 4 i + j (i < 8) of the pass, so each K and V load instruction
+// head, split) of NWV waves; wave w takes the 8-position passes w, w + NWV,
+// ... of the split (short passes keep every wave busy on splits of a few
+// hundred positions and the register set small: 8.8% faster decode at 8192
+// positions than 32-position passes, 2.8% at 32700). Every lane works on
+// the same slice of the row throughout: lane (c, j) = (l % 16, l / 16) holds
+// dims [c HD/16, (c + 1) HD/16) of positions 4 i + j (i < 2) of the pass,
+// so each K and V load instruction
 // reads 4 whole rows (1 KB at HD 128) and a lane's scores are those of the
 // very positions whose V it holds: the probabilities never leave the lane.
 // Partial dot products are summed over the 16 lanes of a row (4 shuffles),
@@ -721,7 +724,7 @@ __global__ __launch_bounds__(512) void attn_decode_direct_kernel(const int32_t* 
     const int32_t pos_ld = pos_a ? ld_scalar_i32(pos_a) : 0;
     kernarg_warm(p);
     constexpr int NWV = 8;                           // waves per block
-    constexpr int PP = 32;                           // positions per pass
+    constexpr int PP = 8;                            // positions per pass (2 rows a lane)
     constexpr int VD = HD / 16;                      // dims per lane
     constexpr int NI = PP / 4;                       // rows per lane per pass
     constexpr int G4 = kAttnMaxGroups;

@@ -125,13 +125,6 @@ struct ModelState {
     std::vector<AttnParams> p_attn_ss;
     hipGraphExec_t g_step_ss = nullptr;
     hipGraphExec_t g_prefill_ss = nullptr;
-    // with an f16 cache, split steps from split_short_max up to split_staged_max
-    // run the four-subgroup kernel that stages rows in LDS (p_attn_st) instead
-    // of the direct kernel (0: no such variant)
-    uint32_t split_staged_max = 0;
-    std::vector<AttnParams> p_attn_st;
-    hipGraphExec_t g_step_st = nullptr;
-    hipGraphExec_t g_prefill_st = nullptr;
     // the same steps with the fused attention + o kernel, one per pass count
     // (index np - 1: contexts of 32 (np - 1) < L <= 32 np positions)
     hipGraphExec_t g_step_ao[kFusedMaxPasses] = {};
@@ -312,8 +305,6 @@ void free_model(qora_hip_ctx* c) {
     if (m.g_prefill) (void)hipGraphExecDestroy(m.g_prefill);
     if (m.g_step_ss) (void)hipGraphExecDestroy(m.g_step_ss);
     if (m.g_prefill_ss) (void)hipGraphExecDestroy(m.g_prefill_ss);
-    if (m.g_step_st) (void)hipGraphExecDestroy(m.g_step_st);
-    if (m.g_prefill_st) (void)hipGraphExecDestroy(m.g_prefill_st);
     for (hipGraphExec_t g : m.g_step_ao)
         if (g) (void)hipGraphExecDestroy(g);
     for (hipGraphExec_t g : m.g_prefill_ao)
@@ -367,12 +358,8 @@ int pack_model_gemv(qora_hip_ctx* c, int fmt, const GemvPlan& pl, GemvParams* p)
 
 // np > 0: attention inside the o GEMV for contexts of at most 32 np
 // positions (short contexts, see attn_o_max), or with chunked, the chunked
-// step whose column tiles take 32 np positions each; np = 0: split attention,
-// with the capacity's kernel (split 0), the one-subgroup kernel (kSplitShort)
-// or the staged four-subgroup kernel (kSplitStaged)
-constexpr uint32_t kSplitShort = 1, kSplitStaged = 2;
-
-int record_step(qora_hip_ctx* c, bool with_lm_head, uint32_t np, bool chunked = false, uint32_t split = 0) {
+// step whose column tiles take 32 np positions each; np = 0: split attention
+int record_step(qora_hip_ctx* c, bool with_lm_head, uint32_t np, bool chunked = false, bool split_short = false) {
     ModelState& m = c->m;
     const hipStream_t s = c->stream;
     HIP_TRY(c, launch_embed(with_lm_head ? m.p_emb_tok : m.p_emb_prompt, s));
@@ -381,10 +368,7 @@ int record_step(qora_hip_ctx* c, bool with_lm_head, uint32_t np, bool chunked = 
         if (np) {
             HIP_TRY(c, launch_attn_o(m.pl_o, m.p_ao[l], np, chunked, s));
         } else {
-            const std::vector<AttnParams>& pa = split == kSplitShort    ? m.p_attn_ss
-                                                : split == kSplitStaged ? m.p_attn_st
-                                                                        : m.p_attn;
-            HIP_TRY(c, launch_attn(pa[l], s));
+            HIP_TRY(c, launch_attn(split_short ? m.p_attn_ss[l] : m.p_attn[l], s));
             HIP_TRY(c, launch_gemv(m.fmt, m.pl_o, m.p_o[l], s));
         }
         HIP_TRY(c, launch_gemv(m.fmt, m.pl_gu, m.p_gu[l], s));
@@ -404,8 +388,7 @@ int record_step(qora_hip_ctx* c, bool with_lm_head, uint32_t np, bool chunked = 
 // replaying the captured graph (for profilers that do not follow graphs).
 // Attention subgroups per block (1 or 4): by default 4 when a split can hold
 // more than one 32-position pass; QORA_HIP_ATTN_NSG overrides.
-constexpr uint32_t kSplitShortMax = 4096;    // see split_short_max
-constexpr uint32_t kSplitStagedMax = 8192;   // see split_staged_max
+constexpr uint32_t kSplitShortMax = 4096;   // see split_short_max
 
 uint32_t attn_nsg(uint32_t max_chunk) {
     const char* v = tuning_env("QORA_HIP_ATTN_NSG");
@@ -456,13 +439,13 @@ uint32_t attn_ch_limit(const ModelState& m, int cus) {
 struct StepAttn {
     uint32_t np;
     bool chunked;
-    uint32_t split;             // np = 0: kSplitShort, kSplitStaged or 0 (see record_step)
+    bool split_short;           // np = 0: the one-subgroup split attention (p_attn_ss)
 };
 
 StepAttn step_attn(const ModelState& m, uint64_t pos) {
-    if (pos < (uint64_t)m.attn_o_max) return {(uint32_t)(pos / kFusedPass) + 1u, false, 0u};
-    if (pos < (uint64_t)m.attn_ch_max) return {(uint32_t)(pos / ((uint64_t)kFusedPass * m.pl_o.tiles)) + 1u, true, 0u};
-    return {0u, false, pos < (uint64_t)m.split_short_max ? kSplitShort : pos < (uint64_t)m.split_staged_max ? kSplitStaged : 0u};
+    if (pos < (uint64_t)m.attn_o_max) return {(uint32_t)(pos / kFusedPass) + 1u, false, false};
+    if (pos < (uint64_t)m.attn_ch_max) return {(uint32_t)(pos / ((uint64_t)kFusedPass * m.pl_o.tiles)) + 1u, true, false};
+    return {0u, false, pos < (uint64_t)m.split_short_max};
 }
 
 bool eager_mode() {
@@ -474,10 +457,9 @@ bool eager_mode() {
 int launch_step(qora_hip_ctx* c, bool with_lm_head, uint64_t pos) {
     ModelState& m = c->m;
     const StepAttn sa = step_attn(m, pos);
-    if (eager_mode()) return record_step(c, with_lm_head, sa.np, sa.chunked, sa.split);
-    hipGraphExec_t g = !sa.np ? (sa.split == kSplitShort    ? (with_lm_head ? m.g_step_ss : m.g_prefill_ss)
-                                 : sa.split == kSplitStaged ? (with_lm_head ? m.g_step_st : m.g_prefill_st)
-                                                            : (with_lm_head ? m.g_step : m.g_prefill))
+    if (eager_mode()) return record_step(c, with_lm_head, sa.np, sa.chunked, sa.split_short);
+    hipGraphExec_t g = !sa.np ? (sa.split_short ? (with_lm_head ? m.g_step_ss : m.g_prefill_ss)
+                                                : (with_lm_head ? m.g_step : m.g_prefill))
                        : sa.chunked ? (with_lm_head ? m.g_step_ch[sa.np - 1] : m.g_prefill_ch[sa.np - 1])
                                     : (with_lm_head ? m.g_step_ao[sa.np - 1] : m.g_prefill_ao[sa.np - 1]);
     HIP_TRY(c, hipGraphLaunch(g, c->stream));
@@ -485,9 +467,9 @@ int launch_step(qora_hip_ctx* c, bool with_lm_head, uint64_t pos) {
 }
 
 int capture_step(qora_hip_ctx* c, bool with_lm_head, uint32_t np, hipGraphExec_t* out, bool chunked = false,
-                 uint32_t split = 0) {
+                 bool split_short = false) {
     HIP_TRY(c, hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
-    const int rc = record_step(c, with_lm_head, np, chunked, split);
+    const int rc = record_step(c, with_lm_head, np, chunked, split_short);
     hipGraph_t g = nullptr;
     const hipError_t e = hipStreamEndCapture(c->stream, &g);
     if (rc) {
@@ -952,17 +934,6 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
         m.p_attn_ss = m.p_attn;
         for (AttnParams& a : m.p_attn_ss) a.nsg = 1;
     }
-    // An f16 cache's long-context steps run the direct kernel, whose eight
-    // waves take a pass of 32 positions each: with fewer than eight passes a
-    // split (below 16384 positions) some of them idle, and up to
-    // kSplitStagedMax positions the staged kernel is faster (same model and
-    // cache: 967 against 934 tok/s at ~4100 positions, even at ~8200, 763
-    // against 811 at ~16400).
-    if (m.split_short_max && m.split_short_max < m.cap && m.p_attn[0].kv_f16 && !tuning_env("QORA_HIP_ATTN_STAGED")) {
-        m.split_staged_max = std::min<uint32_t>(kSplitStagedMax, m.cap);
-        m.p_attn_st = m.p_attn;
-        for (AttnParams& a : m.p_attn_st) a.staged = 1;
-    }
     m.p_lm = RowdotParams{};
     m.p_lm.w = (const uint8_t*)emb->w;
     m.p_lm.scales = (const uint16_t*)emb->scales;
@@ -1008,12 +979,8 @@ extern "C" int qora_hip_model_init(qora_hip_ctx* c, const qora_model_desc* d) {
     if (int rc = capture_step(c, true, 0, &m.g_step)) { free_model(c); return rc; }
     if (int rc = capture_step(c, false, 0, &m.g_prefill)) { free_model(c); return rc; }
     if (m.split_short_max) {
-        if (int rc = capture_step(c, true, 0, &m.g_step_ss, false, kSplitShort)) { free_model(c); return rc; }
-        if (int rc = capture_step(c, false, 0, &m.g_prefill_ss, false, kSplitShort)) { free_model(c); return rc; }
-    }
-    if (m.split_staged_max) {
-        if (int rc = capture_step(c, true, 0, &m.g_step_st, false, kSplitStaged)) { free_model(c); return rc; }
-        if (int rc = capture_step(c, false, 0, &m.g_prefill_st, false, kSplitStaged)) { free_model(c); return rc; }
+        if (int rc = capture_step(c, true, 0, &m.g_step_ss, false, true)) { free_model(c); return rc; }
+        if (int rc = capture_step(c, false, 0, &m.g_prefill_ss, false, true)) { free_model(c); return rc; }
     }
     // one fused variant per pass count a step below attn_o_max can need
     for (uint32_t np = 1; m.attn_o_max && np <= (m.attn_o_max - 1) / kFusedPass + 1; ++np) {

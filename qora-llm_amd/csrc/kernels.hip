@@ -451,7 +451,7 @@ void attn_geometry(uint32_t positions, uint32_t* chunk, uint32_t* s_max) {
 hipError_t launch_attn(const AttnParams& p, hipStream_t stream) {
     const dim3 grid(p.s_max, p.KVH);
     const bool lng = p.nsg > 1;
-    if (lng && p.kv_f16 && !p.staged && (p.hd == 128 || p.hd == 64) && p.groups <= (uint32_t)kAttnMaxGroups &&
+    if (lng && p.kv_f16 && (p.hd == 128 || p.hd == 64) && p.groups <= (uint32_t)kAttnMaxGroups &&
         !tuning_env("QORA_HIP_ATTN_STAGED")) {
         const dim3 grid_t(p.KVH, p.s_max);
         if (p.hd == 128) hipLaunchKernelGGL((attn_decode_direct_kernel<128>), grid_t, dim3(512), 0, stream, p.pos, p);

@@ -317,7 +317,6 @@ struct AttnParams {
     float* part;               // [KVH][s_max][groups][hd + 2]
     uint32_t s_max;
     uint32_t nsg;              // 1: attn_decode_kernel; > 1: attn_decode_long_kernel (4 passes in flight per split)
-    uint32_t staged;           // nsg > 1 over an f16 cache: 0 runs attn_decode_direct_kernel, 1 the staged kernel
     // cache addressing: element (pos, kvh, d) at pos * kv_ps + kvh * kv_hs + d;
     // kv_ps = 0: token-major [pos][KVH][hd] (kv_ps = KVH hd, kv_hs = hd)
     uint64_t kv_ps, kv_hs;

@@ -201,9 +201,8 @@ def test_long_context_decode_matches_oracle(ctx, pkg, orc, kv_dtype, hd, cap, n)
     """Decode over a cache of ~6000 uploaded positions (capacity 8192): the
     split length follows the context (96 positions per split here) and each
     attention block runs four subgroups; the appended row lands in a pass
-    owned by a later subgroup. With an f16 cache, steps from 4096 to 8191
-    positions run the kernel that stages rows in LDS, steps from 8192 on
-    (~9000 positions, capacity 16384) the direct kernel."""
+    owned by a later subgroup (the direct kernel, for an f16 cache: a later
+    wave), at capacities 8192 and 16384."""
     heads, kvh = (16, 4) if hd == 128 else (4, 2)
     cfg = pkg.ModelConfig(num_layers=4, vocab=1000, hidden=256, intermediate=704, num_heads=heads,
                           num_kv_heads=kvh, head_dim=hd, rope_half_dim=hd // 2, rope_theta=5e6, rope_positions=cap)
@@ -234,10 +233,8 @@ def test_split_steps_below_4096_positions_at_a_large_capacity(ctx, pkg, orc, kv_
     would run the long-context attention; steps that append a position below
     4096 run the one-subgroup split attention from their own graph instead
     (64-position splits past 2048: two passes a split). Logits against the
-    oracle, the steps crossing from one graph to the other at 4096. With an
-    f16 cache the steps from 4096 on run the staged four-subgroup kernel
-    from a third graph, up to the capacity at 8192, and from 8192 on (a
-    capacity of 16384) the direct kernel, the steps crossing at 8192."""
+    oracle, the steps crossing from one graph to the other at 4096, and
+    split steps near 8192 positions at capacities 8192 and 16384."""
     print(f"case split steps below 4096 kv_dtype={kv_dtype} n={n} cap={cap}", flush=True)
     cfg = pkg.ModelConfig(num_layers=3, vocab=1000, hidden=256, intermediate=704, num_heads=4,
                           num_kv_heads=2, head_dim=64, rope_half_dim=32, rope_theta=5e6, rope_positions=cap)
@@ -503,7 +500,7 @@ def test_eager_launches_match_the_captured_graphs(ctx, pkg, monkeypatch, kv_dtyp
     host picks for the step, so the logits are bit-identical. Steps from each
     attention variant of a capacity of 8192: fused (below 256 positions),
     chunked (below 512), one-subgroup split (below 4096), the long-context
-    kernels above (staged for an f16 cache below 8192)."""
+    kernel above."""
     cap = 8192
     cfg = pkg.ModelConfig(num_layers=2, vocab=1000, hidden=256, intermediate=704, num_heads=4,
                           num_kv_heads=2, head_dim=64, rope_half_dim=32, rope_theta=5e6, rope_positions=cap)
